@@ -1,0 +1,915 @@
+// ggml-hip.hip — the gfx950 ggml backend: device buffers, host<->device tensor transfers (with
+// the weight-plane repack of Q4_0/Q8_0), and graph execution.
+//
+// graph_compute walks the ggml graph in node order (the order ggml-cpu executes, which the
+// reference relies on for the KV-cache writes: model.cpp:1413-1414 precede the attention reads)
+// and issues kernels on the backend's stream. With fusion on (default), it recognizes the
+// per-token patterns of build_graph (reference model.cpp:1296-1474) and runs them as fused
+// kernels:
+//   rms_norm -> mul(weight)                 one kernel, also emitting the Q8_0/Q8_K activation
+//   mul_mat x {q,k,v} sharing one input     one multi-matrix GEMV launch
+//   mul_mat(gate), mul_mat(up), silu, mul   one GEMV launch with a SwiGLU epilogue (+ Q8_0 act)
+//   mul_mat -> add(residual)                the residual add in the GEMV epilogue
+//   K^T Q -> soft_max -> cont(V^T) -> V KQ -> permute -> cont
+//                                           split-KV decode attention (+ Q8_0 act of its output)
+// Everything else runs one kernel per node. Intermediate tensors swallowed by a fusion are not
+// written (they have no other consumer and are not graph outputs). The graph allocator does not
+// recycle memory inside a graph for this backend's buffers (buffer type flag), so executing a
+// fused group at its first member's position can never clobber a live tensor.
+#include "ggml-hip.h"
+#include "ggml-backend-impl.h"
+#include "kernels.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace {
+
+// ---------------------------------------------------------------------------------------------
+// devices
+
+struct hip_device {
+    int id = 0;
+    bool ready = false;
+    hipStream_t stream = nullptr;
+    // device staging for repacked uploads/downloads
+    uint8_t * staging = nullptr;
+    size_t staging_size = 0;
+    ggml_backend_buffer_type buft{};
+    char name[64] = { 0 };
+};
+
+std::vector<hip_device> & devices() {
+    static std::vector<hip_device> d(16);
+    return d;
+}
+
+int device_count() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void) hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+hip_device & dev(int id) {
+    hip_device & d = devices()[id];
+    if (!d.ready) {
+        HIP_CHECK(hipSetDevice(id));
+        // default priority on purpose: streams of different priorities are not mixed here
+        HIP_CHECK(hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking));
+        d.id = id;
+        d.ready = true;
+    }
+    HIP_CHECK(hipSetDevice(id));
+    return d;
+}
+
+uint8_t * staging(hip_device & d, size_t size) {
+    if (size > d.staging_size) {
+        if (d.staging) HIP_CHECK(hipFree(d.staging));
+        d.staging_size = std::max(size, (size_t) 1 << 24);
+        HIP_CHECK(hipMalloc(&d.staging, d.staging_size));
+    }
+    return d.staging;
+}
+
+bool is_repacked(int type) { return type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0; }
+int qs_bytes_of(int type) { return type == GGML_TYPE_Q4_0 ? Q4_0_QS : Q8_0_QS; }
+
+// planes of a repacked tensor: base allocation (view_src or self) and the block index of t
+struct planes {
+    uint8_t * qs;
+    __half * d;
+    int64_t first_block;  // block index of t->data within the base tensor
+    int64_t base_blocks;
+};
+
+planes planes_of(const ggml_tensor * t) {
+    const ggml_tensor * base = t->view_src ? t->view_src : t;
+    const size_t bs = ggml_type_size(t->type);
+    planes p;
+    p.base_blocks = (int64_t) (ggml_nbytes(base) / bs);
+    p.qs = (uint8_t *) base->data;
+    p.d = (__half *) ((uint8_t *) base->data + p.base_blocks * qs_bytes_of(t->type));
+    const size_t off = (size_t) ((const char *) t->data - (const char *) base->data);
+    if (off % bs) HIP_ABORT("tensor '%s': view offset is not block aligned", t->name);
+    p.first_block = (int64_t) (off / bs);
+    return p;
+}
+
+// ---------------------------------------------------------------------------------------------
+// buffers
+
+struct buf_ctx {
+    int device;
+    void * base;
+};
+
+void buf_free(ggml_backend_buffer_t b) {
+    buf_ctx * c = (buf_ctx *) b->context;
+    HIP_CHECK(hipSetDevice(c->device));
+    HIP_CHECK(hipFree(c->base));
+    delete c;
+}
+
+void * buf_base(ggml_backend_buffer_t b) { return ((buf_ctx *) b->context)->base; }
+
+void buf_set(ggml_backend_buffer_t b, ggml_tensor * t, const void * data, size_t off, size_t size) {
+    hip_device & d = dev(((buf_ctx *) b->context)->device);
+    if (is_repacked(t->type)) {
+        const size_t bs = ggml_type_size(t->type);
+        if (off % bs || size % bs) HIP_ABORT("tensor_set on '%s': partial block write", t->name);
+        const planes p = planes_of(t);
+        const size_t chunk = (size_t) (64u << 20) / bs * bs;
+        for (size_t done = 0; done < size; done += chunk) {
+            const size_t n = std::min(chunk, size - done);
+            uint8_t * st = staging(d, n);
+            HIP_CHECK(hipMemcpyAsync(st, (const uint8_t *) data + done, n, hipMemcpyHostToDevice, d.stream));
+            launch_repack_q(t->type, st, p.qs, p.d, (int64_t) (n / bs), p.first_block + (int64_t) ((off + done) / bs), d.stream);
+            HIP_CHECK(hipStreamSynchronize(d.stream));
+        }
+        return;
+    }
+    HIP_CHECK(hipMemcpyAsync((char *) t->data + off, data, size, hipMemcpyHostToDevice, d.stream));
+    HIP_CHECK(hipStreamSynchronize(d.stream));
+}
+
+void buf_get(ggml_backend_buffer_t b, const ggml_tensor * t, void * data, size_t off, size_t size) {
+    hip_device & d = dev(((buf_ctx *) b->context)->device);
+    if (is_repacked(t->type)) {
+        const size_t bs = ggml_type_size(t->type);
+        if (off % bs || size % bs) HIP_ABORT("tensor_get on '%s': partial block read", t->name);
+        const planes p = planes_of(t);
+        const size_t chunk = (size_t) (64u << 20) / bs * bs;
+        for (size_t done = 0; done < size; done += chunk) {
+            const size_t n = std::min(chunk, size - done);
+            uint8_t * st = staging(d, n);
+            launch_unpack_q(t->type, st, p.qs, p.d, (int64_t) (n / bs), p.first_block + (int64_t) ((off + done) / bs), d.stream);
+            HIP_CHECK(hipMemcpyAsync((uint8_t *) data + done, st, n, hipMemcpyDeviceToHost, d.stream));
+            HIP_CHECK(hipStreamSynchronize(d.stream));
+        }
+        return;
+    }
+    HIP_CHECK(hipMemcpyAsync(data, (const char *) t->data + off, size, hipMemcpyDeviceToHost, d.stream));
+    HIP_CHECK(hipStreamSynchronize(d.stream));
+}
+
+void buf_memset(ggml_backend_buffer_t b, ggml_tensor * t, uint8_t v, size_t off, size_t size) {
+    hip_device & d = dev(((buf_ctx *) b->context)->device);
+    if (is_repacked(t->type) && v != 0) HIP_ABORT("tensor_memset on '%s': only zero fills are supported for %s", t->name, ggml_type_name(t->type));
+    if (is_repacked(t->type)) {
+        const size_t bs = ggml_type_size(t->type);
+        if (off % bs || size % bs) HIP_ABORT("tensor_memset on '%s': partial block", t->name);
+        const planes p = planes_of(t);
+        const int64_t b0 = p.first_block + (int64_t) (off / bs), nb = (int64_t) (size / bs);
+        HIP_CHECK(hipMemsetAsync(p.qs + b0 * qs_bytes_of(t->type), 0, nb * qs_bytes_of(t->type), d.stream));
+        HIP_CHECK(hipMemsetAsync(p.d + b0, 0, nb * sizeof(__half), d.stream));
+    } else {
+        HIP_CHECK(hipMemsetAsync((char *) t->data + off, v, size, d.stream));
+    }
+    HIP_CHECK(hipStreamSynchronize(d.stream));
+}
+
+void buf_clear(ggml_backend_buffer_t b, uint8_t v) {
+    buf_ctx * c = (buf_ctx *) b->context;
+    hip_device & d = dev(c->device);
+    HIP_CHECK(hipMemsetAsync(c->base, v, b->size, d.stream));
+    HIP_CHECK(hipStreamSynchronize(d.stream));
+}
+
+const char * buft_name(ggml_backend_buffer_type_t t) { return ((hip_device *) t->context)->name; }
+size_t buft_align(ggml_backend_buffer_type_t) { return 256; }
+bool buft_is_host(ggml_backend_buffer_type_t) { return false; }
+bool buft_no_reuse(ggml_backend_buffer_type_t) { return true; }
+
+ggml_backend_buffer_t buft_alloc(ggml_backend_buffer_type_t t, size_t size) {
+    hip_device & d = dev(((hip_device *) t->context)->id);
+    void * p = nullptr;
+    if (hipMalloc(&p, std::max<size_t>(size, 256)) != hipSuccess) {
+        (void) hipGetLastError();
+        fprintf(stderr, "ggml-hip: failed to allocate %.1f MiB on device %d\n", size / 1048576.0, d.id);
+        return nullptr;
+    }
+    buf_ctx * c = new buf_ctx{ d.id, p };
+    ggml_backend_buffer_i iface = { buf_free, buf_base, nullptr, buf_set, buf_get, buf_memset, buf_clear };
+    return ggml_backend_buffer_init(t, iface, c, size);
+}
+
+// ---------------------------------------------------------------------------------------------
+// backend context
+
+struct prof_entry { int64_t launches = 0; double ms = 0.0; double bytes = 0.0; };
+
+struct pending_event { std::string name; double bytes; hipEvent_t a, b; };
+
+struct scratch_arena {
+    std::vector<std::pair<uint8_t *, size_t>> chunks;
+    size_t chunk = 0, off = 0;
+    void reset() { chunk = 0; off = 0; }
+    void * alloc(size_t size) {
+        size = (size + 255) & ~(size_t) 255;
+        while (chunk < chunks.size() && off + size > chunks[chunk].second) { chunk++; off = 0; }
+        if (chunk == chunks.size()) {
+            const size_t cap = std::max(size, (size_t) 64 << 20);
+            uint8_t * p = nullptr;
+            HIP_CHECK(hipMalloc(&p, cap));
+            chunks.push_back({ p, cap });
+            off = 0;
+        }
+        void * r = chunks[chunk].first + off;
+        off += size;
+        return r;
+    }
+    void release() {
+        for (auto & c : chunks) HIP_CHECK(hipFree(c.first));
+        chunks.clear();
+        reset();
+    }
+};
+
+struct act_entry {       // quantized copy of an activation tensor
+    int kind;            // 1 = q8 (Q8_0 semantics), 2 = q8K
+    q8_act q8;
+    q8k_act q8k;
+    int64_t K, ncols;
+};
+
+struct hip_backend_ctx {
+    int device = 0;
+    bool fusion = true;
+    bool graph_replay = true;
+    bool profiling = false;
+    scratch_arena scratch;
+    std::map<std::string, prof_entry> prof;
+    std::vector<pending_event> pending;
+    std::vector<hipEvent_t> event_pool;
+    size_t event_next = 0;
+};
+
+// ---------------------------------------------------------------------------------------------
+// graph executor
+
+tview tv(const ggml_tensor * t) {
+    tview v;
+    v.data = (char *) t->data;
+    v.type = t->type;
+    for (int i = 0; i < 4; i++) { v.ne[i] = t->ne[i]; v.nb[i] = (int64_t) t->nb[i]; }
+    return v;
+}
+
+int dot_kind(int wtype) {
+    if (wtype == GGML_TYPE_Q4_0 || wtype == GGML_TYPE_Q8_0) return 1;
+    if (wtype == GGML_TYPE_Q4_K) return 2;
+    return 0;
+}
+
+bool is_2d_contig(const ggml_tensor * t) { return t->ne[2] == 1 && t->ne[3] == 1 && ggml_is_contiguous(t); }
+
+class executor {
+public:
+    executor(hip_backend_ctx & ctx, ggml_cgraph * g) : c_(ctx), g_(g), st_(dev(ctx.device).stream) {}
+
+    void run() {
+        c_.scratch.reset();
+        index_graph();
+        done_.assign(g_->n_nodes, false);
+        for (int i = 0; i < g_->n_nodes; i++) {
+            if (done_[i]) continue;
+            exec_node(i);
+            done_[i] = true;
+        }
+    }
+
+private:
+    hip_backend_ctx & c_;
+    ggml_cgraph * g_;
+    hipStream_t st_;
+    std::unordered_map<const ggml_tensor *, int> idx_;
+    std::vector<std::vector<int>> users_;
+    std::vector<bool> done_;
+    std::unordered_map<const ggml_tensor *, act_entry> act_;
+
+    // ---- graph structure ----
+    void index_graph() {
+        idx_.clear();
+        idx_.reserve(g_->n_nodes * 2);
+        for (int i = 0; i < g_->n_nodes; i++) idx_[g_->nodes[i]] = i;
+        users_.assign(g_->n_nodes, {});
+        for (int i = 0; i < g_->n_nodes; i++) {
+            const ggml_tensor * n = g_->nodes[i];
+            for (int s = 0; s < GGML_MAX_SRC; s++) {
+                if (!n->src[s]) continue;
+                if (s > 0 && n->src[s] == n->src[s - 1]) continue;
+                auto it = idx_.find(n->src[s]);
+                if (it != idx_.end()) users_[it->second].push_back(i);
+            }
+        }
+    }
+    int node_index(const ggml_tensor * t) const {
+        auto it = idx_.find(t);
+        return it == idx_.end() ? -1 : it->second;
+    }
+    bool is_output(int i) const { return i == g_->n_nodes - 1 || (g_->nodes[i]->flags & GGML_TENSOR_FLAG_OUTPUT); }
+    // the single consumer of node i, or -1 (0 or >1 users, or a graph output)
+    int sole_user(int i) const {
+        if (i < 0 || is_output(i) || users_[i].size() != 1) return -1;
+        return users_[i][0];
+    }
+
+    // ---- profiling ----
+    hipEvent_t event() {
+        if (c_.event_next == c_.event_pool.size()) {
+            hipEvent_t e;
+            HIP_CHECK(hipEventCreate(&e));
+            c_.event_pool.push_back(e);
+        }
+        return c_.event_pool[c_.event_next++];
+    }
+    struct prof_scope {
+        executor * ex;
+        const char * name;
+        double bytes;
+        hipEvent_t a = nullptr;
+        prof_scope(executor * e, const char * n, double b) : ex(e), name(n), bytes(b) {
+            if (ex->c_.profiling) { a = ex->event(); HIP_CHECK(hipEventRecord(a, ex->st_)); }
+        }
+        ~prof_scope() {
+            if (!a) return;
+            hipEvent_t b = ex->event();
+            HIP_CHECK(hipEventRecord(b, ex->st_));
+            ex->c_.pending.push_back({ name, bytes, a, b });
+        }
+    };
+
+    // ---- activation quantization ----
+    const act_entry * ensure_act(const ggml_tensor * x, int kind) {
+        auto it = act_.find(x);
+        if (it != act_.end() && it->second.kind == kind) return &it->second;
+        const int64_t K = x->ne[0], ncols = x->ne[1];
+        act_entry e = alloc_act(kind, K, ncols);
+        const int64_t col_stride = (int64_t) (x->nb[1] / sizeof(float));
+        if (kind == 1) {
+            prof_scope ps(this, "quantize_q8", (double) (K * ncols * 4));
+            launch_quantize_q8((const float *) x->data, col_stride, K, ncols, e.q8, st_);
+        } else {
+            prof_scope ps(this, "quantize_q8K", (double) (K * ncols * 4));
+            launch_quantize_q8k((const float *) x->data, col_stride, K, ncols, e.q8k, st_);
+        }
+        act_[x] = e;
+        return &act_[x];
+    }
+    act_entry alloc_act(int kind, int64_t K, int64_t ncols) {
+        act_entry e{};
+        e.kind = kind;
+        e.K = K;
+        e.ncols = ncols;
+        if (kind == 1) {
+            e.q8.qs = (int8_t *) c_.scratch.alloc((size_t) (K * ncols));
+            e.q8.d = (float *) c_.scratch.alloc((size_t) (K / 32 * ncols) * 4);
+            e.q8.s = (int32_t *) c_.scratch.alloc((size_t) (K / 32 * ncols) * 4);
+        } else {
+            e.q8k.qs = (int8_t *) c_.scratch.alloc((size_t) (K * ncols));
+            e.q8k.d = (float *) c_.scratch.alloc((size_t) (K / 256 * ncols) * 4);
+            e.q8k.bsums = (int16_t *) c_.scratch.alloc((size_t) (K / 16 * ncols) * 2);
+        }
+        return e;
+    }
+    // the quantized form all consumers of node i want (0: none / mixed / not all quantized mul_mats)
+    int wanted_act_kind(int i) const {
+        if (i < 0 || users_[i].empty()) return 0;
+        int kind = 0;
+        for (int u : users_[i]) {
+            const ggml_tensor * n = g_->nodes[u];
+            if (n->op != GGML_OP_MUL_MAT || n->src[1] != g_->nodes[i]) return 0;
+            const int k = dot_kind(n->src[0]->type);
+            if (k == 0 || (kind && k != kind)) return 0;
+            kind = k;
+        }
+        return kind;
+    }
+
+    // ---- dispatch ----
+    void exec_node(int i) {
+        ggml_tensor * n = g_->nodes[i];
+        switch (n->op) {
+            case GGML_OP_NONE: case GGML_OP_RESHAPE: case GGML_OP_VIEW: case GGML_OP_PERMUTE: case GGML_OP_TRANSPOSE:
+                return;
+            case GGML_OP_RMS_NORM: op_rms_norm(i); return;
+            case GGML_OP_MUL_MAT: op_mul_mat(i); return;
+            case GGML_OP_GET_ROWS: op_get_rows(n); return;
+            case GGML_OP_ADD: { prof_scope ps(this, "add", 0); launch_binary(0, tv(n->src[0]), tv(n->src[1]), tv(n), st_); return; }
+            case GGML_OP_MUL: { prof_scope ps(this, "mul", 0); launch_binary(1, tv(n->src[0]), tv(n->src[1]), tv(n), st_); return; }
+            case GGML_OP_SCALE: {
+                float s;
+                memcpy(&s, n->op_params, 4);
+                prof_scope ps(this, "scale", 0);
+                launch_unary(4, s, tv(n->src[0]), tv(n), st_);
+                return;
+            }
+            case GGML_OP_SQR: { prof_scope ps(this, "sqr", 0); launch_unary(3, 0, tv(n->src[0]), tv(n), st_); return; }
+            case GGML_OP_UNARY: {
+                const int u = n->op_params[0];
+                const int op = u == GGML_UNARY_OP_SILU ? 0 : u == GGML_UNARY_OP_RELU ? 1 : u == GGML_UNARY_OP_SIGMOID ? 2 : -1;
+                if (op < 0) HIP_ABORT("unsupported unary op %d", u);
+                prof_scope ps(this, "unary", 0);
+                launch_unary(op, 0, tv(n->src[0]), tv(n), st_);
+                return;
+            }
+            case GGML_OP_CPY: case GGML_OP_CONT: case GGML_OP_DUP: {
+                if (ggml_is_quantized(n->type) || ggml_is_quantized(n->src[0]->type)) HIP_ABORT("copy of quantized tensor '%s'", n->name);
+                prof_scope ps(this, "cpy", (double) (ggml_nbytes(n->src[0]) + ggml_nbytes(n)));
+                launch_cpy(tv(n->src[0]), tv(n), st_);
+                return;
+            }
+            case GGML_OP_ROPE: op_rope(n); return;
+            case GGML_OP_SOFT_MAX: {
+                float scale, max_bias;
+                memcpy(&scale, &n->op_params[0], 4);
+                memcpy(&max_bias, &n->op_params[1], 4);
+                tview m{};
+                if (n->src[1]) m = tv(n->src[1]);
+                prof_scope ps(this, "soft_max", 0);
+                launch_soft_max(tv(n->src[0]), n->src[1] ? &m : nullptr, tv(n), scale, max_bias, st_);
+                return;
+            }
+            case GGML_OP_FLASH_ATTN_EXT: op_flash_attn(n); return;
+            case GGML_OP_ARGMAX: { prof_scope ps(this, "argmax", 0); launch_argmax(tv(n->src[0]), (int32_t *) n->data, st_); return; }
+            default:
+                HIP_ABORT("op %s is not supported by the hip backend (node '%s')", ggml_op_name(n->op), n->name);
+        }
+    }
+
+    void op_get_rows(ggml_tensor * n) {
+        const ggml_tensor * a = n->src[0];
+        planes p{};
+        if (is_repacked(a->type)) p = planes_of(a);
+        prof_scope ps(this, "get_rows", (double) ggml_nbytes(n));
+        launch_get_rows(tv(a), tv(n->src[1]), tv(n), p.qs, p.d, p.first_block, st_);
+    }
+
+    void op_rope(ggml_tensor * n) {
+        rope_params p{};
+        p.n_dims = n->op_params[1];
+        p.mode = n->op_params[2];
+        const int n_ctx_orig = n->op_params[4];
+        float freq_base, beta_fast, beta_slow;
+        memcpy(&freq_base, n->op_params + 5, 4);
+        memcpy(&p.freq_scale, n->op_params + 6, 4);
+        memcpy(&p.ext_factor, n->op_params + 7, 4);
+        memcpy(&p.attn_factor, n->op_params + 8, 4);
+        memcpy(&beta_fast, n->op_params + 9, 4);
+        memcpy(&beta_slow, n->op_params + 10, 4);
+        ggml_rope_yarn_corr_dims(p.n_dims, n_ctx_orig, freq_base, beta_fast, beta_slow, p.corr_dims);
+        p.theta_scale = powf(freq_base, -2.0f / p.n_dims);
+        if (n->src[0]->type != GGML_TYPE_F32 || n->type != GGML_TYPE_F32) HIP_ABORT("rope: f32 only");
+        prof_scope ps(this, "rope", 0);
+        launch_rope(tv(n->src[0]), (const int32_t *) n->src[1]->data, n->src[2] ? (const float *) n->src[2]->data : nullptr,
+                    tv(n), p, st_);
+    }
+
+    // rms_norm, fused with a following weight multiply (and activation quantization) when possible
+    void op_rms_norm(int i) {
+        ggml_tensor * n = g_->nodes[i];
+        float eps;
+        memcpy(&eps, n->op_params, 4);
+        const ggml_tensor * x = n->src[0];
+        const bool rows_ok = x->type == GGML_TYPE_F32 && ggml_is_contiguous(x) && ggml_is_contiguous(n);
+        if (c_.fusion && rows_ok) {
+            const int u = sole_user(i);
+            if (u >= 0) {
+                ggml_tensor * m = g_->nodes[u];
+                const ggml_tensor * w = m->src[1];
+                if (m->op == GGML_OP_MUL && m->src[0] == n && w->type == GGML_TYPE_F32 && ggml_nrows(w) == 1 &&
+                    w->ne[0] == x->ne[0] && ggml_is_contiguous(w) && ggml_is_contiguous(m)) {
+                    const int64_t N = x->ne[0], rows = ggml_nrows(x);
+                    const int kind = wanted_act_kind(u);
+                    act_entry e{};
+                    const bool q = (kind == 1 && N % 32 == 0) || (kind == 2 && N % 256 == 0);
+                    if (q) e = alloc_act(kind, N, rows);
+                    prof_scope ps(this, "rms_norm_mul", (double) (N * rows * 8 + N * 4));
+                    launch_rms_norm((const float *) x->data, N, (const float *) w->data, (float *) m->data, N, N, rows, eps,
+                                    q && kind == 1 ? &e.q8 : nullptr, q && kind == 2 ? &e.q8k : nullptr, st_);
+                    if (q && m->ne[1] == rows) act_[m] = e;
+                    done_[u] = true;
+                    return;
+                }
+            }
+        }
+        prof_scope ps(this, "rms_norm", 0);
+        if (rows_ok) {
+            launch_rms_norm((const float *) x->data, x->ne[0], nullptr, (float *) n->data, n->ne[0], x->ne[0], ggml_nrows(x), eps,
+                            nullptr, nullptr, st_);
+        } else {
+            launch_rms_norm_strided(tv(x), tv(n), eps, st_);
+        }
+    }
+
+    bool gemv_capable(const ggml_tensor * mm) const {
+        const ggml_tensor * w = mm->src[0];
+        const ggml_tensor * x = mm->src[1];
+        if (!dot_kind(w->type)) return false;
+        if (!is_2d_contig(w)) return false;
+        if (x->type != GGML_TYPE_F32 || x->nb[0] != sizeof(float) || x->ne[2] != 1 || x->ne[3] != 1) return false;
+        if (!is_2d_contig(mm)) return false;
+        if (w->ne[0] % (w->type == GGML_TYPE_Q4_K ? 256 : 32)) return false;
+        return true;
+    }
+
+    void op_mul_mat(int i) {
+        ggml_tensor * n = g_->nodes[i];
+        if (c_.fusion && try_attention(i)) return;
+        if (gemv_capable(n)) { op_gemv(i); return; }
+        if (ggml_is_quantized(n->src[0]->type)) {
+            HIP_ABORT("mul_mat '%s': quantized %s weights with this layout are not supported", n->name, ggml_type_name(n->src[0]->type));
+        }
+        if (n->src[1]->type != GGML_TYPE_F32 || n->src[0]->nb[0] != ggml_type_size(n->src[0]->type)) {
+            HIP_ABORT("mul_mat '%s': unsupported operand layout", n->name);
+        }
+        prof_scope ps(this, "mul_mat_generic", (double) (ggml_nbytes(n->src[0]) + ggml_nbytes(n->src[1]) + ggml_nbytes(n)));
+        launch_mul_mat_generic(tv(n->src[0]), tv(n->src[1]), tv(n), st_);
+    }
+
+    // quantized GEMV for node i, grouped with the other pending mul_mats that read the same input
+    void op_gemv(int i) {
+        ggml_tensor * n = g_->nodes[i];
+        const ggml_tensor * x = n->src[1];
+        const int wtype = n->src[0]->type;
+        const int64_t K = n->src[0]->ne[0], ncols = x->ne[1];
+        std::vector<int> group = { i };
+        if (c_.fusion) {
+            const int xi = node_index(x);
+            const std::vector<int> & cands = xi >= 0 ? users_[xi] : std::vector<int>();
+            std::vector<int> others;
+            if (xi < 0) {
+                for (int j = i + 1; j < g_->n_nodes; j++) {
+                    const ggml_tensor * m = g_->nodes[j];
+                    if (m->op == GGML_OP_MUL_MAT && m->src[1] == x) others.push_back(j);
+                }
+            } else {
+                for (int j : cands) if (j != i) others.push_back(j);
+            }
+            for (int j : others) {
+                const ggml_tensor * m = g_->nodes[j];
+                if (done_[j] || m->op != GGML_OP_MUL_MAT || m->src[1] != x) continue;
+                if (m->src[0]->type != wtype || m->src[0]->ne[0] != K || !gemv_capable(m)) continue;
+                if ((int) group.size() == GEMV_MAX_MATS) break;
+                group.push_back(j);
+            }
+        }
+
+        // SwiGLU pair inside the group: gate -> silu -> mul(silu, up)
+        int gate = -1, up = -1, mulnode = -1;
+        if (c_.fusion && group.size() >= 2) {
+            for (int a : group) {
+                const int s = sole_user(a);
+                if (s < 0) continue;
+                const ggml_tensor * sn = g_->nodes[s];
+                if (sn->op != GGML_OP_UNARY || sn->op_params[0] != GGML_UNARY_OP_SILU) continue;
+                const int m = sole_user(s);
+                if (m < 0) continue;
+                const ggml_tensor * mn = g_->nodes[m];
+                if (mn->op != GGML_OP_MUL || mn->src[0] != sn) continue;
+                const int b = node_index(mn->src[1]);
+                if (b < 0 || sole_user(b) != m || std::find(group.begin(), group.end(), b) == group.end()) continue;
+                if (!ggml_are_same_shape(g_->nodes[a], g_->nodes[b]) || !is_2d_contig(mn)) continue;
+                gate = a; up = b; mulnode = m;
+                break;
+            }
+        }
+
+        const int kind = dot_kind(wtype);
+        const act_entry * xa = ensure_act(x, kind);
+
+        auto fill_mat = [&](gemv_mat & gm, int j, double & bytes) {
+            ggml_tensor * mm = g_->nodes[j];
+            const ggml_tensor * w = mm->src[0];
+            if (is_repacked(w->type)) {
+                const planes p = planes_of(w);
+                gm.w = p.qs + p.first_block * qs_bytes_of(w->type);
+                gm.wd = p.d + p.first_block;
+            } else {
+                gm.w = (const uint8_t *) w->data;
+                gm.wd = nullptr;
+            }
+            gm.n_rows = (int32_t) w->ne[1];
+            gm.y = (float *) mm->data;
+            gm.y_stride = (int64_t) (mm->nb[1] / sizeof(float));
+            gm.add = nullptr;
+            gm.add_stride = 0;
+            bytes += (double) ggml_nbytes(w) + (double) (w->ne[1] * ncols * 4);
+            // residual add epilogue
+            const int u = c_.fusion ? sole_user(j) : -1;
+            if (u >= 0) {
+                ggml_tensor * an = g_->nodes[u];
+                if (an->op == GGML_OP_ADD && an->src[0] == mm && an->src[1]->type == GGML_TYPE_F32 &&
+                    ggml_are_same_shape(an->src[1], mm) && is_2d_contig(an->src[1]) && is_2d_contig(an)) {
+                    gm.y = (float *) an->data;
+                    gm.y_stride = (int64_t) (an->nb[1] / sizeof(float));
+                    gm.add = (const float *) an->src[1]->data;
+                    gm.add_stride = (int64_t) (an->src[1]->nb[1] / sizeof(float));
+                    bytes += (double) (w->ne[1] * ncols * 4);
+                    done_[u] = true;
+                }
+            }
+        };
+
+        gemv_launch L{};
+        L.type = wtype;
+        L.K = (int) K;
+        L.ncols = (int) ncols;
+        if (kind == 1) { L.xq = xa->q8.qs; L.xd = xa->q8.d; L.xs = xa->q8.s; }
+        else { L.xq = xa->q8k.qs; L.xd = xa->q8k.d; L.xbs = xa->q8k.bsums; }
+        double bytes = (double) (K * ncols * 4);
+
+        if (gate >= 0) {
+            // SwiGLU launch for (gate, up); the rest of the group goes in a second launch
+            gemv_launch S = L;
+            S.n_mats = 2;
+            S.swiglu = true;
+            double sb = bytes;
+            fill_mat(S.m[0], gate, sb);
+            fill_mat(S.m[1], up, sb);
+            ggml_tensor * mn = g_->nodes[mulnode];
+            S.m[0].y = (float *) mn->data;
+            S.m[0].y_stride = (int64_t) (mn->nb[1] / sizeof(float));
+            S.m[0].add = nullptr;
+            sb -= (double) (g_->nodes[gate]->ne[0] * ncols * 4); // gate/up outputs are not written, act is
+            const int qk = wanted_act_kind(mulnode);
+            if (qk == 1 && mn->ne[0] % 32 == 0) {
+                act_entry e = alloc_act(1, mn->ne[0], ncols);
+                S.act_q = e.q8;
+                act_[mn] = e;
+            }
+            {
+                prof_scope ps(this, wtype == GGML_TYPE_Q4_0 ? "gemv_q4_0_swiglu" :
+                                    wtype == GGML_TYPE_Q8_0 ? "gemv_q8_0_swiglu" : "gemv_q4_K_swiglu", sb);
+                launch_gemv(S, st_);
+            }
+            done_[gate] = done_[up] = done_[mulnode] = true;
+            done_[sole_user(gate)] = true; // the silu node
+            std::vector<int> rest;
+            for (int j : group) if (j != gate && j != up) rest.push_back(j);
+            group = rest;
+            if (group.empty()) return;
+        }
+
+        L.n_mats = (int) group.size();
+        for (size_t k = 0; k < group.size(); k++) fill_mat(L.m[k], group[k], bytes);
+        {
+            prof_scope ps(this, wtype == GGML_TYPE_Q4_0 ? "gemv_q4_0" : wtype == GGML_TYPE_Q8_0 ? "gemv_q8_0" : "gemv_q4_K", bytes);
+            launch_gemv(L, st_);
+        }
+        for (int j : group) done_[j] = true;
+    }
+
+    // K^T Q -> soft_max -> cont(permute(V)) -> V KQ -> permute -> cont  ==>  split-KV attention
+    bool try_attention(int i) {
+        ggml_tensor * kq = g_->nodes[i];
+        const ggml_tensor * kp = kq->src[0];
+        const ggml_tensor * qp = kq->src[1];
+        if (kp->type != GGML_TYPE_F16 || kp->op != GGML_OP_PERMUTE || qp->type != GGML_TYPE_F32) return false;
+        const int sm = sole_user(i);
+        if (sm < 0) return false;
+        ggml_tensor * smn = g_->nodes[sm];
+        if (smn->op != GGML_OP_SOFT_MAX || smn->src[0] != kq) return false;
+        float scale, max_bias;
+        memcpy(&scale, &smn->op_params[0], 4);
+        memcpy(&max_bias, &smn->op_params[1], 4);
+        if (max_bias != 0.0f) return false;
+        const int kqv = sole_user(sm);
+        if (kqv < 0) return false;
+        ggml_tensor * kqvn = g_->nodes[kqv];
+        if (kqvn->op != GGML_OP_MUL_MAT || kqvn->src[1] != smn) return false;
+        const ggml_tensor * vt = kqvn->src[0];
+        const int vti = node_index(vt);
+        if (vt->op != GGML_OP_CONT || vti < 0 || sole_user(vti) != kqv) return false;
+        const ggml_tensor * vp = vt->src[0];
+        if (vp->op != GGML_OP_PERMUTE || vp->type != GGML_TYPE_F16) return false;
+        const int pm = sole_user(kqv);
+        if (pm < 0) return false;
+        ggml_tensor * pmn = g_->nodes[pm];
+        if (pmn->op != GGML_OP_PERMUTE) return false;
+        const int ct = sole_user(pm);
+        if (ct < 0) return false;
+        ggml_tensor * ctn = g_->nodes[ct];
+        if (ctn->op != GGML_OP_CONT || !is_2d_contig(ctn)) return false;
+
+        const int hd = (int) kp->ne[0], n_kv = (int) kp->ne[1], n_head_kv = (int) kp->ne[2];
+        const int n_q = (int) qp->ne[1], n_head = (int) qp->ne[2];
+        if (kp->ne[3] != 1 || qp->ne[3] != 1 || qp->ne[0] != hd) return false;
+        if (vp->ne[0] != n_kv || vp->ne[1] != hd || vp->ne[2] != n_head_kv) return false;
+        if (kp->nb[0] != 2 || vp->nb[1] != 2 || qp->nb[0] != 4) return false;
+        if (n_q < 1 || n_q > 4 || n_head % n_head_kv || n_head / n_head_kv > 8) return false;
+        if (hd != 64 && hd != 96 && hd != 128) return false;
+        if (ctn->ne[0] != (int64_t) hd * n_head || ctn->ne[1] != n_q) return false;
+        const ggml_tensor * mask = smn->src[1];
+        if (mask && (mask->ne[0] != n_kv || mask->nb[0] != ggml_type_size(mask->type))) return false;
+        // 16-byte alignment of the K rows for the staged loads
+        if (((uintptr_t) kp->data) % 16 || kp->nb[1] % 16 || kp->nb[2] % 16) return false;
+
+        attn_launch A{};
+        A.q = (const float *) qp->data;
+        A.q_nb1 = (int64_t) (qp->nb[2] / 4);
+        A.q_nb2 = (int64_t) (qp->nb[1] / 4);
+        A.k = (const __half *) kp->data;
+        A.k_nb1 = (int64_t) (kp->nb[2] / 2);
+        A.k_nb2 = (int64_t) (kp->nb[1] / 2);
+        A.v = (const __half *) vp->data;
+        A.v_nb1 = (int64_t) (vp->nb[2] / 2);
+        A.v_nb2 = (int64_t) (vp->nb[0] / 2);
+        A.mask = mask ? mask->data : nullptr;
+        A.mask_f16 = mask && mask->type == GGML_TYPE_F16;
+        A.mask_nb1 = mask ? (int64_t) mask->nb[1] : 0;
+        A.out = (float *) ctn->data;
+        A.out_nb1 = (int64_t) (ctn->nb[1] / 4);
+        A.n_kv = n_kv; A.n_q = n_q; A.n_head = n_head; A.n_head_kv = n_head_kv; A.hd = hd;
+        A.scale = scale;
+        A.scratch_bytes = attn_scratch_bytes(n_kv, n_q, n_head, hd);
+        A.scratch = (float *) c_.scratch.alloc((size_t) A.scratch_bytes);
+        if (wanted_act_kind(ct) == 1) {
+            act_entry e = alloc_act(1, ctn->ne[0], n_q);
+            A.out_q = e.q8;
+            act_[ctn] = e;
+        }
+        const double bytes = (double) n_kv * n_head_kv * hd * 2 * 2 + (double) n_head * hd * n_q * 8 +
+                             (mask ? (double) n_kv * n_q * ggml_type_size(mask->type) : 0.0);
+        {
+            prof_scope ps(this, "attn_decode", bytes);
+            launch_attn_decode(A, st_);
+        }
+        done_[i] = done_[sm] = done_[vti] = done_[kqv] = done_[pm] = done_[ct] = true;
+        return true;
+    }
+
+    void op_flash_attn(ggml_tensor * n) {
+        const ggml_tensor * q = n->src[0], * k = n->src[1], * v = n->src[2], * mask = n->src[3];
+        float scale, max_bias, softcap;
+        memcpy(&scale, &n->op_params[0], 4);
+        memcpy(&max_bias, &n->op_params[1], 4);
+        memcpy(&softcap, &n->op_params[2], 4);
+        const int hd = (int) q->ne[0], n_q = (int) q->ne[1], n_head = (int) q->ne[2];
+        const int n_kv = (int) k->ne[1], n_head_kv = (int) k->ne[2];
+        const bool ok = max_bias == 0.0f && softcap == 0.0f && k->type == GGML_TYPE_F16 && v->type == GGML_TYPE_F16 &&
+                        q->type == GGML_TYPE_F32 && q->nb[0] == 4 && k->nb[0] == 2 && v->nb[0] == 2 && v->ne[0] == hd &&
+                        n_q >= 1 && n_q <= 4 && n_head % n_head_kv == 0 && n_head / n_head_kv <= 8 &&
+                        (hd == 64 || hd == 96 || hd == 128) && ggml_is_contiguous(n) &&
+                        ((uintptr_t) k->data) % 16 == 0 && k->nb[1] % 16 == 0 && k->nb[2] % 16 == 0 &&
+                        (!mask || (mask->ne[0] == n_kv && mask->nb[0] == ggml_type_size(mask->type)));
+        if (!ok) HIP_ABORT("flash_attn_ext '%s': unsupported configuration", n->name);
+        attn_launch A{};
+        A.q = (const float *) q->data;
+        A.q_nb1 = (int64_t) (q->nb[2] / 4);
+        A.q_nb2 = (int64_t) (q->nb[1] / 4);
+        A.k = (const __half *) k->data;
+        A.k_nb1 = (int64_t) (k->nb[2] / 2);
+        A.k_nb2 = (int64_t) (k->nb[1] / 2);
+        A.v = (const __half *) v->data;
+        A.v_nb1 = (int64_t) (v->nb[2] / 2);
+        A.v_nb2 = (int64_t) (v->nb[1] / 2);
+        A.mask = mask ? mask->data : nullptr;
+        A.mask_f16 = mask && mask->type == GGML_TYPE_F16;
+        A.mask_nb1 = mask ? (int64_t) mask->nb[1] : 0;
+        A.out = (float *) n->data;
+        A.out_nb1 = (int64_t) (n->nb[2] / 4);
+        A.n_kv = n_kv; A.n_q = n_q; A.n_head = n_head; A.n_head_kv = n_head_kv; A.hd = hd;
+        A.scale = scale;
+        A.scratch_bytes = attn_scratch_bytes(n_kv, n_q, n_head, hd);
+        A.scratch = (float *) c_.scratch.alloc((size_t) A.scratch_bytes);
+        const double bytes = (double) n_kv * n_head_kv * hd * 2 * 2 + (double) n_head * hd * n_q * 8;
+        prof_scope ps(this, "attn_decode", bytes);
+        launch_attn_decode(A, st_);
+    }
+};
+
+// ---------------------------------------------------------------------------------------------
+// backend interface
+
+const char * be_name(ggml_backend_t b) { return ((hip_device *) &dev(((hip_backend_ctx *) b->context)->device))->name; }
+
+void be_free(ggml_backend_t b) {
+    hip_backend_ctx * c = (hip_backend_ctx *) b->context;
+    dev(c->device);
+    HIP_CHECK(hipStreamSynchronize(dev(c->device).stream));
+    c->scratch.release();
+    for (hipEvent_t e : c->event_pool) HIP_CHECK(hipEventDestroy(e));
+    delete c;
+    delete b;
+}
+
+ggml_backend_buffer_type_t be_buft(ggml_backend_t b) { return ggml_backend_hip_buffer_type(((hip_backend_ctx *) b->context)->device); }
+
+void collect_profile(hip_backend_ctx * c) {
+    for (pending_event & p : c->pending) {
+        float ms = 0.0f;
+        HIP_CHECK(hipEventElapsedTime(&ms, p.a, p.b));
+        prof_entry & e = c->prof[p.name];
+        e.launches++;
+        e.ms += ms;
+        e.bytes += p.bytes;
+    }
+    c->pending.clear();
+    c->event_next = 0;
+}
+
+enum ggml_status be_compute(ggml_backend_t b, ggml_cgraph * g) {
+    hip_backend_ctx * c = (hip_backend_ctx *) b->context;
+    hip_device & d = dev(c->device);
+    executor ex(*c, g);
+    ex.run();
+    HIP_CHECK(hipStreamSynchronize(d.stream));
+    if (c->profiling) collect_profile(c);
+    return GGML_STATUS_SUCCESS;
+}
+
+void be_sync(ggml_backend_t b) { HIP_CHECK(hipStreamSynchronize(dev(((hip_backend_ctx *) b->context)->device).stream)); }
+
+ggml_backend_t hip_init_by_name(const char * params) { return ggml_backend_hip_init(params ? atoi(params) : 0); }
+
+struct hip_register {
+    hip_register() { ggml_backend_register("HIP", hip_init_by_name); }
+} g_hip_register;
+
+} // namespace
+
+extern "C" {
+
+int ggml_backend_hip_get_device_count(void) { return device_count(); }
+
+void ggml_backend_hip_get_device_description(int device, char * description, size_t description_size) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, device) != hipSuccess) {
+        (void) hipGetLastError();
+        snprintf(description, description_size, "unavailable");
+        return;
+    }
+    snprintf(description, description_size, "%s (%s, %d CUs, %.0f GiB)", p.name, p.gcnArchName, p.multiProcessorCount,
+             p.totalGlobalMem / 1073741824.0);
+}
+
+ggml_backend_buffer_type_t ggml_backend_hip_buffer_type(int device) {
+    hip_device & d = devices()[device];
+    if (!d.buft.context) {
+        d.id = device;
+        snprintf(d.name, sizeof(d.name), "HIP%d", device);
+        d.buft.iface = { buft_name, buft_alloc, buft_align, nullptr, buft_is_host, buft_no_reuse };
+        d.buft.context = &d;
+    }
+    return &d.buft;
+}
+
+ggml_backend_t ggml_backend_hip_init(int device) {
+    if (device < 0 || device >= device_count()) return nullptr;
+    dev(device);
+    ggml_backend_hip_buffer_type(device);
+    hip_backend_ctx * c = new hip_backend_ctx();
+    c->device = device;
+    if (getenv("GGML_HIP_NO_FUSION")) c->fusion = false;
+    ggml_backend * b = new ggml_backend();
+    b->iface.get_name = be_name;
+    b->iface.free = be_free;
+    b->iface.get_default_buffer_type = be_buft;
+    b->iface.graph_compute = be_compute;
+    b->iface.synchronize = be_sync;
+    b->context = c;
+    return b;
+}
+
+bool ggml_backend_is_hip(ggml_backend_t backend) { return backend && backend->iface.graph_compute == be_compute; }
+
+void ggml_backend_hip_set_fusion(ggml_backend_t backend, bool enable) {
+    if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->fusion = enable;
+}
+void ggml_backend_hip_set_graph_replay(ggml_backend_t backend, bool enable) {
+    if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->graph_replay = enable;
+}
+void ggml_backend_hip_set_profiling(ggml_backend_t backend, bool enable) {
+    if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->profiling = enable;
+}
+void ggml_backend_hip_reset_profile(ggml_backend_t backend) {
+    if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->prof.clear();
+}
+int ggml_backend_hip_profile_count(ggml_backend_t backend) {
+    return ggml_backend_is_hip(backend) ? (int) ((hip_backend_ctx *) backend->context)->prof.size() : 0;
+}
+bool ggml_backend_hip_profile_entry(ggml_backend_t backend, int i, char * name, size_t name_size,
+                                    int64_t * launches, double * total_ms, double * total_bytes) {
+    if (!ggml_backend_is_hip(backend)) return false;
+    hip_backend_ctx * c = (hip_backend_ctx *) backend->context;
+    if (i < 0 || i >= (int) c->prof.size()) return false;
+    auto it = c->prof.begin();
+    std::advance(it, i);
+    snprintf(name, name_size, "%s", it->first.c_str());
+    *launches = it->second.launches;
+    *total_ms = it->second.ms;
+    *total_bytes = it->second.bytes;
+    return true;
+}
+
+} // extern "C"

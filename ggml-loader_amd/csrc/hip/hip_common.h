@@ -1,0 +1,78 @@
+// hip_common.h — shared definitions of the gfx950 backend: error checks, wavefront reductions,
+// and the device-side storage layouts of the quantized weight formats.
+//
+// Device weight layouts. A Q4_0 or Q8_0 tensor of nb blocks is stored by this backend as two
+// planes inside the same allocation (same total bytes as the GGUF layout):
+//     [ qs plane: nb x 16 B (Q4_0) or nb x 32 B (Q8_0) ][ d plane: nb x fp16 ]
+// so that a lane's block payload is one (Q4_0) or two (Q8_0) aligned 128-bit loads and a
+// wavefront reads consecutive blocks of a row as one contiguous span. Block b of the tensor
+// (row-major over rows, then blocks within the row) sits at qs + b*QS and d + b. Q4_K keeps the
+// GGUF layout (144-byte blocks are already 16-byte aligned). ggml_backend_tensor_set/get
+// translate between layouts, so callers always see GGUF bytes.
+//
+// Activation ("x") operands of the integer dots are quantized by this backend into:
+//     q8 for Q4_0/Q8_0 weights: int8 qs[K], float d[K/32] (the fp16-rounded block scale, as
+//         ggml's Q8_0 stores it), int32 s[K/32] (sum of the block's int8 values)
+//     q8K for Q4_K weights:    int8 qs[K], float d[K/256], int16 bsums[K/16]
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+
+#define HIP_CHECK(expr)                                                                             \
+    do {                                                                                            \
+        hipError_t err_ = (expr);                                                                   \
+        if (err_ != hipSuccess) {                                                                   \
+            fprintf(stderr, "HIP error %s at %s:%d: %s\n", hipGetErrorName(err_), __FILE__, __LINE__, \
+                    hipGetErrorString(err_));                                                       \
+            abort();                                                                                \
+        }                                                                                           \
+    } while (0)
+
+#define HIP_ABORT(...) do { fprintf(stderr, "ggml-hip: " __VA_ARGS__); fputc('\n', stderr); abort(); } while (0)
+
+constexpr int WAVE = 64;
+
+// byte sizes of the device planes
+constexpr int Q4_0_QS = 16;
+constexpr int Q8_0_QS = 32;
+constexpr int Q4_K_BYTES = 144;
+
+struct q4k_block { __half d; __half dmin; uint8_t scales[12]; uint8_t qs[128]; };
+static_assert(sizeof(q4k_block) == 144, "q4_K block");
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+// sum within aligned groups of G lanes (G a power of two <= 64)
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// round half to even, valid for |v| < 2^22 (the result ggml's nearest_int gives)
+__device__ __forceinline__ int round_half_even(float v) { return __float2int_rn(v); }

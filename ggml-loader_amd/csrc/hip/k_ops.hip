@@ -1,0 +1,491 @@
+// k_ops.hip — normalization, element-wise, RoPE, softmax, copies, row gathers and the generic
+// (non-quantized) mul_mat used off the fused decode path. Arithmetic follows the ggml op
+// semantics the graph encodes (reference model.cpp:1071-1474): RMSNorm sums x*x in double and
+// scales by 1/sqrtf(mean + eps) before the weight multiply; RoPE iterates theta *= theta_scale
+// in float from theta = pos; softmax exponentiates w - max with the sum kept in double.
+#include "kernels.h"
+
+#include "ggml.h"
+
+// ---------------------------------------------------------------------------------------------
+// typed element access
+
+__device__ __forceinline__ float ld(const char * p, int type) {
+    switch (type) {
+        case GGML_TYPE_F32: return *(const float *) p;
+        case GGML_TYPE_F16: return __half2float(*(const __half *) p);
+        case GGML_TYPE_BF16: return __uint_as_float(((uint32_t) *(const uint16_t *) p) << 16);
+        case GGML_TYPE_I32: return (float) *(const int32_t *) p;
+        default: return 0.0f;
+    }
+}
+
+__device__ __forceinline__ void st(char * p, int type, float v) {
+    switch (type) {
+        case GGML_TYPE_F32: *(float *) p = v; break;
+        case GGML_TYPE_F16: *(__half *) p = __float2half_rn(v); break;
+        case GGML_TYPE_BF16: {
+            uint32_t u = __float_as_uint(v);
+            if ((u & 0x7fffffffu) > 0x7f800000u) u = (u >> 16) | 64u;
+            else u = (u + (0x7fffu + ((u >> 16) & 1u))) >> 16;
+            *(uint16_t *) p = (uint16_t) u;
+            break;
+        }
+        case GGML_TYPE_I32: *(int32_t *) p = (int32_t) v; break;
+        default: break;
+    }
+}
+
+struct idx4 { int64_t i0, i1, i2, i3; };
+
+__device__ __forceinline__ idx4 unflatten(int64_t i, const int64_t ne[4]) {
+    idx4 r;
+    r.i0 = i % ne[0]; i /= ne[0];
+    r.i1 = i % ne[1]; i /= ne[1];
+    r.i2 = i % ne[2]; i /= ne[2];
+    r.i3 = i;
+    return r;
+}
+
+__device__ __forceinline__ char * at(const tview & t, int64_t i0, int64_t i1, int64_t i2, int64_t i3) {
+    return t.data + i0 * t.nb[0] + i1 * t.nb[1] + i2 * t.nb[2] + i3 * t.nb[3];
+}
+
+static int64_t nelem(const tview & t) { return t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3]; }
+
+static unsigned grid1(int64_t n, int threads) { return (unsigned) ((n + threads - 1) / threads); }
+
+// ---------------------------------------------------------------------------------------------
+// RMSNorm (+ weight multiply, + activation quantization)
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+template <int QUANT> // 0 none, 1 Q8_0 (32-blocks), 2 Q8_K (256-blocks)
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float * __restrict__ x, int64_t x_stride,
+        const float * __restrict__ w, float * __restrict__ y, int64_t y_stride, int64_t n, float eps,
+        q8_act q8, q8k_act q8k) {
+    __shared__ double s_part[4];
+    __shared__ float s_fx[4];
+    __shared__ int s_ix[4];
+    __shared__ float s_vx[4];
+    const int64_t row = blockIdx.x;
+    const float * xr = x + row * x_stride;
+    float * yr = y + row * y_stride;
+    const int t = threadIdx.x;
+    double sum = 0.0;
+    for (int64_t i = t; i < n; i += 256) sum += (double) (xr[i] * xr[i]);
+    sum = wave_sum_d(sum);
+    if ((t % 64) == 0) s_part[t / 64] = sum;
+    __syncthreads();
+    const double total = s_part[0] + s_part[1] + s_part[2] + s_part[3];
+    const float mean = (float) (total / (double) n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t i0 = 0; i0 < n; i0 += 256) {
+        const int64_t i = i0 + t;
+        float v = 0.0f;
+        if (i < n) {
+            v = xr[i] * scale;
+            if (w) v = v * w[i];
+            yr[i] = v;
+        }
+        if (QUANT == 1) {
+            // 32 consecutive elements live in 32 consecutive lanes
+            const float amax = group_max<32>(fabsf(v));
+            const float dd = amax / 127;
+            const float id = dd ? 1.0f / dd : 0.0f;
+            const int q = (int) roundf(v * id);
+            const float qsum = group_sum<32>((float) q);
+            if (i < n) {
+                q8.qs[row * n + i] = (int8_t) q;
+                if ((i % 32) == 0) {
+                    q8.d[row * (n / 32) + i / 32] = __half2float(__float2half_rn(dd));
+                    q8.s[row * (n / 32) + i / 32] = (int32_t) qsum;
+                }
+            }
+        } else if (QUANT == 2) {
+            // one super-block of 256 per iteration; max magnitude with the lowest index on ties
+            float ax = fabsf(v);
+            int idx = t;
+            float val = v;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ax2 = __shfl_xor(ax, o, WAVE);
+                const int idx2 = __shfl_xor(idx, o, WAVE);
+                const float val2 = __shfl_xor(val, o, WAVE);
+                if (ax2 > ax || (ax2 == ax && idx2 < idx)) { ax = ax2; idx = idx2; val = val2; }
+            }
+            __syncthreads();
+            if ((t % 64) == 0) { s_fx[t / 64] = ax; s_ix[t / 64] = idx; s_vx[t / 64] = val; }
+            __syncthreads();
+            float bax = s_fx[0], bval = s_vx[0];
+            int bidx = s_ix[0];
+            for (int wv = 1; wv < 4; wv++) {
+                if (s_fx[wv] > bax || (s_fx[wv] == bax && s_ix[wv] < bidx)) { bax = s_fx[wv]; bidx = s_ix[wv]; bval = s_vx[wv]; }
+            }
+            int q = 0;
+            const int64_t sb = i0 / 256;
+            if (bax != 0.0f) {
+                const float iscale = -127.f / bval;
+                q = round_half_even(iscale * v);
+                q = q < 127 ? q : 127;
+                if (t == 0) q8k.d[row * (n / 256) + sb] = 1 / iscale;
+            } else if (t == 0) {
+                q8k.d[row * (n / 256) + sb] = 0.0f;
+            }
+            q8k.qs[row * n + i] = (int8_t) q;
+            const float bs = group_sum<16>((float) q);
+            if ((t % 16) == 0) q8k.bsums[row * (n / 16) + i / 16] = (int16_t) bs;
+        }
+    }
+}
+
+void launch_rms_norm(const float * x, int64_t x_stride, const float * w, float * y, int64_t y_stride,
+                     int64_t n, int64_t ncols, float eps, const q8_act * q8, const q8k_act * q8k, hipStream_t st) {
+    q8_act a{};
+    q8k_act b{};
+    if (q8) {
+        if (n % 32) HIP_ABORT("rms_norm: q8 output needs n %% 32 == 0");
+        a = *q8;
+        hipLaunchKernelGGL(rms_norm_kernel<1>, dim3((unsigned) ncols), dim3(256), 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    } else if (q8k) {
+        if (n % 256) HIP_ABORT("rms_norm: q8K output needs n %% 256 == 0");
+        b = *q8k;
+        hipLaunchKernelGGL(rms_norm_kernel<2>, dim3((unsigned) ncols), dim3(256), 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    } else {
+        hipLaunchKernelGGL(rms_norm_kernel<0>, dim3((unsigned) ncols), dim3(256), 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    }
+    HIP_CHECK(hipGetLastError());
+}
+
+// generic strided: one block per row (i1, i2, i3)
+__global__ __launch_bounds__(256) void rms_norm_strided_kernel(tview x, tview y, float eps) {
+    __shared__ double s_part[4];
+    const int64_t r = blockIdx.x;
+    const int64_t i1 = r % x.ne[1], i2 = (r / x.ne[1]) % x.ne[2], i3 = r / (x.ne[1] * x.ne[2]);
+    const int t = threadIdx.x;
+    double sum = 0.0;
+    for (int64_t i = t; i < x.ne[0]; i += 256) {
+        const float v = *(const float *) at(x, i, i1, i2, i3);
+        sum += (double) (v * v);
+    }
+    sum = wave_sum_d(sum);
+    if ((t % 64) == 0) s_part[t / 64] = sum;
+    __syncthreads();
+    const double total = s_part[0] + s_part[1] + s_part[2] + s_part[3];
+    const float mean = (float) (total / (double) x.ne[0]);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t i = t; i < x.ne[0]; i += 256) {
+        *(float *) at(y, i, i1, i2, i3) = *(const float *) at(x, i, i1, i2, i3) * scale;
+    }
+}
+
+void launch_rms_norm_strided(const tview & x, const tview & y, float eps, hipStream_t st) {
+    const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
+    hipLaunchKernelGGL(rms_norm_strided_kernel, dim3((unsigned) rows), dim3(256), 0, st, x, y, eps);
+    HIP_CHECK(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------------
+// element-wise
+
+__global__ void binary_kernel(int op, tview a, tview b, tview d, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const idx4 k = unflatten(i, d.ne);
+    const float x = ld(at(a, k.i0, k.i1, k.i2, k.i3), a.type);
+    const float y = ld(at(b, k.i0 % b.ne[0], k.i1 % b.ne[1], k.i2 % b.ne[2], k.i3 % b.ne[3]), b.type);
+    st(at(d, k.i0, k.i1, k.i2, k.i3), d.type, op == 0 ? x + y : x * y);
+}
+
+void launch_binary(int op, const tview & a, const tview & b, const tview & dst, hipStream_t st) {
+    const int64_t n = nelem(dst);
+    if (n == 0) return;
+    hipLaunchKernelGGL(binary_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, op, a, b, dst, n);
+    HIP_CHECK(hipGetLastError());
+}
+
+__global__ void unary_kernel(int op, float s, tview a, tview d, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const idx4 k = unflatten(i, d.ne);
+    const float x = ld(at(a, k.i0, k.i1, k.i2, k.i3), a.type);
+    float y;
+    switch (op) {
+        case 0: y = x / (1.0f + expf(-x)); break;
+        case 1: y = x > 0.0f ? x : 0.0f; break;
+        case 2: y = 1.0f / (1.0f + expf(-x)); break;
+        case 3: y = x * x; break;
+        default: y = x * s; break;
+    }
+    st(at(d, k.i0, k.i1, k.i2, k.i3), d.type, y);
+}
+
+void launch_unary(int op, float s, const tview & a, const tview & dst, hipStream_t st) {
+    const int64_t n = nelem(dst);
+    if (n == 0) return;
+    hipLaunchKernelGGL(unary_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, op, s, a, dst, n);
+    HIP_CHECK(hipGetLastError());
+}
+
+// element i (row-major over the src shape) -> element i (row-major over the dst shape)
+__global__ void cpy_kernel(tview s, tview d, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const idx4 a = unflatten(i, s.ne);
+    const idx4 b = unflatten(i, d.ne);
+    const char * sp = at(s, a.i0, a.i1, a.i2, a.i3);
+    char * dp = at(d, b.i0, b.i1, b.i2, b.i3);
+    if (s.type == d.type) {
+        if (s.type == GGML_TYPE_F32 || s.type == GGML_TYPE_I32) *(uint32_t *) dp = *(const uint32_t *) sp;
+        else *(uint16_t *) dp = *(const uint16_t *) sp;
+    } else {
+        st(dp, d.type, ld(sp, s.type));
+    }
+}
+
+void launch_cpy(const tview & src, const tview & dst, hipStream_t st) {
+    const int64_t n = nelem(src);
+    if (n == 0) return;
+    hipLaunchKernelGGL(cpy_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, src, dst, n);
+    HIP_CHECK(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------------
+// get_rows: dst[:, i10, i11, i12] = dequant(a[:, ids[i10, i11, i12], i11, i12])
+
+__global__ void get_rows_kernel(tview a, tview ids, tview d, const uint8_t * qs, const __half * dpl, int64_t first_block) {
+    const int64_t r = blockIdx.x;
+    const int64_t i10 = r % ids.ne[0], i11 = (r / ids.ne[0]) % ids.ne[1], i12 = r / (ids.ne[0] * ids.ne[1]);
+    const int32_t row = *(const int32_t *) at(ids, i10, i11, i12, 0);
+    const int64_t ne00 = a.ne[0];
+    float * out = (float *) at(d, 0, i10, i11, i12);
+    const int64_t byte_off = row * a.nb[1] + i11 * a.nb[2] + i12 * a.nb[3];
+    for (int64_t e = threadIdx.x; e < ne00; e += blockDim.x) {
+        float v;
+        switch (a.type) {
+            case GGML_TYPE_Q4_0: {
+                const int64_t blk = first_block + byte_off / 18 + e / 32;
+                const int j = (int) (e % 32);
+                const uint8_t b = qs[blk * Q4_0_QS + (j & 15)];
+                const int q = j < 16 ? (b & 0x0F) : (b >> 4);
+                v = (float) (q - 8) * __half2float(dpl[blk]);
+                break;
+            }
+            case GGML_TYPE_Q8_0: {
+                const int64_t blk = first_block + byte_off / 34 + e / 32;
+                v = (float) (int8_t) qs[blk * Q8_0_QS + e % 32] * __half2float(dpl[blk]);
+                break;
+            }
+            case GGML_TYPE_Q4_K: {
+                const q4k_block * b = (const q4k_block *) (a.data + byte_off) + e / 256;
+                const int k = (int) (e % 256);
+                const int j = k / 32;     // sub-block
+                const int l = k % 32;
+                const uint8_t * s = b->scales;
+                int sc, m;
+                if (j < 4) { sc = s[j] & 63; m = s[j + 4] & 63; }
+                else { sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4); m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+                const uint8_t qb = b->qs[32 * (j / 2) + l];
+                const int q = (j & 1) ? (qb >> 4) : (qb & 0x0F);
+                const float dd = __half2float(b->d) * (float) sc;
+                const float mm = __half2float(b->dmin) * (float) m;
+                v = dd * (float) q - mm;
+                break;
+            }
+            default:
+                v = ld(a.data + byte_off + e * a.nb[0], a.type);
+                break;
+        }
+        out[e] = v;
+    }
+}
+
+void launch_get_rows(const tview & a, const tview & ids, const tview & dst, const uint8_t * qs_plane,
+                     const __half * d_plane, int64_t first_block, hipStream_t st) {
+    const int64_t rows = ids.ne[0] * ids.ne[1] * ids.ne[2];
+    if (rows == 0) return;
+    hipLaunchKernelGGL(get_rows_kernel, dim3((unsigned) rows), dim3(256), 0, st, a, ids, dst, qs_plane, d_plane, first_block);
+    HIP_CHECK(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------------
+// RoPE: one thread per rotated pair of one (head, token) row
+
+__device__ __forceinline__ void rope_cs(float theta_extrap, const rope_params & p, int i0, float & c, float & s) {
+    const float theta_interp = p.freq_scale * theta_extrap;
+    float theta = theta_interp;
+    float mscale = p.attn_factor;
+    if (p.ext_factor != 0.0f) {
+        const float y = (i0 / 2 - p.corr_dims[0]) / fmaxf(0.001f, p.corr_dims[1] - p.corr_dims[0]);
+        const float ramp = 1 - fminf(1, fmaxf(0, y));
+        const float ramp_mix = ramp * p.ext_factor;
+        theta = theta_interp * (1 - ramp_mix) + theta_extrap * ramp_mix;
+        mscale *= 1.0f + 0.1f * logf(1.0f / p.freq_scale);
+    }
+    c = cosf(theta) * mscale;
+    s = sinf(theta) * mscale;
+}
+
+__global__ void rope_kernel(tview x, const int32_t * __restrict__ pos, const float * __restrict__ ff, tview d, rope_params p, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t half = x.ne[0] / 2;
+    const int64_t ip = i % half;
+    int64_t r = i / half;
+    const int64_t i1 = r % x.ne[1]; r /= x.ne[1];
+    const int64_t i2 = r % x.ne[2]; r /= x.ne[2];
+    const int64_t i3 = r;
+    const int i0 = (int) (2 * ip);
+    if (i0 >= p.n_dims) {
+        for (int k = 0; k < 2; k++) *(float *) at(d, i0 + k, i1, i2, i3) = *(const float *) at(x, i0 + k, i1, i2, i3);
+        return;
+    }
+    // theta after i0/2 multiplications by theta_scale, in float, as the CPU cache builds it
+    float theta = (float) pos[i2];
+    for (int k = 0; k < i0 / 2; k++) theta *= p.theta_scale;
+    const float f = ff ? ff[i0 / 2] : 1.0f;
+    float c, s;
+    rope_cs(theta / f, p, i0, c, s);
+    int64_t a0, a1;
+    if (p.mode & GGML_ROPE_TYPE_NEOX) { a0 = i0 / 2; a1 = i0 / 2 + p.n_dims / 2; }
+    else { a0 = i0; a1 = i0 + 1; }
+    const float x0 = *(const float *) at(x, a0, i1, i2, i3);
+    const float x1 = *(const float *) at(x, a1, i1, i2, i3);
+    *(float *) at(d, a0, i1, i2, i3) = x0 * c - x1 * s;
+    *(float *) at(d, a1, i1, i2, i3) = x0 * s + x1 * c;
+}
+
+void launch_rope(const tview & src, const int32_t * pos, const float * freq_factors, const tview & dst,
+                 const rope_params & p, hipStream_t st) {
+    const int64_t n = nelem(src) / 2;
+    if (n == 0) return;
+    hipLaunchKernelGGL(rope_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, src, pos, freq_factors, dst, p, n);
+    HIP_CHECK(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------------
+// softmax over ne0 of each row: y = exp(w - max) / sum, w = x*scale + slope*mask
+
+__global__ __launch_bounds__(256) void soft_max_kernel(tview a, tview m, int has_mask, tview d, float scale,
+                                                        float m0, float m1, uint32_t n_head_log2, float max_bias) {
+    __shared__ float s_red[4];
+    __shared__ double s_sum[4];
+    const int64_t r = blockIdx.x;
+    const int64_t i1 = r % a.ne[1], i2 = (r / a.ne[1]) % a.ne[2], i3 = r / (a.ne[1] * a.ne[2]);
+    const int t = threadIdx.x;
+    const int64_t nc = a.ne[0];
+    float slope = 1.0f;
+    if (max_bias > 0.0f) {
+        const uint32_t h = (uint32_t) i2;
+        slope = h < n_head_log2 ? powf(m0, (float) (h + 1)) : powf(m1, (float) (2 * (h - n_head_log2) + 1));
+    }
+    float mx = -INFINITY;
+    for (int64_t i = t; i < nc; i += 256) {
+        float w = *(const float *) at(a, i, i1, i2, i3) * scale;
+        if (has_mask) w += slope * ld(at(m, i, i1, i2 % m.ne[2], i3 % m.ne[3]), m.type);
+        *(float *) at(d, i, i1, i2, i3) = w;
+        mx = fmaxf(mx, w);
+    }
+    mx = wave_max(mx);
+    if ((t % 64) == 0) s_red[t / 64] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    double sum = 0.0;
+    for (int64_t i = t; i < nc; i += 256) {
+        float * p = (float *) at(d, i, i1, i2, i3);
+        const float v = expf(*p - mx);
+        *p = v;
+        sum += (double) v;
+    }
+    sum = wave_sum_d(sum);
+    if ((t % 64) == 0) s_sum[t / 64] = sum;
+    __syncthreads();
+    const double total = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
+    const float inv = (float) (1.0 / total);
+    for (int64_t i = t; i < nc; i += 256) *(float *) at(d, i, i1, i2, i3) *= inv;
+}
+
+void launch_soft_max(const tview & a, const tview * mask, const tview & dst, float scale, float max_bias, hipStream_t st) {
+    const int64_t rows = a.ne[1] * a.ne[2] * a.ne[3];
+    const uint32_t n_head = (uint32_t) a.ne[2];
+    const uint32_t n_head_log2 = n_head ? 1u << (uint32_t) floor(log2((double) n_head)) : 1u;
+    const float m0 = powf(2.0f, -(max_bias) / n_head_log2);
+    const float m1 = powf(2.0f, -(max_bias / 2.0f) / n_head_log2);
+    tview m{};
+    if (mask) m = *mask;
+    hipLaunchKernelGGL(soft_max_kernel, dim3((unsigned) rows), dim3(256), 0, st, a, m, mask ? 1 : 0, dst, scale, m0, m1, n_head_log2, max_bias);
+    HIP_CHECK(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------------
+// argmax of each row (first index of the maximum)
+
+__global__ __launch_bounds__(256) void argmax_kernel(tview a, int32_t * out) {
+    __shared__ float s_v[4];
+    __shared__ int s_i[4];
+    const int64_t r = blockIdx.x;
+    const int t = threadIdx.x;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int64_t i = t; i < a.ne[0]; i += 256) {
+        const float v = *(const float *) at(a, i, r, 0, 0);
+        if (v > bv) { bv = v; bi = (int) i; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = __shfl_xor(bv, o, WAVE);
+        const int i2 = __shfl_xor(bi, o, WAVE);
+        if (v2 > bv || (v2 == bv && i2 < bi)) { bv = v2; bi = i2; }
+    }
+    if ((t % 64) == 0) { s_v[t / 64] = bv; s_i[t / 64] = bi; }
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < 4; w++) if (s_v[w] > bv || (s_v[w] == bv && s_i[w] < bi)) { bv = s_v[w]; bi = s_i[w]; }
+        if (bi == 0x7fffffff) bi = 0;
+        out[r] = bi;
+    }
+}
+
+void launch_argmax(const tview & a, int32_t * out, hipStream_t st) {
+    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned) a.ne[1]), dim3(256), 0, st, a, out);
+    HIP_CHECK(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------------------------
+// generic mul_mat (F32/F16/BF16 src0, rows contiguous): one wave per output element.
+// src1 is first rounded to src0's type, as ggml converts it to the weight's dot type.
+
+__global__ __launch_bounds__(256) void mul_mat_generic_kernel(tview s0, tview s1, tview d, int64_t n_out) {
+    const int64_t o = (int64_t) blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+    if (o >= n_out) return;
+    const int lane = threadIdx.x % WAVE;
+    const idx4 k = unflatten(o, d.ne);    // (i01, i11, i12, i13)
+    const int64_t r2 = s1.ne[2] / s0.ne[2], r3 = s1.ne[3] / s0.ne[3];
+    const char * a = at(s0, 0, k.i0, k.i2 / r2, k.i3 / r3);
+    const int64_t K = s0.ne[0];
+    float acc = 0.0f;
+    for (int64_t i = lane; i < K; i += WAVE) {
+        const float w = ld(a + i * s0.nb[0], s0.type);
+        float x = *(const float *) at(s1, i, k.i1, k.i2, k.i3);
+        if (s0.type == GGML_TYPE_F16) x = __half2float(__float2half_rn(x));
+        else if (s0.type == GGML_TYPE_BF16) {
+            uint32_t u = __float_as_uint(x);
+            u = (u + (0x7fffu + ((u >> 16) & 1u))) & 0xffff0000u;
+            x = __uint_as_float(u);
+        }
+        acc += w * x;
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) *(float *) at(d, k.i0, k.i1, k.i2, k.i3) = acc;
+}
+
+void launch_mul_mat_generic(const tview & src0, const tview & src1, const tview & dst, hipStream_t st) {
+    const int64_t n = nelem(dst);
+    if (n == 0) return;
+    hipLaunchKernelGGL(mul_mat_generic_kernel, dim3(grid1(n, 4)), dim3(256), 0, st, src0, src1, dst, n);
+    HIP_CHECK(hipGetLastError());
+}

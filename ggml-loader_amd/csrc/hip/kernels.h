@@ -1,0 +1,125 @@
+// kernels.h — host-side launchers of the gfx950 kernels. Every launcher takes plain device
+// pointers, sizes and the stream it enqueues on; shape checks happen in the caller (the graph
+// executor) before launch.
+#pragma once
+
+#include "hip_common.h"
+
+// A strided view of a tensor (ggml ne/nb convention, nb in bytes).
+struct tview {
+    char *  data;
+    int     type;    // ggml_type
+    int64_t ne[4];
+    int64_t nb[4];
+};
+
+// ---------------------------------------------------------------------------------------------
+// weight layout conversion (GGUF bytes <-> device planes), on the stream
+void launch_repack_q(int type, const uint8_t * raw, uint8_t * qs_plane, __half * d_plane,
+                     int64_t nblocks, int64_t first_block, hipStream_t st);
+void launch_unpack_q(int type, uint8_t * raw, const uint8_t * qs_plane, const __half * d_plane,
+                     int64_t nblocks, int64_t first_block, hipStream_t st);
+
+// ---------------------------------------------------------------------------------------------
+// activation quantization of ncols columns of K floats (column c at x + c*x_col_stride floats)
+struct q8_act { int8_t * qs; float * d; int32_t * s; };     // Q8_0 semantics, per-column K / K/32 / K/32
+struct q8k_act { int8_t * qs; float * d; int16_t * bsums; }; // Q8_K semantics, per-column K / K/256 / K/16
+
+void launch_quantize_q8(const float * x, int64_t x_col_stride, int64_t K, int64_t ncols, q8_act out, hipStream_t st);
+void launch_quantize_q8k(const float * x, int64_t x_col_stride, int64_t K, int64_t ncols, q8k_act out, hipStream_t st);
+
+// ---------------------------------------------------------------------------------------------
+// quantized GEMV / small-batch GEMM: y[c][r] = W[r] . x[c] (+ add[c][r]) for up to 4 weight
+// matrices of one type and row length K sharing the same activation (one launch).
+constexpr int GEMV_MAX_MATS = 4;
+
+struct gemv_mat {
+    const uint8_t * w;     // Q4_0/Q8_0: qs plane of the first row; Q4_K: first block
+    const __half *  wd;    // Q4_0/Q8_0: d plane of the first row
+    float *         y;     // output column 0
+    const float *   add;   // optional residual added to the output (nullptr: none)
+    int64_t         y_stride;   // floats between output columns
+    int64_t         add_stride;
+    int32_t         n_rows;
+};
+
+struct gemv_launch {
+    int        type;       // GGML_TYPE_Q4_0 / Q8_0 / Q4_K
+    int        K;
+    int        ncols;
+    int        n_mats;
+    gemv_mat   m[GEMV_MAX_MATS];
+    // activation (already quantized; column c at +c*K int8 and +c*K/32 (q8) or K/256 (q8K) scales)
+    const int8_t *  xq;
+    const float *   xd;
+    const int32_t * xs;    // q8: block sums
+    const int16_t * xbs;   // q8K: 16-wise sums
+    // SwiGLU epilogue: m[0] = gate, m[1] = up (same n_rows); writes act = silu(g) * u to m[0].y
+    // and, when act_q.qs is set, the Q8_0-quantized act (for the following down projection)
+    bool       swiglu;
+    q8_act     act_q;
+};
+
+void launch_gemv(const gemv_launch & L, hipStream_t st);
+
+// ---------------------------------------------------------------------------------------------
+// element-wise / normalization / positional kernels
+
+// y[c] = rmsnorm(x[c]) (* w), for ncols rows of n floats; optional fused activation quantization
+void launch_rms_norm(const float * x, int64_t x_stride, const float * w, float * y, int64_t y_stride,
+                     int64_t n, int64_t ncols, float eps, const q8_act * q8, const q8k_act * q8k, hipStream_t st);
+// generic strided rms_norm over ne0 of every row
+void launch_rms_norm_strided(const tview & x, const tview & y, float eps, hipStream_t st);
+
+// dst = a (op) broadcast(b); op: 0 add, 1 mul
+void launch_binary(int op, const tview & a, const tview & b, const tview & dst, hipStream_t st);
+// unary: 0 silu, 1 relu, 2 sigmoid, 3 sqr, 4 scale(s)
+void launch_unary(int op, float s, const tview & a, const tview & dst, hipStream_t st);
+// element-wise copy with type conversion in row-major element order (shapes may differ)
+void launch_cpy(const tview & src, const tview & dst, hipStream_t st);
+// dst rows = dequantized rows of a selected by I32 ids
+void launch_get_rows(const tview & a, const tview & ids, const tview & dst, const uint8_t * qs_plane,
+                     const __half * d_plane, int64_t first_block, hipStream_t st);
+
+struct rope_params {
+    int   n_dims;
+    int   mode;
+    float freq_scale;
+    float ext_factor;
+    float attn_factor;
+    float corr_dims[2];
+    float theta_scale;     // powf(freq_base, -2/n_dims), evaluated on the host
+};
+void launch_rope(const tview & src, const int32_t * pos, const float * freq_factors, const tview & dst,
+                 const rope_params & p, hipStream_t st);
+
+void launch_soft_max(const tview & a, const tview * mask, const tview & dst, float scale, float max_bias, hipStream_t st);
+void launch_argmax(const tview & a, int32_t * out, hipStream_t st);
+
+// generic F32/F16/BF16 mul_mat (src0 rows contiguous): one wave per output element
+void launch_mul_mat_generic(const tview & src0, const tview & src1, const tview & dst, hipStream_t st);
+
+// ---------------------------------------------------------------------------------------------
+// decode attention over the F16 KV cache: out[h*hd + i, q] for q < n_q, h < n_head
+struct attn_launch {
+    const float *  q;          // Q (post-RoPE) element (i, head, token) at q + i + head*q_nb1 + token*q_nb2 (floats)
+    int64_t        q_nb1, q_nb2;
+    const __half * k;          // K cache: element (i, kv_head, pos) at k + i + kv_head*k_nb1 + pos*k_nb2 (halves)
+    int64_t        k_nb1, k_nb2;
+    const __half * v;
+    int64_t        v_nb1, v_nb2;
+    const void *   mask;       // [n_kv, >= n_q] rows of mask_nb1 bytes; F32 or F16; nullptr = none
+    int            mask_f16;
+    int64_t        mask_nb1;
+    float *        out;        // out + i + head*hd + token*out_nb1 (floats)
+    int64_t        out_nb1;
+    int n_kv, n_q, n_head, n_head_kv, hd;
+    float scale;
+    // split-KV scratch: partial (max, sum, acc[hd]) per (split, head, q)
+    float *        scratch;
+    int64_t        scratch_bytes;
+    // quantized copy of out for the o-projection (Q8_0 semantics), optional
+    q8_act         out_q;
+};
+int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd);
+void launch_attn_decode(const attn_launch & A, hipStream_t st);

@@ -1,0 +1,48 @@
+// ggml-hip.h — the MI355X (gfx950) backend, selected as `--backend hip`.
+//
+// The first three entry points mirror the Vulkan trio init_backend() calls (model.cpp:800-813:
+// ggml_backend_vk_get_device_count / _get_device_description / _init); init_backend("hip") calls
+// these instead. Device memory, weights, the F16 KV cache and activations live in HIP buffers
+// owned by the backend; ggml_backend_graph_compute runs the graph with hand-written gfx950
+// kernels and returns when the results are complete.
+#pragma once
+
+#include "ggml-backend.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// replaces ggml_backend_vk_get_device_count (model.cpp:801)
+GGML_API int  ggml_backend_hip_get_device_count(void);
+// replaces ggml_backend_vk_get_device_description (model.cpp:806)
+GGML_API void ggml_backend_hip_get_device_description(int device, char * description, size_t description_size);
+// replaces ggml_backend_vk_init (model.cpp:808); NULL if the device cannot be opened
+GGML_API ggml_backend_t ggml_backend_hip_init(int device);
+GGML_API bool ggml_backend_is_hip(ggml_backend_t backend);
+GGML_API ggml_backend_buffer_type_t ggml_backend_hip_buffer_type(int device);
+
+// ---- extensions of this backend (no counterpart in the reference) ----
+
+// Graph-level fusion (fused norm+quantize, QKV/gate-up multi-GEMV, rope+KV append, split-KV
+// decode attention). On by default; off runs one kernel per ggml node. Used by the parity tests
+// to check both paths against the oracle.
+GGML_API void ggml_backend_hip_set_fusion(ggml_backend_t backend, bool enable);
+// Replays the per-token launch sequence through a HIP graph when the ggml graph's structure is
+// unchanged from the previous call. On by default.
+GGML_API void ggml_backend_hip_set_graph_replay(ggml_backend_t backend, bool enable);
+
+// Per-kernel timing with HIP events recorded on the backend's own stream. While enabled, every
+// launch of graph_compute is bracketed by events; stats accumulate per kernel name until reset.
+GGML_API void ggml_backend_hip_set_profiling(ggml_backend_t backend, bool enable);
+GGML_API void ggml_backend_hip_reset_profile(ggml_backend_t backend);
+// Number of distinct kernel names recorded.
+GGML_API int  ggml_backend_hip_profile_count(ggml_backend_t backend);
+// Entry i: name, number of launches, total milliseconds, total algorithmic bytes (weights,
+// activations and KV bytes the launches must touch once). Returns false if i is out of range.
+GGML_API bool ggml_backend_hip_profile_entry(ggml_backend_t backend, int i, char * name, size_t name_size,
+                                             int64_t * launches, double * total_ms, double * total_bytes);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,62 @@
+/*
+ * oracle.h — CPU reference (test oracle) for GGML-Loader's per-token forward pass.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the product (ggml-loader_amd/) includes, links or loads
+ * this; only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, and only as
+ * the checker / baseline, never as the thing measured or shipped.
+ *
+ * It restates the arithmetic of ggml's CPU backend (upstream ggml is an un-vendored, absent
+ * submodule in the reference: .gitmodules:1-3), the way GGML-Loader's `--backend cpu` computes
+ * forward_step (model.cpp:790-799, 1496-1597), in plain C with a fixed float operation order
+ * (-ffp-contract=off). It is also registered as the "CPU" ggml backend so the same graph that the
+ * HIP backend runs can be computed here (ggml_backend_cpu_init, include/ggml-cpu.h).
+ *
+ * Pinning status of each primitive is listed in oracle/README.md.
+ */
+#ifndef GGML_LOADER_ORACLE_H
+#define GGML_LOADER_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* IEEE binary16 conversions (round to nearest even) */
+float    oracle_fp16_to_fp32(uint16_t h);
+uint16_t oracle_fp32_to_fp16(float f);
+
+/* reference quantizers (restating ggml quantize_row_*_ref) over k elements */
+void oracle_quantize_q4_0(const float * x, void * y, int64_t k);
+void oracle_quantize_q8_0(const float * x, void * y, int64_t k);
+void oracle_quantize_q4_K(const float * x, void * y, int64_t k);
+void oracle_quantize_q8_K(const float * x, void * y, int64_t k);
+
+/* row decoders (type = ggml type id: 0 f32, 1 f16, 2 q4_0, 8 q8_0, 12 q4_K, 30 bf16); 0 on unknown type */
+int oracle_dequantize(int type, const void * x, float * y, int64_t k);
+
+/* block dot products with the activation already in the weight's dot type */
+float oracle_vec_dot_q4_0_q8_0(int64_t n, const void * x, const void * y);
+float oracle_vec_dot_q8_0_q8_0(int64_t n, const void * x, const void * y);
+float oracle_vec_dot_q4_K_q8_K(int64_t n, const void * x, const void * y);
+
+/* y[r] = W[r] . x for nrows rows of a weight of type `type`, with ggml-cpu's activation
+   quantization (Q4_0/Q8_0 -> Q8_0, Q4_K -> Q8_K, F16 -> F16, F32 exact) */
+void oracle_gemv(int type, const void * w, int64_t nrows, int64_t k, const float * x, float * y, int n_threads);
+
+/* RoPE of one vector of ne0 floats at position pos (ggml_rope_ext semantics, ext_factor 0
+   unless given) */
+void oracle_rope(float * dst, const float * src, int64_t ne0, int n_dims, int mode, int32_t pos,
+                 float freq_base, float freq_scale, float ext_factor, float attn_factor,
+                 float beta_fast, float beta_slow, int n_ctx_orig, const float * freq_factors);
+
+/* MoE router as in the reference's moe_route (qwen_model.c:551-606): softmax over n_expert
+   logits, top-k by insertion (ties keep the lower id), renormalize the k weights */
+void oracle_moe_route(const float * logits, int n_expert, int top_k, int32_t * ids, float * w);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

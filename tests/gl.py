@@ -1,0 +1,207 @@
+"""Test helpers: load the product package and the oracle, build small ggml graphs through the
+C-ABI, and compare results.
+
+The oracle (oracle/_build/libggml-cpu-oracle.so, the CPU restatement of ggml-cpu) is loaded only
+here, in tests, as the checker.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import importlib.util
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG_INIT = os.path.join(ROOT, "ggml-loader_amd", "__init__.py")
+ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "libggml-cpu-oracle.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libmoe_ref.so")
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def load_pkg():
+    if "ggml_loader_amd" in sys.modules:
+        return sys.modules["ggml_loader_amd"]
+    spec = importlib.util.spec_from_file_location("ggml_loader_amd", PKG_INIT)
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["ggml_loader_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+gl = load_pkg()
+_oracle = None
+
+
+def oracle():
+    """The oracle library (also registers the "CPU" ggml backend)."""
+    global _oracle
+    if _oracle is None:
+        gl.libs()
+        if not os.path.exists(ORACLE_SO):
+            raise RuntimeError(f"{ORACLE_SO} missing: run `make -C oracle`")
+        if not gl.libs()["core"].ggml_backend_load(ORACLE_SO.encode()):
+            raise RuntimeError("loading the oracle backend failed")
+        o = C.CDLL(ORACLE_SO, mode=C.RTLD_GLOBAL)
+        vp, i64 = C.c_void_p, C.c_int64
+        o.oracle_fp16_to_fp32.restype = C.c_float
+        o.oracle_fp16_to_fp32.argtypes = [C.c_uint16]
+        o.oracle_fp32_to_fp16.restype = C.c_uint16
+        o.oracle_fp32_to_fp16.argtypes = [C.c_float]
+        for n in ("oracle_quantize_q4_0", "oracle_quantize_q8_0", "oracle_quantize_q4_K", "oracle_quantize_q8_K"):
+            getattr(o, n).restype = None
+            getattr(o, n).argtypes = [vp, vp, i64]
+        o.oracle_dequantize.restype = C.c_int
+        o.oracle_dequantize.argtypes = [C.c_int, vp, vp, i64]
+        for n in ("oracle_vec_dot_q4_0_q8_0", "oracle_vec_dot_q8_0_q8_0", "oracle_vec_dot_q4_K_q8_K"):
+            getattr(o, n).restype = C.c_float
+            getattr(o, n).argtypes = [i64, vp, vp]
+        o.oracle_gemv.restype = None
+        o.oracle_gemv.argtypes = [C.c_int, vp, i64, i64, vp, vp, C.c_int]
+        o.oracle_rope.restype = None
+        o.oracle_rope.argtypes = [vp, vp, i64, C.c_int, C.c_int, C.c_int32] + [C.c_float] * 6 + [C.c_int, vp]
+        o.oracle_moe_route.restype = None
+        o.oracle_moe_route.argtypes = [vp, C.c_int, C.c_int, vp, vp]
+        _oracle = o
+    return _oracle
+
+
+def cpu_backend(n_threads: int = 8):
+    oracle()
+    b = gl.libs()["core"].ggml_backend_init_by_name(b"CPU", str(n_threads).encode())
+    if not b:
+        raise RuntimeError("CPU backend not registered")
+    return b
+
+
+def ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ---- quantization helpers (through the oracle) ----
+BLOCK = {gl.Q4_0: (32, 18), gl.Q8_0: (32, 34), gl.Q4_K: (256, 144), gl.Q8_K: (256, 292)}
+
+
+def quantize(x: np.ndarray, qtype: int, impl: str = "oracle") -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    qk, bs = BLOCK[qtype]
+    assert x.size % qk == 0
+    out = np.zeros(x.size // qk * bs, dtype=np.uint8)
+    if impl == "oracle":
+        fn = {gl.Q4_0: "oracle_quantize_q4_0", gl.Q8_0: "oracle_quantize_q8_0", gl.Q4_K: "oracle_quantize_q4_K",
+              gl.Q8_K: "oracle_quantize_q8_K"}[qtype]
+        getattr(oracle(), fn)(ptr(x), ptr(out), x.size)
+    else:
+        n_per_row = x.shape[-1] if x.ndim > 1 else x.size
+        gl.libs()["core"].ggml_quantize_chunk(qtype, ptr(x), ptr(out), 0, x.size // n_per_row, n_per_row, None)
+    return out
+
+
+def dequantize(q: np.ndarray, qtype: int, n: int, impl: str = "oracle") -> np.ndarray:
+    out = np.zeros(n, dtype=np.float32)
+    q = np.ascontiguousarray(q)
+    if impl == "oracle":
+        assert oracle().oracle_dequantize(qtype, ptr(q), ptr(out), n)
+    else:
+        assert gl.libs()["core"].ggml_dequantize_row(qtype, ptr(q), ptr(out), n)
+    return out
+
+
+def randn(n, seed, std=1.0, mean=0.0):
+    """The product's seeded normal generator (also used by the synthetic models)."""
+    out = np.empty(n, dtype=np.float32)
+    gl.libs()["loader"].gl_fill_normal(out.ctypes.data_as(C.POINTER(C.c_float)), n, seed, 0, mean, std)
+    return out
+
+
+# ---- error metrics ----
+def rel_err(x, ref) -> float:
+    """max |x - ref| / max |ref| (normwise, infinity norm)."""
+    x = np.asarray(x, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = np.max(np.abs(ref))
+    return float(np.max(np.abs(x - ref)) / (den if den > 0 else 1.0))
+
+
+def rel_err_floor(x, ref) -> float:
+    """The reference's per-element convention (test_vulkan.c:103-109): |x-ref| / (|ref| if |ref| > 1e-3 else 1)."""
+    x = np.asarray(x, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = np.where(np.abs(ref) > 1e-3, np.abs(ref), 1.0)
+    return float(np.max(np.abs(x - ref) / den))
+
+
+# ---- graph builder over the C-ABI ----
+class Graph:
+    """One no_alloc ggml context; tensors are allocated on a backend by compute()."""
+
+    def __init__(self, mem: int = 256 << 20):
+        self.core = gl.libs()["core"]
+        self.ctx = self.core.ggml_init(gl.ggml_init_params(mem, None, True))
+        self.inputs = []
+        self.buf = None
+
+    def __getattr__(self, name):
+        # g.mul_mat(a, b) -> ggml_mul_mat(ctx, a, b)
+        fn = getattr(self.core, "ggml_" + name)
+        return lambda *args: fn(self.ctx, *args)
+
+    def tensor(self, ttype, *ne, data=None, name=None):
+        f = {1: self.core.ggml_new_tensor_1d, 2: self.core.ggml_new_tensor_2d, 3: self.core.ggml_new_tensor_3d,
+             4: self.core.ggml_new_tensor_4d}[len(ne)]
+        t = f(self.ctx, ttype, *ne)
+        if name:
+            self.core.ggml_set_name(t, name.encode())
+        if data is not None:
+            self.inputs.append((t, np.ascontiguousarray(data)))
+        return t
+
+    def compute(self, backend, outs):
+        if not isinstance(outs, (list, tuple)):
+            outs = [outs]
+        gf = self.core.ggml_new_graph(self.ctx)
+        for o in outs:
+            self.core.ggml_build_forward_expand(gf, o)
+        self.buf = self.core.ggml_backend_alloc_ctx_tensors(self.ctx, backend)
+        for t, a in self.inputs:
+            assert a.nbytes == self.core.ggml_nbytes(t), (a.nbytes, self.core.ggml_nbytes(t))
+            self.core.ggml_backend_tensor_set(t, ptr(a), 0, a.nbytes)
+        assert self.core.ggml_backend_graph_compute(backend, gf) == 0
+        res = []
+        for o in outs:
+            res.append(self.read(o))
+        return res if len(res) > 1 else res[0]
+
+    def read(self, t, dtype=np.float32):
+        nb = self.core.ggml_nbytes(t)
+        out = np.empty(nb // np.dtype(dtype).itemsize, dtype=dtype)
+        self.core.ggml_backend_tensor_get(t, ptr(out), 0, nb)
+        return out
+
+    def n_nodes(self, outs):
+        gf = self.core.ggml_new_graph(self.ctx)
+        for o in (outs if isinstance(outs, (list, tuple)) else [outs]):
+            self.core.ggml_build_forward_expand(gf, o)
+        return self.core.ggml_graph_n_nodes(gf)
+
+    def close(self):
+        if self.buf:
+            self.core.ggml_backend_buffer_free(self.buf)
+            self.buf = None
+        if self.ctx:
+            self.core.ggml_free(self.ctx)
+            self.ctx = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+def run_on(backend, build):
+    """build(g) -> (outs, raw-dtype) ; returns the computed output(s) on `backend`."""
+    with Graph() as g:
+        outs = build(g)
+        return g.compute(backend, outs)

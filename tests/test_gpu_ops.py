@@ -1,0 +1,285 @@
+"""Op-level parity of the HIP backend against the oracle (CPU restatement of ggml-cpu), through the
+ggml C-ABI: each test builds the same small ggml graph twice and runs it on both backends.
+
+Bars: integer/byte work (weight repack round trips, f32->f16 KV writes, argmax) bit-exact;
+float outputs within max relative error 2e-3 (normwise, rel_err in gl.py). GEMVs, whose block
+integer dots and activation quantization are identical on both sides, are also held to 1e-4.
+"""
+import numpy as np
+import pytest
+
+from gl import Graph, cpu_backend, gl, quantize, rel_err, run_on
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def hip():
+    b = gl.hip_backend(0)
+    yield b
+    gl.libs()["core"].ggml_backend_free(b)
+
+
+@pytest.fixture(scope="module")
+def cpu():
+    b = cpu_backend(16)
+    yield b
+    gl.libs()["core"].ggml_backend_free(b)
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def both(hip, cpu, build, fusion=True):
+    gl.libs()["hip"].ggml_backend_hip_set_fusion(hip, fusion)
+    try:
+        return run_on(hip, build), run_on(cpu, build)
+    finally:
+        gl.libs()["hip"].ggml_backend_hip_set_fusion(hip, True)
+
+
+def qweight(qtype, K, N, seed, std=0.02):
+    w = (rng(seed).standard_normal((N, K)) * std).astype(np.float32)
+    return quantize(w, qtype, impl="product")
+
+
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K])
+def test_weight_repack_roundtrip(hip, qtype):
+    K, N = 512, 96
+    q = qweight(qtype, K, N, 1)
+    with Graph() as g:
+        w = g.tensor(qtype, K, N, data=q)
+        g.compute(hip, [])
+        back = g.read(w, np.uint8)
+    assert np.array_equal(back, q)
+
+
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K, gl.F16, gl.F32])
+def test_get_rows(hip, cpu, qtype):
+    K, N = 512, 40
+    if qtype in (gl.F16, gl.F32):
+        w = (rng(2).standard_normal((N, K)) * 0.1).astype(np.float16 if qtype == gl.F16 else np.float32)
+    else:
+        w = qweight(qtype, K, N, 2, std=0.1)
+    ids = np.array([3, 0, 39, 3, 17], dtype=np.int32)
+
+    def build(g):
+        wt = g.tensor(qtype, K, N, data=w)
+        it = g.tensor(gl.I32, len(ids), data=ids)
+        return g.get_rows(wt, it)
+
+    a, b = both(hip, cpu, build)
+    assert np.array_equal(a, b)  # dequantization is exact on both sides
+
+
+@pytest.mark.parametrize("qtype,K,N", [
+    (gl.Q4_0, 4096, 4096),
+    (gl.Q4_0, 3072, 1024),
+    (gl.Q4_0, 8192, 3072),
+    (gl.Q4_0, 96, 7),
+    (gl.Q8_0, 3072, 640),
+    (gl.Q8_0, 8192, 300),
+    (gl.Q4_K, 2560, 1024),
+    (gl.Q4_K, 9728, 512),
+    (gl.Q4_K, 768, 200),
+])
+@pytest.mark.parametrize("ncols", [1, 3, 8, 13])
+def test_gemv(hip, cpu, qtype, K, N, ncols):
+    w = qweight(qtype, K, N, K + N)
+    x = rng(7).standard_normal((ncols, K)).astype(np.float32)
+
+    def build(g):
+        wt = g.tensor(qtype, K, N, data=w)
+        xt = g.tensor(gl.F32, K, ncols, data=x)
+        return g.mul_mat(wt, xt)
+
+    a, b = both(hip, cpu, build)
+    assert rel_err(a, b) < 1e-4
+
+
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q4_K])
+def test_gemv_residual_and_qkv_group(hip, cpu, qtype):
+    K = 1024
+    Nq, Nk = 1024, 256
+    wq, wk, wv, wo = (qweight(qtype, K, n, s) for n, s in ((Nq, 11), (Nk, 12), (Nk, 13), (K, 14)))
+    x = rng(3).standard_normal((1, K)).astype(np.float32)
+    r = rng(4).standard_normal((1, K)).astype(np.float32)
+
+    def build(g):
+        xt = g.tensor(gl.F32, K, 1, data=x)
+        rt = g.tensor(gl.F32, K, 1, data=r)
+        q = g.mul_mat(g.tensor(qtype, K, Nq, data=wq), xt)
+        k = g.mul_mat(g.tensor(qtype, K, Nk, data=wk), xt)
+        v = g.mul_mat(g.tensor(qtype, K, Nk, data=wv), xt)
+        o = g.add(g.mul_mat(g.tensor(qtype, K, K, data=wo), q), rt)
+        return [q, k, v, o]
+
+    for fusion in (True, False):
+        hs, cs = both(hip, cpu, build, fusion)
+        for a, b in zip(hs, cs):
+            assert rel_err(a, b) < 1e-4
+
+
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K])
+@pytest.mark.parametrize("ncols", [1, 2])
+def test_swiglu_ffn(hip, cpu, qtype, ncols):
+    E, F = 512, 1536
+    wg, wu, wd = qweight(qtype, E, F, 21), qweight(qtype, E, F, 22), qweight(qtype, F, E, 23)
+    x = rng(5).standard_normal((ncols, E)).astype(np.float32)
+    r = rng(6).standard_normal((ncols, E)).astype(np.float32)
+
+    def build(g):
+        xt = g.tensor(gl.F32, E, ncols, data=x)
+        gate = g.mul_mat(g.tensor(qtype, E, F, data=wg), xt)
+        up = g.mul_mat(g.tensor(qtype, E, F, data=wu), xt)
+        act = g.mul(g.silu(gate), up)
+        down = g.mul_mat(g.tensor(qtype, F, E, data=wd), act)
+        return g.add(down, g.tensor(gl.F32, E, ncols, data=r))
+
+    for fusion in (True, False):
+        a, b = both(hip, cpu, build, fusion)
+        assert rel_err(a, b) < 1e-3
+
+
+@pytest.mark.parametrize("n,rows", [(3072, 1), (2560, 3), (128, 40), (96, 7)])
+def test_rms_norm_mul_then_gemv(hip, cpu, n, rows):
+    x = rng(8).standard_normal((rows, n)).astype(np.float32) * 3
+    w = (1 + 0.01 * rng(9).standard_normal(n)).astype(np.float32)
+    qtype = gl.Q4_K if n % 256 == 0 else gl.Q4_0
+    W = qweight(qtype, n, 64, 10)
+
+    def build(g):
+        xt = g.tensor(gl.F32, n, rows, data=x)
+        y = g.mul(g.rms_norm(xt, 1e-5), g.tensor(gl.F32, n, data=w))
+        return [y, g.mul_mat(g.tensor(qtype, n, 64, data=W), y)]
+
+    for fusion in (True, False):
+        (y1, z1), (y2, z2) = both(hip, cpu, build, fusion)
+        assert rel_err(y1, y2) < 1e-5
+        assert rel_err(z1, z2) < 1e-4
+
+
+@pytest.mark.parametrize("mode", [gl.ROPE_NORMAL, gl.ROPE_NEOX])
+@pytest.mark.parametrize("hd,n_head,theta", [(128, 8, 500000.0), (128, 4, 1e6), (96, 4, 10000.0)])
+def test_rope(hip, cpu, mode, hd, n_head, theta):
+    pos = np.array([0, 1, 7, 2048, 8191], dtype=np.int32)
+    x = rng(11).standard_normal((len(pos), n_head, hd)).astype(np.float32)
+
+    def build(g):
+        xt = g.tensor(gl.F32, hd, n_head, len(pos), data=x)
+        pt = g.tensor(gl.I32, len(pos), data=pos)
+        return g.rope_ext(xt, pt, None, hd, mode, 4096, theta, 1.0, 0.0, 1.0, 0.0, 0.0)
+
+    a, b = both(hip, cpu, build)
+    assert rel_err(a, b) < 1e-4
+
+
+def test_soft_max_masked(hip, cpu):
+    n_kv, n_q, n_head = 300, 3, 5
+    x = rng(12).standard_normal((n_head, n_q, n_kv)).astype(np.float32) * 4
+    mask = np.zeros((n_q, n_kv), dtype=np.float32)
+    for q in range(n_q):
+        mask[q, n_kv - n_q + q + 1:] = -np.inf
+
+    def build(g):
+        xt = g.tensor(gl.F32, n_kv, n_q, n_head, data=x)
+        mt = g.tensor(gl.F32, n_kv, n_q, data=mask)
+        return g.soft_max_ext(xt, mt, 0.125, 0.0)
+
+    a, b = both(hip, cpu, build)
+    assert rel_err(a, b) < 1e-5
+
+
+def test_kv_append_f16_exact(hip, cpu):
+    hd, nkv, n_ctx, n_past, n_new = 128, 8, 64, 17, 3
+    cache = np.zeros((n_ctx, nkv, hd), dtype=np.float16)
+    src = rng(13).standard_normal((n_new, nkv, hd)).astype(np.float32) * 10
+
+    def build(g):
+        c = g.tensor(gl.F16, hd, nkv, n_ctx, data=cache)
+        s = g.tensor(gl.F32, hd, nkv, n_new, data=src)
+        nb1, nb2 = hd * 2, hd * nkv * 2
+        dst = g.view_3d(c, hd, nkv, n_new, nb1, nb2, n_past * nb2)
+        cp = g.cpy(s, dst)
+        return cp
+
+    a, b = both(hip, cpu, build)
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+    expect = src.astype(np.float16)  # numpy rounds to nearest even
+    assert np.array_equal(a.view(np.uint16).reshape(n_new, nkv, hd), expect.view(np.uint16))
+
+
+def test_argmax(hip, cpu):
+    x = rng(14).standard_normal((3, 5000)).astype(np.float32)
+    x[1, 4000] = x[1, 123] = 50.0  # tie: the first index wins
+
+    def build(g):
+        return g.argmax(g.tensor(gl.F32, 5000, 3, data=x))
+
+    a, b = both(hip, cpu, build)
+    assert np.array_equal(a.view(np.int32), b.view(np.int32))
+    assert a.view(np.int32)[1] == 123
+
+
+def attention_graph(g, hd, n_head, n_head_kv, n_kv, n_new, n_ctx, kc, vc, q, mask, flash=False):
+    """The attention block of build_graph (reference model.cpp:1416-1444)."""
+    K_cache = g.tensor(gl.F16, hd, n_head_kv, n_ctx, data=kc)
+    V_cache = g.tensor(gl.F16, hd, n_head_kv, n_ctx, data=vc)
+    Qcur = g.tensor(gl.F32, hd, n_head, n_new, data=q)
+    m = g.tensor(gl.F32, n_kv, n_new, data=mask)
+    nb1, nb2 = hd * 2, hd * n_head_kv * 2
+    K_full = g.view_3d(K_cache, hd, n_head_kv, n_kv, nb1, nb2, 0)
+    V_full = g.view_3d(V_cache, hd, n_head_kv, n_kv, nb1, nb2, 0)
+    Q = g.permute(Qcur, 0, 2, 1, 3)
+    K = g.permute(K_full, 0, 2, 1, 3)
+    scale = 1.0 / np.sqrt(hd)
+    if flash:
+        V = g.permute(V_full, 0, 2, 1, 3)
+        out = g.flash_attn_ext(Q, K, V, g.cast(m, gl.F16), scale, 0.0, 0.0)
+        return g.cont_2d(out, hd * n_head, n_new)
+    KQ = g.soft_max_ext(g.mul_mat(K, Q), m, scale, 0.0)
+    V_trans = g.cont_3d(g.permute(V_full, 1, 2, 0, 3), n_kv, hd, n_head_kv)
+    KQV = g.mul_mat(V_trans, KQ)
+    return g.cont_2d(g.permute(KQV, 0, 2, 1, 3), hd * n_head, n_new)
+
+
+@pytest.mark.parametrize("hd,n_head,n_head_kv,n_kv,n_new", [
+    (128, 24, 8, 2049, 1),    # Llama-3B shape at position 2048
+    (128, 32, 8, 8193, 1),    # Qwen3 shape at position 8192
+    (128, 32, 4, 4097, 1),    # MoE config attention
+    (96, 32, 32, 130, 1),     # Phi-3 head dim
+    (64, 8, 8, 1, 1),         # first token: output = V
+    (128, 24, 8, 64, 1),
+    (128, 24, 8, 65, 2),
+    (128, 16, 8, 200, 4),
+])
+@pytest.mark.parametrize("flash", [False, True])
+def test_attention_decode(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
+    r = rng(n_kv + hd)
+    n_ctx = n_kv + 3
+    kc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+    vc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+    q = r.standard_normal((n_new, n_head, hd)).astype(np.float32)
+    mask = np.zeros((n_new, n_kv), dtype=np.float32)
+    n_past = n_kv - n_new
+    for i in range(n_new):
+        mask[i, n_past + i + 1:] = -np.inf
+
+    def build(g):
+        return attention_graph(g, hd, n_head, n_head_kv, n_kv, n_new, n_ctx, kc, vc, q, mask, flash)
+
+    for fusion in (True, False):
+        if flash and not fusion:
+            continue
+        a, b = both(hip, cpu, build, fusion)
+        assert rel_err(a, b) < TOL, (fusion, rel_err(a, b))
+    if n_kv == 1:
+        # a single key: the output is that key's V row for every head of the group
+        grp = n_head // n_head_kv
+        expect = np.repeat(vc[0].astype(np.float32), grp, axis=0).reshape(-1)
+        assert rel_err(a, expect) < 1e-6
