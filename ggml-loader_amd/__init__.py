@@ -147,6 +147,7 @@ def _declare(core, hip, loader):
     _sig(core, "ggml_backend_get_default_buffer_type", vp, vp)
     _sig(core, "ggml_backend_init_by_name", vp, C.c_char_p, C.c_char_p)
     _sig(core, "ggml_backend_load", C.c_bool, C.c_char_p)
+    _sig(core, "ggml_backend_set_eval_callback", None, vp, vp, vp)
     _sig(core, "ggml_gallocr_new", vp, vp)
     _sig(core, "ggml_gallocr_free", None, vp)
     _sig(core, "ggml_gallocr_alloc_graph", C.c_bool, vp, vp)

@@ -115,6 +115,10 @@ ggml_backend_buffer_t ggml_backend_alloc_buffer(ggml_backend_t backend, size_t s
 size_t ggml_backend_get_alignment(ggml_backend_t backend) {
     return ggml_backend_buft_get_alignment(ggml_backend_get_default_buffer_type(backend));
 }
+void ggml_backend_set_eval_callback(ggml_backend_t backend, ggml_backend_eval_callback cb, void * user_data) {
+    if (!backend->iface.set_eval_callback) BK_ABORT("backend %s does not report node evaluations", ggml_backend_name(backend));
+    backend->iface.set_eval_callback(backend, cb, user_data);
+}
 void ggml_backend_synchronize(ggml_backend_t backend) { if (backend->iface.synchronize) backend->iface.synchronize(backend); }
 enum ggml_status ggml_backend_graph_compute(ggml_backend_t backend, struct ggml_cgraph * cgraph) {
     enum ggml_status st = backend->iface.graph_compute(backend, cgraph);

@@ -241,11 +241,25 @@ struct act_entry {       // quantized copy of an activation tensor
     int64_t K, ncols;
 };
 
+// fusion switches (all on by default; GGML_HIP_FUSE=<bitmask> narrows them for A/B runs)
+enum fuse_bits {
+    FUSE_NORM   = 1,   // rms_norm -> mul(weight) [+ activation quantization]
+    FUSE_GROUP  = 2,   // mul_mats sharing one input in one launch
+    FUSE_SWIGLU = 4,   // gate/up -> silu -> mul in the GEMV epilogue
+    FUSE_ADD    = 8,   // residual add in the GEMV epilogue
+    FUSE_ATTN   = 16,  // split-KV decode attention
+    FUSE_ACTQ   = 32,  // producers emit the Q8 activation their GEMV consumers read
+    FUSE_ALL    = 63,
+};
+
 struct hip_backend_ctx {
     int device = 0;
     bool fusion = true;
+    int fuse_mask = FUSE_ALL;
     bool graph_replay = true;
     bool profiling = false;
+    ggml_backend_eval_callback cb = nullptr;
+    void * cb_user = nullptr;
     scratch_arena scratch;
     std::map<std::string, prof_entry> prof;
     std::vector<pending_event> pending;
@@ -272,6 +286,16 @@ int dot_kind(int wtype) {
 
 bool is_2d_contig(const ggml_tensor * t) { return t->ne[2] == 1 && t->ne[3] == 1 && ggml_is_contiguous(t); }
 
+// the nodes of one decode-attention chain (anchored at the K^T Q mul_mat)
+struct attn_match {
+    int kq = -1, sm = -1, vt = -1, kqv = -1, pm = -1, ct = -1;
+    const ggml_tensor * kp = nullptr;   // permuted K cache view [hd, n_kv, n_head_kv]
+    const ggml_tensor * qp = nullptr;   // permuted Q [hd, n_q, n_head]
+    const ggml_tensor * vp = nullptr;   // permuted V cache view [n_kv, hd, n_head_kv]
+    const ggml_tensor * mask = nullptr;
+    float scale = 1.0f;
+};
+
 class executor {
 public:
     executor(hip_backend_ctx & ctx, ggml_cgraph * g) : c_(ctx), g_(g), st_(dev(ctx.device).stream) {}
@@ -280,10 +304,24 @@ public:
         c_.scratch.reset();
         index_graph();
         done_.assign(g_->n_nodes, false);
+        attn_.clear();
+        // plan the attention fusions first: the V^T copy precedes K^T Q in node order and must
+        // not run when the chain is replaced
+        if (fuse(FUSE_ATTN)) {
+            for (int i = 0; i < g_->n_nodes; i++) {
+                attn_match m;
+                if (g_->nodes[i]->op == GGML_OP_MUL_MAT && match_attention(i, m)) {
+                    attn_[i] = m;
+                    done_[m.vt] = true;
+                }
+            }
+        }
         for (int i = 0; i < g_->n_nodes; i++) {
             if (done_[i]) continue;
+            wrote_.clear();
             exec_node(i);
             done_[i] = true;
+            if (c_.cb) report();
         }
     }
 
@@ -295,6 +333,17 @@ private:
     std::vector<std::vector<int>> users_;
     std::vector<bool> done_;
     std::unordered_map<const ggml_tensor *, act_entry> act_;
+    std::unordered_map<int, attn_match> attn_;
+    std::vector<const ggml_tensor *> wrote_;
+
+    bool fuse(int bit) const { return c_.fusion && (c_.fuse_mask & bit); }
+
+    void report() {
+        HIP_CHECK(hipStreamSynchronize(st_));
+        for (const ggml_tensor * t : wrote_) {
+            if (!c_.cb((ggml_tensor *) t, false, c_.cb_user)) { c_.cb = nullptr; return; }
+        }
+    }
 
     // ---- graph structure ----
     void index_graph() {
@@ -306,7 +355,9 @@ private:
             const ggml_tensor * n = g_->nodes[i];
             for (int s = 0; s < GGML_MAX_SRC; s++) {
                 if (!n->src[s]) continue;
-                if (s > 0 && n->src[s] == n->src[s - 1]) continue;
+                bool dup = false;
+                for (int r = 0; r < s; r++) dup = dup || n->src[r] == n->src[s];
+                if (dup) continue;
                 auto it = idx_.find(n->src[s]);
                 if (it != idx_.end()) users_[it->second].push_back(i);
             }
@@ -383,7 +434,7 @@ private:
     }
     // the quantized form all consumers of node i want (0: none / mixed / not all quantized mul_mats)
     int wanted_act_kind(int i) const {
-        if (i < 0 || users_[i].empty()) return 0;
+        if (!fuse(FUSE_ACTQ) || i < 0 || users_[i].empty()) return 0;
         int kind = 0;
         for (int u : users_[i]) {
             const ggml_tensor * n = g_->nodes[u];
@@ -403,6 +454,10 @@ private:
                 return;
             case GGML_OP_RMS_NORM: op_rms_norm(i); return;
             case GGML_OP_MUL_MAT: op_mul_mat(i); return;
+            default: break;
+        }
+        wrote_.push_back(n);
+        switch (n->op) {
             case GGML_OP_GET_ROWS: op_get_rows(n); return;
             case GGML_OP_ADD: { prof_scope ps(this, "add", 0); launch_binary(0, tv(n->src[0]), tv(n->src[1]), tv(n), st_); return; }
             case GGML_OP_MUL: { prof_scope ps(this, "mul", 0); launch_binary(1, tv(n->src[0]), tv(n->src[1]), tv(n), st_); return; }
@@ -481,7 +536,7 @@ private:
         memcpy(&eps, n->op_params, 4);
         const ggml_tensor * x = n->src[0];
         const bool rows_ok = x->type == GGML_TYPE_F32 && ggml_is_contiguous(x) && ggml_is_contiguous(n);
-        if (c_.fusion && rows_ok) {
+        if (fuse(FUSE_NORM) && rows_ok) {
             const int u = sole_user(i);
             if (u >= 0) {
                 ggml_tensor * m = g_->nodes[u];
@@ -489,19 +544,21 @@ private:
                 if (m->op == GGML_OP_MUL && m->src[0] == n && w->type == GGML_TYPE_F32 && ggml_nrows(w) == 1 &&
                     w->ne[0] == x->ne[0] && ggml_is_contiguous(w) && ggml_is_contiguous(m)) {
                     const int64_t N = x->ne[0], rows = ggml_nrows(x);
-                    const int kind = wanted_act_kind(u);
+                    const int kind = m->ne[1] == rows ? wanted_act_kind(u) : 0;
                     act_entry e{};
                     const bool q = (kind == 1 && N % 32 == 0) || (kind == 2 && N % 256 == 0);
                     if (q) e = alloc_act(kind, N, rows);
                     prof_scope ps(this, "rms_norm_mul", (double) (N * rows * 8 + N * 4));
                     launch_rms_norm((const float *) x->data, N, (const float *) w->data, (float *) m->data, N, N, rows, eps,
                                     q && kind == 1 ? &e.q8 : nullptr, q && kind == 2 ? &e.q8k : nullptr, st_);
-                    if (q && m->ne[1] == rows) act_[m] = e;
+                    if (q) act_[m] = e;
                     done_[u] = true;
+                    wrote_.push_back(m);
                     return;
                 }
             }
         }
+        wrote_.push_back(n);
         prof_scope ps(this, "rms_norm", 0);
         if (rows_ok) {
             launch_rms_norm((const float *) x->data, x->ne[0], nullptr, (float *) n->data, n->ne[0], x->ne[0], ggml_nrows(x), eps,
@@ -524,7 +581,8 @@ private:
 
     void op_mul_mat(int i) {
         ggml_tensor * n = g_->nodes[i];
-        if (c_.fusion && try_attention(i)) return;
+        auto at = attn_.find(i);
+        if (at != attn_.end()) { run_attention(at->second); return; }
         if (gemv_capable(n)) { op_gemv(i); return; }
         if (ggml_is_quantized(n->src[0]->type)) {
             HIP_ABORT("mul_mat '%s': quantized %s weights with this layout are not supported", n->name, ggml_type_name(n->src[0]->type));
@@ -532,6 +590,7 @@ private:
         if (n->src[1]->type != GGML_TYPE_F32 || n->src[0]->nb[0] != ggml_type_size(n->src[0]->type)) {
             HIP_ABORT("mul_mat '%s': unsupported operand layout", n->name);
         }
+        wrote_.push_back(n);
         prof_scope ps(this, "mul_mat_generic", (double) (ggml_nbytes(n->src[0]) + ggml_nbytes(n->src[1]) + ggml_nbytes(n)));
         launch_mul_mat_generic(tv(n->src[0]), tv(n->src[1]), tv(n), st_);
     }
@@ -543,9 +602,8 @@ private:
         const int wtype = n->src[0]->type;
         const int64_t K = n->src[0]->ne[0], ncols = x->ne[1];
         std::vector<int> group = { i };
-        if (c_.fusion) {
+        if (fuse(FUSE_GROUP)) {
             const int xi = node_index(x);
-            const std::vector<int> & cands = xi >= 0 ? users_[xi] : std::vector<int>();
             std::vector<int> others;
             if (xi < 0) {
                 for (int j = i + 1; j < g_->n_nodes; j++) {
@@ -553,11 +611,12 @@ private:
                     if (m->op == GGML_OP_MUL_MAT && m->src[1] == x) others.push_back(j);
                 }
             } else {
-                for (int j : cands) if (j != i) others.push_back(j);
+                for (int j : users_[xi]) if (j != i) others.push_back(j);
             }
             for (int j : others) {
                 const ggml_tensor * m = g_->nodes[j];
                 if (done_[j] || m->op != GGML_OP_MUL_MAT || m->src[1] != x) continue;
+                if (attn_.count(j)) continue;
                 if (m->src[0]->type != wtype || m->src[0]->ne[0] != K || !gemv_capable(m)) continue;
                 if ((int) group.size() == GEMV_MAX_MATS) break;
                 group.push_back(j);
@@ -566,7 +625,7 @@ private:
 
         // SwiGLU pair inside the group: gate -> silu -> mul(silu, up)
         int gate = -1, up = -1, mulnode = -1;
-        if (c_.fusion && group.size() >= 2) {
+        if (fuse(FUSE_SWIGLU) && group.size() >= 2) {
             for (int a : group) {
                 const int s = sole_user(a);
                 if (s < 0) continue;
@@ -587,7 +646,7 @@ private:
         const int kind = dot_kind(wtype);
         const act_entry * xa = ensure_act(x, kind);
 
-        auto fill_mat = [&](gemv_mat & gm, int j, double & bytes) {
+        auto fill_mat = [&](gemv_mat & gm, int j, double & bytes, bool epilogue) {
             ggml_tensor * mm = g_->nodes[j];
             const ggml_tensor * w = mm->src[0];
             if (is_repacked(w->type)) {
@@ -604,8 +663,9 @@ private:
             gm.add = nullptr;
             gm.add_stride = 0;
             bytes += (double) ggml_nbytes(w) + (double) (w->ne[1] * ncols * 4);
+            const ggml_tensor * written = mm;
             // residual add epilogue
-            const int u = c_.fusion ? sole_user(j) : -1;
+            const int u = (epilogue && fuse(FUSE_ADD)) ? sole_user(j) : -1;
             if (u >= 0) {
                 ggml_tensor * an = g_->nodes[u];
                 if (an->op == GGML_OP_ADD && an->src[0] == mm && an->src[1]->type == GGML_TYPE_F32 &&
@@ -616,8 +676,10 @@ private:
                     gm.add_stride = (int64_t) (an->src[1]->nb[1] / sizeof(float));
                     bytes += (double) (w->ne[1] * ncols * 4);
                     done_[u] = true;
+                    written = an;
                 }
             }
+            if (epilogue) wrote_.push_back(written);
         };
 
         gemv_launch L{};
@@ -626,16 +688,16 @@ private:
         L.ncols = (int) ncols;
         if (kind == 1) { L.xq = xa->q8.qs; L.xd = xa->q8.d; L.xs = xa->q8.s; }
         else { L.xq = xa->q8k.qs; L.xd = xa->q8k.d; L.xbs = xa->q8k.bsums; }
-        double bytes = (double) (K * ncols * 4);
+        const double x_bytes = (double) (K * ncols * 4);
 
         if (gate >= 0) {
             // SwiGLU launch for (gate, up); the rest of the group goes in a second launch
             gemv_launch S = L;
             S.n_mats = 2;
             S.swiglu = true;
-            double sb = bytes;
-            fill_mat(S.m[0], gate, sb);
-            fill_mat(S.m[1], up, sb);
+            double sb = x_bytes;
+            fill_mat(S.m[0], gate, sb, false);
+            fill_mat(S.m[1], up, sb, false);
             ggml_tensor * mn = g_->nodes[mulnode];
             S.m[0].y = (float *) mn->data;
             S.m[0].y_stride = (int64_t) (mn->nb[1] / sizeof(float));
@@ -652,6 +714,7 @@ private:
                                     wtype == GGML_TYPE_Q8_0 ? "gemv_q8_0_swiglu" : "gemv_q4_K_swiglu", sb);
                 launch_gemv(S, st_);
             }
+            wrote_.push_back(mn);
             done_[gate] = done_[up] = done_[mulnode] = true;
             done_[sole_user(gate)] = true; // the silu node
             std::vector<int> rest;
@@ -660,8 +723,9 @@ private:
             if (group.empty()) return;
         }
 
+        double bytes = x_bytes;
         L.n_mats = (int) group.size();
-        for (size_t k = 0; k < group.size(); k++) fill_mat(L.m[k], group[k], bytes);
+        for (size_t k = 0; k < group.size(); k++) fill_mat(L.m[k], group[k], bytes, true);
         {
             prof_scope ps(this, wtype == GGML_TYPE_Q4_0 ? "gemv_q4_0" : wtype == GGML_TYPE_Q8_0 ? "gemv_q8_0" : "gemv_q4_K", bytes);
             launch_gemv(L, st_);
@@ -670,14 +734,14 @@ private:
     }
 
     // K^T Q -> soft_max -> cont(permute(V)) -> V KQ -> permute -> cont  ==>  split-KV attention
-    bool try_attention(int i) {
-        ggml_tensor * kq = g_->nodes[i];
+    bool match_attention(int i, attn_match & M) const {
+        const ggml_tensor * kq = g_->nodes[i];
         const ggml_tensor * kp = kq->src[0];
         const ggml_tensor * qp = kq->src[1];
         if (kp->type != GGML_TYPE_F16 || kp->op != GGML_OP_PERMUTE || qp->type != GGML_TYPE_F32) return false;
         const int sm = sole_user(i);
         if (sm < 0) return false;
-        ggml_tensor * smn = g_->nodes[sm];
+        const ggml_tensor * smn = g_->nodes[sm];
         if (smn->op != GGML_OP_SOFT_MAX || smn->src[0] != kq) return false;
         float scale, max_bias;
         memcpy(&scale, &smn->op_params[0], 4);
@@ -685,7 +749,7 @@ private:
         if (max_bias != 0.0f) return false;
         const int kqv = sole_user(sm);
         if (kqv < 0) return false;
-        ggml_tensor * kqvn = g_->nodes[kqv];
+        const ggml_tensor * kqvn = g_->nodes[kqv];
         if (kqvn->op != GGML_OP_MUL_MAT || kqvn->src[1] != smn) return false;
         const ggml_tensor * vt = kqvn->src[0];
         const int vti = node_index(vt);
@@ -694,26 +758,36 @@ private:
         if (vp->op != GGML_OP_PERMUTE || vp->type != GGML_TYPE_F16) return false;
         const int pm = sole_user(kqv);
         if (pm < 0) return false;
-        ggml_tensor * pmn = g_->nodes[pm];
+        const ggml_tensor * pmn = g_->nodes[pm];
         if (pmn->op != GGML_OP_PERMUTE) return false;
         const int ct = sole_user(pm);
         if (ct < 0) return false;
-        ggml_tensor * ctn = g_->nodes[ct];
+        const ggml_tensor * ctn = g_->nodes[ct];
         if (ctn->op != GGML_OP_CONT || !is_2d_contig(ctn)) return false;
 
-        const int hd = (int) kp->ne[0], n_kv = (int) kp->ne[1], n_head_kv = (int) kp->ne[2];
-        const int n_q = (int) qp->ne[1], n_head = (int) qp->ne[2];
+        const int64_t hd = kp->ne[0], n_kv = kp->ne[1], n_head_kv = kp->ne[2];
+        const int64_t n_q = qp->ne[1], n_head = qp->ne[2];
         if (kp->ne[3] != 1 || qp->ne[3] != 1 || qp->ne[0] != hd) return false;
         if (vp->ne[0] != n_kv || vp->ne[1] != hd || vp->ne[2] != n_head_kv) return false;
         if (kp->nb[0] != 2 || vp->nb[1] != 2 || qp->nb[0] != 4) return false;
         if (n_q < 1 || n_q > 4 || n_head % n_head_kv || n_head / n_head_kv > 8) return false;
         if (hd != 64 && hd != 96 && hd != 128) return false;
-        if (ctn->ne[0] != (int64_t) hd * n_head || ctn->ne[1] != n_q) return false;
+        if (ctn->ne[0] != hd * n_head || ctn->ne[1] != n_q) return false;
         const ggml_tensor * mask = smn->src[1];
         if (mask && (mask->ne[0] != n_kv || mask->nb[0] != ggml_type_size(mask->type))) return false;
-        // 16-byte alignment of the K rows for the staged loads
+        // 16-byte alignment of the K rows for the staged loads; 4-byte V rows for half2 loads
         if (((uintptr_t) kp->data) % 16 || kp->nb[1] % 16 || kp->nb[2] % 16) return false;
+        if (((uintptr_t) vp->data) % 4 || vp->nb[0] % 4 || vp->nb[2] % 4) return false;
+        M.kq = i; M.sm = sm; M.vt = vti; M.kqv = kqv; M.pm = pm; M.ct = ct;
+        M.kp = kp; M.qp = qp; M.vp = vp; M.mask = mask; M.scale = scale;
+        return true;
+    }
 
+    void run_attention(const attn_match & M) {
+        const ggml_tensor * kp = M.kp, * qp = M.qp, * vp = M.vp, * mask = M.mask;
+        ggml_tensor * ctn = g_->nodes[M.ct];
+        const int hd = (int) kp->ne[0], n_kv = (int) kp->ne[1], n_head_kv = (int) kp->ne[2];
+        const int n_q = (int) qp->ne[1], n_head = (int) qp->ne[2];
         attn_launch A{};
         A.q = (const float *) qp->data;
         A.q_nb1 = (int64_t) (qp->nb[2] / 4);
@@ -730,10 +804,10 @@ private:
         A.out = (float *) ctn->data;
         A.out_nb1 = (int64_t) (ctn->nb[1] / 4);
         A.n_kv = n_kv; A.n_q = n_q; A.n_head = n_head; A.n_head_kv = n_head_kv; A.hd = hd;
-        A.scale = scale;
+        A.scale = M.scale;
         A.scratch_bytes = attn_scratch_bytes(n_kv, n_q, n_head, hd);
         A.scratch = (float *) c_.scratch.alloc((size_t) A.scratch_bytes);
-        if (wanted_act_kind(ct) == 1) {
+        if (wanted_act_kind(M.ct) == 1) {
             act_entry e = alloc_act(1, ctn->ne[0], n_q);
             A.out_q = e.q8;
             act_[ctn] = e;
@@ -744,8 +818,8 @@ private:
             prof_scope ps(this, "attn_decode", bytes);
             launch_attn_decode(A, st_);
         }
-        done_[i] = done_[sm] = done_[vti] = done_[kqv] = done_[pm] = done_[ct] = true;
-        return true;
+        done_[M.kq] = done_[M.sm] = done_[M.vt] = done_[M.kqv] = done_[M.pm] = done_[M.ct] = true;
+        wrote_.push_back(ctn);
     }
 
     void op_flash_attn(ggml_tensor * n) {
@@ -761,6 +835,7 @@ private:
                         n_q >= 1 && n_q <= 4 && n_head % n_head_kv == 0 && n_head / n_head_kv <= 8 &&
                         (hd == 64 || hd == 96 || hd == 128) && ggml_is_contiguous(n) &&
                         ((uintptr_t) k->data) % 16 == 0 && k->nb[1] % 16 == 0 && k->nb[2] % 16 == 0 &&
+                        ((uintptr_t) v->data) % 4 == 0 && v->nb[1] % 4 == 0 && v->nb[2] % 4 == 0 &&
                         (!mask || (mask->ne[0] == n_kv && mask->nb[0] == ggml_type_size(mask->type)));
         if (!ok) HIP_ABORT("flash_attn_ext '%s': unsupported configuration", n->name);
         attn_launch A{};
@@ -828,6 +903,12 @@ enum ggml_status be_compute(ggml_backend_t b, ggml_cgraph * g) {
     return GGML_STATUS_SUCCESS;
 }
 
+void be_set_eval_callback(ggml_backend_t b, ggml_backend_eval_callback cb, void * user) {
+    hip_backend_ctx * c = (hip_backend_ctx *) b->context;
+    c->cb = cb;
+    c->cb_user = user;
+}
+
 void be_sync(ggml_backend_t b) { HIP_CHECK(hipStreamSynchronize(dev(((hip_backend_ctx *) b->context)->device).stream)); }
 
 ggml_backend_t hip_init_by_name(const char * params) { return ggml_backend_hip_init(params ? atoi(params) : 0); }
@@ -871,12 +952,14 @@ ggml_backend_t ggml_backend_hip_init(int device) {
     hip_backend_ctx * c = new hip_backend_ctx();
     c->device = device;
     if (getenv("GGML_HIP_NO_FUSION")) c->fusion = false;
+    if (const char * m = getenv("GGML_HIP_FUSE")) c->fuse_mask = atoi(m);
     ggml_backend * b = new ggml_backend();
     b->iface.get_name = be_name;
     b->iface.free = be_free;
     b->iface.get_default_buffer_type = be_buft;
     b->iface.graph_compute = be_compute;
     b->iface.synchronize = be_sync;
+    b->iface.set_eval_callback = be_set_eval_callback;
     b->context = c;
     return b;
 }

@@ -74,5 +74,22 @@ __device__ __forceinline__ float group_max(float v) {
 
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// Transcendentals of the float ops are evaluated in double and rounded once, i.e. the correctly
+// rounded float result (barring astronomically rare double-rounding cases). The CPU oracle defines
+// the same semantics, so RoPE angles, softmax weights and SiLU agree bit-for-bit across backends
+// instead of drifting by the ulp-level differences of two float libm implementations.
+__device__ __forceinline__ float exp_cr(float x) { return (float) exp((double) x); }
+__device__ __forceinline__ float cos_cr(float x) { return (float) cos((double) x); }
+__device__ __forceinline__ float sin_cr(float x) { return (float) sin((double) x); }
+__device__ __forceinline__ float log_cr(float x) { return (float) log((double) x); }
+
 // round half to even, valid for |v| < 2^22 (the result ggml's nearest_int gives)
 __device__ __forceinline__ int round_half_even(float v) { return __float2int_rn(v); }
+
+// Pin a float result in a register before a narrowing conversion. Without it the compiler folds
+// __float2half_rn(a * b) into one v_fma_mixlo_f16, which rounds the exact product to f16 once
+// instead of to float first; the two differ whenever the float product is an f16 rounding tie.
+__device__ __forceinline__ float as_f32(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}

@@ -1,30 +1,55 @@
 // k_attn.hip — split-KV decode attention over the persistent F16 KV cache (GQA).
 //
 // Replaces the graph's KQ = K^T Q -> softmax(KQ*scale + mask) -> V^T-materialization -> V KQ
-// chain (reference model.cpp:1416-1444) for n_q <= 4 query tokens. Semantics kept from that
-// chain: Q is rounded to F16 before the QK dot (ggml converts the F32 operand of an F16 mul_mat),
-// scores are scaled, masked, and softmax-normalized in f32; V is never transposed or copied.
+// chain (reference model.cpp:1416-1444) for n_q <= 4 query tokens, with that chain's arithmetic:
+//   * QK dot: Q rounded to F16 (ggml converts the F32 operand of an F16 mul_mat), products of the
+//     two F16 values (exact in f32) summed in double, the sum rounded to float once;
+//   * softmax over the whole row: w = kq*scale + mask, M = max w, e = exp(w - M), S = sum e in
+//     double, p = e * (float)(1/S), then p rounded to F16 (the operand conversion of the V mul_mat);
+//   * PV: products of F16 p and F16 V (exact in f32) summed in double, rounded to float once.
+// The double sums are exact for these operands in practice, so the result does not depend on the
+// summation order and equals the CPU reference's float. V is read in place (never transposed).
+// This matters beyond the op: the attention output is quantized to Q8_0 for the output
+// projection, and any drift shifts values across int8 rounding boundaries, which the following
+// layers amplify.
 //
-// Pass 1 (grid: splits x kv_heads): one wavefront per (chunk of 64 positions, KV head). The
-// chunk's K rows are staged through LDS (coalesced 16-byte loads; rows padded to 65 dwords so
-// lane t reading row t is conflict-free); lane t then computes the scores of position t for every
-// query head of the GQA group with packed f16 dot products (v_dot2_f32_f16). The chunk's max
-// and exp-sum per head come from wave reductions; the V rows are streamed once (coalesced, two
-// dims per lane) into an unnormalized accumulator per head. Partials (max, sum, acc[hd]) go to
-// scratch. Pass 2 (grid: heads x queries) merges the splits with the usual max-rescaling and
-// writes the output, optionally also as Q8_0 blocks for the output projection.
+// Four launches:
+//   scores   (64-position chunk, KV head) blocks: the chunk's K rows staged through LDS with
+//            coalesced 16-byte loads (rows padded by one dword so lane t reading row t is
+//            conflict-free); one wave per (query, head of the GQA group), lane = position.
+//   softmax  one block per (query, head) row: max, exp, double sum, F16 probabilities.
+//   pv       (chunk, KV head) blocks: V rows staged through LDS; one wave per (query, head),
+//            two dims per lane, double accumulation; partials per chunk.
+//   combine  per (head, query): sum of the chunk partials, output (+ optional Q8_0 blocks).
+// Scratch: scores f32 [n_q][n_head][n_kv], probabilities f32 [n_q][n_head][n_kv],
+// partials f64 [chunks][n_q][n_head][hd].
 #include "kernels.h"
 
 #include "ggml.h"
 
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
 constexpr int ATT_CHUNK = 64;
 constexpr int ATT_MAX_Q = 4;
+constexpr int ATT_THREADS = 256;
+
+struct attn_scratch {
+    float * scores;
+    float * probs;
+    double * parts;
+};
+
+__host__ __device__ inline attn_scratch scratch_of(const attn_launch & A) {
+    const int64_t rows = (int64_t) A.n_q * A.n_head * A.n_kv;
+    attn_scratch s;
+    s.scores = A.scratch;
+    s.probs = s.scores + rows;
+    s.parts = (double *) (s.probs + rows + (rows & 1));
+    return s;
+}
 
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd) {
     const int64_t splits = (n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
-    return splits * (int64_t) n_head * n_q * (hd + 2) * (int64_t) sizeof(float);
+    const int64_t rows = (int64_t) n_q * n_head * n_kv;
+    return (2 * rows + 1) * (int64_t) sizeof(float) + splits * n_q * n_head * hd * (int64_t) sizeof(double);
 }
 
 __device__ __forceinline__ float mask_at(const attn_launch & A, int q, int t) {
@@ -33,132 +58,155 @@ __device__ __forceinline__ float mask_at(const attn_launch & A, int q, int t) {
     return A.mask_f16 ? __half2float(((const __half *) row)[t]) : ((const float *) row)[t];
 }
 
-template <int HD, int G>
-__global__ __launch_bounds__(64) void attn_split_kernel(const attn_launch A) {
-    constexpr int HD2 = HD / 2;          // half2 per row
-    constexpr int STRIDE = HD2 + 1;      // padded LDS row (dwords)
-    __shared__ uint32_t s_k[ATT_CHUNK * STRIDE];
-    __shared__ uint32_t s_q[ATT_MAX_Q][G][HD2];
-    __shared__ float s_p[ATT_MAX_Q][G][ATT_CHUNK];
+__device__ __forceinline__ double wave_sum_dbl(double v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
 
-    const int split = blockIdx.x;
-    const int kvh = blockIdx.y;
-    const int lane = threadIdx.x;
+// stage rows [t0, t0+nt) of a [pos][hd] F16 cache view (row stride nb_pos halves) into LDS rows of
+// STRIDE dwords; rows >= nt are zero
+template <int HD, int STRIDE>
+__device__ __forceinline__ void stage_rows(uint32_t * dst, const __half * base, int64_t nb_pos, int t0, int nt) {
+    constexpr int PIECES = HD / 8;                                   // 16-byte pieces per row
+    constexpr int ITER = ATT_CHUNK * PIECES / ATT_THREADS;
+    uint4 v[ITER];
+#pragma unroll
+    for (int it = 0; it < ITER; it++) {
+        const int pc = threadIdx.x + it * ATT_THREADS;
+        const int r = pc / PIECES, c = pc % PIECES;
+        v[it] = make_uint4(0, 0, 0, 0);
+        if (r < nt) v[it] = *(const uint4 *) (base + (int64_t) (t0 + r) * nb_pos + c * 8);
+    }
+#pragma unroll
+    for (int it = 0; it < ITER; it++) {
+        const int pc = threadIdx.x + it * ATT_THREADS;
+        const int r = pc / PIECES, c = pc % PIECES;
+        uint32_t * d = dst + r * STRIDE + c * 4;
+        d[0] = v[it].x; d[1] = v[it].y; d[2] = v[it].z; d[3] = v[it].w;
+    }
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_launch A) {
+    constexpr int HD2 = HD / 2;
+    constexpr int STRIDE = HD2 + 1;
+    __shared__ uint32_t s_k[ATT_CHUNK * STRIDE];
+    __shared__ float s_q[ATT_MAX_Q * G][HD];
+    const int split = blockIdx.x, kvh = blockIdx.y;
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
     const int t0 = split * ATT_CHUNK;
     const int nt = min(ATT_CHUNK, A.n_kv - t0);
     const int n_q = A.n_q;
+    const attn_scratch S = scratch_of(A);
 
-    // stage this chunk's K rows (16-byte pieces, 4 rows x 16 pieces per wave-wide load at HD=128)
-    constexpr int PIECES = HD / 8; // 8 halves per 16-byte piece
-    for (int pc = lane; pc < ATT_CHUNK * PIECES; pc += 64) {
-        const int r = pc / PIECES, c = pc % PIECES;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (r < nt) v = *(const uint4 *) (A.k + (int64_t) kvh * A.k_nb1 + (int64_t) (t0 + r) * A.k_nb2 + c * 8);
-        uint32_t * dst = s_k + r * STRIDE + c * 4;
-        dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
-    }
-    // queries of this KV head's group, rounded to f16
-    for (int i = lane; i < n_q * G * HD2; i += 64) {
-        const int q = i / (G * HD2), g = (i / HD2) % G, d2 = i % HD2;
-        const int h = kvh * G + g;
-        const float * qp = A.q + (int64_t) h * A.q_nb1 + (int64_t) q * A.q_nb2 + 2 * d2;
-        const __half2 hv = __floats2half2_rn(qp[0], qp[1]);
-        s_q[q][g][d2] = *(const uint32_t *) &hv;
+    stage_rows<HD, STRIDE>(s_k, A.k + (int64_t) kvh * A.k_nb1, A.k_nb2, t0, nt);
+    for (int i = threadIdx.x; i < n_q * G * HD; i += ATT_THREADS) {
+        const int pr = i / HD, d = i % HD;
+        const int q = pr / G, g = pr % G;
+        const float v = A.q[(int64_t) (kvh * G + g) * A.q_nb1 + (int64_t) q * A.q_nb2 + d];
+        s_q[pr][d] = __half2float(__float2half_rn(v));
     }
     __syncthreads();
 
-    float m_loc[ATT_MAX_Q][G];
-    float l_loc[ATT_MAX_Q][G];
-#pragma unroll
-    for (int q = 0; q < ATT_MAX_Q; q++) {
-        if (q >= n_q) break;
-        float sc[G];
-#pragma unroll
-        for (int g = 0; g < G; g++) sc[g] = 0.0f;
+    for (int pr = wave; pr < n_q * G; pr += ATT_THREADS / WAVE) {
+        const int q = pr / G, g = pr % G, h = kvh * G + g;
         if (lane < nt) {
             const uint32_t * kr = s_k + lane * STRIDE;
+            const float * qv = s_q[pr];
+            double acc = 0.0;
 #pragma unroll 8
             for (int d2 = 0; d2 < HD2; d2++) {
-                const uint32_t kk = kr[d2];
-                const f16x2 kv = __builtin_bit_cast(f16x2, kk);
-#pragma unroll
-                for (int g = 0; g < G; g++) {
-                    const f16x2 qv = __builtin_bit_cast(f16x2, s_q[q][g][d2]);
-                    sc[g] = __builtin_amdgcn_fdot2(kv, qv, sc[g], false);
-                }
+                const __half2 k2 = *(const __half2 *) &kr[d2];
+                const float2 kf = __half22float2(k2);
+                acc += (double) (kf.x * qv[2 * d2]);
+                acc += (double) (kf.y * qv[2 * d2 + 1]);
             }
-        }
-        const float mv = lane < nt ? mask_at(A, q, t0 + lane) : -INFINITY;
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float s = lane < nt ? sc[g] * A.scale + mv : -INFINITY;
-            const float m = wave_max(s);
-            const float p = (m == -INFINITY) ? 0.0f : expf(s - m);
-            const float l = wave_sum(p);
-            m_loc[q][g] = m;
-            l_loc[q][g] = l;
-            s_p[q][g][lane] = p;
-        }
-    }
-    __syncthreads();
-
-    // V: lane owns dims (2*lane, 2*lane+1); unnormalized sum of p * v over the chunk
-    const bool has_dim = 2 * lane < HD;
-    float acc[ATT_MAX_Q][G][2];
-    for (int q = 0; q < ATT_MAX_Q; q++)
-#pragma unroll
-        for (int g = 0; g < G; g++) { acc[q][g][0] = 0.0f; acc[q][g][1] = 0.0f; }
-    if (has_dim) {
-        const __half2 * vb = (const __half2 *) (A.v + (int64_t) kvh * A.v_nb1) + lane;
-#pragma unroll 4
-        for (int t = 0; t < nt; t++) {
-            const float2 vf = __half22float2(vb[(int64_t) (t0 + t) * (A.v_nb2 / 2)]);
-#pragma unroll
-            for (int q = 0; q < ATT_MAX_Q; q++) {
-                if (q >= n_q) break;
-#pragma unroll
-                for (int g = 0; g < G; g++) {
-                    const float p = s_p[q][g][t];
-                    acc[q][g][0] += p * vf.x;
-                    acc[q][g][1] += p * vf.y;
-                }
-            }
-        }
-    }
-    // partial layout: [split][q][head] x (max, sum, acc[HD])
-#pragma unroll
-    for (int q = 0; q < ATT_MAX_Q; q++) {
-        if (q >= n_q) break;
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            const int h = kvh * G + g;
-            float * part = A.scratch + (((int64_t) split * n_q + q) * A.n_head + h) * (HD + 2);
-            if (lane == 0) { part[0] = m_loc[q][g]; part[1] = l_loc[q][g]; }
-            if (has_dim) { part[2 + 2 * lane] = acc[q][g][0]; part[3 + 2 * lane] = acc[q][g][1]; }
+            // softmax input as the graph forms it: (float) kq * scale + mask
+            const float s = (float) acc * A.scale + mask_at(A, q, t0 + lane);
+            S.scores[((int64_t) q * A.n_head + h) * A.n_kv + t0 + lane] = s;
         }
     }
 }
 
-// merge the splits of one (head, query); block = HD threads (one per dim)
+// one block per (head, query) row
+__global__ __launch_bounds__(ATT_THREADS) void attn_softmax_kernel(const attn_launch A) {
+    __shared__ float s_m[ATT_THREADS / WAVE];
+    __shared__ double s_s[ATT_THREADS / WAVE];
+    const int h = blockIdx.x, q = blockIdx.y;
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const attn_scratch S = scratch_of(A);
+    const float * sc = S.scores + ((int64_t) q * A.n_head + h) * A.n_kv;
+    float * pr = S.probs + ((int64_t) q * A.n_head + h) * A.n_kv;
+    float m = -INFINITY;
+    for (int t = threadIdx.x; t < A.n_kv; t += ATT_THREADS) m = fmaxf(m, sc[t]);
+    m = wave_max(m);
+    if (lane == 0) s_m[wave] = m;
+    __syncthreads();
+    float M = s_m[0];
+    for (int w = 1; w < ATT_THREADS / WAVE; w++) M = fmaxf(M, s_m[w]);
+    double sum = 0.0;
+    for (int t = threadIdx.x; t < A.n_kv; t += ATT_THREADS) {
+        const float e = M == -INFINITY ? 0.0f : exp_cr(sc[t] - M);
+        pr[t] = e;
+        sum += (double) e;
+    }
+    sum = wave_sum_dbl(sum);
+    if (lane == 0) s_s[wave] = sum;
+    __syncthreads();
+    double tot = 0.0;
+    for (int w = 0; w < ATT_THREADS / WAVE; w++) tot += s_s[w];
+    const float inv = tot > 0.0 ? (float) (1.0 / tot) : 0.0f;
+    for (int t = threadIdx.x; t < A.n_kv; t += ATT_THREADS) pr[t] = __half2float(__float2half_rn(as_f32(pr[t] * inv)));
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch A) {
+    constexpr int HD2 = HD / 2;
+    constexpr int STRIDE = HD2;   // rows read along dims: consecutive lanes, consecutive dwords
+    __shared__ uint32_t s_v[ATT_CHUNK * STRIDE];
+    __shared__ float s_p[ATT_MAX_Q * G][ATT_CHUNK];
+    const int split = blockIdx.x, kvh = blockIdx.y;
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const int t0 = split * ATT_CHUNK;
+    const int nt = min(ATT_CHUNK, A.n_kv - t0);
+    const int n_q = A.n_q;
+    const attn_scratch S = scratch_of(A);
+
+    stage_rows<HD, STRIDE>(s_v, A.v + (int64_t) kvh * A.v_nb1, A.v_nb2, t0, nt);
+    for (int i = threadIdx.x; i < n_q * G * ATT_CHUNK; i += ATT_THREADS) {
+        const int pr = i / ATT_CHUNK, t = i % ATT_CHUNK;
+        const int q = pr / G, g = pr % G;
+        s_p[pr][t] = t < nt ? S.probs[((int64_t) q * A.n_head + kvh * G + g) * A.n_kv + t0 + t] : 0.0f;
+    }
+    __syncthreads();
+
+    for (int pr = wave; pr < n_q * G; pr += ATT_THREADS / WAVE) {
+        const int q = pr / G, g = pr % G, h = kvh * G + g;
+        if (lane < HD2) {
+            double a0 = 0.0, a1 = 0.0;
+#pragma unroll 8
+            for (int t = 0; t < nt; t++) {
+                const float p = s_p[pr][t];
+                const float2 vf = __half22float2(*(const __half2 *) &s_v[t * STRIDE + lane]);
+                a0 += (double) (p * vf.x);
+                a1 += (double) (p * vf.y);
+            }
+            double * part = S.parts + (((int64_t) split * n_q + q) * A.n_head + h) * HD;
+            part[2 * lane] = a0;
+            part[2 * lane + 1] = a1;
+        }
+    }
+}
+
+// sum the chunk partials of one (head, query); block = HD threads (one per dim)
 template <int HD>
 __global__ void attn_combine_kernel(const attn_launch A, int n_splits) {
     const int h = blockIdx.x, q = blockIdx.y, d = threadIdx.x;
-    float m = -INFINITY;
-    for (int s = 0; s < n_splits; s++) {
-        const float * part = A.scratch + (((int64_t) s * A.n_q + q) * A.n_head + h) * (HD + 2);
-        m = fmaxf(m, part[0]);
-    }
-    float l = 0.0f, o = 0.0f;
-    if (m != -INFINITY) {
-        for (int s = 0; s < n_splits; s++) {
-            const float * part = A.scratch + (((int64_t) s * A.n_q + q) * A.n_head + h) * (HD + 2);
-            if (part[0] == -INFINITY) continue;
-            const float w = expf(part[0] - m);
-            l += w * part[1];
-            o += w * part[2 + d];
-        }
-    }
-    const float v = l > 0.0f ? o / l : 0.0f;
+    const attn_scratch S = scratch_of(A);
+    double acc = 0.0;
+    for (int s = 0; s < n_splits; s++) acc += S.parts[(((int64_t) s * A.n_q + q) * A.n_head + h) * HD + d];
+    const float v = (float) acc;
     const int64_t oi = (int64_t) h * HD + d;
     A.out[(int64_t) q * A.out_nb1 + oi] = v;
     if (A.out_q.qs) {
@@ -180,7 +228,11 @@ __global__ void attn_combine_kernel(const attn_launch A, int n_splits) {
 template <int HD, int G>
 static void launch_attn_t(const attn_launch & A, hipStream_t st) {
     const int splits = (A.n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
-    hipLaunchKernelGGL((attn_split_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(64), 0, st, A);
+    hipLaunchKernelGGL((attn_scores_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
+    HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(attn_softmax_kernel, dim3(A.n_head, A.n_q), dim3(ATT_THREADS), 0, st, A);
+    HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL((attn_pv_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
     HIP_CHECK(hipGetLastError());
     hipLaunchKernelGGL(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(HD), 0, st, A, splits);
     HIP_CHECK(hipGetLastError());

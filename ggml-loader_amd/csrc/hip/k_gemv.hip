@@ -3,11 +3,14 @@
 // Q4_0 / Q8_0 / Q4_K integer-dot GEMVs.
 //
 // GEMV mapping: a wavefront owns 64/LPR rows; LPR lanes split a row's blocks (lane l takes blocks
-// l, l+LPR, ...), so one load instruction moves LPR consecutive 16-byte block payloads per row.
-// Each lane decodes its blocks in registers, does the integer dot with v_dot4_i32_i8 against the
-// quantized activation, scales by the block scales, and the LPR partials are combined with
-// cross-lane shuffles. Rows of up to four matrices (e.g. Q, K and V, or gate and up) are
-// concatenated in one grid so one launch streams all of them.
+// l, l+LPR, ...), so one load instruction moves LPR consecutive 16-byte block payloads per row,
+// and every lane issues all of its weight loads before the first use. The column's quantized
+// activation is staged once per workgroup in LDS. Each lane decodes its blocks in registers and
+// does the integer dot with v_dot4_i32_i8; the per-block float terms go to LDS and one lane per
+// row adds them in block order — the float summation order of ggml-cpu's scalar dot kernels, so
+// the GEMV result is the same float as the CPU reference's (the integer parts are exact in any
+// order). Rows of up to four matrices (Q, K and V, or gate and up) are concatenated in one grid
+// so one launch streams all of them; grid.y runs over the activation columns.
 #include "kernels.h"
 
 #include "ggml.h"
@@ -163,6 +166,7 @@ struct gemv_kargs {
     gemv_launch L;
     int total_rows;
     int row_begin[GEMV_MAX_MATS + 1];
+    int rows_per_block;
 };
 
 __device__ __forceinline__ int find_mat(const gemv_kargs & a, int row) {
@@ -172,8 +176,7 @@ __device__ __forceinline__ int find_mat(const gemv_kargs & a, int row) {
     return m;
 }
 
-// integer dot of one Q4_0 block payload (16 bytes of nibbles) with 32 int8 activations;
-// returns sum(q * x) with q in 0..15 (the -8 offset is applied by the caller via the block sum)
+// sum(q * x) over one Q4_0 block with q in 0..15 (the -8 offset is applied through the block sum)
 __device__ __forceinline__ int dot_q4_0_block(const uint4 q, const int4 xa, const int4 xb) {
     int s = 0;
     s = dot4((int) (q.x & 0x0F0F0F0Fu), xa.x, s);
@@ -200,240 +203,321 @@ __device__ __forceinline__ int dot_q8_0_block(const uint4 qa, const uint4 qb, co
     return s;
 }
 
-// 6-bit scale/min j (0..7) of a Q4_K block from its 12 scale bytes held in 3 dwords
-__device__ __forceinline__ void q4k_sc_m(const uint32_t s[3], int j, int & sc, int & m) {
-    const uint8_t * b = (const uint8_t *) s;
+// byte i (0..11) of the 12 Q4_K scale bytes held in three dwords
+__device__ __forceinline__ int sbyte(uint32_t w0, uint32_t w1, uint32_t w2, int i) {
+    const uint32_t w = i < 4 ? w0 : (i < 8 ? w1 : w2);
+    return (int) ((w >> (8 * (i & 3))) & 0xff);
+}
+
+// 6-bit scale/min j (0..7) of a Q4_K block (moe_stream/dequant.c:132-141 layout)
+__device__ __forceinline__ void q4k_sc_m(uint32_t w0, uint32_t w1, uint32_t w2, int j, int & sc, int & m) {
     if (j < 4) {
-        sc = b[j] & 63;
-        m = b[j + 4] & 63;
+        sc = sbyte(w0, w1, w2, j) & 63;
+        m = sbyte(w0, w1, w2, j + 4) & 63;
     } else {
-        sc = (b[j + 4] & 0x0F) | ((b[j - 4] >> 6) << 4);
-        m = (b[j + 4] >> 4) | ((b[j] >> 6) << 4);
+        sc = (sbyte(w0, w1, w2, j + 4) & 0x0F) | ((sbyte(w0, w1, w2, j - 4) >> 6) << 4);
+        m = (sbyte(w0, w1, w2, j + 4) >> 4) | ((sbyte(w0, w1, w2, j) >> 6) << 4);
     }
 }
 
-// partial dot of Q4_K unit u (sub-blocks 2p, 2p+1 of super-block sb) with the Q8_K activation
-__device__ __forceinline__ float q4k_unit(const uint8_t * __restrict__ wrow, int u, const int8_t * __restrict__ xq,
-                                          const float * __restrict__ xd, const int16_t * __restrict__ xbs) {
-    const int sb = u >> 2, p = u & 3;
-    const uint8_t * blk = wrow + (int64_t) sb * Q4_K_BYTES;
+// Per-lane integer partials of Q4_K unit u = (super-block u/4, sub-block pair p = u%4): aux[l] =
+// sum over the pair's 64 elements e with e%8 == l of sc_sub * q4 * q8, mins = the pair's share of
+// sum(bsums * m). (ggml's generic q4_K x q8_K kernel accumulates exactly these integers.)
+__device__ __forceinline__ void q4k_unit_ints(const uint8_t * blk, int p, const int8_t * xq, const int16_t * xbs,
+                                              int aux[8], int & mins) {
     const uint4 hdr = *(const uint4 *) blk;
     const uint4 qa = *(const uint4 *) (blk + 16 + 32 * p);
     const uint4 qb = *(const uint4 *) (blk + 32 + 32 * p);
-    const int8_t * xp = xq + (int64_t) sb * 256 + 64 * p;
-    const int4 x0 = *(const int4 *) (xp + 0);
-    const int4 x1 = *(const int4 *) (xp + 16);
-    const int4 x2 = *(const int4 *) (xp + 32);
-    const int4 x3 = *(const int4 *) (xp + 48);
-    int lo = 0, hi = 0;
-    lo = dot4((int) (qa.x & 0x0F0F0F0Fu), x0.x, lo);
-    lo = dot4((int) (qa.y & 0x0F0F0F0Fu), x0.y, lo);
-    lo = dot4((int) (qa.z & 0x0F0F0F0Fu), x0.z, lo);
-    lo = dot4((int) (qa.w & 0x0F0F0F0Fu), x0.w, lo);
-    lo = dot4((int) (qb.x & 0x0F0F0F0Fu), x1.x, lo);
-    lo = dot4((int) (qb.y & 0x0F0F0F0Fu), x1.y, lo);
-    lo = dot4((int) (qb.z & 0x0F0F0F0Fu), x1.z, lo);
-    lo = dot4((int) (qb.w & 0x0F0F0F0Fu), x1.w, lo);
-    hi = dot4((int) ((qa.x >> 4) & 0x0F0F0F0Fu), x2.x, hi);
-    hi = dot4((int) ((qa.y >> 4) & 0x0F0F0F0Fu), x2.y, hi);
-    hi = dot4((int) ((qa.z >> 4) & 0x0F0F0F0Fu), x2.z, hi);
-    hi = dot4((int) ((qa.w >> 4) & 0x0F0F0F0Fu), x2.w, hi);
-    hi = dot4((int) ((qb.x >> 4) & 0x0F0F0F0Fu), x3.x, hi);
-    hi = dot4((int) ((qb.y >> 4) & 0x0F0F0F0Fu), x3.y, hi);
-    hi = dot4((int) ((qb.z >> 4) & 0x0F0F0F0Fu), x3.z, hi);
-    hi = dot4((int) ((qb.w >> 4) & 0x0F0F0F0Fu), x3.w, hi);
-    const uint32_t sc3[3] = { hdr.y, hdr.z, hdr.w };
     int sc_a, m_a, sc_b, m_b;
-    q4k_sc_m(sc3, 2 * p, sc_a, m_a);
-    q4k_sc_m(sc3, 2 * p + 1, sc_b, m_b);
-    const int16_t * bs = xbs + (int64_t) sb * 16 + 4 * p;
-    const int msum = m_a * ((int) bs[0] + (int) bs[1]) + m_b * ((int) bs[2] + (int) bs[3]);
-    const float dw = __half2float(__ushort_as_half((unsigned short) (hdr.x & 0xffff)));
-    const float dmin = __half2float(__ushort_as_half((unsigned short) (hdr.x >> 16)));
-    const float dx = xd[sb];
-    return (dw * dx) * (float) (sc_a * lo + sc_b * hi) - (dmin * dx) * (float) msum;
+    q4k_sc_m(hdr.y, hdr.z, hdr.w, 2 * p, sc_a, m_a);
+    q4k_sc_m(hdr.y, hdr.z, hdr.w, 2 * p + 1, sc_b, m_b);
+    const uint32_t q[8] = { qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w };
+    const int4 x0 = *(const int4 *) (xq + 0), x1 = *(const int4 *) (xq + 16);
+    const int4 x2 = *(const int4 *) (xq + 32), x3 = *(const int4 *) (xq + 48);
+    const int xl[8] = { x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w };
+    const int xh[8] = { x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w };
+#pragma unroll
+    for (int l = 0; l < 8; l++) aux[l] = 0;
+    // element e of a sub-block sits in dword e/4, byte e%4; e%8 = 4*(dword%2) + byte
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+        const uint32_t lo = q[w] & 0x0F0F0F0Fu, hi = (q[w] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int byte = 0; byte < 4; byte++) {
+            const int l = 4 * (w & 1) + byte;
+            const int ql = (int) ((lo >> (8 * byte)) & 0xff), qh = (int) ((hi >> (8 * byte)) & 0xff);
+            const int vl = (int) (int8_t) ((xl[w] >> (8 * byte)) & 0xff), vh = (int) (int8_t) ((xh[w] >> (8 * byte)) & 0xff);
+            aux[l] += sc_a * (ql * vl) + sc_b * (qh * vh);
+        }
+    }
+    mins = m_a * ((int) xbs[4 * p] + (int) xbs[4 * p + 1]) + m_b * ((int) xbs[4 * p + 2] + (int) xbs[4 * p + 3]);
 }
 
-template <int TYPE, int LPR, int NCOLS, bool SWIGLU>
+// dynamic LDS layout: [staged activation][terms]
+struct gemv_lds {
+    int8_t * xq;
+    float * xd;
+    int32_t * xs;      // q8
+    int16_t * xbs;     // q8K
+    float * terms;     // [rows_per_block * n_chain][T] (T = nb for Q4_0/Q8_0, 9 * nsb for Q4_K)
+};
+
+template <int TYPE>
+__host__ __device__ inline size_t gemv_lds_bytes(int K, int rows_per_block, int n_chain) {
+    if (TYPE == GGML_TYPE_Q4_K) {
+        const int nsb = K / 256;
+        return (size_t) K + (size_t) nsb * 4 + (size_t) (K / 16) * 2 + 16 + (size_t) rows_per_block * n_chain * nsb * 9 * 4;
+    }
+    const int nb = K / 32;
+    return (size_t) K + (size_t) nb * 8 + (size_t) rows_per_block * n_chain * nb * 4;
+}
+
+template <int TYPE, int LPR, bool SWIGLU, int ITS>
 __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
     constexpr int RPW = WAVE / LPR;
+    constexpr int NCH = SWIGLU ? 2 : 1;          // gate and up chains
     const int lane = threadIdx.x % WAVE;
     const int wave = threadIdx.x / WAVE;
-    const int waves = blockDim.x / WAVE;
     const int g = lane / LPR;
     const int l = lane % LPR;
-    const int row = (blockIdx.x * waves + wave) * RPW + g;
-    const int col0 = blockIdx.y * NCOLS;
+    const int rows_pb = a.rows_per_block;
+    const int rib = wave * RPW + g;               // row in block
+    const int row = blockIdx.x * rows_pb + rib;
+    const int col = blockIdx.y;
     const gemv_launch & L = a.L;
-    const int ncols = min(NCOLS, L.ncols - col0);
+    const int K = L.K;
     const bool valid = row < a.total_rows;
     const int mi = SWIGLU ? 0 : find_mat(a, valid ? row : 0);
     const int lrow = SWIGLU ? row : row - a.row_begin[mi];
-    const int K = L.K;
 
-    float acc[NCOLS];
-    float acc2[NCOLS];
-#pragma unroll
-    for (int c = 0; c < NCOLS; c++) { acc[c] = 0.0f; acc2[c] = 0.0f; }
+    // ---- stage the activation column in LDS ----
+    gemv_lds s;
+    s.xq = (int8_t *) smem;
+    if (TYPE == GGML_TYPE_Q4_K) {
+        const int nsb = K / 256;
+        s.xd = (float *) (smem + K);
+        s.xbs = (int16_t *) (smem + K + nsb * 4);
+        s.terms = (float *) (smem + ((K + nsb * 4 + (K / 16) * 2 + 15) & ~15));
+        for (int i = threadIdx.x * 16; i < K; i += blockDim.x * 16) *(int4 *) (s.xq + i) = *(const int4 *) (L.xq + (int64_t) col * K + i);
+        for (int i = threadIdx.x; i < nsb; i += blockDim.x) s.xd[i] = L.xd[(int64_t) col * nsb + i];
+        for (int i = threadIdx.x; i < K / 16; i += blockDim.x) s.xbs[i] = L.xbs[(int64_t) col * (K / 16) + i];
+    } else {
+        const int nb = K / 32;
+        s.xd = (float *) (smem + K);
+        s.xs = (int32_t *) (smem + K + nb * 4);
+        s.terms = (float *) (smem + K + nb * 8);
+        for (int i = threadIdx.x * 16; i < K; i += blockDim.x * 16) *(int4 *) (s.xq + i) = *(const int4 *) (L.xq + (int64_t) col * K + i);
+        for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+            s.xd[i] = L.xd[(int64_t) col * nb + i];
+            s.xs[i] = L.xs[(int64_t) col * nb + i];
+        }
+    }
+    __syncthreads();
 
-    if (valid) {
-        if (TYPE == GGML_TYPE_Q4_0 || TYPE == GGML_TYPE_Q8_0) {
-            constexpr int QS = TYPE == GGML_TYPE_Q4_0 ? Q4_0_QS : Q8_0_QS;
-            const int nb = K / 32;
-            const uint8_t * wq = L.m[mi].w + (int64_t) lrow * nb * QS;
-            const __half * wd = L.m[mi].wd + (int64_t) lrow * nb;
-            const uint8_t * wq2 = SWIGLU ? L.m[1].w + (int64_t) lrow * nb * QS : nullptr;
-            const __half * wd2 = SWIGLU ? L.m[1].wd + (int64_t) lrow * nb : nullptr;
-#pragma unroll 4
-            for (int b = l; b < nb; b += LPR) {
-                uint4 qa = *(const uint4 *) (wq + (int64_t) b * QS);
-                uint4 qb = qa;
-                if (TYPE == GGML_TYPE_Q8_0) qb = *(const uint4 *) (wq + (int64_t) b * QS + 16);
-                const float dw = __half2float(wd[b]);
-                uint4 ra = qa, rb = qb;
-                float dw2 = 0.0f;
-                if (SWIGLU) {
-                    ra = *(const uint4 *) (wq2 + (int64_t) b * QS);
-                    rb = ra;
-                    if (TYPE == GGML_TYPE_Q8_0) rb = *(const uint4 *) (wq2 + (int64_t) b * QS + 16);
-                    dw2 = __half2float(wd2[b]);
-                }
+    // ---- per-block terms ----
+    if (TYPE == GGML_TYPE_Q4_0 || TYPE == GGML_TYPE_Q8_0) {
+        constexpr int QS = TYPE == GGML_TYPE_Q4_0 ? Q4_0_QS : Q8_0_QS;
+        constexpr int MAXIT = ITS;   // blocks per lane (nb <= ITS * LPR)
+        const int nb = K / 32;
 #pragma unroll
-                for (int c = 0; c < NCOLS; c++) {
-                    if (c < ncols) {
-                        const int64_t col = col0 + c;
-                        const int8_t * xp = L.xq + col * K + (int64_t) b * 32;
-                        const int4 xa = *(const int4 *) xp;
-                        const int4 xb = *(const int4 *) (xp + 16);
-                        const float dx = L.xd[col * nb + b];
-                        if (TYPE == GGML_TYPE_Q4_0) {
-                            const int xs8 = 8 * L.xs[col * nb + b];
-                            const int sumi = dot_q4_0_block(qa, xa, xb) - xs8;
-                            acc[c] += (float) sumi * dw * dx;
-                            if (SWIGLU) {
-                                const int sumi2 = dot_q4_0_block(ra, xa, xb) - xs8;
-                                acc2[c] += (float) sumi2 * dw2 * dx;
-                            }
-                        } else {
-                            const int sumi = dot_q8_0_block(qa, qb, xa, xb);
-                            acc[c] += (float) sumi * (dw * dx);
-                            if (SWIGLU) {
-                                const int sumi2 = dot_q8_0_block(ra, rb, xa, xb);
-                                acc2[c] += (float) sumi2 * (dw2 * dx);
-                            }
-                        }
-                    }
+        for (int ch = 0; ch < NCH; ch++) {
+            if (!valid) break;
+            const uint8_t * wq = L.m[SWIGLU ? ch : mi].w + (int64_t) lrow * nb * QS;
+            const __half * wd = L.m[SWIGLU ? ch : mi].wd + (int64_t) lrow * nb;
+            float * terms = s.terms + (rib * NCH + ch) * nb;
+            // issue every weight load of this lane first
+            uint4 qa[MAXIT], qb[MAXIT];
+            float dw[MAXIT];
+#pragma unroll
+            for (int it = 0; it < MAXIT; it++) {
+                const int b = l + it * LPR;
+                if (b < nb) {
+                    qa[it] = *(const uint4 *) (wq + (int64_t) b * QS);
+                    if (TYPE == GGML_TYPE_Q8_0) qb[it] = *(const uint4 *) (wq + (int64_t) b * QS + 16);
+                    dw[it] = __half2float(wd[b]);
                 }
             }
-        } else { // Q4_K
-            const int units = K / 64;
-            const int64_t row_bytes = (int64_t) (K / 256) * Q4_K_BYTES;
-            const uint8_t * wrow = L.m[mi].w + (int64_t) lrow * row_bytes;
-            const uint8_t * wrow2 = SWIGLU ? L.m[1].w + (int64_t) lrow * row_bytes : nullptr;
-#pragma unroll 2
-            for (int u = l; u < units; u += LPR) {
 #pragma unroll
-                for (int c = 0; c < NCOLS; c++) {
-                    if (c < ncols) {
-                        const int64_t col = col0 + c;
-                        const int8_t * xq = L.xq + col * K;
-                        const float * xd = L.xd + col * (K / 256);
-                        const int16_t * xbs = L.xbs + col * (K / 16);
-                        acc[c] += q4k_unit(wrow, u, xq, xd, xbs);
-                        if (SWIGLU) acc2[c] += q4k_unit(wrow2, u, xq, xd, xbs);
+            for (int it = 0; it < MAXIT; it++) {
+                const int b = l + it * LPR;
+                if (b < nb) {
+                    const int4 xa = *(const int4 *) (s.xq + b * 32);
+                    const int4 xb = *(const int4 *) (s.xq + b * 32 + 16);
+                    const float dx = s.xd[b];
+                    float t;
+                    if (TYPE == GGML_TYPE_Q4_0) {
+                        const int sumi = dot_q4_0_block(qa[it], xa, xb) - 8 * s.xs[b];
+                        t = ((float) sumi * dw[it]) * dx;           // ggml: sumi*d_x*d_y
+                    } else {
+                        const int sumi = dot_q8_0_block(qa[it], qb[it], xa, xb);
+                        t = (float) sumi * (dw[it] * dx);           // ggml: sumi*(d_x*d_y)
                     }
+                    terms[b] = t;
+                }
+            }
+        }
+    } else { // Q4_K: per (super-block, l) products d*aux32[l] and dmin*mins
+        constexpr int MAXU = 608 / LPR;   // supports K <= 9728 * 4 (units = K/64 <= 608)
+        const int units = K / 64, nsb = K / 256;
+        const int64_t row_bytes = (int64_t) nsb * Q4_K_BYTES;
+#pragma unroll
+        for (int ch = 0; ch < NCH; ch++) {
+            const uint8_t * wrow = L.m[SWIGLU ? ch : mi].w + (int64_t) (valid ? lrow : 0) * row_bytes;
+            float * terms = s.terms + (rib * NCH + ch) * nsb * 9;
+#pragma unroll 2
+            for (int it = 0; it < MAXU; it++) {
+                const int u = l + it * LPR;
+                if (it * LPR >= units) break;       // uniform across the group
+                int aux[8], mins = 0;
+                const int sb = u >> 2, p = u & 3;
+                if (valid && u < units) {
+                    q4k_unit_ints(wrow + (int64_t) sb * Q4_K_BYTES, p, s.xq + sb * 256 + 64 * p, s.xbs + sb * 16, aux, mins);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 8; k++) aux[k] = 0;
+                }
+                // the 4 units of a super-block sit on 4 consecutive lanes: combine (exact integers)
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    aux[k] += __shfl_xor(aux[k], 1, WAVE);
+                    aux[k] += __shfl_xor(aux[k], 2, WAVE);
+                }
+                mins += __shfl_xor(mins, 1, WAVE);
+                mins += __shfl_xor(mins, 2, WAVE);
+                if (valid && u < units) {
+                    const uint8_t * blk = wrow + (int64_t) sb * Q4_K_BYTES;
+                    const uint32_t dd = *(const uint32_t *) blk;
+                    const float yd = s.xd[sb];
+                    const float d = __half2float(__ushort_as_half((unsigned short) (dd & 0xffff))) * yd;
+                    const float dmin = __half2float(__ushort_as_half((unsigned short) (dd >> 16))) * yd;
+                    // this lane stores the products for l = 2p, 2p+1 (static register indexing)
+                    float t0 = 0.0f, t1 = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        if (k == 2 * p) t0 = d * (float) aux[k];
+                        if (k == 2 * p + 1) t1 = d * (float) aux[k];
+                    }
+                    float * tt = terms + sb * 9;
+                    tt[2 * p] = t0;
+                    tt[2 * p + 1] = t1;
+                    if (p == 0) tt[8] = dmin * (float) mins;
                 }
             }
         }
     }
+    __syncthreads();
 
+    // ---- ordered sums, one lane per chain ----
+    float res[NCH];
 #pragma unroll
-    for (int c = 0; c < NCOLS; c++) {
-        acc[c] = group_sum<LPR>(acc[c]);
-        if (SWIGLU) acc2[c] = group_sum<LPR>(acc2[c]);
+    for (int ch = 0; ch < NCH; ch++) res[ch] = 0.0f;
+    if (TYPE == GGML_TYPE_Q4_0 || TYPE == GGML_TYPE_Q8_0) {
+        const int nb = K / 32;
+        if (l < NCH && valid) {
+            const float * terms = s.terms + (rib * NCH + l) * nb;
+            float acc = 0.0f;
+#pragma unroll 8
+            for (int b = 0; b < nb; b++) acc = acc + terms[b];
+            res[0] = acc;
+        }
+        // lane 0 holds gate (or the single chain), lane 1 holds up
+        const float mine = res[0];
+#pragma unroll
+        for (int ch = 0; ch < NCH; ch++) res[ch] = __shfl(mine, g * LPR + ch, WAVE);
+    } else {
+        const int nsb = K / 256;
+        // lanes 0..8 of a group: l < 8 -> sums[l] chain, l == 8 -> the mins chain (per ch)
+        float v = 0.0f;
+        const int ch = l / 9, k = l % 9;
+        if (ch < NCH && valid) {
+            const float * terms = s.terms + (rib * NCH + ch) * nsb * 9;
+            if (k < 8) {
+                for (int i = 0; i < nsb; i++) v = v + terms[i * 9 + k];
+            } else {
+                for (int i = 0; i < nsb; i++) v = v - terms[i * 9 + 8];
+            }
+        }
+        // sumf (the mins chain) then += sums[0..7] in order
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            float f = __shfl(v, g * LPR + c * 9 + 8, WAVE);
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) f = f + __shfl(v, g * LPR + c * 9 + kk, WAVE);
+            res[c] = f;
+        }
     }
 
     if (!SWIGLU) {
         if (valid && l == 0) {
             const gemv_mat & m = L.m[mi];
-#pragma unroll
-            for (int c = 0; c < NCOLS; c++) {
-                if (c < ncols) {
-                    const int64_t col = col0 + c;
-                    float v = acc[c];
-                    if (m.add) v += m.add[col * m.add_stride + lrow];
-                    m.y[col * m.y_stride + lrow] = v;
-                }
-            }
+            float v = res[0];
+            if (m.add) v = v + m.add[(int64_t) col * m.add_stride + lrow];
+            m.y[(int64_t) col * m.y_stride + lrow] = v;
         }
         return;
     }
 
-    // SwiGLU epilogue: act = silu(gate) * up; optional Q8_0 quantization of 32-row groups
-    // (rows per block is a multiple of 32 and n_rows % 32 == 0 when act_q is requested)
-    __shared__ float s_act[NCOLS][512 / 4];
-    const int rows_per_block = waves * RPW;
-    const int row_in_block = wave * RPW + g;
-#pragma unroll
-    for (int c = 0; c < NCOLS; c++) {
-        const float gv = acc[c], uv = acc2[c];
-        const float act = gv / (1.0f + expf(-gv)) * uv;
-        if (valid && l == 0 && c < ncols) {
-            L.m[0].y[(int64_t) (col0 + c) * L.m[0].y_stride + lrow] = act;
-        }
-        if (l == 0) s_act[c][row_in_block] = act;
-    }
+    // SwiGLU epilogue: act = silu(gate) * up (two roundings, as the silu and mul ops); optional Q8_0
+    // quantization of 32-row groups (rows per block is a multiple of 32 when act_q is requested)
+    const float gv = res[0], uv = res[NCH - 1];
+    const float sl = gv / (1.0f + exp_cr(-gv));
+    const float act = sl * uv;
+    if (valid && l == 0) L.m[0].y[(int64_t) col * L.m[0].y_stride + lrow] = act;
     if (L.act_q.qs == nullptr) return;
     __syncthreads();
-    // one 32-lane half-wave per (column, 32-row block)
-    const int n_qblk = rows_per_block / 32;
+    float * s_act = s.terms;   // reuse: terms are consumed
+    if (l == 0) s_act[rib] = valid ? act : 0.0f;
+    __syncthreads();
+    const int n_qblk = rows_pb / 32;
     const int half = threadIdx.x / 32;
     const int j = threadIdx.x % 32;
     const int64_t nb_out = a.total_rows / 32;
-    for (int task = half; task < NCOLS * n_qblk; task += blockDim.x / 32) {
-        const int c = task / n_qblk, qb = task % n_qblk;
-        const int out_row = blockIdx.x * rows_per_block + qb * 32 + j;
-        const bool ok = c < ncols && out_row < a.total_rows;
-        const float v = ok ? s_act[c][qb * 32 + j] : 0.0f;
+    if (half < n_qblk) {
+        const int out_row = blockIdx.x * rows_pb + half * 32 + j;
+        const bool ok = out_row < a.total_rows;
+        const float v = ok ? s_act[half * 32 + j] : 0.0f;
         const float amax = group_max<32>(fabsf(v));
         const float dd = amax / 127;
         const float id = dd ? 1.0f / dd : 0.0f;
         const int q = (int) roundf(v * id);
         const float qsum = group_sum<32>((float) q);
         if (ok) {
-            const int64_t col = col0 + c;
-            L.act_q.qs[col * a.total_rows + out_row] = (int8_t) q;
+            L.act_q.qs[(int64_t) col * a.total_rows + out_row] = (int8_t) q;
             if (j == 0) {
-                L.act_q.d[col * nb_out + out_row / 32] = __half2float(__float2half_rn(dd));
-                L.act_q.s[col * nb_out + out_row / 32] = (int32_t) qsum;
+                L.act_q.d[(int64_t) col * nb_out + out_row / 32] = __half2float(__float2half_rn(dd));
+                L.act_q.s[(int64_t) col * nb_out + out_row / 32] = (int32_t) qsum;
             }
         }
     }
 }
 
-template <int TYPE, int LPR, int NCOLS, bool SWIGLU>
-static void launch_gemv_t(const gemv_kargs & ka, int waves, hipStream_t st) {
+template <int TYPE, int LPR, bool SWIGLU, int ITS>
+static void launch_gemv_its(gemv_kargs & ka, int waves, hipStream_t st) {
     constexpr int RPW = WAVE / LPR;
-    const int rows_per_block = waves * RPW;
-    const int grid_x = (ka.total_rows + rows_per_block - 1) / rows_per_block;
-    const int grid_y = (ka.L.ncols + NCOLS - 1) / NCOLS;
-    hipLaunchKernelGGL((gemv_kernel<TYPE, LPR, NCOLS, SWIGLU>), dim3(grid_x, grid_y), dim3(waves * WAVE), 0, st, ka);
+    ka.rows_per_block = waves * RPW;
+    const int grid_x = (ka.total_rows + ka.rows_per_block - 1) / ka.rows_per_block;
+    const size_t lds = gemv_lds_bytes<TYPE>(ka.L.K, ka.rows_per_block, SWIGLU ? 2 : 1);
+    if (lds > 160 * 1024) HIP_ABORT("gemv: K=%d needs %zu bytes of LDS", ka.L.K, lds);
+    hipLaunchKernelGGL((gemv_kernel<TYPE, LPR, SWIGLU, ITS>), dim3(grid_x, ka.L.ncols), dim3(waves * WAVE), lds, st, ka);
     HIP_CHECK(hipGetLastError());
 }
 
-template <int TYPE, int LPR>
-static void launch_gemv_cols(const gemv_kargs & ka, int waves, hipStream_t st) {
-    const int nc = ka.L.ncols;
-    if (ka.L.swiglu) {
-        if (nc == 1) launch_gemv_t<TYPE, LPR, 1, true>(ka, waves, st);
-        else if (nc == 2) launch_gemv_t<TYPE, LPR, 2, true>(ka, waves, st);
-        else if (nc <= 4) launch_gemv_t<TYPE, LPR, 4, true>(ka, waves, st);
-        else launch_gemv_t<TYPE, LPR, 8, true>(ka, waves, st);
+// ITS = weight blocks per lane for Q4_0/Q8_0 (register-resident, loaded up front)
+template <int TYPE, int LPR, bool SWIGLU>
+static void launch_gemv_t(gemv_kargs & ka, int waves, hipStream_t st) {
+    if constexpr (TYPE == GGML_TYPE_Q4_K) {
+        launch_gemv_its<TYPE, LPR, SWIGLU, 1>(ka, waves, st);
     } else {
-        if (nc == 1) launch_gemv_t<TYPE, LPR, 1, false>(ka, waves, st);
-        else if (nc == 2) launch_gemv_t<TYPE, LPR, 2, false>(ka, waves, st);
-        else if (nc <= 4) launch_gemv_t<TYPE, LPR, 4, false>(ka, waves, st);
-        else launch_gemv_t<TYPE, LPR, 8, false>(ka, waves, st);
+        const int its = (ka.L.K / 32 + LPR - 1) / LPR;
+        if (its <= 1) launch_gemv_its<TYPE, LPR, SWIGLU, 1>(ka, waves, st);
+        else if (its <= 2) launch_gemv_its<TYPE, LPR, SWIGLU, 2>(ka, waves, st);
+        else if (its <= 4) launch_gemv_its<TYPE, LPR, SWIGLU, 4>(ka, waves, st);
+        else if (its <= 6) launch_gemv_its<TYPE, LPR, SWIGLU, 6>(ka, waves, st);
+        else if (its <= 8) launch_gemv_its<TYPE, LPR, SWIGLU, 8>(ka, waves, st);
+        else if (its <= 16) launch_gemv_its<TYPE, LPR, SWIGLU, 16>(ka, waves, st);
+        else if constexpr (TYPE == GGML_TYPE_Q4_0) launch_gemv_its<TYPE, LPR, SWIGLU, 32>(ka, waves, st);
+        else HIP_ABORT("gemv q8_0: K=%d exceeds 8192", ka.L.K);
     }
 }
 
@@ -449,20 +533,21 @@ void launch_gemv(const gemv_launch & L, hipStream_t st) {
     ka.total_rows = L.swiglu ? L.m[0].n_rows : r;
     if (L.swiglu && (L.n_mats != 2 || L.m[0].n_rows != L.m[1].n_rows)) HIP_ABORT("gemv: swiglu needs two equal matrices");
     if (L.swiglu && L.act_q.qs && (ka.total_rows % 32 != 0)) HIP_ABORT("gemv: quantized swiglu output needs rows %% 32 == 0");
-    // 8 waves x (64/LPR) rows: a multiple of 32 rows per block, as the swiglu quantization needs
-    const int waves = 8;
     switch (L.type) {
         case GGML_TYPE_Q4_0:
-            if (L.K % 32) HIP_ABORT("gemv q4_0: K %% 32");
-            launch_gemv_cols<GGML_TYPE_Q4_0, 16>(ka, waves, st);
+            if (L.K % 32 || L.K > 16384) HIP_ABORT("gemv q4_0: K=%d unsupported", L.K);
+            if (L.swiglu) launch_gemv_t<GGML_TYPE_Q4_0, 16, true>(ka, 8, st);
+            else launch_gemv_t<GGML_TYPE_Q4_0, 16, false>(ka, 4, st);
             break;
         case GGML_TYPE_Q8_0:
-            if (L.K % 32) HIP_ABORT("gemv q8_0: K %% 32");
-            launch_gemv_cols<GGML_TYPE_Q8_0, 16>(ka, waves, st);
+            if (L.K % 32 || L.K > 16384) HIP_ABORT("gemv q8_0: K=%d unsupported", L.K);
+            if (L.swiglu) launch_gemv_t<GGML_TYPE_Q8_0, 16, true>(ka, 8, st);
+            else launch_gemv_t<GGML_TYPE_Q8_0, 16, false>(ka, 4, st);
             break;
         case GGML_TYPE_Q4_K:
-            if (L.K % 256) HIP_ABORT("gemv q4_K: K %% 256");
-            launch_gemv_cols<GGML_TYPE_Q4_K, 8>(ka, waves, st);
+            if (L.K % 256 || L.K / 64 > 608) HIP_ABORT("gemv q4_K: K=%d unsupported", L.K);
+            if (L.swiglu) launch_gemv_t<GGML_TYPE_Q4_K, 32, true>(ka, 8, st);
+            else launch_gemv_t<GGML_TYPE_Q4_K, 16, false>(ka, 4, st);
             break;
         default:
             HIP_ABORT("gemv: unsupported weight type %d", L.type);

@@ -64,7 +64,9 @@ __device__ __forceinline__ double wave_sum_d(double v) {
     return v;
 }
 
-template <int QUANT> // 0 none, 1 Q8_0 (32-blocks), 2 Q8_K (256-blocks)
+// One 256-thread block per row; each thread holds its EPT elements (i = it*256 + t) in registers,
+// so the row is read once with every load issued up front.
+template <int QUANT, int EPT> // QUANT: 0 none, 1 Q8_0 (32-blocks), 2 Q8_K (256-blocks)
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float * __restrict__ x, int64_t x_stride,
         const float * __restrict__ w, float * __restrict__ y, int64_t y_stride, int64_t n, float eps,
         q8_act q8, q8k_act q8k) {
@@ -76,28 +78,37 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float * __restrict_
     const float * xr = x + row * x_stride;
     float * yr = y + row * y_stride;
     const int t = threadIdx.x;
+    float v[EPT];
+#pragma unroll
+    for (int it = 0; it < EPT; it++) {
+        const int64_t i = (int64_t) it * 256 + t;
+        v[it] = i < n ? xr[i] : 0.0f;
+    }
     double sum = 0.0;
-    for (int64_t i = t; i < n; i += 256) sum += (double) (xr[i] * xr[i]);
+#pragma unroll
+    for (int it = 0; it < EPT; it++) sum += (double) (v[it] * v[it]);
     sum = wave_sum_d(sum);
     if ((t % 64) == 0) s_part[t / 64] = sum;
     __syncthreads();
     const double total = s_part[0] + s_part[1] + s_part[2] + s_part[3];
     const float mean = (float) (total / (double) n);
     const float scale = 1.0f / sqrtf(mean + eps);
-    for (int64_t i0 = 0; i0 < n; i0 += 256) {
-        const int64_t i = i0 + t;
-        float v = 0.0f;
+#pragma unroll
+    for (int it = 0; it < EPT; it++) {
+        const int64_t i = (int64_t) it * 256 + t;
+        if ((int64_t) it * 256 >= n) break;       // uniform
+        float o = 0.0f;
         if (i < n) {
-            v = xr[i] * scale;
-            if (w) v = v * w[i];
-            yr[i] = v;
+            o = v[it] * scale;
+            if (w) o = o * w[i];
+            yr[i] = o;
         }
         if (QUANT == 1) {
             // 32 consecutive elements live in 32 consecutive lanes
-            const float amax = group_max<32>(fabsf(v));
+            const float amax = group_max<32>(fabsf(o));
             const float dd = amax / 127;
             const float id = dd ? 1.0f / dd : 0.0f;
-            const int q = (int) roundf(v * id);
+            const int q = (int) roundf(o * id);
             const float qsum = group_sum<32>((float) q);
             if (i < n) {
                 q8.qs[row * n + i] = (int8_t) q;
@@ -108,14 +119,14 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float * __restrict_
             }
         } else if (QUANT == 2) {
             // one super-block of 256 per iteration; max magnitude with the lowest index on ties
-            float ax = fabsf(v);
+            float ax = fabsf(o);
             int idx = t;
-            float val = v;
+            float val = o;
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ax2 = __shfl_xor(ax, o, WAVE);
-                const int idx2 = __shfl_xor(idx, o, WAVE);
-                const float val2 = __shfl_xor(val, o, WAVE);
+            for (int off = 32; off > 0; off >>= 1) {
+                const float ax2 = __shfl_xor(ax, off, WAVE);
+                const int idx2 = __shfl_xor(idx, off, WAVE);
+                const float val2 = __shfl_xor(val, off, WAVE);
                 if (ax2 > ax || (ax2 == ax && idx2 < idx)) { ax = ax2; idx = idx2; val = val2; }
             }
             __syncthreads();
@@ -127,10 +138,10 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float * __restrict_
                 if (s_fx[wv] > bax || (s_fx[wv] == bax && s_ix[wv] < bidx)) { bax = s_fx[wv]; bidx = s_ix[wv]; bval = s_vx[wv]; }
             }
             int q = 0;
-            const int64_t sb = i0 / 256;
+            const int64_t sb = (int64_t) it;
             if (bax != 0.0f) {
                 const float iscale = -127.f / bval;
-                q = round_half_even(iscale * v);
+                q = round_half_even(iscale * o);
                 q = q < 127 ? q : 127;
                 if (t == 0) q8k.d[row * (n / 256) + sb] = 1 / iscale;
             } else if (t == 0) {
@@ -143,22 +154,34 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float * __restrict_
     }
 }
 
+template <int QUANT>
+static void launch_rms_norm_q(const float * x, int64_t x_stride, const float * w, float * y, int64_t y_stride,
+                              int64_t n, int64_t ncols, float eps, q8_act a, q8k_act b, hipStream_t st) {
+    const int64_t ept = (n + 255) / 256;
+    dim3 grid((unsigned) ncols), blk(256);
+    if (ept <= 1) hipLaunchKernelGGL((rms_norm_kernel<QUANT, 1>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    else if (ept <= 2) hipLaunchKernelGGL((rms_norm_kernel<QUANT, 2>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    else if (ept <= 4) hipLaunchKernelGGL((rms_norm_kernel<QUANT, 4>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    else if (ept <= 8) hipLaunchKernelGGL((rms_norm_kernel<QUANT, 8>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    else if (ept <= 16) hipLaunchKernelGGL((rms_norm_kernel<QUANT, 16>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    else if (ept <= 32) hipLaunchKernelGGL((rms_norm_kernel<QUANT, 32>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    else HIP_ABORT("rms_norm: rows of %lld elements are not supported", (long long) n);
+    HIP_CHECK(hipGetLastError());
+}
+
 void launch_rms_norm(const float * x, int64_t x_stride, const float * w, float * y, int64_t y_stride,
                      int64_t n, int64_t ncols, float eps, const q8_act * q8, const q8k_act * q8k, hipStream_t st) {
     q8_act a{};
     q8k_act b{};
     if (q8) {
         if (n % 32) HIP_ABORT("rms_norm: q8 output needs n %% 32 == 0");
-        a = *q8;
-        hipLaunchKernelGGL(rms_norm_kernel<1>, dim3((unsigned) ncols), dim3(256), 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+        launch_rms_norm_q<1>(x, x_stride, w, y, y_stride, n, ncols, eps, *q8, b, st);
     } else if (q8k) {
         if (n % 256) HIP_ABORT("rms_norm: q8K output needs n %% 256 == 0");
-        b = *q8k;
-        hipLaunchKernelGGL(rms_norm_kernel<2>, dim3((unsigned) ncols), dim3(256), 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+        launch_rms_norm_q<2>(x, x_stride, w, y, y_stride, n, ncols, eps, a, *q8k, st);
     } else {
-        hipLaunchKernelGGL(rms_norm_kernel<0>, dim3((unsigned) ncols), dim3(256), 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+        launch_rms_norm_q<0>(x, x_stride, w, y, y_stride, n, ncols, eps, a, b, st);
     }
-    HIP_CHECK(hipGetLastError());
 }
 
 // generic strided: one block per row (i1, i2, i3)
@@ -215,9 +238,9 @@ __global__ void unary_kernel(int op, float s, tview a, tview d, int64_t n) {
     const float x = ld(at(a, k.i0, k.i1, k.i2, k.i3), a.type);
     float y;
     switch (op) {
-        case 0: y = x / (1.0f + expf(-x)); break;
+        case 0: y = x / (1.0f + exp_cr(-x)); break;
         case 1: y = x > 0.0f ? x : 0.0f; break;
-        case 2: y = 1.0f / (1.0f + expf(-x)); break;
+        case 2: y = 1.0f / (1.0f + exp_cr(-x)); break;
         case 3: y = x * x; break;
         default: y = x * s; break;
     }
@@ -324,10 +347,10 @@ __device__ __forceinline__ void rope_cs(float theta_extrap, const rope_params & 
         const float ramp = 1 - fminf(1, fmaxf(0, y));
         const float ramp_mix = ramp * p.ext_factor;
         theta = theta_interp * (1 - ramp_mix) + theta_extrap * ramp_mix;
-        mscale *= 1.0f + 0.1f * logf(1.0f / p.freq_scale);
+        mscale *= 1.0f + 0.1f * log_cr(1.0f / p.freq_scale);
     }
-    c = cosf(theta) * mscale;
-    s = sinf(theta) * mscale;
+    c = cos_cr(theta) * mscale;
+    s = sin_cr(theta) * mscale;
 }
 
 __global__ void rope_kernel(tview x, const int32_t * __restrict__ pos, const float * __restrict__ ff, tview d, rope_params p, int64_t n) {
@@ -397,7 +420,7 @@ __global__ __launch_bounds__(256) void soft_max_kernel(tview a, tview m, int has
     double sum = 0.0;
     for (int64_t i = t; i < nc; i += 256) {
         float * p = (float *) at(d, i, i1, i2, i3);
-        const float v = expf(*p - mx);
+        const float v = exp_cr(*p - mx);
         *p = v;
         sum += (double) v;
     }
@@ -467,7 +490,8 @@ __global__ __launch_bounds__(256) void mul_mat_generic_kernel(tview s0, tview s1
     const int64_t r2 = s1.ne[2] / s0.ne[2], r3 = s1.ne[3] / s0.ne[3];
     const char * a = at(s0, 0, k.i0, k.i2 / r2, k.i3 / r3);
     const int64_t K = s0.ne[0];
-    float acc = 0.0f;
+    // products rounded to float, summed in double, as ggml-cpu's f16/f32 vec_dot
+    double acc = 0.0;
     for (int64_t i = lane; i < K; i += WAVE) {
         const float w = ld(a + i * s0.nb[0], s0.type);
         float x = *(const float *) at(s1, i, k.i1, k.i2, k.i3);
@@ -477,10 +501,10 @@ __global__ __launch_bounds__(256) void mul_mat_generic_kernel(tview s0, tview s1
             u = (u + (0x7fffu + ((u >> 16) & 1u))) & 0xffff0000u;
             x = __uint_as_float(u);
         }
-        acc += w * x;
+        acc += (double) (w * x);
     }
-    acc = wave_sum(acc);
-    if (lane == 0) *(float *) at(d, k.i0, k.i1, k.i2, k.i3) = acc;
+    acc = wave_sum_d(acc);
+    if (lane == 0) *(float *) at(d, k.i0, k.i1, k.i2, k.i3) = (float) acc;
 }
 
 void launch_mul_mat_generic(const tview & src0, const tview & src1, const tview & dst, hipStream_t st) {

@@ -56,6 +56,12 @@ GGML_API size_t ggml_backend_get_alignment(ggml_backend_t backend);
 GGML_API void   ggml_backend_synchronize(ggml_backend_t backend);
 GGML_API enum ggml_status ggml_backend_graph_compute(ggml_backend_t backend, struct ggml_cgraph * cgraph);
 
+// Called after a backend has computed a node (its data is complete and readable with
+// ggml_backend_tensor_get). `ask` is always false here; return false to stop reporting. Used by
+// debugging and parity tools to compare intermediate tensors across backends.
+typedef bool (*ggml_backend_eval_callback)(struct ggml_tensor * t, bool ask, void * user_data);
+GGML_API void ggml_backend_set_eval_callback(ggml_backend_t backend, ggml_backend_eval_callback cb, void * user_data);
+
 // synchronous host<->tensor copies (offset/size in bytes of the tensor's GGML layout)
 GGML_API void ggml_backend_tensor_set(struct ggml_tensor * tensor, const void * data, size_t offset, size_t size);
 GGML_API void ggml_backend_tensor_get(const struct ggml_tensor * tensor, void * data, size_t offset, size_t size);

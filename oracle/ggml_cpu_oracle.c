@@ -10,10 +10,11 @@
  *             Q4_K -> Q8_K, F16 -> F16, F32 stays), then one block-integer dot per block with a
  *             float block-sum (ggml_vec_dot_*_generic). F16/F32 dots accumulate in double.
  *   RMS_NORM  sum of x*x in double, mean cast to float, scale = 1/sqrtf(mean + eps).
- *   SOFT_MAX  w = x*scale + mask; max; exp(w - max) (expf) summed in double; scale by 1/sum.
+ *   SOFT_MAX  w = x*scale + mask; max; exp(w - max) summed in double; scale by 1/sum.
  *   ROPE      per-position cos/sin cache with theta *= theta_scale iterated in float,
  *             theta_scale = powf(base, -2/n_dims); NORMAL pairs (2i, 2i+1), NEOX (i, i+n_dims/2).
- *   SILU      x / (1 + expf(-x)).
+ *   SILU      x / (1 + exp(-x)).
+ *   exp/cos/sin are correctly rounded (see exp_cr below).
  *   CPY/CONT  element-wise with f32 -> f16 round-to-nearest-even.
  */
 #include "oracle.h"
@@ -29,6 +30,16 @@
 #include <string.h>
 
 typedef double ggml_float;
+
+/* Transcendentals of the float ops (RoPE cos/sin, softmax and SiLU exp) are the correctly rounded
+ * float results: evaluated in double and rounded once. ggml-cpu calls the platform's cosf/sinf/
+ * expf, whose last-ulp behaviour differs between libms (glibc's cosf/sinf are off by one ulp on
+ * ~1% of RoPE angles; the reference itself targets Android's bionic), so the oracle fixes the
+ * platform-independent choice and the HIP backend evaluates the same way. */
+static inline float exp_cr(float x) { return (float) exp((double) x); }
+static inline float cos_cr(float x) { return (float) cos((double) x); }
+static inline float sin_cr(float x) { return (float) sin((double) x); }
+static inline float log_cr(float x) { return (float) log((double) x); }
 
 /* ------------------------------------------------------------------------------------------ */
 /* binary16 — the branch-free formulation of the FP16 library (fp16_ieee_{from,to}_fp32_value),
@@ -513,10 +524,10 @@ static void rope_yarn(float theta_extrap, float freq_scale, const float corr_dim
     if (ext_factor != 0.0f) {
         const float ramp_mix = yarn_ramp(corr_dims[0], corr_dims[1], (int) i0) * ext_factor;
         theta = theta_interp * (1 - ramp_mix) + theta_extrap * ramp_mix;
-        mscale *= 1.0f + 0.1f * logf(1.0f / freq_scale);
+        mscale *= 1.0f + 0.1f * log_cr(1.0f / freq_scale);
     }
-    *cos_theta = cosf(theta) * mscale;
-    *sin_theta = sinf(theta) * mscale;
+    *cos_theta = cos_cr(theta) * mscale;
+    *sin_theta = sin_cr(theta) * mscale;
 }
 
 static void corr_dims_of(int n_dims, int n_ctx_orig, float freq_base, float beta_fast, float beta_slow, float dims[2]) {
@@ -628,7 +639,11 @@ static void store_f(const struct ggml_tensor * t, char * p, float v) {
     }
 }
 
-typedef struct { int n_threads; } cpu_ctx;
+typedef struct {
+    int n_threads;
+    ggml_backend_eval_callback cb;
+    void * cb_user;
+} cpu_ctx;
 
 static void op_dup(struct ggml_tensor * dst, const struct ggml_tensor * src, int nth) {
     /* element-wise copy in row-major order of src into row-major order of dst (shapes may differ
@@ -721,9 +736,9 @@ static void op_unary(struct ggml_tensor * dst, const struct ggml_tensor * a, int
             float y;
             if (dst->op == GGML_OP_SCALE) y = x * s;
             else if (dst->op == GGML_OP_SQR) y = x * x;
-            else if (kind == GGML_UNARY_OP_SILU) y = x / (1.0f + expf(-x));
+            else if (kind == GGML_UNARY_OP_SILU) y = x / (1.0f + exp_cr(-x));
             else if (kind == GGML_UNARY_OP_RELU) y = x > 0.f ? x : 0.f;
-            else if (kind == GGML_UNARY_OP_SIGMOID) y = 1.0f / (1.0f + expf(-x));
+            else if (kind == GGML_UNARY_OP_SIGMOID) y = 1.0f / (1.0f + exp_cr(-x));
             else { fprintf(stderr, "oracle: unary op %d\n", kind); abort(); }
             store_f(dst, ELEM(dst, i0, i1, i2, i3), y);
         }
@@ -757,7 +772,7 @@ static void op_soft_max(struct ggml_tensor * dst, const struct ggml_tensor * a, 
         for (int64_t i = 0; i < nc; i++) max = max > wp[i] ? max : wp[i];
         ggml_float sum = 0.0;
         for (int64_t i = 0; i < nc; i++) {
-            const float v = expf(wp[i] - max);
+            const float v = exp_cr(wp[i] - max);
             sum += (ggml_float) v;
             dp[i] = v;
         }
@@ -895,10 +910,10 @@ static void op_flash_attn(struct ggml_tensor * dst, const struct ggml_tensor * q
             float ms = 1.0f, vs = 1.0f;
             if (sf > M) {
                 M = sf;
-                ms = expf(Mold - M);
+                ms = exp_cr(Mold - M);
                 for (int64_t i = 0; i < DV; i++) acc[i] *= ms;
             } else {
-                vs = expf(sf - M);
+                vs = exp_cr(sf - M);
             }
             for (int64_t i = 0; i < DV; i++) acc[i] += load_f(v, ELEM(v, i, ic, iq2 / rv2, iq3)) * vs;
             S = S * ms + vs;
@@ -980,9 +995,18 @@ static const char * cpu_name(ggml_backend_t b) { (void) b; return "CPU"; }
 static void cpu_free(ggml_backend_t b) { free(b->context); free(b); }
 static ggml_backend_buffer_type_t cpu_default_buft(ggml_backend_t b) { (void) b; return &g_cpu_buft; }
 static enum ggml_status cpu_graph_compute(ggml_backend_t b, struct ggml_cgraph * g) {
-    const int nth = ((cpu_ctx *) b->context)->n_threads;
-    for (int i = 0; i < g->n_nodes; i++) compute_node(g->nodes[i], nth);
+    cpu_ctx * c = (cpu_ctx *) b->context;
+    for (int i = 0; i < g->n_nodes; i++) {
+        compute_node(g->nodes[i], c->n_threads);
+        if (c->cb && !c->cb(g->nodes[i], false, c->cb_user)) c->cb = NULL;
+    }
     return GGML_STATUS_SUCCESS;
+}
+
+static void cpu_set_eval_callback(ggml_backend_t b, ggml_backend_eval_callback cb, void * user) {
+    cpu_ctx * c = (cpu_ctx *) b->context;
+    c->cb = cb;
+    c->cb_user = user;
 }
 
 ggml_backend_t ggml_backend_cpu_init(void) {
@@ -994,6 +1018,7 @@ ggml_backend_t ggml_backend_cpu_init(void) {
     b->iface.get_default_buffer_type = cpu_default_buft;
     b->iface.graph_compute = cpu_graph_compute;
     b->iface.synchronize = NULL;
+    b->iface.set_eval_callback = cpu_set_eval_callback;
     b->context = c;
     return b;
 }

@@ -171,6 +171,8 @@ class Graph:
         res = []
         for o in outs:
             res.append(self.read(o))
+        if not res:
+            return None
         return res if len(res) > 1 else res[0]
 
     def read(self, t, dtype=np.float32):
@@ -205,3 +207,49 @@ def run_on(backend, build):
     with Graph() as g:
         outs = build(g)
         return g.compute(backend, outs)
+
+
+# ---- node-by-node capture (debugging / parity localization) ----
+EVAL_CB = C.CFUNCTYPE(C.c_bool, gl.T, C.c_bool, C.c_void_p)
+OP_NAMES = ["NONE", "DUP", "ADD", "MUL", "SCALE", "SQR", "RMS_NORM", "MUL_MAT", "MUL_MAT_ID", "CPY", "CONT", "RESHAPE",
+            "VIEW", "PERMUTE", "TRANSPOSE", "GET_ROWS", "SOFT_MAX", "ROPE", "FLASH_ATTN_EXT", "ARGMAX", "UNARY"]
+NOOP = {"NONE", "RESHAPE", "VIEW", "PERMUTE", "TRANSPOSE"}
+
+
+def capture(backend, store: list):
+    """Record (op, shape, f32 data) of every node the backend reports; returns the callback object
+    (keep it alive while the backend computes)."""
+    core = gl.libs()["core"]
+
+    def cb(t, ask, user):
+        tt = t.contents
+        op = OP_NAMES[tt.op] if tt.op < len(OP_NAMES) else str(tt.op)
+        if op in NOOP:
+            return True
+        shape = tuple(tt.ne[i] for i in range(4))
+        if tt.type == gl.F32 and core.ggml_is_contiguous(t):
+            n = core.ggml_nbytes(t) // 4
+            a = np.empty(n, dtype=np.float32)
+            core.ggml_backend_tensor_get(t, ptr(a), 0, n * 4)
+        else:
+            a = None
+        store.append((op, shape, a))
+        return True
+
+    f = EVAL_CB(cb)
+    core.ggml_backend_set_eval_callback(backend, f, None)
+    return f
+
+
+def first_divergence(a: list, b: list, tol=1e-4):
+    """Compare two captured sequences (same graph); returns list of (i, op, shape, err) above tol."""
+    out = []
+    for i, ((oa, sa, xa), (ob, sb, xb)) in enumerate(zip(a, b)):
+        if oa != ob or sa != sb:
+            out.append((i, f"{oa}/{ob}", sa, float("nan")))
+            break
+        if xa is not None and xb is not None and xa.size == xb.size:
+            e = rel_err(xa, xb)
+            if e > tol:
+                out.append((i, oa, sa, e))
+    return out

@@ -1,7 +1,9 @@
 """Model-level parity: the whole forward_step (build_graph -> gallocr -> graph_compute) on the HIP
 backend against the same step on the oracle CPU backend, on identical seeded synthetic GGUF
 models. Bars: logits within max relative error 2e-3 (normwise), greedy
-top-1 agreement >= 99% over 256 decode steps.
+top-1 agreement >= 99% over 256 decode steps. The HIP kernels reproduce the oracle's float
+rounding chain, so the tiny models are also held to bit-identical logits and an identical
+free-running greedy sequence.
 """
 import os
 
@@ -50,13 +52,13 @@ def test_decode_parity_tiny(models, arch, fusion):
         gl.libs()["hip"].ggml_backend_hip_set_fusion(h.backend, fusion)
         lh = h.forward(0, prompt)
         lc = c.forward(0, prompt)
-        assert rel_err(lh, lc) < TOL
+        assert np.array_equal(lh, lc), (arch, "prefill", rel_err(lh, lc))
         n_past = len(prompt)
         tok = int(np.argmax(lc))
         for step in range(6):
             lh = h.forward(n_past, [tok])
             lc = c.forward(n_past, [tok])
-            assert rel_err(lh, lc) < TOL, (arch, step, rel_err(lh, lc))
+            assert np.array_equal(lh, lc), (arch, step, rel_err(lh, lc))
             n_past += 1
             tok = int(np.argmax(lc))
 
@@ -75,9 +77,10 @@ def test_greedy_agreement_256(models):
             agree += int(np.argmax(logits)) == int(ref_tokens[i])
             tok = int(ref_tokens[i])
         hip_tokens, _ = h.decode_loop(0, 1, n)
-    assert agree / n >= 0.99, agree
     prefix = int(np.argmax(np.concatenate([hip_tokens != ref_tokens, [True]])))
     print(f"teacher-forced agreement {agree}/{n}; free-running identical prefix {prefix}/{n}")
+    assert agree / n >= 0.99, agree
+    assert prefix == n, prefix
 
 
 @pytest.mark.skipif(os.environ.get("GL_SKIP_FULL") == "1", reason="full-size check disabled")
