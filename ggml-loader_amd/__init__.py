@@ -101,6 +101,8 @@ def _declare(core, hip, loader):
     _sig(core, "ggml_new_tensor_3d", T, vp, i32, i64, i64, i64)
     _sig(core, "ggml_new_tensor_4d", T, vp, i32, i64, i64, i64, i64)
     _sig(core, "ggml_set_name", T, T, C.c_char_p)
+    _sig(core, "ggml_set_input", None, T)
+    _sig(core, "ggml_set_output", None, T)
     _sig(core, "ggml_get_tensor", T, vp, C.c_char_p)
     _sig(core, "ggml_get_rows", T, vp, T, T)
     _sig(core, "ggml_rms_norm", T, vp, T, f32)

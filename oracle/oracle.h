@@ -11,7 +11,29 @@
  * (-ffp-contract=off). It is also registered as the "CPU" ggml backend so the same graph that the
  * HIP backend runs can be computed here (ggml_backend_cpu_init, include/ggml-cpu.h).
  *
- * Pinning status of each primitive is listed in oracle/README.md.
+ * What pins each primitive (tests/test_oracle.py, tests/test_host.py; golden vectors made by
+ * tests/golden/make_golden.py from the reference's src/moe_stream sources via Makefile.ref):
+ *   fp16 <-> fp32              IEEE binary16 (numpy): all 65536 codes; 3M f32 patterns incl. ties
+ *   Q4_0 decode                closed form over every nibble at every position, 8 scales
+ *   Q8_0, Q4_K decode          reference dequant_row golden vectors, bit-exact (dequant.c:94-251)
+ *   Q4_0/Q8_0/Q8_K quantizers  error bounds (round to nearest within d/2, the +8 clip of Q4_0),
+ *                              zero and constant blocks, Q8_K block sums; the product's quantizer
+ *                              byte-identical. Byte-level equality with upstream ggml's
+ *                              quantize_row_*_ref: parity unpinned (upstream ggml is absent)
+ *   Q4_K quantizer             RMS-error bound, zero block, product byte-identical; byte-level
+ *                              equality with upstream ggml: parity unpinned
+ *   vec dots / gemv            fp64 brute force over the same quantized operands; one-hot columns;
+ *                              reference sc_matmul golden (Q4_K) within the activation-quantization
+ *                              bound. ggml-cpu's block-sum order itself: parity unpinned
+ *   rms_norm, softmax, silu    reference sc_rmsnorm / sc_softmax / sc_swiglu golden vectors
+ *                              (tolerance: float vs double sums); softmax masks and row sums
+ *   rope                       reference sc_rope golden (NEOX); position 0 identity; pair norms;
+ *                              theta_0 = pos; NORMAL == NEOX on interleaved pairs; partial dims
+ *   attention chain            n_kv = 1 -> V; equal keys -> mean of V (exact); fp64 GQA brute force
+ *                              that also rejects the h % n_head_kv mapping
+ *   moe_route                  brute-force top-k (ties -> lower id) and renormalized softmax
+ *   forward_step               float64 numpy transformer on synthetic GGUFs of 4 archs, rejecting
+ *                              the other RoPE pair layout
  */
 #ifndef GGML_LOADER_ORACLE_H
 #define GGML_LOADER_ORACLE_H

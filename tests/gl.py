@@ -118,16 +118,16 @@ def randn(n, seed, std=1.0, mean=0.0):
 # ---- error metrics ----
 def rel_err(x, ref) -> float:
     """max |x - ref| / max |ref| (normwise, infinity norm)."""
-    x = np.asarray(x, dtype=np.float64)
-    ref = np.asarray(ref, dtype=np.float64)
+    x = np.asarray(x, dtype=np.float64).ravel()
+    ref = np.asarray(ref, dtype=np.float64).ravel()
     den = np.max(np.abs(ref))
     return float(np.max(np.abs(x - ref)) / (den if den > 0 else 1.0))
 
 
 def rel_err_floor(x, ref) -> float:
     """The reference's per-element convention (test_vulkan.c:103-109): |x-ref| / (|ref| if |ref| > 1e-3 else 1)."""
-    x = np.asarray(x, dtype=np.float64)
-    ref = np.asarray(ref, dtype=np.float64)
+    x = np.asarray(x, dtype=np.float64).ravel()
+    ref = np.asarray(ref, dtype=np.float64).ravel()
     den = np.where(np.abs(ref) > 1e-3, np.abs(ref), 1.0)
     return float(np.max(np.abs(x - ref) / den))
 
@@ -207,6 +207,28 @@ def run_on(backend, build):
     with Graph() as g:
         outs = build(g)
         return g.compute(backend, outs)
+
+
+def attention_graph(g, hd, n_head, n_head_kv, n_kv, n_new, n_ctx, kc, vc, q, mask, flash=False):
+    """The attention block of build_graph (reference model.cpp:1416-1444)."""
+    K_cache = g.tensor(gl.F16, hd, n_head_kv, n_ctx, data=kc)
+    V_cache = g.tensor(gl.F16, hd, n_head_kv, n_ctx, data=vc)
+    Qcur = g.tensor(gl.F32, hd, n_head, n_new, data=q)
+    m = g.tensor(gl.F32, n_kv, n_new, data=mask)
+    nb1, nb2 = hd * 2, hd * n_head_kv * 2
+    K_full = g.view_3d(K_cache, hd, n_head_kv, n_kv, nb1, nb2, 0)
+    V_full = g.view_3d(V_cache, hd, n_head_kv, n_kv, nb1, nb2, 0)
+    Q = g.permute(Qcur, 0, 2, 1, 3)
+    K = g.permute(K_full, 0, 2, 1, 3)
+    scale = 1.0 / np.sqrt(hd)
+    if flash:
+        V = g.permute(V_full, 0, 2, 1, 3)
+        out = g.flash_attn_ext(Q, K, V, g.cast(m, gl.F16), scale, 0.0, 0.0)
+        return g.cont_2d(out, hd * n_head, n_new)
+    KQ = g.soft_max_ext(g.mul_mat(K, Q), m, scale, 0.0)
+    V_trans = g.cont_3d(g.permute(V_full, 1, 2, 0, 3), n_kv, hd, n_head_kv)
+    KQV = g.mul_mat(V_trans, KQ)
+    return g.cont_2d(g.permute(KQV, 0, 2, 1, 3), hd * n_head, n_new)
 
 
 # ---- node-by-node capture (debugging / parity localization) ----

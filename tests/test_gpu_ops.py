@@ -11,7 +11,7 @@ rel_err in gl.py), the ggml test-backend-ops bar for that op.
 import numpy as np
 import pytest
 
-from gl import Graph, cpu_backend, gl, quantize, rel_err, run_on
+from gl import Graph, attention_graph, cpu_backend, gl, quantize, rel_err, run_on
 
 pytestmark = pytest.mark.gpu
 
@@ -227,28 +227,6 @@ def test_argmax(hip, cpu):
     a, b = both(hip, cpu, build)
     assert np.array_equal(a.view(np.int32), b.view(np.int32))
     assert a.view(np.int32)[1] == 123
-
-
-def attention_graph(g, hd, n_head, n_head_kv, n_kv, n_new, n_ctx, kc, vc, q, mask, flash=False):
-    """The attention block of build_graph (reference model.cpp:1416-1444)."""
-    K_cache = g.tensor(gl.F16, hd, n_head_kv, n_ctx, data=kc)
-    V_cache = g.tensor(gl.F16, hd, n_head_kv, n_ctx, data=vc)
-    Qcur = g.tensor(gl.F32, hd, n_head, n_new, data=q)
-    m = g.tensor(gl.F32, n_kv, n_new, data=mask)
-    nb1, nb2 = hd * 2, hd * n_head_kv * 2
-    K_full = g.view_3d(K_cache, hd, n_head_kv, n_kv, nb1, nb2, 0)
-    V_full = g.view_3d(V_cache, hd, n_head_kv, n_kv, nb1, nb2, 0)
-    Q = g.permute(Qcur, 0, 2, 1, 3)
-    K = g.permute(K_full, 0, 2, 1, 3)
-    scale = 1.0 / np.sqrt(hd)
-    if flash:
-        V = g.permute(V_full, 0, 2, 1, 3)
-        out = g.flash_attn_ext(Q, K, V, g.cast(m, gl.F16), scale, 0.0, 0.0)
-        return g.cont_2d(out, hd * n_head, n_new)
-    KQ = g.soft_max_ext(g.mul_mat(K, Q), m, scale, 0.0)
-    V_trans = g.cont_3d(g.permute(V_full, 1, 2, 0, 3), n_kv, hd, n_head_kv)
-    KQV = g.mul_mat(V_trans, KQ)
-    return g.cont_2d(g.permute(KQV, 0, 2, 1, 3), hd * n_head, n_new)
 
 
 @pytest.mark.parametrize("hd,n_head,n_head_kv,n_kv,n_new", [
