@@ -47,21 +47,54 @@ def ensure_model(gl, path, config, seed):
     log(f"[bench] wrote synthetic {config} model {path} in {time.time() - t:.1f}s")
 
 
-def cpu_baseline(gl, model_path, n_pos, token, seconds, n_threads):
+def cpu_baseline(gl, model_path, n_pos, token, seconds, threads):
     """The oracle (CPU restatement of ggml-cpu, this repository's oracle/) timed on the host cores
-    on a bounded sample of the same workload: a few decode steps at the same position."""
+    on a bounded sample of the same workload: decode steps at the same position, one untimed warmup
+    step, at each thread count (the reference's cmd_bench hard-codes 8, cmd_bench.cpp:107)."""
     spec = importlib.util.spec_from_file_location("gl_test_helpers", os.path.join(ROOT, "tests", "gl.py"))
     helpers = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(helpers)
     helpers.oracle()  # registers the CPU backend
-    with gl.Session(model_path, "cpu", n_ctx=n_pos + 2, n_threads=n_threads) as c:
-        c.kv_fill_random(n_pos, seed=3)
-        _, t1 = c.decode_loop(n_pos, token, 1, fixed_pos=True)  # warmup, also sizes the sample
-        n = max(1, min(64, int(seconds / max(t1, 1e-6))))
-        _, t = c.decode_loop(n_pos, token, n, fixed_pos=True)
-    return {"value": n / t, "unit": "tok/s", "cores": n_threads, "kind": "port",
-            "sample": f"{n} decode steps at position {n_pos} ({t:.1f}s), oracle/ CPU restatement of ggml-cpu "
-                      f"(upstream ggml unavailable offline), {n_threads} threads"}
+    runs = {}
+    for nt in threads:
+        with gl.Session(model_path, "cpu", n_ctx=n_pos + 2, n_threads=nt) as c:
+            c.kv_fill_random(n_pos, seed=3)
+            _, t1 = c.decode_loop(n_pos, token, 1, fixed_pos=True)  # warmup, also sizes the sample
+            n = max(1, min(64, int(seconds / len(threads) / max(t1, 1e-6))))
+            _, t = c.decode_loop(n_pos, token, n, fixed_pos=True)
+        runs[nt] = (n / t, n, t)
+        log(f"[bench] cpu baseline {nt} threads: {n} steps in {t:.2f}s -> {n / t:.2f} tok/s")
+    main_nt = threads[0]
+    v, n, t = runs[main_nt]
+    return {"value": round(v, 3), "unit": "tok/s", "cores": main_nt, "kind": "port",
+            "sample": f"{n} decode steps at position {n_pos} ({t:.1f}s) of the same synthetic model on the oracle/ "
+                      f"CPU restatement of ggml-cpu (restated ggml-cpu semantics; upstream ggml unavailable offline), "
+                      f"{main_nt} threads",
+            "by_threads": {str(k): round(r[0], 3) for k, r in runs.items()}}
+
+
+def copy_kernel(gl, mb, reps):
+    """Runs the backend's own contiguous f32 copy (a ggml_cpy graph node) over mb MiB reps times:
+    the known-size kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
+    core = gl.libs()["core"]
+    n = mb * (1 << 20) // 4
+    ctx = core.ggml_init(gl.ggml_init_params(1 << 20, None, True))
+    a = core.ggml_new_tensor_1d(ctx, gl.F32, n)
+    b = core.ggml_new_tensor_1d(ctx, gl.F32, n)
+    out = core.ggml_cpy(ctx, a, b)
+    gf = core.ggml_new_graph(ctx)
+    core.ggml_build_forward_expand(gf, out)
+    be = gl.hip_backend(0)
+    buf = core.ggml_backend_alloc_ctx_tensors(ctx, be)
+    t = time.time()
+    for _ in range(reps):
+        assert core.ggml_backend_graph_compute(be, gf) == 0
+    dt = time.time() - t
+    core.ggml_backend_buffer_free(buf)
+    core.ggml_backend_free(be)
+    core.ggml_free(ctx)
+    print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "reps": reps,
+                      "GB/s": round(2 * n * 4 * reps / dt / 1e9, 1)}), flush=True)
 
 
 def main():
@@ -73,9 +106,10 @@ def main():
     ap.add_argument("--n-past", type=int, default=2048)
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--model-dir", default=os.environ.get("GL_BENCH_DIR", "/tmp/gl_bench"))
-    ap.add_argument("--profile-steps", type=int, default=10)
-    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--breakdown-steps", type=int, default=10, help="untimed steps with every kernel timed")
+    ap.add_argument("--cpu-seconds", type=float, default=24.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0, help="only run the copy kernel of this size (counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -86,6 +120,9 @@ def main():
     gl = load_pkg()
     if gl.hip_device_count() < 1:
         raise SystemExit("bench.py: no HIP device")
+    if args.copy_mb:
+        copy_kernel(gl, args.copy_mb, args.steps)
+        return
     cfg = gl.CONFIGS[args.config]
     wname = {gl.Q4_0: "q4_0", gl.Q8_0: "q8_0", gl.Q4_K: "q4_K"}[cfg["wtype"]]
     model_path = os.path.join(args.model_dir, f"{args.config}_{wname}_seed{args.seed}.gguf")
@@ -94,48 +131,64 @@ def main():
     n_past = args.n_past
     token = 12345 % cfg["n_vocab"]
     hipl = gl.libs()["hip"]
+    dominant = "gemv_" + wname
     with gl.Session(model_path, "hip", n_ctx=n_past + 2) as s:
         s.kv_fill_random(n_past, seed=3)
         s.decode_loop(n_past, token, args.warmup, fixed_pos=True)
+
+        # timed region: K steps; HIP events on the backend's stream bracket every launch of the
+        # dominant kernel (and only those), so its launch durations come from these same steps
+        hipl.ggml_backend_hip_set_profile_filter(s.backend, dominant.encode())
+        hipl.ggml_backend_hip_reset_profile(s.backend)
+        hipl.ggml_backend_hip_set_profiling(s.backend, True)
         _, secs = s.decode_loop(n_past, token, args.steps, fixed_pos=True)
+        hipl.ggml_backend_hip_set_profiling(s.backend, False)
+        timed = gl.profile(s.backend)
         value = args.steps / secs
         log(f"[bench] {args.steps} steps in {secs:.4f}s -> {value:.1f} tok/s ({1000 * secs / args.steps:.3f} ms/step)")
 
-        # per-kernel HIP-event timing over a second pass of the same steps
-        hipl.ggml_backend_hip_set_profiling(s.backend, True)
+        # untimed breakdown: every kernel bracketed
+        hipl.ggml_backend_hip_set_profile_filter(s.backend, b"")
         hipl.ggml_backend_hip_reset_profile(s.backend)
-        s.decode_loop(n_past, token, args.profile_steps, fixed_pos=True)
-        prof = gl.profile(s.backend)
+        hipl.ggml_backend_hip_set_profiling(s.backend, True)
+        s.decode_loop(n_past, token, args.breakdown_steps, fixed_pos=True)
         hipl.ggml_backend_hip_set_profiling(s.backend, False)
+        prof = gl.profile(s.backend)
         weights_bytes = s.get("weights_bytes")
 
     total_ms = sum(v[1] for v in prof.values())
+    breakdown = {}
     for k, (n, ms, by) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
         gbs = by / (ms * 1e-3) / 1e9 if ms > 0 and by > 0 else 0.0
-        log(f"[bench]   {k:22s} {n / args.profile_steps:7.1f}/step {ms / n * 1e3:8.2f} us/launch "
+        log(f"[bench]   {k:22s} {n / args.breakdown_steps:7.1f}/step {ms / n * 1e3:8.2f} us/launch "
             f"{100 * ms / total_ms:5.1f}%  {gbs:8.1f} GB/s")
-    gemv = [v for k, v in prof.items() if k.startswith("gemv_" + wname)]
+        breakdown[k] = {"launches_per_step": round(n / args.breakdown_steps, 2), "us_per_launch": round(ms / n * 1e3, 2),
+                        "GB/s": round(gbs, 1)}
+    gemv = [v for k, v in timed.items() if k.startswith(dominant)]
     g_launch = sum(v[0] for v in gemv)
     g_ms = sum(v[1] for v in gemv)
     g_bytes = sum(v[2] for v in gemv)
     achieved = g_bytes / (g_ms * 1e-3) / 1e9 if g_ms > 0 else 0.0
     roofline = {
         "bound": "hbm",
-        "kernel": f"gemv_{wname} (all launches of a step: fused QKV, O+residual, gate/up+SwiGLU, down+residual, LM head)",
         "achieved": round(achieved, 1),
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBS, 4),
         "traffic": None,
+        "kernel": f"{dominant}* (every quantized-GEMV launch of a step: QKV, O+residual, gate/up+SwiGLU, "
+                  "down+residual, LM head)",
+        "launches_per_step": round(g_launch / args.steps, 2),
         "bytes_per_launch": round(g_bytes / g_launch) if g_launch else None,
         "us_per_launch": round(g_ms / g_launch * 1e3, 3) if g_launch else None,
-        "kernel_time_per_step_ms": round(total_ms / args.profile_steps, 4),
+        "share_of_step": round(g_ms / (secs * 1e3), 4),
     }
 
     cpu = None
     if not args.no_cpu_baseline:
         try:
-            cpu = cpu_baseline(gl, model_path, n_past, token, args.cpu_seconds, min(16, os.cpu_count() or 1))
+            n_cpu = min(16, os.cpu_count() or 1)
+            cpu = cpu_baseline(gl, model_path, n_past, token, args.cpu_seconds, [n_cpu, 8] if n_cpu != 8 else [8])
         except Exception as e:  # the baseline is reported, never required
             log(f"[bench] cpu baseline failed: {e}")
 
@@ -150,14 +203,17 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 weights x q8_0 activations (int8 dot), f32 accumulate, f16 KV",
-        "data": "synthetic (seeded random-init weights N(0,0.02) quantized to Q4_0; KV cache N(0,1) F16)",
+        "dtype": "int8",
+        "data": f"synthetic (seeded random-init weights N(0,0.02) quantized to {wname.upper()}; KV cache N(0,1) F16)",
         "config": {"workload": f"{args.config}: Llama-arch decode, 1 token at position {n_past}, batch 1 "
                                f"(hidden 3072, 28 layers, 24/8 heads, head_dim 128, FFN 8192, vocab 128256, Q4_0)",
                    "global_batch": 1, "seq_len": n_past + 1, "parallelism": "single GPU",
-                   "weights_bytes": weights_bytes},
+                   "weights_bytes": weights_bytes,
+                   "arithmetic": "Q4_0 weights x Q8_0 activations by int8 dot products, f32 block sums; "
+                                 "F16 KV with f64 dot accumulation"},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "kernel_breakdown_us_per_step": {k: round(v["launches_per_step"] * v["us_per_launch"], 1) for k, v in breakdown.items()},
     }
     print(json.dumps(out), flush=True)
 

@@ -249,7 +249,8 @@ enum fuse_bits {
     FUSE_ADD    = 8,   // residual add in the GEMV epilogue
     FUSE_ATTN   = 16,  // split-KV decode attention
     FUSE_ACTQ   = 32,  // producers emit the Q8 activation their GEMV consumers read
-    FUSE_ALL    = 63,
+    FUSE_NORMQ  = 64,  // rms_norm * w folded into the prologue of the GEMVs that consume it
+    FUSE_ALL    = 127,
 };
 
 struct hip_backend_ctx {
@@ -258,6 +259,7 @@ struct hip_backend_ctx {
     int fuse_mask = FUSE_ALL;
     bool graph_replay = true;
     bool profiling = false;
+    std::string profile_filter;      // only kernels whose name starts with this get events
     ggml_backend_eval_callback cb = nullptr;
     void * cb_user = nullptr;
     scratch_arena scratch;
@@ -305,6 +307,8 @@ public:
         index_graph();
         done_.assign(g_->n_nodes, false);
         attn_.clear();
+        norm_.clear();
+        act_.clear();
         // plan the attention fusions first: the V^T copy precedes K^T Q in node order and must
         // not run when the chain is replaced
         if (fuse(FUSE_ATTN)) {
@@ -333,6 +337,7 @@ private:
     std::vector<std::vector<int>> users_;
     std::vector<bool> done_;
     std::unordered_map<const ggml_tensor *, act_entry> act_;
+    std::unordered_map<const ggml_tensor *, gemv_norm> norm_;   // deferred rms_norm * w outputs
     std::unordered_map<int, attn_match> attn_;
     std::vector<const ggml_tensor *> wrote_;
 
@@ -389,7 +394,11 @@ private:
         double bytes;
         hipEvent_t a = nullptr;
         prof_scope(executor * e, const char * n, double b) : ex(e), name(n), bytes(b) {
-            if (ex->c_.profiling) { a = ex->event(); HIP_CHECK(hipEventRecord(a, ex->st_)); }
+            if (ex->c_.profiling && ex->c_.profile_filter.compare(0, ex->c_.profile_filter.size(), n, 0,
+                                                                  ex->c_.profile_filter.size()) == 0) {
+                a = ex->event();
+                HIP_CHECK(hipEventRecord(a, ex->st_));
+            }
         }
         ~prof_scope() {
             if (!a) return;
@@ -444,6 +453,22 @@ private:
             kind = k;
         }
         return kind;
+    }
+
+    // rms_norm * w (node u, rows of N) whose every consumer is a quantized GEMV that can compute the
+    // normalization in its prologue: the normalized activation is then never materialized
+    bool norm_deferrable(int u, int64_t N) const {
+        if (!fuse(FUSE_NORMQ) || !fuse(FUSE_ACTQ) || is_output(u) || users_[u].empty()) return false;
+        const ggml_tensor * m = g_->nodes[u];
+        int kind = 0;
+        for (int j : users_[u]) {
+            const ggml_tensor * n = g_->nodes[j];
+            if (n->op != GGML_OP_MUL_MAT || n->src[1] != m || n->src[0] == m || attn_.count(j) || !gemv_capable(n)) return false;
+            const int k = dot_kind(n->src[0]->type);
+            if (kind && k != kind) return false;
+            kind = k;
+        }
+        return N <= (kind == 2 ? GEMV_NORM_MAX_K_Q8K : GEMV_NORM_MAX_K_Q8);
     }
 
     // ---- dispatch ----
@@ -535,7 +560,8 @@ private:
         float eps;
         memcpy(&eps, n->op_params, 4);
         const ggml_tensor * x = n->src[0];
-        const bool rows_ok = x->type == GGML_TYPE_F32 && ggml_is_contiguous(x) && ggml_is_contiguous(n);
+        const bool rows_ok = x->type == GGML_TYPE_F32 && ggml_is_contiguous(x) && ggml_is_contiguous(n) &&
+                             x->ne[0] <= RMS_NORM_MAX_ROW;
         if (fuse(FUSE_NORM) && rows_ok) {
             const int u = sole_user(i);
             if (u >= 0) {
@@ -544,6 +570,11 @@ private:
                 if (m->op == GGML_OP_MUL && m->src[0] == n && w->type == GGML_TYPE_F32 && ggml_nrows(w) == 1 &&
                     w->ne[0] == x->ne[0] && ggml_is_contiguous(w) && ggml_is_contiguous(m)) {
                     const int64_t N = x->ne[0], rows = ggml_nrows(x);
+                    if (m->ne[1] == rows && norm_deferrable(u, N) && ((uintptr_t) x->data | (uintptr_t) w->data) % 16 == 0) {
+                        norm_[m] = gemv_norm{ (const float *) x->data, N, (const float *) w->data, eps };
+                        done_[u] = true;
+                        return;
+                    }
                     const int kind = m->ne[1] == rows ? wanted_act_kind(u) : 0;
                     act_entry e{};
                     const bool q = (kind == 1 && N % 32 == 0) || (kind == 2 && N % 256 == 0);
@@ -625,7 +656,7 @@ private:
 
         // SwiGLU pair inside the group: gate -> silu -> mul(silu, up)
         int gate = -1, up = -1, mulnode = -1;
-        if (fuse(FUSE_SWIGLU) && group.size() >= 2) {
+        if (fuse(FUSE_SWIGLU) && group.size() >= 2 && (wtype == GGML_TYPE_Q4_K || K <= gemv_swiglu_max_k(wtype))) {
             for (int a : group) {
                 const int s = sole_user(a);
                 if (s < 0) continue;
@@ -644,7 +675,8 @@ private:
         }
 
         const int kind = dot_kind(wtype);
-        const act_entry * xa = ensure_act(x, kind);
+        const auto nz = norm_.find(x);
+        const act_entry * xa = nz == norm_.end() ? ensure_act(x, kind) : nullptr;
 
         auto fill_mat = [&](gemv_mat & gm, int j, double & bytes, bool epilogue) {
             ggml_tensor * mm = g_->nodes[j];
@@ -686,9 +718,10 @@ private:
         L.type = wtype;
         L.K = (int) K;
         L.ncols = (int) ncols;
-        if (kind == 1) { L.xq = xa->q8.qs; L.xd = xa->q8.d; L.xs = xa->q8.s; }
+        if (!xa) L.norm = nz->second;
+        else if (kind == 1) { L.xq = xa->q8.qs; L.xd = xa->q8.d; L.xs = xa->q8.s; }
         else { L.xq = xa->q8k.qs; L.xd = xa->q8k.d; L.xbs = xa->q8k.bsums; }
-        const double x_bytes = (double) (K * ncols * 4);
+        const double x_bytes = (double) (K * ncols * 4) + (xa ? 0.0 : (double) (K * 4));
 
         if (gate >= 0) {
             // SwiGLU launch for (gate, up); the rest of the group goes in a second launch
@@ -974,6 +1007,9 @@ void ggml_backend_hip_set_graph_replay(ggml_backend_t backend, bool enable) {
 }
 void ggml_backend_hip_set_profiling(ggml_backend_t backend, bool enable) {
     if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->profiling = enable;
+}
+void ggml_backend_hip_set_profile_filter(ggml_backend_t backend, const char * prefix) {
+    if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->profile_filter = prefix ? prefix : "";
 }
 void ggml_backend_hip_reset_profile(ggml_backend_t backend) {
     if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->prof.clear();

@@ -57,6 +57,12 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
 // sum within aligned groups of G lanes (G a power of two <= 64)
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {

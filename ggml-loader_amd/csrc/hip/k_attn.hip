@@ -58,12 +58,6 @@ __device__ __forceinline__ float mask_at(const attn_launch & A, int q, int t) {
     return A.mask_f16 ? __half2float(((const __half *) row)[t]) : ((const float *) row)[t];
 }
 
-__device__ __forceinline__ double wave_sum_dbl(double v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
-
 // stage rows [t0, t0+nt) of a [pos][hd] F16 cache view (row stride nb_pos halves) into LDS rows of
 // STRIDE dwords; rows >= nt are zero
 template <int HD, int STRIDE>
@@ -151,7 +145,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_kernel(const attn_la
         pr[t] = e;
         sum += (double) e;
     }
-    sum = wave_sum_dbl(sum);
+    sum = wave_sum_d(sum);
     if (lane == 0) s_s[wave] = sum;
     __syncthreads();
     double tot = 0.0;

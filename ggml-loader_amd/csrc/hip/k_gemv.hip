@@ -272,6 +272,153 @@ __host__ __device__ inline size_t gemv_lds_bytes(int K, int rows_per_block, int 
     return (size_t) K + (size_t) nb * 8 + (size_t) rows_per_block * n_chain * nb * 4;
 }
 
+template <int TYPE>
+__device__ __forceinline__ gemv_lds lds_layout(uint8_t * smem, int K) {
+    gemv_lds s;
+    s.xq = (int8_t *) smem;
+    s.xs = nullptr;
+    s.xbs = nullptr;
+    if (TYPE == GGML_TYPE_Q4_K) {
+        const int nsb = K / 256;
+        s.xd = (float *) (smem + K);
+        s.xbs = (int16_t *) (smem + K + nsb * 4);
+        s.terms = (float *) (smem + ((K + nsb * 4 + (K / 16) * 2 + 15) & ~15));
+    } else {
+        const int nb = K / 32;
+        s.xd = (float *) (smem + K);
+        s.xs = (int32_t *) (smem + K + nb * 4);
+        s.terms = (float *) (smem + K + nb * 8);
+    }
+    return s;
+}
+
+__device__ __forceinline__ int pack4(int a, int b, int c, int d) {
+    return (a & 0xff) | ((b & 0xff) << 8) | ((c & 0xff) << 16) | (d << 24);
+}
+
+// rms_norm(x) * w of column col, quantized straight into the LDS staging area with the roundings of
+// ggml's rms_norm -> mul -> quantize_row_q8_0 (Q4_0/Q8_0 weights) or quantize_row_q8_K (Q4_K)
+// chain. Thread t owns one 32-element Q8_0 block (one 16-element group of a Q8_K super-block), so
+// block maxima and sums are thread-local; only the sum of squares is reduced over the workgroup.
+template <int TYPE>
+__device__ __forceinline__ void stage_norm(const gemv_launch & L, int col, const gemv_lds & s, double * s_red) {
+    constexpr int C = TYPE == GGML_TYPE_Q4_K ? 16 : 32;
+    const int K = L.K;
+    const int t = threadIdx.x;
+    const int lane = t % WAVE, wave = t / WAVE;
+    const bool has = t < K / C;
+    float v[C], wv[C];
+#pragma unroll
+    for (int e = 0; e < C; e++) { v[e] = 0.0f; wv[e] = 1.0f; }
+    if (has) {
+        const float4 * xr = (const float4 *) (L.norm.x + (int64_t) col * L.norm.x_stride + (int64_t) t * C);
+#pragma unroll
+        for (int k = 0; k < C / 4; k++) {
+            const float4 f = xr[k];
+            v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+        }
+        if (L.norm.w) {
+            const float4 * wr = (const float4 *) (L.norm.w + (int64_t) t * C);
+#pragma unroll
+            for (int k = 0; k < C / 4; k++) {
+                const float4 f = wr[k];
+                wv[4 * k] = f.x; wv[4 * k + 1] = f.y; wv[4 * k + 2] = f.z; wv[4 * k + 3] = f.w;
+            }
+        }
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int e = 0; e < C; e++) ss += (double) (v[e] * v[e]);
+    ss = wave_sum_d(ss);
+    if (lane == 0) s_red[wave] = ss;
+    __syncthreads();
+    double total = 0.0;
+    for (int w = 0; w < (int) (blockDim.x / WAVE); w++) total += s_red[w];
+    const float mean = (float) (total / (double) K);
+    const float scale = 1.0f / sqrtf(mean + L.norm.eps);
+#pragma unroll
+    for (int e = 0; e < C; e++) {
+        v[e] = v[e] * scale;
+        if (L.norm.w) v[e] = v[e] * wv[e];
+    }
+    if (TYPE != GGML_TYPE_Q4_K) {
+        if (!has) return;
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < C; e++) amax = fmaxf(amax, fabsf(v[e]));
+        const float dd = amax / 127;
+        const float id = dd ? 1.0f / dd : 0.0f;
+        int q[C];
+        int sum = 0;
+#pragma unroll
+        for (int e = 0; e < C; e++) {
+            q[e] = (int) roundf(v[e] * id);
+            sum += q[e];
+        }
+        int4 * dst = (int4 *) (s.xq + t * C);
+        dst[0] = make_int4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]),
+                           pack4(q[8], q[9], q[10], q[11]), pack4(q[12], q[13], q[14], q[15]));
+        dst[1] = make_int4(pack4(q[16], q[17], q[18], q[19]), pack4(q[20], q[21], q[22], q[23]),
+                           pack4(q[24], q[25], q[26], q[27]), pack4(q[28], q[29], q[30], q[31]));
+        s.xd[t] = __half2float(__float2half_rn(dd));
+        s.xs[t] = sum;
+    } else {
+        // the super-block's value of largest magnitude, the first one on ties (16 lanes per block)
+        float ax = -1.0f, val = 0.0f;
+        int idx = 0;
+        if (has) {
+#pragma unroll
+            for (int e = 0; e < C; e++) {
+                const float a = fabsf(v[e]);
+                if (a > ax) { ax = a; idx = t * C + e; val = v[e]; }
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            const float ax2 = __shfl_xor(ax, o, WAVE);
+            const int idx2 = __shfl_xor(idx, o, WAVE);
+            const float val2 = __shfl_xor(val, o, WAVE);
+            if (ax2 > ax || (ax2 == ax && idx2 < idx)) { ax = ax2; idx = idx2; val = val2; }
+        }
+        if (!has) return;
+        int q[C];
+        int bsum = 0;
+        const float iscale = ax != 0.0f ? -127.f / val : 0.0f;
+#pragma unroll
+        for (int e = 0; e < C; e++) {
+            int qv = ax != 0.0f ? round_half_even(iscale * v[e]) : 0;
+            q[e] = qv < 127 ? qv : 127;
+            bsum += q[e];
+        }
+        *(int4 *) (s.xq + t * C) = make_int4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]),
+                                             pack4(q[8], q[9], q[10], q[11]), pack4(q[12], q[13], q[14], q[15]));
+        s.xbs[t] = (int16_t) bsum;
+        if ((t % 16) == 0) s.xd[t / 16] = ax != 0.0f ? 1 / iscale : 0.0f;
+    }
+}
+
+// the quantized activation column in LDS: copied, or computed by the RMSNorm prologue
+template <int TYPE>
+__device__ __forceinline__ void stage_x(const gemv_launch & L, int col, const gemv_lds & s, double * s_red) {
+    const int K = L.K;
+    if (L.norm.x) {
+        stage_norm<TYPE>(L, col, s, s_red);
+    } else if (TYPE == GGML_TYPE_Q4_K) {
+        const int nsb = K / 256;
+        for (int i = threadIdx.x * 16; i < K; i += blockDim.x * 16) *(int4 *) (s.xq + i) = *(const int4 *) (L.xq + (int64_t) col * K + i);
+        for (int i = threadIdx.x; i < nsb; i += blockDim.x) s.xd[i] = L.xd[(int64_t) col * nsb + i];
+        for (int i = threadIdx.x; i < K / 16; i += blockDim.x) s.xbs[i] = L.xbs[(int64_t) col * (K / 16) + i];
+    } else {
+        const int nb = K / 32;
+        for (int i = threadIdx.x * 16; i < K; i += blockDim.x * 16) *(int4 *) (s.xq + i) = *(const int4 *) (L.xq + (int64_t) col * K + i);
+        for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+            s.xd[i] = L.xd[(int64_t) col * nb + i];
+            s.xs[i] = L.xs[(int64_t) col * nb + i];
+        }
+    }
+    __syncthreads();
+}
+
 template <int TYPE, int LPR, bool SWIGLU, int ITS>
 __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -291,53 +438,37 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
     const int mi = SWIGLU ? 0 : find_mat(a, valid ? row : 0);
     const int lrow = SWIGLU ? row : row - a.row_begin[mi];
 
-    // ---- stage the activation column in LDS ----
-    gemv_lds s;
-    s.xq = (int8_t *) smem;
-    if (TYPE == GGML_TYPE_Q4_K) {
-        const int nsb = K / 256;
-        s.xd = (float *) (smem + K);
-        s.xbs = (int16_t *) (smem + K + nsb * 4);
-        s.terms = (float *) (smem + ((K + nsb * 4 + (K / 16) * 2 + 15) & ~15));
-        for (int i = threadIdx.x * 16; i < K; i += blockDim.x * 16) *(int4 *) (s.xq + i) = *(const int4 *) (L.xq + (int64_t) col * K + i);
-        for (int i = threadIdx.x; i < nsb; i += blockDim.x) s.xd[i] = L.xd[(int64_t) col * nsb + i];
-        for (int i = threadIdx.x; i < K / 16; i += blockDim.x) s.xbs[i] = L.xbs[(int64_t) col * (K / 16) + i];
-    } else {
-        const int nb = K / 32;
-        s.xd = (float *) (smem + K);
-        s.xs = (int32_t *) (smem + K + nb * 4);
-        s.terms = (float *) (smem + K + nb * 8);
-        for (int i = threadIdx.x * 16; i < K; i += blockDim.x * 16) *(int4 *) (s.xq + i) = *(const int4 *) (L.xq + (int64_t) col * K + i);
-        for (int i = threadIdx.x; i < nb; i += blockDim.x) {
-            s.xd[i] = L.xd[(int64_t) col * nb + i];
-            s.xs[i] = L.xs[(int64_t) col * nb + i];
-        }
-    }
-    __syncthreads();
+    const gemv_lds s = lds_layout<TYPE>(smem, K);
+    __shared__ double s_red[512 / WAVE];
 
     // ---- per-block terms ----
     if (TYPE == GGML_TYPE_Q4_0 || TYPE == GGML_TYPE_Q8_0) {
         constexpr int QS = TYPE == GGML_TYPE_Q4_0 ? Q4_0_QS : Q8_0_QS;
         constexpr int MAXIT = ITS;   // blocks per lane (nb <= ITS * LPR)
         const int nb = K / 32;
+        // every weight load of this lane is issued before the activation is staged, so the weight
+        // stream is in flight while the column is copied or normalized and quantized
+        uint4 qa[NCH][MAXIT], qb[NCH][MAXIT];
+        float dw[NCH][MAXIT];
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++) {
-            if (!valid) break;
             const uint8_t * wq = L.m[SWIGLU ? ch : mi].w + (int64_t) lrow * nb * QS;
             const __half * wd = L.m[SWIGLU ? ch : mi].wd + (int64_t) lrow * nb;
-            float * terms = s.terms + (rib * NCH + ch) * nb;
-            // issue every weight load of this lane first
-            uint4 qa[MAXIT], qb[MAXIT];
-            float dw[MAXIT];
 #pragma unroll
             for (int it = 0; it < MAXIT; it++) {
                 const int b = l + it * LPR;
-                if (b < nb) {
-                    qa[it] = *(const uint4 *) (wq + (int64_t) b * QS);
-                    if (TYPE == GGML_TYPE_Q8_0) qb[it] = *(const uint4 *) (wq + (int64_t) b * QS + 16);
-                    dw[it] = __half2float(wd[b]);
+                if (valid && b < nb) {
+                    qa[ch][it] = *(const uint4 *) (wq + (int64_t) b * QS);
+                    if (TYPE == GGML_TYPE_Q8_0) qb[ch][it] = *(const uint4 *) (wq + (int64_t) b * QS + 16);
+                    dw[ch][it] = __half2float(wd[b]);
                 }
             }
+        }
+        stage_x<TYPE>(L, col, s, s_red);
+#pragma unroll
+        for (int ch = 0; ch < NCH; ch++) {
+            if (!valid) break;
+            float * terms = s.terms + (rib * NCH + ch) * nb;
 #pragma unroll
             for (int it = 0; it < MAXIT; it++) {
                 const int b = l + it * LPR;
@@ -347,17 +478,18 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                     const float dx = s.xd[b];
                     float t;
                     if (TYPE == GGML_TYPE_Q4_0) {
-                        const int sumi = dot_q4_0_block(qa[it], xa, xb) - 8 * s.xs[b];
-                        t = ((float) sumi * dw[it]) * dx;           // ggml: sumi*d_x*d_y
+                        const int sumi = dot_q4_0_block(qa[ch][it], xa, xb) - 8 * s.xs[b];
+                        t = ((float) sumi * dw[ch][it]) * dx;           // ggml: sumi*d_x*d_y
                     } else {
-                        const int sumi = dot_q8_0_block(qa[it], qb[it], xa, xb);
-                        t = (float) sumi * (dw[it] * dx);           // ggml: sumi*(d_x*d_y)
+                        const int sumi = dot_q8_0_block(qa[ch][it], qb[ch][it], xa, xb);
+                        t = (float) sumi * (dw[ch][it] * dx);           // ggml: sumi*(d_x*d_y)
                     }
                     terms[b] = t;
                 }
             }
         }
     } else { // Q4_K: per (super-block, l) products d*aux32[l] and dmin*mins
+        stage_x<TYPE>(L, col, s, s_red);
         constexpr int MAXU = 608 / LPR;   // supports K <= 9728 * 4 (units = K/64 <= 608)
         const int units = K / 64, nsb = K / 256;
         const int64_t row_bytes = (int64_t) nsb * Q4_K_BYTES;
@@ -503,7 +635,8 @@ static void launch_gemv_its(gemv_kargs & ka, int waves, hipStream_t st) {
     HIP_CHECK(hipGetLastError());
 }
 
-// ITS = weight blocks per lane for Q4_0/Q8_0 (register-resident, loaded up front)
+// ITS = weight blocks per lane for Q4_0/Q8_0, held in registers from the up-front loads. The ladder
+// stops where the registers of both SwiGLU chains would spill (12) and at 16 for a single chain.
 template <int TYPE, int LPR, bool SWIGLU>
 static void launch_gemv_t(gemv_kargs & ka, int waves, hipStream_t st) {
     if constexpr (TYPE == GGML_TYPE_Q4_K) {
@@ -515,9 +648,16 @@ static void launch_gemv_t(gemv_kargs & ka, int waves, hipStream_t st) {
         else if (its <= 4) launch_gemv_its<TYPE, LPR, SWIGLU, 4>(ka, waves, st);
         else if (its <= 6) launch_gemv_its<TYPE, LPR, SWIGLU, 6>(ka, waves, st);
         else if (its <= 8) launch_gemv_its<TYPE, LPR, SWIGLU, 8>(ka, waves, st);
-        else if (its <= 16) launch_gemv_its<TYPE, LPR, SWIGLU, 16>(ka, waves, st);
-        else if constexpr (TYPE == GGML_TYPE_Q4_0) launch_gemv_its<TYPE, LPR, SWIGLU, 32>(ka, waves, st);
-        else HIP_ABORT("gemv q8_0: K=%d exceeds 8192", ka.L.K);
+        else if constexpr (!SWIGLU) {
+            if (its <= 12) launch_gemv_its<TYPE, LPR, SWIGLU, 12>(ka, waves, st);
+            else if (its <= 16) launch_gemv_its<TYPE, LPR, SWIGLU, 16>(ka, waves, st);
+            else HIP_ABORT("gemv: K=%d is too long", ka.L.K);
+        } else if constexpr (TYPE == GGML_TYPE_Q4_0) {
+            if (its <= 12) launch_gemv_its<TYPE, LPR, SWIGLU, 12>(ka, waves, st);
+            else HIP_ABORT("gemv: SwiGLU launch with K=%d exceeds %d", ka.L.K, gemv_swiglu_max_k(TYPE));
+        } else {
+            HIP_ABORT("gemv: SwiGLU launch with K=%d exceeds %d", ka.L.K, gemv_swiglu_max_k(TYPE));
+        }
     }
 }
 
@@ -533,16 +673,23 @@ void launch_gemv(const gemv_launch & L, hipStream_t st) {
     ka.total_rows = L.swiglu ? L.m[0].n_rows : r;
     if (L.swiglu && (L.n_mats != 2 || L.m[0].n_rows != L.m[1].n_rows)) HIP_ABORT("gemv: swiglu needs two equal matrices");
     if (L.swiglu && L.act_q.qs && (ka.total_rows % 32 != 0)) HIP_ABORT("gemv: quantized swiglu output needs rows %% 32 == 0");
+    if (L.norm.x) {
+        const int max_k = L.type == GGML_TYPE_Q4_K ? GEMV_NORM_MAX_K_Q8K : GEMV_NORM_MAX_K_Q8;
+        if (L.K > max_k) HIP_ABORT("gemv: the RMSNorm prologue handles K <= %d (K=%d)", max_k, L.K);
+        if (((uintptr_t) L.norm.x | (uintptr_t) L.norm.w) % 16 || L.norm.x_stride % 4) HIP_ABORT("gemv: RMSNorm prologue operands must be 16-byte aligned");
+    }
     switch (L.type) {
         case GGML_TYPE_Q4_0:
-            if (L.K % 32 || L.K > 16384) HIP_ABORT("gemv q4_0: K=%d unsupported", L.K);
+            if (L.K % 32 || L.K > GEMV_MAX_K) HIP_ABORT("gemv q4_0: K=%d unsupported", L.K);
             if (L.swiglu) launch_gemv_t<GGML_TYPE_Q4_0, 16, true>(ka, 8, st);
-            else launch_gemv_t<GGML_TYPE_Q4_0, 16, false>(ka, 4, st);
+            else if (L.K <= 8192) launch_gemv_t<GGML_TYPE_Q4_0, 16, false>(ka, 4, st);
+            else launch_gemv_t<GGML_TYPE_Q4_0, 32, false>(ka, 4, st);
             break;
         case GGML_TYPE_Q8_0:
-            if (L.K % 32 || L.K > 16384) HIP_ABORT("gemv q8_0: K=%d unsupported", L.K);
+            if (L.K % 32 || L.K > GEMV_MAX_K) HIP_ABORT("gemv q8_0: K=%d unsupported", L.K);
             if (L.swiglu) launch_gemv_t<GGML_TYPE_Q8_0, 16, true>(ka, 8, st);
-            else launch_gemv_t<GGML_TYPE_Q8_0, 16, false>(ka, 4, st);
+            else if (L.K <= 8192) launch_gemv_t<GGML_TYPE_Q8_0, 16, false>(ka, 4, st);
+            else launch_gemv_t<GGML_TYPE_Q8_0, 32, false>(ka, 4, st);
             break;
         case GGML_TYPE_Q4_K:
             if (L.K % 256 || L.K / 64 > 608) HIP_ABORT("gemv q4_K: K=%d unsupported", L.K);

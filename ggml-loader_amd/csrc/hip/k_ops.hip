@@ -58,12 +58,6 @@ static unsigned grid1(int64_t n, int threads) { return (unsigned) ((n + threads 
 // ---------------------------------------------------------------------------------------------
 // RMSNorm (+ weight multiply, + activation quantization)
 
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
-
 // One 256-thread block per row; each thread holds its EPT elements (i = it*256 + t) in registers,
 // so the row is read once with every load issued up front.
 template <int QUANT, int EPT> // QUANT: 0 none, 1 Q8_0 (32-blocks), 2 Q8_K (256-blocks)

@@ -32,6 +32,10 @@ void launch_quantize_q8k(const float * x, int64_t x_col_stride, int64_t K, int64
 // quantized GEMV / small-batch GEMM: y[c][r] = W[r] . x[c] (+ add[c][r]) for up to 4 weight
 // matrices of one type and row length K sharing the same activation (one launch).
 constexpr int GEMV_MAX_MATS = 4;
+constexpr int GEMV_MAX_K = 16384;          // Q4_0 / Q8_0 rows
+// longest Q4_0 / Q8_0 rows of a gate/up pair in one SwiGLU launch (both chains' weight blocks stay
+// in registers)
+constexpr int gemv_swiglu_max_k(int type) { return type == 8 /* GGML_TYPE_Q8_0 */ ? 4096 : 6144; }
 
 struct gemv_mat {
     const uint8_t * w;     // Q4_0/Q8_0: qs plane of the first row; Q4_K: first block
@@ -43,17 +47,36 @@ struct gemv_mat {
     int32_t         n_rows;
 };
 
+// RMSNorm prologue of a GEMV: the activation is rms_norm(x) * w, computed and quantized by every
+// workgroup for its column (ggml's rms_norm -> mul -> quantize_row_q8_0 / q8_K chain, same roundings)
+struct gemv_norm {
+    const float * x;       // raw input, column c at x + c * x_stride (nullptr: no prologue)
+    int64_t       x_stride;
+    const float * w;       // norm weight [K] (nullptr: rms_norm without the multiply)
+    float         eps;
+};
+
+// largest K the prologue handles (one 32-element Q8_0 block or one 16-element Q8_K group per thread
+// of the smallest launch, 256 threads)
+constexpr int GEMV_NORM_MAX_K_Q8 = 256 * 32;
+// longest row of the register-resident rms_norm kernel (32 elements per thread); longer rows go
+// through the strided kernel
+constexpr int RMS_NORM_MAX_ROW = 256 * 32;
+constexpr int GEMV_NORM_MAX_K_Q8K = 256 * 16;
+
 struct gemv_launch {
     int        type;       // GGML_TYPE_Q4_0 / Q8_0 / Q4_K
     int        K;
     int        ncols;
     int        n_mats;
     gemv_mat   m[GEMV_MAX_MATS];
-    // activation (already quantized; column c at +c*K int8 and +c*K/32 (q8) or K/256 (q8K) scales)
+    // activation (already quantized; column c at +c*K int8 and +c*K/32 (q8) or K/256 (q8K) scales),
+    // unused when norm.x is set
     const int8_t *  xq;
     const float *   xd;
     const int32_t * xs;    // q8: block sums
     const int16_t * xbs;   // q8K: 16-wise sums
+    gemv_norm  norm;
     // SwiGLU epilogue: m[0] = gate, m[1] = up (same n_rows); writes act = silu(g) * u to m[0].y
     // and, when act_q.qs is set, the Q8_0-quantized act (for the following down projection)
     bool       swiglu;

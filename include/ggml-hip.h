@@ -35,6 +35,9 @@ GGML_API void ggml_backend_hip_set_graph_replay(ggml_backend_t backend, bool ena
 // Per-kernel timing with HIP events recorded on the backend's own stream. While enabled, every
 // launch of graph_compute is bracketed by events; stats accumulate per kernel name until reset.
 GGML_API void ggml_backend_hip_set_profiling(ggml_backend_t backend, bool enable);
+// Restricts the events to kernels whose name starts with prefix (NULL or "" = every kernel), so a
+// timed run can measure one kernel without bracketing every launch.
+GGML_API void ggml_backend_hip_set_profile_filter(ggml_backend_t backend, const char * prefix);
 GGML_API void ggml_backend_hip_reset_profile(ggml_backend_t backend);
 // Number of distinct kernel names recorded.
 GGML_API int  ggml_backend_hip_profile_count(ggml_backend_t backend);

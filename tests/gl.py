@@ -162,6 +162,7 @@ class Graph:
             outs = [outs]
         gf = self.core.ggml_new_graph(self.ctx)
         for o in outs:
+            self.core.ggml_set_output(o)   # read back after compute: ggml's output contract
             self.core.ggml_build_forward_expand(gf, o)
         self.buf = self.core.ggml_backend_alloc_ctx_tensors(self.ctx, backend)
         for t, a in self.inputs:

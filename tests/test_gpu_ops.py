@@ -167,6 +167,35 @@ def test_rms_norm_mul_then_gemv(hip, cpu, n, rows):
         assert np.array_equal(z1, z2), (fusion, rel_err(z1, z2))
 
 
+@pytest.mark.parametrize("qtype,n", [(gl.Q4_0, 3072), (gl.Q8_0, 4096), (gl.Q4_K, 2560), (gl.Q4_K, 4096),
+                                     (gl.Q4_0, 96), (gl.Q4_0, 9216)])
+@pytest.mark.parametrize("ncols", [1, 3])
+def test_rms_norm_folded_into_gemv(hip, cpu, qtype, n, ncols):
+    """rms_norm * w read only by GEMVs (Q, K and V; a gate/up pair with SwiGLU): the GEMVs compute
+    and quantize the normalization in their prologue and it is never materialized (K = 9216 is
+    beyond the prologue and takes the materialized path)."""
+    x = rng(20).standard_normal((ncols, n)).astype(np.float32) * 2
+    w1 = (1 + 0.01 * rng(21).standard_normal(n)).astype(np.float32)
+    w2 = (1 + 0.01 * rng(27).standard_normal(n)).astype(np.float32)
+    Wq, Wk, Wv = (qweight(qtype, n, r, s) for r, s in ((256, 22), (64, 23), (64, 24)))
+    Wg, Wu = qweight(qtype, n, 512, 25), qweight(qtype, n, 512, 26)
+
+    def build(g):
+        xt = g.tensor(gl.F32, n, ncols, data=x)
+        y = g.mul(g.rms_norm(xt, 1e-5), g.tensor(gl.F32, n, data=w1))
+        q = g.mul_mat(g.tensor(qtype, n, 256, data=Wq), y)
+        k = g.mul_mat(g.tensor(qtype, n, 64, data=Wk), y)
+        v = g.mul_mat(g.tensor(qtype, n, 64, data=Wv), y)
+        y2 = g.mul(g.rms_norm(xt, 1e-6), g.tensor(gl.F32, n, data=w2))
+        act = g.mul(g.silu(g.mul_mat(g.tensor(qtype, n, 512, data=Wg), y2)), g.mul_mat(g.tensor(qtype, n, 512, data=Wu), y2))
+        return [q, k, v, act]
+
+    for fusion in (True, False):
+        hs, cs = both(hip, cpu, build, fusion)
+        for a, b in zip(hs, cs):
+            assert np.array_equal(a, b), (fusion, rel_err(a, b))
+
+
 @pytest.mark.parametrize("mode", [gl.ROPE_NORMAL, gl.ROPE_NEOX])
 @pytest.mark.parametrize("hd,n_head,theta", [(128, 8, 500000.0), (128, 4, 1e6), (96, 4, 10000.0)])
 def test_rope(hip, cpu, mode, hd, n_head, theta):
