@@ -28,6 +28,8 @@
 #include <unordered_map>
 #include <vector>
 
+thread_local launch_timing g_launch_timing;
+
 namespace {
 
 // ---------------------------------------------------------------------------------------------
@@ -250,7 +252,8 @@ enum fuse_bits {
     FUSE_ATTN   = 16,  // split-KV decode attention
     FUSE_ACTQ   = 32,  // producers emit the Q8 activation their GEMV consumers read
     FUSE_NORMQ  = 64,  // rms_norm * w folded into the prologue of the GEMVs that consume it
-    FUSE_ALL    = 127,
+    FUSE_ROPE   = 128, // RoPE stored straight into the KV cache; independent RoPE/copies in one launch
+    FUSE_ALL    = 255,
 };
 
 struct hip_backend_ctx {
@@ -388,23 +391,24 @@ private:
         }
         return c_.event_pool[c_.event_next++];
     }
+    // times the kernels launched while it lives (one op) through their dispatch timestamps
     struct prof_scope {
         executor * ex;
         const char * name;
         double bytes;
-        hipEvent_t a = nullptr;
+        bool on = false;
         prof_scope(executor * e, const char * n, double b) : ex(e), name(n), bytes(b) {
             if (ex->c_.profiling && ex->c_.profile_filter.compare(0, ex->c_.profile_filter.size(), n, 0,
                                                                   ex->c_.profile_filter.size()) == 0) {
-                a = ex->event();
-                HIP_CHECK(hipEventRecord(a, ex->st_));
+                g_launch_timing = launch_timing{ ex->event(), ex->event(), 0 };
+                on = true;
             }
         }
         ~prof_scope() {
-            if (!a) return;
-            hipEvent_t b = ex->event();
-            HIP_CHECK(hipEventRecord(b, ex->st_));
-            ex->c_.pending.push_back({ name, bytes, a, b });
+            if (!on) return;
+            const launch_timing t = g_launch_timing;
+            g_launch_timing = launch_timing{};
+            if (t.launches > 0) ex->c_.pending.push_back({ name, bytes, t.start, t.stop });
         }
     };
 
@@ -478,6 +482,7 @@ private:
             case GGML_OP_NONE: case GGML_OP_RESHAPE: case GGML_OP_VIEW: case GGML_OP_PERMUTE: case GGML_OP_TRANSPOSE:
                 return;
             case GGML_OP_RMS_NORM: op_rms_norm(i); return;
+            case GGML_OP_ROPE: op_rope(i); return;
             case GGML_OP_MUL_MAT: op_mul_mat(i); return;
             default: break;
         }
@@ -508,7 +513,7 @@ private:
                 launch_cpy(tv(n->src[0]), tv(n), st_);
                 return;
             }
-            case GGML_OP_ROPE: op_rope(n); return;
+
             case GGML_OP_SOFT_MAX: {
                 float scale, max_bias;
                 memcpy(&scale, &n->op_params[0], 4);
@@ -534,7 +539,18 @@ private:
         launch_get_rows(tv(a), tv(n->src[1]), tv(n), p.qs, p.d, p.first_block, st_);
     }
 
-    void op_rope(ggml_tensor * n) {
+    static bool is_view_op(int op) {
+        return op == GGML_OP_NONE || op == GGML_OP_RESHAPE || op == GGML_OP_VIEW || op == GGML_OP_PERMUTE ||
+               op == GGML_OP_TRANSPOSE;
+    }
+    // the data of t is final before the next launch: a leaf, a finished node, or a view of one
+    bool ready(const ggml_tensor * t) const {
+        const int k = node_index(t);
+        if (k < 0 || done_[k]) return true;
+        return is_view_op(t->op) && t->src[0] && ready(t->src[0]);
+    }
+
+    static rope_params rope_params_of(const ggml_tensor * n) {
         rope_params p{};
         p.n_dims = n->op_params[1];
         p.mode = n->op_params[2];
@@ -548,10 +564,62 @@ private:
         memcpy(&beta_slow, n->op_params + 10, 4);
         ggml_rope_yarn_corr_dims(p.n_dims, n_ctx_orig, freq_base, beta_fast, beta_slow, p.corr_dims);
         p.theta_scale = powf(freq_base, -2.0f / p.n_dims);
+        return p;
+    }
+
+    // RoPE node i as a job; when its only consumer copies it into an F16/F32 tensor of the same shape
+    // (the KV cache append), the rotation is stored there directly
+    void add_rope_job(rope_batch & B, std::vector<int> & members, int i) {
+        ggml_tensor * n = g_->nodes[i];
         if (n->src[0]->type != GGML_TYPE_F32 || n->type != GGML_TYPE_F32) HIP_ABORT("rope: f32 only");
-        prof_scope ps(this, "rope", 0);
-        launch_rope(tv(n->src[0]), (const int32_t *) n->src[1]->data, n->src[2] ? (const float *) n->src[2]->data : nullptr,
-                    tv(n), p, st_);
+        ggml_tensor * dst = n;
+        const int u = fuse(FUSE_ROPE) ? sole_user(i) : -1;
+        if (u >= 0) {
+            ggml_tensor * c = g_->nodes[u];
+            if (c->op == GGML_OP_CPY && c->src[0] == n && (c->type == GGML_TYPE_F16 || c->type == GGML_TYPE_F32) &&
+                ggml_are_same_shape(n, c)) {
+                dst = c;
+                members.push_back(u);
+            }
+        }
+        B.job[B.n_jobs++] = rope_job{ tv(n->src[0]), tv(dst), (const int32_t *) n->src[1]->data,
+                                      n->src[2] ? (const float *) n->src[2]->data : nullptr, rope_params_of(n),
+                                      ggml_nelements(n->src[0]) / 2 };
+        members.push_back(i);
+        wrote_.push_back(dst);
+    }
+
+    // RoPE node i, launched together with the RoPE nodes and F32 -> F16/F32 copies that follow it
+    // in the graph and whose inputs are already final (the window holds views, RoPEs and copies
+    // only, none of which reads what another writes)
+    void op_rope(int i) {
+        rope_batch B{};
+        std::vector<int> members;
+        add_rope_job(B, members, i);
+        if (fuse(FUSE_ROPE)) {
+            for (int j = i + 1; j < g_->n_nodes && B.n_jobs < ROPE_MAX_JOBS; j++) {
+                const ggml_tensor * m = g_->nodes[j];
+                if (done_[j] || std::find(members.begin(), members.end(), j) != members.end() || is_view_op(m->op)) continue;
+                if (m->op == GGML_OP_ROPE && m->src[0]->type == GGML_TYPE_F32 && m->type == GGML_TYPE_F32 &&
+                    ready(m->src[0]) && ready(m->src[1]) && (!m->src[2] || ready(m->src[2]))) {
+                    add_rope_job(B, members, j);
+                    continue;
+                }
+                if (m->op == GGML_OP_CPY && m->src[0]->type == GGML_TYPE_F32 &&
+                    (m->type == GGML_TYPE_F16 || m->type == GGML_TYPE_F32) && ready(m->src[0])) {
+                    B.job[B.n_jobs++] = rope_job{ tv(m->src[0]), tv(m), nullptr, nullptr, rope_params{}, ggml_nelements(m->src[0]) };
+                    members.push_back(j);
+                    wrote_.push_back(m);
+                    continue;
+                }
+                break;
+            }
+        }
+        {
+            prof_scope ps(this, "rope", 0);
+            launch_rope_batch(B, st_);
+        }
+        for (int j : members) done_[j] = true;
     }
 
     // rms_norm, fused with a following weight multiply (and activation quantization) when possible

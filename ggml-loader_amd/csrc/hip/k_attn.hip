@@ -222,14 +222,10 @@ __global__ void attn_combine_kernel(const attn_launch A, int n_splits) {
 template <int HD, int G>
 static void launch_attn_t(const attn_launch & A, hipStream_t st) {
     const int splits = (A.n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
-    hipLaunchKernelGGL((attn_scores_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
-    HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(attn_softmax_kernel, dim3(A.n_head, A.n_q), dim3(ATT_THREADS), 0, st, A);
-    HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL((attn_pv_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
-    HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(HD), 0, st, A, splits);
-    HIP_CHECK(hipGetLastError());
+    launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
+    launch(attn_softmax_kernel, dim3(A.n_head, A.n_q), dim3(ATT_THREADS), 0, st, A);
+    launch((attn_pv_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
+    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(HD), 0, st, A, splits);
 }
 
 template <int HD>

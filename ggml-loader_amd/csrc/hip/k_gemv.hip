@@ -53,8 +53,7 @@ void launch_repack_q(int type, const uint8_t * raw, uint8_t * qs_plane, __half *
     qs_geometry(type, qsb, bb);
     const int threads = 256;
     const int64_t grid = (nblocks + threads - 1) / threads;
-    hipLaunchKernelGGL(repack_q_kernel, dim3((unsigned) grid), dim3(threads), 0, st, qsb, bb, raw, qs_plane, d_plane, nblocks, first_block);
-    HIP_CHECK(hipGetLastError());
+    launch(repack_q_kernel, dim3((unsigned) grid), dim3(threads), 0, st, qsb, bb, raw, qs_plane, d_plane, nblocks, first_block);
 }
 
 void launch_unpack_q(int type, uint8_t * raw, const uint8_t * qs_plane, const __half * d_plane,
@@ -64,8 +63,7 @@ void launch_unpack_q(int type, uint8_t * raw, const uint8_t * qs_plane, const __
     qs_geometry(type, qsb, bb);
     const int threads = 256;
     const int64_t grid = (nblocks + threads - 1) / threads;
-    hipLaunchKernelGGL(unpack_q_kernel, dim3((unsigned) grid), dim3(threads), 0, st, qsb, bb, raw, qs_plane, d_plane, nblocks, first_block);
-    HIP_CHECK(hipGetLastError());
+    launch(unpack_q_kernel, dim3((unsigned) grid), dim3(threads), 0, st, qsb, bb, raw, qs_plane, d_plane, nblocks, first_block);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -98,8 +96,7 @@ __global__ void quantize_q8_kernel(const float * __restrict__ x, int64_t x_col_s
 void launch_quantize_q8(const float * x, int64_t x_col_stride, int64_t K, int64_t ncols, q8_act out, hipStream_t st) {
     const int64_t nblk = K / 32;
     dim3 grid((unsigned) ((nblk + 7) / 8), (unsigned) ncols);
-    hipLaunchKernelGGL(quantize_q8_kernel, grid, dim3(256), 0, st, x, x_col_stride, K, out.qs, out.d, out.s);
-    HIP_CHECK(hipGetLastError());
+    launch(quantize_q8_kernel, grid, dim3(256), 0, st, x, x_col_stride, K, out.qs, out.d, out.s);
 }
 
 // Q8_K (ggml quantize_row_q8_K_ref): max = the value of largest magnitude (first one on ties),
@@ -155,8 +152,7 @@ __global__ void quantize_q8k_kernel(const float * __restrict__ x, int64_t x_col_
 
 void launch_quantize_q8k(const float * x, int64_t x_col_stride, int64_t K, int64_t ncols, q8k_act out, hipStream_t st) {
     dim3 grid((unsigned) (K / 256), (unsigned) ncols);
-    hipLaunchKernelGGL(quantize_q8k_kernel, grid, dim3(256), 0, st, x, x_col_stride, K, out.qs, out.d, out.bsums);
-    HIP_CHECK(hipGetLastError());
+    launch(quantize_q8k_kernel, grid, dim3(256), 0, st, x, x_col_stride, K, out.qs, out.d, out.bsums);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -631,8 +627,7 @@ static void launch_gemv_its(gemv_kargs & ka, int waves, hipStream_t st) {
     const int grid_x = (ka.total_rows + ka.rows_per_block - 1) / ka.rows_per_block;
     const size_t lds = gemv_lds_bytes<TYPE>(ka.L.K, ka.rows_per_block, SWIGLU ? 2 : 1);
     if (lds > 160 * 1024) HIP_ABORT("gemv: K=%d needs %zu bytes of LDS", ka.L.K, lds);
-    hipLaunchKernelGGL((gemv_kernel<TYPE, LPR, SWIGLU, ITS>), dim3(grid_x, ka.L.ncols), dim3(waves * WAVE), lds, st, ka);
-    HIP_CHECK(hipGetLastError());
+    launch((gemv_kernel<TYPE, LPR, SWIGLU, ITS>), dim3(grid_x, ka.L.ncols), dim3(waves * WAVE), lds, st, ka);
 }
 
 // ITS = weight blocks per lane for Q4_0/Q8_0, held in registers from the up-front loads. The ladder

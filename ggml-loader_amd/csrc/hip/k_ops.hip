@@ -23,9 +23,9 @@ __device__ __forceinline__ float ld(const char * p, int type) {
 __device__ __forceinline__ void st(char * p, int type, float v) {
     switch (type) {
         case GGML_TYPE_F32: *(float *) p = v; break;
-        case GGML_TYPE_F16: *(__half *) p = __float2half_rn(v); break;
+        case GGML_TYPE_F16: *(__half *) p = __float2half_rn(as_f32(v)); break;
         case GGML_TYPE_BF16: {
-            uint32_t u = __float_as_uint(v);
+            uint32_t u = __float_as_uint(as_f32(v));
             if ((u & 0x7fffffffu) > 0x7f800000u) u = (u >> 16) | 64u;
             else u = (u + (0x7fffu + ((u >> 16) & 1u))) >> 16;
             *(uint16_t *) p = (uint16_t) u;
@@ -153,14 +153,13 @@ static void launch_rms_norm_q(const float * x, int64_t x_stride, const float * w
                               int64_t n, int64_t ncols, float eps, q8_act a, q8k_act b, hipStream_t st) {
     const int64_t ept = (n + 255) / 256;
     dim3 grid((unsigned) ncols), blk(256);
-    if (ept <= 1) hipLaunchKernelGGL((rms_norm_kernel<QUANT, 1>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
-    else if (ept <= 2) hipLaunchKernelGGL((rms_norm_kernel<QUANT, 2>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
-    else if (ept <= 4) hipLaunchKernelGGL((rms_norm_kernel<QUANT, 4>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
-    else if (ept <= 8) hipLaunchKernelGGL((rms_norm_kernel<QUANT, 8>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
-    else if (ept <= 16) hipLaunchKernelGGL((rms_norm_kernel<QUANT, 16>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
-    else if (ept <= 32) hipLaunchKernelGGL((rms_norm_kernel<QUANT, 32>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    if (ept <= 1) launch((rms_norm_kernel<QUANT, 1>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    else if (ept <= 2) launch((rms_norm_kernel<QUANT, 2>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    else if (ept <= 4) launch((rms_norm_kernel<QUANT, 4>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    else if (ept <= 8) launch((rms_norm_kernel<QUANT, 8>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    else if (ept <= 16) launch((rms_norm_kernel<QUANT, 16>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
+    else if (ept <= 32) launch((rms_norm_kernel<QUANT, 32>), grid, blk, 0, st, x, x_stride, w, y, y_stride, n, eps, a, b);
     else HIP_ABORT("rms_norm: rows of %lld elements are not supported", (long long) n);
-    HIP_CHECK(hipGetLastError());
 }
 
 void launch_rms_norm(const float * x, int64_t x_stride, const float * w, float * y, int64_t y_stride,
@@ -202,8 +201,7 @@ __global__ __launch_bounds__(256) void rms_norm_strided_kernel(tview x, tview y,
 
 void launch_rms_norm_strided(const tview & x, const tview & y, float eps, hipStream_t st) {
     const int64_t rows = x.ne[1] * x.ne[2] * x.ne[3];
-    hipLaunchKernelGGL(rms_norm_strided_kernel, dim3((unsigned) rows), dim3(256), 0, st, x, y, eps);
-    HIP_CHECK(hipGetLastError());
+    launch(rms_norm_strided_kernel, dim3((unsigned) rows), dim3(256), 0, st, x, y, eps);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -221,8 +219,7 @@ __global__ void binary_kernel(int op, tview a, tview b, tview d, int64_t n) {
 void launch_binary(int op, const tview & a, const tview & b, const tview & dst, hipStream_t st) {
     const int64_t n = nelem(dst);
     if (n == 0) return;
-    hipLaunchKernelGGL(binary_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, op, a, b, dst, n);
-    HIP_CHECK(hipGetLastError());
+    launch(binary_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, op, a, b, dst, n);
 }
 
 __global__ void unary_kernel(int op, float s, tview a, tview d, int64_t n) {
@@ -244,8 +241,7 @@ __global__ void unary_kernel(int op, float s, tview a, tview d, int64_t n) {
 void launch_unary(int op, float s, const tview & a, const tview & dst, hipStream_t st) {
     const int64_t n = nelem(dst);
     if (n == 0) return;
-    hipLaunchKernelGGL(unary_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, op, s, a, dst, n);
-    HIP_CHECK(hipGetLastError());
+    launch(unary_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, op, s, a, dst, n);
 }
 
 // element i (row-major over the src shape) -> element i (row-major over the dst shape)
@@ -267,8 +263,7 @@ __global__ void cpy_kernel(tview s, tview d, int64_t n) {
 void launch_cpy(const tview & src, const tview & dst, hipStream_t st) {
     const int64_t n = nelem(src);
     if (n == 0) return;
-    hipLaunchKernelGGL(cpy_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, src, dst, n);
-    HIP_CHECK(hipGetLastError());
+    launch(cpy_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, src, dst, n);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -325,8 +320,7 @@ void launch_get_rows(const tview & a, const tview & ids, const tview & dst, cons
                      const __half * d_plane, int64_t first_block, hipStream_t st) {
     const int64_t rows = ids.ne[0] * ids.ne[1] * ids.ne[2];
     if (rows == 0) return;
-    hipLaunchKernelGGL(get_rows_kernel, dim3((unsigned) rows), dim3(256), 0, st, a, ids, dst, qs_plane, d_plane, first_block);
-    HIP_CHECK(hipGetLastError());
+    launch(get_rows_kernel, dim3((unsigned) rows), dim3(256), 0, st, a, ids, dst, qs_plane, d_plane, first_block);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -347,41 +341,73 @@ __device__ __forceinline__ void rope_cs(float theta_extrap, const rope_params & 
     s = sin_cr(theta) * mscale;
 }
 
-__global__ void rope_kernel(tview x, const int32_t * __restrict__ pos, const float * __restrict__ ff, tview d, rope_params p, int64_t n) {
-    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
+// pair li of a RoPE job (row-major over pairs of the src rows); the result is stored in dst's type
+__device__ __forceinline__ void rope_pair(const rope_job & J, int64_t li) {
+    const tview & x = J.src;
+    const tview & d = J.dst;
+    const rope_params & p = J.p;
     const int64_t half = x.ne[0] / 2;
-    const int64_t ip = i % half;
-    int64_t r = i / half;
+    const int64_t ip = li % half;
+    int64_t r = li / half;
     const int64_t i1 = r % x.ne[1]; r /= x.ne[1];
     const int64_t i2 = r % x.ne[2]; r /= x.ne[2];
     const int64_t i3 = r;
     const int i0 = (int) (2 * ip);
     if (i0 >= p.n_dims) {
-        for (int k = 0; k < 2; k++) *(float *) at(d, i0 + k, i1, i2, i3) = *(const float *) at(x, i0 + k, i1, i2, i3);
+        for (int k = 0; k < 2; k++) st(at(d, i0 + k, i1, i2, i3), d.type, *(const float *) at(x, i0 + k, i1, i2, i3));
         return;
     }
     // theta after i0/2 multiplications by theta_scale, in float, as the CPU cache builds it
-    float theta = (float) pos[i2];
+    float theta = (float) J.pos[i2];
     for (int k = 0; k < i0 / 2; k++) theta *= p.theta_scale;
-    const float f = ff ? ff[i0 / 2] : 1.0f;
-    float c, s;
-    rope_cs(theta / f, p, i0, c, s);
+    const float f = J.ff ? J.ff[i0 / 2] : 1.0f;
+    float c, sn;
+    rope_cs(theta / f, p, i0, c, sn);
     int64_t a0, a1;
     if (p.mode & GGML_ROPE_TYPE_NEOX) { a0 = i0 / 2; a1 = i0 / 2 + p.n_dims / 2; }
     else { a0 = i0; a1 = i0 + 1; }
     const float x0 = *(const float *) at(x, a0, i1, i2, i3);
     const float x1 = *(const float *) at(x, a1, i1, i2, i3);
-    *(float *) at(d, a0, i1, i2, i3) = x0 * c - x1 * s;
-    *(float *) at(d, a1, i1, i2, i3) = x0 * s + x1 * c;
+    st(at(d, a0, i1, i2, i3), d.type, x0 * c - x1 * sn);
+    st(at(d, a1, i1, i2, i3), d.type, x0 * sn + x1 * c);
+}
+
+// element li of a copy job (row-major over src, written row-major over dst, converted to dst's type)
+__device__ __forceinline__ void copy_elem(const rope_job & J, int64_t li) {
+    const idx4 a = unflatten(li, J.src.ne);
+    const idx4 b = unflatten(li, J.dst.ne);
+    st(at(J.dst, b.i0, b.i1, b.i2, b.i3), J.dst.type, ld(at(J.src, a.i0, a.i1, a.i2, a.i3), J.src.type));
+}
+
+// Independent RoPE and copy jobs of one decode step in one launch (Q rotation; K rotation stored
+// straight into the F16 KV cache; V appended to it). Each job owns a whole number of workgroups.
+__global__ __launch_bounds__(256) void rope_batch_kernel(const rope_batch B) {
+    int j = 0;
+#pragma unroll
+    for (int k = 1; k < ROPE_MAX_JOBS; k++) if (k < B.n_jobs && (int64_t) blockIdx.x >= B.first_block[k]) j = k;
+    const rope_job & J = B.job[j];
+    const int64_t li = ((int64_t) blockIdx.x - B.first_block[j]) * blockDim.x + threadIdx.x;
+    if (li >= J.n) return;
+    if (J.pos) rope_pair(J, li);
+    else copy_elem(J, li);
+}
+
+void launch_rope_batch(rope_batch & B, hipStream_t st) {
+    int64_t blocks = 0;
+    for (int k = 0; k < B.n_jobs; k++) {
+        B.first_block[k] = blocks;
+        blocks += grid1(B.job[k].n, 256);
+    }
+    if (blocks == 0) return;
+    launch(rope_batch_kernel, dim3((unsigned) blocks), dim3(256), 0, st, B);
 }
 
 void launch_rope(const tview & src, const int32_t * pos, const float * freq_factors, const tview & dst,
                  const rope_params & p, hipStream_t st) {
-    const int64_t n = nelem(src) / 2;
-    if (n == 0) return;
-    hipLaunchKernelGGL(rope_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, src, pos, freq_factors, dst, p, n);
-    HIP_CHECK(hipGetLastError());
+    rope_batch B{};
+    B.n_jobs = 1;
+    B.job[0] = rope_job{ src, dst, pos, freq_factors, p, nelem(src) / 2 };
+    launch_rope_batch(B, st);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -434,8 +460,7 @@ void launch_soft_max(const tview & a, const tview * mask, const tview & dst, flo
     const float m1 = powf(2.0f, -(max_bias / 2.0f) / n_head_log2);
     tview m{};
     if (mask) m = *mask;
-    hipLaunchKernelGGL(soft_max_kernel, dim3((unsigned) rows), dim3(256), 0, st, a, m, mask ? 1 : 0, dst, scale, m0, m1, n_head_log2, max_bias);
-    HIP_CHECK(hipGetLastError());
+    launch(soft_max_kernel, dim3((unsigned) rows), dim3(256), 0, st, a, m, mask ? 1 : 0, dst, scale, m0, m1, n_head_log2, max_bias);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -468,8 +493,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(tview a, int32_t * out) {
 }
 
 void launch_argmax(const tview & a, int32_t * out, hipStream_t st) {
-    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned) a.ne[1]), dim3(256), 0, st, a, out);
-    HIP_CHECK(hipGetLastError());
+    launch(argmax_kernel, dim3((unsigned) a.ne[1]), dim3(256), 0, st, a, out);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -504,6 +528,5 @@ __global__ __launch_bounds__(256) void mul_mat_generic_kernel(tview s0, tview s1
 void launch_mul_mat_generic(const tview & src0, const tview & src1, const tview & dst, hipStream_t st) {
     const int64_t n = nelem(dst);
     if (n == 0) return;
-    hipLaunchKernelGGL(mul_mat_generic_kernel, dim3(grid1(n, 4)), dim3(256), 0, st, src0, src1, dst, n);
-    HIP_CHECK(hipGetLastError());
+    launch(mul_mat_generic_kernel, dim3(grid1(n, 4)), dim3(256), 0, st, src0, src1, dst, n);
 }

@@ -5,6 +5,31 @@
 
 #include "hip_common.h"
 
+#include <hip/hip_ext.h>
+
+// Timing of one executor op. While stop is set, the op's kernels are launched through
+// hipExtLaunchKernel, which stamps start (first launch) and stop (each launch; the last one wins)
+// from the kernel dispatches themselves, so timing puts no event markers between kernels.
+struct launch_timing {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+    int launches = 0;
+};
+extern thread_local launch_timing g_launch_timing;
+
+template <typename... KArgs, typename... Args>
+inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem, hipStream_t st, Args... args) {
+    launch_timing & t = g_launch_timing;
+    if (t.stop) {
+        hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t) shmem, st, t.launches == 0 ? t.start : nullptr, t.stop, 0,
+                              args...);
+        t.launches++;
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, shmem, st, args...);
+    }
+    HIP_CHECK(hipGetLastError());
+}
+
 // A strided view of a tensor (ggml ne/nb convention, nb in bytes).
 struct tview {
     char *  data;
@@ -115,6 +140,23 @@ struct rope_params {
 };
 void launch_rope(const tview & src, const int32_t * pos, const float * freq_factors, const tview & dst,
                  const rope_params & p, hipStream_t st);
+
+// Up to ROPE_MAX_JOBS independent jobs in one launch: RoPE of src into dst (pos set; dst F32, or
+// F16 when the rotation is stored straight into the KV cache) or a converting copy (pos null).
+constexpr int ROPE_MAX_JOBS = 4;
+struct rope_job {
+    tview src, dst;
+    const int32_t * pos;
+    const float * ff;          // optional frequency factors
+    rope_params p;
+    int64_t n;                 // work items: rotation pairs, or elements for a copy
+};
+struct rope_batch {
+    rope_job job[ROPE_MAX_JOBS];
+    int64_t first_block[ROPE_MAX_JOBS];
+    int n_jobs;
+};
+void launch_rope_batch(rope_batch & B, hipStream_t st);
 
 void launch_soft_max(const tview & a, const tview * mask, const tview & dst, float scale, float max_bias, hipStream_t st);
 void launch_argmax(const tview & a, int32_t * out, hipStream_t st);

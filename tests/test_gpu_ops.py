@@ -211,6 +211,47 @@ def test_rope(hip, cpu, mode, hd, n_head, theta):
     assert np.array_equal(a, b), rel_err(a, b)
 
 
+@pytest.mark.parametrize("mode,hd,n_new", [(gl.ROPE_NORMAL, 128, 1), (gl.ROPE_NEOX, 128, 3), (gl.ROPE_NEOX, 96, 1)])
+def test_rope_and_kv_append_batched(hip, cpu, mode, hd, n_new):
+    """The decode step's RoPE(Q), RoPE(K) -> F16 cache and V -> F16 cache (reference
+    model.cpp:1389-1414): one launch on the fused path, the K rotation stored straight into the cache."""
+    n_head, n_head_kv, n_ctx, n_past = 24, 8, 40, 17
+    r = rng(40 + hd)
+    q = r.standard_normal((n_new, n_head, hd)).astype(np.float32)
+    k = r.standard_normal((n_new, n_head_kv, hd)).astype(np.float32) * 3
+    v = r.standard_normal((n_new, n_head_kv, hd)).astype(np.float32) * 3
+    pos = np.arange(n_past, n_past + n_new, dtype=np.int32) + 2000
+    cache0 = r.standard_normal((2, n_ctx, n_head_kv, hd)).astype(np.float16)
+
+    def run(backend, fusion):
+        with Graph() as g:
+            kc = g.tensor(gl.F16, hd, n_head_kv, n_ctx, data=cache0[0])
+            vc = g.tensor(gl.F16, hd, n_head_kv, n_ctx, data=cache0[1])
+            pt = g.tensor(gl.I32, n_new, data=pos)
+            qr = g.rope_ext(g.tensor(gl.F32, hd, n_head, n_new, data=q), pt, None, hd, mode, 4096, 500000.0, 1.0, 0.0, 1.0, 0.0, 0.0)
+            kr = g.rope_ext(g.tensor(gl.F32, hd, n_head_kv, n_new, data=k), pt, None, hd, mode, 4096, 500000.0, 1.0, 0.0, 1.0, 0.0, 0.0)
+            nb1, nb2 = hd * 2, hd * n_head_kv * 2
+            ck = g.cpy(kr, g.view_3d(kc, hd, n_head_kv, n_new, nb1, nb2, n_past * nb2))
+            cv = g.cpy(g.tensor(gl.F32, hd, n_head_kv, n_new, data=v), g.view_3d(vc, hd, n_head_kv, n_new, nb1, nb2, n_past * nb2))
+            gl.libs()["hip"].ggml_backend_hip_set_fusion(hip, fusion)
+            try:
+                qo = g.compute(backend, [qr, ck, cv])[0]
+            finally:
+                gl.libs()["hip"].ggml_backend_hip_set_fusion(hip, True)
+            return qo, g.read(kc, np.float16), g.read(vc, np.float16)
+
+    ref = run(cpu, True)
+    for fusion in (True, False):
+        got = run(hip, fusion)
+        assert np.array_equal(got[0], ref[0]), fusion
+        assert np.array_equal(got[1].view(np.uint16), ref[1].view(np.uint16)), fusion
+        assert np.array_equal(got[2].view(np.uint16), ref[2].view(np.uint16)), fusion
+    # untouched cache rows keep their contents; the new V rows are the f16 rounding of v
+    kcache = ref[1].reshape(n_ctx, n_head_kv, hd)
+    assert np.array_equal(kcache[:n_past].view(np.uint16), cache0[0][:n_past].view(np.uint16))
+    assert np.array_equal(ref[2].reshape(n_ctx, n_head_kv, hd)[n_past:n_past + n_new], v.astype(np.float16))
+
+
 def test_soft_max_masked(hip, cpu):
     n_kv, n_q, n_head = 300, 3, 5
     x = rng(12).standard_normal((n_head, n_q, n_kv)).astype(np.float32) * 4
