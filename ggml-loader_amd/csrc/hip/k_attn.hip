@@ -13,16 +13,21 @@
 // projection, and any drift shifts values across int8 rounding boundaries, which the following
 // layers amplify.
 //
-// Four launches:
-//   scores   (64-position chunk, KV head) blocks: the chunk's K rows staged through LDS with
+// Four launches, each issuing its memory reads in independent batches (a dependent load per loop
+// iteration would put one L2/HBM round trip per iteration on the critical path):
+//   scores   (64-position chunk, KV head) workgroups: the chunk's K rows staged through LDS with
 //            coalesced 16-byte loads (rows padded by one dword so lane t reading row t is
 //            conflict-free); one wave per (query, head of the GQA group), lane = position.
-//   softmax  one block per (query, head) row: max, exp, double sum, F16 probabilities.
-//   pv       (chunk, KV head) blocks: V rows staged through LDS; one wave per (query, head),
-//            two dims per lane, double accumulation; partials per chunk.
-//   combine  per (head, query): sum of the chunk partials, output (+ optional Q8_0 blocks).
-// Scratch: scores f32 [n_q][n_head][n_kv], probabilities f32 [n_q][n_head][n_kv],
-// partials f64 [chunks][n_q][n_head][hd].
+//   stats    one workgroup per (query, head) row: M = max, 1/S = 1/sum exp(s - M) in double.
+//   pv       (128-position chunk, KV head) workgroups: p = F16(exp(s - M) * (1/S)) for the chunk,
+//            the chunk's V rows staged in LDS (every load issued up front), one partial per
+//            (chunk, query, head) accumulated in double; one wave per (query, head), two dims per
+//            lane.
+//   combine  one thread per output element: the partials added in chunk order (+ Q8_0 blocks).
+// Workgroups exchange results only across launch boundaries: a flag-and-fence hand-off inside a
+// launch costs a write-back and invalidation of the L2 of every XCD that takes part.
+// Scratch: scores f32 [n_q][n_head][n_kv], row statistics f32 [n_q][n_head][2] (M, 1/S),
+// partials f64 [pv chunks][n_q][n_head][hd].
 #include "kernels.h"
 
 #include "ggml.h"
@@ -30,26 +35,32 @@
 constexpr int ATT_CHUNK = 64;
 constexpr int ATT_MAX_Q = 4;
 constexpr int ATT_THREADS = 256;
+constexpr int ATT_WAVES = ATT_THREADS / WAVE;
+
+constexpr int PV_CHUNK = 128;
+constexpr int STATS_BATCH = 16;      // score loads per thread in flight in the statistics kernel
 
 struct attn_scratch {
     float * scores;
-    float * probs;
+    float * stats;
     double * parts;
 };
 
 __host__ __device__ inline attn_scratch scratch_of(const attn_launch & A) {
     const int64_t rows = (int64_t) A.n_q * A.n_head * A.n_kv;
+    const int64_t nst = (int64_t) A.n_q * A.n_head * 2;
     attn_scratch s;
     s.scores = A.scratch;
-    s.probs = s.scores + rows;
-    s.parts = (double *) (s.probs + rows + (rows & 1));
+    s.stats = s.scores + rows;
+    s.parts = (double *) (s.stats + nst + ((rows + nst) & 1));
     return s;
 }
 
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd) {
-    const int64_t splits = (n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
+    const int64_t splits = (n_kv + PV_CHUNK - 1) / PV_CHUNK;
     const int64_t rows = (int64_t) n_q * n_head * n_kv;
-    return (2 * rows + 1) * (int64_t) sizeof(float) + splits * n_q * n_head * hd * (int64_t) sizeof(double);
+    const int64_t nst = (int64_t) n_q * n_head * 2;
+    return (rows + nst + 1) * (int64_t) sizeof(float) + splits * n_q * n_head * hd * (int64_t) sizeof(double);
 }
 
 __device__ __forceinline__ float mask_at(const attn_launch & A, int q, int t) {
@@ -59,11 +70,11 @@ __device__ __forceinline__ float mask_at(const attn_launch & A, int q, int t) {
 }
 
 // stage rows [t0, t0+nt) of a [pos][hd] F16 cache view (row stride nb_pos halves) into LDS rows of
-// STRIDE dwords; rows >= nt are zero
-template <int HD, int STRIDE>
+// STRIDE dwords; rows nt..ROWS-1 are zero. Every load is issued before the first LDS store.
+template <int HD, int STRIDE, int ROWS>
 __device__ __forceinline__ void stage_rows(uint32_t * dst, const __half * base, int64_t nb_pos, int t0, int nt) {
     constexpr int PIECES = HD / 8;                                   // 16-byte pieces per row
-    constexpr int ITER = ATT_CHUNK * PIECES / ATT_THREADS;
+    constexpr int ITER = ROWS * PIECES / ATT_THREADS;
     uint4 v[ITER];
 #pragma unroll
     for (int it = 0; it < ITER; it++) {
@@ -94,7 +105,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
     const int n_q = A.n_q;
     const attn_scratch S = scratch_of(A);
 
-    stage_rows<HD, STRIDE>(s_k, A.k + (int64_t) kvh * A.k_nb1, A.k_nb2, t0, nt);
+    stage_rows<HD, STRIDE, ATT_CHUNK>(s_k, A.k + (int64_t) kvh * A.k_nb1, A.k_nb2, t0, nt);
     for (int i = threadIdx.x; i < n_q * G * HD; i += ATT_THREADS) {
         const int pr = i / HD, d = i % HD;
         const int q = pr / G, g = pr % G;
@@ -103,7 +114,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
     }
     __syncthreads();
 
-    for (int pr = wave; pr < n_q * G; pr += ATT_THREADS / WAVE) {
+    for (int pr = wave; pr < n_q * G; pr += ATT_WAVES) {
         const int q = pr / G, g = pr % G, h = kvh * G + g;
         if (lane < nt) {
             const uint32_t * kr = s_k + lane * STRIDE;
@@ -123,60 +134,108 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
     }
 }
 
-// one block per (head, query) row
-__global__ __launch_bounds__(ATT_THREADS) void attn_softmax_kernel(const attn_launch A) {
-    __shared__ float s_m[ATT_THREADS / WAVE];
-    __shared__ double s_s[ATT_THREADS / WAVE];
+// one workgroup per (head, query) row
+__global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_launch A) {
+    __shared__ float s_m[ATT_WAVES];
+    __shared__ double s_s[ATT_WAVES];
     const int h = blockIdx.x, q = blockIdx.y;
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
     const attn_scratch S = scratch_of(A);
     const float * sc = S.scores + ((int64_t) q * A.n_head + h) * A.n_kv;
-    float * pr = S.probs + ((int64_t) q * A.n_head + h) * A.n_kv;
+    constexpr int SPAN = ATT_THREADS * STATS_BATCH;
+    const bool one_batch = A.n_kv <= SPAN;          // values stay in registers for the exp pass
+    float v[STATS_BATCH];
     float m = -INFINITY;
-    for (int t = threadIdx.x; t < A.n_kv; t += ATT_THREADS) m = fmaxf(m, sc[t]);
+    for (int base = 0; base < A.n_kv; base += SPAN) {
+#pragma unroll
+        for (int k = 0; k < STATS_BATCH; k++) {
+            const int t = base + k * ATT_THREADS + threadIdx.x;
+            v[k] = t < A.n_kv ? sc[t] : -INFINITY;
+        }
+#pragma unroll
+        for (int k = 0; k < STATS_BATCH; k++) m = fmaxf(m, v[k]);
+    }
     m = wave_max(m);
     if (lane == 0) s_m[wave] = m;
     __syncthreads();
     float M = s_m[0];
-    for (int w = 1; w < ATT_THREADS / WAVE; w++) M = fmaxf(M, s_m[w]);
+    for (int w = 1; w < ATT_WAVES; w++) M = fmaxf(M, s_m[w]);
     double sum = 0.0;
-    for (int t = threadIdx.x; t < A.n_kv; t += ATT_THREADS) {
-        const float e = M == -INFINITY ? 0.0f : exp_cr(sc[t] - M);
-        pr[t] = e;
-        sum += (double) e;
+    if (M != -INFINITY) {
+        for (int base = 0; base < A.n_kv; base += SPAN) {
+            if (!one_batch) {
+#pragma unroll
+                for (int k = 0; k < STATS_BATCH; k++) {
+                    const int t = base + k * ATT_THREADS + threadIdx.x;
+                    v[k] = t < A.n_kv ? sc[t] : -INFINITY;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < STATS_BATCH; k++) {
+                if (base + k * ATT_THREADS + (int) threadIdx.x < A.n_kv) sum += (double) exp_cr(v[k] - M);
+            }
+        }
     }
     sum = wave_sum_d(sum);
     if (lane == 0) s_s[wave] = sum;
     __syncthreads();
-    double tot = 0.0;
-    for (int w = 0; w < ATT_THREADS / WAVE; w++) tot += s_s[w];
-    const float inv = tot > 0.0 ? (float) (1.0 / tot) : 0.0f;
-    for (int t = threadIdx.x; t < A.n_kv; t += ATT_THREADS) pr[t] = __half2float(__float2half_rn(as_f32(pr[t] * inv)));
+    if (threadIdx.x == 0) {
+        double tot = 0.0;
+        for (int w = 0; w < ATT_WAVES; w++) tot += s_s[w];
+        float * st = S.stats + ((int64_t) q * A.n_head + h) * 2;
+        st[0] = M;
+        st[1] = tot > 0.0 ? (float) (1.0 / tot) : 0.0f;
+    }
 }
 
 template <int HD, int G>
 __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch A) {
     constexpr int HD2 = HD / 2;
     constexpr int STRIDE = HD2;   // rows read along dims: consecutive lanes, consecutive dwords
-    __shared__ uint32_t s_v[ATT_CHUNK * STRIDE];
-    __shared__ float s_p[ATT_MAX_Q * G][ATT_CHUNK];
+    constexpr int R = ATT_MAX_Q * G;
+    __shared__ uint32_t s_v[PV_CHUNK * STRIDE];
+    __shared__ float s_p[R][PV_CHUNK];
     const int split = blockIdx.x, kvh = blockIdx.y;
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-    const int t0 = split * ATT_CHUNK;
-    const int nt = min(ATT_CHUNK, A.n_kv - t0);
-    const int n_q = A.n_q;
+    const int t0 = split * PV_CHUNK;
+    const int nt = min(PV_CHUNK, A.n_kv - t0);
+    const int n_rows = A.n_q * G;
     const attn_scratch S = scratch_of(A);
 
-    stage_rows<HD, STRIDE>(s_v, A.v + (int64_t) kvh * A.v_nb1, A.v_nb2, t0, nt);
-    for (int i = threadIdx.x; i < n_q * G * ATT_CHUNK; i += ATT_THREADS) {
-        const int pr = i / ATT_CHUNK, t = i % ATT_CHUNK;
-        const int q = pr / G, g = pr % G;
-        s_p[pr][t] = t < nt ? S.probs[((int64_t) q * A.n_head + kvh * G + g) * A.n_kv + t0 + t] : 0.0f;
+    // the V chunk's loads go out first; p is formed while they are in flight
+    constexpr int PIECES = HD / 8;
+    constexpr int ITER = PV_CHUNK * PIECES / ATT_THREADS;
+    uint4 vv[ITER];
+    const __half * vbase = A.v + (int64_t) kvh * A.v_nb1;
+#pragma unroll
+    for (int it = 0; it < ITER; it++) {
+        const int pc = threadIdx.x + it * ATT_THREADS;
+        const int r = pc / PIECES, c = pc % PIECES;
+        vv[it] = make_uint4(0, 0, 0, 0);
+        if (r < nt) vv[it] = *(const uint4 *) (vbase + (int64_t) (t0 + r) * A.v_nb2 + c * 8);
+    }
+    for (int i = threadIdx.x; i < n_rows * PV_CHUNK; i += ATT_THREADS) {
+        const int pr = i / PV_CHUNK, t = i % PV_CHUNK;
+        const int64_t row = (int64_t) (pr / G) * A.n_head + kvh * G + pr % G;
+        float p = 0.0f;
+        if (t < nt) {
+            const float M = S.stats[row * 2], inv = S.stats[row * 2 + 1];
+            const float e = M == -INFINITY ? 0.0f : exp_cr(S.scores[row * A.n_kv + t0 + t] - M);
+            p = __half2float(__float2half_rn(as_f32(e * inv)));
+        }
+        s_p[pr][t] = p;
+    }
+#pragma unroll
+    for (int it = 0; it < ITER; it++) {
+        const int pc = threadIdx.x + it * ATT_THREADS;
+        const int r = pc / PIECES, c = pc % PIECES;
+        uint32_t * d = s_v + r * STRIDE + c * 4;
+        d[0] = vv[it].x; d[1] = vv[it].y; d[2] = vv[it].z; d[3] = vv[it].w;
     }
     __syncthreads();
 
-    for (int pr = wave; pr < n_q * G; pr += ATT_THREADS / WAVE) {
-        const int q = pr / G, g = pr % G, h = kvh * G + g;
+    for (int pr = wave; pr < n_rows; pr += ATT_WAVES) {
+        const int q = pr / G, h = kvh * G + pr % G;
         if (lane < HD2) {
             double a0 = 0.0, a1 = 0.0;
 #pragma unroll 8
@@ -186,20 +245,30 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
                 a0 += (double) (p * vf.x);
                 a1 += (double) (p * vf.y);
             }
-            double * part = S.parts + (((int64_t) split * n_q + q) * A.n_head + h) * HD;
+            double * part = S.parts + (((int64_t) split * A.n_q + q) * A.n_head + h) * HD;
             part[2 * lane] = a0;
             part[2 * lane + 1] = a1;
         }
     }
 }
 
-// sum the chunk partials of one (head, query); block = HD threads (one per dim)
+// one thread per output element (head, dim) of one query: the chunk partials added in chunk order
 template <int HD>
-__global__ void attn_combine_kernel(const attn_launch A, int n_splits) {
+__global__ __launch_bounds__(HD) void attn_combine_kernel(const attn_launch A, int n_splits) {
     const int h = blockIdx.x, q = blockIdx.y, d = threadIdx.x;
     const attn_scratch S = scratch_of(A);
+    const double * pp = S.parts + ((int64_t) q * A.n_head + h) * HD + d;
+    const int64_t step = (int64_t) A.n_q * A.n_head * HD;
     double acc = 0.0;
-    for (int s = 0; s < n_splits; s++) acc += S.parts[(((int64_t) s * A.n_q + q) * A.n_head + h) * HD + d];
+    int s = 0;
+    for (; s + 8 <= n_splits; s += 8) {
+        double v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = pp[(s + k) * step];
+#pragma unroll
+        for (int k = 0; k < 8; k++) acc += v[k];
+    }
+    for (; s < n_splits; s++) acc += pp[s * step];
     const float v = (float) acc;
     const int64_t oi = (int64_t) h * HD + d;
     A.out[(int64_t) q * A.out_nb1 + oi] = v;
@@ -222,10 +291,11 @@ __global__ void attn_combine_kernel(const attn_launch A, int n_splits) {
 template <int HD, int G>
 static void launch_attn_t(const attn_launch & A, hipStream_t st) {
     const int splits = (A.n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
+    const int pv_splits = (A.n_kv + PV_CHUNK - 1) / PV_CHUNK;
     launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
-    launch(attn_softmax_kernel, dim3(A.n_head, A.n_q), dim3(ATT_THREADS), 0, st, A);
-    launch((attn_pv_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
-    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(HD), 0, st, A, splits);
+    launch(attn_stats_kernel, dim3(A.n_head, A.n_q), dim3(ATT_THREADS), 0, st, A);
+    launch((attn_pv_kernel<HD, G>), dim3(pv_splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
+    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(HD), 0, st, A, pv_splits);
 }
 
 template <int HD>

@@ -180,7 +180,7 @@ struct attn_launch {
     int64_t        out_nb1;
     int n_kv, n_q, n_head, n_head_kv, hd;
     float scale;
-    // split-KV scratch: partial (max, sum, acc[hd]) per (split, head, q)
+    // split-KV scratch (attn_scratch_bytes): scores, row statistics, per-chunk partials
     float *        scratch;
     int64_t        scratch_bytes;
     // quantized copy of out for the o-projection (Q8_0 semantics), optional
