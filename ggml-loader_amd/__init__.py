@@ -198,6 +198,7 @@ def _declare(core, hip, loader):
     _sig(hip, "ggml_backend_hip_set_graph_replay", None, vp, C.c_bool)
     _sig(hip, "ggml_backend_hip_set_profiling", None, vp, C.c_bool)
     _sig(hip, "ggml_backend_hip_set_profile_filter", None, vp, C.c_char_p)
+    _sig(hip, "ggml_backend_hip_set_profile_sampling", None, vp, i32)
     _sig(hip, "ggml_backend_hip_reset_profile", None, vp)
     _sig(hip, "ggml_backend_hip_profile_count", i32, vp)
     _sig(hip, "ggml_backend_hip_profile_entry", C.c_bool, vp, i32, C.c_char_p, sz, C.POINTER(i64),

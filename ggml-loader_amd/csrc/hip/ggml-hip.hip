@@ -262,6 +262,9 @@ struct hip_backend_ctx {
     int fuse_mask = FUSE_ALL;
     bool graph_replay = true;
     bool profiling = false;
+    int profile_every = 1;           // time one graph compute in every profile_every
+    int64_t computes = 0;
+    bool timing = false;             // this compute is timed
     std::string profile_filter;      // only kernels whose name starts with this get events
     ggml_backend_eval_callback cb = nullptr;
     void * cb_user = nullptr;
@@ -398,7 +401,7 @@ private:
         double bytes;
         bool on = false;
         prof_scope(executor * e, const char * n, double b) : ex(e), name(n), bytes(b) {
-            if (ex->c_.profiling && ex->c_.profile_filter.compare(0, ex->c_.profile_filter.size(), n, 0,
+            if (ex->c_.timing && ex->c_.profile_filter.compare(0, ex->c_.profile_filter.size(), n, 0,
                                                                   ex->c_.profile_filter.size()) == 0) {
                 g_launch_timing = launch_timing{ ex->event(), ex->event(), 0 };
                 on = true;
@@ -459,20 +462,27 @@ private:
         return kind;
     }
 
+    // the weight type of the quantized GEMVs that are node u's only consumers (-1: some consumer is
+    // not such a GEMV, or they mix dot types)
+    int gemv_only_consumers(int u) const {
+        if (users_[u].empty()) return -1;
+        const ggml_tensor * m = g_->nodes[u];
+        int wtype = -1;
+        for (int j : users_[u]) {
+            const ggml_tensor * n = g_->nodes[j];
+            if (n->op != GGML_OP_MUL_MAT || n->src[1] != m || n->src[0] == m || attn_.count(j) || !gemv_capable(n)) return -1;
+            if (wtype >= 0 && dot_kind(n->src[0]->type) != dot_kind(wtype)) return -1;
+            wtype = n->src[0]->type;
+        }
+        return wtype;
+    }
+
     // rms_norm * w (node u, rows of N) whose every consumer is a quantized GEMV that can compute the
     // normalization in its prologue: the normalized activation is then never materialized
     bool norm_deferrable(int u, int64_t N) const {
-        if (!fuse(FUSE_NORMQ) || !fuse(FUSE_ACTQ) || is_output(u) || users_[u].empty()) return false;
-        const ggml_tensor * m = g_->nodes[u];
-        int kind = 0;
-        for (int j : users_[u]) {
-            const ggml_tensor * n = g_->nodes[j];
-            if (n->op != GGML_OP_MUL_MAT || n->src[1] != m || n->src[0] == m || attn_.count(j) || !gemv_capable(n)) return false;
-            const int k = dot_kind(n->src[0]->type);
-            if (kind && k != kind) return false;
-            kind = k;
-        }
-        return N <= (kind == 2 ? GEMV_NORM_MAX_K_Q8K : GEMV_NORM_MAX_K_Q8);
+        if (!fuse(FUSE_NORMQ) || !fuse(FUSE_ACTQ) || is_output(u)) return false;
+        const int wtype = gemv_only_consumers(u);
+        return wtype >= 0 && N <= gemv_prologue_max_k(wtype, true);
     }
 
     // ---- dispatch ----
@@ -639,7 +649,7 @@ private:
                     w->ne[0] == x->ne[0] && ggml_is_contiguous(w) && ggml_is_contiguous(m)) {
                     const int64_t N = x->ne[0], rows = ggml_nrows(x);
                     if (m->ne[1] == rows && norm_deferrable(u, N) && ((uintptr_t) x->data | (uintptr_t) w->data) % 16 == 0) {
-                        norm_[m] = gemv_norm{ (const float *) x->data, N, (const float *) w->data, eps };
+                        norm_[m] = gemv_norm{ (const float *) x->data, N, (const float *) w->data, eps, 1 };
                         done_[u] = true;
                         return;
                     }
@@ -804,11 +814,10 @@ private:
             S.m[0].y_stride = (int64_t) (mn->nb[1] / sizeof(float));
             S.m[0].add = nullptr;
             sb -= (double) (g_->nodes[gate]->ne[0] * ncols * 4); // gate/up outputs are not written, act is
-            const int qk = wanted_act_kind(mulnode);
-            if (qk == 1 && mn->ne[0] % 32 == 0) {
-                act_entry e = alloc_act(1, mn->ne[0], ncols);
-                S.act_q = e.q8;
-                act_[mn] = e;
+            // the GEMVs reading act (the down projection) quantize it in their prologue
+            const int dtype = fuse(FUSE_ACTQ) ? gemv_only_consumers(mulnode) : -1;
+            if (dtype >= 0 && mn->ne[0] <= gemv_prologue_max_k(dtype, false) && ((uintptr_t) mn->data) % 16 == 0) {
+                norm_[mn] = gemv_norm{ (const float *) mn->data, (int64_t) (mn->nb[1] / sizeof(float)), nullptr, 0.0f, 0 };
             }
             {
                 prof_scope ps(this, wtype == GGML_TYPE_Q4_0 ? "gemv_q4_0_swiglu" :
@@ -997,10 +1006,11 @@ void collect_profile(hip_backend_ctx * c) {
 enum ggml_status be_compute(ggml_backend_t b, ggml_cgraph * g) {
     hip_backend_ctx * c = (hip_backend_ctx *) b->context;
     hip_device & d = dev(c->device);
+    c->timing = c->profiling && (c->computes++ % c->profile_every) == 0;
     executor ex(*c, g);
     ex.run();
     HIP_CHECK(hipStreamSynchronize(d.stream));
-    if (c->profiling) collect_profile(c);
+    if (c->timing) collect_profile(c);
     return GGML_STATUS_SUCCESS;
 }
 
@@ -1075,6 +1085,9 @@ void ggml_backend_hip_set_graph_replay(ggml_backend_t backend, bool enable) {
 }
 void ggml_backend_hip_set_profiling(ggml_backend_t backend, bool enable) {
     if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->profiling = enable;
+}
+void ggml_backend_hip_set_profile_sampling(ggml_backend_t backend, int every) {
+    if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->profile_every = every > 1 ? every : 1;
 }
 void ggml_backend_hip_set_profile_filter(ggml_backend_t backend, const char * prefix) {
     if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->profile_filter = prefix ? prefix : "";

@@ -292,35 +292,107 @@ __device__ __forceinline__ int pack4(int a, int b, int c, int d) {
     return (a & 0xff) | ((b & 0xff) << 8) | ((c & 0xff) << 16) | (d << 24);
 }
 
-// rms_norm(x) * w of column col, quantized straight into the LDS staging area with the roundings of
-// ggml's rms_norm -> mul -> quantize_row_q8_0 (Q4_0/Q8_0 weights) or quantize_row_q8_K (Q4_K)
-// chain. Thread t owns one 32-element Q8_0 block (one 16-element group of a Q8_K super-block), so
-// block maxima and sums are thread-local; only the sum of squares is reduced over the workgroup.
+// Quantizes chunk c (C = 32 or 16 values in v, already in their final float form) of the staged
+// column into LDS with ggml's quantize_row_q8_0 (Q4_0/Q8_0 weights) or quantize_row_q8_K (Q4_K)
+// roundings. A Q8_0 block is one thread's chunk; a Q8_K super-block is the chunks of 16
+// consecutive lanes, which must all call this together (has = the chunk exists).
+template <int TYPE, int C>
+__device__ __forceinline__ void quant_chunk(const float (&v)[C], int c, bool has, const gemv_lds & s) {
+    if (TYPE != GGML_TYPE_Q4_K) {
+        if (!has) return;
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < C; e++) amax = fmaxf(amax, fabsf(v[e]));
+        const float dd = amax / 127;
+        const float id = dd ? 1.0f / dd : 0.0f;
+        int q[C];
+        int sum = 0;
+#pragma unroll
+        for (int e = 0; e < C; e++) {
+            q[e] = (int) roundf(v[e] * id);
+            sum += q[e];
+        }
+        int4 * dst = (int4 *) (s.xq + c * C);
+        dst[0] = make_int4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]),
+                           pack4(q[8], q[9], q[10], q[11]), pack4(q[12], q[13], q[14], q[15]));
+        dst[1] = make_int4(pack4(q[16], q[17], q[18], q[19]), pack4(q[20], q[21], q[22], q[23]),
+                           pack4(q[24], q[25], q[26], q[27]), pack4(q[28], q[29], q[30], q[31]));
+        s.xd[c] = __half2float(__float2half_rn(dd));
+        s.xs[c] = sum;
+    } else {
+        // the super-block's value of largest magnitude, the first one on ties
+        float ax = -1.0f, val = 0.0f;
+        int idx = 0;
+        if (has) {
+#pragma unroll
+            for (int e = 0; e < C; e++) {
+                const float a = fabsf(v[e]);
+                if (a > ax) { ax = a; idx = c * C + e; val = v[e]; }
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            const float ax2 = __shfl_xor(ax, o, WAVE);
+            const int idx2 = __shfl_xor(idx, o, WAVE);
+            const float val2 = __shfl_xor(val, o, WAVE);
+            if (ax2 > ax || (ax2 == ax && idx2 < idx)) { ax = ax2; idx = idx2; val = val2; }
+        }
+        if (!has) return;
+        int q[C];
+        int bsum = 0;
+        const float iscale = ax != 0.0f ? -127.f / val : 0.0f;
+#pragma unroll
+        for (int e = 0; e < C; e++) {
+            const int qv = ax != 0.0f ? round_half_even(iscale * v[e]) : 0;
+            q[e] = qv < 127 ? qv : 127;
+            bsum += q[e];
+        }
+        *(int4 *) (s.xq + c * C) = make_int4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]),
+                                             pack4(q[8], q[9], q[10], q[11]), pack4(q[12], q[13], q[14], q[15]));
+        s.xbs[c] = (int16_t) bsum;
+        if ((c % 16) == 0) s.xd[c / 16] = ax != 0.0f ? 1 / iscale : 0.0f;
+    }
+}
+
+template <int C>
+__device__ __forceinline__ void load_chunk(float (&v)[C], const float * p) {
+#pragma unroll
+    for (int k = 0; k < C / 4; k++) {
+        const float4 f = ((const float4 *) p)[k];
+        v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+    }
+}
+
+// The activation prologue: x of column col quantized straight into the LDS staging area, as
+// rms_norm(x) * w (rms set: ggml's rms_norm -> mul -> quantize chain, same roundings; one chunk per
+// thread, so only the sum of squares is reduced over the workgroup) or as x itself (the quantize
+// that ggml-cpu applies to a mul_mat's activation; several chunks per thread).
 template <int TYPE>
 __device__ __forceinline__ void stage_norm(const gemv_launch & L, int col, const gemv_lds & s, double * s_red) {
     constexpr int C = TYPE == GGML_TYPE_Q4_K ? 16 : 32;
     const int K = L.K;
     const int t = threadIdx.x;
+    const float * xcol = L.norm.x + (int64_t) col * L.norm.x_stride;
+    if (!L.norm.rms) {
+        for (int c0 = 0; c0 < K / C; c0 += blockDim.x) {
+            const int c = c0 + t;
+            const bool has = c < K / C;
+            float v[C];
+#pragma unroll
+            for (int e = 0; e < C; e++) v[e] = 0.0f;
+            if (has) load_chunk(v, xcol + (int64_t) c * C);
+            quant_chunk<TYPE, C>(v, c, has, s);
+        }
+        return;
+    }
     const int lane = t % WAVE, wave = t / WAVE;
     const bool has = t < K / C;
     float v[C], wv[C];
 #pragma unroll
     for (int e = 0; e < C; e++) { v[e] = 0.0f; wv[e] = 1.0f; }
     if (has) {
-        const float4 * xr = (const float4 *) (L.norm.x + (int64_t) col * L.norm.x_stride + (int64_t) t * C);
-#pragma unroll
-        for (int k = 0; k < C / 4; k++) {
-            const float4 f = xr[k];
-            v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
-        }
-        if (L.norm.w) {
-            const float4 * wr = (const float4 *) (L.norm.w + (int64_t) t * C);
-#pragma unroll
-            for (int k = 0; k < C / 4; k++) {
-                const float4 f = wr[k];
-                wv[4 * k] = f.x; wv[4 * k + 1] = f.y; wv[4 * k + 2] = f.z; wv[4 * k + 3] = f.w;
-            }
-        }
+        load_chunk(v, xcol + (int64_t) t * C);
+        if (L.norm.w) load_chunk(wv, L.norm.w + (int64_t) t * C);
     }
     double ss = 0.0;
 #pragma unroll
@@ -337,60 +409,7 @@ __device__ __forceinline__ void stage_norm(const gemv_launch & L, int col, const
         v[e] = v[e] * scale;
         if (L.norm.w) v[e] = v[e] * wv[e];
     }
-    if (TYPE != GGML_TYPE_Q4_K) {
-        if (!has) return;
-        float amax = 0.0f;
-#pragma unroll
-        for (int e = 0; e < C; e++) amax = fmaxf(amax, fabsf(v[e]));
-        const float dd = amax / 127;
-        const float id = dd ? 1.0f / dd : 0.0f;
-        int q[C];
-        int sum = 0;
-#pragma unroll
-        for (int e = 0; e < C; e++) {
-            q[e] = (int) roundf(v[e] * id);
-            sum += q[e];
-        }
-        int4 * dst = (int4 *) (s.xq + t * C);
-        dst[0] = make_int4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]),
-                           pack4(q[8], q[9], q[10], q[11]), pack4(q[12], q[13], q[14], q[15]));
-        dst[1] = make_int4(pack4(q[16], q[17], q[18], q[19]), pack4(q[20], q[21], q[22], q[23]),
-                           pack4(q[24], q[25], q[26], q[27]), pack4(q[28], q[29], q[30], q[31]));
-        s.xd[t] = __half2float(__float2half_rn(dd));
-        s.xs[t] = sum;
-    } else {
-        // the super-block's value of largest magnitude, the first one on ties (16 lanes per block)
-        float ax = -1.0f, val = 0.0f;
-        int idx = 0;
-        if (has) {
-#pragma unroll
-            for (int e = 0; e < C; e++) {
-                const float a = fabsf(v[e]);
-                if (a > ax) { ax = a; idx = t * C + e; val = v[e]; }
-            }
-        }
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            const float ax2 = __shfl_xor(ax, o, WAVE);
-            const int idx2 = __shfl_xor(idx, o, WAVE);
-            const float val2 = __shfl_xor(val, o, WAVE);
-            if (ax2 > ax || (ax2 == ax && idx2 < idx)) { ax = ax2; idx = idx2; val = val2; }
-        }
-        if (!has) return;
-        int q[C];
-        int bsum = 0;
-        const float iscale = ax != 0.0f ? -127.f / val : 0.0f;
-#pragma unroll
-        for (int e = 0; e < C; e++) {
-            int qv = ax != 0.0f ? round_half_even(iscale * v[e]) : 0;
-            q[e] = qv < 127 ? qv : 127;
-            bsum += q[e];
-        }
-        *(int4 *) (s.xq + t * C) = make_int4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]),
-                                             pack4(q[8], q[9], q[10], q[11]), pack4(q[12], q[13], q[14], q[15]));
-        s.xbs[t] = (int16_t) bsum;
-        if ((t % 16) == 0) s.xd[t / 16] = ax != 0.0f ? 1 / iscale : 0.0f;
-    }
+    quant_chunk<TYPE, C>(v, t, has, s);
 }
 
 // the quantized activation column in LDS: copied, or computed by the RMSNorm prologue
@@ -545,8 +564,22 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
         if (l < NCH && valid) {
             const float * terms = s.terms + (rib * NCH + l) * nb;
             float acc = 0.0f;
-#pragma unroll 8
-            for (int b = 0; b < nb; b++) acc = acc + terms[b];
+            if ((nb & 3) == 0) {
+                // 16 terms per step: the four 16-byte LDS reads go out together, then the adds
+                const float4 * t4 = (const float4 *) terms;
+                const int n4 = nb / 4;
+                for (int b4 = 0; b4 < n4; b4 += 4) {
+                    float4 v[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) v[k] = b4 + k < n4 ? t4[b4 + k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        if (b4 + k < n4) acc = acc + v[k].x + v[k].y + v[k].z + v[k].w;
+                    }
+                }
+            } else {
+                for (int b = 0; b < nb; b++) acc = acc + terms[b];
+            }
             res[0] = acc;
         }
         // lane 0 holds gate (or the single chain), lane 1 holds up
@@ -586,38 +619,11 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
         return;
     }
 
-    // SwiGLU epilogue: act = silu(gate) * up (two roundings, as the silu and mul ops); optional Q8_0
-    // quantization of 32-row groups (rows per block is a multiple of 32 when act_q is requested)
+    // SwiGLU epilogue: act = silu(gate) * up (two roundings, as the silu and mul ops)
     const float gv = res[0], uv = res[NCH - 1];
     const float sl = gv / (1.0f + exp_cr(-gv));
     const float act = sl * uv;
     if (valid && l == 0) L.m[0].y[(int64_t) col * L.m[0].y_stride + lrow] = act;
-    if (L.act_q.qs == nullptr) return;
-    __syncthreads();
-    float * s_act = s.terms;   // reuse: terms are consumed
-    if (l == 0) s_act[rib] = valid ? act : 0.0f;
-    __syncthreads();
-    const int n_qblk = rows_pb / 32;
-    const int half = threadIdx.x / 32;
-    const int j = threadIdx.x % 32;
-    const int64_t nb_out = a.total_rows / 32;
-    if (half < n_qblk) {
-        const int out_row = blockIdx.x * rows_pb + half * 32 + j;
-        const bool ok = out_row < a.total_rows;
-        const float v = ok ? s_act[half * 32 + j] : 0.0f;
-        const float amax = group_max<32>(fabsf(v));
-        const float dd = amax / 127;
-        const float id = dd ? 1.0f / dd : 0.0f;
-        const int q = (int) roundf(v * id);
-        const float qsum = group_sum<32>((float) q);
-        if (ok) {
-            L.act_q.qs[(int64_t) col * a.total_rows + out_row] = (int8_t) q;
-            if (j == 0) {
-                L.act_q.d[(int64_t) col * nb_out + out_row / 32] = __half2float(__float2half_rn(dd));
-                L.act_q.s[(int64_t) col * nb_out + out_row / 32] = (int32_t) qsum;
-            }
-        }
-    }
 }
 
 template <int TYPE, int LPR, bool SWIGLU, int ITS>
@@ -656,6 +662,20 @@ static void launch_gemv_t(gemv_kargs & ka, int waves, hipStream_t st) {
     }
 }
 
+// Lanes per row for a single-chain Q4_0/Q8_0 launch of 4-wave workgroups: the fewest (longest
+// register-resident run of blocks per lane) that still gives about two workgroups per CU, so short
+// matrices (the o-projection, the down projection) spread over the whole chip.
+template <int TYPE, bool SWIGLU>
+static void launch_gemv_lanes(gemv_kargs & ka, hipStream_t st) {
+    constexpr int WAVES = 4, TARGET_BLOCKS = 512;
+    const int rows = ka.total_rows, K = ka.L.K;
+    const auto blocks = [&](int lpr) { return (rows + WAVES * (WAVE / lpr) - 1) / (WAVES * (WAVE / lpr)); };
+    const int k16 = SWIGLU ? gemv_swiglu_max_k(TYPE) : 8192;     // longest K of 16 lanes per row
+    if (K <= k16 && blocks(16) >= TARGET_BLOCKS) launch_gemv_t<TYPE, 16, SWIGLU>(ka, WAVES, st);
+    else if (K <= 2 * k16 && blocks(32) >= TARGET_BLOCKS) launch_gemv_t<TYPE, 32, SWIGLU>(ka, WAVES, st);
+    else launch_gemv_t<TYPE, 64, SWIGLU>(ka, WAVES, st);
+}
+
 void launch_gemv(const gemv_launch & L, hipStream_t st) {
     gemv_kargs ka;
     ka.L = L;
@@ -667,24 +687,21 @@ void launch_gemv(const gemv_launch & L, hipStream_t st) {
     for (int i = L.n_mats; i <= GEMV_MAX_MATS; i++) ka.row_begin[i] = r;
     ka.total_rows = L.swiglu ? L.m[0].n_rows : r;
     if (L.swiglu && (L.n_mats != 2 || L.m[0].n_rows != L.m[1].n_rows)) HIP_ABORT("gemv: swiglu needs two equal matrices");
-    if (L.swiglu && L.act_q.qs && (ka.total_rows % 32 != 0)) HIP_ABORT("gemv: quantized swiglu output needs rows %% 32 == 0");
     if (L.norm.x) {
-        const int max_k = L.type == GGML_TYPE_Q4_K ? GEMV_NORM_MAX_K_Q8K : GEMV_NORM_MAX_K_Q8;
-        if (L.K > max_k) HIP_ABORT("gemv: the RMSNorm prologue handles K <= %d (K=%d)", max_k, L.K);
+        const int max_k = gemv_prologue_max_k(L.type, L.norm.rms != 0);
+        if (L.K > max_k) HIP_ABORT("gemv: the activation prologue handles K <= %d (K=%d)", max_k, L.K);
         if (((uintptr_t) L.norm.x | (uintptr_t) L.norm.w) % 16 || L.norm.x_stride % 4) HIP_ABORT("gemv: RMSNorm prologue operands must be 16-byte aligned");
     }
     switch (L.type) {
         case GGML_TYPE_Q4_0:
             if (L.K % 32 || L.K > GEMV_MAX_K) HIP_ABORT("gemv q4_0: K=%d unsupported", L.K);
-            if (L.swiglu) launch_gemv_t<GGML_TYPE_Q4_0, 16, true>(ka, 8, st);
-            else if (L.K <= 8192) launch_gemv_t<GGML_TYPE_Q4_0, 16, false>(ka, 4, st);
-            else launch_gemv_t<GGML_TYPE_Q4_0, 32, false>(ka, 4, st);
+            if (L.swiglu) launch_gemv_lanes<GGML_TYPE_Q4_0, true>(ka, st);
+            else launch_gemv_lanes<GGML_TYPE_Q4_0, false>(ka, st);
             break;
         case GGML_TYPE_Q8_0:
             if (L.K % 32 || L.K > GEMV_MAX_K) HIP_ABORT("gemv q8_0: K=%d unsupported", L.K);
-            if (L.swiglu) launch_gemv_t<GGML_TYPE_Q8_0, 16, true>(ka, 8, st);
-            else if (L.K <= 8192) launch_gemv_t<GGML_TYPE_Q8_0, 16, false>(ka, 4, st);
-            else launch_gemv_t<GGML_TYPE_Q8_0, 32, false>(ka, 4, st);
+            if (L.swiglu) launch_gemv_lanes<GGML_TYPE_Q8_0, true>(ka, st);
+            else launch_gemv_lanes<GGML_TYPE_Q8_0, false>(ka, st);
             break;
         case GGML_TYPE_Q4_K:
             if (L.K % 256 || L.K / 64 > 608) HIP_ABORT("gemv q4_K: K=%d unsupported", L.K);

@@ -72,22 +72,25 @@ struct gemv_mat {
     int32_t         n_rows;
 };
 
-// RMSNorm prologue of a GEMV: the activation is rms_norm(x) * w, computed and quantized by every
-// workgroup for its column (ggml's rms_norm -> mul -> quantize_row_q8_0 / q8_K chain, same roundings)
+// Activation prologue of a GEMV: every workgroup quantizes its column of x itself, either as
+// rms_norm(x) * w (rms set: ggml's rms_norm -> mul -> quantize_row_q8_0 / q8_K chain, same
+// roundings) or as x (the activation quantization ggml-cpu applies inside mul_mat).
 struct gemv_norm {
-    const float * x;       // raw input, column c at x + c * x_stride (nullptr: no prologue)
+    const float * x;       // column c at x + c * x_stride (nullptr: no prologue)
     int64_t       x_stride;
-    const float * w;       // norm weight [K] (nullptr: rms_norm without the multiply)
+    const float * w;       // norm weight [K] (rms only; nullptr: rms_norm without the multiply)
     float         eps;
+    int           rms;
 };
 
-// largest K the prologue handles (one 32-element Q8_0 block or one 16-element Q8_K group per thread
-// of the smallest launch, 256 threads)
-constexpr int GEMV_NORM_MAX_K_Q8 = 256 * 32;
+// largest K of the prologue: with rms, one 32-element Q8_0 block or one 16-element Q8_K group per
+// thread of a 256-thread workgroup; without, up to 8 of them per thread
+constexpr int gemv_prologue_max_k(int type, bool rms) {
+    return (type == 12 /* GGML_TYPE_Q4_K */ ? 16 : 32) * 256 * (rms ? 1 : 8);
+}
 // longest row of the register-resident rms_norm kernel (32 elements per thread); longer rows go
 // through the strided kernel
 constexpr int RMS_NORM_MAX_ROW = 256 * 32;
-constexpr int GEMV_NORM_MAX_K_Q8K = 256 * 16;
 
 struct gemv_launch {
     int        type;       // GGML_TYPE_Q4_0 / Q8_0 / Q4_K
@@ -103,9 +106,7 @@ struct gemv_launch {
     const int16_t * xbs;   // q8K: 16-wise sums
     gemv_norm  norm;
     // SwiGLU epilogue: m[0] = gate, m[1] = up (same n_rows); writes act = silu(g) * u to m[0].y
-    // and, when act_q.qs is set, the Q8_0-quantized act (for the following down projection)
     bool       swiglu;
-    q8_act     act_q;
 };
 
 void launch_gemv(const gemv_launch & L, hipStream_t st);

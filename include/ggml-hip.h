@@ -38,6 +38,9 @@ GGML_API void ggml_backend_hip_set_profiling(ggml_backend_t backend, bool enable
 // Restricts the events to kernels whose name starts with prefix (NULL or "" = every kernel), so a
 // timed run can measure one kernel without bracketing every launch.
 GGML_API void ggml_backend_hip_set_profile_filter(ggml_backend_t backend, const char * prefix);
+// Times one graph compute in every `every` (1 = all) while profiling is on: reading back the
+// events costs host time after each timed compute, which sampling keeps out of most steps.
+GGML_API void ggml_backend_hip_set_profile_sampling(ggml_backend_t backend, int every);
 GGML_API void ggml_backend_hip_reset_profile(ggml_backend_t backend);
 // Number of distinct kernel names recorded.
 GGML_API int  ggml_backend_hip_profile_count(ggml_backend_t backend);
