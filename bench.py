@@ -74,6 +74,40 @@ def cpu_baseline(gl, model_path, n_pos, token, seconds, threads):
             "by_threads": {str(k): round(r[0], 3) for k, r in runs.items()}}
 
 
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "gemv_q4_0_llama3b_decode_traffic.json")
+
+
+def summarize_pmc(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_mb, kernel_prefix):
+    """HBM bytes per launch of the kernels whose name starts with kernel_prefix, from four
+    rocprofv3 --pmc runs (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each over the bench and
+    over the copy kernel of copy_mb MiB). Each counter is scaled by what it reads for the copy,
+    whose bytes are known: scale = copy bytes / counter bytes."""
+    import csv
+    import glob
+
+    def per_dispatch(d, prefix):
+        vals = []
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                name = r["Kernel_Name"]
+                if name.startswith(prefix):
+                    vals.append(float(r["Counter_Value"]) * 1024.0)
+        if not vals:
+            raise SystemExit(f"no {prefix} dispatches in {d}")
+        return sum(vals) / len(vals), len(vals)
+
+    copy_bytes = copy_mb * (1 << 20)
+    cf, _ = per_dispatch(copy_fetch_dir, "cpy_kernel")
+    cw, _ = per_dispatch(copy_write_dir, "cpy_kernel")
+    f, n = per_dispatch(fetch_dir, kernel_prefix)
+    w, _ = per_dispatch(write_dir, kernel_prefix)
+    fs, ws = copy_bytes / cf, copy_bytes / cw
+    return {"kernel_prefix": kernel_prefix, "dispatches": n,
+            "fetch_size_bytes_per_dispatch": round(f), "write_size_bytes_per_dispatch": round(w),
+            "fetch_scale": round(fs, 4), "write_scale": round(ws, 4),
+            "copy_kernel_bytes": copy_bytes, "traffic_bytes_per_launch": round(f * fs + w * ws)}
+
+
 def copy_kernel(gl, mb, reps):
     """Runs the backend's own contiguous f32 copy (a ggml_cpy graph node) over mb MiB reps times:
     the known-size kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
@@ -111,7 +145,14 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=24.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0, help="only run the copy kernel of this size (counter calibration)")
+    ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
+                    help="print the HBM bytes per launch of the dominant kernel from rocprofv3 --pmc runs")
+    ap.add_argument("--copy-mb-of-pmc", type=int, default=256, help="size of the copy kernel of the calibration runs")
     args = ap.parse_args()
+
+    if args.summarize_pmc:
+        print(json.dumps(summarize_pmc(*args.summarize_pmc, args.copy_mb_of_pmc, "void gemv_kernel<2,")), flush=True)
+        return
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -170,6 +211,10 @@ def main():
         breakdown[k] = {"launches_per_step": round(n / args.breakdown_steps, 2), "us_per_launch": round(ms / n * 1e3, 2),
                         "GB/s": round(gbs, 1)}
     timed_steps = (args.steps + PROFILE_EVERY - 1) // PROFILE_EVERY
+    # HBM bytes per launch measured by rocprofv3 --pmc on this workload (profiles/, see its summary)
+    traffic = None
+    if os.path.exists(TRAFFIC_JSON):
+        traffic = json.load(open(TRAFFIC_JSON))["traffic_bytes_per_launch"]
     gemv = [v for k, v in timed.items() if k.startswith(dominant)]
     g_launch = sum(v[0] for v in gemv)
     g_ms = sum(v[1] for v in gemv)
@@ -181,7 +226,7 @@ def main():
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBS, 4),
-        "traffic": None,
+        "traffic": traffic,
         "kernel": f"{dominant}* (every quantized-GEMV launch of a step: QKV, O+residual, gate/up+SwiGLU, "
                   "down+residual, LM head)",
         "launches_per_step": round(g_launch / timed_steps, 2),

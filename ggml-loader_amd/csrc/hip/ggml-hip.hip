@@ -477,6 +477,12 @@ private:
         return wtype;
     }
 
+    int64_t max_consumer_rows(int u) const {
+        int64_t r = 0;
+        for (int j : users_[u]) r = std::max(r, (int64_t) g_->nodes[j]->src[0]->ne[1]);
+        return r;
+    }
+
     // rms_norm * w (node u, rows of N) whose every consumer is a quantized GEMV that can compute the
     // normalization in its prologue: the normalized activation is then never materialized
     bool norm_deferrable(int u, int64_t N) const {
@@ -649,8 +655,26 @@ private:
                     w->ne[0] == x->ne[0] && ggml_is_contiguous(w) && ggml_is_contiguous(m)) {
                     const int64_t N = x->ne[0], rows = ggml_nrows(x);
                     if (m->ne[1] == rows && norm_deferrable(u, N) && ((uintptr_t) x->data | (uintptr_t) w->data) % 16 == 0) {
-                        norm_[m] = gemv_norm{ (const float *) x->data, N, (const float *) w->data, eps, 1 };
+                        const gemv_norm nz{ (const float *) x->data, N, (const float *) w->data, eps, 1 };
                         done_[u] = true;
+                        if (max_consumer_rows(u) <= GEMV_PROLOGUE_MAX_ROWS) {
+                            norm_[m] = nz;      // every consumer workgroup normalizes for itself
+                            return;
+                        }
+                        // a very wide consumer (the LM head): normalize and quantize once
+                        const int wtype = gemv_only_consumers(u);
+                        const int kind = dot_kind(wtype);
+                        act_entry e = alloc_act(kind, N, rows);
+                        gemv_launch L{};
+                        L.type = wtype;
+                        L.K = (int) N;
+                        L.ncols = (int) rows;
+                        L.norm = nz;
+                        {
+                            prof_scope ps(this, "act_quant", (double) (N * rows * 4 + N * 4));
+                            launch_act_quant(L, e.q8, e.q8k, st_);
+                        }
+                        act_[m] = e;
                         return;
                     }
                     const int kind = m->ne[1] == rows ? wanted_act_kind(u) : 0;

@@ -367,16 +367,51 @@ __device__ __forceinline__ void load_chunk(float (&v)[C], const float * p) {
 // rms_norm(x) * w (rms set: ggml's rms_norm -> mul -> quantize chain, same roundings; one chunk per
 // thread, so only the sum of squares is reduced over the workgroup) or as x itself (the quantize
 // that ggml-cpu applies to a mul_mat's activation; several chunks per thread).
+//
+// Loads complete in issue order, so the prologue's loads go out before the weight stream: the
+// prologue then computes while the weights are in flight instead of after they arrive. The first
+// 32 values per thread (one Q8_0 block, or two Q8_K groups in the quantize-only mode) are loaded by
+// prologue_load into registers; further chunks are loaded when they are quantized.
+constexpr int PRO_REGS = 32;
+
 template <int TYPE>
-__device__ __forceinline__ void stage_norm(const gemv_launch & L, int col, const gemv_lds & s, double * s_red) {
+__device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, float (&xv)[PRO_REGS], float (&wv)[PRO_REGS]) {
     constexpr int C = TYPE == GGML_TYPE_Q4_K ? 16 : 32;
-    const int K = L.K;
+#pragma unroll
+    for (int e = 0; e < PRO_REGS; e++) { xv[e] = 0.0f; wv[e] = 1.0f; }
+    if (!L.norm.x) return;
+    const int nchunk = L.K / C;
     const int t = threadIdx.x;
     const float * xcol = L.norm.x + (int64_t) col * L.norm.x_stride;
+    float (&x0)[C] = *reinterpret_cast<float (*)[C]>(&xv[0]);
+    if (t < nchunk) {
+        load_chunk(x0, xcol + (int64_t) t * C);
+        if (L.norm.rms && L.norm.w) load_chunk(*reinterpret_cast<float (*)[C]>(&wv[0]), L.norm.w + (int64_t) t * C);
+    }
+    if (C * 2 == PRO_REGS && !L.norm.rms && t + (int) blockDim.x < nchunk) {
+        load_chunk(*reinterpret_cast<float (*)[C]>(&xv[PRO_REGS - C]), xcol + (int64_t) (t + blockDim.x) * C);
+    }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void prologue_finish(const gemv_launch & L, int col, float (&xv)[PRO_REGS], const float (&wv)[PRO_REGS],
+                                                const gemv_lds & s, double * s_red) {
+    constexpr int C = TYPE == GGML_TYPE_Q4_K ? 16 : 32;
+    const int K = L.K;
+    const int nchunk = K / C;
+    const int t = threadIdx.x;
+    float (&x0)[C] = *reinterpret_cast<float (*)[C]>(&xv[0]);
     if (!L.norm.rms) {
-        for (int c0 = 0; c0 < K / C; c0 += blockDim.x) {
+        quant_chunk<TYPE, C>(x0, t, t < nchunk, s);
+        int c0 = blockDim.x;
+        if (C * 2 == PRO_REGS) {
+            quant_chunk<TYPE, C>(*reinterpret_cast<float (*)[C]>(&xv[PRO_REGS - C]), c0 + t, c0 + t < nchunk, s);
+            c0 += blockDim.x;
+        }
+        const float * xcol = L.norm.x + (int64_t) col * L.norm.x_stride;
+        for (; c0 < nchunk; c0 += blockDim.x) {
             const int c = c0 + t;
-            const bool has = c < K / C;
+            const bool has = c < nchunk;
             float v[C];
 #pragma unroll
             for (int e = 0; e < C; e++) v[e] = 0.0f;
@@ -386,17 +421,9 @@ __device__ __forceinline__ void stage_norm(const gemv_launch & L, int col, const
         return;
     }
     const int lane = t % WAVE, wave = t / WAVE;
-    const bool has = t < K / C;
-    float v[C], wv[C];
-#pragma unroll
-    for (int e = 0; e < C; e++) { v[e] = 0.0f; wv[e] = 1.0f; }
-    if (has) {
-        load_chunk(v, xcol + (int64_t) t * C);
-        if (L.norm.w) load_chunk(wv, L.norm.w + (int64_t) t * C);
-    }
     double ss = 0.0;
 #pragma unroll
-    for (int e = 0; e < C; e++) ss += (double) (v[e] * v[e]);
+    for (int e = 0; e < C; e++) ss += (double) (x0[e] * x0[e]);
     ss = wave_sum_d(ss);
     if (lane == 0) s_red[wave] = ss;
     __syncthreads();
@@ -406,18 +433,19 @@ __device__ __forceinline__ void stage_norm(const gemv_launch & L, int col, const
     const float scale = 1.0f / sqrtf(mean + L.norm.eps);
 #pragma unroll
     for (int e = 0; e < C; e++) {
-        v[e] = v[e] * scale;
-        if (L.norm.w) v[e] = v[e] * wv[e];
+        x0[e] = x0[e] * scale;
+        if (L.norm.w) x0[e] = x0[e] * wv[e];
     }
-    quant_chunk<TYPE, C>(v, t, has, s);
+    quant_chunk<TYPE, C>(x0, t, t < nchunk, s);
 }
 
-// the quantized activation column in LDS: copied, or computed by the RMSNorm prologue
+// the quantized activation column in LDS: finished by the prologue, or copied
 template <int TYPE>
-__device__ __forceinline__ void stage_x(const gemv_launch & L, int col, const gemv_lds & s, double * s_red) {
+__device__ __forceinline__ void stage_x(const gemv_launch & L, int col, const gemv_lds & s, double * s_red,
+                                        float (&xv)[PRO_REGS], const float (&wv)[PRO_REGS]) {
     const int K = L.K;
     if (L.norm.x) {
-        stage_norm<TYPE>(L, col, s, s_red);
+        prologue_finish<TYPE>(L, col, xv, wv, s, s_red);
     } else if (TYPE == GGML_TYPE_Q4_K) {
         const int nsb = K / 256;
         for (int i = threadIdx.x * 16; i < K; i += blockDim.x * 16) *(int4 *) (s.xq + i) = *(const int4 *) (L.xq + (int64_t) col * K + i);
@@ -432,6 +460,46 @@ __device__ __forceinline__ void stage_x(const gemv_launch & L, int col, const ge
         }
     }
     __syncthreads();
+}
+
+// The prologue run once per column into global memory, for consumers too wide to redo it in every
+// workgroup (the LM head): same arithmetic, so the GEMV that copies the result computes the same floats.
+template <int TYPE>
+__global__ __launch_bounds__(256) void act_quant_kernel(const gemv_launch L, q8_act q8, q8k_act q8k) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ double s_red[256 / WAVE];
+    const int col = blockIdx.x;
+    const int K = L.K;
+    const gemv_lds s = lds_layout<TYPE>(smem, K);
+    float xv[PRO_REGS], wv[PRO_REGS];
+    prologue_load<TYPE>(L, col, xv, wv);
+    prologue_finish<TYPE>(L, col, xv, wv, s, s_red);
+    __syncthreads();
+    int8_t * qs = (TYPE == GGML_TYPE_Q4_K ? q8k.qs : q8.qs) + (int64_t) col * K;
+    for (int i = threadIdx.x * 16; i < K; i += blockDim.x * 16) *(int4 *) (qs + i) = *(const int4 *) (s.xq + i);
+    if (TYPE == GGML_TYPE_Q4_K) {
+        for (int i = threadIdx.x; i < K / 256; i += blockDim.x) q8k.d[(int64_t) col * (K / 256) + i] = s.xd[i];
+        for (int i = threadIdx.x; i < K / 16; i += blockDim.x) q8k.bsums[(int64_t) col * (K / 16) + i] = s.xbs[i];
+    } else {
+        for (int i = threadIdx.x; i < K / 32; i += blockDim.x) {
+            q8.d[(int64_t) col * (K / 32) + i] = s.xd[i];
+            q8.s[(int64_t) col * (K / 32) + i] = s.xs[i];
+        }
+    }
+}
+
+void launch_act_quant(const gemv_launch & L, const q8_act & q8, const q8k_act & q8k, hipStream_t st) {
+    if (!L.norm.x || L.K > gemv_prologue_max_k(L.type, L.norm.rms != 0)) HIP_ABORT("act_quant: K=%d unsupported", L.K);
+    switch (L.type) {
+        case GGML_TYPE_Q4_0: case GGML_TYPE_Q8_0:
+            launch(act_quant_kernel<GGML_TYPE_Q4_0>, dim3(L.ncols), dim3(256), gemv_lds_bytes<GGML_TYPE_Q4_0>(L.K, 0, 0), st, L, q8, q8k);
+            break;
+        case GGML_TYPE_Q4_K:
+            launch(act_quant_kernel<GGML_TYPE_Q4_K>, dim3(L.ncols), dim3(256), gemv_lds_bytes<GGML_TYPE_Q4_K>(L.K, 0, 0), st, L, q8, q8k);
+            break;
+        default:
+            HIP_ABORT("act_quant: unsupported weight type %d", L.type);
+    }
 }
 
 template <int TYPE, int LPR, bool SWIGLU, int ITS>
@@ -461,8 +529,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
         constexpr int QS = TYPE == GGML_TYPE_Q4_0 ? Q4_0_QS : Q8_0_QS;
         constexpr int MAXIT = ITS;   // blocks per lane (nb <= ITS * LPR)
         const int nb = K / 32;
-        // every weight load of this lane is issued before the activation is staged, so the weight
-        // stream is in flight while the column is copied or normalized and quantized
+        // prologue loads, then every weight load of this lane, then the prologue's arithmetic: the
+        // weight stream is in flight while the column is normalized and quantized
+        float xv[PRO_REGS], wv[PRO_REGS];
+        prologue_load<TYPE>(L, col, xv, wv);
         uint4 qa[NCH][MAXIT], qb[NCH][MAXIT];
         float dw[NCH][MAXIT];
 #pragma unroll
@@ -479,7 +549,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                 }
             }
         }
-        stage_x<TYPE>(L, col, s, s_red);
+        stage_x<TYPE>(L, col, s, s_red, xv, wv);
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++) {
             if (!valid) break;
@@ -504,7 +574,9 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
             }
         }
     } else { // Q4_K: per (super-block, l) products d*aux32[l] and dmin*mins
-        stage_x<TYPE>(L, col, s, s_red);
+        float xv[PRO_REGS], wv[PRO_REGS];
+        prologue_load<TYPE>(L, col, xv, wv);
+        stage_x<TYPE>(L, col, s, s_red, xv, wv);
         constexpr int MAXU = 608 / LPR;   // supports K <= 9728 * 4 (units = K/64 <= 608)
         const int units = K / 64, nsb = K / 256;
         const int64_t row_bytes = (int64_t) nsb * Q4_K_BYTES;

@@ -110,6 +110,10 @@ struct gemv_launch {
 };
 
 void launch_gemv(const gemv_launch & L, hipStream_t st);
+// L.norm's prologue for L.ncols columns of L.K, written once to q8 (Q4_0/Q8_0 consumers) or q8k (Q4_K)
+void launch_act_quant(const gemv_launch & L, const q8_act & q8, const q8k_act & q8k, hipStream_t st);
+// consumers with more rows than this get the activation quantized once instead of per workgroup
+constexpr int GEMV_PROLOGUE_MAX_ROWS = 32768;
 
 // ---------------------------------------------------------------------------------------------
 // element-wise / normalization / positional kernels
