@@ -22,6 +22,7 @@ BIN_DIR = os.path.join(PKG_DIR, "bin")
 # ggml type ids (GGUF on-disk ids)
 F32, F16, Q4_0, Q8_0, Q4_K, Q8_K, I32, BF16 = 0, 1, 2, 8, 12, 15, 26, 30
 ROPE_NORMAL, ROPE_NEOX = 0, 2
+SORT_ASC, SORT_DESC = 0, 1
 UNARY_SILU = 1
 
 _libs: dict | None = None
@@ -129,6 +130,10 @@ def _declare(core, hip, loader):
     _sig(core, "ggml_unary", T, vp, T, i32)
     _sig(core, "ggml_flash_attn_ext", T, vp, T, T, T, T, f32, f32, f32)
     _sig(core, "ggml_argmax", T, vp, T)
+    _sig(core, "ggml_div", T, vp, T, T)
+    _sig(core, "ggml_sum_rows", T, vp, T)
+    _sig(core, "ggml_argsort", T, vp, T, i32)
+    _sig(core, "ggml_top_k", T, vp, T, i32)
     _sig(core, "ggml_new_graph", vp, vp)
     _sig(core, "ggml_build_forward_expand", None, vp, T)
     _sig(core, "ggml_graph_n_nodes", i32, vp)

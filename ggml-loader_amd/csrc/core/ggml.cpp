@@ -86,7 +86,7 @@ const char * ggml_op_name(enum ggml_op op) {
     static const char * names[GGML_OP_COUNT] = {
         "NONE", "DUP", "ADD", "MUL", "SCALE", "SQR", "RMS_NORM", "MUL_MAT", "MUL_MAT_ID", "CPY", "CONT",
         "RESHAPE", "VIEW", "PERMUTE", "TRANSPOSE", "GET_ROWS", "SOFT_MAX", "ROPE", "FLASH_ATTN_EXT",
-        "ARGMAX", "UNARY",
+        "ARGMAX", "UNARY", "DIV", "SUM_ROWS", "ARGSORT",
     };
     return ((int) op >= 0 && op < GGML_OP_COUNT) ? names[op] : "?";
 }
@@ -432,6 +432,7 @@ static ggml_tensor * binary_op(ggml_context * ctx, ggml_tensor * a, ggml_tensor 
 }
 struct ggml_tensor * ggml_mul(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b) { return binary_op(ctx, a, b, GGML_OP_MUL); }
 struct ggml_tensor * ggml_add(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b) { return binary_op(ctx, a, b, GGML_OP_ADD); }
+struct ggml_tensor * ggml_div(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b) { return binary_op(ctx, a, b, GGML_OP_DIV); }
 
 struct ggml_tensor * ggml_scale(struct ggml_context * ctx, struct ggml_tensor * a, float s) {
     ggml_tensor * r = ggml_dup_tensor(ctx, a);
@@ -683,6 +684,29 @@ struct ggml_tensor * ggml_flash_attn_ext(struct ggml_context * ctx, struct ggml_
     r->src[2] = v;
     r->src[3] = mask;
     return r;
+}
+
+struct ggml_tensor * ggml_sum_rows(struct ggml_context * ctx, struct ggml_tensor * a) {
+    GGML_CHECK(a->type == GGML_TYPE_F32);
+    ggml_tensor * r = ggml_new_tensor_4d(ctx, GGML_TYPE_F32, 1, a->ne[1], a->ne[2], a->ne[3]);
+    r->op = GGML_OP_SUM_ROWS;
+    r->src[0] = a;
+    return r;
+}
+
+struct ggml_tensor * ggml_argsort(struct ggml_context * ctx, struct ggml_tensor * a, enum ggml_sort_order order) {
+    GGML_CHECK(a->type == GGML_TYPE_F32);
+    ggml_tensor * r = ggml_new_tensor_4d(ctx, GGML_TYPE_I32, a->ne[0], a->ne[1], a->ne[2], a->ne[3]);
+    r->op_params[0] = (int32_t) order;
+    r->op = GGML_OP_ARGSORT;
+    r->src[0] = a;
+    return r;
+}
+
+struct ggml_tensor * ggml_top_k(struct ggml_context * ctx, struct ggml_tensor * a, int k) {
+    GGML_CHECK(k > 0 && k <= a->ne[0]);
+    ggml_tensor * s = ggml_argsort(ctx, a, GGML_SORT_ORDER_DESC);
+    return ggml_view_4d(ctx, s, k, s->ne[1], s->ne[2], s->ne[3], s->nb[1], s->nb[2], s->nb[3], 0);
 }
 
 struct ggml_tensor * ggml_argmax(struct ggml_context * ctx, struct ggml_tensor * a) {

@@ -419,7 +419,11 @@ private:
     const act_entry * ensure_act(const ggml_tensor * x, int kind) {
         auto it = act_.find(x);
         if (it != act_.end() && it->second.kind == kind) return &it->second;
-        const int64_t K = x->ne[0], ncols = x->ne[1];
+        const int64_t K = x->ne[0], ncols = ggml_nrows(x);
+        if (x->type != GGML_TYPE_F32 || x->nb[0] != sizeof(float) ||
+            (x->ne[2] > 1 && x->nb[2] != x->nb[1] * x->ne[1]) || (x->ne[3] > 1 && x->nb[3] != x->nb[2] * x->ne[2])) {
+            HIP_ABORT("activation '%s' for a quantized mul_mat: rows must be f32 and evenly strided", x->name);
+        }
         act_entry e = alloc_act(kind, K, ncols);
         const int64_t col_stride = (int64_t) (x->nb[1] / sizeof(float));
         if (kind == 1) {
@@ -470,7 +474,8 @@ private:
         int wtype = -1;
         for (int j : users_[u]) {
             const ggml_tensor * n = g_->nodes[j];
-            if (n->op != GGML_OP_MUL_MAT || n->src[1] != m || n->src[0] == m || attn_.count(j) || !gemv_capable(n)) return -1;
+            if ((n->op != GGML_OP_MUL_MAT && n->op != GGML_OP_MUL_MAT_ID) || n->src[1] != m || n->src[0] == m || attn_.count(j) ||
+                !gemv_capable(n)) return -1;
             if (wtype >= 0 && dot_kind(n->src[0]->type) != dot_kind(wtype)) return -1;
             wtype = n->src[0]->type;
         }
@@ -500,6 +505,13 @@ private:
             case GGML_OP_RMS_NORM: op_rms_norm(i); return;
             case GGML_OP_ROPE: op_rope(i); return;
             case GGML_OP_MUL_MAT: op_mul_mat(i); return;
+            case GGML_OP_MUL_MAT_ID:
+                if (!gemv_capable(n)) HIP_ABORT("mul_mat_id '%s': unsupported operands", n->name);
+                op_gemv(i);
+                return;
+            case GGML_OP_MUL:
+                if (fuse(FUSE_ADD) && op_moe_wsum(i)) return;
+                break;
             default: break;
         }
         wrote_.push_back(n);
@@ -507,6 +519,13 @@ private:
             case GGML_OP_GET_ROWS: op_get_rows(n); return;
             case GGML_OP_ADD: { prof_scope ps(this, "add", 0); launch_binary(0, tv(n->src[0]), tv(n->src[1]), tv(n), st_); return; }
             case GGML_OP_MUL: { prof_scope ps(this, "mul", 0); launch_binary(1, tv(n->src[0]), tv(n->src[1]), tv(n), st_); return; }
+            case GGML_OP_DIV: { prof_scope ps(this, "div", 0); launch_binary(2, tv(n->src[0]), tv(n->src[1]), tv(n), st_); return; }
+            case GGML_OP_SUM_ROWS: { prof_scope ps(this, "sum_rows", 0); launch_sum_rows(tv(n->src[0]), tv(n), st_); return; }
+            case GGML_OP_ARGSORT: {
+                prof_scope ps(this, "argsort", 0);
+                launch_argsort(tv(n->src[0]), tv(n), n->op_params[0] == GGML_SORT_ORDER_DESC, st_);
+                return;
+            }
             case GGML_OP_SCALE: {
                 float s;
                 memcpy(&s, n->op_params, 4);
@@ -705,11 +724,18 @@ private:
         const ggml_tensor * w = mm->src[0];
         const ggml_tensor * x = mm->src[1];
         if (!dot_kind(w->type)) return false;
-        if (!is_2d_contig(w)) return false;
-        if (x->type != GGML_TYPE_F32 || x->nb[0] != sizeof(float) || x->ne[2] != 1 || x->ne[3] != 1) return false;
-        if (!is_2d_contig(mm)) return false;
         if (w->ne[0] % (w->type == GGML_TYPE_Q4_K ? 256 : 32)) return false;
-        return true;
+        if (x->type != GGML_TYPE_F32 || x->nb[0] != sizeof(float)) return false;
+        if (mm->op == GGML_OP_MUL_MAT_ID) {
+            // experts [K, N, n_expert] stored contiguously; activation [K, x_cols, n_tok] with evenly
+            // strided rows; output [N, n_slots, n_tok] contiguous
+            const ggml_tensor * ids = mm->src[2];
+            return ggml_is_contiguous(w) && w->ne[3] == 1 && x->ne[3] == 1 && x->nb[2] == x->nb[1] * x->ne[1] &&
+                   ids->type == GGML_TYPE_I32 && ids->nb[0] == sizeof(int32_t) && ggml_is_contiguous(mm);
+        }
+        if (!is_2d_contig(w)) return false;
+        if (x->ne[2] != 1 || x->ne[3] != 1) return false;
+        return is_2d_contig(mm);
     }
 
     void op_mul_mat(int i) {
@@ -733,7 +759,10 @@ private:
         ggml_tensor * n = g_->nodes[i];
         const ggml_tensor * x = n->src[1];
         const int wtype = n->src[0]->type;
-        const int64_t K = n->src[0]->ne[0], ncols = x->ne[1];
+        const bool by_id = n->op == GGML_OP_MUL_MAT_ID;
+        const ggml_tensor * ids = by_id ? n->src[2] : nullptr;
+        const int64_t K = n->src[0]->ne[0];
+        const int64_t ncols = by_id ? ids->ne[0] * ids->ne[1] : x->ne[1];   // launch columns
         std::vector<int> group = { i };
         if (fuse(FUSE_GROUP)) {
             const int xi = node_index(x);
@@ -741,14 +770,14 @@ private:
             if (xi < 0) {
                 for (int j = i + 1; j < g_->n_nodes; j++) {
                     const ggml_tensor * m = g_->nodes[j];
-                    if (m->op == GGML_OP_MUL_MAT && m->src[1] == x) others.push_back(j);
+                    if (m->op == n->op && m->src[1] == x) others.push_back(j);
                 }
             } else {
                 for (int j : users_[xi]) if (j != i) others.push_back(j);
             }
             for (int j : others) {
                 const ggml_tensor * m = g_->nodes[j];
-                if (done_[j] || m->op != GGML_OP_MUL_MAT || m->src[1] != x) continue;
+                if (done_[j] || m->op != n->op || m->src[1] != x || (by_id && m->src[2] != ids)) continue;
                 if (attn_.count(j)) continue;
                 if (m->src[0]->type != wtype || m->src[0]->ne[0] != K || !gemv_capable(m)) continue;
                 if ((int) group.size() == GEMV_MAX_MATS) break;
@@ -770,7 +799,7 @@ private:
                 if (mn->op != GGML_OP_MUL || mn->src[0] != sn) continue;
                 const int b = node_index(mn->src[1]);
                 if (b < 0 || sole_user(b) != m || std::find(group.begin(), group.end(), b) == group.end()) continue;
-                if (!ggml_are_same_shape(g_->nodes[a], g_->nodes[b]) || !is_2d_contig(mn)) continue;
+                if (!ggml_are_same_shape(g_->nodes[a], g_->nodes[b]) || !(by_id ? ggml_is_contiguous(mn) : is_2d_contig(mn))) continue;
                 gate = a; up = b; mulnode = m;
                 break;
             }
@@ -796,7 +825,10 @@ private:
             gm.y_stride = (int64_t) (mm->nb[1] / sizeof(float));
             gm.add = nullptr;
             gm.add_stride = 0;
-            bytes += (double) ggml_nbytes(w) + (double) (w->ne[1] * ncols * 4);
+            // the weights one launch must read: every row, or the rows of the selected experts
+            const double wbytes = by_id ? std::min((double) ggml_nbytes(w), (double) ncols * (double) w->nb[2])
+                                        : (double) ggml_nbytes(w);
+            bytes += wbytes + (double) (w->ne[1] * ncols * 4);
             const ggml_tensor * written = mm;
             // residual add epilogue
             const int u = (epilogue && fuse(FUSE_ADD)) ? sole_user(j) : -1;
@@ -823,7 +855,15 @@ private:
         if (!xa) L.norm = nz->second;
         else if (kind == 1) { L.xq = xa->q8.qs; L.xd = xa->q8.d; L.xs = xa->q8.s; }
         else { L.xq = xa->q8k.qs; L.xd = xa->q8k.d; L.xbs = xa->q8k.bsums; }
-        const double x_bytes = (double) (K * ncols * 4) + (xa ? 0.0 : (double) (K * 4));
+        if (by_id) {
+            L.ids = (const int32_t *) ids->data;
+            L.ids_stride = (int64_t) (ids->nb[1] / sizeof(int32_t));
+            L.n_slots = (int) ids->ne[0];
+            L.x_cols = (int) x->ne[1];
+            L.n_experts = (int) n->src[0]->ne[2];
+            L.expert_rows = n->src[0]->ne[1];
+        }
+        const double x_bytes = (double) (K * ggml_nrows(x) * 4) + (xa ? 0.0 : (double) (K * 4));
 
         if (gate >= 0) {
             // SwiGLU launch for (gate, up); the rest of the group goes in a second launch
@@ -865,6 +905,73 @@ private:
             launch_gemv(L, st_);
         }
         for (int j : group) done_[j] = true;
+    }
+
+    // mul(experts [n_embd, k, T], w [1, k, T]) -> views of the k slots -> add chain in slot order
+    // (-> residual add)  ==>  one kernel with the same float operations in the same order
+    bool op_moe_wsum(int i) {
+        const ggml_tensor * m = g_->nodes[i];
+        const ggml_tensor * e = m->src[0], * w = m->src[1];
+        const int64_t n_embd = e->ne[0], k = e->ne[1], T = e->ne[2];
+        if (k < 2 || e->ne[3] != 1 || m->type != GGML_TYPE_F32 || e->type != GGML_TYPE_F32 || w->type != GGML_TYPE_F32) return false;
+        if (!ggml_is_contiguous(m) || w->ne[0] != 1 || w->ne[1] != k || w->ne[2] != T || w->nb[0] != sizeof(float)) return false;
+        if (e->nb[0] != sizeof(float) || is_output(i) || (int64_t) users_[i].size() != k) return false;
+        // the slot views, by offset
+        std::vector<int> view(k, -1);
+        for (int u : users_[i]) {
+            const ggml_tensor * v = g_->nodes[u];
+            if (v->op != GGML_OP_VIEW || v->src[0] != m || v->ne[0] != n_embd || v->ne[1] != T || v->ne[2] != 1 ||
+                v->nb[1] != m->nb[2]) return false;
+            const int64_t off = (const char *) v->data - (const char *) m->data;
+            if (off % (int64_t) m->nb[1] || off / (int64_t) m->nb[1] >= k || view[off / m->nb[1]] >= 0) return false;
+            view[off / m->nb[1]] = u;
+        }
+        // the chain add(add(add(v0, v1), v2), ...)
+        std::vector<int> chain;
+        int cur = view[0];
+        for (int64_t sl = 1; sl < k; sl++) {
+            const int a = sole_user(cur);
+            if (a < 0 || sole_user(view[sl]) != a) return false;
+            const ggml_tensor * an = g_->nodes[a];
+            if (an->op != GGML_OP_ADD || an->src[0] != g_->nodes[cur] || an->src[1] != g_->nodes[view[sl]]) return false;
+            chain.push_back(a);
+            cur = a;
+        }
+        ggml_tensor * last = g_->nodes[cur];
+        moe_wsum M{};
+        M.e = (const float *) e->data;        // e * w is formed inside the kernel, per slot
+        M.e_nb1 = (int64_t) (e->nb[1] / sizeof(float));
+        M.e_nb2 = (int64_t) (e->nb[2] / sizeof(float));
+        M.w = (const float *) w->data;
+        M.w_nb1 = (int64_t) (w->nb[1] / sizeof(float));
+        M.w_nb2 = (int64_t) (w->nb[2] / sizeof(float));
+        M.n_embd = n_embd;
+        M.n_tok = T;
+        M.k = (int) k;
+        // residual add of the sum
+        const int r = sole_user(cur);
+        if (r >= 0) {
+            ggml_tensor * rn = g_->nodes[r];
+            const ggml_tensor * res = rn->src[1];
+            if (rn->op == GGML_OP_ADD && rn->src[0] == last && res->type == GGML_TYPE_F32 && ggml_are_same_shape(res, last) &&
+                res->nb[0] == sizeof(float) && is_2d_contig(rn)) {
+                M.res = (const float *) res->data;
+                M.res_nb1 = (int64_t) (res->nb[1] / sizeof(float));
+                chain.push_back(r);
+                last = rn;
+            }
+        }
+        if (!is_2d_contig(last)) return false;
+        M.out = (float *) last->data;
+        M.out_nb1 = (int64_t) (last->nb[1] / sizeof(float));
+        {
+            prof_scope ps(this, "moe_wsum", (double) (n_embd * k * T * 4 + n_embd * T * 4 * (M.res ? 2 : 1)));
+            launch_moe_wsum(M, st_);
+        }
+        for (int v : view) done_[v] = true;
+        for (int a : chain) done_[a] = true;
+        wrote_.push_back(last);
+        return true;
     }
 
     // K^T Q -> soft_max -> cont(permute(V)) -> V KQ -> permute -> cont  ==>  split-KV attention

@@ -524,6 +524,17 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
     const gemv_lds s = lds_layout<TYPE>(smem, K);
     __shared__ double s_red[512 / WAVE];
 
+    // mul_mat_id: the expert of this column and its activation column
+    int xcol = col;
+    int64_t erow = 0;
+    if (L.ids) {
+        const int t = col / L.n_slots, sl = col % L.n_slots;
+        xcol = t * L.x_cols + sl % L.x_cols;
+        const int e = min(max(L.ids[(int64_t) t * L.ids_stride + sl], 0), L.n_experts - 1);
+        erow = (int64_t) e * L.expert_rows;
+    }
+    const int64_t wrow_i = erow + lrow;           // weight row of this lane's output row
+
     // ---- per-block terms ----
     if (TYPE == GGML_TYPE_Q4_0 || TYPE == GGML_TYPE_Q8_0) {
         constexpr int QS = TYPE == GGML_TYPE_Q4_0 ? Q4_0_QS : Q8_0_QS;
@@ -532,13 +543,13 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
         // prologue loads, then every weight load of this lane, then the prologue's arithmetic: the
         // weight stream is in flight while the column is normalized and quantized
         float xv[PRO_REGS], wv[PRO_REGS];
-        prologue_load<TYPE>(L, col, xv, wv);
+        prologue_load<TYPE>(L, xcol, xv, wv);
         uint4 qa[NCH][MAXIT], qb[NCH][MAXIT];
         float dw[NCH][MAXIT];
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++) {
-            const uint8_t * wq = L.m[SWIGLU ? ch : mi].w + (int64_t) lrow * nb * QS;
-            const __half * wd = L.m[SWIGLU ? ch : mi].wd + (int64_t) lrow * nb;
+            const uint8_t * wq = L.m[SWIGLU ? ch : mi].w + wrow_i * nb * QS;
+            const __half * wd = L.m[SWIGLU ? ch : mi].wd + wrow_i * nb;
 #pragma unroll
             for (int it = 0; it < MAXIT; it++) {
                 const int b = l + it * LPR;
@@ -549,7 +560,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                 }
             }
         }
-        stage_x<TYPE>(L, col, s, s_red, xv, wv);
+        stage_x<TYPE>(L, xcol, s, s_red, xv, wv);
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++) {
             if (!valid) break;
@@ -575,14 +586,14 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
         }
     } else { // Q4_K: per (super-block, l) products d*aux32[l] and dmin*mins
         float xv[PRO_REGS], wv[PRO_REGS];
-        prologue_load<TYPE>(L, col, xv, wv);
-        stage_x<TYPE>(L, col, s, s_red, xv, wv);
+        prologue_load<TYPE>(L, xcol, xv, wv);
+        stage_x<TYPE>(L, xcol, s, s_red, xv, wv);
         constexpr int MAXU = 608 / LPR;   // supports K <= 9728 * 4 (units = K/64 <= 608)
         const int units = K / 64, nsb = K / 256;
         const int64_t row_bytes = (int64_t) nsb * Q4_K_BYTES;
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++) {
-            const uint8_t * wrow = L.m[SWIGLU ? ch : mi].w + (int64_t) (valid ? lrow : 0) * row_bytes;
+            const uint8_t * wrow = L.m[SWIGLU ? ch : mi].w + (valid ? wrow_i : erow) * row_bytes;
             float * terms = s.terms + (rib * NCH + ch) * nsb * 9;
 #pragma unroll 2
             for (int it = 0; it < MAXU; it++) {
@@ -759,6 +770,7 @@ void launch_gemv(const gemv_launch & L, hipStream_t st) {
     for (int i = L.n_mats; i <= GEMV_MAX_MATS; i++) ka.row_begin[i] = r;
     ka.total_rows = L.swiglu ? L.m[0].n_rows : r;
     if (L.swiglu && (L.n_mats != 2 || L.m[0].n_rows != L.m[1].n_rows)) HIP_ABORT("gemv: swiglu needs two equal matrices");
+    if (L.ids && (L.n_slots < 1 || L.x_cols < 1 || L.n_experts < 1 || L.ncols % L.n_slots)) HIP_ABORT("gemv: bad mul_mat_id geometry");
     if (L.norm.x) {
         const int max_k = gemv_prologue_max_k(L.type, L.norm.rms != 0);
         if (L.K > max_k) HIP_ABORT("gemv: the activation prologue handles K <= %d (K=%d)", max_k, L.K);

@@ -213,13 +213,79 @@ __global__ void binary_kernel(int op, tview a, tview b, tview d, int64_t n) {
     const idx4 k = unflatten(i, d.ne);
     const float x = ld(at(a, k.i0, k.i1, k.i2, k.i3), a.type);
     const float y = ld(at(b, k.i0 % b.ne[0], k.i1 % b.ne[1], k.i2 % b.ne[2], k.i3 % b.ne[3]), b.type);
-    st(at(d, k.i0, k.i1, k.i2, k.i3), d.type, op == 0 ? x + y : x * y);
+    st(at(d, k.i0, k.i1, k.i2, k.i3), d.type, op == 0 ? x + y : op == 1 ? x * y : x / y);
 }
 
 void launch_binary(int op, const tview & a, const tview & b, const tview & dst, hipStream_t st) {
     const int64_t n = nelem(dst);
     if (n == 0) return;
     launch(binary_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, op, a, b, dst, n);
+}
+
+// ---------------------------------------------------------------------------------------------
+// MoE routing and expert combination
+
+// one wave per row: the row sum accumulated in double (ggml's generic row sum)
+__global__ void sum_rows_kernel(tview a, tview d, int64_t rows) {
+    const int64_t r = (int64_t) blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+    const int lane = threadIdx.x % WAVE;
+    if (r >= rows) return;
+    const int64_t i1 = r % a.ne[1], i2 = (r / a.ne[1]) % a.ne[2], i3 = r / (a.ne[1] * a.ne[2]);
+    double sum = 0.0;
+    for (int64_t i0 = lane; i0 < a.ne[0]; i0 += WAVE) sum += (double) ld(at(a, i0, i1, i2, i3), a.type);
+    sum = wave_sum_d(sum);
+    if (lane == 0) st(at(d, 0, i1, i2, i3), d.type, (float) sum);
+}
+
+void launch_sum_rows(const tview & a, const tview & dst, hipStream_t st) {
+    const int64_t rows = a.ne[1] * a.ne[2] * a.ne[3];
+    if (rows == 0) return;
+    launch(sum_rows_kernel, dim3(grid1(rows, 4)), dim3(256), 0, st, a, dst, rows);
+}
+
+// one workgroup per row: element i goes to position rank(i) = the number of elements ordered before
+// it, where equal values order by ascending index (a stable sort; the router's tie rule)
+__global__ __launch_bounds__(256) void argsort_kernel(tview a, tview d, int desc) {
+    extern __shared__ float s_row[];
+    const int64_t r = blockIdx.x;
+    const int64_t i1 = r % a.ne[1], i2 = (r / a.ne[1]) % a.ne[2], i3 = r / (a.ne[1] * a.ne[2]);
+    const int n = (int) a.ne[0];
+    for (int i = threadIdx.x; i < n; i += blockDim.x) s_row[i] = ld(at(a, i, i1, i2, i3), a.type);
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = s_row[i];
+        int rank = 0;
+        for (int j = 0; j < n; j++) {
+            const float u = s_row[j];
+            rank += (desc ? u > v : u < v) || (u == v && j < i);
+        }
+        *(int32_t *) at(d, rank, i1, i2, i3) = i;
+    }
+}
+
+void launch_argsort(const tview & a, const tview & dst, bool desc, hipStream_t st) {
+    const int64_t rows = a.ne[1] * a.ne[2] * a.ne[3];
+    if (a.ne[0] > ARGSORT_MAX_ROW) HIP_ABORT("argsort: rows of %lld exceed %d", (long long) a.ne[0], ARGSORT_MAX_ROW);
+    if (rows == 0) return;
+    launch(argsort_kernel, dim3((unsigned) rows), dim3(256), (size_t) a.ne[0] * sizeof(float), st, a, dst, desc ? 1 : 0);
+}
+
+// out[:, t] = ((e[:, 0, t] * w[0, t] + e[:, 1, t] * w[1, t]) + ...) (+ res[:, t]): the graph's
+// mul by the routing weights, its chain of adds over the slots in order, and the residual add
+__global__ void moe_wsum_kernel(moe_wsum M) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t t = blockIdx.y;
+    if (i >= M.n_embd) return;
+    const float * e = M.e + t * M.e_nb2 + i;
+    const float * w = M.w + t * M.w_nb2;
+    float acc = e[0] * w[0];
+    for (int s = 1; s < M.k; s++) acc = acc + e[s * M.e_nb1] * w[s * M.w_nb1];
+    if (M.res) acc = acc + M.res[t * M.res_nb1 + i];
+    M.out[t * M.out_nb1 + i] = acc;
+}
+
+void launch_moe_wsum(const moe_wsum & M, hipStream_t st) {
+    launch(moe_wsum_kernel, dim3(grid1(M.n_embd, 256), (unsigned) M.n_tok), dim3(256), 0, st, M);
 }
 
 __global__ void unary_kernel(int op, float s, tview a, tview d, int64_t n) {

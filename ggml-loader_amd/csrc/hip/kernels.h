@@ -105,6 +105,15 @@ struct gemv_launch {
     const int32_t * xs;    // q8: block sums
     const int16_t * xbs;   // q8K: 16-wise sums
     gemv_norm  norm;
+    // ggml_mul_mat_id: grid column c is (token c / n_slots, slot c % n_slots); it reads the rows of
+    // expert ids[token * ids_stride + slot] (expert e's rows begin e * expert_rows rows into every
+    // matrix; ids are clamped to [0, n_experts)) and activation column token * x_cols + slot % x_cols
+    const int32_t * ids;   // nullptr: a plain GEMV
+    int64_t    ids_stride;
+    int        n_slots;
+    int        x_cols;
+    int        n_experts;
+    int64_t    expert_rows;
     // SwiGLU epilogue: m[0] = gate, m[1] = up (same n_rows); writes act = silu(g) * u to m[0].y
     bool       swiglu;
 };
@@ -164,6 +173,22 @@ struct rope_batch {
 void launch_rope_batch(rope_batch & B, hipStream_t st);
 
 void launch_soft_max(const tview & a, const tview * mask, const tview & dst, float scale, float max_bias, hipStream_t st);
+
+// ---------------------------------------------------------------------------------------------
+// MoE routing and expert combination
+void launch_sum_rows(const tview & a, const tview & dst, hipStream_t st);
+constexpr int ARGSORT_MAX_ROW = 16384;
+void launch_argsort(const tview & a, const tview & dst, bool desc, hipStream_t st);
+// out[:, t] = sum over slots s in order of e[:, s, t] * w[s, t] (+ res[:, t]); strides in floats
+struct moe_wsum {
+    const float * e;   int64_t e_nb1, e_nb2;
+    const float * w;   int64_t w_nb1, w_nb2;
+    const float * res; int64_t res_nb1;
+    float *       out; int64_t out_nb1;
+    int64_t n_embd, n_tok;
+    int k;
+};
+void launch_moe_wsum(const moe_wsum & M, hipStream_t st);
 void launch_argmax(const tview & a, int32_t * out, hipStream_t st);
 
 // generic F32/F16/BF16 mul_mat (src0 rows contiguous): one wave per output element

@@ -417,8 +417,30 @@ static built_graph build_graph(struct ggml_context * ctx, const model & m, const
 
 static struct ggml_tensor * build_moe_ffn(struct ggml_context * ctx, const hparams & hp, const layer_weights & l,
                                           struct ggml_tensor * y, int64_t n_new, built_graph & bg) {
-    (void) ctx; (void) hp; (void) l; (void) y; (void) n_new; (void) bg;
-    throw gl_error("qwen3moe expert FFN graph is not available in this build yet");
+    (void) bg;
+    const int64_t n_embd = hp.n_embd, n_expert = hp.n_expert, k = hp.n_expert_used;
+    // router: logits [n_expert, n_new] from the f32 router, softmax over all experts
+    struct ggml_tensor * probs = ggml_soft_max_ext(ctx, ggml_mul_mat(ctx, l.ffn_gate_inp, y), nullptr, 1.0f, 0.0f);
+    // top-k by probability (stable: an earlier expert wins a tie), then their probabilities,
+    // renormalized to sum to one
+    struct ggml_tensor * selected = ggml_top_k(ctx, probs, (int) k);                          // I32 [k, n_new]
+    struct ggml_tensor * w = ggml_get_rows(ctx, ggml_reshape_3d(ctx, probs, 1, n_expert, n_new), selected);  // [1, k, n_new]
+    w = ggml_reshape_2d(ctx, w, k, n_new);
+    w = ggml_div(ctx, w, ggml_sum_rows(ctx, w));
+    w = ggml_reshape_3d(ctx, w, 1, k, n_new);
+    // experts: gate/up on the token's activation, SwiGLU, down on each slot's activation
+    struct ggml_tensor * x = ggml_reshape_3d(ctx, y, n_embd, 1, n_new);
+    struct ggml_tensor * gate = ggml_mul_mat_id(ctx, l.ffn_gate_exps, x, selected);           // [n_ff_exp, k, n_new]
+    struct ggml_tensor * up = ggml_mul_mat_id(ctx, l.ffn_up_exps, x, selected);
+    struct ggml_tensor * act = ggml_mul(ctx, ggml_silu(ctx, gate), up);
+    struct ggml_tensor * experts = ggml_mul_mat_id(ctx, l.ffn_down_exps, act, selected);     // [n_embd, k, n_new]
+    experts = ggml_mul(ctx, experts, w);
+    // out = w_0 down_0 + w_1 down_1 + ... in slot order
+    struct ggml_tensor * out = ggml_view_2d(ctx, experts, n_embd, n_new, experts->nb[2], 0);
+    for (int64_t i = 1; i < k; i++) {
+        out = ggml_add(ctx, out, ggml_view_2d(ctx, experts, n_embd, n_new, experts->nb[2], (size_t) i * experts->nb[1]));
+    }
+    return out;
 }
 
 // model.cpp:1476-1494

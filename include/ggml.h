@@ -94,6 +94,9 @@ enum ggml_op {
     GGML_OP_FLASH_ATTN_EXT,
     GGML_OP_ARGMAX,
     GGML_OP_UNARY,
+    GGML_OP_DIV,
+    GGML_OP_SUM_ROWS,
+    GGML_OP_ARGSORT,
     GGML_OP_COUNT,
 };
 
@@ -249,6 +252,21 @@ GGML_API struct ggml_tensor * ggml_flash_attn_ext(struct ggml_context * ctx, str
 
 // index of the max of each row (first max wins) -> I32 [a->ne[1]]
 GGML_API struct ggml_tensor * ggml_argmax(struct ggml_context * ctx, struct ggml_tensor * a);
+
+// ---- MoE routing (the router of qwen_model.c:551-606 as graph ops) ----
+enum ggml_sort_order {
+    GGML_SORT_ORDER_ASC,
+    GGML_SORT_ORDER_DESC,
+};
+// a / b, b repeated over a (like ggml_mul)
+GGML_API struct ggml_tensor * ggml_div(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b);
+// F32 [1, ne1, ne2, ne3]: the sum of each row
+GGML_API struct ggml_tensor * ggml_sum_rows(struct ggml_context * ctx, struct ggml_tensor * a);
+// I32, same shape: the indices that sort each row; equal values keep ascending index order (the
+// router's rule: an earlier expert wins a tie)
+GGML_API struct ggml_tensor * ggml_argsort(struct ggml_context * ctx, struct ggml_tensor * a, enum ggml_sort_order order);
+// I32 [k, ne1, ne2, ne3]: a view of the first k columns of ggml_argsort(a, DESC)
+GGML_API struct ggml_tensor * ggml_top_k(struct ggml_context * ctx, struct ggml_tensor * a, int k);
 
 // ---- graph (model.cpp:1300, 1413-1414, 1472) ----
 GGML_API struct ggml_cgraph * ggml_new_graph(struct ggml_context * ctx);

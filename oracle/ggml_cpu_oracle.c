@@ -718,7 +718,7 @@ static void op_binary(struct ggml_tensor * dst, const struct ggml_tensor * a, co
         for (int64_t i0 = 0; i0 < a->ne[0]; i0++) {
             const float x = load_f(a, ELEM(a, i0, i1, i2, i3));
             const float y = load_f(b, ELEM(b, i0 % b->ne[0], i1 % b->ne[1], i2 % b->ne[2], i3 % b->ne[3]));
-            store_f(dst, ELEM(dst, i0, i1, i2, i3), op == GGML_OP_ADD ? x + y : x * y);
+            store_f(dst, ELEM(dst, i0, i1, i2, i3), op == GGML_OP_ADD ? x + y : op == GGML_OP_MUL ? x * y : x / y);
         }
     }
 }
@@ -935,6 +935,40 @@ static void op_argmax(struct ggml_tensor * dst, const struct ggml_tensor * a) {
     }
 }
 
+/* sum of each row, accumulated in double (ggml's generic ggml_vec_sum_f32) */
+static void op_sum_rows(struct ggml_tensor * dst, const struct ggml_tensor * a) {
+    for (int64_t i3 = 0; i3 < a->ne[3]; i3++)
+    for (int64_t i2 = 0; i2 < a->ne[2]; i2++)
+    for (int64_t i1 = 0; i1 < a->ne[1]; i1++) {
+        ggml_float sum = 0.0;
+        for (int64_t i0 = 0; i0 < a->ne[0]; i0++) sum += (ggml_float) load_f(a, ELEM(a, i0, i1, i2, i3));
+        store_f(dst, ELEM(dst, 0, i1, i2, i3), (float) sum);
+    }
+}
+
+/* indices that sort each row, equal values in ascending index order: the tie rule of the router's
+   top-k insertion (qwen_model.c:577-590, an earlier expert wins). Insertion sort: stable. */
+static void op_argsort(struct ggml_tensor * dst, const struct ggml_tensor * a) {
+    const int desc = dst->op_params[0] == GGML_SORT_ORDER_DESC;
+    const int64_t n = a->ne[0];
+    for (int64_t i3 = 0; i3 < a->ne[3]; i3++)
+    for (int64_t i2 = 0; i2 < a->ne[2]; i2++)
+    for (int64_t i1 = 0; i1 < a->ne[1]; i1++) {
+        int32_t * out = (int32_t *) ELEM(dst, 0, i1, i2, i3);
+        for (int64_t i = 0; i < n; i++) {
+            const float v = load_f(a, ELEM(a, i, i1, i2, i3));
+            int64_t j = i;
+            while (j > 0) {
+                const float u = load_f(a, ELEM(a, out[j - 1], i1, i2, i3));
+                if (desc ? !(u < v) : !(u > v)) break;
+                out[j] = out[j - 1];
+                j--;
+            }
+            out[j] = (int32_t) i;
+        }
+    }
+}
+
 static void compute_node(struct ggml_tensor * t, int nth) {
     switch (t->op) {
         case GGML_OP_NONE: case GGML_OP_RESHAPE: case GGML_OP_VIEW: case GGML_OP_PERMUTE: case GGML_OP_TRANSPOSE:
@@ -943,7 +977,9 @@ static void compute_node(struct ggml_tensor * t, int nth) {
         case GGML_OP_CPY: op_dup(t, t->src[0], nth); return;
         case GGML_OP_GET_ROWS: op_get_rows(t, t->src[0], t->src[1], nth); return;
         case GGML_OP_RMS_NORM: op_rms_norm(t, t->src[0], nth); return;
-        case GGML_OP_ADD: case GGML_OP_MUL: op_binary(t, t->src[0], t->src[1], nth); return;
+        case GGML_OP_ADD: case GGML_OP_MUL: case GGML_OP_DIV: op_binary(t, t->src[0], t->src[1], nth); return;
+        case GGML_OP_SUM_ROWS: op_sum_rows(t, t->src[0]); return;
+        case GGML_OP_ARGSORT: op_argsort(t, t->src[0]); return;
         case GGML_OP_SCALE: case GGML_OP_SQR: case GGML_OP_UNARY: op_unary(t, t->src[0], nth); return;
         case GGML_OP_SOFT_MAX: op_soft_max(t, t->src[0], t->src[1], nth); return;
         case GGML_OP_ROPE: op_rope(t, t->src[0], t->src[1], t->src[2], nth); return;

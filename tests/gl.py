@@ -232,10 +232,34 @@ def attention_graph(g, hd, n_head, n_head_kv, n_kv, n_new, n_ctx, kc, vc, q, mas
     return g.cont_2d(g.permute(KQV, 0, 2, 1, 3), hd * n_head, n_new)
 
 
+def moe_ffn_graph(g, y, router, gate_exps, up_exps, down_exps, k, residual=None):
+    """The routed expert FFN of model.cpp's build_moe_ffn (softmax router, top-k, renormalized
+    weights, mul_mat_id gate/up/down with SiLU, weighted sum over the slots in order)."""
+    core = gl.libs()["core"]
+    tt = lambda t: t.contents
+    n_embd, n_tok = tt(y).ne[0], tt(y).ne[1]
+    n_expert = tt(router).ne[1]
+    probs = g.soft_max_ext(g.mul_mat(router, y), None, 1.0, 0.0)
+    sel = g.top_k(probs, k)
+    w = g.get_rows(g.reshape_3d(probs, 1, n_expert, n_tok), sel)
+    w = g.reshape_2d(w, k, n_tok)
+    w = g.div(w, g.sum_rows(w))
+    w = g.reshape_3d(w, 1, k, n_tok)
+    x = g.reshape_3d(y, n_embd, 1, n_tok)
+    act = g.mul(g.silu(g.mul_mat_id(gate_exps, x, sel)), g.mul_mat_id(up_exps, x, sel))
+    experts = g.mul(g.mul_mat_id(down_exps, act, sel), w)
+    nb1, nb2 = tt(experts).nb[1], tt(experts).nb[2]
+    out = g.view_2d(experts, n_embd, n_tok, nb2, 0)
+    for i in range(1, k):
+        out = g.add(out, g.view_2d(experts, n_embd, n_tok, nb2, i * nb1))
+    return g.add(out, residual) if residual is not None else out
+
+
 # ---- node-by-node capture (debugging / parity localization) ----
 EVAL_CB = C.CFUNCTYPE(C.c_bool, gl.T, C.c_bool, C.c_void_p)
 OP_NAMES = ["NONE", "DUP", "ADD", "MUL", "SCALE", "SQR", "RMS_NORM", "MUL_MAT", "MUL_MAT_ID", "CPY", "CONT", "RESHAPE",
-            "VIEW", "PERMUTE", "TRANSPOSE", "GET_ROWS", "SOFT_MAX", "ROPE", "FLASH_ATTN_EXT", "ARGMAX", "UNARY"]
+            "VIEW", "PERMUTE", "TRANSPOSE", "GET_ROWS", "SOFT_MAX", "ROPE", "FLASH_ATTN_EXT", "ARGMAX", "UNARY",
+            "DIV", "SUM_ROWS", "ARGSORT"]
 NOOP = {"NONE", "RESHAPE", "VIEW", "PERMUTE", "TRANSPOSE"}
 
 

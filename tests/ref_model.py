@@ -15,6 +15,9 @@ Per layer (model.cpp:1318-1467):
     h = rms_norm(x) * ffn_norm
     x = x + W_down (silu(W_gate h) * W_up h)       (phi3: gate/up = halves of W_up h, :1116-1121)
 Head: logits = W_out (rms_norm(x) * output_norm), W_out = token_embd when output.weight is absent.
+MoE FFN (qwen3moe; the routing of qwen_model.c:551-606 and the expert sum of :608-734):
+    p = softmax(W_router h); the k experts of largest p (an earlier expert wins a tie);
+    w = p_sel / sum(p_sel); x = x + sum_k w_k W_down[e_k] (silu(W_gate[e_k] h) * W_up[e_k] h)
 """
 import numpy as np
 
@@ -48,6 +51,7 @@ class RefModel:
         self.n_ff = kv("feed_forward_length")
         self.eps = kv("attention.layer_norm_rms_epsilon")
         self.base = kv("rope.freq_base", 10000.0)
+        self.n_expert_used = kv("expert_used_count", 0)
         self.neox = (a != "llama") if rope_mode is None else rope_mode == "neox"
         self.gqa = gqa or (lambda h, G, hkv: h // G)
         self.w = {n: _dequant(*g.raw(n)) for n in g.tensors}
@@ -73,7 +77,29 @@ class RefModel:
             y[..., 0:n_rot:2], y[..., 1:n_rot:2] = a * c - b * s, a * s + b * c
         return y
 
+    def moe(self, p, h):
+        W = self.w
+        out = np.zeros_like(h)
+        for t in range(h.shape[0]):
+            logits = W[p + "ffn_gate_inp.weight"] @ h[t]
+            e = np.exp(logits - logits.max())
+            probs = e / e.sum()
+            order = sorted(range(len(probs)), key=lambda i: (-probs[i], i))
+            sel = order[: self.n_expert_used]
+            # relative gap between the last selected expert and the first one left out
+            gap = (probs[order[self.n_expert_used - 1]] - probs[order[self.n_expert_used]]) / probs[order[self.n_expert_used - 1]]
+            self.route_margin = min(self.route_margin, gap)
+            wk = probs[sel] / probs[sel].sum()
+            for k, ex in enumerate(sel):
+                g = W[p + "ffn_gate_exps.weight"][ex] @ h[t]
+                u = W[p + "ffn_up_exps.weight"][ex] @ h[t]
+                out[t] += wk[k] * (W[p + "ffn_down_exps.weight"][ex] @ (g / (1 + np.exp(-g)) * u))
+        return out
+
     def forward(self, n_past, tokens):
+        """Logits of the last token; route_margin is then the smallest relative gap between the
+        k-th and (k+1)-th expert probability over the step's MoE layers (inf without MoE)."""
+        self.route_margin = float("inf")
         W = self.w
         H, Hkv, d = self.n_head, self.n_head_kv, self.hd
         tokens = np.asarray(tokens)
@@ -109,6 +135,9 @@ class RefModel:
                     out[t, hh] = (e / e.sum()) @ V[:n_kv, kv]
             x = x + out.reshape(n_new, H * d) @ W[p + "attn_output.weight"].T
             h = self.rms(x, W[p + "ffn_norm.weight"], self.eps)
+            if p + "ffn_gate_inp.weight" in W:
+                x = x + self.moe(p, h)
+                continue
             if p + "ffn_gate.weight" in W:
                 gate, up = h @ W[p + "ffn_gate.weight"].T, h @ W[p + "ffn_up.weight"].T
             else:

@@ -25,6 +25,9 @@ TINY = {
                   n_vocab=900, rope_theta=1e6, wtype=gl.Q8_0),
     "phi3": dict(arch="phi3", n_embd=384, n_layer=2, n_head=4, n_head_kv=4, head_dim=96, n_ff=512,
                  n_vocab=700, wtype=gl.Q8_0),
+    "qwen3moe": dict(arch="qwen3moe", n_embd=512, n_layer=2, n_head=8, n_head_kv=2, head_dim=64, n_ff=512,
+                     n_vocab=800, n_expert=32, n_expert_used=8, n_ff_exp=256, rope_theta=1e6, rms_eps=1e-6,
+                     wtype=gl.Q4_K),
 }
 
 

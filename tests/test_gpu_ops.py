@@ -11,7 +11,7 @@ rel_err in gl.py), the ggml test-backend-ops bar for that op.
 import numpy as np
 import pytest
 
-from gl import Graph, attention_graph, cpu_backend, gl, quantize, rel_err, run_on
+from gl import Graph, attention_graph, cpu_backend, gl, moe_ffn_graph, quantize, rel_err, run_on
 
 pytestmark = pytest.mark.gpu
 
@@ -380,3 +380,44 @@ def test_attention_f16_probability_ties(hip, cpu):
     for fusion in (True, False):
         a, b = both(hip, cpu, build, fusion)
         assert np.array_equal(a, b), (fusion, t, rel_err(a, b))
+
+
+# ---- MoE --------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [8, 128, 1000])
+def test_argsort_sum_rows_div(hip, cpu, n):
+    x = rng(60 + n).integers(-4, 5, (3, n)).astype(np.float32) * 0.5     # ties
+    x[1] = rng(61).standard_normal(n).astype(np.float32)
+
+    def build(g):
+        xt = g.tensor(gl.F32, n, 3, data=x)
+        s = g.sum_rows(xt)
+        return [g.argsort(xt, gl.SORT_DESC), g.argsort(xt, gl.SORT_ASC), s, g.div(xt, s)]
+
+    hs, cs = both(hip, cpu, build)
+    for a, b in zip(hs, cs):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(hs[0].view(np.int32).reshape(3, n), np.argsort(-x, axis=1, kind="stable"))
+
+
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K])
+@pytest.mark.parametrize("n_tok", [1, 3])
+def test_moe_ffn(hip, cpu, qtype, n_tok):
+    """The routed expert FFN (router, top-k, renormalized weights, mul_mat_id gate/up/down, SwiGLU,
+    weighted slot sum, residual): fused into the GEMV and weighted-sum kernels or node by node."""
+    n_embd, E, k, ff = 512, 32, 8, 256
+    r = rng(70)
+    y = r.standard_normal((n_tok, n_embd)).astype(np.float32)
+    res = r.standard_normal((n_tok, n_embd)).astype(np.float32)
+    router = (r.standard_normal((E, n_embd)) * 0.05).astype(np.float32)
+    wg, wu = (qweight(qtype, n_embd, E * ff, s, std=0.05) for s in (71, 72))
+    wd = qweight(qtype, ff, E * n_embd, 73, std=0.05)
+
+    def build(g):
+        return moe_ffn_graph(g, g.tensor(gl.F32, n_embd, n_tok, data=y), g.tensor(gl.F32, n_embd, E, data=router),
+                             g.tensor(qtype, n_embd, ff, E, data=wg), g.tensor(qtype, n_embd, ff, E, data=wu),
+                             g.tensor(qtype, ff, n_embd, E, data=wd), k, g.tensor(gl.F32, n_embd, n_tok, data=res))
+
+    for fusion in (True, False):
+        a, b = both(hip, cpu, build, fusion)
+        assert np.array_equal(a, b), (fusion, rel_err(a, b))

@@ -443,3 +443,56 @@ def test_moe_route_brute_force():
         ref = e[order] / e[order].sum()
         assert np.allclose(w, ref, rtol=1e-6, atol=0)
         assert abs(float(w.astype(np.float64).sum()) - 1.0) < 1e-6
+
+
+# ---- MoE routing ops and mul_mat_id ----------------------------------------------------------
+
+def test_argsort_is_stable_and_top_k_is_its_prefix(cpu):
+    x = rng(40).integers(-3, 4, (6, 50)).astype(np.float32)     # many ties
+    for order in (gl.SORT_ASC, gl.SORT_DESC):
+        got = run_cpu(cpu, lambda g: g.argsort(g.tensor(gl.F32, 50, 6, data=x), order)).view(np.int32).reshape(6, 50)
+        expect = np.argsort(x if order == gl.SORT_ASC else -x, axis=1, kind="stable")
+        assert np.array_equal(got, expect), order
+
+
+def test_sum_rows_and_div(cpu):
+    x = (rng(41).standard_normal((5, 37)) * 3).astype(np.float32)
+    s = run_cpu(cpu, lambda g: g.sum_rows(g.tensor(gl.F32, 37, 5, data=x)))
+    assert np.array_equal(s, x.astype(np.float64).sum(1).astype(np.float32))
+    d = run_cpu(cpu, lambda g: g.div(g.tensor(gl.F32, 37, 5, data=x), g.tensor(gl.F32, 1, 5, data=s)))
+    assert np.array_equal(d.reshape(5, 37), x / s[:, None])
+
+
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q4_K])
+def test_mul_mat_id_brute_force(cpu, qtype):
+    """dst[:, s, t] = W[ids[s, t]] . x[:, s % x_cols, t] on the activation ggml quantizes"""
+    K, N, E, k, T = 512, 48, 6, 3, 2
+    W = quantize((rng(42).standard_normal((E, N, K)) * 0.05).astype(np.float32), qtype)
+    Wd = dequantize(W, qtype, E * N * K).reshape(E, N, K).astype(np.float64)
+    ids = np.array([[4, 0, 4], [1, 5, 2]], dtype=np.int32)          # [T][k]: repeats allowed
+    for x_cols in (1, k):
+        x = rng(43 + x_cols).standard_normal((T, x_cols, K)).astype(np.float32)
+        got = run_cpu(cpu, lambda g: g.mul_mat_id(g.tensor(qtype, K, N, E, data=W), g.tensor(gl.F32, K, x_cols, T, data=x),
+                                                   g.tensor(gl.I32, k, T, data=ids))).reshape(T, k, N)
+        for t in range(T):
+            for s in range(k):
+                ref = Wd[ids[t, s]] @ act_dequant(x[t, s % x_cols], qtype)
+                assert rel_err(got[t, s], ref) < 2e-6
+
+
+def test_moe_ffn_graph_routing(cpu):
+    """The graph's router picks the experts of largest probability (ties to the lower id) and
+    renormalizes their weights: with a one-hot expert FFN the output exposes both."""
+    n_embd, E, k, ff = 256, 8, 3, 256
+    y = rng(44).standard_normal((1, n_embd)).astype(np.float32)
+    router = (rng(45).standard_normal((E, n_embd)) * 0.1).astype(np.float32)
+    logits = router.astype(np.float64) @ y[0].astype(np.float64)
+    with Graph() as g:
+        yt = g.tensor(gl.F32, n_embd, 1, data=y)
+        rt = g.tensor(gl.F32, n_embd, E, data=router)
+        probs = g.soft_max_ext(g.mul_mat(rt, yt), None, 1.0, 0.0)
+        sel = g.argsort(probs, gl.SORT_DESC)
+        p, order = g.compute(cpu, [probs, sel])
+    order = order.view(np.int32)
+    assert order[:k].tolist() == sorted(range(E), key=lambda i: (-logits[i], i))[:k]
+    assert np.allclose(p, np.exp(logits - logits.max()) / np.exp(logits - logits.max()).sum(), rtol=1e-6)
