@@ -28,8 +28,8 @@ GGML_API ggml_backend_buffer_type_t ggml_backend_hip_buffer_type(int device);
 // decode attention). On by default; off runs one kernel per ggml node. Used by the parity tests
 // to check both paths against the oracle.
 GGML_API void ggml_backend_hip_set_fusion(ggml_backend_t backend, bool enable);
-// Replays the per-token launch sequence through a HIP graph when the ggml graph's structure is
-// unchanged from the previous call. On by default.
+// Reserved for replaying the per-token launch sequence through a captured HIP graph. This build
+// stores the flag and launches every kernel from the host either way.
 GGML_API void ggml_backend_hip_set_graph_replay(ggml_backend_t backend, bool enable);
 
 // Per-kernel timing with HIP events recorded on the backend's own stream. While enabled, every
