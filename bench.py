@@ -132,6 +132,47 @@ def copy_kernel(gl, mb, reps):
                       "GB/s": round(2 * n * 4 * reps / dt / 1e9, 1)}), flush=True)
 
 
+def prefill_bench(gl, args):
+    """--prefill N: one forward_step of N prompt tokens at position 0 per step (the reference's
+    prefill of a 512-token prompt for the phi3 config, model.cpp:1624-1657, which calls forward_step
+    once for the hip backend). Prints its own JSON line; the default run's line is the decode metric."""
+    cfg = gl.CONFIGS[args.config]
+    wname = {gl.Q4_0: "q4_0", gl.Q8_0: "q8_0", gl.Q4_K: "q4_K"}[cfg["wtype"]]
+    model_path = os.path.join(args.model_dir, f"{args.config}_{wname}_seed{args.seed}.gguf")
+    ensure_model(gl, model_path, args.config, args.seed)
+    import numpy as np
+    n = args.prefill
+    tokens = np.random.default_rng(args.seed).integers(0, cfg["n_vocab"], n).astype(np.int32)
+    hipl = gl.libs()["hip"]
+    with gl.Session(model_path, "hip", n_ctx=n) as s:
+        for _ in range(args.warmup):
+            s.forward(0, tokens)
+        t = time.perf_counter()
+        for _ in range(args.steps):
+            s.forward(0, tokens)
+        secs = time.perf_counter() - t
+        hipl.ggml_backend_hip_set_profile_filter(s.backend, b"")
+        hipl.ggml_backend_hip_reset_profile(s.backend)
+        hipl.ggml_backend_hip_set_profiling(s.backend, True)
+        s.forward(0, tokens)
+        hipl.ggml_backend_hip_set_profiling(s.backend, False)
+        prof = gl.profile(s.backend)
+    ms_step = 1000 * secs / args.steps
+    log(f"[bench] prefill {n}: {args.steps} steps in {secs:.4f}s -> {n / (secs / args.steps):.1f} tok/s ({ms_step:.3f} ms/step)")
+    total_ms = sum(v[1] for v in prof.values())
+    breakdown = {}
+    for k, (cnt, ms, by) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
+        log(f"[bench]   {k:22s} {cnt:5d} launches {ms / cnt * 1e3:10.2f} us/launch {100 * ms / total_ms:5.1f}%")
+        breakdown[k] = {"launches": cnt, "us_per_launch": round(ms / cnt * 1e3, 2), "ms": round(ms, 3)}
+    print(json.dumps({
+        "metric": f"prefill tokens/s ({n}-token prompt)", "value": round(n / (secs / args.steps), 1), "unit": "tok/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True, "data": f"synthetic (seeded random-init weights quantized to {wname.upper()})",
+        "config": {"workload": f"{args.config}: prefill of {n} tokens at position 0", "n_tokens": n},
+        "kernel_ms_per_step": {k: v["ms"] for k, v in breakdown.items()},
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -139,6 +180,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="llama3b")
     ap.add_argument("--n-past", type=int, default=2048)
+    ap.add_argument("--prefill", type=int, default=0, help="time forward_step over this many prompt tokens instead")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--model-dir", default=os.environ.get("GL_BENCH_DIR", "/tmp/gl_bench"))
     ap.add_argument("--breakdown-steps", type=int, default=10, help="untimed steps with every kernel timed")
@@ -164,6 +206,9 @@ def main():
         raise SystemExit("bench.py: no HIP device")
     if args.copy_mb:
         copy_kernel(gl, args.copy_mb, args.steps)
+        return
+    if args.prefill:
+        prefill_bench(gl, args)
         return
     cfg = gl.CONFIGS[args.config]
     wname = {gl.Q4_0: "q4_0", gl.Q8_0: "q8_0", gl.Q4_K: "q4_K"}[cfg["wtype"]]

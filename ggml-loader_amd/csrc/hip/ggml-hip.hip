@@ -676,11 +676,11 @@ private:
                     if (m->ne[1] == rows && norm_deferrable(u, N) && ((uintptr_t) x->data | (uintptr_t) w->data) % 16 == 0) {
                         const gemv_norm nz{ (const float *) x->data, N, (const float *) w->data, eps, 1 };
                         done_[u] = true;
-                        if (max_consumer_rows(u) <= GEMV_PROLOGUE_MAX_ROWS) {
+                        if (max_consumer_rows(u) <= GEMV_PROLOGUE_MAX_ROWS && !gemm_consumer(u)) {
                             norm_[m] = nz;      // every consumer workgroup normalizes for itself
                             return;
                         }
-                        // a very wide consumer (the LM head): normalize and quantize once
+                        // a very wide consumer (the LM head) or a GEMM: normalize and quantize once
                         const int wtype = gemv_only_consumers(u);
                         const int kind = dot_kind(wtype);
                         act_entry e = alloc_act(kind, N, rows);
@@ -738,10 +738,65 @@ private:
         return is_2d_contig(mm);
     }
 
+    // a quantized mul_mat over a prefill-width batch: the int8-MFMA GEMM (same floats as the GEMV)
+    bool gemm_route(const ggml_tensor * mm) const {
+        return mm->op == GGML_OP_MUL_MAT && mm->src[1]->ne[1] >= GEMM_MIN_COLS && gemv_capable(mm) &&
+               gemm_supported(mm->src[0]->type, mm->src[0]->ne[0], mm->src[0]->ne[1]) &&
+               (mm->nb[1] / sizeof(float)) % 4 == 0 && ((uintptr_t) mm->data) % 16 == 0;
+    }
+    bool gemm_consumer(int u) const {
+        for (int j : users_[u]) if (gemm_route(g_->nodes[j])) return true;
+        return false;
+    }
+
+    void op_gemm(int i) {
+        ggml_tensor * n = g_->nodes[i];
+        const ggml_tensor * w = n->src[0];
+        const ggml_tensor * x = n->src[1];
+        const act_entry * xa = ensure_act(x, 1);
+        gemm_launch G{};
+        G.type = w->type;
+        G.K = w->ne[0];
+        G.n_rows = w->ne[1];
+        G.ncols = x->ne[1];
+        const planes p = planes_of(w);
+        G.w = p.qs + p.first_block * qs_bytes_of(w->type);
+        G.wd = p.d + p.first_block;
+        G.xq = xa->q8.qs;
+        G.xd = xa->q8.d;
+        G.y = (float *) n->data;
+        G.y_stride = (int64_t) (n->nb[1] / sizeof(float));
+        double bytes = (double) ggml_nbytes(w) + (double) (G.K * G.ncols) * (1.0 + 4.0 / 32) + (double) (G.n_rows * G.ncols * 4);
+        ggml_tensor * written = n;
+        const int u = fuse(FUSE_ADD) ? sole_user(i) : -1;
+        if (u >= 0) {
+            ggml_tensor * an = g_->nodes[u];
+            if (an->op == GGML_OP_ADD && an->src[0] == n && an->src[1]->type == GGML_TYPE_F32 &&
+                ggml_are_same_shape(an->src[1], n) && is_2d_contig(an->src[1]) && is_2d_contig(an) &&
+                (((uintptr_t) an->data | (uintptr_t) an->src[1]->data) % 16) == 0 &&
+                (an->nb[1] / sizeof(float)) % 4 == 0 && (an->src[1]->nb[1] / sizeof(float)) % 4 == 0) {
+                G.y = (float *) an->data;
+                G.y_stride = (int64_t) (an->nb[1] / sizeof(float));
+                G.add = (const float *) an->src[1]->data;
+                G.add_stride = (int64_t) (an->src[1]->nb[1] / sizeof(float));
+                bytes += (double) (G.n_rows * G.ncols * 4);
+                done_[u] = true;
+                written = an;
+            }
+        }
+        {
+            prof_scope ps(this, w->type == GGML_TYPE_Q4_0 ? "gemm_q4_0" : "gemm_q8_0", bytes);
+            launch_gemm(G, st_);
+        }
+        wrote_.push_back(written);
+        done_[i] = true;
+    }
+
     void op_mul_mat(int i) {
         ggml_tensor * n = g_->nodes[i];
         auto at = attn_.find(i);
         if (at != attn_.end()) { run_attention(at->second); return; }
+        if (gemm_route(n)) { op_gemm(i); return; }
         if (gemv_capable(n)) { op_gemv(i); return; }
         if (ggml_is_quantized(n->src[0]->type)) {
             HIP_ABORT("mul_mat '%s': quantized %s weights with this layout are not supported", n->name, ggml_type_name(n->src[0]->type));

@@ -72,6 +72,29 @@ struct gemv_mat {
     int32_t         n_rows;
 };
 
+// ---------------------------------------------------------------------------------------------
+// prefill GEMM on the int8 matrix cores: y[c][r] = W[r] . x[c] (+ add[c][r]) for Q4_0 / Q8_0
+// weights in the plane layout and Q8_0-quantized activation columns; the same floats as the GEMV.
+constexpr int GEMM_MIN_COLS = 64;   // narrower products stay on the GEMV
+
+struct gemm_launch {
+    int             type;      // GGML_TYPE_Q4_0 / Q8_0
+    int64_t         K;         // row length (a multiple of 128)
+    int64_t         n_rows;    // a multiple of 4
+    int64_t         ncols;
+    const uint8_t * w;         // qs plane of row 0
+    const __half *  wd;        // d plane of row 0
+    const int8_t *  xq;        // activation column c at xq + c * K
+    const float *   xd;        // and its block scales at xd + c * K / 32
+    float *         y;         // output column c at y + c * y_stride
+    int64_t         y_stride;
+    const float *   add;       // optional residual, column c at add + c * add_stride
+    int64_t         add_stride;
+};
+
+bool gemm_supported(int type, int64_t K, int64_t n_rows);
+void launch_gemm(const gemm_launch & G, hipStream_t st);
+
 // Activation prologue of a GEMV: every workgroup quantizes its column of x itself, either as
 // rms_norm(x) * w (rms set: ggml's rms_norm -> mul -> quantize_row_q8_0 / q8_K chain, same
 // roundings) or as x (the activation quantization ggml-cpu applies inside mul_mat).

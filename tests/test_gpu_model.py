@@ -66,6 +66,25 @@ def test_decode_parity_tiny(models, arch, fusion):
             tok = int(np.argmax(lc))
 
 
+@pytest.mark.parametrize("arch", ["llama", "phi3", "qwen2"])
+def test_prefill_parity_long_prompt(models, arch):
+    """A 100-token prompt in one forward_step (the quantized projections run on the prefill GEMM,
+    attention on the graph's own K^T Q -> softmax -> V chain), then decode steps on its KV cache."""
+    prompt = [int(t) for t in np.random.default_rng(11).integers(0, TINY[arch]["n_vocab"], 100)]
+    with gl.Session(models[arch], "hip", n_ctx=128) as h, gl.Session(models[arch], "cpu", n_ctx=128, n_threads=16) as c:
+        lh = h.forward(0, prompt)
+        lc = c.forward(0, prompt)
+        assert np.array_equal(lh, lc), (arch, "prefill", rel_err(lh, lc))
+        n_past = len(prompt)
+        tok = int(np.argmax(lc))
+        for step in range(4):
+            lh = h.forward(n_past, [tok])
+            lc = c.forward(n_past, [tok])
+            assert np.array_equal(lh, lc), (arch, step, rel_err(lh, lc))
+            n_past += 1
+            tok = int(np.argmax(lc))
+
+
 def test_greedy_agreement_256(models):
     """Teacher-forced top-1 agreement over 256 decode steps (tokens from the CPU greedy run)."""
     path = models["llama"]

@@ -105,6 +105,70 @@ def test_gemv(hip, cpu, qtype, K, N, ncols):
     assert np.array_equal(a, b), rel_err(a, b)
 
 
+def profiled(hip, fn):
+    """Runs fn with every kernel timed; returns (fn's result, kernel names launched)."""
+    h = gl.libs()["hip"]
+    h.ggml_backend_hip_set_profile_filter(hip, b"")
+    h.ggml_backend_hip_reset_profile(hip)
+    h.ggml_backend_hip_set_profiling(hip, True)
+    try:
+        out = fn()
+    finally:
+        h.ggml_backend_hip_set_profiling(hip, False)
+    return out, set(gl.profile(hip))
+
+
+@pytest.mark.parametrize("qtype,K,N", [
+    (gl.Q8_0, 3072, 1152),   # phi3 QKV shape, a slice of its rows
+    (gl.Q8_0, 8192, 768),    # the down projection's row length
+    (gl.Q4_0, 3072, 1024),
+    (gl.Q4_0, 256, 100),     # rows end inside a 16-row tile
+    (gl.Q8_0, 128, 4),       # one row group, one 4-block step
+    (gl.Q8_0, 384, 36),
+])
+@pytest.mark.parametrize("ncols", [64, 100, 512])
+def test_gemm_prefill(hip, cpu, qtype, K, N, ncols):
+    """Prefill-width mul_mat on the int8-MFMA GEMM: the same floats as the oracle's block-ordered
+    sums, including partial row and column tiles."""
+    w = qweight(qtype, K, N, K + 3 * N)
+    x = rng(K + ncols).standard_normal((ncols, K)).astype(np.float32)
+
+    def build(g):
+        wt = g.tensor(qtype, K, N, data=w)
+        xt = g.tensor(gl.F32, K, ncols, data=x)
+        return g.mul_mat(wt, xt)
+
+    a, names = profiled(hip, lambda: run_on(hip, build))
+    b = run_on(cpu, build)
+    assert any(n.startswith("gemm_") for n in names), names
+    assert np.array_equal(a, b), rel_err(a, b)
+
+
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0])
+def test_gemm_norm_qkv_residual(hip, cpu, qtype):
+    """rms_norm * w feeding three prefill-width GEMMs (normalized and quantized once), and a GEMM
+    whose residual add is fused into its store."""
+    K, ncols = 512, 96
+    x = rng(30).standard_normal((ncols, K)).astype(np.float32) * 2
+    nw = (1 + 0.01 * rng(31).standard_normal(K)).astype(np.float32)
+    r = rng(32).standard_normal((ncols, K)).astype(np.float32)
+    Wq, Wk, Wv, Wo = (qweight(qtype, K, n, s) for n, s in ((512, 33), (128, 34), (128, 35), (512, 36)))
+
+    def build(g):
+        xt = g.tensor(gl.F32, K, ncols, data=x)
+        y = g.mul(g.rms_norm(xt, 1e-5), g.tensor(gl.F32, K, data=nw))
+        q = g.mul_mat(g.tensor(qtype, K, 512, data=Wq), y)
+        k = g.mul_mat(g.tensor(qtype, K, 128, data=Wk), y)
+        v = g.mul_mat(g.tensor(qtype, K, 128, data=Wv), y)
+        o = g.add(g.mul_mat(g.tensor(qtype, K, K, data=Wo), q), g.tensor(gl.F32, K, ncols, data=r))
+        return [q, k, v, o]
+
+    for fusion in (True, False):
+        hs, cs = both(hip, cpu, build, fusion)
+        for a, b in zip(hs, cs):
+            assert np.array_equal(a, b), (fusion, rel_err(a, b))
+
+
 @pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q4_K])
 def test_gemv_residual_and_qkv_group(hip, cpu, qtype):
     K = 1024
