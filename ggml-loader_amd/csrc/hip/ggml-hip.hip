@@ -1029,6 +1029,13 @@ private:
         return true;
     }
 
+    // the prefill attention kernel: a row of scores fits its LDS, K and V rows 16-byte aligned
+    static bool prefill_attn_ok(int64_t n_kv, int64_t hd, const void * k, size_t k_nb_a, size_t k_nb_b,
+                                const void * v, size_t v_nb_a, size_t v_nb_b) {
+        return n_kv <= attn_prefill_max_kv((int) hd) && ((uintptr_t) k | (uintptr_t) v) % 16 == 0 &&
+               k_nb_a % 16 == 0 && k_nb_b % 16 == 0 && v_nb_a % 16 == 0 && v_nb_b % 16 == 0;
+    }
+
     // K^T Q -> soft_max -> cont(permute(V)) -> V KQ -> permute -> cont  ==>  split-KV attention
     bool match_attention(int i, attn_match & M) const {
         const ggml_tensor * kq = g_->nodes[i];
@@ -1066,8 +1073,10 @@ private:
         if (kp->ne[3] != 1 || qp->ne[3] != 1 || qp->ne[0] != hd) return false;
         if (vp->ne[0] != n_kv || vp->ne[1] != hd || vp->ne[2] != n_head_kv) return false;
         if (kp->nb[0] != 2 || vp->nb[1] != 2 || qp->nb[0] != 4) return false;
-        if (n_q < 1 || n_q > 4 || n_head % n_head_kv || n_head / n_head_kv > 8) return false;
+        if (n_q < 1 || n_head % n_head_kv) return false;
         if (hd != 64 && hd != 96 && hd != 128) return false;
+        if (n_q <= 4 ? n_head / n_head_kv > 8
+                     : !prefill_attn_ok(n_kv, hd, kp->data, kp->nb[1], kp->nb[2], vp->data, vp->nb[0], vp->nb[2])) return false;
         if (ctn->ne[0] != hd * n_head || ctn->ne[1] != n_q) return false;
         const ggml_tensor * mask = smn->src[1];
         if (mask && (mask->ne[0] != n_kv || mask->nb[0] != ggml_type_size(mask->type))) return false;
@@ -1101,16 +1110,19 @@ private:
         A.out_nb1 = (int64_t) (ctn->nb[1] / 4);
         A.n_kv = n_kv; A.n_q = n_q; A.n_head = n_head; A.n_head_kv = n_head_kv; A.hd = hd;
         A.scale = M.scale;
-        A.scratch_bytes = attn_scratch_bytes(n_kv, n_q, n_head, hd);
-        A.scratch = (float *) c_.scratch.alloc((size_t) A.scratch_bytes);
-        if (wanted_act_kind(M.ct) == 1) {
-            act_entry e = alloc_act(1, ctn->ne[0], n_q);
-            A.out_q = e.q8;
-            act_[ctn] = e;
-        }
         const double bytes = (double) n_kv * n_head_kv * hd * 2 * 2 + (double) n_head * hd * n_q * 8 +
                              (mask ? (double) n_kv * n_q * ggml_type_size(mask->type) : 0.0);
-        {
+        if (n_q > 4) {
+            prof_scope ps(this, "attn_prefill", bytes);
+            launch_attn_prefill(A, st_);
+        } else {
+            A.scratch_bytes = attn_scratch_bytes(n_kv, n_q, n_head, hd);
+            A.scratch = (float *) c_.scratch.alloc((size_t) A.scratch_bytes);
+            if (wanted_act_kind(M.ct) == 1) {
+                act_entry e = alloc_act(1, ctn->ne[0], n_q);
+                A.out_q = e.q8;
+                act_[ctn] = e;
+            }
             prof_scope ps(this, "attn_decode", bytes);
             launch_attn_decode(A, st_);
         }
@@ -1128,7 +1140,9 @@ private:
         const int n_kv = (int) k->ne[1], n_head_kv = (int) k->ne[2];
         const bool ok = max_bias == 0.0f && softcap == 0.0f && k->type == GGML_TYPE_F16 && v->type == GGML_TYPE_F16 &&
                         q->type == GGML_TYPE_F32 && q->nb[0] == 4 && k->nb[0] == 2 && v->nb[0] == 2 && v->ne[0] == hd &&
-                        n_q >= 1 && n_q <= 4 && n_head % n_head_kv == 0 && n_head / n_head_kv <= 8 &&
+                        n_q >= 1 && n_head % n_head_kv == 0 &&
+                        (n_q <= 4 ? n_head / n_head_kv <= 8
+                                  : prefill_attn_ok(n_kv, hd, k->data, k->nb[1], k->nb[2], v->data, v->nb[1], v->nb[2])) &&
                         (hd == 64 || hd == 96 || hd == 128) && ggml_is_contiguous(n) &&
                         ((uintptr_t) k->data) % 16 == 0 && k->nb[1] % 16 == 0 && k->nb[2] % 16 == 0 &&
                         ((uintptr_t) v->data) % 4 == 0 && v->nb[1] % 4 == 0 && v->nb[2] % 4 == 0 &&
@@ -1151,9 +1165,14 @@ private:
         A.out_nb1 = (int64_t) (n->nb[2] / 4);
         A.n_kv = n_kv; A.n_q = n_q; A.n_head = n_head; A.n_head_kv = n_head_kv; A.hd = hd;
         A.scale = scale;
+        const double bytes = (double) n_kv * n_head_kv * hd * 2 * 2 + (double) n_head * hd * n_q * 8;
+        if (n_q > 4) {
+            prof_scope ps(this, "attn_prefill", bytes);
+            launch_attn_prefill(A, st_);
+            return;
+        }
         A.scratch_bytes = attn_scratch_bytes(n_kv, n_q, n_head, hd);
         A.scratch = (float *) c_.scratch.alloc((size_t) A.scratch_bytes);
-        const double bytes = (double) n_kv * n_head_kv * hd * 2 * 2 + (double) n_head * hd * n_q * 8;
         prof_scope ps(this, "attn_decode", bytes);
         launch_attn_decode(A, st_);
     }

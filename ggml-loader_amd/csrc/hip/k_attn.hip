@@ -326,3 +326,215 @@ void launch_attn_decode(const attn_launch & A, hipStream_t st) {
         default: HIP_ABORT("attn: unsupported head dim %d", A.hd);
     }
 }
+
+// ---------------------------------------------------------------------------------------------
+// Prefill attention: the same chain arithmetic for a batch of queries (n_q > 4), one workgroup per
+// (tile of APF_Q queries, head), all of a row's scores held in LDS.
+//   scores  K rows staged per 64-position chunk; S[query][pos] from v_mfma_f64_16x16x4f64 over the
+//           head dimension (the F16 operands are exact in double, the sum accumulates in double as
+//           the chain's), rounded to float, times scale, plus mask. A chunk whose mask is -inf for
+//           every query of the tile is not computed: its scores are -inf, as the chain forms them.
+//   stats   per row: M = max, e = exp(s - M), S = sum e in double, p = F16(e * (float)(1/S)).
+//   pv      V rows staged per chunk; out[query][dim] from the f64 MFMA over positions with the F16
+//           p (skipped chunks have p = 0 throughout and add nothing), rounded to float.
+// f64 MFMA 16x16x4 lane layout: A[i][k] at lane i + 16k, B[k][j] at lane j + 16k, D[i][j] in
+// register i / 4 of lane j + 16 (i % 4).
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+constexpr int APF_Q = 16;            // queries per workgroup (one MFMA row tile)
+constexpr int APF_CHUNK = 64;        // positions per staged K / V chunk (one MFMA column tile per wave)
+constexpr int APF_MAX_CHUNKS = 128;  // positions <= 8192
+
+template <int HD>
+constexpr int apf_static_lds() {
+    return (APF_Q + APF_CHUNK) * (HD + 2) * 2 + APF_MAX_CHUNKS * 4;
+}
+
+__host__ __device__ inline int apf_row_stride(int n_kv) {
+    return (n_kv + APF_CHUNK - 1) / APF_CHUNK * APF_CHUNK + 4;   // floats; +4 spreads rows over banks
+}
+
+template <int HD>
+__global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_launch A) {
+    constexpr int KSTR = HD + 2;     // halves per staged row (one dword of padding)
+    constexpr int PIECES = HD / 8;   // 16-byte pieces per row
+    __shared__ __half s_q[APF_Q * KSTR];
+    __shared__ __half s_kv[APF_CHUNK * KSTR];
+    __shared__ int s_live[APF_MAX_CHUNKS];
+    extern __shared__ float s_s[];   // [APF_Q][SS]: scores, then e, then p
+    const int q0 = blockIdx.x * APF_Q, h = blockIdx.y;
+    const int kvh = h / (A.n_head / A.n_head_kv);
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const int n_kv = A.n_kv, n_q = A.n_q;
+    const int SS = apf_row_stride(n_kv);
+    const int n_chunks = (n_kv + APF_CHUNK - 1) / APF_CHUNK;
+    const __half * kbase = A.k + (int64_t) kvh * A.k_nb1;
+    const __half * vbase = A.v + (int64_t) kvh * A.v_nb1;
+
+    // Q tile rounded to F16 (rows past n_q repeat the last query; their results are not stored)
+    for (int i = threadIdx.x; i < APF_Q * HD; i += ATT_THREADS) {
+        const int qi = i / HD, d = i % HD;
+        const int q = min(q0 + qi, n_q - 1);
+        s_q[qi * KSTR + d] = __float2half_rn(A.q[(int64_t) h * A.q_nb1 + (int64_t) q * A.q_nb2 + d]);
+    }
+
+    // rows [t0, t0 + nt) of a cache view into s_kv, zero past nt; every load before the first store
+    auto stage = [&](const __half * base, int64_t nb_pos, int t0, int nt) {
+        constexpr int ITER = (APF_CHUNK * PIECES + ATT_THREADS - 1) / ATT_THREADS;
+        uint4 v[ITER];
+#pragma unroll
+        for (int it = 0; it < ITER; it++) {
+            const int pc = threadIdx.x + it * ATT_THREADS;
+            const int r = pc / PIECES, c = pc % PIECES;
+            v[it] = make_uint4(0, 0, 0, 0);
+            if (pc < APF_CHUNK * PIECES && r < nt) v[it] = *(const uint4 *) (base + (int64_t) (t0 + r) * nb_pos + c * 8);
+        }
+#pragma unroll
+        for (int it = 0; it < ITER; it++) {
+            const int pc = threadIdx.x + it * ATT_THREADS;
+            if (pc >= APF_CHUNK * PIECES) break;
+            const int r = pc / PIECES, c = pc % PIECES;
+            uint32_t * d = (uint32_t *) (s_kv + r * KSTR + c * 8);
+            d[0] = v[it].x; d[1] = v[it].y; d[2] = v[it].z; d[3] = v[it].w;
+        }
+    };
+
+    // ---- scores ----
+    for (int ch = 0; ch < n_chunks; ch++) {
+        const int t0 = ch * APF_CHUNK, nt = min(APF_CHUNK, n_kv - t0);
+        bool any = !A.mask;
+        if (A.mask) {
+            for (int idx = threadIdx.x; idx < APF_Q * APF_CHUNK; idx += ATT_THREADS) {
+                const int qi = idx / APF_CHUNK, t = idx % APF_CHUNK;
+                if (q0 + qi < n_q && t < nt && mask_at(A, q0 + qi, t0 + t) != -INFINITY) any = true;
+            }
+        }
+        const bool live = __syncthreads_or(any);   // also orders the previous chunk's s_kv reads
+        if (threadIdx.x == 0) s_live[ch] = live;
+        if (!live) {
+            for (int idx = threadIdx.x; idx < APF_Q * APF_CHUNK; idx += ATT_THREADS) {
+                const int qi = idx / APF_CHUNK, t = idx % APF_CHUNK;
+                if (t < nt) s_s[qi * SS + t0 + t] = -INFINITY;
+            }
+            continue;
+        }
+        stage(kbase, A.k_nb2, t0, nt);
+        __syncthreads();
+        v4d acc = { 0.0, 0.0, 0.0, 0.0 };
+        const __half * qr = s_q + (lane % 16) * KSTR + lane / 16;
+        const __half * kr = s_kv + (wave * 16 + lane % 16) * KSTR + lane / 16;
+#pragma unroll 4
+        for (int d0 = 0; d0 < HD; d0 += 4) {
+            const double a = (double) __half2float(qr[d0]);
+            const double b = (double) __half2float(kr[d0]);
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc, 0, 0, 0);
+        }
+        const int t = wave * 16 + lane % 16;
+        if (t < nt) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int qi = lane / 16 + 4 * r;
+                const int q = min(q0 + qi, n_q - 1);
+                s_s[qi * SS + t0 + t] = (float) acc[r] * A.scale + mask_at(A, q, t0 + t);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- row statistics and probabilities ----
+    for (int qi = wave; qi < APF_Q; qi += ATT_WAVES) {
+        float * row = s_s + qi * SS;
+        float m = -INFINITY;
+        for (int t = lane; t < n_kv; t += WAVE) m = fmaxf(m, row[t]);
+        m = wave_max(m);
+        double sum = 0.0;
+        for (int t = lane; t < n_kv; t += WAVE) {
+            const float e = m == -INFINITY ? 0.0f : exp_cr(row[t] - m);
+            row[t] = e;
+            sum += (double) e;
+        }
+        sum = wave_sum_d(sum);
+        const float inv = sum > 0.0 ? (float) (1.0 / sum) : 0.0f;
+        for (int t = lane; t < n_kv; t += WAVE) row[t] = __half2float(__float2half_rn(as_f32(row[t] * inv)));
+    }
+
+    // ---- P V ----
+    constexpr int NT = HD / 16;                  // 16-dim output tiles
+    constexpr int TPW = (NT + ATT_WAVES - 1) / ATT_WAVES;
+    v4d acc[TPW];
+#pragma unroll
+    for (int k = 0; k < TPW; k++) acc[k] = v4d{ 0.0, 0.0, 0.0, 0.0 };
+    for (int ch = 0; ch < n_chunks; ch++) {
+        __syncthreads();                         // s_live / p visible; previous s_kv reads done
+        if (!s_live[ch]) continue;
+        const int t0 = ch * APF_CHUNK, nt = min(APF_CHUNK, n_kv - t0);
+        stage(vbase, A.v_nb2, t0, nt);
+        __syncthreads();
+        for (int k0 = 0; k0 < APF_CHUNK; k0 += 4) {
+            const int t = k0 + lane / 16;
+            const double a = t < nt ? (double) s_s[(lane % 16) * SS + t0 + t] : 0.0;
+#pragma unroll
+            for (int k = 0; k < TPW; k++) {
+                const int jt = wave + k * ATT_WAVES;
+                if (jt < NT) {
+                    const double b = (double) __half2float(s_kv[t * KSTR + jt * 16 + lane % 16]);
+                    acc[k] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[k], 0, 0, 0);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < TPW; k++) {
+        const int jt = wave + k * ATT_WAVES;
+        if (jt >= NT) continue;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int q = q0 + lane / 16 + 4 * r;
+            if (q < n_q) A.out[(int64_t) q * A.out_nb1 + (int64_t) h * HD + jt * 16 + lane % 16] = (float) acc[k][r];
+        }
+    }
+}
+
+static int max_lds_per_block() {
+    static int v = -1;
+    if (v < 0) {
+        int dev = 0;
+        HIP_CHECK(hipGetDevice(&dev));
+        HIP_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+    }
+    return v;
+}
+
+static int apf_static_lds_of(int hd) {
+    return hd == 64 ? apf_static_lds<64>() : hd == 96 ? apf_static_lds<96>() : apf_static_lds<128>();
+}
+
+int attn_prefill_max_kv(int hd) {
+    if (hd != 64 && hd != 96 && hd != 128) return 0;
+    const int rows = (max_lds_per_block() - apf_static_lds_of(hd)) / (APF_Q * (int) sizeof(float)) - 4;
+    return std::min(rows / APF_CHUNK * APF_CHUNK, APF_MAX_CHUNKS * APF_CHUNK);
+}
+
+template <int HD>
+static void launch_attn_prefill_hd(const attn_launch & A, hipStream_t st) {
+    const size_t lds = (size_t) APF_Q * apf_row_stride(A.n_kv) * sizeof(float);
+    if (lds + apf_static_lds<HD>() > 65536) {
+        HIP_CHECK(hipFuncSetAttribute((const void *) attn_prefill_kernel<HD>, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds));
+    }
+    launch(attn_prefill_kernel<HD>, dim3((A.n_q + APF_Q - 1) / APF_Q, A.n_head), dim3(ATT_THREADS), lds, st, A);
+}
+
+void launch_attn_prefill(const attn_launch & A, hipStream_t st) {
+    if (A.n_q < 1 || A.n_kv < 1 || A.n_kv > attn_prefill_max_kv(A.hd)) HIP_ABORT("attn prefill: n_kv %d out of range", A.n_kv);
+    if (A.n_head % A.n_head_kv) HIP_ABORT("attn prefill: n_head %% n_head_kv");
+    if (A.out_q.qs) HIP_ABORT("attn prefill: no quantized output");
+    if (((uintptr_t) A.k | (uintptr_t) A.v) % 16 || A.k_nb1 % 8 || A.k_nb2 % 8 || A.v_nb1 % 8 || A.v_nb2 % 8) {
+        HIP_ABORT("attn prefill: K and V rows must be 16-byte aligned");
+    }
+    switch (A.hd) {
+        case 64: launch_attn_prefill_hd<64>(A, st); break;
+        case 96: launch_attn_prefill_hd<96>(A, st); break;
+        case 128: launch_attn_prefill_hd<128>(A, st); break;
+        default: HIP_ABORT("attn prefill: unsupported head dim %d", A.hd);
+    }
+}

@@ -241,3 +241,7 @@ struct attn_launch {
 };
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd);
 void launch_attn_decode(const attn_launch & A, hipStream_t st);
+// n_q > 4 (prefill): one workgroup per (16-query tile, head), a row's scores in LDS (no scratch, no
+// quantized output); n_kv up to attn_prefill_max_kv(hd), 0 for an unsupported head dim
+int attn_prefill_max_kv(int hd);
+void launch_attn_prefill(const attn_launch & A, hipStream_t st);

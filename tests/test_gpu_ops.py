@@ -404,6 +404,39 @@ def test_attention_decode(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
         assert rel_err(a, expect) < 1e-6
 
 
+@pytest.mark.parametrize("hd,n_head,n_head_kv,n_kv,n_new", [
+    (96, 32, 32, 512, 512),   # Phi-3 prefill of 512 tokens, one layer
+    (128, 8, 2, 100, 100),    # GQA, partial last query tile and position chunk
+    (64, 4, 4, 77, 37),       # after 40 cached positions
+    (128, 24, 8, 300, 20),
+    (96, 6, 2, 1000, 5),      # the smallest batch past the decode kernels
+])
+@pytest.mark.parametrize("flash", [False, True])
+def test_attention_prefill(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
+    """Attention over a prefill-width query batch (causal mask): the chain's float roundings
+    exactly (its fully masked position chunks are skipped), flash_attn_ext within tolerance."""
+    r = rng(n_kv + hd + n_new)
+    n_ctx = n_kv + 3
+    kc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+    vc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+    q = r.standard_normal((n_new, n_head, hd)).astype(np.float32)
+    mask = np.zeros((n_new, n_kv), dtype=np.float32)
+    n_past = n_kv - n_new
+    for i in range(n_new):
+        mask[i, n_past + i + 1:] = -np.inf
+
+    def build(g):
+        return attention_graph(g, hd, n_head, n_head_kv, n_kv, n_new, n_ctx, kc, vc, q, mask, flash)
+
+    a, names = profiled(hip, lambda: run_on(hip, build))
+    b = run_on(cpu, build)
+    assert "attn_prefill" in names, names
+    if flash:
+        assert rel_err(a, b) < TOL, rel_err(a, b)
+    else:
+        assert np.array_equal(a, b), rel_err(a, b)
+
+
 def f16_tie_scores(n_kv, seed):
     """Scores (F16, one head, scale 1/8) whose softmax holds a probability p = e * (1/S) that is an
     exact F16 rounding tie as a float, while the exact product e * (1/S) lies on the side whose
