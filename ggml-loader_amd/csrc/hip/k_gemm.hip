@@ -1,140 +1,221 @@
 // k_gemm.hip — the prefill GEMM: Q4_0 / Q8_0 weights times Q8_0-quantized activation columns on
-// the int8 matrix cores.
+// the matrix cores.
 //
 // ggml-cpu computes every output of a quantized mul_mat as a float sum over the weight row's
 // 32-element blocks, in block order, of an exact integer block dot scaled by the two fp16 block
-// scales: Q8_0 sumf += sumi * (d_w * d_x), Q4_0 sumf += (sumi * d_w) * d_x. One
-// v_mfma_i32_16x16x32_i8 yields the integer dots of one block for a tile of 16 weight rows x 16
-// activation columns (exact in any order), so the kernel issues one MFMA per tile and block and
-// adds the scaled terms to f32 accumulators in block order: every output is the same float as the
-// GEMV's and the CPU reference's. The per-term float work (convert, two multiplies, one add) runs on
-// the VALU and bounds the kernel, not the MFMA rate.
+// scales: Q8_0 sumf += sumi * (d_w * d_x), Q4_0 sumf += (sumi * d_w) * d_x. The integer quants are
+// staged as f16 (integers of magnitude <= 128 are exact in f16), so one v_mfma_f32_16x16x32_f16
+// yields the block dots of a tile of 16 weight rows x 16 activation columns as f32 — exact, since
+// every product and partial sum is an integer below 2^24 — and the kernel adds the scaled terms to
+// f32 accumulators in block order: every output is the same float as the GEMV's and the CPU
+// reference's. The per-term float work (two multiplies, one add) runs on the VALU and bounds the
+// kernel, not the MFMA rate.
 //
-// Tiling: a workgroup is 2 x 2 waves; a wave owns WM x WN MFMA tiles. In a tile, lane l holds
-// weight row l%16 and activation column l%16 with the k-slice 8(l/16)..8(l/16)+7 of the block (for
-// Q4_0 the low nibbles of bytes 0-15 are elements 0-15 and the high nibbles 16-31, so the slice is 8
-// bytes and one nibble half), and receives the results of rows 4(l/16)..4(l/16)+3 of column l%16.
-// Each step loads KB blocks of every operand; the next step's loads are in flight while the current
-// step is reduced. Workgroups are numbered so that the column tiles of one row tile run on one XCD
-// and share its L2.
+// Tiling: a workgroup is 2 x 2 waves; a wave owns WTM x WTN MFMA tiles. Each pipeline stage moves
+// KB blocks of the workgroup's weight rows and activation columns from global memory (16-byte
+// loads, consecutive threads on consecutive bytes) into LDS, converting the quants to f16 and the
+// fp16 weight scales to float on the way; the next stage's loads are in flight while the current
+// stage is reduced, with one barrier per stage. In a tile, lane l reads weight row l%16 and
+// activation column l%16, k-slice 8(l/16)..8(l/16)+7 of the block (one 16-byte LDS read each), and
+// receives the results of rows 4(l/16)..4(l/16)+3 of column l%16. Workgroups are numbered so that
+// the column tiles of one row tile run on one XCD and share its L2.
 #include "kernels.h"
 
 #include "ggml.h"
 
-typedef int v4i __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int KB = 4;   // blocks per pipeline step
+// 4 int8 (one dword) -> 4 f16 in two dwords: bytes biased by 128 are placed under the f16 exponent
+// of 1024 (0x64xx = 1024 + byte), then 1152 is subtracted, both exact
+__device__ __forceinline__ void i8x4_to_f16(uint32_t v, uint32_t & lo, uint32_t & hi) {
+    const uint32_t u = v ^ 0x80808080u;
+    lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const __half2 bias = __halves2half2(__ushort_as_half(0xE480), __ushort_as_half(0xE480));   // -1152
+    lo = __builtin_bit_cast(uint32_t, __hadd2(__builtin_bit_cast(__half2, lo), bias));
+    hi = __builtin_bit_cast(uint32_t, __hadd2(__builtin_bit_cast(__half2, hi), bias));
+}
 
-// the lane's 8 int8 weights of one block from its 8 loaded bytes
-template <int TYPE>
-__device__ __forceinline__ long a_slice(uint64_t raw, int q) {
-    if constexpr (TYPE == GGML_TYPE_Q8_0) {
-        return (long) raw;
-    } else {
-        // nibble n -> int8 n - 8 in every byte: (n | 0x80) - 8 stays in [0x78, 0x87] (no borrow
-        // between bytes), and flipping bit 7 turns it into n - 8 as a signed byte
-        const int sh = (q >> 1) * 4;
-        uint32_t lo = ((uint32_t) raw >> sh) & 0x0F0F0F0Fu;
-        uint32_t hi = ((uint32_t) (raw >> 32) >> sh) & 0x0F0F0F0Fu;
-        lo = ((lo | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
-        hi = ((hi | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
-        return (long) (((uint64_t) hi << 32) | lo);
+// 4 nibbles (the low or high halves of one dword) -> 4 f16 of value nibble - 8
+__device__ __forceinline__ void u4x4_to_f16(uint32_t n, uint32_t & lo, uint32_t & hi) {
+    lo = __builtin_amdgcn_perm(0x64646464u, n, 0x04010400u);
+    hi = __builtin_amdgcn_perm(0x64646464u, n, 0x04030402u);
+    const __half2 bias = __halves2half2(__ushort_as_half(0xE408), __ushort_as_half(0xE408));   // -1032
+    lo = __builtin_bit_cast(uint32_t, __hadd2(__builtin_bit_cast(__half2, lo), bias));
+    hi = __builtin_bit_cast(uint32_t, __hadd2(__builtin_bit_cast(__half2, hi), bias));
+}
+
+// 32 int8 -> 32 f16 (64 bytes) at dst
+__device__ __forceinline__ void store_i8x32(_Float16 * dst, const uint4 & a, const uint4 & b) {
+    const uint32_t w[8] = { a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w };
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        uint32_t l0, h0, l1, h1;
+        i8x4_to_f16(w[2 * k], l0, h0);
+        i8x4_to_f16(w[2 * k + 1], l1, h1);
+        *(uint4 *) (dst + 8 * k) = make_uint4(l0, h0, l1, h1);
     }
 }
 
-template <int WM, int WN>
-struct gemm_stage {
-    uint64_t a[WM][KB];    // weight bytes per tile row and block
-    uint64_t b[WN][KB];    // activation int8 per tile column and block
-    uint64_t wd[WM][4];    // fp16 d of KB blocks for each of the lane's 4 output rows
-    float4   xd[WN];       // activation d of KB blocks for the lane's column
+// one Q4_0 block's 16 bytes -> its 32 weights (low nibbles are elements 0-15, high 16-31) as f16
+__device__ __forceinline__ void store_q4x32(_Float16 * dst, const uint4 & a) {
+    const uint32_t w[4] = { a.x, a.y, a.z, a.w };
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        uint32_t l0, h0, l1, h1;
+        u4x4_to_f16(w[2 * k] & 0x0F0F0F0Fu, l0, h0);
+        u4x4_to_f16(w[2 * k + 1] & 0x0F0F0F0Fu, l1, h1);
+        *(uint4 *) (dst + 8 * k) = make_uint4(l0, h0, l1, h1);
+        u4x4_to_f16((w[2 * k] >> 4) & 0x0F0F0F0Fu, l0, h0);
+        u4x4_to_f16((w[2 * k + 1] >> 4) & 0x0F0F0F0Fu, l1, h1);
+        *(uint4 *) (dst + 16 + 8 * k) = make_uint4(l0, h0, l1, h1);
+    }
+}
+
+template <int TYPE, int WTM, int WTN, int KB>
+struct gemm_cfg {
+    static constexpr int QB = TYPE == GGML_TYPE_Q4_0 ? Q4_0_QS : Q8_0_QS;
+    static constexpr int BM = 32 * WTM, BN = 32 * WTN;
+    static constexpr int ROW = KB * 32 + 8;                               // f16 per LDS row (16-byte pad)
+    static constexpr int UA = (BM * KB + 255) / 256, UB = (BN * KB + 255) / 256;   // staged blocks per thread
+    static constexpr int A_HALVES = BM * ROW, B_HALVES = BN * ROW;
+    static constexpr size_t LDS = 2 * ((size_t) (A_HALVES + B_HALVES) * 2 + (size_t) KB * (BM + BN) * 4);
 };
 
-template <int TYPE, int WM, int WN>
+template <int TYPE, int WTM, int WTN, int KB>
 __global__ __launch_bounds__(256) void gemm_q_kernel(const gemm_launch G) {
-    constexpr int QB = TYPE == GGML_TYPE_Q4_0 ? Q4_0_QS : Q8_0_QS;
-    constexpr int BM = 32 * WM, BN = 32 * WN;
-    static_assert(KB == 4, "the scale loads move 4 blocks");
+    using C = gemm_cfg<TYPE, WTM, WTN, KB>;
+    constexpr int QB = C::QB, BM = C::BM, BN = C::BN, ROW = C::ROW;
+    extern __shared__ __align__(16) uint8_t g_lds[];
+    _Float16 * sA = (_Float16 *) g_lds;                       // [2][BM][ROW]
+    _Float16 * sB = sA + 2 * C::A_HALVES;                     // [2][BN][ROW]
+    float * sdw = (float *) (sB + 2 * C::B_HALVES);           // [2][KB][BM]
+    float * sdx = sdw + 2 * KB * BM;                          // [2][KB][BN]
+
     const int64_t M = G.n_rows, N = G.ncols, K = G.K, nb = K / 32;
-    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
     const int q = lane / 16, c = lane % 16;
 
     const int64_t n_ct = (N + BN - 1) / BN, tiles = ((M + BM - 1) / BM) * n_ct;
     int64_t t = blockIdx.x;
     if (tiles % 8 == 0) t = (int64_t) (blockIdx.x % 8) * (tiles / 8) + blockIdx.x / 8;
-    const int64_t row0 = (t / n_ct) * BM + (wave / 2) * 16 * WM;
-    const int64_t col0 = (t % n_ct) * BN + (wave % 2) * 16 * WN;
+    const int64_t m0 = (t / n_ct) * BM, n0 = (t % n_ct) * BN;
+    const int wr = (wave / 2) * 16 * WTM, wc = (wave % 2) * 16 * WTN;   // wave's tile origin in the workgroup tile
 
-    // operand rows / columns clamped into range (their results are not stored)
-    const uint8_t * pa[WM];
-    const __half * pd[WM];
-    for (int i = 0; i < WM; i++) {
-        const int64_t ra = min(row0 + 16 * i + c, M - 1);
-        pa[i] = G.w + ra * nb * QB + (TYPE == GGML_TYPE_Q4_0 ? 8 * (q & 1) : 8 * q);
-        pd[i] = G.wd + min(row0 + 16 * i + 4 * q, M - 4) * nb;
-    }
-    const int8_t * pb[WN];
-    const float * px[WN];
-    for (int j = 0; j < WN; j++) {
-        const int64_t cb = min(col0 + 16 * j + c, N - 1);
-        pb[j] = G.xq + cb * K + 8 * q;
-        px[j] = G.xd + cb * nb;
-    }
-
-    auto load = [&](gemm_stage<WM, WN> & s, int64_t b) {
-        for (int i = 0; i < WM; i++)
-            for (int k = 0; k < KB; k++) s.a[i][k] = *(const uint64_t *) (pa[i] + (b + k) * QB);
-        for (int j = 0; j < WN; j++)
-            for (int k = 0; k < KB; k++) s.b[j][k] = *(const uint64_t *) (pb[j] + (b + k) * 32);
-        for (int i = 0; i < WM; i++)
-            for (int r = 0; r < 4; r++) s.wd[i][r] = *(const uint64_t *) (pd[i] + r * nb + b);
-        for (int j = 0; j < WN; j++) s.xd[j] = *(const float4 *) (px[j] + b);
-    };
-
-    float acc[WM][WN][4];
-    for (int i = 0; i < WM; i++)
-        for (int j = 0; j < WN; j++)
-            for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
-
-    gemm_stage<WM, WN> cur, nxt;
-    load(cur, 0);
-    for (int64_t b = 0; b < nb; b += KB) {
-        if (b + KB < nb) load(nxt, b + KB);
-        for (int k = 0; k < KB; k++) {
-            v4i s[WM][WN];
-            for (int i = 0; i < WM; i++) {
-                const long a = a_slice<TYPE>(cur.a[i][k], q);
-                for (int j = 0; j < WN; j++) {
-                    s[i][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, (long) cur.b[j][k], v4i{ 0, 0, 0, 0 }, 0, 0, 0);
-                }
-            }
-            float dw[WM][4];
-            for (int i = 0; i < WM; i++)
-                for (int r = 0; r < 4; r++)
-                    dw[i][r] = __half2float(__ushort_as_half((unsigned short) (cur.wd[i][r] >> (16 * k))));
-            for (int j = 0; j < WN; j++) {
-                const float dx = k == 0 ? cur.xd[j].x : k == 1 ? cur.xd[j].y : k == 2 ? cur.xd[j].z : cur.xd[j].w;
-                for (int i = 0; i < WM; i++)
-                    for (int r = 0; r < 4; r++) {
-                        if constexpr (TYPE == GGML_TYPE_Q8_0) {
-                            const float dd = dw[i][r] * dx;
-                            acc[i][j][r] += (float) s[i][j][r] * dd;
-                        } else {
-                            acc[i][j][r] += ((float) s[i][j][r] * dw[i][r]) * dx;
-                        }
-                    }
+    // staging: unit u = (row or column, block of the stage); rows / columns past the end repeat the last one
+    uint4 ra[C::UA][2], rb[C::UB][2];
+    __half rd[C::UA];
+    float rx[C::UB];
+    auto load = [&](int64_t b0) {
+#pragma unroll
+        for (int k = 0; k < C::UA; k++) {
+            const int u = tid + 256 * k;
+            if (u < BM * KB) {
+                const int64_t row = min(m0 + u / KB, M - 1);
+                const int64_t blk = row * nb + b0 + u % KB;
+                const uint4 * p = (const uint4 *) (G.w + blk * QB);
+                ra[k][0] = p[0];
+                if constexpr (QB == 32) ra[k][1] = p[1];
+                rd[k] = G.wd[blk];
             }
         }
-        cur = nxt;
+#pragma unroll
+        for (int k = 0; k < C::UB; k++) {
+            const int u = tid + 256 * k;
+            if (u < BN * KB) {
+                const int64_t col = min(n0 + u / KB, N - 1);
+                const uint4 * p = (const uint4 *) (G.xq + col * K + (b0 + u % KB) * 32);
+                rb[k][0] = p[0];
+                rb[k][1] = p[1];
+                rx[k] = G.xd[col * nb + b0 + u % KB];
+            }
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < C::UA; k++) {
+            const int u = tid + 256 * k;
+            if (u < BM * KB) {
+                const int r = u / KB, kb = u % KB;
+                _Float16 * dst = sA + buf * C::A_HALVES + r * ROW + kb * 32;
+                if constexpr (QB == 32) store_i8x32(dst, ra[k][0], ra[k][1]);
+                else store_q4x32(dst, ra[k][0]);
+                sdw[(buf * KB + kb) * BM + r] = __half2float(rd[k]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < C::UB; k++) {
+            const int u = tid + 256 * k;
+            if (u < BN * KB) {
+                const int cc = u / KB, kb = u % KB;
+                store_i8x32(sB + buf * C::B_HALVES + cc * ROW + kb * 32, rb[k][0], rb[k][1]);
+                sdx[(buf * KB + kb) * BN + cc] = rx[k];
+            }
+        }
+    };
+
+    float acc[WTM][WTN][4];
+#pragma unroll
+    for (int i = 0; i < WTM; i++)
+#pragma unroll
+        for (int j = 0; j < WTN; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
+
+    const int64_t n_stages = nb / KB;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int64_t s = 0; s < n_stages; s++) {
+        const int buf = (int) (s & 1);
+        if (s + 1 < n_stages) load((s + 1) * KB);
+        const _Float16 * A = sA + buf * C::A_HALVES;
+        const _Float16 * B = sB + buf * C::B_HALVES;
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++) {
+            f16x8 a[WTM], b[WTN];
+            f32x4 dw[WTM];
+            float dx[WTN];
+#pragma unroll
+            for (int i = 0; i < WTM; i++) {
+                a[i] = *(const f16x8 *) (A + (wr + 16 * i + c) * ROW + kb * 32 + 8 * q);
+                dw[i] = *(const f32x4 *) (sdw + (buf * KB + kb) * BM + wr + 16 * i + 4 * q);
+            }
+#pragma unroll
+            for (int j = 0; j < WTN; j++) {
+                b[j] = *(const f16x8 *) (B + (wc + 16 * j + c) * ROW + kb * 32 + 8 * q);
+                dx[j] = sdx[(buf * KB + kb) * BN + wc + 16 * j + c];
+            }
+#pragma unroll
+            for (int i = 0; i < WTM; i++)
+#pragma unroll
+                for (int j = 0; j < WTN; j++) {
+                    const f32x4 sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        if constexpr (TYPE == GGML_TYPE_Q8_0) {
+                            const float dd = dw[i][r] * dx[j];
+                            acc[i][j][r] += sv[r] * dd;
+                        } else {
+                            acc[i][j][r] += (sv[r] * dw[i][r]) * dx[j];
+                        }
+                    }
+                }
+        }
+        if (s + 1 < n_stages) store(buf ^ 1);
+        __syncthreads();
     }
 
-    for (int j = 0; j < WN; j++) {
-        const int64_t col = col0 + 16 * j + c;
+#pragma unroll
+    for (int j = 0; j < WTN; j++) {
+        const int64_t col = n0 + wc + 16 * j + c;
         if (col >= N) continue;
-        for (int i = 0; i < WM; i++) {
-            const int64_t r0 = row0 + 16 * i + 4 * q;
+#pragma unroll
+        for (int i = 0; i < WTM; i++) {
+            const int64_t r0 = m0 + wr + 16 * i + 4 * q;
             if (r0 >= M) continue;
             float v[4] = { acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3] };
             if (G.add) {
@@ -151,26 +232,33 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const gemm_launch G) {
     }
 }
 
-template <int TYPE, int WM, int WN>
+template <int TYPE, int WTM, int WTN, int KB>
 void launch_gemm_t(const gemm_launch & G, hipStream_t st) {
-    const int64_t BM = 32 * WM, BN = 32 * WN;
-    const int64_t tiles = ((G.n_rows + BM - 1) / BM) * ((G.ncols + BN - 1) / BN);
-    launch(gemm_q_kernel<TYPE, WM, WN>, dim3((unsigned) tiles), dim3(256), 0, st, G);
+    using C = gemm_cfg<TYPE, WTM, WTN, KB>;
+    static bool attr = false;
+    if (!attr && C::LDS > 65536) {
+        HIP_CHECK(hipFuncSetAttribute((const void *) gemm_q_kernel<TYPE, WTM, WTN, KB>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int) C::LDS));
+    }
+    attr = true;
+    const int64_t tiles = ((G.n_rows + C::BM - 1) / C::BM) * ((G.ncols + C::BN - 1) / C::BN);
+    launch(gemm_q_kernel<TYPE, WTM, WTN, KB>, dim3((unsigned) tiles), dim3(256), C::LDS, st, G);
 }
+
+int64_t n_tiles(const gemm_launch & G, int bm, int bn) { return ((G.n_rows + bm - 1) / bm) * ((G.ncols + bn - 1) / bn); }
 
 template <int TYPE>
 void launch_gemm_type(const gemm_launch & G, hipStream_t st) {
-    // 64 x 128 tiles unless that leaves fewer than two workgroups per CU
-    const int64_t big = ((G.n_rows + 63) / 64) * ((G.ncols + 127) / 128);
-    if (big >= 512) launch_gemm_t<TYPE, 2, 4>(G, st);
-    else launch_gemm_t<TYPE, 1, 4>(G, st);
+    // the largest workgroup tile that still gives every CU two workgroups
+    if (n_tiles(G, 128, 128) >= 512) launch_gemm_t<TYPE, 4, 4, 2>(G, st);
+    else if (n_tiles(G, 64, 128) >= 512) launch_gemm_t<TYPE, 2, 4, 2>(G, st);
+    else launch_gemm_t<TYPE, 1, 2, 4>(G, st);
 }
 
 } // namespace
 
 bool gemm_supported(int type, int64_t K, int64_t n_rows) {
-    return (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0) && K > 0 && K % (32 * KB) == 0 && n_rows > 0 &&
-           n_rows % 4 == 0;
+    return (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0) && K > 0 && K % 128 == 0 && n_rows > 0;
 }
 
 void launch_gemm(const gemm_launch & G, hipStream_t st) {
@@ -178,8 +266,7 @@ void launch_gemm(const gemm_launch & G, hipStream_t st) {
         HIP_ABORT("gemm: unsupported geometry (type %d, K %lld, rows %lld, cols %lld)", G.type, (long long) G.K,
                   (long long) G.n_rows, (long long) G.ncols);
     }
-    const uintptr_t align = (uintptr_t) G.y | (uintptr_t) G.add | (uintptr_t) G.w | (uintptr_t) G.wd |
-                            (uintptr_t) G.xq | (uintptr_t) G.xd;
+    const uintptr_t align = (uintptr_t) G.y | (uintptr_t) G.add | (uintptr_t) G.w | (uintptr_t) G.xq;
     if (align % 16 || G.y_stride % 4 || (G.add && G.add_stride % 4)) {
         HIP_ABORT("gemm: operands must be 16-byte aligned with strides of whole float4s");
     }

@@ -80,7 +80,7 @@ constexpr int GEMM_MIN_COLS = 64;   // narrower products stay on the GEMV
 struct gemm_launch {
     int             type;      // GGML_TYPE_Q4_0 / Q8_0
     int64_t         K;         // row length (a multiple of 128)
-    int64_t         n_rows;    // a multiple of 4
+    int64_t         n_rows;
     int64_t         ncols;
     const uint8_t * w;         // qs plane of row 0
     const __half *  wd;        // d plane of row 0
