@@ -158,6 +158,9 @@ void launch_quantize_q8k(const float * x, int64_t x_col_stride, int64_t K, int64
 // ---------------------------------------------------------------------------------------------
 // GEMV kernels
 
+// Grid rows: the matrices' rows one after another, each matrix starting on a workgroup boundary
+// (row_begin[i] is a multiple of rows_per_block), so every workgroup reads a single matrix and
+// selects it with uniform (scalar) arithmetic. Rows past a matrix's n_rows are padding.
 struct gemv_kargs {
     gemv_launch L;
     int total_rows;
@@ -249,6 +252,42 @@ __device__ __forceinline__ void q4k_unit_ints(const uint8_t * blk, int p, const 
     mins = m_a * ((int) xbs[4 * p] + (int) xbs[4 * p + 1]) + m_b * ((int) xbs[4 * p + 2] + (int) xbs[4 * p + 3]);
 }
 
+// floats between the term rows of two Q4_0/Q8_0 chains: 4 more than the terms, so the 16-byte
+// reads of consecutive chains (one lane each) start on different LDS banks
+__host__ __device__ constexpr int gemv_term_stride(int nb) { return nb + 4; }
+
+// The float sum of a chain's block terms in block order (ggml-cpu's sumf += term), 32 terms per
+// step with the next step's LDS reads in flight during the adds.
+__device__ __forceinline__ float ordered_sum(const float * terms, int nb) {
+    float acc = 0.0f;
+    if ((nb & 31) == 0) {
+        const float4 * t4 = (const float4 *) terms;
+        const int n32 = nb / 32;
+        float4 cur[8], nxt[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) cur[k] = t4[k];
+        for (int b = 0; b < n32; b++) {
+            if (b + 1 < n32) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) nxt[k] = t4[(b + 1) * 8 + k];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) acc = acc + cur[k].x + cur[k].y + cur[k].z + cur[k].w;
+#pragma unroll
+            for (int k = 0; k < 8; k++) cur[k] = nxt[k];
+        }
+    } else if ((nb & 3) == 0) {
+        const float4 * t4 = (const float4 *) terms;
+        for (int b4 = 0; b4 < nb / 4; b4++) {
+            const float4 v = t4[b4];
+            acc = acc + v.x + v.y + v.z + v.w;
+        }
+    } else {
+        for (int b = 0; b < nb; b++) acc = acc + terms[b];
+    }
+    return acc;
+}
+
 // dynamic LDS layout: [staged activation][terms]
 struct gemv_lds {
     int8_t * xq;
@@ -265,7 +304,7 @@ __host__ __device__ inline size_t gemv_lds_bytes(int K, int rows_per_block, int 
         return (size_t) K + (size_t) nsb * 4 + (size_t) (K / 16) * 2 + 16 + (size_t) rows_per_block * n_chain * nsb * 9 * 4;
     }
     const int nb = K / 32;
-    return (size_t) K + (size_t) nb * 8 + (size_t) rows_per_block * n_chain * nb * 4;
+    return (size_t) K + (size_t) nb * 8 + (size_t) rows_per_block * n_chain * gemv_term_stride(nb) * 4;
 }
 
 template <int TYPE>
@@ -374,22 +413,44 @@ __device__ __forceinline__ void load_chunk(float (&v)[C], const float * p) {
 // prologue_load into registers; further chunks are loaded when they are quantized.
 constexpr int PRO_REGS = 32;
 
-template <int TYPE>
+template <int TYPE, bool PRO>
 __device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, float (&xv)[PRO_REGS], float (&wv)[PRO_REGS]) {
+    // Every load here is unconditional (indices clamped; a thread past the end loads the last
+    // chunk again and never uses it), so none of them sits in a branch that the compiler would
+    // close with a wait before the weight loads are issued.
     constexpr int C = TYPE == GGML_TYPE_Q4_K ? 16 : 32;
+    const int t = threadIdx.x;
 #pragma unroll
     for (int e = 0; e < PRO_REGS; e++) { xv[e] = 0.0f; wv[e] = 1.0f; }
-    if (!L.norm.x) return;
-    const int nchunk = L.K / C;
-    const int t = threadIdx.x;
-    const float * xcol = L.norm.x + (int64_t) col * L.norm.x_stride;
-    float (&x0)[C] = *reinterpret_cast<float (*)[C]>(&xv[0]);
-    if (t < nchunk) {
-        load_chunk(x0, xcol + (int64_t) t * C);
-        if (L.norm.rms && L.norm.w) load_chunk(*reinterpret_cast<float (*)[C]>(&wv[0]), L.norm.w + (int64_t) t * C);
-    }
-    if (C * 2 == PRO_REGS && !L.norm.rms && t + (int) blockDim.x < nchunk) {
-        load_chunk(*reinterpret_cast<float (*)[C]>(&xv[PRO_REGS - C]), xcol + (int64_t) (t + blockDim.x) * C);
+    if constexpr (!PRO) {
+        // an already quantized Q8_0 column: its quants (xv, 4 x 16 bytes per thread) and block
+        // scales and sums (wv[0..1], wv[2..3]), ahead of the weights as well
+        if constexpr (TYPE != GGML_TYPE_Q4_K) {
+            const int K = L.K, nb = K / 32;
+            const int8_t * xq = L.xq + (int64_t) col * K;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int i = min(t + k * (int) blockDim.x, K / 16 - 1);
+                const int4 v = *(const int4 *) (xq + i * 16);
+                xv[4 * k] = __int_as_float(v.x); xv[4 * k + 1] = __int_as_float(v.y);
+                xv[4 * k + 2] = __int_as_float(v.z); xv[4 * k + 3] = __int_as_float(v.w);
+            }
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int i = min(t + k * (int) blockDim.x, nb - 1);
+                wv[k] = L.xd[(int64_t) col * nb + i];
+                wv[2 + k] = __int_as_float(L.xs[(int64_t) col * nb + i]);
+            }
+        }
+        return;
+    } else {
+        const int nchunk = L.K / C;
+        const float * xcol = L.norm.x + (int64_t) col * L.norm.x_stride;
+        load_chunk(*reinterpret_cast<float (*)[C]>(&xv[0]), xcol + (int64_t) min(t, nchunk - 1) * C);
+        if (L.norm.rms && L.norm.w) load_chunk(*reinterpret_cast<float (*)[C]>(&wv[0]), L.norm.w + (int64_t) min(t, nchunk - 1) * C);
+        if (C * 2 == PRO_REGS && !L.norm.rms) {
+            load_chunk(*reinterpret_cast<float (*)[C]>(&xv[PRO_REGS - C]), xcol + (int64_t) min(t + (int) blockDim.x, nchunk - 1) * C);
+        }
     }
 }
 
@@ -422,8 +483,10 @@ __device__ __forceinline__ void prologue_finish(const gemv_launch & L, int col, 
     }
     const int lane = t % WAVE, wave = t / WAVE;
     double ss = 0.0;
+    if (t < nchunk) {
 #pragma unroll
-    for (int e = 0; e < C; e++) ss += (double) (x0[e] * x0[e]);
+        for (int e = 0; e < C; e++) ss += (double) (x0[e] * x0[e]);
+    }
     ss = wave_sum_d(ss);
     if (lane == 0) s_red[wave] = ss;
     __syncthreads();
@@ -440,23 +503,35 @@ __device__ __forceinline__ void prologue_finish(const gemv_launch & L, int col, 
 }
 
 // the quantized activation column in LDS: finished by the prologue, or copied
-template <int TYPE>
+template <int TYPE, bool PRO>
 __device__ __forceinline__ void stage_x(const gemv_launch & L, int col, const gemv_lds & s, double * s_red,
                                         float (&xv)[PRO_REGS], const float (&wv)[PRO_REGS]) {
     const int K = L.K;
-    if (L.norm.x) {
+    if constexpr (PRO) {
         prologue_finish<TYPE>(L, col, xv, wv, s, s_red);
-    } else if (TYPE == GGML_TYPE_Q4_K) {
+    } else if constexpr (TYPE == GGML_TYPE_Q4_K) {
         const int nsb = K / 256;
         for (int i = threadIdx.x * 16; i < K; i += blockDim.x * 16) *(int4 *) (s.xq + i) = *(const int4 *) (L.xq + (int64_t) col * K + i);
         for (int i = threadIdx.x; i < nsb; i += blockDim.x) s.xd[i] = L.xd[(int64_t) col * nsb + i];
         for (int i = threadIdx.x; i < K / 16; i += blockDim.x) s.xbs[i] = L.xbs[(int64_t) col * (K / 16) + i];
     } else {
+        // from the registers prologue_load filled (K <= 64 * blockDim, nb <= 2 * blockDim)
         const int nb = K / 32;
-        for (int i = threadIdx.x * 16; i < K; i += blockDim.x * 16) *(int4 *) (s.xq + i) = *(const int4 *) (L.xq + (int64_t) col * K + i);
-        for (int i = threadIdx.x; i < nb; i += blockDim.x) {
-            s.xd[i] = L.xd[(int64_t) col * nb + i];
-            s.xs[i] = L.xs[(int64_t) col * nb + i];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = threadIdx.x + k * blockDim.x;
+            if (i * 16 < K) {
+                *(int4 *) (s.xq + i * 16) = make_int4(__float_as_int(xv[4 * k]), __float_as_int(xv[4 * k + 1]),
+                                                      __float_as_int(xv[4 * k + 2]), __float_as_int(xv[4 * k + 3]));
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int i = threadIdx.x + k * blockDim.x;
+            if (i < nb) {
+                s.xd[i] = wv[k];
+                s.xs[i] = __float_as_int(wv[2 + k]);
+            }
         }
     }
     __syncthreads();
@@ -472,7 +547,7 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const gemv_launch L, q8_
     const int K = L.K;
     const gemv_lds s = lds_layout<TYPE>(smem, K);
     float xv[PRO_REGS], wv[PRO_REGS];
-    prologue_load<TYPE>(L, col, xv, wv);
+    prologue_load<TYPE, true>(L, col, xv, wv);
     prologue_finish<TYPE>(L, col, xv, wv, s, s_red);
     __syncthreads();
     int8_t * qs = (TYPE == GGML_TYPE_Q4_K ? q8k.qs : q8.qs) + (int64_t) col * K;
@@ -502,7 +577,7 @@ void launch_act_quant(const gemv_launch & L, const q8_act & q8, const q8k_act & 
     }
 }
 
-template <int TYPE, int LPR, bool SWIGLU, int ITS>
+template <int TYPE, int LPR, bool SWIGLU, int ITS, bool PRO>
 __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int RPW = WAVE / LPR;
@@ -517,9 +592,9 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
     const int col = blockIdx.y;
     const gemv_launch & L = a.L;
     const int K = L.K;
-    const bool valid = row < a.total_rows;
-    const int mi = SWIGLU ? 0 : find_mat(a, valid ? row : 0);
+    const int mi = SWIGLU ? 0 : find_mat(a, blockIdx.x * rows_pb);   // uniform: the workgroup's matrix
     const int lrow = SWIGLU ? row : row - a.row_begin[mi];
+    const bool valid = row < a.total_rows && lrow < L.m[mi].n_rows;
 
     const gemv_lds s = lds_layout<TYPE>(smem, K);
     __shared__ double s_red[512 / WAVE];
@@ -543,28 +618,30 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
         // prologue loads, then every weight load of this lane, then the prologue's arithmetic: the
         // weight stream is in flight while the column is normalized and quantized
         float xv[PRO_REGS], wv[PRO_REGS];
-        prologue_load<TYPE>(L, xcol, xv, wv);
+        prologue_load<TYPE, PRO>(L, xcol, xv, wv);
+        // Straight-line loads (row and block clamped into the matrix; the extra lanes' values are
+        // never used) so they all issue back to back; the fp16 scales stay raw until the dots.
         uint4 qa[NCH][MAXIT], qb[NCH][MAXIT];
-        float dw[NCH][MAXIT];
+        uint32_t dwb[NCH][MAXIT];
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++) {
-            const uint8_t * wq = L.m[SWIGLU ? ch : mi].w + wrow_i * nb * QS;
-            const __half * wd = L.m[SWIGLU ? ch : mi].wd + wrow_i * nb;
+            const gemv_mat & wm = L.m[SWIGLU ? ch : mi];
+            const int64_t wr = erow + min(lrow, wm.n_rows - 1);
+            const uint8_t * wq = wm.w + wr * nb * QS;
+            const unsigned short * wd = (const unsigned short *) wm.wd + wr * nb;
 #pragma unroll
             for (int it = 0; it < MAXIT; it++) {
-                const int b = l + it * LPR;
-                if (valid && b < nb) {
-                    qa[ch][it] = *(const uint4 *) (wq + (int64_t) b * QS);
-                    if (TYPE == GGML_TYPE_Q8_0) qb[ch][it] = *(const uint4 *) (wq + (int64_t) b * QS + 16);
-                    dw[ch][it] = __half2float(wd[b]);
-                }
+                const int b = min(l + it * LPR, nb - 1);
+                qa[ch][it] = *(const uint4 *) (wq + (int64_t) b * QS);
+                if (TYPE == GGML_TYPE_Q8_0) qb[ch][it] = *(const uint4 *) (wq + (int64_t) b * QS + 16);
+                dwb[ch][it] = wd[b];
             }
         }
-        stage_x<TYPE>(L, xcol, s, s_red, xv, wv);
+        stage_x<TYPE, PRO>(L, xcol, s, s_red, xv, wv);
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++) {
             if (!valid) break;
-            float * terms = s.terms + (rib * NCH + ch) * nb;
+            float * terms = s.terms + (rib * NCH + ch) * gemv_term_stride(nb);
 #pragma unroll
             for (int it = 0; it < MAXIT; it++) {
                 const int b = l + it * LPR;
@@ -572,13 +649,14 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                     const int4 xa = *(const int4 *) (s.xq + b * 32);
                     const int4 xb = *(const int4 *) (s.xq + b * 32 + 16);
                     const float dx = s.xd[b];
+                    const float dw = __half2float(__ushort_as_half((unsigned short) dwb[ch][it]));
                     float t;
                     if (TYPE == GGML_TYPE_Q4_0) {
                         const int sumi = dot_q4_0_block(qa[ch][it], xa, xb) - 8 * s.xs[b];
-                        t = ((float) sumi * dw[ch][it]) * dx;           // ggml: sumi*d_x*d_y
+                        t = ((float) sumi * dw) * dx;           // ggml: sumi*d_x*d_y
                     } else {
                         const int sumi = dot_q8_0_block(qa[ch][it], qb[ch][it], xa, xb);
-                        t = (float) sumi * (dw[ch][it] * dx);           // ggml: sumi*(d_x*d_y)
+                        t = (float) sumi * (dw * dx);           // ggml: sumi*(d_x*d_y)
                     }
                     terms[b] = t;
                 }
@@ -586,8 +664,8 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
         }
     } else { // Q4_K: per (super-block, l) products d*aux32[l] and dmin*mins
         float xv[PRO_REGS], wv[PRO_REGS];
-        prologue_load<TYPE>(L, xcol, xv, wv);
-        stage_x<TYPE>(L, xcol, s, s_red, xv, wv);
+        prologue_load<TYPE, PRO>(L, xcol, xv, wv);
+        stage_x<TYPE, PRO>(L, xcol, s, s_red, xv, wv);
         constexpr int MAXU = 608 / LPR;   // supports K <= 9728 * 4 (units = K/64 <= 608)
         const int units = K / 64, nsb = K / 256;
         const int64_t row_bytes = (int64_t) nsb * Q4_K_BYTES;
@@ -636,40 +714,44 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
             }
         }
     }
-    __syncthreads();
+    if constexpr (TYPE == GGML_TYPE_Q4_0 || TYPE == GGML_TYPE_Q8_0) {
+        // ---- ordered sums: every chain of the workgroup on its own lane of wave 0 (lane = row *
+        // NCH + chain), so one wave instruction advances all of them ----
+        __syncthreads();
+        if (wave != 0) return;
+        const int nb = K / 32;
+        const int r = lane / NCH, ch = lane % NCH;
+        const int rrow = blockIdx.x * rows_pb + r;
+        const bool has = r < rows_pb && rrow < a.total_rows && (SWIGLU || rrow - a.row_begin[mi] < L.m[mi].n_rows);
+        float acc = 0.0f;
+        if (has) acc = ordered_sum(s.terms + (r * NCH + ch) * gemv_term_stride(nb), nb);
+        if constexpr (SWIGLU) {
+            // act = silu(gate) * up (two roundings, as the silu and mul ops); up sits on the next lane
+            const float uv = __shfl_down(acc, 1, WAVE);
+            if (has && ch == 0) {
+                const float sl = acc / (1.0f + exp_cr(-acc));
+                L.m[0].y[(int64_t) col * L.m[0].y_stride + rrow] = sl * uv;
+            }
+        } else if (has) {
+            const int rl = rrow - a.row_begin[mi];
+            const gemv_mat & m = L.m[mi];
+            float v = acc;
+            if (m.add) v = v + m.add[(int64_t) col * m.add_stride + rl];
+            m.y[(int64_t) col * m.y_stride + rl] = v;
+        }
+        return;
+    }
+
+    // a Q4_K row's terms were written by lanes of its own wave: a wave-level ordering point suffices
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // ---- ordered sums, one lane per chain ----
     float res[NCH];
 #pragma unroll
     for (int ch = 0; ch < NCH; ch++) res[ch] = 0.0f;
-    if (TYPE == GGML_TYPE_Q4_0 || TYPE == GGML_TYPE_Q8_0) {
-        const int nb = K / 32;
-        if (l < NCH && valid) {
-            const float * terms = s.terms + (rib * NCH + l) * nb;
-            float acc = 0.0f;
-            if ((nb & 3) == 0) {
-                // 16 terms per step: the four 16-byte LDS reads go out together, then the adds
-                const float4 * t4 = (const float4 *) terms;
-                const int n4 = nb / 4;
-                for (int b4 = 0; b4 < n4; b4 += 4) {
-                    float4 v[4];
-#pragma unroll
-                    for (int k = 0; k < 4; k++) v[k] = b4 + k < n4 ? t4[b4 + k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        if (b4 + k < n4) acc = acc + v[k].x + v[k].y + v[k].z + v[k].w;
-                    }
-                }
-            } else {
-                for (int b = 0; b < nb; b++) acc = acc + terms[b];
-            }
-            res[0] = acc;
-        }
-        // lane 0 holds gate (or the single chain), lane 1 holds up
-        const float mine = res[0];
-#pragma unroll
-        for (int ch = 0; ch < NCH; ch++) res[ch] = __shfl(mine, g * LPR + ch, WAVE);
-    } else {
+    {
         const int nsb = K / 256;
         // lanes 0..8 of a group: l < 8 -> sums[l] chain, l == 8 -> the mins chain (per ch)
         float v = 0.0f;
@@ -713,10 +795,24 @@ template <int TYPE, int LPR, bool SWIGLU, int ITS>
 static void launch_gemv_its(gemv_kargs & ka, int waves, hipStream_t st) {
     constexpr int RPW = WAVE / LPR;
     ka.rows_per_block = waves * RPW;
+    if (!SWIGLU) {
+        // every matrix starts on a workgroup boundary
+        int r = 0;
+        for (int i = 0; i < ka.L.n_mats; i++) {
+            ka.row_begin[i] = r;
+            r += (ka.L.m[i].n_rows + ka.rows_per_block - 1) / ka.rows_per_block * ka.rows_per_block;
+        }
+        for (int i = ka.L.n_mats; i <= GEMV_MAX_MATS; i++) ka.row_begin[i] = r;
+        ka.total_rows = r;
+    }
     const int grid_x = (ka.total_rows + ka.rows_per_block - 1) / ka.rows_per_block;
     const size_t lds = gemv_lds_bytes<TYPE>(ka.L.K, ka.rows_per_block, SWIGLU ? 2 : 1);
+    if (TYPE != GGML_TYPE_Q4_K && ka.rows_per_block * (SWIGLU ? 2 : 1) > WAVE) {
+        HIP_ABORT("gemv: %d chains per workgroup exceed one wave", ka.rows_per_block * (SWIGLU ? 2 : 1));
+    }
     if (lds > 160 * 1024) HIP_ABORT("gemv: K=%d needs %zu bytes of LDS", ka.L.K, lds);
-    launch((gemv_kernel<TYPE, LPR, SWIGLU, ITS>), dim3(grid_x, ka.L.ncols), dim3(waves * WAVE), lds, st, ka);
+    if (ka.L.norm.x) launch((gemv_kernel<TYPE, LPR, SWIGLU, ITS, true>), dim3(grid_x, ka.L.ncols), dim3(waves * WAVE), lds, st, ka);
+    else launch((gemv_kernel<TYPE, LPR, SWIGLU, ITS, false>), dim3(grid_x, ka.L.ncols), dim3(waves * WAVE), lds, st, ka);
 }
 
 // ITS = weight blocks per lane for Q4_0/Q8_0, held in registers from the up-front loads. The ladder
