@@ -157,6 +157,7 @@ def prefill_bench(gl, args):
         s.forward(0, tokens)
         hipl.ggml_backend_hip_set_profiling(s.backend, False)
         prof = gl.profile(s.backend)
+    prof.pop("host_enqueue", None)
     ms_step = 1000 * secs / args.steps
     log(f"[bench] prefill {n}: {args.steps} steps in {secs:.4f}s -> {n / (secs / args.steps):.1f} tok/s ({ms_step:.3f} ms/step)")
     total_ms = sum(v[1] for v in prof.values())
@@ -247,6 +248,8 @@ def main():
         prof = gl.profile(s.backend)
         weights_bytes = s.get("weights_bytes")
 
+    host = timed.pop("host_enqueue", None)
+    prof.pop("host_enqueue", None)
     total_ms = sum(v[1] for v in prof.values())
     breakdown = {}
     for k, (n, ms, by) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
@@ -310,7 +313,10 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernel_breakdown_us_per_step": {k: round(v["launches_per_step"] * v["us_per_launch"], 1) for k, v in breakdown.items()},
+        "host_enqueue_us_per_step": round(host[1] / host[0] * 1e3, 1) if host else None,
     }
+    if host:
+        log(f"[bench] host enqueue {host[1] / host[0] * 1e3:.1f} us/step (graph walk + kernel submission)")
     print(json.dumps(out), flush=True)
 
 

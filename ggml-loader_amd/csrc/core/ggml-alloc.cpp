@@ -12,7 +12,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
-#include <unordered_map>
+#include <cstdint>
 #include <vector>
 
 namespace {
@@ -80,46 +80,79 @@ struct ggml_gallocr {
     // plan of the last graph
     std::vector<std::pair<ggml_tensor *, size_t>> offsets;
     size_t plan_size = 0;
+    // planning tables, kept across calls (a graph is replanned every decode step): an
+    // open-addressing map tensor -> slot, and per slot its last consumer, offset and the next
+    // slot freed after the same node
+    std::vector<ggml_tensor *> keys;
+    std::vector<int> last_use, free_next, free_head;
+    std::vector<size_t> off;
+    std::vector<char> placed;
 };
+
+static int slot_of(ggml_gallocr * ga, ggml_tensor * t) {
+    const size_t mask = ga->keys.size() - 1;
+    size_t h = (size_t) ((reinterpret_cast<uintptr_t>(t) >> 4) * 0x9E3779B97F4A7C15ull) & mask;
+    for (;; h = (h + 1) & mask) {
+        if (ga->keys[h] == t) return (int) h;
+        if (!ga->keys[h]) {
+            ga->keys[h] = t;
+            ga->last_use[h] = -1;
+            ga->placed[h] = 0;
+            return (int) h;
+        }
+    }
+}
 
 static void plan_graph(ggml_gallocr * ga, ggml_cgraph * g) {
     ga->offsets.clear();
-    std::unordered_map<ggml_tensor *, int> last_use;
+    size_t cap = 64;
+    while (cap < 4 * (size_t) (g->n_nodes + g->n_leafs)) cap <<= 1;
+    ga->keys.assign(cap, nullptr);
+    ga->last_use.resize(cap);
+    ga->free_next.resize(cap);
+    ga->off.resize(cap);
+    ga->placed.resize(cap);
+    ga->free_head.assign((size_t) g->n_nodes, -1);
     for (int i = 0; i < g->n_nodes; i++) {
         ggml_tensor * n = g->nodes[i];
         for (int s = 0; s < GGML_MAX_SRC; s++) {
-            if (n->src[s]) last_use[base_of(n->src[s])] = i;
+            if (n->src[s]) ga->last_use[slot_of(ga, base_of(n->src[s]))] = i;
         }
-        if (n->view_src) last_use[n->view_src] = std::max(last_use[n->view_src], i);
+        if (n->view_src) {
+            const int k = slot_of(ga, n->view_src);
+            ga->last_use[k] = std::max(ga->last_use[k], i);
+        }
     }
     arena a(ga->alignment);
-    std::unordered_map<ggml_tensor *, size_t> placed;
     auto place = [&](ggml_tensor * t) {
-        if (!needs_alloc(t) || placed.count(t)) return;
-        const size_t sz = ggml_backend_buft_get_alloc_size(ga->buft, t);
-        const size_t off = a.alloc(sz);
-        placed[t] = off;
-        ga->offsets.push_back({ t, off });
+        if (!needs_alloc(t)) return;
+        const int k = slot_of(ga, t);
+        if (ga->placed[k]) return;
+        const size_t o = a.alloc(ggml_backend_buft_get_alloc_size(ga->buft, t));
+        ga->placed[k] = 1;
+        ga->off[k] = o;
+        ga->offsets.push_back({ t, o });
     };
     for (int i = 0; i < g->n_leafs; i++) place(g->leafs[i]);
-    // frees scheduled per node index
-    std::vector<std::vector<ggml_tensor *>> frees(g->n_nodes);
-    for (int i = 0; i < g->n_nodes; i++) {
+    // frees scheduled per node index: a list per consumer node, built from the last node back so
+    // each list runs in ascending producer order
+    for (int i = g->n_nodes - 2; i >= 0; i--) {
         ggml_tensor * n = g->nodes[i];
-        if (!needs_alloc(n)) continue;
-        if (n->flags & GGML_TENSOR_FLAG_OUTPUT) continue;
-        if (i == g->n_nodes - 1) continue;
-        auto it = last_use.find(n);
-        if (it == last_use.end()) continue; // unconsumed: graph output
-        frees[it->second].push_back(n);
+        if (!needs_alloc(n) || (n->flags & GGML_TENSOR_FLAG_OUTPUT)) continue;
+        const int k = slot_of(ga, n);
+        const int lu = ga->last_use[k];
+        if (lu < 0) continue; // unconsumed: graph output
+        ga->free_next[k] = ga->free_head[lu];
+        ga->free_head[lu] = k;
     }
     const bool reuse = !(ga->buft->iface.no_reuse && ga->buft->iface.no_reuse(ga->buft));
     for (int i = 0; i < g->n_nodes; i++) {
         place(g->nodes[i]);
         if (!reuse) continue;
-        for (ggml_tensor * t : frees[i]) {
+        for (int k = ga->free_head[i]; k >= 0; k = ga->free_next[k]) {
+            ggml_tensor * t = ga->keys[k];
             if (t == g->nodes[i]) continue;
-            a.release(placed[t], ggml_backend_buft_get_alloc_size(ga->buft, t));
+            a.release(ga->off[k], ggml_backend_buft_get_alloc_size(ga->buft, t));
         }
     }
     ga->plan_size = a.peak();

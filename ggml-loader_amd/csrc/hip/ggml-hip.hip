@@ -21,6 +21,7 @@
 #include "kernels.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -42,6 +43,13 @@ struct hip_device {
     // device staging for repacked uploads/downloads
     uint8_t * staging = nullptr;
     size_t staging_size = 0;
+    // pinned host ring for small uploads: tensor_set copies the bytes into it and queues the copy
+    // on the stream without waiting; the ring starts over whenever the stream has drained
+    uint8_t * up_ring = nullptr;
+    size_t up_off = 0;
+    // pinned host landing area for downloads
+    uint8_t * down = nullptr;
+    size_t down_size = 0;
     ggml_backend_buffer_type buft{};
     char name[64] = { 0 };
 };
@@ -80,6 +88,33 @@ uint8_t * staging(hip_device & d, size_t size) {
         HIP_CHECK(hipMalloc(&d.staging, d.staging_size));
     }
     return d.staging;
+}
+
+constexpr size_t UP_RING = (size_t) 4 << 20;        // bytes of the upload ring
+constexpr size_t UP_SMALL = (size_t) 256 << 10;      // uploads up to this size go through the ring
+constexpr size_t DOWN_MAX = (size_t) 16 << 20;       // downloads up to this size land in pinned memory
+
+// the stream has no queued work left: the upload ring can be reused from its start
+void drained(hip_device & d) { d.up_off = 0; }
+
+// a slot of the upload ring for size bytes, or nullptr when it does not fit before the stream drains
+uint8_t * upload_slot(hip_device & d, size_t size) {
+    if (size > UP_SMALL) return nullptr;
+    if (!d.up_ring) HIP_CHECK(hipHostMalloc((void **) &d.up_ring, UP_RING, hipHostMallocDefault));
+    const size_t off = (d.up_off + 255) & ~(size_t) 255;
+    if (off + size > UP_RING) return nullptr;
+    d.up_off = off + size;
+    return d.up_ring + off;
+}
+
+uint8_t * download_area(hip_device & d, size_t size) {
+    if (size > DOWN_MAX) return nullptr;
+    if (size > d.down_size) {
+        if (d.down) HIP_CHECK(hipHostFree(d.down));
+        d.down_size = std::max(size, (size_t) 1 << 20);
+        HIP_CHECK(hipHostMalloc((void **) &d.down, d.down_size, hipHostMallocDefault));
+    }
+    return d.down;
 }
 
 bool is_repacked(int type) { return type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0; }
@@ -136,11 +171,19 @@ void buf_set(ggml_backend_buffer_t b, ggml_tensor * t, const void * data, size_t
             HIP_CHECK(hipMemcpyAsync(st, (const uint8_t *) data + done, n, hipMemcpyHostToDevice, d.stream));
             launch_repack_q(t->type, st, p.qs, p.d, (int64_t) (n / bs), p.first_block + (int64_t) ((off + done) / bs), d.stream);
             HIP_CHECK(hipStreamSynchronize(d.stream));
+            drained(d);
         }
+        return;
+    }
+    if (uint8_t * slot = upload_slot(d, size)) {
+        // the caller's bytes are copied now; the device copy is ordered before later work on the stream
+        memcpy(slot, data, size);
+        HIP_CHECK(hipMemcpyAsync((char *) t->data + off, slot, size, hipMemcpyHostToDevice, d.stream));
         return;
     }
     HIP_CHECK(hipMemcpyAsync((char *) t->data + off, data, size, hipMemcpyHostToDevice, d.stream));
     HIP_CHECK(hipStreamSynchronize(d.stream));
+    drained(d);
 }
 
 void buf_get(ggml_backend_buffer_t b, const ggml_tensor * t, void * data, size_t off, size_t size) {
@@ -156,11 +199,20 @@ void buf_get(ggml_backend_buffer_t b, const ggml_tensor * t, void * data, size_t
             launch_unpack_q(t->type, st, p.qs, p.d, (int64_t) (n / bs), p.first_block + (int64_t) ((off + done) / bs), d.stream);
             HIP_CHECK(hipMemcpyAsync((uint8_t *) data + done, st, n, hipMemcpyDeviceToHost, d.stream));
             HIP_CHECK(hipStreamSynchronize(d.stream));
+            drained(d);
         }
+        return;
+    }
+    if (uint8_t * area = download_area(d, size)) {
+        HIP_CHECK(hipMemcpyAsync(area, (const char *) t->data + off, size, hipMemcpyDeviceToHost, d.stream));
+        HIP_CHECK(hipStreamSynchronize(d.stream));
+        drained(d);
+        memcpy(data, area, size);
         return;
     }
     HIP_CHECK(hipMemcpyAsync(data, (const char *) t->data + off, size, hipMemcpyDeviceToHost, d.stream));
     HIP_CHECK(hipStreamSynchronize(d.stream));
+    drained(d);
 }
 
 void buf_memset(ggml_backend_buffer_t b, ggml_tensor * t, uint8_t v, size_t off, size_t size) {
@@ -177,6 +229,7 @@ void buf_memset(ggml_backend_buffer_t b, ggml_tensor * t, uint8_t v, size_t off,
         HIP_CHECK(hipMemsetAsync((char *) t->data + off, v, size, d.stream));
     }
     HIP_CHECK(hipStreamSynchronize(d.stream));
+    drained(d);
 }
 
 void buf_clear(ggml_backend_buffer_t b, uint8_t v) {
@@ -184,6 +237,7 @@ void buf_clear(ggml_backend_buffer_t b, uint8_t v) {
     hip_device & d = dev(c->device);
     HIP_CHECK(hipMemsetAsync(c->base, v, b->size, d.stream));
     HIP_CHECK(hipStreamSynchronize(d.stream));
+    drained(d);
 }
 
 const char * buft_name(ggml_backend_buffer_type_t t) { return ((hip_device *) t->context)->name; }
@@ -1187,6 +1241,7 @@ void be_free(ggml_backend_t b) {
     hip_backend_ctx * c = (hip_backend_ctx *) b->context;
     dev(c->device);
     HIP_CHECK(hipStreamSynchronize(dev(c->device).stream));
+    drained(dev(c->device));
     c->scratch.release();
     for (hipEvent_t e : c->event_pool) HIP_CHECK(hipEventDestroy(e));
     delete c;
@@ -1212,9 +1267,17 @@ enum ggml_status be_compute(ggml_backend_t b, ggml_cgraph * g) {
     hip_backend_ctx * c = (hip_backend_ctx *) b->context;
     hip_device & d = dev(c->device);
     c->timing = c->profiling && (c->computes++ % c->profile_every) == 0;
+    const auto t0 = std::chrono::steady_clock::now();
     executor ex(*c, g);
     ex.run();
+    if (c->profiling) {
+        // host time spent walking the graph and enqueuing its kernels (the "host_enqueue" entry)
+        prof_entry & e = c->prof["host_enqueue"];
+        e.launches++;
+        e.ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    }
     HIP_CHECK(hipStreamSynchronize(d.stream));
+    drained(d);
     if (c->timing) collect_profile(c);
     return GGML_STATUS_SUCCESS;
 }
@@ -1225,7 +1288,11 @@ void be_set_eval_callback(ggml_backend_t b, ggml_backend_eval_callback cb, void 
     c->cb_user = user;
 }
 
-void be_sync(ggml_backend_t b) { HIP_CHECK(hipStreamSynchronize(dev(((hip_backend_ctx *) b->context)->device).stream)); }
+void be_sync(ggml_backend_t b) {
+    hip_device & d = dev(((hip_backend_ctx *) b->context)->device);
+    HIP_CHECK(hipStreamSynchronize(d.stream));
+    drained(d);
+}
 
 ggml_backend_t hip_init_by_name(const char * params) { return ggml_backend_hip_init(params ? atoi(params) : 0); }
 

@@ -521,10 +521,22 @@ std::vector<float> prefill(const model & m, const hparams & hp, kv_cache & kv, d
 
 // model.cpp:1659-1666: greedy, first index of the maximum wins
 int32_t argmax(const std::vector<float> & logits) {
-    int32_t best = 0;
-    float best_v = logits[0];
-    for (size_t i = 1; i < logits.size(); i++) {
-        if (logits[i] > best_v) { best_v = logits[i]; best = (int32_t) i; }
+    // the first index of the largest value: the maximum from eight independent running maxima (no
+    // loop-carried branch), then its first occurrence; a leading NaN keeps index 0, as the
+    // single-pass compare does
+    const float * v = logits.data();
+    const size_t n = logits.size();
+    float m[8];
+    for (int k = 0; k < 8; k++) m[k] = v[0];
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        for (int k = 0; k < 8; k++) m[k] = v[i + k] > m[k] ? v[i + k] : m[k];
     }
-    return best;
+    float best = v[0];
+    for (int k = 0; k < 8; k++) best = m[k] > best ? m[k] : best;
+    for (; i < n; i++) best = v[i] > best ? v[i] : best;
+    for (size_t j = 0; j < n; j++) {
+        if (v[j] == best) return (int32_t) j;
+    }
+    return 0;
 }

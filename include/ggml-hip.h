@@ -34,6 +34,8 @@ GGML_API void ggml_backend_hip_set_graph_replay(ggml_backend_t backend, bool ena
 
 // Per-kernel timing with HIP events recorded on the backend's own stream. While enabled, every
 // launch of graph_compute is bracketed by events; stats accumulate per kernel name until reset.
+// The entry "host_enqueue" holds the host time each graph_compute spends walking the graph and
+// submitting its kernels (one count per compute).
 GGML_API void ggml_backend_hip_set_profiling(ggml_backend_t backend, bool enable);
 // Restricts the events to kernels whose name starts with prefix (NULL or "" = every kernel), so a
 // timed run can measure one kernel without bracketing every launch.
