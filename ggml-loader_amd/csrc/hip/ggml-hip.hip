@@ -704,11 +704,77 @@ private:
                 break;
             }
         }
+        if (defer_rope(B, members)) {
+            for (int j : members) done_[j] = true;
+            return;
+        }
         {
             prof_scope ps(this, "rope", 0);
             launch_rope_batch(B, st_);
         }
         for (int j : members) done_[j] = true;
+    }
+
+    // A RoPE batch of exactly {Q rotation, K rotation copied into the K cache, V copy into the V
+    // cache} whose rotated Q is read only by a decode attention over those caches, with the new
+    // rows at that attention's last n_q positions: it runs inside the attention's scores kernel
+    // (attn_launch.rope) instead of in a launch of its own.
+    struct pending_rope { int anchor = -1; rope_job q, k, v; };
+    pending_rope prope_;
+
+    bool defer_rope(const rope_batch & B, const std::vector<int> & members) {
+        if (!fuse(FUSE_ATTN) || B.n_jobs != 3 || members.size() != 4) return false;
+        int qi = -1, kc = -1, vc = -1;
+        for (int j : members) {
+            const ggml_tensor * m = g_->nodes[j];
+            if (m->op == GGML_OP_ROPE) {
+                const int u = sole_user(j);
+                const bool copied = u >= 0 && g_->nodes[u]->op == GGML_OP_CPY &&
+                                    std::find(members.begin(), members.end(), u) != members.end();
+                if (!copied) qi = j;
+            } else if (m->op == GGML_OP_CPY) {
+                if (m->src[0]->op == GGML_OP_ROPE) kc = j;
+                else vc = j;
+            }
+        }
+        if (qi < 0 || kc < 0 || vc < 0) return false;
+        int jq = -1, jk = -1, jv = -1;
+        for (int k = 0; k < 3; k++) {
+            const rope_job & J = B.job[k];
+            if (J.dst.data == g_->nodes[qi]->data && J.pos) jq = k;
+            else if (J.dst.data == g_->nodes[kc]->data && J.pos) jk = k;
+            else if (J.dst.data == g_->nodes[vc]->data && !J.pos) jv = k;
+        }
+        if (jq < 0 || jk < 0 || jv < 0) return false;
+        // Q and K rotate with the same positions, frequency factors and parameters (one table of
+        // rotation pairs serves both), over at most the head dimension
+        const rope_job & q = B.job[jq], & k = B.job[jk];
+        if (q.pos != k.pos || q.ff != k.ff || memcmp(&q.p, &k.p, sizeof(rope_params)) != 0 || q.p.n_dims > q.src.ne[0]) return false;
+        // rotated Q -> permute -> the attention anchor (and nothing else)
+        const int p = sole_user(qi);
+        if (p < 0 || g_->nodes[p]->op != GGML_OP_PERMUTE) return false;
+        const int a = sole_user(p);
+        auto it = attn_.find(a);
+        if (a < 0 || it == attn_.end()) return false;
+        const attn_match & M = it->second;
+        const ggml_tensor * kp = M.kp, * vp = M.vp, * qp = M.qp;
+        const ggml_tensor * kn = g_->nodes[kc], * vn = g_->nodes[vc];
+        const int64_t hd = kp->ne[0], n_kv = kp->ne[1], n_head_kv = kp->ne[2], n_q = qp->ne[1], n_head = qp->ne[2];
+        if (qp != g_->nodes[p] || n_q > 4 || n_kv < n_q || kn->type != GGML_TYPE_F16 || vn->type != GGML_TYPE_F16) return false;
+        const int64_t shape_q[3] = { hd, n_head, n_q }, shape_kv[3] = { hd, n_head_kv, n_q };
+        for (int d = 0; d < 3; d++) {
+            if (B.job[jq].src.ne[d] != shape_q[d] || B.job[jk].src.ne[d] != shape_kv[d] ||
+                B.job[jv].src.ne[d] != shape_kv[d] || kn->ne[d] != shape_kv[d] || vn->ne[d] != shape_kv[d]) return false;
+        }
+        // the new rows are the attention's last n_q positions of the same caches
+        if ((const char *) kn->data != (const char *) kp->data + (n_kv - n_q) * kp->nb[1] ||
+            kn->nb[1] != kp->nb[2] || kn->nb[2] != kp->nb[1] || kn->nb[0] != 2) return false;
+        if ((const char *) vn->data != (const char *) vp->data + (n_kv - n_q) * vp->nb[0] ||
+            vn->nb[1] != vp->nb[2] || vn->nb[2] != vp->nb[0] || vn->nb[0] != 2) return false;
+        prope_ = pending_rope{ a, B.job[jq], B.job[jk], B.job[jv] };
+        wrote_.push_back(g_->nodes[kc]);
+        wrote_.push_back(g_->nodes[vc]);
+        return true;
     }
 
     // rms_norm, fused with a following weight multiply (and activation quantization) when possible
@@ -1164,6 +1230,13 @@ private:
         A.out_nb1 = (int64_t) (ctn->nb[1] / 4);
         A.n_kv = n_kv; A.n_q = n_q; A.n_head = n_head; A.n_head_kv = n_head_kv; A.hd = hd;
         A.scale = M.scale;
+        if (prope_.anchor == M.kq) {
+            A.rope = 1;
+            A.rq = prope_.q;
+            A.rk = prope_.k;
+            A.rv = prope_.v;
+            prope_.anchor = -1;
+        }
         const double bytes = (double) n_kv * n_head_kv * hd * 2 * 2 + (double) n_head * hd * n_q * 8 +
                              (mask ? (double) n_kv * n_q * ggml_type_size(mask->type) : 0.0);
         if (n_q > 4) {

@@ -29,6 +29,7 @@
 // Scratch: scores f32 [n_q][n_head][n_kv], row statistics f32 [n_q][n_head][2] (M, 1/S),
 // partials f64 [pv chunks][n_q][n_head][hd].
 #include "kernels.h"
+#include "tview_ops.h"
 
 #include "ggml.h"
 
@@ -71,8 +72,10 @@ __device__ __forceinline__ float mask_at(const attn_launch & A, int q, int t) {
 
 // stage rows [t0, t0+nt) of a [pos][hd] F16 cache view (row stride nb_pos halves) into LDS rows of
 // STRIDE dwords; rows nt..ROWS-1 are zero. Every load is issued before the first LDS store.
-template <int HD, int STRIDE, int ROWS>
-__device__ __forceinline__ void stage_rows(uint32_t * dst, const __half * base, int64_t nb_pos, int t0, int nt) {
+struct no_work { __device__ void operator()() const {} };
+
+template <int HD, int STRIDE, int ROWS, typename F = no_work>
+__device__ __forceinline__ void stage_rows(uint32_t * dst, const __half * base, int64_t nb_pos, int t0, int nt, F while_loading = F()) {
     constexpr int PIECES = HD / 8;                                   // 16-byte pieces per row
     constexpr int ITER = ROWS * PIECES / ATT_THREADS;
     uint4 v[ITER];
@@ -83,6 +86,7 @@ __device__ __forceinline__ void stage_rows(uint32_t * dst, const __half * base, 
         v[it] = make_uint4(0, 0, 0, 0);
         if (r < nt) v[it] = *(const uint4 *) (base + (int64_t) (t0 + r) * nb_pos + c * 8);
     }
+    while_loading();
 #pragma unroll
     for (int it = 0; it < ITER; it++) {
         const int pc = threadIdx.x + it * ATT_THREADS;
@@ -105,12 +109,41 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
     const int n_q = A.n_q;
     const attn_scratch S = scratch_of(A);
 
-    stage_rows<HD, STRIDE, ATT_CHUNK>(s_k, A.k + (int64_t) kvh * A.k_nb1, A.k_nb2, t0, nt);
+    // RoPE: the (cos, sin) of every rotation pair of the new tokens, one pair per thread, while the
+    // chunk's K rows are in flight (Q and K rotate with the same positions and parameters)
+    __shared__ float2 s_cs[ATT_MAX_Q][HD / 2];
+    stage_rows<HD, STRIDE, ATT_CHUNK>(s_k, A.k + (int64_t) kvh * A.k_nb1, A.k_nb2, t0, nt, [&]() {
+        if (!A.rope) return;
+        const int half = A.rq.p.n_dims / 2;
+        for (int i = threadIdx.x; i < n_q * half; i += ATT_THREADS) {
+            float c, sn;
+            rope_pair_cs(A.rq.p, A.rq.ff, A.rq.pos[i / half], i % half, c, sn);
+            s_cs[i / half][i % half] = make_float2(c, sn);
+        }
+    });
+    if (A.rope) __syncthreads();   // s_cs complete
     for (int i = threadIdx.x; i < n_q * G * HD; i += ATT_THREADS) {
         const int pr = i / HD, d = i % HD;
         const int q = pr / G, g = pr % G;
-        const float v = A.q[(int64_t) (kvh * G + g) * A.q_nb1 + (int64_t) q * A.q_nb2 + d];
-        s_q[pr][d] = __half2float(__float2half_rn(v));
+        const float v = A.rope ? rope_value_cs(A.rq, kvh * G + g, q, 0, d, s_cs[q])
+                               : A.q[(int64_t) (kvh * G + g) * A.q_nb1 + (int64_t) q * A.q_nb2 + d];
+        s_q[pr][d] = __half2float(__float2half_rn(as_f32(v)));
+    }
+    if (A.rope) {
+        // the new positions of this chunk: K rotated into the cache and over its staged row, V appended
+        const int first_new = A.n_kv - n_q;
+        if (first_new + n_q > t0 && first_new < t0 + nt) {
+            __syncthreads();   // the staged rows are in LDS
+            for (int i = threadIdx.x; i < n_q * HD; i += ATT_THREADS) {
+                const int t = i / HD, d = i % HD;
+                const int pos = first_new + t;
+                if (pos < t0 || pos >= t0 + nt) continue;
+                const float kr = rope_value_cs(A.rk, kvh, t, 0, d, s_cs[t]);
+                st(at(A.rk.dst, d, kvh, t, 0), GGML_TYPE_F16, kr);
+                ((__half *) (s_k + (pos - t0) * STRIDE))[d] = __float2half_rn(as_f32(kr));
+                st(at(A.rv.dst, d, kvh, t, 0), GGML_TYPE_F16, ld(at(A.rv.src, d, kvh, t, 0), A.rv.src.type));
+            }
+        }
     }
     __syncthreads();
 

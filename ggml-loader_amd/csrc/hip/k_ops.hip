@@ -4,52 +4,12 @@
 // scales by 1/sqrtf(mean + eps) before the weight multiply; RoPE iterates theta *= theta_scale
 // in float from theta = pos; softmax exponentiates w - max with the sum kept in double.
 #include "kernels.h"
+#include "tview_ops.h"
 
 #include "ggml.h"
 
 // ---------------------------------------------------------------------------------------------
 // typed element access
-
-__device__ __forceinline__ float ld(const char * p, int type) {
-    switch (type) {
-        case GGML_TYPE_F32: return *(const float *) p;
-        case GGML_TYPE_F16: return __half2float(*(const __half *) p);
-        case GGML_TYPE_BF16: return __uint_as_float(((uint32_t) *(const uint16_t *) p) << 16);
-        case GGML_TYPE_I32: return (float) *(const int32_t *) p;
-        default: return 0.0f;
-    }
-}
-
-__device__ __forceinline__ void st(char * p, int type, float v) {
-    switch (type) {
-        case GGML_TYPE_F32: *(float *) p = v; break;
-        case GGML_TYPE_F16: *(__half *) p = __float2half_rn(as_f32(v)); break;
-        case GGML_TYPE_BF16: {
-            uint32_t u = __float_as_uint(as_f32(v));
-            if ((u & 0x7fffffffu) > 0x7f800000u) u = (u >> 16) | 64u;
-            else u = (u + (0x7fffu + ((u >> 16) & 1u))) >> 16;
-            *(uint16_t *) p = (uint16_t) u;
-            break;
-        }
-        case GGML_TYPE_I32: *(int32_t *) p = (int32_t) v; break;
-        default: break;
-    }
-}
-
-struct idx4 { int64_t i0, i1, i2, i3; };
-
-__device__ __forceinline__ idx4 unflatten(int64_t i, const int64_t ne[4]) {
-    idx4 r;
-    r.i0 = i % ne[0]; i /= ne[0];
-    r.i1 = i % ne[1]; i /= ne[1];
-    r.i2 = i % ne[2]; i /= ne[2];
-    r.i3 = i;
-    return r;
-}
-
-__device__ __forceinline__ char * at(const tview & t, int64_t i0, int64_t i1, int64_t i2, int64_t i3) {
-    return t.data + i0 * t.nb[0] + i1 * t.nb[1] + i2 * t.nb[2] + i3 * t.nb[3];
-}
 
 static int64_t nelem(const tview & t) { return t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3]; }
 
@@ -391,21 +351,6 @@ void launch_get_rows(const tview & a, const tview & ids, const tview & dst, cons
 
 // ---------------------------------------------------------------------------------------------
 // RoPE: one thread per rotated pair of one (head, token) row
-
-__device__ __forceinline__ void rope_cs(float theta_extrap, const rope_params & p, int i0, float & c, float & s) {
-    const float theta_interp = p.freq_scale * theta_extrap;
-    float theta = theta_interp;
-    float mscale = p.attn_factor;
-    if (p.ext_factor != 0.0f) {
-        const float y = (i0 / 2 - p.corr_dims[0]) / fmaxf(0.001f, p.corr_dims[1] - p.corr_dims[0]);
-        const float ramp = 1 - fminf(1, fmaxf(0, y));
-        const float ramp_mix = ramp * p.ext_factor;
-        theta = theta_interp * (1 - ramp_mix) + theta_extrap * ramp_mix;
-        mscale *= 1.0f + 0.1f * log_cr(1.0f / p.freq_scale);
-    }
-    c = cos_cr(theta) * mscale;
-    s = sin_cr(theta) * mscale;
-}
 
 // pair li of a RoPE job (row-major over pairs of the src rows); the result is stored in dst's type
 __device__ __forceinline__ void rope_pair(const rope_job & J, int64_t li) {

@@ -238,6 +238,12 @@ struct attn_launch {
     int64_t        scratch_bytes;
     // quantized copy of out for the o-projection (Q8_0 semantics), optional
     q8_act         out_q;
+    // RoPE of the new tokens folded in (rope set; decode only): Q is read from rq.src and rotated
+    // in the scores kernel (the rotated Q is not stored); the workgroup whose position chunk holds
+    // new position n_kv - n_q + t rotates K row t of rk.src into rk.dst (the K cache) and copies V
+    // row t of rv.src into rv.dst (the V cache)
+    int            rope;
+    rope_job       rq, rk, rv;
 };
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd);
 void launch_attn_decode(const attn_launch & A, hipStream_t st);

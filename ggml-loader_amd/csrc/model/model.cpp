@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <emmintrin.h>
 
 // ---- gguf metadata helpers (model.cpp:15-59) ----
 
@@ -521,17 +522,21 @@ std::vector<float> prefill(const model & m, const hparams & hp, kv_cache & kv, d
 
 // model.cpp:1659-1666: greedy, first index of the maximum wins
 int32_t argmax(const std::vector<float> & logits) {
-    // the first index of the largest value: the maximum from eight independent running maxima (no
-    // loop-carried branch), then its first occurrence; a leading NaN keeps index 0, as the
-    // single-pass compare does
+    // the first index of the largest value: the maximum from eight running maxima in two SSE
+    // registers (no loop-carried branch), then its first occurrence; a leading NaN keeps index 0,
+    // as the single-pass compare does
     const float * v = logits.data();
     const size_t n = logits.size();
-    float m[8];
-    for (int k = 0; k < 8; k++) m[k] = v[0];
+    // maxps(a, b) returns a > b ? a : b, so a NaN value never replaces a running maximum
+    __m128 m0 = _mm_set1_ps(v[0]), m1 = m0;
     size_t i = 0;
     for (; i + 8 <= n; i += 8) {
-        for (int k = 0; k < 8; k++) m[k] = v[i + k] > m[k] ? v[i + k] : m[k];
+        m0 = _mm_max_ps(_mm_loadu_ps(v + i), m0);
+        m1 = _mm_max_ps(_mm_loadu_ps(v + i + 4), m1);
     }
+    float m[8];
+    _mm_storeu_ps(m, m0);
+    _mm_storeu_ps(m + 4, m1);
     float best = v[0];
     for (int k = 0; k < 8; k++) best = m[k] > best ? m[k] : best;
     for (; i < n; i++) best = v[i] > best ? v[i] : best;

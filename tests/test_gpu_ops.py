@@ -316,6 +316,61 @@ def test_rope_and_kv_append_batched(hip, cpu, mode, hd, n_new):
     assert np.array_equal(ref[2].reshape(n_ctx, n_head_kv, hd)[n_past:n_past + n_new], v.astype(np.float16))
 
 
+@pytest.mark.parametrize("mode,hd,n_head,n_head_kv", [(gl.ROPE_NORMAL, 128, 24, 8), (gl.ROPE_NEOX, 96, 8, 8),
+                                                     (gl.ROPE_NEOX, 64, 8, 2)])
+@pytest.mark.parametrize("n_new", [1, 3])
+def test_attention_with_rope_and_kv_append(hip, cpu, mode, hd, n_head, n_head_kv, n_new):
+    """RoPE(Q), RoPE(K) -> F16 cache, V -> F16 cache, then decode attention over the caches (the
+    reference's per-layer order, model.cpp:1389-1444): on the fused path the rotations and the
+    cache writes happen inside the attention's scores kernel, with the same floats and cache rows."""
+    n_ctx, n_past = 140, 129          # the new rows straddle a 64-position chunk boundary for n_new = 3
+    n_kv = n_past + n_new
+    r = rng(60 + hd + n_new)
+    q = r.standard_normal((n_new, n_head, hd)).astype(np.float32)
+    k = r.standard_normal((n_new, n_head_kv, hd)).astype(np.float32) * 2
+    v = r.standard_normal((n_new, n_head_kv, hd)).astype(np.float32) * 2
+    pos = np.arange(n_past, n_kv, dtype=np.int32)
+    cache0 = r.standard_normal((2, n_ctx, n_head_kv, hd)).astype(np.float16)
+    mask = np.zeros((n_new, n_kv), dtype=np.float32)
+    for i in range(n_new):
+        mask[i, n_past + i + 1:] = -np.inf
+
+    def run(backend, fusion):
+        with Graph() as g:
+            kc = g.tensor(gl.F16, hd, n_head_kv, n_ctx, data=cache0[0])
+            vc = g.tensor(gl.F16, hd, n_head_kv, n_ctx, data=cache0[1])
+            pt = g.tensor(gl.I32, n_new, data=pos)
+            m = g.tensor(gl.F32, n_kv, n_new, data=mask)
+            qr = g.rope_ext(g.tensor(gl.F32, hd, n_head, n_new, data=q), pt, None, hd, mode, 4096, 10000.0, 1.0, 0.0, 1.0, 0.0, 0.0)
+            kr = g.rope_ext(g.tensor(gl.F32, hd, n_head_kv, n_new, data=k), pt, None, hd, mode, 4096, 10000.0, 1.0, 0.0, 1.0, 0.0, 0.0)
+            nb1, nb2 = hd * 2, hd * n_head_kv * 2
+            ck = g.cpy(kr, g.view_3d(kc, hd, n_head_kv, n_new, nb1, nb2, n_past * nb2))
+            cv = g.cpy(g.tensor(gl.F32, hd, n_head_kv, n_new, data=v), g.view_3d(vc, hd, n_head_kv, n_new, nb1, nb2, n_past * nb2))
+            K = g.permute(g.view_3d(kc, hd, n_head_kv, n_kv, nb1, nb2, 0), 0, 2, 1, 3)
+            V_full = g.view_3d(vc, hd, n_head_kv, n_kv, nb1, nb2, 0)
+            KQ = g.soft_max_ext(g.mul_mat(K, g.permute(qr, 0, 2, 1, 3)), m, 1.0 / np.sqrt(hd), 0.0)
+            KQV = g.mul_mat(g.cont_3d(g.permute(V_full, 1, 2, 0, 3), n_kv, hd, n_head_kv), KQ)
+            out = g.cont_2d(g.permute(KQV, 0, 2, 1, 3), hd * n_head, n_new)
+            gl.libs()["hip"].ggml_backend_hip_set_fusion(hip, fusion)
+            try:
+                if backend is hip:
+                    o, names = profiled(hip, lambda: g.compute(backend, [ck, cv, out])[2])
+                else:
+                    o, names = g.compute(backend, [ck, cv, out])[2], set()
+            finally:
+                gl.libs()["hip"].ggml_backend_hip_set_fusion(hip, True)
+            return o, g.read(kc, np.float16), g.read(vc, np.float16), names
+
+    ref = run(cpu, True)
+    for fusion in (True, False):
+        got = run(hip, fusion)
+        assert np.array_equal(got[0], ref[0]), (fusion, rel_err(got[0], ref[0]))
+        assert np.array_equal(got[1].view(np.uint16), ref[1].view(np.uint16)), fusion
+        assert np.array_equal(got[2].view(np.uint16), ref[2].view(np.uint16)), fusion
+        if fusion:
+            assert "rope" not in got[3] and "attn_decode" in got[3], got[3]
+
+
 def test_soft_max_masked(hip, cpu):
     n_kv, n_q, n_head = 300, 3, 5
     x = rng(12).standard_normal((n_head, n_q, n_kv)).astype(np.float32) * 4
