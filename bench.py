@@ -14,6 +14,7 @@ Prints one JSON line (see the "config", "roofline" and "cpu_baseline" keys).
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import importlib.util
 import json
 import os
@@ -38,43 +39,89 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+# the position each decode configuration is quoted at
+DEFAULT_N_PAST = {"llama3b": 2048, "qwen3": 8192, "qwen3moe": 4096, "phi3mini": 2048}
+WNAME = {2: "q4_0", 8: "q8_0", 12: "q4_K"}
+
+
+def model_path_of(gl, args):
+    cfg = gl.CONFIGS[args.config]
+    shared = "_sharedexp" if cfg.get("n_expert") else ""
+    return os.path.join(args.model_dir, f"{args.config}_{WNAME[cfg['wtype']]}_seed{args.seed}{shared}.gguf")
+
+
 def ensure_model(gl, path, config, seed):
     if os.path.exists(path):
         return
     os.makedirs(os.path.dirname(path), exist_ok=True)
     t = time.time()
-    gl.synth_model(path + ".tmp", seed=seed, n_threads=min(16, os.cpu_count() or 1), **gl.CONFIGS[config])
+    cfg = dict(gl.CONFIGS[config])
+    if cfg.get("n_expert"):
+        cfg["share_experts"] = True   # layer 0's experts in every layer (routers stay per layer)
+    log(f"[bench] writing synthetic {config} model {path}")
+    gl.synth_model(path + ".tmp", seed=seed, n_threads=min(16, os.cpu_count() or 1), **cfg)
     os.replace(path + ".tmp", path)
     log(f"[bench] wrote synthetic {config} model {path} in {time.time() - t:.1f}s")
 
 
-def cpu_baseline(gl, model_path, n_pos, token, seconds, threads):
-    """The oracle (CPU restatement of ggml-cpu, this repository's oracle/) timed on the host cores
-    on a bounded sample of the same workload: decode steps at the same position, one untimed warmup
-    step, at each thread count (the reference's cmd_bench hard-codes 8, cmd_bench.cpp:107)."""
+def describe(cfg, n_past, batch):
+    """The workload of a decode configuration in words."""
+    arch = cfg["arch"]
+    ffn = (f"{cfg['n_expert']} experts x FFN {cfg['n_ff_exp']}, top-{cfg['n_expert_used']}" if cfg.get("n_expert")
+           else f"FFN {cfg['n_ff']}")
+    toks = "1 token" if batch == 1 else f"{batch} tokens"
+    return (f"{arch} decode, {toks} at position {n_past}, batch {batch} (hidden {cfg['n_embd']}, "
+            f"{cfg['n_layer']} layers, {cfg['n_head']}/{cfg['n_head_kv']} heads, head_dim {cfg['head_dim']}, {ffn}, "
+            f"vocab {cfg['n_vocab']}, {WNAME[cfg['wtype']].upper()})")
+
+
+def oracle_helpers():
+    """tests/gl.py, whose oracle() registers the oracle's CPU backend (the cpu_baseline leg only)."""
     spec = importlib.util.spec_from_file_location("gl_test_helpers", os.path.join(ROOT, "tests", "gl.py"))
     helpers = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(helpers)
-    helpers.oracle()  # registers the CPU backend
+    helpers.oracle()
+    return helpers
+
+
+def cpu_baseline(gl, model_path, n_pos, tokens, seconds, threads):
+    """The oracle (CPU restatement of ggml-cpu, this repository's oracle/) timed on the host cores
+    on a bounded sample of the same workload: steps of len(tokens) new tokens at the same position,
+    one untimed warmup step, at each thread count (the reference's cmd_bench hard-codes 8,
+    cmd_bench.cpp:107)."""
+    oracle_helpers()
+    batch = len(tokens)
     runs = {}
     for nt in threads:
-        with gl.Session(model_path, "cpu", n_ctx=n_pos + 2, n_threads=nt) as c:
+        with gl.Session(model_path, "cpu", n_ctx=n_pos + batch + 1, n_threads=nt) as c:
             c.kv_fill_random(n_pos, seed=3)
-            _, t1 = c.decode_loop(n_pos, token, 1, fixed_pos=True)  # warmup, also sizes the sample
+
+            def steps(k):
+                if batch == 1:
+                    return c.decode_loop(n_pos, int(tokens[0]), k, fixed_pos=True)[1]
+                t = time.perf_counter()
+                for _ in range(k):
+                    c.forward(n_pos, tokens)
+                return time.perf_counter() - t
+
+            t1 = steps(1)  # warmup, also sizes the sample
             n = max(1, min(64, int(seconds / len(threads) / max(t1, 1e-6))))
-            _, t = c.decode_loop(n_pos, token, n, fixed_pos=True)
-        runs[nt] = (n / t, n, t)
-        log(f"[bench] cpu baseline {nt} threads: {n} steps in {t:.2f}s -> {n / t:.2f} tok/s")
+            t = steps(n)
+        runs[nt] = (n * batch / t, n, t)
+        log(f"[bench] cpu baseline {nt} threads: {n} steps in {t:.2f}s -> {n * batch / t:.2f} tok/s")
     main_nt = threads[0]
     v, n, t = runs[main_nt]
+    what = "decode steps" if batch == 1 else f"{batch}-token steps"
     return {"value": round(v, 3), "unit": "tok/s", "cores": main_nt, "kind": "port",
-            "sample": f"{n} decode steps at position {n_pos} ({t:.1f}s) of the same synthetic model on the oracle/ "
+            "sample": f"{n} {what} at position {n_pos} ({t:.1f}s) of the same synthetic model on the oracle/ "
                       f"CPU restatement of ggml-cpu (restated ggml-cpu semantics; upstream ggml unavailable offline), "
                       f"{main_nt} threads",
             "by_threads": {str(k): round(r[0], 3) for k, r in runs.items()}}
 
 
-TRAFFIC_JSON = os.path.join(ROOT, "profiles", "gemv_q4_0_llama3b_decode_traffic.json")
+def traffic_json(wname, config):
+    """HBM bytes per launch of the dominant kernel, from rocprofv3 --pmc runs (profiles/)."""
+    return os.path.join(ROOT, "profiles", f"gemv_{wname}_{config}_decode_traffic.json")
 
 
 def summarize_pmc(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_mb, kernel_prefix):
@@ -137,8 +184,8 @@ def prefill_bench(gl, args):
     prefill of a 512-token prompt for the phi3 config, model.cpp:1624-1657, which calls forward_step
     once for the hip backend). Prints its own JSON line; the default run's line is the decode metric."""
     cfg = gl.CONFIGS[args.config]
-    wname = {gl.Q4_0: "q4_0", gl.Q8_0: "q8_0", gl.Q4_K: "q4_K"}[cfg["wtype"]]
-    model_path = os.path.join(args.model_dir, f"{args.config}_{wname}_seed{args.seed}.gguf")
+    wname = WNAME[cfg["wtype"]]
+    model_path = model_path_of(gl, args)
     ensure_model(gl, model_path, args.config, args.seed)
     import numpy as np
     n = args.prefill
@@ -174,14 +221,121 @@ def prefill_bench(gl, args):
     }), flush=True)
 
 
+def gemv_bench(gl, args):
+    """--gemv: BASELINE.json configs[0], one quantized GEMV y = W x (ggml_mul_mat) with W 4096 x 4096
+    drawn from N(0, 0.02) and quantized to Q4_0, x f32 N(0, 1). One graph holds --gemv-copies
+    independent GEMVs, each with its own copy of W and its own x, so that consecutive launches read
+    weights that are not in the 256 MB Infinity Cache (the copies together are larger). A step is one
+    GEMV; its algorithmic bytes are W + x + y."""
+    import numpy as np
+    K = N = 4096
+    R = args.gemv_copies
+    core, hipl, loader = gl.libs()["core"], gl.libs()["hip"], gl.libs()["loader"]
+    vp = lambda a: a.ctypes.data_as(C.c_void_p)
+    w = np.empty(K * N, dtype=np.float32)
+    fp = lambda a: a.ctypes.data_as(C.POINTER(C.c_float))
+    loader.gl_fill_normal(fp(w), w.size, args.seed, 0, 0.0, 0.02)
+    wq = np.empty(core.ggml_row_size(gl.Q4_0, K) * N, dtype=np.uint8)
+    core.ggml_quantize_chunk(gl.Q4_0, vp(w), vp(wq), 0, N, K, None)
+    xs = np.empty((R, K), dtype=np.float32)
+    loader.gl_fill_normal(fp(xs), xs.size, args.seed + 1, 0, 0.0, 1.0)
+
+    def graph(backend, copies):
+        ctx = core.ggml_init(gl.ggml_init_params(copies * 4 * core.ggml_tensor_overhead() + core.ggml_graph_overhead()
+                                                 + (1 << 20), None, True))
+        ws = [core.ggml_new_tensor_2d(ctx, gl.Q4_0, K, N) for _ in range(copies)]
+        xt = [core.ggml_new_tensor_2d(ctx, gl.F32, K, 1) for _ in range(copies)]
+        ys = [core.ggml_mul_mat(ctx, ws[r], xt[r]) for r in range(copies)]
+        gf = core.ggml_new_graph(ctx)
+        for y in ys:
+            core.ggml_set_output(y)
+            core.ggml_build_forward_expand(gf, y)
+        buf = core.ggml_backend_alloc_ctx_tensors(ctx, backend)
+        for r in range(copies):
+            core.ggml_backend_tensor_set(ws[r], vp(wq), 0, wq.nbytes)
+            core.ggml_backend_tensor_set(xt[r], vp(xs[r]), 0, K * 4)
+        return ctx, gf, buf, ys
+
+    be = gl.hip_backend(0)
+    ctx, gf, buf, ys = graph(be, R)
+    for _ in range(args.warmup):
+        assert core.ggml_backend_graph_compute(be, gf) == 0
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        assert core.ggml_backend_graph_compute(be, gf) == 0
+    secs = time.perf_counter() - t
+    hipl.ggml_backend_hip_set_profile_filter(be, b"")
+    hipl.ggml_backend_hip_reset_profile(be)
+    hipl.ggml_backend_hip_set_profiling(be, True)
+    for _ in range(args.breakdown_steps):
+        assert core.ggml_backend_graph_compute(be, gf) == 0
+    hipl.ggml_backend_hip_set_profiling(be, False)
+    prof = gl.profile(be)
+    prof.pop("host_enqueue", None)
+    y0 = np.empty(N, dtype=np.float32)
+    core.ggml_backend_tensor_get(ys[0], vp(y0), 0, N * 4)
+    core.ggml_backend_buffer_free(buf)
+    core.ggml_free(ctx)
+    core.ggml_backend_free(be)
+
+    n_gemv = args.steps * R
+    us_gemv = 1e6 * secs / n_gemv
+    alg = wq.nbytes + K * 4 + N * 4
+    for k, (cnt, ms, by) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
+        log(f"[bench]   {k:22s} {cnt / (args.breakdown_steps * R):5.2f}/GEMV {ms / cnt * 1e3:8.2f} us/launch")
+    g = prof.get("gemv_q4_0")
+    k_us = g[1] / g[0] * 1e3 if g else None
+    log(f"[bench] gemv 4096x4096 Q4_0: {us_gemv:.2f} us per GEMV (wall, {R} copies), kernel {k_us:.2f} us "
+        f"-> {alg / (k_us * 1e-6) / 1e9:.1f} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        oracle_helpers()
+        cb = core.ggml_backend_init_by_name(b"CPU", str(min(16, os.cpu_count() or 1)).encode())
+        cctx, cgf, cbuf, cys = graph(cb, 1)
+        assert core.ggml_backend_graph_compute(cb, cgf) == 0
+        yc = np.empty(N, dtype=np.float32)
+        core.ggml_backend_tensor_get(cys[0], vp(yc), 0, N * 4)
+        n = 0
+        t = time.perf_counter()
+        while time.perf_counter() - t < min(args.cpu_seconds, 10.0):
+            assert core.ggml_backend_graph_compute(cb, cgf) == 0
+            n += 1
+        ct = time.perf_counter() - t
+        core.ggml_backend_buffer_free(cbuf)
+        core.ggml_free(cctx)
+        core.ggml_backend_free(cb)
+        err = float(np.max(np.abs(y0 - yc) / np.maximum(np.abs(yc), 1e-3)))
+        log(f"[bench] cpu baseline: {n} GEMVs in {ct:.2f}s; max rel err of the GPU result {err:.2e}")
+        cpu = {"value": round(alg * n / ct / 1e9, 3), "unit": "GB/s", "cores": min(16, os.cpu_count() or 1),
+               "kind": "port", "us_per_gemv": round(1e6 * ct / n, 1),
+               "sample": f"{n} GEMVs ({ct:.1f}s) of the same W and x on the oracle/ CPU restatement of ggml-cpu",
+               "gpu_max_rel_err": err}
+    print(json.dumps({
+        "metric": "quant-GEMV HBM GB/s (4096x4096 Q4_0 ggml_mul_mat)", "value": round(alg / (k_us * 1e-6) / 1e9, 1),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "us_per_gemv_wall": round(us_gemv, 3), "higher_is_better": True, "dtype": "int8",
+        "data": "synthetic (W ~ N(0,0.02) quantized to Q4_0, x ~ N(0,1), seeded)",
+        "config": {"workload": f"C1: y = W x, W 4096x4096 Q4_0, x f32; {R} weight copies in rotation",
+                   "bytes_per_gemv": alg},
+        "roofline": {"bound": "hbm", "achieved": round(alg / (k_us * 1e-6) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(alg / (k_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "us_per_launch": round(k_us, 3)},
+        "cpu_baseline": cpu,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="llama3b")
-    ap.add_argument("--n-past", type=int, default=2048)
+    ap.add_argument("--n-past", type=int, default=None, help="KV positions before the step (default: per config)")
+    ap.add_argument("--batch", type=int, default=1, help="new tokens per decode step")
     ap.add_argument("--prefill", type=int, default=0, help="time forward_step over this many prompt tokens instead")
+    ap.add_argument("--gemv", action="store_true", help="time the single 4096x4096 Q4_0 GEMV instead")
+    ap.add_argument("--gemv-copies", type=int, default=40, help="weight copies the --gemv graph rotates over")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--model-dir", default=os.environ.get("GL_BENCH_DIR", "/tmp/gl_bench"))
     ap.add_argument("--breakdown-steps", type=int, default=10, help="untimed steps with every kernel timed")
@@ -211,18 +365,40 @@ def main():
     if args.prefill:
         prefill_bench(gl, args)
         return
+    if args.gemv:
+        gemv_bench(gl, args)
+        return
+    decode_bench(gl, args)
+
+
+def decode_bench(gl, args):
+    """A step is one forward_step of --batch new tokens at position n_past (the same position every
+    step) followed, at batch 1, by the greedy argmax: the reference's cmd_bench tg loop body."""
+    import numpy as np
     cfg = gl.CONFIGS[args.config]
-    wname = {gl.Q4_0: "q4_0", gl.Q8_0: "q8_0", gl.Q4_K: "q4_K"}[cfg["wtype"]]
-    model_path = os.path.join(args.model_dir, f"{args.config}_{wname}_seed{args.seed}.gguf")
+    wname = WNAME[cfg["wtype"]]
+    model_path = model_path_of(gl, args)
     ensure_model(gl, model_path, args.config, args.seed)
 
-    n_past = args.n_past
+    n_past = args.n_past if args.n_past is not None else DEFAULT_N_PAST.get(args.config, 2048)
+    batch = args.batch
     token = 12345 % cfg["n_vocab"]
+    tokens = np.random.default_rng(args.seed).integers(0, cfg["n_vocab"], batch).astype(np.int32)
+    tokens[0] = token
     hipl = gl.libs()["hip"]
     dominant = "gemv_" + wname
-    with gl.Session(model_path, "hip", n_ctx=n_past + 2) as s:
+    with gl.Session(model_path, "hip", n_ctx=n_past + batch + 1) as s:
         s.kv_fill_random(n_past, seed=3)
-        s.decode_loop(n_past, token, args.warmup, fixed_pos=True)
+
+        def steps(k):
+            if batch == 1:
+                return s.decode_loop(n_past, token, k, fixed_pos=True)[1]
+            t = time.perf_counter()
+            for _ in range(k):
+                s.forward(n_past, tokens)
+            return time.perf_counter() - t
+
+        steps(args.warmup)
 
         # timed region: K steps. In every 10th step the dominant kernel's launches (and only those)
         # carry HIP events stamped by their own dispatches on the backend's stream, so its launch
@@ -232,18 +408,18 @@ def main():
         hipl.ggml_backend_hip_set_profile_sampling(s.backend, PROFILE_EVERY)
         hipl.ggml_backend_hip_reset_profile(s.backend)
         hipl.ggml_backend_hip_set_profiling(s.backend, True)
-        _, secs = s.decode_loop(n_past, token, args.steps, fixed_pos=True)
+        secs = steps(args.steps)
         hipl.ggml_backend_hip_set_profiling(s.backend, False)
         hipl.ggml_backend_hip_set_profile_sampling(s.backend, 1)
         timed = gl.profile(s.backend)
-        value = args.steps / secs
+        value = args.steps * batch / secs
         log(f"[bench] {args.steps} steps in {secs:.4f}s -> {value:.1f} tok/s ({1000 * secs / args.steps:.3f} ms/step)")
 
         # untimed breakdown: every kernel bracketed
         hipl.ggml_backend_hip_set_profile_filter(s.backend, b"")
         hipl.ggml_backend_hip_reset_profile(s.backend)
         hipl.ggml_backend_hip_set_profiling(s.backend, True)
-        s.decode_loop(n_past, token, args.breakdown_steps, fixed_pos=True)
+        steps(args.breakdown_steps)
         hipl.ggml_backend_hip_set_profiling(s.backend, False)
         prof = gl.profile(s.backend)
         weights_bytes = s.get("weights_bytes")
@@ -261,13 +437,15 @@ def main():
     timed_steps = (args.steps + PROFILE_EVERY - 1) // PROFILE_EVERY
     # HBM bytes per launch measured by rocprofv3 --pmc on this workload (profiles/, see its summary)
     traffic = None
-    if os.path.exists(TRAFFIC_JSON):
-        traffic = json.load(open(TRAFFIC_JSON))["traffic_bytes_per_launch"]
+    tj = traffic_json(wname, args.config)
+    if batch == 1 and os.path.exists(tj):
+        traffic = json.load(open(tj))["traffic_bytes_per_launch"]
     gemv = [v for k, v in timed.items() if k.startswith(dominant)]
     g_launch = sum(v[0] for v in gemv)
     g_ms = sum(v[1] for v in gemv)
     g_bytes = sum(v[2] for v in gemv)
     achieved = g_bytes / (g_ms * 1e-3) / 1e9 if g_ms > 0 else 0.0
+    moe = bool(cfg.get("n_expert"))
     roofline = {
         "bound": "hbm",
         "achieved": round(achieved, 1),
@@ -275,24 +453,33 @@ def main():
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBS, 4),
         "traffic": traffic,
-        "kernel": f"{dominant}* (every quantized-GEMV launch of a step: QKV, O+residual, gate/up+SwiGLU, "
-                  "down+residual, LM head)",
+        "kernel": f"{dominant}* (every quantized-GEMV launch of a step: QKV, O+residual, "
+                  + ("routed-expert gate/up+SwiGLU and down (mul_mat_id)" if moe else "gate/up+SwiGLU, down+residual")
+                  + ", LM head)",
         "launches_per_step": round(g_launch / timed_steps, 2),
         "bytes_per_launch": round(g_bytes / g_launch) if g_launch else None,
         "us_per_launch": round(g_ms / g_launch * 1e3, 3) if g_launch else None,
         "share_of_step": round((g_ms / timed_steps) / (secs * 1e3 / args.steps), 4),
     }
+    if moe and batch > 1:
+        roofline["bytes_note"] = ("mul_mat_id launches count the selected experts' bytes once per (token, slot) "
+                                  "column, so repeated experts are counted again")
 
     cpu = None
     if not args.no_cpu_baseline:
         try:
             n_cpu = min(16, os.cpu_count() or 1)
-            cpu = cpu_baseline(gl, model_path, n_past, token, args.cpu_seconds, [n_cpu, 8] if n_cpu != 8 else [8])
+            cpu = cpu_baseline(gl, model_path, n_past, tokens, args.cpu_seconds, [n_cpu, 8] if n_cpu != 8 else [8])
         except Exception as e:  # the baseline is reported, never required
             log(f"[bench] cpu baseline failed: {e}")
 
+    dot = "Q8_K" if cfg["wtype"] == gl.Q4_K else "Q8_0"
+    data = f"synthetic (seeded random-init weights N(0,0.02) quantized to {wname.upper()}; KV cache N(0,1) F16)"
+    if moe:
+        data = data[:-1] + "; every layer holds layer 0's expert weights, routers per layer)"
     out = {
-        "metric": "batch-1 decode tokens/s; quant-GEMV HBM GB/s as % of MI355X peak",
+        "metric": "batch-1 decode tokens/s; quant-GEMV HBM GB/s as % of MI355X peak" if batch == 1
+                  else f"decode tokens/s at batch {batch}; quant-GEMV HBM GB/s as % of MI355X peak",
         "value": round(value, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -303,12 +490,11 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": f"synthetic (seeded random-init weights N(0,0.02) quantized to {wname.upper()}; KV cache N(0,1) F16)",
-        "config": {"workload": f"{args.config}: Llama-arch decode, 1 token at position {n_past}, batch 1 "
-                               f"(hidden 3072, 28 layers, 24/8 heads, head_dim 128, FFN 8192, vocab 128256, Q4_0)",
-                   "global_batch": 1, "seq_len": n_past + 1, "parallelism": "single GPU",
+        "data": data,
+        "config": {"workload": f"{args.config}: " + describe(cfg, n_past, batch),
+                   "global_batch": batch, "seq_len": n_past + batch, "parallelism": "single GPU",
                    "weights_bytes": weights_bytes,
-                   "arithmetic": "Q4_0 weights x Q8_0 activations by int8 dot products, f32 block sums; "
+                   "arithmetic": f"{wname.upper()} weights x {dot} activations by int8 dot products, f32 block sums; "
                                  "F16 KV with f64 dot accumulation"},
         "roofline": roofline,
         "cpu_baseline": cpu,

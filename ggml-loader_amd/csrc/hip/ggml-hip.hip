@@ -962,7 +962,7 @@ private:
 
         // SwiGLU pair inside the group: gate -> silu -> mul(silu, up)
         int gate = -1, up = -1, mulnode = -1;
-        if (fuse(FUSE_SWIGLU) && group.size() >= 2 && (wtype == GGML_TYPE_Q4_K || K <= gemv_swiglu_max_k(wtype))) {
+        if (fuse(FUSE_SWIGLU) && group.size() >= 2 && K <= gemv_swiglu_max_k(wtype)) {
             for (int a : group) {
                 const int s = sole_user(a);
                 if (s < 0) continue;

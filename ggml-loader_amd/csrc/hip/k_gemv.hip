@@ -221,12 +221,10 @@ __device__ __forceinline__ void q4k_sc_m(uint32_t w0, uint32_t w1, uint32_t w2, 
 
 // Per-lane integer partials of Q4_K unit u = (super-block u/4, sub-block pair p = u%4): aux[l] =
 // sum over the pair's 64 elements e with e%8 == l of sc_sub * q4 * q8, mins = the pair's share of
-// sum(bsums * m). (ggml's generic q4_K x q8_K kernel accumulates exactly these integers.)
-__device__ __forceinline__ void q4k_unit_ints(const uint8_t * blk, int p, const int8_t * xq, const int16_t * xbs,
-                                              int aux[8], int & mins) {
-    const uint4 hdr = *(const uint4 *) blk;
-    const uint4 qa = *(const uint4 *) (blk + 16 + 32 * p);
-    const uint4 qb = *(const uint4 *) (blk + 32 + 32 * p);
+// sum(bsums * m). (ggml's generic q4_K x q8_K kernel accumulates exactly these integers.) hdr is
+// the block's first 16 bytes (d, dmin, scales), qa/qb the pair's 32 quant bytes.
+__device__ __forceinline__ void q4k_unit_ints(const uint4 hdr, const uint4 qa, const uint4 qb, int p, const int8_t * xq,
+                                              const int16_t * xbs, int aux[8], int & mins) {
     int sc_a, m_a, sc_b, m_b;
     q4k_sc_m(hdr.y, hdr.z, hdr.w, 2 * p, sc_a, m_a);
     q4k_sc_m(hdr.y, hdr.z, hdr.w, 2 * p + 1, sc_b, m_b);
@@ -423,24 +421,32 @@ __device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, fl
 #pragma unroll
     for (int e = 0; e < PRO_REGS; e++) { xv[e] = 0.0f; wv[e] = 1.0f; }
     if constexpr (!PRO) {
-        // an already quantized Q8_0 column: its quants (xv, 4 x 16 bytes per thread) and block
-        // scales and sums (wv[0..1], wv[2..3]), ahead of the weights as well
-        if constexpr (TYPE != GGML_TYPE_Q4_K) {
-            const int K = L.K, nb = K / 32;
-            const int8_t * xq = L.xq + (int64_t) col * K;
+        // an already quantized column: its quants (xv, 4 x 16 bytes per thread) and, for Q8_0, the
+        // block scales and sums (wv[0..1], wv[2..3]); for Q8_K the super-block scale (wv[0]) and
+        // two dwords of the 16-element sums (wv[1..2]). Ahead of the weights as well.
+        const int K = L.K;
+        const int8_t * xq = L.xq + (int64_t) col * K;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int i = min(t + k * (int) blockDim.x, K / 16 - 1);
-                const int4 v = *(const int4 *) (xq + i * 16);
-                xv[4 * k] = __int_as_float(v.x); xv[4 * k + 1] = __int_as_float(v.y);
-                xv[4 * k + 2] = __int_as_float(v.z); xv[4 * k + 3] = __int_as_float(v.w);
-            }
+        for (int k = 0; k < 4; k++) {
+            const int i = min(t + k * (int) blockDim.x, K / 16 - 1);
+            const int4 v = *(const int4 *) (xq + i * 16);
+            xv[4 * k] = __int_as_float(v.x); xv[4 * k + 1] = __int_as_float(v.y);
+            xv[4 * k + 2] = __int_as_float(v.z); xv[4 * k + 3] = __int_as_float(v.w);
+        }
+        if constexpr (TYPE != GGML_TYPE_Q4_K) {
+            const int nb = K / 32;
 #pragma unroll
             for (int k = 0; k < 2; k++) {
                 const int i = min(t + k * (int) blockDim.x, nb - 1);
                 wv[k] = L.xd[(int64_t) col * nb + i];
                 wv[2 + k] = __int_as_float(L.xs[(int64_t) col * nb + i]);
             }
+        } else {
+            const int nsb = K / 256;
+            wv[0] = L.xd[(int64_t) col * nsb + min(t, nsb - 1)];
+            const int * bs = (const int *) (L.xbs + (int64_t) col * (K / 16));
+#pragma unroll
+            for (int k = 0; k < 2; k++) wv[1 + k] = __int_as_float(bs[min(t + k * (int) blockDim.x, K / 32 - 1)]);
         }
         return;
     } else {
@@ -448,7 +454,9 @@ __device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, fl
         const float * xcol = L.norm.x + (int64_t) col * L.norm.x_stride;
         load_chunk(*reinterpret_cast<float (*)[C]>(&xv[0]), xcol + (int64_t) min(t, nchunk - 1) * C);
         if (L.norm.rms && L.norm.w) load_chunk(*reinterpret_cast<float (*)[C]>(&wv[0]), L.norm.w + (int64_t) min(t, nchunk - 1) * C);
-        if (C * 2 == PRO_REGS && !L.norm.rms) {
+        if (C * 2 == PRO_REGS) {
+            // the quantize-only mode's second chunk; loaded (and left unused) in the rms mode too, so
+            // that no branch joins before the weight loads (the join would wait for these loads)
             load_chunk(*reinterpret_cast<float (*)[C]>(&xv[PRO_REGS - C]), xcol + (int64_t) min(t + (int) blockDim.x, nchunk - 1) * C);
         }
     }
@@ -510,28 +518,41 @@ __device__ __forceinline__ void stage_x(const gemv_launch & L, int col, const ge
     if constexpr (PRO) {
         prologue_finish<TYPE>(L, col, xv, wv, s, s_red);
     } else if constexpr (TYPE == GGML_TYPE_Q4_K) {
-        const int nsb = K / 256;
-        for (int i = threadIdx.x * 16; i < K; i += blockDim.x * 16) *(int4 *) (s.xq + i) = *(const int4 *) (L.xq + (int64_t) col * K + i);
-        for (int i = threadIdx.x; i < nsb; i += blockDim.x) s.xd[i] = L.xd[(int64_t) col * nsb + i];
-        for (int i = threadIdx.x; i < K / 16; i += blockDim.x) s.xbs[i] = L.xbs[(int64_t) col * (K / 16) + i];
+        // from the registers prologue_load filled; a row longer than they cover (K > 64 * blockDim)
+        // copies the rest here
+        // The stores are unconditional: a thread past the end stores the last element it loaded
+        // (the index was clamped) over that same element. A guarded store would let the compiler
+        // sink its load behind the weight loads, where waiting for it waits for all of them.
+        const int nsb = K / 256, nt = blockDim.x;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = min((int) threadIdx.x + k * nt, K / 16 - 1);
+            *(int4 *) (s.xq + i * 16) = make_int4(__float_as_int(xv[4 * k]), __float_as_int(xv[4 * k + 1]),
+                                                  __float_as_int(xv[4 * k + 2]), __float_as_int(xv[4 * k + 3]));
+        }
+        for (int i = (threadIdx.x + 4 * nt) * 16; i < K; i += nt * 16) *(int4 *) (s.xq + i) = *(const int4 *) (L.xq + (int64_t) col * K + i);
+        s.xd[min((int) threadIdx.x, nsb - 1)] = wv[0];
+        for (int i = threadIdx.x + nt; i < nsb; i += nt) s.xd[i] = L.xd[(int64_t) col * nsb + i];
+        int * sbs = (int *) s.xbs;
+        const int * gbs = (const int *) (L.xbs + (int64_t) col * (K / 16));
+#pragma unroll
+        for (int k = 0; k < 2; k++) sbs[min((int) threadIdx.x + k * nt, K / 32 - 1)] = __float_as_int(wv[1 + k]);
+        for (int i = threadIdx.x + 2 * nt; i < K / 32; i += nt) sbs[i] = gbs[i];
     } else {
-        // from the registers prologue_load filled (K <= 64 * blockDim, nb <= 2 * blockDim)
+        // from the registers prologue_load filled (K <= 64 * blockDim, nb <= 2 * blockDim), with
+        // unconditional stores as in the Q8_K copy above
         const int nb = K / 32;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const int i = threadIdx.x + k * blockDim.x;
-            if (i * 16 < K) {
-                *(int4 *) (s.xq + i * 16) = make_int4(__float_as_int(xv[4 * k]), __float_as_int(xv[4 * k + 1]),
-                                                      __float_as_int(xv[4 * k + 2]), __float_as_int(xv[4 * k + 3]));
-            }
+            const int i = min((int) (threadIdx.x + k * blockDim.x), K / 16 - 1);
+            *(int4 *) (s.xq + i * 16) = make_int4(__float_as_int(xv[4 * k]), __float_as_int(xv[4 * k + 1]),
+                                                  __float_as_int(xv[4 * k + 2]), __float_as_int(xv[4 * k + 3]));
         }
 #pragma unroll
         for (int k = 0; k < 2; k++) {
-            const int i = threadIdx.x + k * blockDim.x;
-            if (i < nb) {
-                s.xd[i] = wv[k];
-                s.xs[i] = __float_as_int(wv[2 + k]);
-            }
+            const int i = min((int) (threadIdx.x + k * blockDim.x), nb - 1);
+            s.xd[i] = wv[k];
+            s.xs[i] = __float_as_int(wv[2 + k]);
         }
     }
     __syncthreads();
@@ -608,7 +629,6 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
         const int e = min(max(L.ids[(int64_t) t * L.ids_stride + sl], 0), L.n_experts - 1);
         erow = (int64_t) e * L.expert_rows;
     }
-    const int64_t wrow_i = erow + lrow;           // weight row of this lane's output row
 
     // ---- per-block terms ----
     if (TYPE == GGML_TYPE_Q4_0 || TYPE == GGML_TYPE_Q8_0) {
@@ -663,28 +683,41 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
             }
         }
     } else { // Q4_K: per (super-block, l) products d*aux32[l] and dmin*mins
+        // as above: the prologue's loads, then every weight load of this lane (ITS units of 64
+        // weights: the block header and the pair's 32 quant bytes; unit and row clamped into the
+        // matrix), then the prologue's arithmetic while the weights are in flight
         float xv[PRO_REGS], wv[PRO_REGS];
         prologue_load<TYPE, PRO>(L, xcol, xv, wv);
-        stage_x<TYPE, PRO>(L, xcol, s, s_red, xv, wv);
-        constexpr int MAXU = 608 / LPR;   // supports K <= 9728 * 4 (units = K/64 <= 608)
         const int units = K / 64, nsb = K / 256;
         const int64_t row_bytes = (int64_t) nsb * Q4_K_BYTES;
+        uint4 hd[NCH][ITS], qa[NCH][ITS], qb[NCH][ITS];
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++) {
-            const uint8_t * wrow = L.m[SWIGLU ? ch : mi].w + (valid ? wrow_i : erow) * row_bytes;
-            float * terms = s.terms + (rib * NCH + ch) * nsb * 9;
-#pragma unroll 2
-            for (int it = 0; it < MAXU; it++) {
-                const int u = l + it * LPR;
-                if (it * LPR >= units) break;       // uniform across the group
-                int aux[8], mins = 0;
-                const int sb = u >> 2, p = u & 3;
-                if (valid && u < units) {
-                    q4k_unit_ints(wrow + (int64_t) sb * Q4_K_BYTES, p, s.xq + sb * 256 + 64 * p, s.xbs + sb * 16, aux, mins);
-                } else {
+            const gemv_mat & wm = L.m[SWIGLU ? ch : mi];
+            const uint8_t * wrow = wm.w + (erow + min(lrow, wm.n_rows - 1)) * row_bytes;
 #pragma unroll
-                    for (int k = 0; k < 8; k++) aux[k] = 0;
-                }
+            for (int it = 0; it < ITS; it++) {
+                const int u = min(l + it * LPR, units - 1);
+                const uint8_t * blk = wrow + (int64_t) (u >> 2) * Q4_K_BYTES;
+                hd[ch][it] = *(const uint4 *) blk;
+                qa[ch][it] = *(const uint4 *) (blk + 16 + 32 * (u & 3));
+                qb[ch][it] = *(const uint4 *) (blk + 32 + 32 * (u & 3));
+            }
+        }
+        stage_x<TYPE, PRO>(L, xcol, s, s_red, xv, wv);
+#pragma unroll
+        for (int ch = 0; ch < NCH; ch++) {
+            float * terms = s.terms + (rib * NCH + ch) * nsb * 9;
+#pragma unroll
+            for (int it = 0; it < ITS; it++) {
+                if (it * LPR >= units) break;       // uniform across the workgroup
+                const int u = l + it * LPR;
+                const int sb = u >> 2, p = u & 3;
+                const bool has = valid && u < units;
+                int aux[8], mins = 0;
+#pragma unroll
+                for (int k = 0; k < 8; k++) aux[k] = 0;
+                if (has) q4k_unit_ints(hd[ch][it], qa[ch][it], qb[ch][it], p, s.xq + sb * 256 + 64 * p, s.xbs + sb * 16, aux, mins);
                 // the 4 units of a super-block sit on 4 consecutive lanes: combine (exact integers)
 #pragma unroll
                 for (int k = 0; k < 8; k++) {
@@ -693,9 +726,8 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                 }
                 mins += __shfl_xor(mins, 1, WAVE);
                 mins += __shfl_xor(mins, 2, WAVE);
-                if (valid && u < units) {
-                    const uint8_t * blk = wrow + (int64_t) sb * Q4_K_BYTES;
-                    const uint32_t dd = *(const uint32_t *) blk;
+                if (has) {
+                    const uint32_t dd = hd[ch][it].x;
                     const float yd = s.xd[sb];
                     const float d = __half2float(__ushort_as_half((unsigned short) (dd & 0xffff))) * yd;
                     const float dmin = __half2float(__ushort_as_half((unsigned short) (dd >> 16))) * yd;
@@ -820,7 +852,20 @@ static void launch_gemv_its(gemv_kargs & ka, int waves, hipStream_t st) {
 template <int TYPE, int LPR, bool SWIGLU>
 static void launch_gemv_t(gemv_kargs & ka, int waves, hipStream_t st) {
     if constexpr (TYPE == GGML_TYPE_Q4_K) {
-        launch_gemv_its<TYPE, LPR, SWIGLU, 1>(ka, waves, st);
+        // units of 64 weights per lane
+        const int its = (ka.L.K / 64 + LPR - 1) / LPR;
+        if (its <= 1) launch_gemv_its<TYPE, LPR, SWIGLU, 1>(ka, waves, st);
+        else if (its <= 2) launch_gemv_its<TYPE, LPR, SWIGLU, 2>(ka, waves, st);
+        else if (its <= 3) launch_gemv_its<TYPE, LPR, SWIGLU, 3>(ka, waves, st);
+        else if (its <= 4) launch_gemv_its<TYPE, LPR, SWIGLU, 4>(ka, waves, st);
+        else if constexpr (!SWIGLU) {
+            if (its <= 6) launch_gemv_its<TYPE, LPR, SWIGLU, 6>(ka, waves, st);
+            else if (its <= 8) launch_gemv_its<TYPE, LPR, SWIGLU, 8>(ka, waves, st);
+            else if (its <= 10) launch_gemv_its<TYPE, LPR, SWIGLU, 10>(ka, waves, st);
+            else HIP_ABORT("gemv q4_K: K=%d is too long", ka.L.K);
+        } else {
+            HIP_ABORT("gemv q4_K: SwiGLU launch with K=%d exceeds %d", ka.L.K, gemv_swiglu_max_k(TYPE));
+        }
     } else {
         const int its = (ka.L.K / 32 + LPR - 1) / LPR;
         if (its <= 1) launch_gemv_its<TYPE, LPR, SWIGLU, 1>(ka, waves, st);
@@ -855,6 +900,21 @@ static void launch_gemv_lanes(gemv_kargs & ka, hipStream_t st) {
     else launch_gemv_t<TYPE, 64, SWIGLU>(ka, WAVES, st);
 }
 
+// Lanes per row for Q4_K launches of 4-wave workgroups, as above: at most 4 units (256 weights)
+// per lane when the rows still fill about two workgroups per CU. A SwiGLU launch uses at least 32
+// lanes per row: its ordered sums put the 9 chains of each of the two matrices on a row's lanes.
+template <bool SWIGLU>
+static void launch_gemv_q4k_lanes(gemv_kargs & ka, hipStream_t st) {
+    constexpr int WAVES = 4, TARGET_BLOCKS = 512;
+    const int rows = ka.total_rows, units = ka.L.K / 64;
+    const auto blocks = [&](int lpr) { return (rows + WAVES * (WAVE / lpr) - 1) / (WAVES * (WAVE / lpr)); };
+    if constexpr (!SWIGLU) {
+        if (units <= 16 * 4 && blocks(16) >= TARGET_BLOCKS) return launch_gemv_t<GGML_TYPE_Q4_K, 16, SWIGLU>(ka, WAVES, st);
+    }
+    if (units <= 32 * 4 && blocks(32) >= TARGET_BLOCKS) launch_gemv_t<GGML_TYPE_Q4_K, 32, SWIGLU>(ka, WAVES, st);
+    else launch_gemv_t<GGML_TYPE_Q4_K, 64, SWIGLU>(ka, WAVES, st);
+}
+
 void launch_gemv(const gemv_launch & L, hipStream_t st) {
     gemv_kargs ka;
     ka.L = L;
@@ -884,9 +944,9 @@ void launch_gemv(const gemv_launch & L, hipStream_t st) {
             else launch_gemv_lanes<GGML_TYPE_Q8_0, false>(ka, st);
             break;
         case GGML_TYPE_Q4_K:
-            if (L.K % 256 || L.K / 64 > 608) HIP_ABORT("gemv q4_K: K=%d unsupported", L.K);
-            if (L.swiglu) launch_gemv_t<GGML_TYPE_Q4_K, 32, true>(ka, 8, st);
-            else launch_gemv_t<GGML_TYPE_Q4_K, 16, false>(ka, 4, st);
+            if (L.K % 256 || L.K / 64 > 640) HIP_ABORT("gemv q4_K: K=%d unsupported", L.K);
+            if (L.swiglu) launch_gemv_q4k_lanes<true>(ka, st);
+            else launch_gemv_q4k_lanes<false>(ka, st);
             break;
         default:
             HIP_ABORT("gemv: unsupported weight type %d", L.type);

@@ -58,9 +58,10 @@ void launch_quantize_q8k(const float * x, int64_t x_col_stride, int64_t K, int64
 // matrices of one type and row length K sharing the same activation (one launch).
 constexpr int GEMV_MAX_MATS = 4;
 constexpr int GEMV_MAX_K = 16384;          // Q4_0 / Q8_0 rows
-// longest Q4_0 / Q8_0 rows of a gate/up pair in one SwiGLU launch (both chains' weight blocks stay
-// in registers)
-constexpr int gemv_swiglu_max_k(int type) { return type == 8 /* GGML_TYPE_Q8_0 */ ? 4096 : 6144; }
+// longest rows of a gate/up pair in one SwiGLU launch (both chains' weight blocks stay in registers)
+constexpr int gemv_swiglu_max_k(int type) {
+    return type == 8 /* GGML_TYPE_Q8_0 */ ? 4096 : type == 12 /* GGML_TYPE_Q4_K */ ? 16384 : 6144;
+}
 
 struct gemv_mat {
     const uint8_t * w;     // Q4_0/Q8_0: qs plane of the first row; Q4_K: first block

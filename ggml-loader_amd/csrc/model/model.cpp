@@ -327,11 +327,19 @@ static struct ggml_tensor * build_ffn_act(struct ggml_context * ctx, const hpara
 static struct ggml_tensor * build_moe_ffn(struct ggml_context * ctx, const hparams & hp, const layer_weights & l,
                                           struct ggml_tensor * y, int64_t n_new, built_graph & bg);
 
+// Graph capacity: the reference's GGML_DEFAULT_GRAPH_SIZE (model.cpp:1486) for the dense archs. A
+// qwen3moe layer adds the router, top-k, renormalization, three mul_mat_id and the per-slot expert
+// sum (about 60 tensors more), which overflows it at 48 layers.
+static size_t graph_size_of(const hparams & hp) {
+    return hp.n_expert > 0 ? std::max<size_t>(GGML_DEFAULT_GRAPH_SIZE, (size_t) hp.n_layer * 160 + 256)
+                           : (size_t) GGML_DEFAULT_GRAPH_SIZE;
+}
+
 // model.cpp:1296-1474 (transformer archs)
 static built_graph build_graph(struct ggml_context * ctx, const model & m, const hparams & hp, kv_cache & kv,
                                int64_t n_past, int64_t n_new, bool use_flash_attn) {
     built_graph bg{};
-    bg.gf = ggml_new_graph(ctx);
+    bg.gf = ggml_new_graph_custom(ctx, graph_size_of(hp), false);
 
     const int64_t head_dim = hp.n_embd_head;
     const int64_t n_kv     = n_past + n_new;
@@ -446,9 +454,9 @@ static struct ggml_tensor * build_moe_ffn(struct ggml_context * ctx, const hpara
 
 // model.cpp:1476-1494
 decode_session init_decode_session(ggml_backend_t backend, const hparams & hp, bool use_flash_attn) {
-    (void) hp;
     decode_session ds;
-    size_t buf_size = ggml_tensor_overhead() * GGML_DEFAULT_GRAPH_SIZE + ggml_graph_overhead();
+    const size_t n = graph_size_of(hp);
+    size_t buf_size = ggml_tensor_overhead() * n + ggml_graph_overhead_custom(n, false);
     ds.graph_buf.resize(buf_size);
     ds.galloc = ggml_gallocr_new(ggml_backend_get_default_buffer_type(backend));
     ds.use_flash_attn = use_flash_attn;

@@ -14,6 +14,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -155,6 +156,17 @@ extern "C" int gl_synth_model(const char * path, const gl_synth_params * p, char
     size_t pos = 0;
     std::vector<uint8_t> out;
     std::vector<float> tmp;
+    std::map<std::string, std::vector<uint8_t>> shared;
+    // progress on stderr in tenths of the data for files over 1 GiB (a large model takes minutes)
+    size_t total = 0;
+    for (const tensor_spec & s : specs) total += ggml_row_size(s.type, s.ne[0]) * (size_t) (s.ne[1] * s.ne[2] * s.ne[3]);
+    int tenth = 0;
+    auto progress = [&]() {
+        if (total < ((size_t) 1 << 30)) return;
+        for (; tenth < 10 && pos * 10 >= total * (size_t) (tenth + 1); tenth++) {
+            fprintf(stderr, "[synth] %s: %d%% of %.2f GB\n", path, 10 * (tenth + 1), total / 1e9);
+        }
+    };
     bool ok = true;
     for (size_t ti = 0; ti < specs.size() && ok; ti++) {
         const tensor_spec & s = specs[ti];
@@ -164,6 +176,18 @@ extern "C" int gl_synth_model(const char * path, const gl_synth_params * p, char
             ok = fwrite(z.data(), 1, z.size(), f) == z.size();
             pos = off;
         }
+        // share_experts: layer 0's expert tensors are kept in memory and written again for every layer
+        const bool expert = s.name.rfind("blk.", 0) == 0 && s.name.find("_exps.weight") != std::string::npos;
+        const std::string suffix = expert ? s.name.substr(s.name.find('.', 4) + 1) : std::string();
+        const bool reuse = p->share_experts && expert && shared.count(suffix) && s.name.rfind("blk.0.", 0) != 0;
+        if (reuse) {
+            const std::vector<uint8_t> & bytes = shared[suffix];
+            ok = fwrite(bytes.data(), 1, bytes.size(), f) == bytes.size();
+            pos += bytes.size();
+            progress();
+            continue;
+        }
+        std::vector<uint8_t> * keep = p->share_experts && expert ? &shared[suffix] : nullptr;
         const uint64_t k = splitmix64(p->seed ^ name_hash(s.name));
         const int64_t ne0 = s.ne[0];
         const int64_t nrows = s.ne[1] * s.ne[2] * s.ne[3];
@@ -182,6 +206,8 @@ extern "C" int gl_synth_model(const char * path, const gl_synth_params * p, char
             }
             ok = fwrite(out.data(), 1, out.size(), f) == out.size();
             pos += out.size();
+            if (keep) keep->insert(keep->end(), out.begin(), out.end());
+            progress();
         }
     }
     const size_t end = (pos + align - 1) / align * align;

@@ -55,10 +55,14 @@ typedef struct {
     float   norm_std;        // norm weights ~ 1 + N(0, norm_std)
     uint64_t seed;
     int32_t n_threads;
+    int32_t share_experts;   // non-zero: every layer's expert tensors hold layer 0's values
 } gl_synth_params;
 
 // Weights are N(0, w_std) floats from a counter-based generator (splitmix64 -> Box-Muller in
-// double), quantized with the ggml reference quantizer of the requested type.
+// double), quantized with the ggml reference quantizer of the requested type. share_experts
+// (qwen3moe) writes layer 0's quantized expert tensors into every layer: the expert weights of a
+// 48-layer, 128-expert model are 29e9 values, minutes of quantization; routers, attention and norm
+// weights stay distinct per layer, so routing still differs from layer to layer.
 GGML_API int gl_synth_model(const char * path, const gl_synth_params * p, char * err, size_t err_size);
 
 // The seeded normal generator the synthetic models use: out[i] = mean + std * z(seed, first + i).

@@ -167,6 +167,39 @@ def test_synthetic_model_is_deterministic(tmp_path):
     assert abs(wq.std() - 0.02) < 2e-3
 
 
+def test_synthetic_shared_experts(tmp_path):
+    """share_experts writes layer 0's expert tensors into every layer and changes nothing else."""
+    cfg = dict(TINY["qwen3moe"], n_layer=3)
+    a, b = str(tmp_path / "a.gguf"), str(tmp_path / "b.gguf")
+    gl.synth_model(a, seed=3, **cfg)
+    gl.synth_model(b, seed=3, share_experts=True, **cfg)
+    fa, fb = GGUFFile(a), GGUFFile(b)
+    assert fa.tensors == fb.tensors
+    n_exp = 0
+    for name in fa.tensors:
+        ra, rb = fa.raw(name)[0], fb.raw(name)[0]
+        if "_exps." in name:
+            r0 = fb.raw("blk.0." + name.split(".", 2)[2])[0]
+            assert np.array_equal(rb, r0), name
+            assert np.array_equal(ra, rb) == name.startswith("blk.0."), name
+            n_exp += 1
+        else:
+            assert np.array_equal(ra, rb), name
+    assert n_exp == 9
+
+
+def test_moe_graph_capacity(tmp_path):
+    """A 48-layer qwen3moe graph (about 60 tensors per layer more than a dense layer) fits the decode
+    session's graph, at one token and at a 16-token step."""
+    p = str(tmp_path / "moe48.gguf")
+    gl.synth_model(p, seed=2, **dict(TINY["qwen3moe"], n_layer=48, n_embd=64, n_head=2, n_head_kv=1, head_dim=32,
+                                     n_expert=8, n_expert_used=2, n_ff_exp=64, n_vocab=64, wtype=gl.Q8_0))
+    with gl.Session(p, "cpu", n_ctx=32, n_threads=4) as s:
+        one = s.forward(0, [5])
+        many = s.forward(1, list(range(16)))
+    assert np.all(np.isfinite(one)) and np.all(np.isfinite(many))
+
+
 def test_seeded_normal_generator():
     from gl import randn
     a = randn(200000, 7)
