@@ -307,7 +307,8 @@ enum fuse_bits {
     FUSE_ACTQ   = 32,  // producers emit the Q8 activation their GEMV consumers read
     FUSE_NORMQ  = 64,  // rms_norm * w folded into the prologue of the GEMVs that consume it
     FUSE_ROPE   = 128, // RoPE stored straight into the KV cache; independent RoPE/copies in one launch
-    FUSE_ALL    = 255,
+    FUSE_ROUTE  = 256, // MoE router softmax -> top-k -> renormalized weights in one launch
+    FUSE_ALL    = 511,
 };
 
 struct hip_backend_ctx {
@@ -566,6 +567,9 @@ private:
             case GGML_OP_MUL:
                 if (fuse(FUSE_ADD) && op_moe_wsum(i)) return;
                 break;
+            case GGML_OP_SOFT_MAX:
+                if (fuse(FUSE_ROUTE) && op_moe_route(i)) return;
+                break;
             default: break;
         }
         wrote_.push_back(n);
@@ -681,6 +685,54 @@ private:
     // RoPE node i, launched together with the RoPE nodes and F32 -> F16/F32 copies that follow it
     // in the graph and whose inputs are already final (the window holds views, RoPEs and copies
     // only, none of which reads what another writes)
+    // rms_norm * w outputs held back for a RoPE (QK-Norm)
+    struct pending_norm { const ggml_tensor * x; const ggml_tensor * w; float eps; };
+    std::unordered_map<const ggml_tensor *, pending_norm> pnorm_;
+
+    // A per-head rms_norm * w (QK-Norm) read only by a RoPE: held back until that RoPE's batch is
+    // placed (folded into the attention, or run just before the RoPE). Launches nothing.
+    bool defer_qk_norm(int i) {
+        const ggml_tensor * n = g_->nodes[i];
+        const ggml_tensor * x = n->src[0];
+        if (!fuse(FUSE_NORM) || !fuse(FUSE_ROPE) || !fuse(FUSE_ATTN) || n->op != GGML_OP_RMS_NORM) return false;
+        if (x->type != GGML_TYPE_F32 || !ggml_is_contiguous(x) || !ggml_is_contiguous(n) || x->ne[0] > 256 ||
+            x->ne[3] != 1 || ggml_nrows(x) > 4 * 64) return false;
+        const int u = sole_user(i);
+        if (u < 0) return false;
+        const ggml_tensor * m = g_->nodes[u];
+        const ggml_tensor * w = m->src[1];
+        if (m->op != GGML_OP_MUL || m->src[0] != n || w->type != GGML_TYPE_F32 || ggml_nrows(w) != 1 ||
+            w->ne[0] != x->ne[0] || !ggml_is_contiguous(w) || !ggml_is_contiguous(m)) return false;
+        const int r = sole_user(u);
+        if (r < 0 || g_->nodes[r]->op != GGML_OP_ROPE || g_->nodes[r]->src[0] != m) return false;
+        float eps;
+        memcpy(&eps, n->op_params, 4);
+        pnorm_[m] = pending_norm{ x, w, eps };
+        done_[u] = true;
+        return true;
+    }
+
+    void materialize_norm(const ggml_tensor * m) {
+        auto it = pnorm_.find(m);
+        if (it == pnorm_.end()) return;
+        const pending_norm pn = it->second;
+        pnorm_.erase(it);
+        const int64_t N = pn.x->ne[0], rows = ggml_nrows(pn.x);
+        prof_scope ps(this, "rms_norm_mul", (double) (N * rows * 8 + N * 4));
+        launch_rms_norm((const float *) pn.x->data, N, (const float *) pn.w->data, (float *) m->data, N, N, rows, pn.eps,
+                        nullptr, nullptr, st_);
+        wrote_.push_back(m);
+    }
+
+    qk_norm qk_norm_of(const ggml_tensor * m) {
+        auto it = pnorm_.find(m);
+        if (it == pnorm_.end()) return qk_norm{};
+        const pending_norm pn = it->second;
+        pnorm_.erase(it);
+        return qk_norm{ (const float *) pn.x->data, (int64_t) (pn.x->nb[1] / sizeof(float)), (int64_t) (pn.x->nb[2] / sizeof(float)),
+                        (const float *) pn.w->data, pn.eps };
+    }
+
     void op_rope(int i) {
         rope_batch B{};
         std::vector<int> members;
@@ -689,6 +741,11 @@ private:
             for (int j = i + 1; j < g_->n_nodes && B.n_jobs < ROPE_MAX_JOBS; j++) {
                 const ggml_tensor * m = g_->nodes[j];
                 if (done_[j] || std::find(members.begin(), members.end(), j) != members.end() || is_view_op(m->op)) continue;
+                // the QK-Norm in front of a later RoPE (held back: nothing runs out of order)
+                if (m->op == GGML_OP_RMS_NORM && ready(m->src[0]) && defer_qk_norm(j)) {
+                    done_[j] = true;
+                    continue;
+                }
                 if (m->op == GGML_OP_ROPE && m->src[0]->type == GGML_TYPE_F32 && m->type == GGML_TYPE_F32 &&
                     ready(m->src[0]) && ready(m->src[1]) && (!m->src[2] || ready(m->src[2]))) {
                     add_rope_job(B, members, j);
@@ -708,6 +765,9 @@ private:
             for (int j : members) done_[j] = true;
             return;
         }
+        for (int j : members) {
+            if (g_->nodes[j]->op == GGML_OP_ROPE) materialize_norm(g_->nodes[j]->src[0]);
+        }
         {
             prof_scope ps(this, "rope", 0);
             launch_rope_batch(B, st_);
@@ -719,7 +779,7 @@ private:
     // cache} whose rotated Q is read only by a decode attention over those caches, with the new
     // rows at that attention's last n_q positions: it runs inside the attention's scores kernel
     // (attn_launch.rope) instead of in a launch of its own.
-    struct pending_rope { int anchor = -1; rope_job q, k, v; };
+    struct pending_rope { int anchor = -1; rope_job q, k, v; qk_norm qn, kn; };
     pending_rope prope_;
 
     bool defer_rope(const rope_batch & B, const std::vector<int> & members) {
@@ -750,6 +810,10 @@ private:
         // rotation pairs serves both), over at most the head dimension
         const rope_job & q = B.job[jq], & k = B.job[jk];
         if (q.pos != k.pos || q.ff != k.ff || memcmp(&q.p, &k.p, sizeof(rope_params)) != 0 || q.p.n_dims > q.src.ne[0]) return false;
+        // the sources are f32 rows of contiguous elements (read as rows by the scores kernel)
+        const rope_job & v = B.job[jv];
+        if (q.src.type != GGML_TYPE_F32 || k.src.type != GGML_TYPE_F32 || v.src.type != GGML_TYPE_F32 ||
+            q.src.nb[0] != 4 || k.src.nb[0] != 4 || v.src.nb[0] != 4) return false;
         // rotated Q -> permute -> the attention anchor (and nothing else)
         const int p = sole_user(qi);
         if (p < 0 || g_->nodes[p]->op != GGML_OP_PERMUTE) return false;
@@ -771,7 +835,13 @@ private:
             kn->nb[1] != kp->nb[2] || kn->nb[2] != kp->nb[1] || kn->nb[0] != 2) return false;
         if ((const char *) vn->data != (const char *) vp->data + (n_kv - n_q) * vp->nb[0] ||
             vn->nb[1] != vp->nb[2] || vn->nb[2] != vp->nb[0] || vn->nb[0] != 2) return false;
-        prope_ = pending_rope{ a, B.job[jq], B.job[jk], B.job[jv] };
+        // held-back QK-Norms of the rotated Q and K (their rows: hd contiguous floats)
+        const ggml_tensor * qsrc = g_->nodes[qi]->src[0], * ksrc = g_->nodes[kc]->src[0]->src[0];
+        for (const ggml_tensor * src : { qsrc, ksrc }) {
+            auto it = pnorm_.find(src);
+            if (it != pnorm_.end() && (it->second.x->ne[0] != hd || it->second.x->nb[0] != sizeof(float))) return false;
+        }
+        prope_ = pending_rope{ a, B.job[jq], B.job[jk], B.job[jv], qk_norm_of(qsrc), qk_norm_of(ksrc) };
         wrote_.push_back(g_->nodes[kc]);
         wrote_.push_back(g_->nodes[vc]);
         return true;
@@ -793,6 +863,7 @@ private:
                 if (m->op == GGML_OP_MUL && m->src[0] == n && w->type == GGML_TYPE_F32 && ggml_nrows(w) == 1 &&
                     w->ne[0] == x->ne[0] && ggml_is_contiguous(w) && ggml_is_contiguous(m)) {
                     const int64_t N = x->ne[0], rows = ggml_nrows(x);
+                    if (defer_qk_norm(i)) return;
                     if (m->ne[1] == rows && norm_deferrable(u, N) && ((uintptr_t) x->data | (uintptr_t) w->data) % 16 == 0) {
                         const gemv_norm nz{ (const float *) x->data, N, (const float *) w->data, eps, 1 };
                         done_[u] = true;
@@ -929,6 +1000,20 @@ private:
         launch_mul_mat_generic(tv(n->src[0]), tv(n->src[1]), tv(n), st_);
     }
 
+    // Whether the GEMVs of a group read activation x (f32, not yet quantized) straight from memory,
+    // quantizing it in their prologue, rather than after a quantization launch of its own: for
+    // launches whose rows (per column) are few enough that redoing it per workgroup stays cheap.
+    bool quantize_in_prologue(const ggml_tensor * x, int wtype, const std::vector<int> & group, bool by_id) const {
+        if (!fuse(FUSE_ACTQ) || x->type != GGML_TYPE_F32 || x->nb[0] != sizeof(float) || x->ne[3] != 1) return false;
+        if (((uintptr_t) x->data) % 16 || x->nb[1] % 16 || x->ne[0] > gemv_prologue_max_k(wtype, false)) return false;
+        // columns evenly strided (mul_mat_id reads column t * ne[1] + slot)
+        if (x->ne[2] > 1 && x->nb[2] != x->nb[1] * x->ne[1]) return false;
+        if (!by_id && x->ne[2] > 1) return false;
+        int64_t rows = 0;
+        for (int j : group) rows += g_->nodes[j]->src[0]->ne[1];
+        return rows <= GEMV_PROLOGUE_MAX_ROWS;
+    }
+
     // quantized GEMV for node i, grouped with the other pending mul_mats that read the same input
     void op_gemv(int i) {
         ggml_tensor * n = g_->nodes[i];
@@ -982,7 +1067,18 @@ private:
 
         const int kind = dot_kind(wtype);
         const auto nz = norm_.find(x);
-        const act_entry * xa = nz == norm_.end() ? ensure_act(x, kind) : nullptr;
+        gemv_norm pro{};
+        const act_entry * xa = nullptr;
+        if (nz != norm_.end()) {
+            pro = nz->second;
+        } else if (act_.count(x) && act_.at(x).kind == kind) {
+            xa = &act_.at(x);
+        } else if (quantize_in_prologue(x, wtype, group, by_id)) {
+            // an f32 activation nobody quantized: every workgroup quantizes it in its prologue
+            pro = gemv_norm{ (const float *) x->data, (int64_t) (x->nb[1] / sizeof(float)), nullptr, 0.0f, 0 };
+        } else {
+            xa = ensure_act(x, kind);
+        }
 
         auto fill_mat = [&](gemv_mat & gm, int j, double & bytes, bool epilogue) {
             ggml_tensor * mm = g_->nodes[j];
@@ -1027,7 +1123,7 @@ private:
         L.type = wtype;
         L.K = (int) K;
         L.ncols = (int) ncols;
-        if (!xa) L.norm = nz->second;
+        if (!xa) L.norm = pro;
         else if (kind == 1) { L.xq = xa->q8.qs; L.xd = xa->q8.d; L.xs = xa->q8.s; }
         else { L.xq = xa->q8k.qs; L.xd = xa->q8k.d; L.xbs = xa->q8k.bsums; }
         if (by_id) {
@@ -1080,6 +1176,69 @@ private:
             launch_gemv(L, st_);
         }
         for (int j : group) done_[j] = true;
+    }
+
+    // The routing of build_moe_ffn (reference qwen_model.c:551-606 semantics):
+    //   probs = soft_max(logits); sel = view(argsort(probs, desc), first k); w = get_rows(probs, sel);
+    //   w = div(w, sum_rows(w))
+    // ==> one kernel per token writing the k expert ids into sel's rows and the renormalized w, with
+    // each op's float roundings. probs, the rest of the argsort and the sum are never stored.
+    bool op_moe_route(int i) {
+        ggml_tensor * sm = g_->nodes[i];
+        const ggml_tensor * lg = sm->src[0];
+        float scale, max_bias;
+        memcpy(&scale, &sm->op_params[0], 4);
+        memcpy(&max_bias, &sm->op_params[1], 4);
+        if (sm->src[1] || max_bias != 0.0f || lg->type != GGML_TYPE_F32 || lg->nb[0] != sizeof(float) ||
+            lg->ne[2] != 1 || lg->ne[3] != 1 || lg->ne[0] > MOE_ROUTE_MAX_EXPERTS || is_output(i) || users_[i].size() != 2) return false;
+        const int64_t E = lg->ne[0], T = lg->ne[1];
+        int as = -1, rs = -1;
+        for (int u : users_[i]) {
+            const ggml_tensor * un = g_->nodes[u];
+            if (un->op == GGML_OP_ARGSORT && un->src[0] == sm && un->op_params[0] == GGML_SORT_ORDER_DESC) as = u;
+            else if (un->op == GGML_OP_RESHAPE && un->src[0] == sm) rs = u;
+        }
+        if (as < 0 || rs < 0 || is_output(as) || users_[as].size() != 1) return false;
+        ggml_tensor * an = g_->nodes[as];
+        const int vs = users_[as][0];
+        const ggml_tensor * vn = g_->nodes[vs];
+        if (vn->op != GGML_OP_VIEW || vn->src[0] != an || vn->data != an->data || vn->nb[1] != an->nb[1] || vn->ne[1] != T) return false;
+        const int64_t k = vn->ne[0];
+        if (k < 1 || k > MOE_ROUTE_MAX_K || an->nb[0] != sizeof(int32_t)) return false;
+        const int gs = sole_user(rs);
+        if (gs < 0) return false;
+        const ggml_tensor * gn = g_->nodes[gs];
+        if (gn->op != GGML_OP_GET_ROWS || gn->src[0] != g_->nodes[rs] || gn->src[1] != vn) return false;
+        const int w2 = sole_user(gs);
+        if (w2 < 0 || g_->nodes[w2]->op != GGML_OP_RESHAPE || users_[w2].size() != 2 || is_output(w2)) return false;
+        int sr = -1, dv = -1;
+        for (int u : users_[w2]) {
+            const ggml_tensor * un = g_->nodes[u];
+            if (un->op == GGML_OP_SUM_ROWS && un->src[0] == g_->nodes[w2]) sr = u;
+            else if (un->op == GGML_OP_DIV && un->src[0] == g_->nodes[w2]) dv = u;
+        }
+        if (sr < 0 || dv < 0 || sole_user(sr) != dv || g_->nodes[dv]->src[1] != g_->nodes[sr]) return false;
+        ggml_tensor * dn = g_->nodes[dv];
+        if (dn->ne[0] != k || dn->ne[1] != T || !is_2d_contig(dn)) return false;
+        moe_route R{};
+        R.logits = (const float *) lg->data;
+        R.logits_nb1 = (int64_t) (lg->nb[1] / sizeof(float));
+        R.n_expert = (int) E;
+        R.k = (int) k;
+        R.n_tok = (int) T;
+        R.scale = scale;
+        R.ids = (int32_t *) an->data;
+        R.ids_nb1 = (int64_t) (an->nb[1] / sizeof(int32_t));
+        R.w = (float *) dn->data;
+        R.w_nb1 = (int64_t) (dn->nb[1] / sizeof(float));
+        {
+            prof_scope ps(this, "moe_route", (double) (E * T * 4 + k * T * 8));
+            launch_moe_route(R, st_);
+        }
+        for (int d : { i, as, vs, rs, gs, w2, sr, dv }) done_[d] = true;
+        wrote_.push_back(an);
+        wrote_.push_back(dn);
+        return true;
     }
 
     // mul(experts [n_embd, k, T], w [1, k, T]) -> views of the k slots -> add chain in slot order
@@ -1195,8 +1354,9 @@ private:
         if (kp->nb[0] != 2 || vp->nb[1] != 2 || qp->nb[0] != 4) return false;
         if (n_q < 1 || n_head % n_head_kv) return false;
         if (hd != 64 && hd != 96 && hd != 128) return false;
-        if (n_q <= 4 ? n_head / n_head_kv > 8
-                     : !prefill_attn_ok(n_kv, hd, kp->data, kp->nb[1], kp->nb[2], vp->data, vp->nb[0], vp->nb[2])) return false;
+        if (n_q > 4 && !prefill_attn_ok(n_kv, hd, kp->data, kp->nb[1], kp->nb[2], vp->data, vp->nb[0], vp->nb[2]) &&
+            n_head / n_head_kv > 8) return false;
+        if (n_q <= 4 && n_head / n_head_kv > 8) return false;
         if (ctn->ne[0] != hd * n_head || ctn->ne[1] != n_q) return false;
         const ggml_tensor * mask = smn->src[1];
         if (mask && (mask->ne[0] != n_kv || mask->nb[0] != ggml_type_size(mask->type))) return false;
@@ -1206,6 +1366,24 @@ private:
         M.kq = i; M.sm = sm; M.vt = vti; M.kqv = kqv; M.pm = pm; M.ct = ct;
         M.kp = kp; M.qp = qp; M.vp = vp; M.mask = mask; M.scale = scale;
         return true;
+    }
+
+    // More queries than the decode kernels take, over more positions than the prefill kernel holds
+    // in LDS (a multi-token step deep into the context): the decode kernels once per group of 4
+    // queries, each group with its own rows of Q, mask and output (same arithmetic per query).
+    void attn_decode_grouped(const attn_launch & A0) {
+        attn_launch A = A0;
+        A.scratch_bytes = attn_scratch_bytes(A0.n_kv, 4, A0.n_head, A0.hd);
+        A.scratch = (float *) c_.scratch.alloc((size_t) A.scratch_bytes);
+        A.out_q = q8_act{};
+        A.rope = 0;
+        for (int q0 = 0; q0 < A0.n_q; q0 += 4) {
+            A.n_q = std::min(4, A0.n_q - q0);
+            A.q = A0.q + (int64_t) q0 * A0.q_nb2;
+            A.mask = A0.mask ? (const char *) A0.mask + (int64_t) q0 * A0.mask_nb1 : nullptr;
+            A.out = A0.out + (int64_t) q0 * A0.out_nb1;
+            launch_attn_decode(A, st_);
+        }
     }
 
     void run_attention(const attn_match & M) {
@@ -1235,13 +1413,18 @@ private:
             A.rq = prope_.q;
             A.rk = prope_.k;
             A.rv = prope_.v;
+            A.qn = prope_.qn;
+            A.kn = prope_.kn;
             prope_.anchor = -1;
         }
         const double bytes = (double) n_kv * n_head_kv * hd * 2 * 2 + (double) n_head * hd * n_q * 8 +
                              (mask ? (double) n_kv * n_q * ggml_type_size(mask->type) : 0.0);
-        if (n_q > 4) {
+        if (n_q > 4 && prefill_attn_ok(n_kv, hd, kp->data, kp->nb[1], kp->nb[2], vp->data, vp->nb[0], vp->nb[2])) {
             prof_scope ps(this, "attn_prefill", bytes);
             launch_attn_prefill(A, st_);
+        } else if (n_q > 4) {
+            prof_scope ps(this, "attn_decode", bytes * ((n_q + 3) / 4));
+            attn_decode_grouped(A);
         } else {
             A.scratch_bytes = attn_scratch_bytes(n_kv, n_q, n_head, hd);
             A.scratch = (float *) c_.scratch.alloc((size_t) A.scratch_bytes);
@@ -1268,8 +1451,8 @@ private:
         const bool ok = max_bias == 0.0f && softcap == 0.0f && k->type == GGML_TYPE_F16 && v->type == GGML_TYPE_F16 &&
                         q->type == GGML_TYPE_F32 && q->nb[0] == 4 && k->nb[0] == 2 && v->nb[0] == 2 && v->ne[0] == hd &&
                         n_q >= 1 && n_head % n_head_kv == 0 &&
-                        (n_q <= 4 ? n_head / n_head_kv <= 8
-                                  : prefill_attn_ok(n_kv, hd, k->data, k->nb[1], k->nb[2], v->data, v->nb[1], v->nb[2])) &&
+                        (n_head / n_head_kv <= 8 ||
+                         (n_q > 4 && prefill_attn_ok(n_kv, hd, k->data, k->nb[1], k->nb[2], v->data, v->nb[1], v->nb[2]))) &&
                         (hd == 64 || hd == 96 || hd == 128) && ggml_is_contiguous(n) &&
                         ((uintptr_t) k->data) % 16 == 0 && k->nb[1] % 16 == 0 && k->nb[2] % 16 == 0 &&
                         ((uintptr_t) v->data) % 4 == 0 && v->nb[1] % 4 == 0 && v->nb[2] % 4 == 0 &&
@@ -1293,9 +1476,14 @@ private:
         A.n_kv = n_kv; A.n_q = n_q; A.n_head = n_head; A.n_head_kv = n_head_kv; A.hd = hd;
         A.scale = scale;
         const double bytes = (double) n_kv * n_head_kv * hd * 2 * 2 + (double) n_head * hd * n_q * 8;
-        if (n_q > 4) {
+        if (n_q > 4 && prefill_attn_ok(n_kv, hd, k->data, k->nb[1], k->nb[2], v->data, v->nb[1], v->nb[2])) {
             prof_scope ps(this, "attn_prefill", bytes);
             launch_attn_prefill(A, st_);
+            return;
+        }
+        if (n_q > 4) {
+            prof_scope ps(this, "attn_decode", bytes * ((n_q + 3) / 4));
+            attn_decode_grouped(A);
             return;
         }
         A.scratch_bytes = attn_scratch_bytes(n_kv, n_q, n_head, hd);

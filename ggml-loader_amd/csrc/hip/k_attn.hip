@@ -96,52 +96,168 @@ __device__ __forceinline__ void stage_rows(uint32_t * dst, const __half * base, 
     }
 }
 
+// Dynamic LDS of the scores kernel, sized for the launch's n_q new tokens (floats): the Q rows
+// [n_q * G][HD] (sources, then rotated in place), the new K and V source rows [n_q][HD] each, the
+// norm weights of Q and K [HD] each, the chunk's mask rows [n_q][ATT_CHUNK], the (cos, sin) pairs
+// [n_q][HD / 2] and the norm scales [n_q * G + n_q].
+template <int HD, int G>
+__host__ __device__ constexpr int scores_dyn_floats(int n_q) {
+    return n_q * G * HD + 2 * n_q * HD + 2 * HD + n_q * ATT_CHUNK + n_q * HD + n_q * G + n_q;
+}
+
 template <int HD, int G>
 __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_launch A) {
     constexpr int HD2 = HD / 2;
     constexpr int STRIDE = HD2 + 1;
     __shared__ uint32_t s_k[ATT_CHUNK * STRIDE];
-    __shared__ float s_q[ATT_MAX_Q * G][HD];
+    extern __shared__ float s_dyn[];
     const int split = blockIdx.x, kvh = blockIdx.y;
-    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int t0 = split * ATT_CHUNK;
     const int nt = min(ATT_CHUNK, A.n_kv - t0);
     const int n_q = A.n_q;
     const attn_scratch S = scratch_of(A);
+    float * s_q = s_dyn;                              // [n_q * G][HD]
+    float * s_kx = s_q + n_q * G * HD;                // [n_q][HD]
+    float * s_vx = s_kx + n_q * HD;                   // [n_q][HD]
+    float * s_qw = s_vx + n_q * HD;                   // [HD]
+    float * s_kw = s_qw + HD;                         // [HD]
+    float * s_mk = s_kw + HD;                         // [n_q][ATT_CHUNK]
+    float2 * s_cs = (float2 *) (s_mk + n_q * ATT_CHUNK);   // [n_q][HD / 2]
+    float * s_qs = (float *) (s_cs + n_q * HD2);      // [n_q * G]
+    float * s_ks = s_qs + n_q * G;                    // [n_q]
 
-    // RoPE: the (cos, sin) of every rotation pair of the new tokens, one pair per thread, while the
-    // chunk's K rows are in flight (Q and K rotate with the same positions and parameters)
-    __shared__ float2 s_cs[ATT_MAX_Q][HD / 2];
+    // Everything else this workgroup reads goes out before the chunk's K loads, so that waiting for
+    // it never waits for them (loads complete in issue order): the Q source rows (before QK-Norm and
+    // RoPE), the new tokens' K and V source rows, norm weights and positions (RoPE), the chunk's F32
+    // mask values. Indices are clamped and the loads unconditional; values past the ends are never
+    // used. Without RoPE the K / V / weight / position loads read Q again (valid, unused).
+    constexpr int QR = (ATT_MAX_Q * G * HD + ATT_THREADS - 1) / ATT_THREADS;
+    constexpr int KR = (ATT_MAX_Q * HD + ATT_THREADS - 1) / ATT_THREADS;
+    const bool qnorm = A.rope && A.qn.x, knorm = A.rope && A.kn.x;
+    const float * qb = !A.rope ? A.q : qnorm ? A.qn.x : (const float *) A.rq.src.data;
+    const int64_t qs1 = !A.rope ? A.q_nb1 : qnorm ? A.qn.nb1 : A.rq.src.nb[1] / 4;
+    const int64_t qs2 = !A.rope ? A.q_nb2 : qnorm ? A.qn.nb2 : A.rq.src.nb[2] / 4;
+    const int nqe = n_q * G * HD, nke = n_q * HD;
+    float qv[QR], kx[KR], vx[KR];
+#pragma unroll
+    for (int j = 0; j < QR; j++) {
+        const int i = min(t + j * ATT_THREADS, nqe - 1);
+        const int pr = i / HD;
+        qv[j] = qb[(int64_t) (kvh * G + pr % G) * qs1 + (int64_t) (pr / G) * qs2 + i % HD];
+    }
+    const float * kb = !A.rope ? qb : knorm ? A.kn.x : (const float *) A.rk.src.data;
+    const int64_t ks1 = !A.rope ? qs1 : knorm ? A.kn.nb1 : A.rk.src.nb[1] / 4;
+    const int64_t ks2 = !A.rope ? qs2 : knorm ? A.kn.nb2 : A.rk.src.nb[2] / 4;
+    const float * vb = !A.rope ? qb : (const float *) A.rv.src.data;
+    const int64_t vs1 = !A.rope ? qs1 : A.rv.src.nb[1] / 4, vs2 = !A.rope ? qs2 : A.rv.src.nb[2] / 4;
+#pragma unroll
+    for (int j = 0; j < KR; j++) {
+        const int i = min(t + j * ATT_THREADS, nke - 1);
+        kx[j] = kb[(int64_t) kvh * ks1 + (int64_t) (i / HD) * ks2 + i % HD];
+        vx[j] = vb[(int64_t) kvh * vs1 + (int64_t) (i / HD) * vs2 + i % HD];
+    }
+    const float qw = (qnorm ? A.qn.w : qb)[min(t, HD - 1)];
+    const float kw = (knorm ? A.kn.w : qb)[min(t, HD - 1)];
+    const int32_t * posp = A.rope ? A.rq.pos : (const int32_t *) qb;
+    const int half = A.rope ? A.rq.p.n_dims / 2 : 1;
+    const int tp = min(t, n_q * half - 1);          // this thread's rotation pair (clamped)
+    const int32_t my_pos = posp[tp / half];
+    const bool mask32 = A.mask && !A.mask_f16;
+    const float * mrow = (const float *) (mask32 ? A.mask : (const void *) qb);
+    float mk[ATT_MAX_Q];
+#pragma unroll
+    for (int q = 0; q < ATT_MAX_Q; q++) {
+        mk[q] = mrow[mask32 ? (int64_t) min(q, n_q - 1) * (A.mask_nb1 / 4) + t0 + min(lane, nt - 1) : 0];
+    }
+
+    // While the chunk's K rows are in flight: the loaded values into LDS and the (cos, sin) of every
+    // rotation pair of the new tokens (one pair per thread; Q and K rotate with the same positions
+    // and parameters). The stores are unconditional, at the clamped indices (a thread past the end
+    // stores the last value again): a guarded store would let the compiler move its load behind the
+    // K loads.
     stage_rows<HD, STRIDE, ATT_CHUNK>(s_k, A.k + (int64_t) kvh * A.k_nb1, A.k_nb2, t0, nt, [&]() {
-        if (!A.rope) return;
-        const int half = A.rq.p.n_dims / 2;
-        for (int i = threadIdx.x; i < n_q * half; i += ATT_THREADS) {
-            float c, sn;
-            rope_pair_cs(A.rq.p, A.rq.ff, A.rq.pos[i / half], i % half, c, sn);
-            s_cs[i / half][i % half] = make_float2(c, sn);
+#pragma unroll
+        for (int j = 0; j < QR; j++) s_q[min(t + j * ATT_THREADS, nqe - 1)] = qv[j];
+#pragma unroll
+        for (int j = 0; j < KR; j++) {
+            const int i = min(t + j * ATT_THREADS, nke - 1);
+            s_kx[i] = kx[j];
+            s_vx[i] = vx[j];
         }
+        s_qw[min(t, HD - 1)] = qw;
+        s_kw[min(t, HD - 1)] = kw;
+#pragma unroll
+        for (int q = 0; q < ATT_MAX_Q; q++) s_mk[min(q, n_q - 1) * ATT_CHUNK + min(lane, nt - 1)] = mk[q];
+        float c, sn;
+        rope_pair_cs(A.rq.p, A.rq.ff, my_pos, tp % half, c, sn);
+        s_cs[tp] = make_float2(c, sn);
     });
-    if (A.rope) __syncthreads();   // s_cs complete
-    for (int i = threadIdx.x; i < n_q * G * HD; i += ATT_THREADS) {
-        const int pr = i / HD, d = i % HD;
-        const int q = pr / G, g = pr % G;
-        const float v = A.rope ? rope_value_cs(A.rq, kvh * G + g, q, 0, d, s_cs[q])
-                               : A.q[(int64_t) (kvh * G + g) * A.q_nb1 + (int64_t) q * A.q_nb2 + d];
-        s_q[pr][d] = __half2float(__float2half_rn(as_f32(v)));
+    __syncthreads();   // K chunk, source rows, weights, mask, (cos, sin) in LDS
+
+    // QK-Norm folded in: the scale of each Q row of the group and of each new K row, one wave per
+    // row (the sum of squares in double, as the rms_norm op)
+    if (qnorm || knorm) {
+        const int nrq = qnorm ? n_q * G : 0, nr = nrq + (knorm ? n_q : 0);
+        for (int r = wave; r < nr; r += ATT_WAVES) {
+            const bool isq = r < nrq;
+            const float * xr = isq ? s_q + r * HD : s_kx + (r - nrq) * HD;
+            double ss = 0.0;
+            for (int e = lane; e < HD; e += WAVE) {
+                const float v = xr[e];
+                ss += (double) (v * v);
+            }
+            ss = wave_sum_d(ss);
+            if (lane == 0) {
+                const float sc = 1.0f / sqrtf((float) (ss / (double) HD) + (isq ? A.qn.eps : A.kn.eps));
+                if (isq) s_qs[r] = sc;
+                else s_ks[r - nrq] = sc;
+            }
+        }
+        __syncthreads();
+    }
+    // Q rows in place: [normalized,] rotated, rounded to F16 (the mul_mat's conversion of Q). One
+    // rotation pair, or one element past n_dims, per item, so each item owns the values it rewrites.
+    const int np = A.rope ? A.rq.p.n_dims / 2 : 0;
+    const bool neox = (A.rq.p.mode & GGML_ROPE_TYPE_NEOX) != 0;
+    const int per_row = HD - np;
+    for (int i = t; i < n_q * G * per_row; i += ATT_THREADS) {
+        const int pr = i / per_row, k = i % per_row;
+        float * xr = s_q + pr * HD;
+        const float sc = qnorm ? s_qs[pr] : 1.0f;
+        if (k < np) {
+            const int a0 = neox ? k : 2 * k, a1 = neox ? k + np : 2 * k + 1;
+            float x0 = xr[a0], x1 = xr[a1];
+            if (qnorm) {
+                x0 = (x0 * sc) * s_qw[a0];
+                x1 = (x1 * sc) * s_qw[a1];
+            }
+            const float2 cs = s_cs[(pr / G) * np + k];
+            xr[a0] = __half2float(__float2half_rn(as_f32(x0 * cs.x - x1 * cs.y)));
+            xr[a1] = __half2float(__float2half_rn(as_f32(x0 * cs.y + x1 * cs.x)));
+        } else {
+            const int d = 2 * np + (k - np);
+            float v = xr[d];
+            if (qnorm) v = (v * sc) * s_qw[d];
+            xr[d] = __half2float(__float2half_rn(as_f32(v)));
+        }
     }
     if (A.rope) {
         // the new positions of this chunk: K rotated into the cache and over its staged row, V appended
         const int first_new = A.n_kv - n_q;
         if (first_new + n_q > t0 && first_new < t0 + nt) {
-            __syncthreads();   // the staged rows are in LDS
-            for (int i = threadIdx.x; i < n_q * HD; i += ATT_THREADS) {
-                const int t = i / HD, d = i % HD;
-                const int pos = first_new + t;
+            for (int i = t; i < nke; i += ATT_THREADS) {
+                const int tk = i / HD, d = i % HD;
+                const int pos = first_new + tk;
                 if (pos < t0 || pos >= t0 + nt) continue;
-                const float kr = rope_value_cs(A.rk, kvh, t, 0, d, s_cs[t]);
-                st(at(A.rk.dst, d, kvh, t, 0), GGML_TYPE_F16, kr);
+                const float * xr = s_kx + tk * HD;
+                const float sc = knorm ? s_ks[tk] : 1.0f;
+                const float kr = rope_value_with(A.rk.p, d, s_cs + tk * np, [&](int e) {
+                    return knorm ? (xr[e] * sc) * s_kw[e] : xr[e];
+                });
+                st(at(A.rk.dst, d, kvh, tk, 0), GGML_TYPE_F16, kr);
                 ((__half *) (s_k + (pos - t0) * STRIDE))[d] = __float2half_rn(as_f32(kr));
-                st(at(A.rv.dst, d, kvh, t, 0), GGML_TYPE_F16, ld(at(A.rv.src, d, kvh, t, 0), A.rv.src.type));
+                st(at(A.rv.dst, d, kvh, tk, 0), GGML_TYPE_F16, s_vx[i]);
             }
         }
     }
@@ -151,17 +267,17 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
         const int q = pr / G, g = pr % G, h = kvh * G + g;
         if (lane < nt) {
             const uint32_t * kr = s_k + lane * STRIDE;
-            const float * qv = s_q[pr];
+            const float * qv2 = s_q + pr * HD;
             double acc = 0.0;
 #pragma unroll 8
             for (int d2 = 0; d2 < HD2; d2++) {
                 const __half2 k2 = *(const __half2 *) &kr[d2];
                 const float2 kf = __half22float2(k2);
-                acc += (double) (kf.x * qv[2 * d2]);
-                acc += (double) (kf.y * qv[2 * d2 + 1]);
+                acc += (double) (kf.x * qv2[2 * d2]);
+                acc += (double) (kf.y * qv2[2 * d2 + 1]);
             }
             // softmax input as the graph forms it: (float) kq * scale + mask
-            const float s = (float) acc * A.scale + mask_at(A, q, t0 + lane);
+            const float s = (float) acc * A.scale + (mask32 ? s_mk[q * ATT_CHUNK + lane] : mask_at(A, q, t0 + lane));
             S.scores[((int64_t) q * A.n_head + h) * A.n_kv + t0 + lane] = s;
         }
     }
@@ -325,7 +441,8 @@ template <int HD, int G>
 static void launch_attn_t(const attn_launch & A, hipStream_t st) {
     const int splits = (A.n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
     const int pv_splits = (A.n_kv + PV_CHUNK - 1) / PV_CHUNK;
-    launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
+    launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(ATT_THREADS),
+           scores_dyn_floats<HD, G>(A.n_q) * sizeof(float), st, A);
     launch(attn_stats_kernel, dim3(A.n_head, A.n_q), dim3(ATT_THREADS), 0, st, A);
     launch((attn_pv_kernel<HD, G>), dim3(pv_splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
     launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(HD), 0, st, A, pv_splits);

@@ -475,6 +475,70 @@ void launch_soft_max(const tview & a, const tview * mask, const tview & dst, flo
 }
 
 // ---------------------------------------------------------------------------------------------
+// MoE routing (one workgroup per token)
+
+__global__ __launch_bounds__(256) void moe_route_kernel(const moe_route R) {
+    __shared__ float s_p[MOE_ROUTE_MAX_EXPERTS];
+    __shared__ int s_ids[MOE_ROUTE_MAX_K];
+    __shared__ float s_red[4];
+    __shared__ double s_sum[4];
+    const int t = threadIdx.x, tok = blockIdx.x, E = R.n_expert;
+    const float * lg = R.logits + (int64_t) tok * R.logits_nb1;
+    if (t < R.k) s_ids[t] = 0;   // (every slot is written below unless a probability is NaN)
+    // softmax, as soft_max_kernel
+    float mx = -INFINITY;
+    for (int i = t; i < E; i += 256) {
+        const float w = lg[i] * R.scale;
+        s_p[i] = w;
+        mx = fmaxf(mx, w);
+    }
+    mx = wave_max(mx);
+    if ((t % 64) == 0) s_red[t / 64] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    double sum = 0.0;
+    for (int i = t; i < E; i += 256) {
+        const float v = exp_cr(s_p[i] - mx);
+        s_p[i] = v;
+        sum += (double) v;
+    }
+    sum = wave_sum_d(sum);
+    if ((t % 64) == 0) s_sum[t / 64] = sum;
+    __syncthreads();
+    const float inv = (float) (1.0 / (s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3]));
+    for (int i = t; i < E; i += 256) s_p[i] *= inv;
+    __syncthreads();
+    // position of each expert in the stable descending order; the first k positions are the top-k
+    for (int i = t; i < E; i += 256) {
+        const float v = s_p[i];
+        int rank = 0;
+        for (int j = 0; j < E; j++) {
+            const float u = s_p[j];
+            rank += (u > v || (u == v && j < i)) ? 1 : 0;
+        }
+        if (rank < R.k) s_ids[rank] = i;
+    }
+    __syncthreads();
+    if (t == 0) {
+        double s = 0.0;
+        for (int r = 0; r < R.k; r++) s += (double) s_p[s_ids[r]];
+        const float sf = (float) s;
+        for (int r = 0; r < R.k; r++) {
+            R.ids[(int64_t) tok * R.ids_nb1 + r] = s_ids[r];
+            R.w[(int64_t) tok * R.w_nb1 + r] = s_p[s_ids[r]] / sf;
+        }
+    }
+}
+
+void launch_moe_route(const moe_route & R, hipStream_t st) {
+    if (R.n_expert < 1 || R.n_expert > MOE_ROUTE_MAX_EXPERTS || R.k < 1 || R.k > MOE_ROUTE_MAX_K || R.k > R.n_expert) {
+        HIP_ABORT("moe_route: %d experts, k=%d unsupported", R.n_expert, R.k);
+    }
+    if (R.n_tok < 1) return;
+    launch(moe_route_kernel, dim3((unsigned) R.n_tok), dim3(256), 0, st, R);
+}
+
+// ---------------------------------------------------------------------------------------------
 // argmax of each row (first index of the maximum)
 
 __global__ __launch_bounds__(256) void argmax_kernel(tview a, int32_t * out) {
@@ -536,8 +600,68 @@ __global__ __launch_bounds__(256) void mul_mat_generic_kernel(tview s0, tview s1
     if (lane == 0) *(float *) at(d, k.i0, k.i1, k.i2, k.i3) = (float) acc;
 }
 
+// F32 / F16 weights with contiguous 16-byte aligned rows (the MoE router, F16 score products): one
+// wave per output, each lane reading 8 consecutive elements of the row and of the activation per
+// chunk, MR_BATCH chunks of loads in flight before the first product; same float products summed
+// in double as above.
+constexpr int MR_BATCH = 4;
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void mul_mat_rows_kernel(tview s0, tview s1, tview d, int64_t n_out) {
+    const int64_t o = (int64_t) blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+    if (o >= n_out) return;
+    const int lane = threadIdx.x % WAVE;
+    const idx4 k = unflatten(o, d.ne);
+    const int64_t r2 = s1.ne[2] / s0.ne[2], r3 = s1.ne[3] / s0.ne[3];
+    const char * a = at(s0, 0, k.i0, k.i2 / r2, k.i3 / r3);
+    const float * x = (const float *) at(s1, 0, k.i1, k.i2, k.i3);
+    const int nch = (int) (s0.ne[0] / 8);
+    double acc = 0.0;
+    for (int c0 = 0; c0 < nch; c0 += MR_BATCH * WAVE) {
+        float w[MR_BATCH][8], v[MR_BATCH][8];
+#pragma unroll
+        for (int j = 0; j < MR_BATCH; j++) {
+            const int c = min(c0 + j * WAVE + lane, nch - 1);
+            const float4 x0 = ((const float4 *) x)[2 * c], x1 = ((const float4 *) x)[2 * c + 1];
+            v[j][0] = x0.x; v[j][1] = x0.y; v[j][2] = x0.z; v[j][3] = x0.w;
+            v[j][4] = x1.x; v[j][5] = x1.y; v[j][6] = x1.z; v[j][7] = x1.w;
+            if (TYPE == GGML_TYPE_F32) {
+                const float4 a0 = ((const float4 *) a)[2 * c], a1 = ((const float4 *) a)[2 * c + 1];
+                w[j][0] = a0.x; w[j][1] = a0.y; w[j][2] = a0.z; w[j][3] = a0.w;
+                w[j][4] = a1.x; w[j][5] = a1.y; w[j][6] = a1.z; w[j][7] = a1.w;
+            } else {
+                const uint4 h = ((const uint4 *) a)[c];
+                const uint32_t hw[4] = { h.x, h.y, h.z, h.w };
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float2 f = __half22float2(*(const __half2 *) &hw[e]);
+                    w[j][2 * e] = f.x; w[j][2 * e + 1] = f.y;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < MR_BATCH; j++) {
+            if (c0 + j * WAVE + lane >= nch) continue;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float xv = TYPE == GGML_TYPE_F16 ? __half2float(__float2half_rn(v[j][e])) : v[j][e];
+                acc += (double) (w[j][e] * xv);
+            }
+        }
+    }
+    acc = wave_sum_d(acc);
+    if (lane == 0) *(float *) at(d, k.i0, k.i1, k.i2, k.i3) = (float) acc;
+}
+
 void launch_mul_mat_generic(const tview & src0, const tview & src1, const tview & dst, hipStream_t st) {
     const int64_t n = nelem(dst);
     if (n == 0) return;
-    launch(mul_mat_generic_kernel, dim3(grid1(n, 4)), dim3(256), 0, st, src0, src1, dst, n);
+    const int64_t es = src0.type == GGML_TYPE_F32 ? 4 : 2;
+    const bool rows = (src0.type == GGML_TYPE_F32 || src0.type == GGML_TYPE_F16) && src0.ne[0] % 8 == 0 &&
+                      src0.nb[0] == es && src1.nb[0] == 4 && ((uintptr_t) src0.data | (uintptr_t) src1.data) % 16 == 0 &&
+                      src0.nb[1] % 16 == 0 && src0.nb[2] % 16 == 0 && src0.nb[3] % 16 == 0 &&
+                      src1.nb[1] % 16 == 0 && src1.nb[2] % 16 == 0 && src1.nb[3] % 16 == 0;
+    if (rows && src0.type == GGML_TYPE_F32) launch(mul_mat_rows_kernel<GGML_TYPE_F32>, dim3(grid1(n, 4)), dim3(256), 0, st, src0, src1, dst, n);
+    else if (rows) launch(mul_mat_rows_kernel<GGML_TYPE_F16>, dim3(grid1(n, 4)), dim3(256), 0, st, src0, src1, dst, n);
+    else launch(mul_mat_generic_kernel, dim3(grid1(n, 4)), dim3(256), 0, st, src0, src1, dst, n);
 }

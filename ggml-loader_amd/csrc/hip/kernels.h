@@ -218,8 +218,35 @@ void launch_argmax(const tview & a, int32_t * out, hipStream_t st);
 // generic F32/F16/BF16 mul_mat (src0 rows contiguous): one wave per output element
 void launch_mul_mat_generic(const tview & src0, const tview & src1, const tview & dst, hipStream_t st);
 
+// MoE routing of one token per workgroup: softmax over the router logits (the soft_max op's
+// arithmetic), the k most probable experts in the stable descending order of argsort (ties: the
+// lower expert id first), and their probabilities divided by their float sum (sum_rows in double).
+constexpr int MOE_ROUTE_MAX_EXPERTS = 1024;
+constexpr int MOE_ROUTE_MAX_K = 32;
+struct moe_route {
+    const float * logits;      // [n_expert] floats per token, token stride logits_nb1
+    int64_t       logits_nb1;
+    int n_expert, k, n_tok;
+    float scale;
+    int32_t *     ids;         // k expert ids per token (stride ids_nb1)
+    int64_t       ids_nb1;
+    float *       w;           // k renormalized weights per token (stride w_nb1)
+    int64_t       w_nb1;
+};
+void launch_moe_route(const moe_route & R, hipStream_t st);
+
 // ---------------------------------------------------------------------------------------------
 // decode attention over the F16 KV cache: out[h*hd + i, q] for q < n_q, h < n_head
+// A per-head RMSNorm * w (QK-Norm) folded into the rotation of a RoPE source: element e of row
+// (head, token) is (x[e] * scale) * w[e], scale = 1 / sqrt(mean(x^2) + eps) over the row's hd
+// elements (the rms_norm -> mul ops' roundings). x == nullptr: none.
+struct qk_norm {
+    const float * x;           // row (head, token) at x + head * nb1 + token * nb2 (floats), contiguous
+    int64_t       nb1, nb2;
+    const float * w;           // [hd]
+    float         eps;
+};
+
 struct attn_launch {
     const float *  q;          // Q (post-RoPE) element (i, head, token) at q + i + head*q_nb1 + token*q_nb2 (floats)
     int64_t        q_nb1, q_nb2;
@@ -245,6 +272,9 @@ struct attn_launch {
     // row t of rv.src into rv.dst (the V cache)
     int            rope;
     rope_job       rq, rk, rv;
+    // with rope: Q and K rows normalized before the rotation (Qwen3's QK-Norm), read from qn.x /
+    // kn.x instead of rq.src / rk.src
+    qk_norm        qn, kn;
 };
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd);
 void launch_attn_decode(const attn_launch & A, hipStream_t st);

@@ -74,17 +74,29 @@ __device__ __forceinline__ void rope_pair_cs(const rope_params & p, const float 
     rope_cs(theta / f, p, 2 * ip, c, s);
 }
 
-// element d of row (i1, i2, i3) of J.src rotated with the (cos, sin) cs[ip] of its pair
-__device__ __forceinline__ float rope_value_cs(const rope_job & J, int64_t i1, int64_t i2, int64_t i3, int d, const float2 * cs) {
-    const rope_params & p = J.p;
-    if (d >= p.n_dims) return *(const float *) at(J.src, d, i1, i2, i3);
+// element d of a row rotated with the (cos, sin) cs[ip] of its pair; val(e) gives element e of the
+// row before the rotation
+template <typename F>
+__device__ __forceinline__ float rope_value_with(const rope_params & p, int d, const float2 * cs, F val) {
+    if (d >= p.n_dims) return val(d);
     const bool neox = (p.mode & GGML_ROPE_TYPE_NEOX) != 0;
     const int ip = neox ? d % (p.n_dims / 2) : d / 2;
     const int a0 = neox ? ip : 2 * ip, a1 = neox ? ip + p.n_dims / 2 : 2 * ip + 1;
-    const float x0 = *(const float *) at(J.src, a0, i1, i2, i3);
-    const float x1 = *(const float *) at(J.src, a1, i1, i2, i3);
+    const float x0 = val(a0), x1 = val(a1);
     const float c = cs[ip].x, sn = cs[ip].y;
     return d == a0 ? x0 * c - x1 * sn : x0 * sn + x1 * c;
+}
+
+// element d of row (i1, i2, i3) of J.src rotated with the (cos, sin) cs[ip] of its pair
+__device__ __forceinline__ float rope_value_cs(const rope_job & J, int64_t i1, int64_t i2, int64_t i3, int d, const float2 * cs) {
+    return rope_value_with(J.p, d, cs, [&](int e) { return *(const float *) at(J.src, e, i1, i2, i3); });
+}
+
+// the same for a row normalized first (qk_norm), with its scale already formed
+__device__ __forceinline__ float rope_value_norm_cs(const rope_params & p, const qk_norm & N, int64_t head, int64_t tok,
+                                                    float scale, int d, const float2 * cs) {
+    const float * xr = N.x + head * N.nb1 + tok * N.nb2;
+    return rope_value_with(p, d, cs, [&](int e) { return (xr[e] * scale) * N.w[e]; });
 }
 
 // element d of row (i1, i2, i3) of J.src rotated as ggml's RoPE does (the arithmetic of one pair of

@@ -105,6 +105,28 @@ def test_gemv(hip, cpu, qtype, K, N, ncols):
     assert np.array_equal(a, b), rel_err(a, b)
 
 
+@pytest.mark.parametrize("wtype", [gl.F32, gl.F16])
+@pytest.mark.parametrize("K,N,ncols,n2", [
+    (2048, 128, 1, 1),     # the MoE router
+    (2048, 128, 16, 1),
+    (4104, 33, 3, 1),      # more than one batch of chunks, a partial one
+    (64, 17, 5, 4),        # batched over dim 2
+    (12, 9, 2, 1),         # rows too short for the vector path
+])
+def test_mul_mat_float_weights(hip, cpu, wtype, K, N, ncols, n2):
+    """F32 / F16 weights (no quantization): float products summed in double, as ggml-cpu's
+    vec_dot_f32 / vec_dot_f16 (with the activation rounded to F16 for F16 weights)."""
+    r = rng(K + N + ncols)
+    w = r.standard_normal((n2, N, K)).astype(np.float16 if wtype == gl.F16 else np.float32)
+    x = r.standard_normal((n2, ncols, K)).astype(np.float32)
+
+    def build(g):
+        return g.mul_mat(g.tensor(wtype, K, N, n2, data=w), g.tensor(gl.F32, K, ncols, n2, data=x))
+
+    a, b = both(hip, cpu, build)
+    assert np.array_equal(a, b), rel_err(a, b)
+
+
 def profiled(hip, fn):
     """Runs fn with every kernel timed; returns (fn's result, kernel names launched)."""
     h = gl.libs()["hip"]
@@ -316,19 +338,25 @@ def test_rope_and_kv_append_batched(hip, cpu, mode, hd, n_new):
     assert np.array_equal(ref[2].reshape(n_ctx, n_head_kv, hd)[n_past:n_past + n_new], v.astype(np.float16))
 
 
-@pytest.mark.parametrize("mode,hd,n_head,n_head_kv", [(gl.ROPE_NORMAL, 128, 24, 8), (gl.ROPE_NEOX, 96, 8, 8),
-                                                     (gl.ROPE_NEOX, 64, 8, 2)])
+@pytest.mark.parametrize("mode,hd,n_head,n_head_kv,qk_norm", [
+    (gl.ROPE_NORMAL, 128, 24, 8, False), (gl.ROPE_NEOX, 96, 8, 8, False), (gl.ROPE_NEOX, 64, 8, 2, False),
+    (gl.ROPE_NEOX, 128, 32, 8, True),    # Qwen3: QK-Norm before the rotations
+    (gl.ROPE_NEOX, 64, 8, 2, True),
+])
 @pytest.mark.parametrize("n_new", [1, 3])
-def test_attention_with_rope_and_kv_append(hip, cpu, mode, hd, n_head, n_head_kv, n_new):
-    """RoPE(Q), RoPE(K) -> F16 cache, V -> F16 cache, then decode attention over the caches (the
-    reference's per-layer order, model.cpp:1389-1444): on the fused path the rotations and the
-    cache writes happen inside the attention's scores kernel, with the same floats and cache rows."""
+def test_attention_with_rope_and_kv_append(hip, cpu, mode, hd, n_head, n_head_kv, qk_norm, n_new):
+    """[QK-Norm (rms_norm * w per head, model.cpp:1382-1387),] RoPE(Q), RoPE(K) -> F16 cache, V -> F16
+    cache, then decode attention over the caches (the reference's per-layer order, model.cpp:1389-1444):
+    on the fused path the norms, rotations and cache writes happen inside the attention's scores
+    kernel, with the same floats and cache rows."""
     n_ctx, n_past = 140, 129          # the new rows straddle a 64-position chunk boundary for n_new = 3
     n_kv = n_past + n_new
     r = rng(60 + hd + n_new)
     q = r.standard_normal((n_new, n_head, hd)).astype(np.float32)
     k = r.standard_normal((n_new, n_head_kv, hd)).astype(np.float32) * 2
     v = r.standard_normal((n_new, n_head_kv, hd)).astype(np.float32) * 2
+    qw = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
+    kw = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
     pos = np.arange(n_past, n_kv, dtype=np.int32)
     cache0 = r.standard_normal((2, n_ctx, n_head_kv, hd)).astype(np.float16)
     mask = np.zeros((n_new, n_kv), dtype=np.float32)
@@ -341,8 +369,12 @@ def test_attention_with_rope_and_kv_append(hip, cpu, mode, hd, n_head, n_head_kv
             vc = g.tensor(gl.F16, hd, n_head_kv, n_ctx, data=cache0[1])
             pt = g.tensor(gl.I32, n_new, data=pos)
             m = g.tensor(gl.F32, n_kv, n_new, data=mask)
-            qr = g.rope_ext(g.tensor(gl.F32, hd, n_head, n_new, data=q), pt, None, hd, mode, 4096, 10000.0, 1.0, 0.0, 1.0, 0.0, 0.0)
-            kr = g.rope_ext(g.tensor(gl.F32, hd, n_head_kv, n_new, data=k), pt, None, hd, mode, 4096, 10000.0, 1.0, 0.0, 1.0, 0.0, 0.0)
+            qs, ks = g.tensor(gl.F32, hd, n_head, n_new, data=q), g.tensor(gl.F32, hd, n_head_kv, n_new, data=k)
+            if qk_norm:
+                qs = g.mul(g.rms_norm(qs, 1e-6), g.tensor(gl.F32, hd, data=qw))
+                ks = g.mul(g.rms_norm(ks, 1e-6), g.tensor(gl.F32, hd, data=kw))
+            qr = g.rope_ext(qs, pt, None, hd, mode, 4096, 10000.0, 1.0, 0.0, 1.0, 0.0, 0.0)
+            kr = g.rope_ext(ks, pt, None, hd, mode, 4096, 10000.0, 1.0, 0.0, 1.0, 0.0, 0.0)
             nb1, nb2 = hd * 2, hd * n_head_kv * 2
             ck = g.cpy(kr, g.view_3d(kc, hd, n_head_kv, n_new, nb1, nb2, n_past * nb2))
             cv = g.cpy(g.tensor(gl.F32, hd, n_head_kv, n_new, data=v), g.view_3d(vc, hd, n_head_kv, n_new, nb1, nb2, n_past * nb2))
@@ -368,7 +400,7 @@ def test_attention_with_rope_and_kv_append(hip, cpu, mode, hd, n_head, n_head_kv
         assert np.array_equal(got[1].view(np.uint16), ref[1].view(np.uint16)), fusion
         assert np.array_equal(got[2].view(np.uint16), ref[2].view(np.uint16)), fusion
         if fusion:
-            assert "rope" not in got[3] and "attn_decode" in got[3], got[3]
+            assert "rope" not in got[3] and "rms_norm_mul" not in got[3] and "attn_decode" in got[3], got[3]
 
 
 def test_soft_max_masked(hip, cpu):
@@ -492,6 +524,37 @@ def test_attention_prefill(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
         assert np.array_equal(a, b), rel_err(a, b)
 
 
+@pytest.mark.parametrize("hd,n_head,n_head_kv,n_kv,n_new", [
+    (128, 32, 4, 4112, 16),   # the MoE config's 16-token step at position 4096
+    (128, 8, 8, 3000, 7),     # a partial last group of queries
+    (64, 4, 2, 9000, 5),
+])
+@pytest.mark.parametrize("flash", [False, True])
+def test_attention_long_context_query_groups(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
+    """A multi-token step over more positions than the prefill kernel holds in LDS: the decode
+    kernels per group of 4 queries, the chain's float roundings exactly."""
+    r = rng(n_kv + 7 * n_new)
+    n_ctx = n_kv + 3
+    kc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+    vc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+    q = r.standard_normal((n_new, n_head, hd)).astype(np.float32)
+    mask = np.zeros((n_new, n_kv), dtype=np.float32)
+    n_past = n_kv - n_new
+    for i in range(n_new):
+        mask[i, n_past + i + 1:] = -np.inf
+
+    def build(g):
+        return attention_graph(g, hd, n_head, n_head_kv, n_kv, n_new, n_ctx, kc, vc, q, mask, flash)
+
+    a, names = profiled(hip, lambda: run_on(hip, build))
+    b = run_on(cpu, build)
+    assert "attn_decode" in names and "attn_prefill" not in names, names
+    if flash:
+        assert rel_err(a, b) < TOL, rel_err(a, b)
+    else:
+        assert np.array_equal(a, b), rel_err(a, b)
+
+
 def f16_tie_scores(n_kv, seed):
     """Scores (F16, one head, scale 1/8) whose softmax holds a probability p = e * (1/S) that is an
     exact F16 rounding tie as a float, while the exact product e * (1/S) lies on the side whose
@@ -573,3 +636,34 @@ def test_moe_ffn(hip, cpu, qtype, n_tok):
     for fusion in (True, False):
         a, b = both(hip, cpu, build, fusion)
         assert np.array_equal(a, b), (fusion, rel_err(a, b))
+    _, names = profiled(hip, lambda: run_on(hip, build))
+    assert "moe_route" in names and "argsort" not in names, names
+
+
+@pytest.mark.parametrize("E,k,n_tok", [(128, 8, 1), (128, 8, 16), (60, 4, 3), (1024, 32, 2), (8, 8, 1)])
+def test_moe_route_fused(hip, cpu, E, k, n_tok):
+    """Router softmax -> top-k -> renormalized weights in one kernel: the same ids (ties: the lower
+    expert first) and weights as the op chain, logits with many exact ties included."""
+    r = rng(E + k + n_tok)
+    lg = r.standard_normal((n_tok, E)).astype(np.float32)
+    lg[0, ::3] = 0.75          # many equal probabilities, some of them among the top
+    if n_tok > 1:
+        lg[1] = np.round(lg[1])
+
+    ids_table = np.tile(np.arange(E, dtype=np.float32), (n_tok, 1))   # row t: expert e -> float(e)
+
+    def build(g):
+        probs = g.soft_max_ext(g.tensor(gl.F32, E, n_tok, data=lg), None, 1.0, 0.0)
+        sel = g.top_k(probs, k)
+        w = g.reshape_2d(g.get_rows(g.reshape_3d(probs, 1, E, n_tok), sel), k, n_tok)
+        w = g.div(w, g.sum_rows(w))
+        ids = g.get_rows(g.tensor(gl.F32, 1, E, n_tok, data=ids_table), sel)   # the selected ids, as floats
+        return [ids, w]
+
+    (ia, wa), names = profiled(hip, lambda: run_on(hip, build))
+    ib, wb = run_on(cpu, build)
+    assert "moe_route" in names, names
+    assert np.array_equal(ia, ib)
+    assert np.array_equal(wa, wb)
+    order = np.argsort(-lg, axis=1, kind="stable")[:, :k]
+    assert np.array_equal(ia.reshape(n_tok, k).astype(np.int64), order)
