@@ -88,6 +88,13 @@ __device__ __forceinline__ float exp_cr(float x) { return (float) exp((double) x
 __device__ __forceinline__ float cos_cr(float x) { return (float) cos((double) x); }
 __device__ __forceinline__ float sin_cr(float x) { return (float) sin((double) x); }
 __device__ __forceinline__ float log_cr(float x) { return (float) log((double) x); }
+// both of the above from one argument reduction
+__device__ __forceinline__ void sincos_cr(float x, float & s, float & c) {
+    double sd, cd;
+    sincos((double) x, &sd, &cd);
+    s = (float) sd;
+    c = (float) cd;
+}
 
 // round half to even, valid for |v| < 2^22 (the result ggml's nearest_int gives)
 __device__ __forceinline__ int round_half_even(float v) { return __float2int_rn(v); }

@@ -17,17 +17,18 @@
 // iteration would put one L2/HBM round trip per iteration on the critical path):
 //   scores   (64-position chunk, KV head) workgroups: the chunk's K rows staged through LDS with
 //            coalesced 16-byte loads (rows padded by one dword so lane t reading row t is
-//            conflict-free); one wave per (query, head of the GQA group), lane = position.
-//   stats    one workgroup per (query, head) row: M = max, 1/S = 1/sum exp(s - M) in double.
-//   pv       (128-position chunk, KV head) workgroups: p = F16(exp(s - M) * (1/S)) for the chunk,
-//            the chunk's V rows staged in LDS (every load issued up front), one partial per
-//            (chunk, query, head) accumulated in double; one wave per (query, head), two dims per
-//            lane.
+//            conflict-free); one wave per (query, head of the GQA group), lane = position; each
+//            row's chunk maximum.
+//   stats    (query, head, 1024-position segment) workgroups: M = the maximum of the row's chunk
+//            maxima, the segment's sum of exp(s - M) in double.
+//   pv       (128-position chunk, KV head) workgroups: 1/S from the segment sums (added in segment
+//            order), p = F16(exp(s - M) * (1/S)) for the chunk, the chunk's V rows staged in LDS
+//            (every load issued up front), one partial per (chunk, query, head) accumulated in
+//            double; one wave per (query, head), two dims per lane.
 //   combine  one thread per output element: the partials added in chunk order (+ Q8_0 blocks).
 // Workgroups exchange results only across launch boundaries: a flag-and-fence hand-off inside a
 // launch costs a write-back and invalidation of the L2 of every XCD that takes part.
-// Scratch: scores f32 [n_q][n_head][n_kv], row statistics f32 [n_q][n_head][2] (M, 1/S),
-// partials f64 [pv chunks][n_q][n_head][hd].
+// Scratch: see attn_scratch.
 #include "kernels.h"
 #include "tview_ops.h"
 
@@ -39,29 +40,41 @@ constexpr int ATT_THREADS = 256;
 constexpr int ATT_WAVES = ATT_THREADS / WAVE;
 
 constexpr int PV_CHUNK = 128;
-constexpr int STATS_BATCH = 16;      // score loads per thread in flight in the statistics kernel
+constexpr int STATS_PER_THREAD = 4;                          // scores per thread of a statistics workgroup
+constexpr int STATS_SEG = ATT_THREADS * STATS_PER_THREAD;    // positions per statistics workgroup
 
+__host__ __device__ inline int attn_chunks(int n_kv) { return (n_kv + ATT_CHUNK - 1) / ATT_CHUNK; }
+__host__ __device__ inline int attn_segs(int n_kv) { return (n_kv + STATS_SEG - 1) / STATS_SEG; }
+
+// Scratch (all per row = (query, head)): scores f32 [n_kv], the maximum of each 64-position chunk
+// f32 [chunks], the row maximum f32, the sum of exp(s - max) over each statistics segment f64
+// [segs], and the PV partials f64 [pv chunks][n_q][n_head][hd].
 struct attn_scratch {
     float * scores;
-    float * stats;
+    float * cmax;
+    float * rmax;
+    double * ssum;
     double * parts;
 };
 
 __host__ __device__ inline attn_scratch scratch_of(const attn_launch & A) {
-    const int64_t rows = (int64_t) A.n_q * A.n_head * A.n_kv;
-    const int64_t nst = (int64_t) A.n_q * A.n_head * 2;
+    const int64_t nrow = (int64_t) A.n_q * A.n_head;
     attn_scratch s;
     s.scores = A.scratch;
-    s.stats = s.scores + rows;
-    s.parts = (double *) (s.stats + nst + ((rows + nst) & 1));
+    s.cmax = s.scores + nrow * A.n_kv;
+    s.rmax = s.cmax + nrow * attn_chunks(A.n_kv);
+    const int64_t nf = nrow * A.n_kv + nrow * attn_chunks(A.n_kv) + nrow;
+    s.ssum = (double *) (A.scratch + nf + (nf & 1));
+    s.parts = s.ssum + nrow * attn_segs(A.n_kv);
     return s;
 }
 
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd) {
-    const int64_t splits = (n_kv + PV_CHUNK - 1) / PV_CHUNK;
-    const int64_t rows = (int64_t) n_q * n_head * n_kv;
-    const int64_t nst = (int64_t) n_q * n_head * 2;
-    return (rows + nst + 1) * (int64_t) sizeof(float) + splits * n_q * n_head * hd * (int64_t) sizeof(double);
+    const int64_t nrow = (int64_t) n_q * n_head;
+    const int64_t nf = nrow * n_kv + nrow * attn_chunks(n_kv) + nrow;
+    const int64_t pv_chunks = (n_kv + PV_CHUNK - 1) / PV_CHUNK;
+    return (nf + (nf & 1)) * (int64_t) sizeof(float) +
+           (nrow * attn_segs(n_kv) + pv_chunks * nrow * hd) * (int64_t) sizeof(double);
 }
 
 __device__ __forceinline__ float mask_at(const attn_launch & A, int q, int t) {
@@ -265,45 +278,49 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
 
     for (int pr = wave; pr < n_q * G; pr += ATT_WAVES) {
         const int q = pr / G, g = pr % G, h = kvh * G + g;
+        float sv = -INFINITY;
         if (lane < nt) {
             const uint32_t * kr = s_k + lane * STRIDE;
             const float * qv2 = s_q + pr * HD;
-            double acc = 0.0;
+            // four independent chains (the sums are exact for these operands, so their order
+            // does not change the result)
+            double acc4[4] = { 0.0, 0.0, 0.0, 0.0 };
 #pragma unroll 8
             for (int d2 = 0; d2 < HD2; d2++) {
                 const __half2 k2 = *(const __half2 *) &kr[d2];
                 const float2 kf = __half22float2(k2);
-                acc += (double) (kf.x * qv2[2 * d2]);
-                acc += (double) (kf.y * qv2[2 * d2 + 1]);
+                acc4[(2 * d2) % 4] += (double) (kf.x * qv2[2 * d2]);
+                acc4[(2 * d2 + 1) % 4] += (double) (kf.y * qv2[2 * d2 + 1]);
             }
+            const double acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
             // softmax input as the graph forms it: (float) kq * scale + mask
             const float s = (float) acc * A.scale + (mask32 ? s_mk[q * ATT_CHUNK + lane] : mask_at(A, q, t0 + lane));
             S.scores[((int64_t) q * A.n_head + h) * A.n_kv + t0 + lane] = s;
+            sv = s;
         }
+        // the chunk's maximum of the row, for the statistics
+        sv = wave_max(sv);
+        if (lane == 0) S.cmax[((int64_t) q * A.n_head + h) * attn_chunks(A.n_kv) + split] = sv;
     }
 }
 
-// one workgroup per (head, query) row
+// one workgroup per (head, query, segment of STATS_SEG positions): the row maximum M from the chunk
+// maxima, and sum exp(s - M) in double over the segment's positions
 __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_launch A) {
     __shared__ float s_m[ATT_WAVES];
     __shared__ double s_s[ATT_WAVES];
-    const int h = blockIdx.x, q = blockIdx.y;
-    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const int h = blockIdx.x, q = blockIdx.y, seg = blockIdx.z;
+    const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const attn_scratch S = scratch_of(A);
-    const float * sc = S.scores + ((int64_t) q * A.n_head + h) * A.n_kv;
-    constexpr int SPAN = ATT_THREADS * STATS_BATCH;
-    const bool one_batch = A.n_kv <= SPAN;          // values stay in registers for the exp pass
-    float v[STATS_BATCH];
+    const int64_t row = (int64_t) q * A.n_head + h;
+    const float * sc = S.scores + row * A.n_kv;
+    const int nch = attn_chunks(A.n_kv);
+    // the segment's scores go out first (clamped indices, unused past the end)
+    float v[STATS_PER_THREAD];
+#pragma unroll
+    for (int k = 0; k < STATS_PER_THREAD; k++) v[k] = sc[min(seg * STATS_SEG + k * ATT_THREADS + t, A.n_kv - 1)];
     float m = -INFINITY;
-    for (int base = 0; base < A.n_kv; base += SPAN) {
-#pragma unroll
-        for (int k = 0; k < STATS_BATCH; k++) {
-            const int t = base + k * ATT_THREADS + threadIdx.x;
-            v[k] = t < A.n_kv ? sc[t] : -INFINITY;
-        }
-#pragma unroll
-        for (int k = 0; k < STATS_BATCH; k++) m = fmaxf(m, v[k]);
-    }
+    for (int c = t; c < nch; c += ATT_THREADS) m = fmaxf(m, S.cmax[row * nch + c]);
     m = wave_max(m);
     if (lane == 0) s_m[wave] = m;
     __syncthreads();
@@ -311,29 +328,19 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_laun
     for (int w = 1; w < ATT_WAVES; w++) M = fmaxf(M, s_m[w]);
     double sum = 0.0;
     if (M != -INFINITY) {
-        for (int base = 0; base < A.n_kv; base += SPAN) {
-            if (!one_batch) {
 #pragma unroll
-                for (int k = 0; k < STATS_BATCH; k++) {
-                    const int t = base + k * ATT_THREADS + threadIdx.x;
-                    v[k] = t < A.n_kv ? sc[t] : -INFINITY;
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < STATS_BATCH; k++) {
-                if (base + k * ATT_THREADS + (int) threadIdx.x < A.n_kv) sum += (double) exp_cr(v[k] - M);
-            }
+        for (int k = 0; k < STATS_PER_THREAD; k++) {
+            if (seg * STATS_SEG + k * ATT_THREADS + t < A.n_kv) sum += (double) exp_cr(v[k] - M);
         }
     }
     sum = wave_sum_d(sum);
     if (lane == 0) s_s[wave] = sum;
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (t == 0) {
         double tot = 0.0;
         for (int w = 0; w < ATT_WAVES; w++) tot += s_s[w];
-        float * st = S.stats + ((int64_t) q * A.n_head + h) * 2;
-        st[0] = M;
-        st[1] = tot > 0.0 ? (float) (1.0 / tot) : 0.0f;
+        S.ssum[row * attn_segs(A.n_kv) + seg] = tot;
+        if (seg == 0) S.rmax[row] = M;
     }
 }
 
@@ -363,12 +370,24 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
         vv[it] = make_uint4(0, 0, 0, 0);
         if (r < nt) vv[it] = *(const uint4 *) (vbase + (int64_t) (t0 + r) * A.v_nb2 + c * 8);
     }
+    // each row's M and 1/S (S: the segment sums added in segment order)
+    __shared__ float s_M[R], s_inv[R];
+    const int nseg = attn_segs(A.n_kv);
+    if ((int) threadIdx.x < n_rows) {
+        const int pr = threadIdx.x;
+        const int64_t row = (int64_t) (pr / G) * A.n_head + kvh * G + pr % G;
+        double tot = 0.0;
+        for (int k = 0; k < nseg; k++) tot += S.ssum[row * nseg + k];
+        s_M[pr] = S.rmax[row];
+        s_inv[pr] = tot > 0.0 ? (float) (1.0 / tot) : 0.0f;
+    }
+    __syncthreads();
     for (int i = threadIdx.x; i < n_rows * PV_CHUNK; i += ATT_THREADS) {
         const int pr = i / PV_CHUNK, t = i % PV_CHUNK;
         const int64_t row = (int64_t) (pr / G) * A.n_head + kvh * G + pr % G;
         float p = 0.0f;
         if (t < nt) {
-            const float M = S.stats[row * 2], inv = S.stats[row * 2 + 1];
+            const float M = s_M[pr], inv = s_inv[pr];
             const float e = M == -INFINITY ? 0.0f : exp_cr(S.scores[row * A.n_kv + t0 + t] - M);
             p = __half2float(__float2half_rn(as_f32(e * inv)));
         }
@@ -386,17 +405,22 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     for (int pr = wave; pr < n_rows; pr += ATT_WAVES) {
         const int q = pr / G, h = kvh * G + pr % G;
         if (lane < HD2) {
-            double a0 = 0.0, a1 = 0.0;
-#pragma unroll 8
-            for (int t = 0; t < nt; t++) {
-                const float p = s_p[pr][t];
+            // two independent chains per dimension (even and odd positions; exact sums as above;
+            // p is 0 past nt)
+            double a0 = 0.0, a1 = 0.0, b0 = 0.0, b1 = 0.0;
+#pragma unroll 4
+            for (int t = 0; t < nt; t += 2) {
+                const float p = s_p[pr][t], pn = s_p[pr][t + 1];
                 const float2 vf = __half22float2(*(const __half2 *) &s_v[t * STRIDE + lane]);
+                const float2 vn = __half22float2(*(const __half2 *) &s_v[(t + 1) * STRIDE + lane]);
                 a0 += (double) (p * vf.x);
                 a1 += (double) (p * vf.y);
+                b0 += (double) (pn * vn.x);
+                b1 += (double) (pn * vn.y);
             }
             double * part = S.parts + (((int64_t) split * A.n_q + q) * A.n_head + h) * HD;
-            part[2 * lane] = a0;
-            part[2 * lane + 1] = a1;
+            part[2 * lane] = a0 + b0;
+            part[2 * lane + 1] = a1 + b1;
         }
     }
 }
@@ -443,7 +467,7 @@ static void launch_attn_t(const attn_launch & A, hipStream_t st) {
     const int pv_splits = (A.n_kv + PV_CHUNK - 1) / PV_CHUNK;
     launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(ATT_THREADS),
            scores_dyn_floats<HD, G>(A.n_q) * sizeof(float), st, A);
-    launch(attn_stats_kernel, dim3(A.n_head, A.n_q), dim3(ATT_THREADS), 0, st, A);
+    launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
     launch((attn_pv_kernel<HD, G>), dim3(pv_splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
     launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(HD), 0, st, A, pv_splits);
 }

@@ -61,8 +61,10 @@ __device__ __forceinline__ void rope_cs(float theta_extrap, const rope_params & 
         theta = theta_interp * (1 - ramp_mix) + theta_extrap * ramp_mix;
         mscale *= 1.0f + 0.1f * log_cr(1.0f / p.freq_scale);
     }
-    c = cos_cr(theta) * mscale;
-    s = sin_cr(theta) * mscale;
+    float sv, cv;
+    sincos_cr(theta, sv, cv);
+    c = cv * mscale;
+    s = sv * mscale;
 }
 
 // the (cos, sin) of rotation pair ip at position pos, as the RoPE kernel forms them (theta by
