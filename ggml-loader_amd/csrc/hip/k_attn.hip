@@ -19,7 +19,7 @@
 //            coalesced 16-byte loads (rows padded by one dword so lane t reading row t is
 //            conflict-free); one wave per (query, head of the GQA group), lane = position; each
 //            row's chunk maximum.
-//   stats    (query, head, 1024-position segment) workgroups: M = the maximum of the row's chunk
+//   stats    (query, head, 2048-position segment) workgroups: M = the maximum of the row's chunk
 //            maxima, the segment's sum of exp(s - M) in double.
 //   pv       (128-position chunk, KV head) workgroups: 1/S from the segment sums (added in segment
 //            order), p = F16(exp(s - M) * (1/S)) for the chunk, the chunk's V rows staged in LDS
@@ -40,7 +40,7 @@ constexpr int ATT_THREADS = 256;
 constexpr int ATT_WAVES = ATT_THREADS / WAVE;
 
 constexpr int PV_CHUNK = 128;
-constexpr int STATS_PER_THREAD = 4;                          // scores per thread of a statistics workgroup
+constexpr int STATS_PER_THREAD = 8;                          // scores per thread of a statistics workgroup
 constexpr int STATS_SEG = ATT_THREADS * STATS_PER_THREAD;    // positions per statistics workgroup
 
 __host__ __device__ inline int attn_chunks(int n_kv) { return (n_kv + ATT_CHUNK - 1) / ATT_CHUNK; }
@@ -202,8 +202,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
         s_kw[min(t, HD - 1)] = kw;
 #pragma unroll
         for (int q = 0; q < ATT_MAX_Q; q++) s_mk[min(q, n_q - 1) * ATT_CHUNK + min(lane, nt - 1)] = mk[q];
-        float c, sn;
-        rope_pair_cs(A.rq.p, A.rq.ff, my_pos, tp % half, c, sn);
+        float c = 1.0f, sn = 0.0f;
+        if (A.rope) rope_pair_cs(A.rq.p, A.rq.ff, my_pos, tp % half, c, sn);
         s_cs[tp] = make_float2(c, sn);
     });
     __syncthreads();   // K chunk, source rows, weights, mask, (cos, sin) in LDS

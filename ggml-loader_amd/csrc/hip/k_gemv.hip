@@ -219,33 +219,44 @@ __device__ __forceinline__ void q4k_sc_m(uint32_t w0, uint32_t w1, uint32_t w2, 
     }
 }
 
+// 4x4 byte transpose: t_b = { byte b of a, byte b of b, byte b of c, byte b of d } (v_perm_b32:
+// selector bytes 0-3 pick from the second operand, 4-7 from the first)
+__device__ __forceinline__ void transpose4(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t t[4]) {
+    const uint32_t p0 = __builtin_amdgcn_perm(b, a, 0x05010400u), p1 = __builtin_amdgcn_perm(b, a, 0x07030602u);
+    const uint32_t q0 = __builtin_amdgcn_perm(d, c, 0x05010400u), q1 = __builtin_amdgcn_perm(d, c, 0x07030602u);
+    t[0] = __builtin_amdgcn_perm(q0, p0, 0x05040100u);
+    t[1] = __builtin_amdgcn_perm(q0, p0, 0x07060302u);
+    t[2] = __builtin_amdgcn_perm(q1, p1, 0x05040100u);
+    t[3] = __builtin_amdgcn_perm(q1, p1, 0x07060302u);
+}
+
+// The 32 bytes of a sub-block rearranged so that dword l holds elements l, l+8, l+16, l+24 (the
+// elements ggml's generic q4_K x q8_K dot accumulates into aux32[l]); in place, 8 dwords.
+__device__ __forceinline__ void q4k_group_by_l(uint32_t * w) {
+    uint32_t t[8];
+    transpose4(w[0], w[2], w[4], w[6], t);
+    transpose4(w[1], w[3], w[5], w[7], t + 4);
+#pragma unroll
+    for (int l = 0; l < 8; l++) w[l] = t[l];
+}
+
 // Per-lane integer partials of Q4_K unit u = (super-block u/4, sub-block pair p = u%4): aux[l] =
 // sum over the pair's 64 elements e with e%8 == l of sc_sub * q4 * q8, mins = the pair's share of
 // sum(bsums * m). (ggml's generic q4_K x q8_K kernel accumulates exactly these integers.) hdr is
-// the block's first 16 bytes (d, dmin, scales), qa/qb the pair's 32 quant bytes.
-__device__ __forceinline__ void q4k_unit_ints(const uint4 hdr, const uint4 qa, const uint4 qb, int p, const int8_t * xq,
-                                              const int16_t * xbs, int aux[8], int & mins) {
+// the block's first 16 bytes (d, dmin, scales), qa/qb the pair's 32 quant bytes (low nibbles:
+// sub-block 2p, high nibbles: 2p + 1); xa/xb the two sub-blocks' activations grouped by l
+// (q4k_group_by_l), so each aux[l] takes one v_dot4 per sub-block.
+__device__ __forceinline__ void q4k_unit_ints(const uint4 hdr, const uint4 qa, const uint4 qb, int p, const int * xa,
+                                              const int * xb, const int16_t * xbs, int aux[8], int & mins) {
     int sc_a, m_a, sc_b, m_b;
     q4k_sc_m(hdr.y, hdr.z, hdr.w, 2 * p, sc_a, m_a);
     q4k_sc_m(hdr.y, hdr.z, hdr.w, 2 * p + 1, sc_b, m_b);
-    const uint32_t q[8] = { qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w };
-    const int4 x0 = *(const int4 *) (xq + 0), x1 = *(const int4 *) (xq + 16);
-    const int4 x2 = *(const int4 *) (xq + 32), x3 = *(const int4 *) (xq + 48);
-    const int xl[8] = { x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w };
-    const int xh[8] = { x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w };
+    uint32_t q[8] = { qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w };
+    q4k_group_by_l(q);
 #pragma unroll
-    for (int l = 0; l < 8; l++) aux[l] = 0;
-    // element e of a sub-block sits in dword e/4, byte e%4; e%8 = 4*(dword%2) + byte
-#pragma unroll
-    for (int w = 0; w < 8; w++) {
-        const uint32_t lo = q[w] & 0x0F0F0F0Fu, hi = (q[w] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-        for (int byte = 0; byte < 4; byte++) {
-            const int l = 4 * (w & 1) + byte;
-            const int ql = (int) ((lo >> (8 * byte)) & 0xff), qh = (int) ((hi >> (8 * byte)) & 0xff);
-            const int vl = (int) (int8_t) ((xl[w] >> (8 * byte)) & 0xff), vh = (int) (int8_t) ((xh[w] >> (8 * byte)) & 0xff);
-            aux[l] += sc_a * (ql * vl) + sc_b * (qh * vh);
-        }
+    for (int l = 0; l < 8; l++) {
+        const int lo = (int) (q[l] & 0x0F0F0F0Fu), hi = (int) ((q[l] >> 4) & 0x0F0F0F0Fu);
+        aux[l] = sc_a * dot4(lo, xa[l], 0) + sc_b * dot4(hi, xb[l], 0);
     }
     mins = m_a * ((int) xbs[4 * p] + (int) xbs[4 * p + 1]) + m_b * ((int) xbs[4 * p + 2] + (int) xbs[4 * p + 3]);
 }
@@ -705,6 +716,16 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
             }
         }
         stage_x<TYPE, PRO>(L, xcol, s, s_red, xv, wv);
+        // the staged activation's sub-blocks grouped by l (one thread per sub-block)
+        for (int sbk = threadIdx.x; sbk < K / 32; sbk += blockDim.x) {
+            uint32_t w8[8];
+            const uint4 lo4 = ((const uint4 *) (s.xq + sbk * 32))[0], hi4 = ((const uint4 *) (s.xq + sbk * 32))[1];
+            w8[0] = lo4.x; w8[1] = lo4.y; w8[2] = lo4.z; w8[3] = lo4.w; w8[4] = hi4.x; w8[5] = hi4.y; w8[6] = hi4.z; w8[7] = hi4.w;
+            q4k_group_by_l(w8);
+            ((uint4 *) (s.xq + sbk * 32))[0] = make_uint4(w8[0], w8[1], w8[2], w8[3]);
+            ((uint4 *) (s.xq + sbk * 32))[1] = make_uint4(w8[4], w8[5], w8[6], w8[7]);
+        }
+        __syncthreads();
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++) {
             float * terms = s.terms + (rib * NCH + ch) * nsb * 9;
@@ -717,7 +738,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                 int aux[8], mins = 0;
 #pragma unroll
                 for (int k = 0; k < 8; k++) aux[k] = 0;
-                if (has) q4k_unit_ints(hd[ch][it], qa[ch][it], qb[ch][it], p, s.xq + sb * 256 + 64 * p, s.xbs + sb * 16, aux, mins);
+                if (has) {
+                    const int * xs = (const int *) (s.xq + sb * 256 + 64 * p);
+                    q4k_unit_ints(hd[ch][it], qa[ch][it], qb[ch][it], p, xs, xs + 8, s.xbs + sb * 16, aux, mins);
+                }
                 // the 4 units of a super-block sit on 4 consecutive lanes: combine (exact integers)
 #pragma unroll
                 for (int k = 0; k < 8; k++) {
