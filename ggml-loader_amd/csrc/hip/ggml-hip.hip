@@ -308,7 +308,8 @@ enum fuse_bits {
     FUSE_NORMQ  = 64,  // rms_norm * w folded into the prologue of the GEMVs that consume it
     FUSE_ROPE   = 128, // RoPE stored straight into the KV cache; independent RoPE/copies in one launch
     FUSE_ROUTE  = 256, // MoE router softmax -> top-k -> renormalized weights in one launch
-    FUSE_ALL    = 511,
+    FUSE_MC     = 512, // several activation columns per GEMV workgroup; mul_mat_id grouped by expert
+    FUSE_ALL    = 1023,
 };
 
 struct hip_backend_ctx {
@@ -867,7 +868,7 @@ private:
                     if (m->ne[1] == rows && norm_deferrable(u, N) && ((uintptr_t) x->data | (uintptr_t) w->data) % 16 == 0) {
                         const gemv_norm nz{ (const float *) x->data, N, (const float *) w->data, eps, 1 };
                         done_[u] = true;
-                        if (max_consumer_rows(u) <= GEMV_PROLOGUE_MAX_ROWS && !gemm_consumer(u)) {
+                        if (max_consumer_rows(u) <= GEMV_PROLOGUE_MAX_ROWS && !gemm_consumer(u) && (rows == 1 || !fuse(FUSE_MC))) {
                             norm_[m] = nz;      // every consumer workgroup normalizes for itself
                             return;
                         }
@@ -1000,6 +1001,37 @@ private:
         launch_mul_mat_generic(tv(n->src[0]), tv(n->src[1]), tv(n), st_);
     }
 
+    // Columns per grouped workgroup: about the columns an active expert gets with uniform routing
+    // (1 - (1 - k/E)^T of the experts are active), as a power of two in [2, 16]
+    static int moe_cols_per_item(int n_slots, int n_tok, int n_experts) {
+        const double active = n_experts * (1.0 - std::pow(1.0 - std::min(1.0, (double) n_slots / n_experts), (double) n_tok));
+        const double avg = (double) n_slots * n_tok / std::max(1.0, active);
+        int nc = 2;
+        while (nc < GEMV_MC_MAX_COLS && nc < avg) nc *= 2;
+        return nc;
+    }
+
+    // The columns of a mul_mat_id grouped by expert (once per ids tensor and graph compute)
+    std::unordered_map<const ggml_tensor *, expert_groups> groups_;
+    const expert_groups & expert_groups_of(const ggml_tensor * ids, int n_experts) {
+        auto it = groups_.find(ids);
+        if (it != groups_.end()) return it->second;
+        const int n_slots = (int) ids->ne[0], n_tok = (int) ids->ne[1], ncol = n_slots * n_tok;
+        expert_groups g{};
+        g.nc = moe_cols_per_item(n_slots, n_tok, n_experts);
+        g.max_items = std::min(n_experts, ncol) + (ncol + g.nc - 1) / g.nc;
+        g.count = (int32_t *) c_.scratch.alloc((size_t) n_experts * sizeof(int32_t));
+        g.offset = (int32_t *) c_.scratch.alloc((size_t) n_experts * sizeof(int32_t));
+        g.cols = (int32_t *) c_.scratch.alloc((size_t) ncol * sizeof(int32_t));
+        g.items = (int32_t *) c_.scratch.alloc((size_t) g.max_items * 3 * sizeof(int32_t));
+        g.n_items = (int32_t *) c_.scratch.alloc(sizeof(int32_t));
+        {
+            prof_scope ps(this, "moe_group", 0);
+            launch_moe_group((const int32_t *) ids->data, (int64_t) (ids->nb[1] / sizeof(int32_t)), n_slots, n_tok, n_experts, g, st_);
+        }
+        return groups_[ids] = g;
+    }
+
     // Whether the GEMVs of a group read activation x (f32, not yet quantized) straight from memory,
     // quantizing it in their prologue, rather than after a quantization launch of its own: for
     // launches whose rows (per column) are few enough that redoing it per workgroup stays cheap.
@@ -1066,10 +1098,35 @@ private:
         }
 
         const int kind = dot_kind(wtype);
+        // several columns (tokens) per workgroup: the activation is quantized once, up front
+        const int64_t n_tok = by_id ? ids->ne[1] : ncols;
+        const int mc_nc = by_id ? moe_cols_per_item((int) ids->ne[0], (int) n_tok, (int) n->src[0]->ne[2]) : 0;
+        const bool mc = fuse(FUSE_MC) && n_tok >= 2 && gemv_mc_fits(wtype, (int) K, false, mc_nc) &&
+                        (gate < 0 || gemv_mc_fits(wtype, (int) K, true, mc_nc));
         const auto nz = norm_.find(x);
         gemv_norm pro{};
         const act_entry * xa = nullptr;
-        if (nz != norm_.end()) {
+        if (mc) {
+            if (act_.count(x) && act_.at(x).kind == kind) {
+                xa = &act_.at(x);
+            } else if (nz != norm_.end() && K <= gemv_prologue_max_k(wtype, nz->second.rms != 0)) {
+                act_entry e = alloc_act(kind, K, ggml_nrows(x));
+                gemv_launch Q{};
+                Q.type = wtype;
+                Q.K = (int) K;
+                Q.ncols = (int) ggml_nrows(x);
+                Q.norm = nz->second;
+                {
+                    prof_scope ps(this, "act_quant", (double) (K * ggml_nrows(x) * 4));
+                    launch_act_quant(Q, e.q8, e.q8k, st_);
+                }
+                act_[x] = e;
+                xa = &act_[x];
+            } else {
+                if (nz != norm_.end()) HIP_ABORT("mul_mat '%s': normalized input too long to quantize", n->name);
+                xa = ensure_act(x, kind);
+            }
+        } else if (nz != norm_.end()) {
             pro = nz->second;
         } else if (act_.count(x) && act_.at(x).kind == kind) {
             xa = &act_.at(x);
@@ -1135,6 +1192,12 @@ private:
             L.expert_rows = n->src[0]->ne[1];
         }
         const double x_bytes = (double) (K * ggml_nrows(x) * 4) + (xa ? 0.0 : (double) (K * 4));
+        // one column per workgroup, or several (mul_mat_id: the tokens routed to each expert)
+        const expert_groups * G = mc && by_id ? &expert_groups_of(ids, (int) n->src[0]->ne[2]) : nullptr;
+        auto run = [&](const gemv_launch & X) {
+            if (mc) launch_gemv_mc(X, G, G ? (int) n_tok : X.ncols, st_);
+            else launch_gemv(X, st_);
+        };
 
         if (gate >= 0) {
             // SwiGLU launch for (gate, up); the rest of the group goes in a second launch
@@ -1150,14 +1213,14 @@ private:
             S.m[0].add = nullptr;
             sb -= (double) (g_->nodes[gate]->ne[0] * ncols * 4); // gate/up outputs are not written, act is
             // the GEMVs reading act (the down projection) quantize it in their prologue
-            const int dtype = fuse(FUSE_ACTQ) ? gemv_only_consumers(mulnode) : -1;
+            const int dtype = fuse(FUSE_ACTQ) && !mc ? gemv_only_consumers(mulnode) : -1;
             if (dtype >= 0 && mn->ne[0] <= gemv_prologue_max_k(dtype, false) && ((uintptr_t) mn->data) % 16 == 0) {
                 norm_[mn] = gemv_norm{ (const float *) mn->data, (int64_t) (mn->nb[1] / sizeof(float)), nullptr, 0.0f, 0 };
             }
             {
                 prof_scope ps(this, wtype == GGML_TYPE_Q4_0 ? "gemv_q4_0_swiglu" :
                                     wtype == GGML_TYPE_Q8_0 ? "gemv_q8_0_swiglu" : "gemv_q4_K_swiglu", sb);
-                launch_gemv(S, st_);
+                run(S);
             }
             wrote_.push_back(mn);
             done_[gate] = done_[up] = done_[mulnode] = true;
@@ -1173,7 +1236,7 @@ private:
         for (size_t k = 0; k < group.size(); k++) fill_mat(L.m[k], group[k], bytes, true);
         {
             prof_scope ps(this, wtype == GGML_TYPE_Q4_0 ? "gemv_q4_0" : wtype == GGML_TYPE_Q8_0 ? "gemv_q8_0" : "gemv_q4_K", bytes);
-            launch_gemv(L, st_);
+            run(L);
         }
         for (int j : group) done_[j] = true;
     }

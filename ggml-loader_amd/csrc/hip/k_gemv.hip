@@ -12,6 +12,7 @@
 // order). Rows of up to four matrices (Q, K and V, or gate and up) are concatenated in one grid
 // so one launch streams all of them; grid.y runs over the activation columns.
 #include "kernels.h"
+#include "gemv_ops.h"
 
 #include "ggml.h"
 
@@ -157,145 +158,6 @@ void launch_quantize_q8k(const float * x, int64_t x_col_stride, int64_t K, int64
 
 // ---------------------------------------------------------------------------------------------
 // GEMV kernels
-
-// Grid rows: the matrices' rows one after another, each matrix starting on a workgroup boundary
-// (row_begin[i] is a multiple of rows_per_block), so every workgroup reads a single matrix and
-// selects it with uniform (scalar) arithmetic. Rows past a matrix's n_rows are padding.
-struct gemv_kargs {
-    gemv_launch L;
-    int total_rows;
-    int row_begin[GEMV_MAX_MATS + 1];
-    int rows_per_block;
-};
-
-__device__ __forceinline__ int find_mat(const gemv_kargs & a, int row) {
-    int m = 0;
-#pragma unroll
-    for (int i = 1; i < GEMV_MAX_MATS; i++) if (i < a.L.n_mats && row >= a.row_begin[i]) m = i;
-    return m;
-}
-
-// sum(q * x) over one Q4_0 block with q in 0..15 (the -8 offset is applied through the block sum)
-__device__ __forceinline__ int dot_q4_0_block(const uint4 q, const int4 xa, const int4 xb) {
-    int s = 0;
-    s = dot4((int) (q.x & 0x0F0F0F0Fu), xa.x, s);
-    s = dot4((int) (q.y & 0x0F0F0F0Fu), xa.y, s);
-    s = dot4((int) (q.z & 0x0F0F0F0Fu), xa.z, s);
-    s = dot4((int) (q.w & 0x0F0F0F0Fu), xa.w, s);
-    s = dot4((int) ((q.x >> 4) & 0x0F0F0F0Fu), xb.x, s);
-    s = dot4((int) ((q.y >> 4) & 0x0F0F0F0Fu), xb.y, s);
-    s = dot4((int) ((q.z >> 4) & 0x0F0F0F0Fu), xb.z, s);
-    s = dot4((int) ((q.w >> 4) & 0x0F0F0F0Fu), xb.w, s);
-    return s;
-}
-
-__device__ __forceinline__ int dot_q8_0_block(const uint4 qa, const uint4 qb, const int4 xa, const int4 xb) {
-    int s = 0;
-    s = dot4((int) qa.x, xa.x, s);
-    s = dot4((int) qa.y, xa.y, s);
-    s = dot4((int) qa.z, xa.z, s);
-    s = dot4((int) qa.w, xa.w, s);
-    s = dot4((int) qb.x, xb.x, s);
-    s = dot4((int) qb.y, xb.y, s);
-    s = dot4((int) qb.z, xb.z, s);
-    s = dot4((int) qb.w, xb.w, s);
-    return s;
-}
-
-// byte i (0..11) of the 12 Q4_K scale bytes held in three dwords
-__device__ __forceinline__ int sbyte(uint32_t w0, uint32_t w1, uint32_t w2, int i) {
-    const uint32_t w = i < 4 ? w0 : (i < 8 ? w1 : w2);
-    return (int) ((w >> (8 * (i & 3))) & 0xff);
-}
-
-// 6-bit scale/min j (0..7) of a Q4_K block (moe_stream/dequant.c:132-141 layout)
-__device__ __forceinline__ void q4k_sc_m(uint32_t w0, uint32_t w1, uint32_t w2, int j, int & sc, int & m) {
-    if (j < 4) {
-        sc = sbyte(w0, w1, w2, j) & 63;
-        m = sbyte(w0, w1, w2, j + 4) & 63;
-    } else {
-        sc = (sbyte(w0, w1, w2, j + 4) & 0x0F) | ((sbyte(w0, w1, w2, j - 4) >> 6) << 4);
-        m = (sbyte(w0, w1, w2, j + 4) >> 4) | ((sbyte(w0, w1, w2, j) >> 6) << 4);
-    }
-}
-
-// 4x4 byte transpose: t_b = { byte b of a, byte b of b, byte b of c, byte b of d } (v_perm_b32:
-// selector bytes 0-3 pick from the second operand, 4-7 from the first)
-__device__ __forceinline__ void transpose4(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t t[4]) {
-    const uint32_t p0 = __builtin_amdgcn_perm(b, a, 0x05010400u), p1 = __builtin_amdgcn_perm(b, a, 0x07030602u);
-    const uint32_t q0 = __builtin_amdgcn_perm(d, c, 0x05010400u), q1 = __builtin_amdgcn_perm(d, c, 0x07030602u);
-    t[0] = __builtin_amdgcn_perm(q0, p0, 0x05040100u);
-    t[1] = __builtin_amdgcn_perm(q0, p0, 0x07060302u);
-    t[2] = __builtin_amdgcn_perm(q1, p1, 0x05040100u);
-    t[3] = __builtin_amdgcn_perm(q1, p1, 0x07060302u);
-}
-
-// The 32 bytes of a sub-block rearranged so that dword l holds elements l, l+8, l+16, l+24 (the
-// elements ggml's generic q4_K x q8_K dot accumulates into aux32[l]); in place, 8 dwords.
-__device__ __forceinline__ void q4k_group_by_l(uint32_t * w) {
-    uint32_t t[8];
-    transpose4(w[0], w[2], w[4], w[6], t);
-    transpose4(w[1], w[3], w[5], w[7], t + 4);
-#pragma unroll
-    for (int l = 0; l < 8; l++) w[l] = t[l];
-}
-
-// Per-lane integer partials of Q4_K unit u = (super-block u/4, sub-block pair p = u%4): aux[l] =
-// sum over the pair's 64 elements e with e%8 == l of sc_sub * q4 * q8, mins = the pair's share of
-// sum(bsums * m). (ggml's generic q4_K x q8_K kernel accumulates exactly these integers.) hdr is
-// the block's first 16 bytes (d, dmin, scales), qa/qb the pair's 32 quant bytes (low nibbles:
-// sub-block 2p, high nibbles: 2p + 1); xa/xb the two sub-blocks' activations grouped by l
-// (q4k_group_by_l), so each aux[l] takes one v_dot4 per sub-block.
-__device__ __forceinline__ void q4k_unit_ints(const uint4 hdr, const uint4 qa, const uint4 qb, int p, const int * xa,
-                                              const int * xb, const int16_t * xbs, int aux[8], int & mins) {
-    int sc_a, m_a, sc_b, m_b;
-    q4k_sc_m(hdr.y, hdr.z, hdr.w, 2 * p, sc_a, m_a);
-    q4k_sc_m(hdr.y, hdr.z, hdr.w, 2 * p + 1, sc_b, m_b);
-    uint32_t q[8] = { qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w };
-    q4k_group_by_l(q);
-#pragma unroll
-    for (int l = 0; l < 8; l++) {
-        const int lo = (int) (q[l] & 0x0F0F0F0Fu), hi = (int) ((q[l] >> 4) & 0x0F0F0F0Fu);
-        aux[l] = sc_a * dot4(lo, xa[l], 0) + sc_b * dot4(hi, xb[l], 0);
-    }
-    mins = m_a * ((int) xbs[4 * p] + (int) xbs[4 * p + 1]) + m_b * ((int) xbs[4 * p + 2] + (int) xbs[4 * p + 3]);
-}
-
-// floats between the term rows of two Q4_0/Q8_0 chains: 4 more than the terms, so the 16-byte
-// reads of consecutive chains (one lane each) start on different LDS banks
-__host__ __device__ constexpr int gemv_term_stride(int nb) { return nb + 4; }
-
-// The float sum of a chain's block terms in block order (ggml-cpu's sumf += term), 32 terms per
-// step with the next step's LDS reads in flight during the adds.
-__device__ __forceinline__ float ordered_sum(const float * terms, int nb) {
-    float acc = 0.0f;
-    if ((nb & 31) == 0) {
-        const float4 * t4 = (const float4 *) terms;
-        const int n32 = nb / 32;
-        float4 cur[8], nxt[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) cur[k] = t4[k];
-        for (int b = 0; b < n32; b++) {
-            if (b + 1 < n32) {
-#pragma unroll
-                for (int k = 0; k < 8; k++) nxt[k] = t4[(b + 1) * 8 + k];
-            }
-#pragma unroll
-            for (int k = 0; k < 8; k++) acc = acc + cur[k].x + cur[k].y + cur[k].z + cur[k].w;
-#pragma unroll
-            for (int k = 0; k < 8; k++) cur[k] = nxt[k];
-        }
-    } else if ((nb & 3) == 0) {
-        const float4 * t4 = (const float4 *) terms;
-        for (int b4 = 0; b4 < nb / 4; b4++) {
-            const float4 v = t4[b4];
-            acc = acc + v.x + v.y + v.z + v.w;
-        }
-    } else {
-        for (int b = 0; b < nb; b++) acc = acc + terms[b];
-    }
-    return acc;
-}
 
 // dynamic LDS layout: [staged activation][terms]
 struct gemv_lds {
@@ -716,15 +578,8 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
             }
         }
         stage_x<TYPE, PRO>(L, xcol, s, s_red, xv, wv);
-        // the staged activation's sub-blocks grouped by l (one thread per sub-block)
-        for (int sbk = threadIdx.x; sbk < K / 32; sbk += blockDim.x) {
-            uint32_t w8[8];
-            const uint4 lo4 = ((const uint4 *) (s.xq + sbk * 32))[0], hi4 = ((const uint4 *) (s.xq + sbk * 32))[1];
-            w8[0] = lo4.x; w8[1] = lo4.y; w8[2] = lo4.z; w8[3] = lo4.w; w8[4] = hi4.x; w8[5] = hi4.y; w8[6] = hi4.z; w8[7] = hi4.w;
-            q4k_group_by_l(w8);
-            ((uint4 *) (s.xq + sbk * 32))[0] = make_uint4(w8[0], w8[1], w8[2], w8[3]);
-            ((uint4 *) (s.xq + sbk * 32))[1] = make_uint4(w8[4], w8[5], w8[6], w8[7]);
-        }
+        // the staged activation's sub-blocks grouped by l
+        group_by_l_lds(s.xq, K / 32);
         __syncthreads();
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++) {
@@ -740,7 +595,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                 for (int k = 0; k < 8; k++) aux[k] = 0;
                 if (has) {
                     const int * xs = (const int *) (s.xq + sb * 256 + 64 * p);
-                    q4k_unit_ints(hd[ch][it], qa[ch][it], qb[ch][it], p, xs, xs + 8, s.xbs + sb * 16, aux, mins);
+                    q4k_unit_dot(q4k_prepare(hd[ch][it], qa[ch][it], qb[ch][it], p), p, xs, xs + 8, s.xbs + sb * 16, aux, mins);
                 }
                 // the 4 units of a super-block sit on 4 consecutive lanes: combine (exact integers)
 #pragma unroll

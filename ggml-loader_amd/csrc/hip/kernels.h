@@ -143,6 +143,26 @@ struct gemv_launch {
 };
 
 void launch_gemv(const gemv_launch & L, hipStream_t st);
+// Several activation columns per workgroup (k_gemv_mc.hip): each weight row block is read once for
+// up to GEMV_MC_MAX_COLS columns; the activation must be quantized already (L.xq, no L.norm). With
+// groups (mul_mat_id): the workgroups of expert e take the columns the ids route to e, listed by
+// launch_moe_group; max_cols is then the most columns one expert can get (the token count).
+constexpr int GEMV_MC_MAX_COLS = 16;
+struct expert_groups {
+    int32_t * count;           // [n_experts] columns routed to each expert
+    int32_t * offset;          // [n_experts] start of each expert's list in cols
+    int32_t * cols;            // [n_slots * n_tok] grid columns (token * n_slots + slot), by expert
+    int32_t * items;           // [max_items][3] workgroup columns: expert, start in cols, count (<= nc)
+    int32_t * n_items;         // items in use
+    int nc;                    // columns per item
+    int max_items;             // n_experts (or the column count, if smaller) + columns / nc
+};
+bool gemv_mc_supported(const gemv_launch & L, int max_cols);
+// a workgroup shape exists for this row length (nc > 0: with exactly nc columns per workgroup)
+bool gemv_mc_fits(int type, int K, bool swiglu, int nc = 0);
+void launch_gemv_mc(const gemv_launch & L, const expert_groups * G, int max_cols, hipStream_t st);
+void launch_moe_group(const int32_t * ids, int64_t ids_stride, int n_slots, int n_tok, int n_experts, const expert_groups & g,
+                      hipStream_t st);
 // L.norm's prologue for L.ncols columns of L.K, written once to q8 (Q4_0/Q8_0 consumers) or q8k (Q4_K)
 void launch_act_quant(const gemv_launch & L, const q8_act & q8, const q8k_act & q8k, hipStream_t st);
 // consumers with more rows than this get the activation quantized once instead of per workgroup

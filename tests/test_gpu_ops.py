@@ -91,7 +91,7 @@ def test_get_rows(hip, cpu, qtype):
     (gl.Q4_K, 9728, 512),
     (gl.Q4_K, 768, 200),
 ])
-@pytest.mark.parametrize("ncols", [1, 3, 8, 13])
+@pytest.mark.parametrize("ncols", [1, 3, 8, 13, 17, 40])
 def test_gemv(hip, cpu, qtype, K, N, ncols):
     w = qweight(qtype, K, N, K + N)
     x = rng(7).standard_normal((ncols, K)).astype(np.float32)
@@ -215,7 +215,7 @@ def test_gemv_residual_and_qkv_group(hip, cpu, qtype):
 
 
 @pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K])
-@pytest.mark.parametrize("ncols", [1, 2])
+@pytest.mark.parametrize("ncols", [1, 2, 16, 21])
 def test_swiglu_ffn(hip, cpu, qtype, ncols):
     E, F = 512, 1536
     wg, wu, wd = qweight(qtype, E, F, 21), qweight(qtype, E, F, 22), qweight(qtype, F, E, 23)
@@ -616,7 +616,7 @@ def test_argsort_sum_rows_div(hip, cpu, n):
 
 
 @pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K])
-@pytest.mark.parametrize("n_tok", [1, 3])
+@pytest.mark.parametrize("n_tok", [1, 3, 16, 37])
 def test_moe_ffn(hip, cpu, qtype, n_tok):
     """The routed expert FFN (router, top-k, renormalized weights, mul_mat_id gate/up/down, SwiGLU,
     weighted slot sum, residual): fused into the GEMV and weighted-sum kernels or node by node."""
@@ -638,6 +638,7 @@ def test_moe_ffn(hip, cpu, qtype, n_tok):
         assert np.array_equal(a, b), (fusion, rel_err(a, b))
     _, names = profiled(hip, lambda: run_on(hip, build))
     assert "moe_route" in names and "argsort" not in names, names
+    assert (n_tok >= 2) == ("moe_group" in names), names   # several tokens: experts read once for all of theirs
 
 
 @pytest.mark.parametrize("E,k,n_tok", [(128, 8, 1), (128, 8, 16), (60, 4, 3), (1024, 32, 2), (8, 8, 1)])
