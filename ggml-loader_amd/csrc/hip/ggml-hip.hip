@@ -1431,20 +1431,24 @@ private:
         return true;
     }
 
-    // More queries than the decode kernels take, over more positions than the prefill kernel holds
-    // in LDS (a multi-token step deep into the context): the decode kernels once per group of 4
-    // queries, each group with its own rows of Q, mask and output (same arithmetic per query).
+    // More queries than the fused decode path takes, over more positions than the prefill kernel
+    // holds in LDS (a multi-token step deep into the context): the decode kernels, whose workgroups
+    // take 4 queries each, over up to ATT_DECODE_MAX_Q queries per launch, each launch with its own
+    // rows of Q, mask and output (same arithmetic per query).
     void attn_decode_grouped(const attn_launch & A0) {
         attn_launch A = A0;
-        A.scratch_bytes = attn_scratch_bytes(A0.n_kv, 4, A0.n_head, A0.hd);
+        A.scratch_bytes = attn_scratch_bytes(A0.n_kv, std::min(A0.n_q, ATT_DECODE_MAX_Q), A0.n_head, A0.hd);
         A.scratch = (float *) c_.scratch.alloc((size_t) A.scratch_bytes);
-        A.out_q = q8_act{};
         A.rope = 0;
-        for (int q0 = 0; q0 < A0.n_q; q0 += 4) {
-            A.n_q = std::min(4, A0.n_q - q0);
+        for (int q0 = 0; q0 < A0.n_q; q0 += ATT_DECODE_MAX_Q) {
+            A.n_q = std::min(ATT_DECODE_MAX_Q, A0.n_q - q0);
             A.q = A0.q + (int64_t) q0 * A0.q_nb2;
             A.mask = A0.mask ? (const char *) A0.mask + (int64_t) q0 * A0.mask_nb1 : nullptr;
             A.out = A0.out + (int64_t) q0 * A0.out_nb1;
+            if (A0.out_q.qs) {
+                const int64_t K = (int64_t) A0.n_head * A0.hd;
+                A.out_q = q8_act{ A0.out_q.qs + q0 * K, A0.out_q.d + q0 * (K / 32), A0.out_q.s + q0 * (K / 32) };
+            }
             launch_attn_decode(A, st_);
         }
     }
@@ -1486,6 +1490,11 @@ private:
             prof_scope ps(this, "attn_prefill", bytes);
             launch_attn_prefill(A, st_);
         } else if (n_q > 4) {
+            if (wanted_act_kind(M.ct) == 1) {
+                act_entry e = alloc_act(1, ctn->ne[0], n_q);
+                A.out_q = e.q8;
+                act_[ctn] = e;
+            }
             prof_scope ps(this, "attn_decode", bytes * ((n_q + 3) / 4));
             attn_decode_grouped(A);
         } else {

@@ -128,7 +128,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int t0 = split * ATT_CHUNK;
     const int nt = min(ATT_CHUNK, A.n_kv - t0);
-    const int n_q = A.n_q;
+    const int q0 = blockIdx.z * ATT_MAX_Q;            // this workgroup's queries: q0 .. q0 + n_q - 1
+    const int n_q = min(ATT_MAX_Q, A.n_q - q0);
     const attn_scratch S = scratch_of(A);
     float * s_q = s_dyn;                              // [n_q * G][HD]
     float * s_kx = s_q + n_q * G * HD;                // [n_q][HD]
@@ -157,7 +158,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
     for (int j = 0; j < QR; j++) {
         const int i = min(t + j * ATT_THREADS, nqe - 1);
         const int pr = i / HD;
-        qv[j] = qb[(int64_t) (kvh * G + pr % G) * qs1 + (int64_t) (pr / G) * qs2 + i % HD];
+        qv[j] = qb[(int64_t) (kvh * G + pr % G) * qs1 + (int64_t) (q0 + pr / G) * qs2 + i % HD];
     }
     const float * kb = !A.rope ? qb : knorm ? A.kn.x : (const float *) A.rk.src.data;
     const int64_t ks1 = !A.rope ? qs1 : knorm ? A.kn.nb1 : A.rk.src.nb[1] / 4;
@@ -181,7 +182,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
     float mk[ATT_MAX_Q];
 #pragma unroll
     for (int q = 0; q < ATT_MAX_Q; q++) {
-        mk[q] = mrow[mask32 ? (int64_t) min(q, n_q - 1) * (A.mask_nb1 / 4) + t0 + min(lane, nt - 1) : 0];
+        mk[q] = mrow[mask32 ? (int64_t) (q0 + min(q, n_q - 1)) * (A.mask_nb1 / 4) + t0 + min(lane, nt - 1) : 0];
     }
 
     // While the chunk's K rows are in flight: the loaded values into LDS and the (cos, sin) of every
@@ -294,13 +295,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
             }
             const double acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
             // softmax input as the graph forms it: (float) kq * scale + mask
-            const float s = (float) acc * A.scale + (mask32 ? s_mk[q * ATT_CHUNK + lane] : mask_at(A, q, t0 + lane));
-            S.scores[((int64_t) q * A.n_head + h) * A.n_kv + t0 + lane] = s;
+            const float s = (float) acc * A.scale + (mask32 ? s_mk[q * ATT_CHUNK + lane] : mask_at(A, q0 + q, t0 + lane));
+            S.scores[((int64_t) (q0 + q) * A.n_head + h) * A.n_kv + t0 + lane] = s;
             sv = s;
         }
         // the chunk's maximum of the row, for the statistics
         sv = wave_max(sv);
-        if (lane == 0) S.cmax[((int64_t) q * A.n_head + h) * attn_chunks(A.n_kv) + split] = sv;
+        if (lane == 0) S.cmax[((int64_t) (q0 + q) * A.n_head + h) * attn_chunks(A.n_kv) + split] = sv;
     }
 }
 
@@ -355,7 +356,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
     const int t0 = split * PV_CHUNK;
     const int nt = min(PV_CHUNK, A.n_kv - t0);
-    const int n_rows = A.n_q * G;
+    const int q0 = blockIdx.z * ATT_MAX_Q;            // this workgroup's queries: q0 .. q0 + n_q - 1
+    const int n_rows = min(ATT_MAX_Q, A.n_q - q0) * G;
     const attn_scratch S = scratch_of(A);
 
     // the V chunk's loads go out first; p is formed while they are in flight
@@ -375,7 +377,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     const int nseg = attn_segs(A.n_kv);
     if ((int) threadIdx.x < n_rows) {
         const int pr = threadIdx.x;
-        const int64_t row = (int64_t) (pr / G) * A.n_head + kvh * G + pr % G;
+        const int64_t row = (int64_t) (q0 + pr / G) * A.n_head + kvh * G + pr % G;
         double tot = 0.0;
         for (int k = 0; k < nseg; k++) tot += S.ssum[row * nseg + k];
         s_M[pr] = S.rmax[row];
@@ -384,7 +386,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     __syncthreads();
     for (int i = threadIdx.x; i < n_rows * PV_CHUNK; i += ATT_THREADS) {
         const int pr = i / PV_CHUNK, t = i % PV_CHUNK;
-        const int64_t row = (int64_t) (pr / G) * A.n_head + kvh * G + pr % G;
+        const int64_t row = (int64_t) (q0 + pr / G) * A.n_head + kvh * G + pr % G;
         float p = 0.0f;
         if (t < nt) {
             const float M = s_M[pr], inv = s_inv[pr];
@@ -403,7 +405,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     __syncthreads();
 
     for (int pr = wave; pr < n_rows; pr += ATT_WAVES) {
-        const int q = pr / G, h = kvh * G + pr % G;
+        const int q = q0 + pr / G, h = kvh * G + pr % G;
         if (lane < HD2) {
             // two independent chains per dimension (even and odd positions; exact sums as above;
             // p is 0 past nt)
@@ -465,10 +467,11 @@ template <int HD, int G>
 static void launch_attn_t(const attn_launch & A, hipStream_t st) {
     const int splits = (A.n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
     const int pv_splits = (A.n_kv + PV_CHUNK - 1) / PV_CHUNK;
-    launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head_kv), dim3(ATT_THREADS),
-           scores_dyn_floats<HD, G>(A.n_q) * sizeof(float), st, A);
+    const int qz = (A.n_q + ATT_MAX_Q - 1) / ATT_MAX_Q;   // groups of up to ATT_MAX_Q queries
+    launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head_kv, qz), dim3(ATT_THREADS),
+           scores_dyn_floats<HD, G>(std::min(A.n_q, ATT_MAX_Q)) * sizeof(float), st, A);
     launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
-    launch((attn_pv_kernel<HD, G>), dim3(pv_splits, A.n_head_kv), dim3(ATT_THREADS), 0, st, A);
+    launch((attn_pv_kernel<HD, G>), dim3(pv_splits, A.n_head_kv, qz), dim3(ATT_THREADS), 0, st, A);
     launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(HD), 0, st, A, pv_splits);
 }
 
@@ -489,7 +492,8 @@ static void launch_attn_hd(const attn_launch & A, hipStream_t st) {
 }
 
 void launch_attn_decode(const attn_launch & A, hipStream_t st) {
-    if (A.n_q < 1 || A.n_q > ATT_MAX_Q) HIP_ABORT("attn: n_q %d out of range", A.n_q);
+    if (A.n_q < 1 || A.n_q > ATT_DECODE_MAX_Q) HIP_ABORT("attn: n_q %d out of range", A.n_q);
+    if (A.rope && A.n_q > ATT_MAX_Q) HIP_ABORT("attn: RoPE folded in for at most %d queries", ATT_MAX_Q);
     if (A.n_head % A.n_head_kv) HIP_ABORT("attn: n_head %% n_head_kv");
     if (A.scratch_bytes < attn_scratch_bytes(A.n_kv, A.n_q, A.n_head, A.hd)) HIP_ABORT("attn: scratch too small");
     if (A.out_q.qs && (A.hd % 32)) HIP_ABORT("attn: quantized output needs hd %% 32 == 0");

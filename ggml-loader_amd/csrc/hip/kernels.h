@@ -297,6 +297,9 @@ struct attn_launch {
     qk_norm        qn, kn;
 };
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd);
+// split-KV decode attention for 1 <= n_q <= ATT_DECODE_MAX_Q queries (groups of 4 per workgroup;
+// RoPE folded in only for n_q <= 4)
+constexpr int ATT_DECODE_MAX_Q = 64;
 void launch_attn_decode(const attn_launch & A, hipStream_t st);
 // n_q > 4 (prefill): one workgroup per (16-query tile, head), a row's scores in LDS (no scratch, no
 // quantized output); n_kv up to attn_prefill_max_kv(hd), 0 for an unsupported head dim
