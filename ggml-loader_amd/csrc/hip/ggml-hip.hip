@@ -781,6 +781,12 @@ private:
     // rows at that attention's last n_q positions: it runs inside the attention's scores kernel
     // (attn_launch.rope) instead of in a launch of its own.
     struct pending_rope { int anchor = -1; rope_job q, k, v; qk_norm qn, kn; };
+    // the (cos, sin) table of the graph's folded RoPE (written by the first attention that uses it)
+    float2 * cs_tab_ = nullptr;
+    const int32_t * cs_pos_ = nullptr;
+    const float * cs_ff_ = nullptr;
+    int cs_n_ = 0;
+    rope_params cs_p_{};
     pending_rope prope_;
 
     bool defer_rope(const rope_batch & B, const std::vector<int> & members) {
@@ -1483,6 +1489,21 @@ private:
             A.qn = prope_.qn;
             A.kn = prope_.kn;
             prope_.anchor = -1;
+            // one (cos, sin) table per graph for the rotations of the same positions and parameters
+            const size_t nbytes = (size_t) n_q * (A.rq.p.n_dims / 2) * sizeof(float2);
+            if (cs_tab_ && cs_pos_ == A.rq.pos && cs_ff_ == A.rq.ff && cs_n_ == n_q &&
+                memcmp(&cs_p_, &A.rq.p, sizeof(rope_params)) == 0) {
+                A.cs_tab = cs_tab_;
+                A.cs_mode = 2;
+            } else {
+                cs_tab_ = (float2 *) c_.scratch.alloc(nbytes);
+                cs_pos_ = A.rq.pos;
+                cs_ff_ = A.rq.ff;
+                cs_n_ = n_q;
+                cs_p_ = A.rq.p;
+                A.cs_tab = cs_tab_;
+                A.cs_mode = 1;
+            }
         }
         const double bytes = (double) n_kv * n_head_kv * hd * 2 * 2 + (double) n_head * hd * n_q * 8 +
                              (mask ? (double) n_kv * n_q * ggml_type_size(mask->type) : 0.0);

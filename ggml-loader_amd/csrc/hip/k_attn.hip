@@ -177,6 +177,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
     const int half = A.rope ? A.rq.p.n_dims / 2 : 1;
     const int tp = min(t, n_q * half - 1);          // this thread's rotation pair (clamped)
     const int32_t my_pos = posp[tp / half];
+    const bool cs_read = A.rope && A.cs_mode == 2;
+    const float2 cs_in = (cs_read ? A.cs_tab : (const float2 *) qb)[cs_read ? tp : 0];
     const bool mask32 = A.mask && !A.mask_f16;
     const float * mrow = (const float *) (mask32 ? A.mask : (const void *) qb);
     float mk[ATT_MAX_Q];
@@ -204,7 +206,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
 #pragma unroll
         for (int q = 0; q < ATT_MAX_Q; q++) s_mk[min(q, n_q - 1) * ATT_CHUNK + min(lane, nt - 1)] = mk[q];
         float c = 1.0f, sn = 0.0f;
-        if (A.rope) rope_pair_cs(A.rq.p, A.rq.ff, my_pos, tp % half, c, sn);
+        if (cs_read) {
+            c = cs_in.x;
+            sn = cs_in.y;
+        } else if (A.rope) {
+            rope_pair_cs(A.rq.p, A.rq.ff, my_pos, tp % half, c, sn);
+            if (A.cs_mode == 1 && blockIdx.x == 0 && blockIdx.y == 0 && t < n_q * half) A.cs_tab[tp] = make_float2(c, sn);
+        }
         s_cs[tp] = make_float2(c, sn);
     });
     __syncthreads();   // K chunk, source rows, weights, mask, (cos, sin) in LDS

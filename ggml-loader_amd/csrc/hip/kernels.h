@@ -295,6 +295,11 @@ struct attn_launch {
     // with rope: Q and K rows normalized before the rotation (Qwen3's QK-Norm), read from qn.x /
     // kn.x instead of rq.src / rk.src
     qk_norm        qn, kn;
+    // with rope: the (cos, sin) table of the new tokens' rotation pairs, [n_q][n_dims / 2]; every
+    // layer rotates with the same positions, so the first attention of a graph computes it and
+    // stores it here (cs_mode 1, workgroup 0), the later ones read it (cs_mode 2); 0: compute only
+    float2 *       cs_tab;
+    int            cs_mode;
 };
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd);
 // split-KV decode attention for 1 <= n_q <= ATT_DECODE_MAX_Q queries (groups of 4 per workgroup;
