@@ -571,6 +571,9 @@ private:
             case GGML_OP_SOFT_MAX:
                 if (fuse(FUSE_ROUTE) && op_moe_route(i)) return;
                 break;
+            case GGML_OP_UNARY:
+                if (fuse(FUSE_SWIGLU) && op_swiglu(i)) return;
+                break;
             default: break;
         }
         wrote_.push_back(n);
@@ -1245,6 +1248,34 @@ private:
             run(L);
         }
         for (int j : group) done_[j] = true;
+    }
+
+    // silu(gate) -> mul(., up) on f32 2-D views (the fused gate/up projection's halves, prefill)
+    // ==> one element-wise kernel, which also writes the Q8_0 activation its quantized consumers read
+    bool op_swiglu(int i) {
+        ggml_tensor * sn = g_->nodes[i];
+        if (sn->op_params[0] != GGML_UNARY_OP_SILU) return false;
+        const int mj = sole_user(i);
+        if (mj < 0) return false;
+        ggml_tensor * mn = g_->nodes[mj];
+        const ggml_tensor * gt = sn->src[0], * up = mn->src[1];
+        if (mn->op != GGML_OP_MUL || mn->src[0] != sn || !ggml_are_same_shape(gt, mn) || !ggml_are_same_shape(up, mn)) return false;
+        if (!ready(up)) return false;   // (separate gate and up projections: up may come after the silu)
+        for (const ggml_tensor * t : { gt, up, (const ggml_tensor *) mn }) {
+            if (t->type != GGML_TYPE_F32 || t->nb[0] != sizeof(float) || t->ne[2] != 1 || t->ne[3] != 1) return false;
+        }
+        const int64_t K = mn->ne[0], ncols = mn->ne[1];
+        const bool q = wanted_act_kind(mj) == 1 && K % 32 == 0 && is_2d_contig(mn);
+        act_entry e{};
+        if (q) e = alloc_act(1, K, ncols);
+        {
+            prof_scope ps(this, "swiglu", (double) (K * ncols * 12));
+            launch_swiglu(tv(gt), tv(up), tv(mn), q ? &e.q8 : nullptr, st_);
+        }
+        if (q) act_[mn] = e;
+        done_[mj] = true;
+        wrote_.push_back(mn);
+        return true;
     }
 
     // The routing of build_moe_ffn (reference qwen_model.c:551-606 semantics):

@@ -264,6 +264,43 @@ __global__ void unary_kernel(int op, float s, tview a, tview d, int64_t n) {
     st(at(d, k.i0, k.i1, k.i2, k.i3), d.type, y);
 }
 
+// act = silu(gate) * up over 2-D f32 views (the silu and mul ops' roundings), and optionally its
+// Q8_0 quantization (quantize_q8_kernel's arithmetic): one thread per element, a Q8_0 block per
+// 32 lanes, 8 blocks per workgroup, grid.y over the columns
+__global__ __launch_bounds__(256) void swiglu_kernel(tview g, tview u, tview d, q8_act q) {
+    const int64_t K = d.ne[0], nblk = K / 32, c = blockIdx.y;
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    const bool ok = i < K;
+    float v = 0.0f;
+    if (ok) {
+        const float x = *(const float *) at(g, i, c, 0, 0);
+        const float y = x / (1.0f + exp_cr(-x));
+        v = y * *(const float *) at(u, i, c, 0, 0);
+        *(float *) at(d, i, c, 0, 0) = v;
+    }
+    if (!q.qs) return;
+    // Q8_0 blocks of 32 consecutive elements (K % 32 == 0: a block never straddles the end)
+    const float amax = group_max<32>(fabsf(v));
+    const float dd = amax / 127;
+    const float id = dd ? 1.0f / dd : 0.0f;
+    const int qv = (int) roundf(v * id);
+    const float qsum = group_sum<32>((float) qv);
+    if (ok) {
+        q.qs[c * K + i] = (int8_t) qv;
+        if ((i % 32) == 0) {
+            q.d[c * nblk + i / 32] = __half2float(__float2half_rn(dd));
+            q.s[c * nblk + i / 32] = (int32_t) qsum;
+        }
+    }
+}
+
+void launch_swiglu(const tview & gate, const tview & up, const tview & dst, const q8_act * q, hipStream_t st) {
+    if (dst.ne[2] != 1 || dst.ne[3] != 1 || (q && dst.ne[0] % 32)) HIP_ABORT("swiglu: unsupported shape");
+    const q8_act none{};
+    launch(swiglu_kernel, dim3((unsigned) ((dst.ne[0] + 255) / 256), (unsigned) dst.ne[1]), dim3(256), 0, st, gate, up, dst,
+           q ? *q : none);
+}
+
 void launch_unary(int op, float s, const tview & a, const tview & dst, hipStream_t st) {
     const int64_t n = nelem(dst);
     if (n == 0) return;

@@ -555,6 +555,28 @@ def test_attention_long_context_query_groups(hip, cpu, hd, n_head, n_head_kv, n_
         assert np.array_equal(a, b), rel_err(a, b)
 
 
+@pytest.mark.parametrize("qtype,ncols", [(gl.Q8_0, 1), (gl.Q8_0, 77), (gl.Q4_0, 100), (gl.Q4_K, 5)])
+def test_swiglu_fused_halves(hip, cpu, qtype, ncols):
+    """The fused gate/up projection's halves (phi3, model.cpp:1119-1121): silu(gate) * up as one
+    kernel that also writes the down projection's Q8_0 input; the same floats as the op chain."""
+    E, F = 256, 512
+    x = rng(80 + ncols).standard_normal((ncols, E)).astype(np.float32)
+    wgu = qweight(qtype, E, 2 * F, 81, std=0.05)
+    wd = qweight(qtype, F, E, 82, std=0.05)
+
+    def build(g):
+        gu = g.mul_mat(g.tensor(qtype, E, 2 * F, data=wgu), g.tensor(gl.F32, E, ncols, data=x))
+        nb1 = 2 * F * 4
+        gate, up = g.view_2d(gu, F, ncols, nb1, 0), g.view_2d(gu, F, ncols, nb1, F * 4)
+        act = g.mul(g.silu(gate), up)
+        return [act, g.mul_mat(g.tensor(qtype, F, E, data=wd), act)]
+
+    (a_act, a_out), names = profiled(hip, lambda: run_on(hip, build))
+    b_act, b_out = run_on(cpu, build)
+    assert "swiglu" in names, names
+    assert np.array_equal(a_act, b_act) and np.array_equal(a_out, b_out), (rel_err(a_act, b_act), rel_err(a_out, b_out))
+
+
 def f16_tie_scores(n_kv, seed):
     """Scores (F16, one head, scale 1/8) whose softmax holds a probability p = e * (1/S) that is an
     exact F16 rounding tie as a float, while the exact product e * (1/S) lies on the side whose
