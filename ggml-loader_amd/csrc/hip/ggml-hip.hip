@@ -954,20 +954,29 @@ private:
         ggml_tensor * n = g_->nodes[i];
         const ggml_tensor * w = n->src[0];
         const ggml_tensor * x = n->src[1];
-        const act_entry * xa = ensure_act(x, 1);
+        const int kind = dot_kind(w->type);
+        const act_entry * xa = ensure_act(x, kind);
         gemm_launch G{};
         G.type = w->type;
         G.K = w->ne[0];
         G.n_rows = w->ne[1];
         G.ncols = x->ne[1];
-        const planes p = planes_of(w);
-        G.w = p.qs + p.first_block * qs_bytes_of(w->type);
-        G.wd = p.d + p.first_block;
-        G.xq = xa->q8.qs;
-        G.xd = xa->q8.d;
+        if (kind == 2) {
+            G.w = (const uint8_t *) w->data;
+            G.xq = xa->q8k.qs;
+            G.xd = xa->q8k.d;
+            G.xbs = xa->q8k.bsums;
+        } else {
+            const planes p = planes_of(w);
+            G.w = p.qs + p.first_block * qs_bytes_of(w->type);
+            G.wd = p.d + p.first_block;
+            G.xq = xa->q8.qs;
+            G.xd = xa->q8.d;
+        }
         G.y = (float *) n->data;
         G.y_stride = (int64_t) (n->nb[1] / sizeof(float));
-        double bytes = (double) ggml_nbytes(w) + (double) (G.K * G.ncols) * (1.0 + 4.0 / 32) + (double) (G.n_rows * G.ncols * 4);
+        const double act_bytes = kind == 2 ? 1.0 + 4.0 / 256 + 2.0 / 16 : 1.0 + 4.0 / 32;
+        double bytes = (double) ggml_nbytes(w) + (double) (G.K * G.ncols) * act_bytes + (double) (G.n_rows * G.ncols * 4);
         ggml_tensor * written = n;
         const int u = fuse(FUSE_ADD) ? sole_user(i) : -1;
         if (u >= 0) {
@@ -986,7 +995,7 @@ private:
             }
         }
         {
-            prof_scope ps(this, w->type == GGML_TYPE_Q4_0 ? "gemm_q4_0" : "gemm_q8_0", bytes);
+            prof_scope ps(this, w->type == GGML_TYPE_Q4_0 ? "gemm_q4_0" : w->type == GGML_TYPE_Q4_K ? "gemm_q4_K" : "gemm_q8_0", bytes);
             launch_gemm(G, st_);
         }
         wrote_.push_back(written);

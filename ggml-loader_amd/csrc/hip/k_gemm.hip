@@ -19,7 +19,10 @@
 // activation column l%16, k-slice 8(l/16)..8(l/16)+7 of the block (one 16-byte LDS read each), and
 // receives the results of rows 4(l/16)..4(l/16)+3 of column l%16. Workgroups are numbered so that
 // the column tiles of one row tile run on one XCD and share its L2.
+//
+// Q4_K weights run on gemm_q4k_kernel (below) against Q8_K activation columns.
 #include "kernels.h"
+#include "gemv_ops.h"
 
 #include "ggml.h"
 
@@ -232,6 +235,260 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const gemm_launch G) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Q4_K x Q8_K. ggml-cpu's generic q4_K x q8_K dot (ggml-cpu/arch-fallback: the oracle's
+// oracle_vec_dot_q4_K_q8_K) keeps eight float accumulators per output, one per element index mod 8:
+// for every 256-element super-block, aux32[l] = sum over the 32 elements e = 8k + l of
+// sc[e / 32] * q4[e] * q8[e] (an exact integer), sums[l] += (d_w * d_x) * aux32[l]; the mins act as
+// sumf -= (dmin_w * d_x) * sum_j bsums[j] * m[j / 2]; the output is sumf + sums[0] + ... + sums[7].
+// Staged in LDS as f16 in the order p = 32 l + k, each l-slice of a super-block is one contiguous
+// 32-element run, so one v_mfma_f32_16x16x32_f16 per slice yields aux32[l] for a 16 x 16 tile: the
+// weight operand is sc * q4 (at most 63 * 15 = 945, exact in f16) and every product and partial
+// sum is an integer below 2^24. The mins term is one v_mfma_f32_16x16x16_f16 of the mins (each
+// repeated for its two 16-element halves) against the 16 bsums (|bsum| <= 16 * 127, exact in f16).
+// Per output the kernel holds the 9 accumulators in registers and adds them in ggml's order, so
+// every output is the GEMV's and the CPU reference's float. A stage is one super-block of the
+// workgroup's rows and columns; the next stage's global loads are in flight while the current one
+// is reduced.
+
+// 4 nibbles (0..15 in the byte lanes of n) -> 4 f16 of value nibble * sc, exact
+__device__ __forceinline__ void u4x4_scaled(uint32_t n, __half2 sc, uint32_t & lo, uint32_t & hi) {
+    lo = __builtin_amdgcn_perm(0x64646464u, n, 0x04010400u);
+    hi = __builtin_amdgcn_perm(0x64646464u, n, 0x04030402u);
+    const __half2 bias = __halves2half2(__ushort_as_half(0xE400), __ushort_as_half(0xE400));   // -1024
+    lo = __builtin_bit_cast(uint32_t, __hmul2(__hadd2(__builtin_bit_cast(__half2, lo), bias), sc));
+    hi = __builtin_bit_cast(uint32_t, __hmul2(__hadd2(__builtin_bit_cast(__half2, hi), bias), sc));
+}
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+template <int WTM, int WTN>
+struct gemm_k_cfg {
+    static constexpr int BM = 32 * WTM, BN = 32 * WTN;
+    static constexpr int ROW = 256 + 8;                                    // f16 per LDS row (16-byte pad)
+    static constexpr int UA = (BM * 4 + 255) / 256, UB = (BN * 4 + 255) / 256;   // (row | column, sub-block pair) units per thread
+    static constexpr size_t LDS = (size_t) (BM + BN) * ROW * 2 + (size_t) (BM + BN) * 16 * 2 + (size_t) (2 * BM + BN) * 4;
+};
+
+template <int WTM, int WTN>
+__global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const gemm_launch G) {
+    using C = gemm_k_cfg<WTM, WTN>;
+    constexpr int BM = C::BM, BN = C::BN, ROW = C::ROW;
+    extern __shared__ __align__(16) uint8_t g_lds[];
+    _Float16 * sA = (_Float16 *) g_lds;            // [BM][ROW]: sc * q4 of the super-block, slice-major
+    _Float16 * sB = sA + BM * ROW;                 // [BN][ROW]: q8, same order
+    _Float16 * sM = sB + BN * ROW;                 // [BM][16]: the min of 16-element group j (m[j / 2])
+    _Float16 * sS = sM + BM * 16;                  // [BN][16]: bsums
+    float * sdw = (float *) (sS + BN * 16);        // [BM] d
+    float * sdm = sdw + BM;                        // [BM] dmin
+    float * sdx = sdm + BM;                        // [BN] activation d
+
+    const int64_t M = G.n_rows, N = G.ncols, K = G.K, nsb = K / 256;
+    const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
+    const int q = lane / 16, c = lane % 16;
+
+    const int64_t n_ct = (N + BN - 1) / BN, tiles = ((M + BM - 1) / BM) * n_ct;
+    int64_t t = blockIdx.x;
+    if (tiles % 8 == 0) t = (int64_t) (blockIdx.x % 8) * (tiles / 8) + blockIdx.x / 8;
+    const int64_t m0 = (t / n_ct) * BM, n0 = (t % n_ct) * BN;
+    const int wr = (wave / 2) * 16 * WTM, wc = (wave % 2) * 16 * WTN;
+
+    // staging units u = (row or column u / 4, sub-block pair u % 4); rows / columns past the end
+    // repeat the last one
+    uint4 rh[C::UA], rq[C::UA][2], rx[C::UB][4];
+    uint2 rs[C::UB];
+    float rd[C::UB];
+    auto load = [&](int64_t sb) {
+#pragma unroll
+        for (int k = 0; k < C::UA; k++) {
+            const int u = tid + 256 * k;
+            if (u < BM * 4) {
+                const int64_t row = min(m0 + u / 4, M - 1);
+                const uint4 * p = (const uint4 *) (G.w + (row * nsb + sb) * 144);
+                rh[k] = p[0];
+                rq[k][0] = p[1 + 2 * (u % 4)];
+                rq[k][1] = p[2 + 2 * (u % 4)];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < C::UB; k++) {
+            const int u = tid + 256 * k;
+            if (u < BN * 4) {
+                const int64_t col = min(n0 + u / 4, N - 1);
+                const uint4 * p = (const uint4 *) (G.xq + col * K + sb * 256 + 64 * (u % 4));
+#pragma unroll
+                for (int v = 0; v < 4; v++) rx[k][v] = p[v];
+                rs[k] = *(const uint2 *) (G.xbs + col * (K / 16) + sb * 16 + 4 * (u % 4));
+                rd[k] = G.xd[col * nsb + sb];
+            }
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int k = 0; k < C::UA; k++) {
+            const int u = tid + 256 * k;
+            if (u < BM * 4) {
+                const int r = u / 4, p = u % 4;
+                int sca, ma, scb, mb;
+                q4k_sc_m(rh[k].y, rh[k].z, rh[k].w, 2 * p, sca, ma);
+                q4k_sc_m(rh[k].y, rh[k].z, rh[k].w, 2 * p + 1, scb, mb);
+                uint32_t w[8] = { rq[k][0].x, rq[k][0].y, rq[k][0].z, rq[k][0].w, rq[k][1].x, rq[k][1].y, rq[k][1].z, rq[k][1].w };
+                q4k_group_by_l(w);      // dword l: the pair's bytes l, l+8, l+16, l+24
+                const __half2 ha = __float2half2_rn((float) sca), hb = __float2half2_rn((float) scb);
+#pragma unroll
+                for (int l = 0; l < 8; l++) {
+                    // k = 8p + 0..3: sub-block 2p (low nibbles); k = 8p + 4..7: sub-block 2p + 1
+                    uint32_t l0, h0, l1, h1;
+                    u4x4_scaled(w[l] & 0x0F0F0F0Fu, ha, l0, h0);
+                    u4x4_scaled((w[l] >> 4) & 0x0F0F0F0Fu, hb, l1, h1);
+                    *(uint4 *) (sA + r * ROW + l * 32 + 8 * p) = make_uint4(l0, h0, l1, h1);
+                }
+                const __half2 mma = __float2half2_rn((float) ma), mmb = __float2half2_rn((float) mb);
+                *(uint2 *) (sM + r * 16 + 4 * p) = make_uint2(__builtin_bit_cast(uint32_t, mma), __builtin_bit_cast(uint32_t, mmb));
+                if (p == 0) {
+                    sdw[r] = __half2float(__ushort_as_half((unsigned short) (rh[k].x & 0xffff)));
+                    sdm[r] = __half2float(__ushort_as_half((unsigned short) (rh[k].x >> 16)));
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < C::UB; k++) {
+            const int u = tid + 256 * k;
+            if (u < BN * 4) {
+                const int cc = u / 4, p = u % 4;
+                const uint32_t v[16] = { rx[k][0].x, rx[k][0].y, rx[k][0].z, rx[k][0].w, rx[k][1].x, rx[k][1].y, rx[k][1].z, rx[k][1].w,
+                                         rx[k][2].x, rx[k][2].y, rx[k][2].z, rx[k][2].w, rx[k][3].x, rx[k][3].y, rx[k][3].z, rx[k][3].w };
+                // element l + 8 t of the pair's 64 sits in dword 2 t + l / 4, byte l % 4
+                uint32_t ta[4], tb[4], tc[4], td[4];
+                transpose4(v[0], v[2], v[4], v[6], ta);       // l = 0..3, t = 0..3
+                transpose4(v[8], v[10], v[12], v[14], tb);    // l = 0..3, t = 4..7
+                transpose4(v[1], v[3], v[5], v[7], tc);       // l = 4..7, t = 0..3
+                transpose4(v[9], v[11], v[13], v[15], td);    // l = 4..7, t = 4..7
+#pragma unroll
+                for (int l = 0; l < 8; l++) {
+                    uint32_t a0, a1, b0, b1;
+                    i8x4_to_f16(l < 4 ? ta[l] : tc[l - 4], a0, a1);
+                    i8x4_to_f16(l < 4 ? tb[l] : td[l - 4], b0, b1);
+                    *(uint4 *) (sB + cc * ROW + l * 32 + 8 * p) = make_uint4(a0, a1, b0, b1);
+                }
+                const __half2 s01 = __halves2half2(__short2half_rn((short) (rs[k].x & 0xffff)), __short2half_rn((short) (rs[k].x >> 16)));
+                const __half2 s23 = __halves2half2(__short2half_rn((short) (rs[k].y & 0xffff)), __short2half_rn((short) (rs[k].y >> 16)));
+                *(uint2 *) (sS + cc * 16 + 4 * p) = make_uint2(__builtin_bit_cast(uint32_t, s01), __builtin_bit_cast(uint32_t, s23));
+                if (p == 0) sdx[cc] = rd[k];
+            }
+        }
+    };
+
+    float sums[WTM][WTN][8][4], mins[WTM][WTN][4];
+#pragma unroll
+    for (int i = 0; i < WTM; i++)
+#pragma unroll
+        for (int j = 0; j < WTN; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                mins[i][j][r] = 0.0f;
+#pragma unroll
+                for (int l = 0; l < 8; l++) sums[i][j][l][r] = 0.0f;
+            }
+
+    load(0);
+    for (int64_t sb = 0; sb < nsb; sb++) {
+        store();
+        __syncthreads();
+        if (sb + 1 < nsb) load(sb + 1);
+
+        float dd[WTM][WTN][4];
+        {
+            f32x4 dw[WTM], dm[WTM];
+            float dx[WTN];
+#pragma unroll
+            for (int i = 0; i < WTM; i++) {
+                dw[i] = *(const f32x4 *) (sdw + wr + 16 * i + 4 * q);
+                dm[i] = *(const f32x4 *) (sdm + wr + 16 * i + 4 * q);
+            }
+            f16x4 am[WTM], bm[WTN];
+#pragma unroll
+            for (int i = 0; i < WTM; i++) am[i] = *(const f16x4 *) (sM + (wr + 16 * i + c) * 16 + 4 * q);
+#pragma unroll
+            for (int j = 0; j < WTN; j++) {
+                dx[j] = sdx[wc + 16 * j + c];
+                bm[j] = *(const f16x4 *) (sS + (wc + 16 * j + c) * 16 + 4 * q);
+            }
+#pragma unroll
+            for (int i = 0; i < WTM; i++)
+#pragma unroll
+                for (int j = 0; j < WTN; j++) {
+                    const f32x4 mv = __builtin_amdgcn_mfma_f32_16x16x16f16(am[i], bm[j], f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        dd[i][j][r] = dw[i][r] * dx[j];
+                        const float dmin = dm[i][r] * dx[j];
+                        mins[i][j][r] = mins[i][j][r] - dmin * mv[r];
+                    }
+                }
+        }
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            f16x8 a[WTM], b[WTN];
+#pragma unroll
+            for (int i = 0; i < WTM; i++) a[i] = *(const f16x8 *) (sA + (wr + 16 * i + c) * ROW + l * 32 + 8 * q);
+#pragma unroll
+            for (int j = 0; j < WTN; j++) b[j] = *(const f16x8 *) (sB + (wc + 16 * j + c) * ROW + l * 32 + 8 * q);
+#pragma unroll
+            for (int i = 0; i < WTM; i++)
+#pragma unroll
+                for (int j = 0; j < WTN; j++) {
+                    const f32x4 sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) sums[i][j][l][r] = sums[i][j][l][r] + dd[i][j][r] * sv[r];
+                }
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int j = 0; j < WTN; j++) {
+        const int64_t col = n0 + wc + 16 * j + c;
+        if (col >= N) continue;
+#pragma unroll
+        for (int i = 0; i < WTM; i++) {
+            const int64_t r0 = m0 + wr + 16 * i + 4 * q;
+            if (r0 >= M) continue;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float acc = mins[i][j][r];
+#pragma unroll
+                for (int l = 0; l < 8; l++) acc = acc + sums[i][j][l][r];
+                v[r] = acc;
+            }
+            if (G.add) {
+                const float * ap = G.add + col * G.add_stride + r0;
+                for (int r = 0; r < 4; r++) if (r0 + r < M) v[r] = v[r] + ap[r];
+            }
+            float * yp = G.y + col * G.y_stride + r0;
+            if (r0 + 3 < M) {
+                *(float4 *) yp = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+                for (int r = 0; r < 4; r++) if (r0 + r < M) yp[r] = v[r];
+            }
+        }
+    }
+}
+
+template <int WTM, int WTN>
+void launch_gemm_q4k_t(const gemm_launch & G, hipStream_t st) {
+    using C = gemm_k_cfg<WTM, WTN>;
+    static bool attr = false;
+    if (!attr && C::LDS > 65536) {
+        HIP_CHECK(hipFuncSetAttribute((const void *) gemm_q4k_kernel<WTM, WTN>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int) C::LDS));
+    }
+    attr = true;
+    const int64_t tiles = ((G.n_rows + C::BM - 1) / C::BM) * ((G.ncols + C::BN - 1) / C::BN);
+    launch(gemm_q4k_kernel<WTM, WTN>, dim3((unsigned) tiles), dim3(256), C::LDS, st, G);
+}
+
 template <int TYPE, int WTM, int WTN, int KB>
 void launch_gemm_t(const gemm_launch & G, hipStream_t st) {
     using C = gemm_cfg<TYPE, WTM, WTN, KB>;
@@ -258,6 +515,7 @@ void launch_gemm_type(const gemm_launch & G, hipStream_t st) {
 } // namespace
 
 bool gemm_supported(int type, int64_t K, int64_t n_rows) {
+    if (type == GGML_TYPE_Q4_K) return K > 0 && K % 256 == 0 && n_rows > 0;
     return (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0) && K > 0 && K % 128 == 0 && n_rows > 0;
 }
 
@@ -269,6 +527,13 @@ void launch_gemm(const gemm_launch & G, hipStream_t st) {
     const uintptr_t align = (uintptr_t) G.y | (uintptr_t) G.add | (uintptr_t) G.w | (uintptr_t) G.xq;
     if (align % 16 || G.y_stride % 4 || (G.add && G.add_stride % 4)) {
         HIP_ABORT("gemm: operands must be 16-byte aligned with strides of whole float4s");
+    }
+    if (G.type == GGML_TYPE_Q4_K) {
+        if (!G.xbs || ((uintptr_t) G.xbs % 8) || ((uintptr_t) G.xd % 4)) HIP_ABORT("gemm: Q4_K needs Q8_K columns with 8-byte aligned bsums");
+        // 64 x 64 tiles where they still give every CU two workgroups, else 32 x 64
+        if (n_tiles(G, 64, 64) >= 512) launch_gemm_q4k_t<2, 2>(G, st);
+        else launch_gemm_q4k_t<1, 2>(G, st);
+        return;
     }
     if (G.type == GGML_TYPE_Q4_0) launch_gemm_type<GGML_TYPE_Q4_0>(G, st);
     else launch_gemm_type<GGML_TYPE_Q8_0>(G, st);

@@ -74,19 +74,21 @@ struct gemv_mat {
 };
 
 // ---------------------------------------------------------------------------------------------
-// prefill GEMM on the int8 matrix cores: y[c][r] = W[r] . x[c] (+ add[c][r]) for Q4_0 / Q8_0
-// weights in the plane layout and Q8_0-quantized activation columns; the same floats as the GEMV.
+// prefill GEMM on the matrix cores: y[c][r] = W[r] . x[c] (+ add[c][r]) for Q4_0 / Q8_0 weights
+// in the plane layout with Q8_0-quantized activation columns, or Q4_K weights (ggml blocks) with
+// Q8_K-quantized columns; the same floats as the GEMV.
 constexpr int GEMM_MIN_COLS = 64;   // narrower products stay on the GEMV
 
 struct gemm_launch {
-    int             type;      // GGML_TYPE_Q4_0 / Q8_0
-    int64_t         K;         // row length (a multiple of 128)
+    int             type;      // GGML_TYPE_Q4_0 / Q8_0 / Q4_K
+    int64_t         K;         // row length (a multiple of 128; of 256 for Q4_K)
     int64_t         n_rows;
     int64_t         ncols;
-    const uint8_t * w;         // qs plane of row 0
-    const __half *  wd;        // d plane of row 0
+    const uint8_t * w;         // Q4_0 / Q8_0: qs plane of row 0; Q4_K: row 0's first block
+    const __half *  wd;        // Q4_0 / Q8_0: d plane of row 0
     const int8_t *  xq;        // activation column c at xq + c * K
-    const float *   xd;        // and its block scales at xd + c * K / 32
+    const float *   xd;        // and its scales at xd + c * K / 32 (Q8_0) or xd + c * K / 256 (Q8_K)
+    const int16_t * xbs;       // Q8_K: the column's 16-element sums at xbs + c * K / 16
     float *         y;         // output column c at y + c * y_stride
     int64_t         y_stride;
     const float *   add;       // optional residual, column c at add + c * add_stride

@@ -66,7 +66,7 @@ def test_decode_parity_tiny(models, arch, fusion):
             tok = int(np.argmax(lc))
 
 
-@pytest.mark.parametrize("arch", ["llama", "phi3", "qwen2"])
+@pytest.mark.parametrize("arch", ["llama", "phi3", "qwen2", "qwen3", "qwen3moe"])
 def test_prefill_parity_long_prompt(models, arch):
     """A 100-token prompt in one forward_step (the quantized projections run on the prefill GEMM,
     attention on the graph's own K^T Q -> softmax -> V chain), then decode steps on its KV cache."""

@@ -147,6 +147,9 @@ def profiled(hip, fn):
     (gl.Q4_0, 256, 100),     # rows end inside a 16-row tile
     (gl.Q8_0, 128, 4),       # one row group, one 4-block step
     (gl.Q8_0, 384, 36),
+    (gl.Q4_K, 2560, 1024),   # Qwen3-shape rows, 64 x 64 tiles
+    (gl.Q4_K, 4096, 72),     # 32 x 64 tiles, rows end inside a 16-row tile
+    (gl.Q4_K, 256, 100),     # one super-block per row
 ])
 @pytest.mark.parametrize("ncols", [64, 100, 512])
 def test_gemm_prefill(hip, cpu, qtype, K, N, ncols):
@@ -166,7 +169,7 @@ def test_gemm_prefill(hip, cpu, qtype, K, N, ncols):
     assert np.array_equal(a, b), rel_err(a, b)
 
 
-@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0])
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K])
 def test_gemm_norm_qkv_residual(hip, cpu, qtype):
     """rms_norm * w feeding three prefill-width GEMMs (normalized and quantized once), and a GEMM
     whose residual add is fused into its store."""
