@@ -401,6 +401,7 @@ private:
     std::unordered_map<const ggml_tensor *, act_entry> act_;
     std::unordered_map<const ggml_tensor *, gemv_norm> norm_;   // deferred rms_norm * w outputs
     std::unordered_map<int, attn_match> attn_;
+    std::unordered_map<int, int> silu_of_;    // mul node -> its held-back silu node (op_swiglu)
     std::vector<const ggml_tensor *> wrote_;
 
     bool fuse(int bit) const { return c_.fusion && (c_.fuse_mask & bit); }
@@ -567,6 +568,7 @@ private:
                 return;
             case GGML_OP_MUL:
                 if (fuse(FUSE_ADD) && op_moe_wsum(i)) return;
+                if (silu_of_.count(i)) { run_swiglu(silu_of_[i], i); return; }
                 break;
             case GGML_OP_SOFT_MAX:
                 if (fuse(FUSE_ROUTE) && op_moe_route(i)) return;
@@ -1259,8 +1261,13 @@ private:
         for (int j : group) done_[j] = true;
     }
 
-    // silu(gate) -> mul(., up) on f32 2-D views (the fused gate/up projection's halves, prefill)
-    // ==> one element-wise kernel, which also writes the Q8_0 activation its quantized consumers read
+    // silu(gate) -> mul(., up) on f32 2-D views (prefill: the fused gate/up projection's halves, or
+    // separate gate and up projections) ==> one element-wise kernel, which also writes the Q8_0 /
+    // Q8_K activation its quantized consumers read
+    static bool disjoint_or_same(const ggml_tensor * a, const ggml_tensor * b) {
+        const uint8_t * a0 = (const uint8_t *) a->data, * b0 = (const uint8_t *) b->data;
+        return a0 == b0 || a0 + ggml_nbytes(a) <= b0 || b0 + ggml_nbytes(b) <= a0;
+    }
     bool op_swiglu(int i) {
         ggml_tensor * sn = g_->nodes[i];
         if (sn->op_params[0] != GGML_UNARY_OP_SILU) return false;
@@ -1269,22 +1276,44 @@ private:
         ggml_tensor * mn = g_->nodes[mj];
         const ggml_tensor * gt = sn->src[0], * up = mn->src[1];
         if (mn->op != GGML_OP_MUL || mn->src[0] != sn || !ggml_are_same_shape(gt, mn) || !ggml_are_same_shape(up, mn)) return false;
-        if (!ready(up)) return false;   // (separate gate and up projections: up may come after the silu)
         for (const ggml_tensor * t : { gt, up, (const ggml_tensor *) mn }) {
             if (t->type != GGML_TYPE_F32 || t->nb[0] != sizeof(float) || t->ne[2] != 1 || t->ne[3] != 1) return false;
         }
+        // the kernel reads gate[i] and up[i] before writing out[i]: the output may sit exactly on
+        // either input, never across one (gate is not an input of the mul, so the allocator may
+        // have reused its memory for the output)
+        if (!disjoint_or_same(mn, gt) || !disjoint_or_same(mn, up)) return false;
+        if (!ready(up)) {
+            // separate projections: up comes after the silu. Hold the silu back (nothing launched)
+            // when the nodes before the mul are only the up projection on the prefill GEMM (no
+            // fused writes elsewhere) and views, and the projection does not write over the gate.
+            for (int k = i + 1; k < mj; k++) {
+                const ggml_tensor * t = g_->nodes[k];
+                if (done_[k] || is_view_op(t->op)) continue;
+                if (t != up || !gemm_route(t) || sole_user(k) != mj || !disjoint_or_same(t, gt) || t->data == gt->data) return false;
+            }
+            silu_of_[mj] = i;
+            return true;
+        }
+        run_swiglu(i, mj);
+        return true;
+    }
+    void run_swiglu(int i, int mj) {
+        const ggml_tensor * gt = g_->nodes[i]->src[0];
+        ggml_tensor * mn = g_->nodes[mj];
+        const ggml_tensor * up = mn->src[1];
         const int64_t K = mn->ne[0], ncols = mn->ne[1];
-        const bool q = wanted_act_kind(mj) == 1 && K % 32 == 0 && is_2d_contig(mn);
+        const int want = is_2d_contig(mn) ? wanted_act_kind(mj) : 0;
+        const int kind = (want == 1 && K % 32 == 0) || (want == 2 && K % 256 == 0) ? want : 0;
         act_entry e{};
-        if (q) e = alloc_act(1, K, ncols);
+        if (kind) e = alloc_act(kind, K, ncols);
         {
             prof_scope ps(this, "swiglu", (double) (K * ncols * 12));
-            launch_swiglu(tv(gt), tv(up), tv(mn), q ? &e.q8 : nullptr, st_);
+            launch_swiglu(tv(gt), tv(up), tv(mn), kind == 1 ? &e.q8 : nullptr, kind == 2 ? &e.q8k : nullptr, st_);
         }
-        if (q) act_[mn] = e;
+        if (kind) act_[mn] = e;
         done_[mj] = true;
         wrote_.push_back(mn);
-        return true;
     }
 
     // The routing of build_moe_ffn (reference qwen_model.c:551-606 semantics):

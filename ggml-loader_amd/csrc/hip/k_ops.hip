@@ -18,6 +18,47 @@ static unsigned grid1(int64_t n, int threads) { return (unsigned) ((n + threads 
 // ---------------------------------------------------------------------------------------------
 // RMSNorm (+ weight multiply, + activation quantization)
 
+// Q8_K quantization (ggml quantize_row_q8_K_ref) of one 256-element super-block held one value per
+// thread of a 256-thread block: the value of largest magnitude (lowest index on ties) sets
+// iscale = -127 / max, q = min(127, round-half-even(iscale * o)), d = 1 / iscale (0 for an all-zero
+// block), bsums = sums of 16 consecutive q. qs, d and bsums point at the super-block's entries.
+// Every thread of the block must call it (it synchronizes the block).
+__device__ void q8k_superblock(float o, int t, int8_t * qs, float * d, int16_t * bsums) {
+    __shared__ float s_fx[4];
+    __shared__ int s_ix[4];
+    __shared__ float s_vx[4];
+    float ax = fabsf(o);
+    int idx = t;
+    float val = o;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ax2 = __shfl_xor(ax, off, WAVE);
+        const int idx2 = __shfl_xor(idx, off, WAVE);
+        const float val2 = __shfl_xor(val, off, WAVE);
+        if (ax2 > ax || (ax2 == ax && idx2 < idx)) { ax = ax2; idx = idx2; val = val2; }
+    }
+    __syncthreads();
+    if ((t % 64) == 0) { s_fx[t / 64] = ax; s_ix[t / 64] = idx; s_vx[t / 64] = val; }
+    __syncthreads();
+    float bax = s_fx[0], bval = s_vx[0];
+    int bidx = s_ix[0];
+    for (int wv = 1; wv < 4; wv++) {
+        if (s_fx[wv] > bax || (s_fx[wv] == bax && s_ix[wv] < bidx)) { bax = s_fx[wv]; bidx = s_ix[wv]; bval = s_vx[wv]; }
+    }
+    int q = 0;
+    if (bax != 0.0f) {
+        const float iscale = -127.f / bval;
+        q = round_half_even(iscale * o);
+        q = q < 127 ? q : 127;
+        if (t == 0) *d = 1 / iscale;
+    } else if (t == 0) {
+        *d = 0.0f;
+    }
+    qs[t] = (int8_t) q;
+    const float bs = group_sum<16>((float) q);
+    if ((t % 16) == 0) bsums[t / 16] = (int16_t) bs;
+}
+
 // One 256-thread block per row; each thread holds its EPT elements (i = it*256 + t) in registers,
 // so the row is read once with every load issued up front.
 template <int QUANT, int EPT> // QUANT: 0 none, 1 Q8_0 (32-blocks), 2 Q8_K (256-blocks)
@@ -25,9 +66,6 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float * __restrict_
         const float * __restrict__ w, float * __restrict__ y, int64_t y_stride, int64_t n, float eps,
         q8_act q8, q8k_act q8k) {
     __shared__ double s_part[4];
-    __shared__ float s_fx[4];
-    __shared__ int s_ix[4];
-    __shared__ float s_vx[4];
     const int64_t row = blockIdx.x;
     const float * xr = x + row * x_stride;
     float * yr = y + row * y_stride;
@@ -72,38 +110,9 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float * __restrict_
                 }
             }
         } else if (QUANT == 2) {
-            // one super-block of 256 per iteration; max magnitude with the lowest index on ties
-            float ax = fabsf(o);
-            int idx = t;
-            float val = o;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const float ax2 = __shfl_xor(ax, off, WAVE);
-                const int idx2 = __shfl_xor(idx, off, WAVE);
-                const float val2 = __shfl_xor(val, off, WAVE);
-                if (ax2 > ax || (ax2 == ax && idx2 < idx)) { ax = ax2; idx = idx2; val = val2; }
-            }
-            __syncthreads();
-            if ((t % 64) == 0) { s_fx[t / 64] = ax; s_ix[t / 64] = idx; s_vx[t / 64] = val; }
-            __syncthreads();
-            float bax = s_fx[0], bval = s_vx[0];
-            int bidx = s_ix[0];
-            for (int wv = 1; wv < 4; wv++) {
-                if (s_fx[wv] > bax || (s_fx[wv] == bax && s_ix[wv] < bidx)) { bax = s_fx[wv]; bidx = s_ix[wv]; bval = s_vx[wv]; }
-            }
-            int q = 0;
-            const int64_t sb = (int64_t) it;
-            if (bax != 0.0f) {
-                const float iscale = -127.f / bval;
-                q = round_half_even(iscale * o);
-                q = q < 127 ? q : 127;
-                if (t == 0) q8k.d[row * (n / 256) + sb] = 1 / iscale;
-            } else if (t == 0) {
-                q8k.d[row * (n / 256) + sb] = 0.0f;
-            }
-            q8k.qs[row * n + i] = (int8_t) q;
-            const float bs = group_sum<16>((float) q);
-            if ((t % 16) == 0) q8k.bsums[row * (n / 16) + i / 16] = (int16_t) bs;
+            // one super-block of 256 per iteration (n % 256 == 0)
+            q8k_superblock(o, t, q8k.qs + row * n + (int64_t) it * 256, q8k.d + row * (n / 256) + it,
+                           q8k.bsums + row * (n / 16) + (int64_t) it * 16);
         }
     }
 }
@@ -265,9 +274,10 @@ __global__ void unary_kernel(int op, float s, tview a, tview d, int64_t n) {
 }
 
 // act = silu(gate) * up over 2-D f32 views (the silu and mul ops' roundings), and optionally its
-// Q8_0 quantization (quantize_q8_kernel's arithmetic): one thread per element, a Q8_0 block per
-// 32 lanes, 8 blocks per workgroup, grid.y over the columns
-__global__ __launch_bounds__(256) void swiglu_kernel(tview g, tview u, tview d, q8_act q) {
+// Q8_0 quantization (quantize_q8_kernel's arithmetic: a block per 32 lanes) or its Q8_K
+// quantization (a workgroup's 256 elements are one super-block): one thread per element, grid.y
+// over the columns
+__global__ __launch_bounds__(256) void swiglu_kernel(tview g, tview u, tview d, q8_act q, q8k_act qk) {
     const int64_t K = d.ne[0], nblk = K / 32, c = blockIdx.y;
     const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
     const bool ok = i < K;
@@ -277,6 +287,12 @@ __global__ __launch_bounds__(256) void swiglu_kernel(tview g, tview u, tview d, 
         const float y = x / (1.0f + exp_cr(-x));
         v = y * *(const float *) at(u, i, c, 0, 0);
         *(float *) at(d, i, c, 0, 0) = v;
+    }
+    if (qk.qs) {
+        // K % 256 == 0: every thread holds an element
+        q8k_superblock(v, threadIdx.x, qk.qs + c * K + (int64_t) blockIdx.x * 256, qk.d + c * (K / 256) + blockIdx.x,
+                       qk.bsums + c * (K / 16) + (int64_t) blockIdx.x * 16);
+        return;
     }
     if (!q.qs) return;
     // Q8_0 blocks of 32 consecutive elements (K % 32 == 0: a block never straddles the end)
@@ -294,11 +310,14 @@ __global__ __launch_bounds__(256) void swiglu_kernel(tview g, tview u, tview d, 
     }
 }
 
-void launch_swiglu(const tview & gate, const tview & up, const tview & dst, const q8_act * q, hipStream_t st) {
-    if (dst.ne[2] != 1 || dst.ne[3] != 1 || (q && dst.ne[0] % 32)) HIP_ABORT("swiglu: unsupported shape");
+void launch_swiglu(const tview & gate, const tview & up, const tview & dst, const q8_act * q, const q8k_act * qk, hipStream_t st) {
+    if (dst.ne[2] != 1 || dst.ne[3] != 1 || (q && dst.ne[0] % 32) || (qk && dst.ne[0] % 256) || (q && qk)) {
+        HIP_ABORT("swiglu: unsupported shape");
+    }
     const q8_act none{};
+    const q8k_act nonek{};
     launch(swiglu_kernel, dim3((unsigned) ((dst.ne[0] + 255) / 256), (unsigned) dst.ne[1]), dim3(256), 0, st, gate, up, dst,
-           q ? *q : none);
+           q ? *q : none, qk ? *qk : nonek);
 }
 
 void launch_unary(int op, float s, const tview & a, const tview & dst, hipStream_t st) {

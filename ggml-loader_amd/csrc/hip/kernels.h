@@ -219,8 +219,8 @@ struct rope_batch {
 void launch_rope_batch(rope_batch & B, hipStream_t st);
 
 void launch_soft_max(const tview & a, const tview * mask, const tview & dst, float scale, float max_bias, hipStream_t st);
-// dst = silu(gate) * up (2-D f32 views), with its Q8_0 quantization into q when q is set
-void launch_swiglu(const tview & gate, const tview & up, const tview & dst, const q8_act * q, hipStream_t st);
+// dst = silu(gate) * up (2-D f32 views), with its Q8_0 (q) or Q8_K (qk) quantization when set
+void launch_swiglu(const tview & gate, const tview & up, const tview & dst, const q8_act * q, const q8k_act * qk, hipStream_t st);
 
 // ---------------------------------------------------------------------------------------------
 // MoE routing and expert combination

@@ -580,6 +580,28 @@ def test_swiglu_fused_halves(hip, cpu, qtype, ncols):
     assert np.array_equal(a_act, b_act) and np.array_equal(a_out, b_out), (rel_err(a_act, b_act), rel_err(a_out, b_out))
 
 
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K])
+def test_swiglu_separate_projections(hip, cpu, qtype):
+    """Separate gate and up projections at prefill width (llama/qwen FFN, model.cpp:1122-1126): the
+    silu comes before the up projection in node order; it is held back and runs with the mul as one
+    kernel writing the down projection's Q8_0 / Q8_K input. The same floats as the op chain."""
+    E, F, ncols = 256, 512, 96
+    x = rng(90).standard_normal((ncols, E)).astype(np.float32)
+    wg, wu = qweight(qtype, E, F, 91, std=0.05), qweight(qtype, E, F, 92, std=0.05)
+    wd = qweight(qtype, F, E, 93, std=0.05)
+
+    def build(g):
+        xt = g.tensor(gl.F32, E, ncols, data=x)
+        gate = g.silu(g.mul_mat(g.tensor(qtype, E, F, data=wg), xt))
+        act = g.mul(gate, g.mul_mat(g.tensor(qtype, E, F, data=wu), xt))
+        return [act, g.mul_mat(g.tensor(qtype, F, E, data=wd), act)]
+
+    (a_act, a_out), names = profiled(hip, lambda: run_on(hip, build))
+    b_act, b_out = run_on(cpu, build)
+    assert "swiglu" in names and "unary" not in names, names
+    assert np.array_equal(a_act, b_act) and np.array_equal(a_out, b_out), (rel_err(a_act, b_act), rel_err(a_out, b_out))
+
+
 def f16_tie_scores(n_kv, seed):
     """Scores (F16, one head, scale 1/8) whose softmax holds a probability p = e * (1/S) that is an
     exact F16 rounding tie as a float, while the exact product e * (1/S) lies on the side whose
