@@ -328,8 +328,10 @@ def gemv_bench(gl, args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    # a decode step is ~2 ms: 300 steps keep the timed region well above the run-to-run noise of a
+    # 0.2 s region (GPU clock ramp, host scheduling), and 50 warmup steps bring the clocks up first
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="llama3b")
     ap.add_argument("--n-past", type=int, default=None, help="KV positions before the step (default: per config)")
     ap.add_argument("--batch", type=int, default=1, help="new tokens per decode step")
@@ -400,20 +402,25 @@ def decode_bench(gl, args):
 
         steps(args.warmup)
 
-        # timed region: K steps. In every 10th step the dominant kernel's launches (and only those)
-        # carry HIP events stamped by their own dispatches on the backend's stream, so its launch
-        # durations come from these same steps; reading the events back costs host time after a
-        # timed step, which the sampling keeps to a tenth of the steps.
+        # timed region: K steps with no events in them. Once a launch carries dispatch-stamped HIP
+        # events, the runtime timestamps every later dispatch of the process too (measured: 1.97 ->
+        # 2.40 ms per Llama-3B step), so no event is used before this region ends.
+        secs = steps(args.steps)
+        value = args.steps * batch / secs
+        log(f"[bench] {args.steps} steps in {secs:.4f}s -> {value:.1f} tok/s ({1000 * secs / args.steps:.3f} ms/step)")
+
+        # the dominant kernel's launch durations: the same K steps again, where in every 10th step
+        # its launches (and only those) carry HIP events stamped by their own dispatches on the
+        # backend's stream (the events add time between kernels, not to them)
         hipl.ggml_backend_hip_set_profile_filter(s.backend, dominant.encode())
         hipl.ggml_backend_hip_set_profile_sampling(s.backend, PROFILE_EVERY)
         hipl.ggml_backend_hip_reset_profile(s.backend)
         hipl.ggml_backend_hip_set_profiling(s.backend, True)
-        secs = steps(args.steps)
+        secs_ev = steps(args.steps)
         hipl.ggml_backend_hip_set_profiling(s.backend, False)
         hipl.ggml_backend_hip_set_profile_sampling(s.backend, 1)
         timed = gl.profile(s.backend)
-        value = args.steps * batch / secs
-        log(f"[bench] {args.steps} steps in {secs:.4f}s -> {value:.1f} tok/s ({1000 * secs / args.steps:.3f} ms/step)")
+        log(f"[bench] kernel-timing pass: {args.steps} steps in {secs_ev:.4f}s ({1000 * secs_ev / args.steps:.3f} ms/step with events)")
 
         # untimed breakdown: every kernel bracketed
         hipl.ggml_backend_hip_set_profile_filter(s.backend, b"")
@@ -460,6 +467,9 @@ def decode_bench(gl, args):
         "bytes_per_launch": round(g_bytes / g_launch) if g_launch else None,
         "us_per_launch": round(g_ms / g_launch * 1e3, 3) if g_launch else None,
         "share_of_step": round((g_ms / timed_steps) / (secs * 1e3 / args.steps), 4),
+        "timing": f"HIP events stamped by the kernel's own dispatches on the backend's stream, in every "
+                  f"{PROFILE_EVERY}th of {args.steps} steps run again right after the timed region "
+                  f"({1000 * secs_ev / args.steps:.3f} ms/step with the events)",
     }
     if moe and batch > 1:
         roofline["bytes_note"] = ("mul_mat_id launches count the selected experts' bytes once per (token, slot) "

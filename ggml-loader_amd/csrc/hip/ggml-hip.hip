@@ -624,7 +624,18 @@ private:
                 return;
             }
             case GGML_OP_FLASH_ATTN_EXT: op_flash_attn(n); return;
-            case GGML_OP_ARGMAX: { prof_scope ps(this, "argmax", 0); launch_argmax(tv(n->src[0]), (int32_t *) n->data, st_); return; }
+            case GGML_OP_ARGMAX: {
+                prof_scope ps(this, "argmax", 0);
+                const tview a = tv(n->src[0]);
+                if (a.ne[1] == 1 && a.ne[0] >= ARGMAX_ROW_MIN) {
+                    float * pv = (float *) c_.scratch.alloc(ARGMAX_PARTS * sizeof(float));
+                    int * pi = (int *) c_.scratch.alloc(ARGMAX_PARTS * sizeof(int));
+                    launch_argmax_row(a, (int32_t *) n->data, pv, pi, st_);
+                } else {
+                    launch_argmax(a, (int32_t *) n->data, st_);
+                }
+                return;
+            }
             default:
                 HIP_ABORT("op %s is not supported by the hip backend (node '%s')", ggml_op_name(n->op), n->name);
         }

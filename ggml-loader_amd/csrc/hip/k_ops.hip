@@ -623,8 +623,57 @@ __global__ __launch_bounds__(256) void argmax_kernel(tview a, int32_t * out) {
     }
 }
 
+// One wide row (the logits of the greedy pick): ARGMAX_PARTS workgroups reduce consecutive chunks
+// to (value, first index), then one workgroup reduces the parts in order of their indices. The
+// comparisons are the one-pass rule's (strictly greater wins, so the first index of the maximum;
+// nothing above -inf: index 0).
+__device__ __forceinline__ void argmax_merge(float & bv, int & bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+__device__ void argmax_block(float & bv, int & bi) {
+    __shared__ float s_v[4];
+    __shared__ int s_i[4];
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) argmax_merge(bv, bi, __shfl_xor(bv, o, WAVE), __shfl_xor(bi, o, WAVE));
+    if ((t % 64) == 0) { s_v[t / 64] = bv; s_i[t / 64] = bi; }
+    __syncthreads();
+    bv = s_v[0];
+    bi = s_i[0];
+    for (int w = 1; w < 4; w++) argmax_merge(bv, bi, s_v[w], s_i[w]);
+}
+
+__global__ __launch_bounds__(256) void argmax_parts_kernel(tview a, int64_t chunk, float * pv, int * pi) {
+    const int64_t i0 = (int64_t) blockIdx.x * chunk, i1 = min(i0 + chunk, a.ne[0]);
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
+        const float v = *(const float *) at(a, i, 0, 0, 0);
+        if (v > bv) { bv = v; bi = (int) i; }
+    }
+    argmax_block(bv, bi);
+    if (threadIdx.x == 0) { pv[blockIdx.x] = bv; pi[blockIdx.x] = bi; }
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float * pv, const int * pi, int n_parts, int32_t * out) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    if ((int) threadIdx.x < n_parts) { bv = pv[threadIdx.x]; bi = pi[threadIdx.x]; }
+    argmax_block(bv, bi);
+    if (threadIdx.x == 0) out[0] = bi == 0x7fffffff ? 0 : bi;
+}
+
 void launch_argmax(const tview & a, int32_t * out, hipStream_t st) {
     launch(argmax_kernel, dim3((unsigned) a.ne[1]), dim3(256), 0, st, a, out);
+}
+
+void launch_argmax_row(const tview & a, int32_t * out, float * part_v, int * part_i, hipStream_t st) {
+    if (a.ne[1] != 1 || a.ne[2] != 1 || a.ne[3] != 1 || a.ne[0] <= 0 || a.ne[0] > INT32_MAX) HIP_ABORT("argmax_row: one row expected");
+    const int64_t chunk = (a.ne[0] + ARGMAX_PARTS - 1) / ARGMAX_PARTS;
+    const int parts = (int) ((a.ne[0] + chunk - 1) / chunk);
+    launch(argmax_parts_kernel, dim3((unsigned) parts), dim3(256), 0, st, a, chunk, part_v, part_i);
+    launch(argmax_final_kernel, dim3(1), dim3(256), 0, st, (const float *) part_v, (const int *) part_i, parts, out);
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -238,6 +238,11 @@ struct moe_wsum {
 };
 void launch_moe_wsum(const moe_wsum & M, hipStream_t st);
 void launch_argmax(const tview & a, int32_t * out, hipStream_t st);
+// one wide row in two launches over ARGMAX_PARTS partial results (part_v / part_i: that many
+// entries of device scratch); the same index as launch_argmax
+constexpr int ARGMAX_PARTS = 128;
+constexpr int64_t ARGMAX_ROW_MIN = 16384;   // narrower rows take the one-workgroup kernel
+void launch_argmax_row(const tview & a, int32_t * out, float * part_v, int * part_i, hipStream_t st);
 
 // generic F32/F16/BF16 mul_mat (src0 rows contiguous): one wave per output element
 void launch_mul_mat_generic(const tview & src0, const tview & src1, const tview & dst, hipStream_t st);

@@ -93,8 +93,7 @@ int gl_forward_step(gl_session * s, int64_t n_past, const int32_t * tokens, int6
             if (tokens[i] < 0 || tokens[i] >= s->n_vocab) throw gl_error("token id out of range");
         }
         std::vector<int32_t> toks(tokens, tokens + n_new);
-        std::vector<float> out = forward_step(s->m, s->hp, s->kv, s->ds, s->backend, n_past, toks, s->n_vocab);
-        if (logits) memcpy(logits, out.data(), out.size() * sizeof(float));
+        forward_step_into(s->m, s->hp, s->kv, s->ds, s->backend, n_past, toks, s->n_vocab, logits);
     } catch (const std::exception & e) {
         set_err(err, err_size, e.what());
         return 1;
@@ -107,12 +106,12 @@ int gl_decode_loop(gl_session * s, int64_t n_past, int32_t first_token, int n_st
     try {
         if (first_token < 0 || first_token >= s->n_vocab) throw gl_error("token id out of range");
         int32_t next = first_token;
-        // cmd_bench.cpp:52-61: time the n_tg loop of forward_step + argmax
+        // cmd_bench.cpp:52-61: time the n_tg loop of forward_step + argmax (the argmax of the last
+        // logits column runs on the backend, so a step reads back one index instead of n_vocab floats)
         auto t0 = std::chrono::steady_clock::now();
         for (int i = 0; i < n_steps; i++) {
             const int64_t pos = fixed_pos ? n_past : n_past + i;
-            std::vector<float> step_logits = forward_step(s->m, s->hp, s->kv, s->ds, s->backend, pos, { next }, s->n_vocab);
-            next = argmax(step_logits);
+            next = forward_step_greedy(s->m, s->hp, s->kv, s->ds, s->backend, pos, { next }, s->n_vocab);
             if (tokens_out) tokens_out[i] = next;
         }
         auto t1 = std::chrono::steady_clock::now();

@@ -468,10 +468,12 @@ void free_decode_session(decode_session & ds) {
     ds.galloc = nullptr;
 }
 
-// model.cpp:1496-1597
-std::vector<float> forward_step(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds,
-                                ggml_backend_t backend, int64_t n_past, const std::vector<int32_t> & new_tokens,
-                                int64_t n_vocab) {
+// model.cpp:1496-1597. logits_out (n_vocab floats, may be null) receives the last column's logits; with greedy_out
+// set instead, the graph ends in the argmax of that column (ggml_argmax: the first index of the
+// maximum, the pick of argmax() below) and only the index is read back.
+static void run_step(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds, ggml_backend_t backend,
+                     int64_t n_past, const std::vector<int32_t> & new_tokens, int64_t n_vocab, float * logits_out,
+                     int32_t * greedy_out) {
     const int64_t n_new = (int64_t) new_tokens.size();
     const int64_t n_kv  = n_past + n_new;
     if (n_new <= 0) throw gl_error("forward_step: no tokens");
@@ -481,6 +483,13 @@ std::vector<float> forward_step(const model & m, const hparams & hp, kv_cache & 
     struct ggml_context * gctx_build = ggml_init(gip);
 
     built_graph bg = build_graph(gctx_build, m, hp, kv, n_past, n_new, ds.use_flash_attn);
+    struct ggml_tensor * pick = nullptr;
+    if (greedy_out) {
+        struct ggml_tensor * last = ggml_view_1d(gctx_build, bg.logits, n_vocab, (size_t) (n_new - 1) * bg.logits->nb[1]);
+        pick = ggml_argmax(gctx_build, last);
+        ggml_set_output(pick);
+        ggml_build_forward_expand(bg.gf, pick);
+    }
 
     if (!ggml_gallocr_alloc_graph(ds.galloc, bg.gf)) {
         ggml_free(gctx_build);
@@ -502,12 +511,34 @@ std::vector<float> forward_step(const model & m, const hparams & hp, kv_cache & 
 
     ggml_backend_graph_compute(backend, bg.gf);
 
-    std::vector<float> last_logits(n_vocab);
-    const size_t last_col_offset = (size_t) (n_new - 1) * n_vocab * sizeof(float);
-    ggml_backend_tensor_get(bg.logits, last_logits.data(), last_col_offset, n_vocab * sizeof(float));
-
+    if (greedy_out) {
+        ggml_backend_tensor_get(pick, greedy_out, 0, sizeof(int32_t));
+    } else if (logits_out) {
+        const size_t last_col_offset = (size_t) (n_new - 1) * n_vocab * sizeof(float);
+        ggml_backend_tensor_get(bg.logits, logits_out, last_col_offset, n_vocab * sizeof(float));
+    }
     ggml_free(gctx_build);
+}
+
+std::vector<float> forward_step(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds,
+                                ggml_backend_t backend, int64_t n_past, const std::vector<int32_t> & new_tokens,
+                                int64_t n_vocab) {
+    std::vector<float> last_logits(n_vocab);
+    run_step(m, hp, kv, ds, backend, n_past, new_tokens, n_vocab, last_logits.data(), nullptr);
     return last_logits;
+}
+
+void forward_step_into(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds, ggml_backend_t backend,
+                       int64_t n_past, const std::vector<int32_t> & new_tokens, int64_t n_vocab, float * logits) {
+    run_step(m, hp, kv, ds, backend, n_past, new_tokens, n_vocab, logits, nullptr);
+}
+
+int32_t forward_step_greedy(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds,
+                            ggml_backend_t backend, int64_t n_past, const std::vector<int32_t> & new_tokens,
+                            int64_t n_vocab) {
+    int32_t tok = 0;
+    run_step(m, hp, kv, ds, backend, n_past, new_tokens, n_vocab, nullptr, &tok);
+    return tok;
 }
 
 // model.cpp:1624-1657 (the Vulkan-only chunking policy is kept for callers that ask for it)

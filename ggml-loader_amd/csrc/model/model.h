@@ -120,6 +120,14 @@ void free_decode_session(decode_session & ds);
 std::vector<float> forward_step(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds,
                                 ggml_backend_t backend, int64_t n_past, const std::vector<int32_t> & new_tokens,
                                 int64_t n_vocab);
+// forward_step writing the last column's logits (n_vocab floats) to logits, or nothing when it is null
+void forward_step_into(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds, ggml_backend_t backend,
+                       int64_t n_past, const std::vector<int32_t> & new_tokens, int64_t n_vocab, float * logits);
+// forward_step + the greedy pick of the last column computed on the backend (only the index is
+// read back; the same token as argmax(forward_step(...)))
+int32_t forward_step_greedy(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds,
+                            ggml_backend_t backend, int64_t n_past, const std::vector<int32_t> & new_tokens,
+                            int64_t n_vocab);
 
 std::vector<float> prefill(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds,
                            ggml_backend_t backend, int64_t n_past, const std::vector<int32_t> & tokens,

@@ -7,6 +7,7 @@
 //                     init_decode_session (model.cpp:667-885, 1476-1494)
 //   gl_forward_step   forward_step (model.cpp:1496-1597): logits of the last new token
 //   gl_decode_loop    run_cycle's tg loop (cmd_bench.cpp:52-59): n steps of forward_step + argmax
+//                     (the argmax runs on the backend; one index is read back per step)
 //   gl_synth_model    writes the seeded synthetic GGUF models the benchmark configs describe
 // Errors return non-zero (or NULL) and write a message into err; nothing here calls exit().
 #pragma once
@@ -27,10 +28,11 @@ GGML_API ggml_backend_t gl_session_backend(gl_session * s);
 // "n_expert_used", "weights_bytes"; -1 for an unknown name
 GGML_API int64_t      gl_session_get(const gl_session * s, const char * name);
 
-// logits: n_vocab floats for the last of the n_new tokens
+// logits: n_vocab floats for the last of the n_new tokens (NULL: computed, not read back)
 GGML_API int gl_forward_step(gl_session * s, int64_t n_past, const int32_t * tokens, int64_t n_new, float * logits,
                              char * err, size_t err_size);
-// Greedy decode: n_steps x {forward_step(n_past_i, {tok}); tok = argmax}. With fixed_pos != 0 every
+// Greedy decode: n_steps x {forward_step(n_past_i, {tok}); tok = argmax} (the first index of the
+// maximum of the last logits column, picked by the graph's argmax op on the backend). With fixed_pos != 0 every
 // step runs at n_past (the same position), otherwise n_past advances by one per step. tokens_out
 // (n_steps entries, may be NULL) receives each step's argmax; *seconds receives the wall time.
 GGML_API int gl_decode_loop(gl_session * s, int64_t n_past, int32_t first_token, int n_steps, int fixed_pos,

@@ -453,6 +453,21 @@ def test_argmax(hip, cpu):
     assert a.view(np.int32)[1] == 123
 
 
+@pytest.mark.parametrize("n,ties", [(16384, (9000, 16383)), (128256, (70000, 130)), (151936, (151935, 151934)), (200003, (1, 0))])
+def test_argmax_wide_row(hip, cpu, n, ties):
+    """One logits row (the greedy pick of forward_step_greedy) in two launches over 128 chunk
+    maxima: the first index of the maximum, also when the tied indices sit in different chunks."""
+    x = rng(15).standard_normal(n).astype(np.float32)
+    for i in ties:
+        x[i] = 40.0
+
+    def build(g):
+        return g.argmax(g.tensor(gl.F32, n, 1, data=x))
+
+    a, b = both(hip, cpu, build)
+    assert a.view(np.int32)[0] == b.view(np.int32)[0] == min(ties)
+
+
 @pytest.mark.parametrize("hd,n_head,n_head_kv,n_kv,n_new", [
     (128, 24, 8, 2049, 1),    # Llama-3B shape at position 2048
     (128, 32, 8, 8193, 1),    # Qwen3 shape at position 8192
