@@ -169,6 +169,39 @@ def test_gemm_prefill(hip, cpu, qtype, K, N, ncols):
     assert np.array_equal(a, b), rel_err(a, b)
 
 
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_gemm_q4k_extreme_blocks(hip, cpu, sign):
+    """The Q4_K GEMM's exactness bounds at their extremes: every 6-bit scale and min 63, every nibble
+    15 (all quant bytes 0xFF, so sc * q4 = 945 in f16) against activations that quantize to -127 or
+    +127 everywhere (|aux32| = 32 * 945 * 127 and |bsum| = 2032, the largest the MFMA sums see), on
+    odd rows; even rows are ordinary quantized weights."""
+    K, N, ncols = 1024, 96, 64
+    w = qweight(gl.Q4_K, K, N, 77).reshape(N, -1).copy()
+    nb = K // 256
+    r = rng(78)
+    for row in range(1, N, 2):
+        blocks = w[row].reshape(nb, 144)
+        blocks[:] = 0xFF
+        for b in range(nb):
+            blocks[b, 0:2] = np.frombuffer(np.float16(0.001 * (1 + r.random())).tobytes(), dtype=np.uint8)
+            blocks[b, 2:4] = np.frombuffer(np.float16(0.0005 * (1 + r.random())).tobytes(), dtype=np.uint8)
+    # a column of equal values quantizes to -127 everywhere; with the first value of each
+    # super-block negated (it sets the scale: the first of the largest magnitudes) the rest is +127
+    x = np.full((ncols, K), 3.0, dtype=np.float32)
+    if sign < 0:
+        x[:, ::256] = -3.0
+    x[::3] *= 0.5
+    x[1::3] = rng(79).standard_normal((len(x[1::3]), K)).astype(np.float32)   # ordinary columns
+
+    def build(g):
+        return g.mul_mat(g.tensor(gl.Q4_K, K, N, data=w.reshape(-1)), g.tensor(gl.F32, K, ncols, data=x))
+
+    a, names = profiled(hip, lambda: run_on(hip, build))
+    b = run_on(cpu, build)
+    assert "gemm_q4_K" in names, names
+    assert np.array_equal(a, b), rel_err(a, b)
+
+
 @pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K])
 def test_gemm_norm_qkv_residual(hip, cpu, qtype):
     """rms_norm * w feeding three prefill-width GEMMs (normalized and quantized once), and a GEMM
