@@ -579,11 +579,14 @@ def test_attention_prefill(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
     (128, 32, 4, 4112, 16),   # the MoE config's 16-token step at position 4096
     (128, 8, 8, 3000, 7),     # a partial last group of queries
     (64, 4, 2, 9000, 5),
+    (96, 8, 8, 2500, 20),     # Phi-3 head dim
+    (128, 24, 8, 2300, 70),   # Llama GQA group of 3, two launches of up to 64 queries
 ])
 @pytest.mark.parametrize("flash", [False, True])
 def test_attention_long_context_query_groups(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
     """A multi-token step over more positions than the prefill kernel holds in LDS: the decode
-    kernels per group of 4 queries, the chain's float roundings exactly."""
+    kernels with the queries in groups of 4 (launches of up to 64 queries), the chain's float
+    roundings exactly."""
     r = rng(n_kv + 7 * n_new)
     n_ctx = n_kv + 3
     kc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
