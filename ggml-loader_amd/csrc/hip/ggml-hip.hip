@@ -567,8 +567,10 @@ private:
                 op_gemv(i);
                 return;
             case GGML_OP_MUL:
-                if (fuse(FUSE_ADD) && op_moe_wsum(i)) return;
+                // a mul whose silu operand was held back runs as the fused SwiGLU (nothing else
+                // may take it: the silu output was never written)
                 if (silu_of_.count(i)) { run_swiglu(silu_of_[i], i); return; }
+                if (fuse(FUSE_ADD) && op_moe_wsum(i)) return;
                 break;
             case GGML_OP_SOFT_MAX:
                 if (fuse(FUSE_ROUTE) && op_moe_route(i)) return;
