@@ -772,7 +772,8 @@ template <int TYPE, bool SWIGLU>
 static void launch_gemv_lanes(gemv_kargs & ka, hipStream_t st) {
     constexpr int WAVES = 4, TARGET_BLOCKS = 512;
     const int rows = ka.total_rows, K = ka.L.K;
-    const auto blocks = [&](int lpr) { return (rows + WAVES * (WAVE / lpr) - 1) / (WAVES * (WAVE / lpr)); };
+    // workgroups of the launch: row blocks times the grid's columns (mul_mat_id: token x slot)
+    const auto blocks = [&](int lpr) { return (rows + WAVES * (WAVE / lpr) - 1) / (WAVES * (WAVE / lpr)) * ka.L.ncols; };
     const int k16 = SWIGLU ? gemv_swiglu_max_k(TYPE) : 8192;     // longest K of 16 lanes per row
     if (K <= k16 && blocks(16) >= TARGET_BLOCKS) launch_gemv_t<TYPE, 16, SWIGLU>(ka, WAVES, st);
     else if (K <= 2 * k16 && blocks(32) >= TARGET_BLOCKS) launch_gemv_t<TYPE, 32, SWIGLU>(ka, WAVES, st);
@@ -786,7 +787,7 @@ template <bool SWIGLU>
 static void launch_gemv_q4k_lanes(gemv_kargs & ka, hipStream_t st) {
     constexpr int WAVES = 4, TARGET_BLOCKS = 512;
     const int rows = ka.total_rows, units = ka.L.K / 64;
-    const auto blocks = [&](int lpr) { return (rows + WAVES * (WAVE / lpr) - 1) / (WAVES * (WAVE / lpr)); };
+    const auto blocks = [&](int lpr) { return (rows + WAVES * (WAVE / lpr) - 1) / (WAVES * (WAVE / lpr)) * ka.L.ncols; };
     if constexpr (!SWIGLU) {
         if (units <= 16 * 4 && blocks(16) >= TARGET_BLOCKS) return launch_gemv_t<GGML_TYPE_Q4_K, 16, SWIGLU>(ka, WAVES, st);
     }
