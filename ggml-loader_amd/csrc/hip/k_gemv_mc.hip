@@ -270,13 +270,28 @@ static bool launch_mc_type(const gemv_launch & L, const expert_groups * G, int m
     const int K = L.K;
     const int n_units = TYPE == GGML_TYPE_Q4_K ? K / 64 : K / 32;
     const int want = G ? G->nc : std::min(GEMV_MC_MAX_COLS, L.ncols);
+    const int rows_total = SWIGLU ? L.m[0].n_rows : [&] { int r = 0; for (int i = 0; i < L.n_mats; i++) r += L.m[i].n_rows; return r; }();
     for (int nc = want; nc >= 1; nc = (G || nc == 1) ? 0 : (nc + 1) / 2) {
+        // the fewest lanes per row (most rows per workgroup) that still give the launch about two
+        // workgroups per CU (grouped mul_mat_id: one row block per work item), else the most
+        // workgroups that fit
+        constexpr int TARGET_BLOCKS = 512;
+        int pick = 0;
         for (int lpr : { 16, 32, 64 }) {
             const int rows_pb = (MC_THREADS / WAVE) * (WAVE / lpr);
             const int chains = rows_pb * NCH * nc;
             if (chains > MC_THREADS || (n_units + lpr - 1) / lpr > 12) continue;
+            const size_t lds_c = (size_t) nc * mc_act_bytes<TYPE>(K) + (size_t) chains * mc_term_stride<TYPE>(K) * 4;
+            if (lds_c > MC_MAX_LDS) continue;
+            pick = lpr;
+            const int64_t blocks = (int64_t) ((rows_total + rows_pb - 1) / rows_pb) * (G ? G->max_items : (L.ncols + nc - 1) / nc);
+            if (blocks >= TARGET_BLOCKS) break;
+        }
+        if (pick) {
+            const int lpr = pick;
+            const int rows_pb = (MC_THREADS / WAVE) * (WAVE / lpr);
+            const int chains = rows_pb * NCH * nc;
             const size_t lds = (size_t) nc * mc_act_bytes<TYPE>(K) + (size_t) chains * mc_term_stride<TYPE>(K) * 4;
-            if (lds > MC_MAX_LDS) continue;
             if (dry) return true;
             gemv_mc_args A{};
             A.a.L = L;
