@@ -402,6 +402,8 @@ private:
     std::unordered_map<const ggml_tensor *, gemv_norm> norm_;   // deferred rms_norm * w outputs
     std::unordered_map<int, attn_match> attn_;
     std::unordered_map<int, int> silu_of_;    // mul node -> its held-back silu node (op_swiglu)
+    struct router_norm { int norm, mul; float eps; };
+    std::unordered_map<int, router_norm> router_norm_;   // router mul_mat node -> the norm it computes
     std::vector<const ggml_tensor *> wrote_;
 
     bool fuse(int bit) const { return c_.fusion && (c_.fuse_mask & bit); }
@@ -872,6 +874,37 @@ private:
         return true;
     }
 
+    // the lowest node index that reads node u's data, directly or through views (INT_MAX: none)
+    int first_reader(int u) const {
+        int first = INT_MAX;
+        for (int j : users_[u]) {
+            const ggml_tensor * t = g_->nodes[j];
+            first = std::min(first, is_view_op(t->op) ? first_reader(j) : j);
+        }
+        return first;
+    }
+
+    // The MoE FFN norm: rms_norm -> mul(w) whose first reader in node order is the F32 router
+    // mul_mat (build_moe_ffn's ffn_gate_inp product). Nothing is launched here: the router launch
+    // normalizes each column itself and writes the mul's output for the later readers (the expert
+    // GEMVs), so the norm costs no launch of its own.
+    bool defer_router_norm(int i, int u, float eps) {
+        if (!fuse(FUSE_ROUTE) || is_output(u)) return false;
+        const ggml_tensor * n = g_->nodes[i], * m = g_->nodes[u];
+        const ggml_tensor * x = n->src[0];
+        const int r = first_reader(u);
+        if (r == INT_MAX) return false;
+        const ggml_tensor * rn = g_->nodes[r];
+        if (rn->op != GGML_OP_MUL_MAT || rn->src[1] != m || !is_2d_contig(rn) || !is_2d_contig(m)) return false;
+        if (!mul_mat_rows_norm_supported(tv(rn->src[0]), x->ne[0]) || x->ne[2] != 1 || x->ne[3] != 1 || x->nb[0] != 4 ||
+            x->nb[1] % 4) {
+            return false;
+        }
+        router_norm_[r] = router_norm{ i, u, eps };
+        done_[u] = true;
+        return true;
+    }
+
     // rms_norm, fused with a following weight multiply (and activation quantization) when possible
     void op_rms_norm(int i) {
         ggml_tensor * n = g_->nodes[i];
@@ -889,6 +922,7 @@ private:
                     w->ne[0] == x->ne[0] && ggml_is_contiguous(w) && ggml_is_contiguous(m)) {
                     const int64_t N = x->ne[0], rows = ggml_nrows(x);
                     if (defer_qk_norm(i)) return;
+                    if (defer_router_norm(i, u, eps)) return;
                     if (m->ne[1] == rows && norm_deferrable(u, N) && ((uintptr_t) x->data | (uintptr_t) w->data) % 16 == 0) {
                         const gemv_norm nz{ (const float *) x->data, N, (const float *) w->data, eps, 1 };
                         done_[u] = true;
@@ -1028,6 +1062,18 @@ private:
         }
         if (n->src[1]->type != GGML_TYPE_F32 || n->src[0]->nb[0] != ggml_type_size(n->src[0]->type)) {
             HIP_ABORT("mul_mat '%s': unsupported operand layout", n->name);
+        }
+        auto rn = router_norm_.find(i);
+        if (rn != router_norm_.end()) {
+            const ggml_tensor * x = g_->nodes[rn->second.norm]->src[0];
+            ggml_tensor * m = g_->nodes[rn->second.mul];
+            const ggml_tensor * nw = m->src[1];
+            wrote_.push_back(m);
+            wrote_.push_back(n);
+            prof_scope ps(this, "router_norm", (double) (ggml_nbytes(n->src[0]) + 2 * ggml_nbytes(x) + ggml_nbytes(n)));
+            launch_mul_mat_rows_norm(tv(n->src[0]), (const float *) x->data, (int64_t) (x->nb[1] / 4), (const float *) nw->data,
+                                     rn->second.eps, (float *) m->data, (int64_t) (m->nb[1] / 4), tv(n), x->ne[1], st_);
+            return;
         }
         wrote_.push_back(n);
         prof_scope ps(this, "mul_mat_generic", (double) (ggml_nbytes(n->src[0]) + ggml_nbytes(n->src[1]) + ggml_nbytes(n)));

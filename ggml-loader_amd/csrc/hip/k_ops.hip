@@ -758,6 +758,80 @@ __global__ __launch_bounds__(256) void mul_mat_rows_kernel(tview s0, tview s1, t
     if (lane == 0) *(float *) at(d, k.i0, k.i1, k.i2, k.i3) = (float) acc;
 }
 
+// The MoE router with the FFN norm folded in: y = rms_norm(x) * nw computed by every workgroup of
+// a column into LDS (the rms_norm_kernel's partition and roundings: per-thread double sums of
+// squares over i = t, t + 256, ..., the four wave sums in order, mean and scale in float, then
+// (x * scale) * nw), written to y_out by the column's first workgroup for the other consumers, and
+// the F32 router rows dotted with it as mul_mat_rows_kernel does (same lane partition, float
+// products summed in double). One wave per router row, 4 rows per workgroup, grid.y = columns.
+__global__ __launch_bounds__(256) void mul_mat_rows_norm_kernel(tview w, const float * __restrict__ x, int64_t x_stride,
+                                                                const float * __restrict__ nw, float eps,
+                                                                float * __restrict__ y_out, int64_t y_stride, tview d) {
+    extern __shared__ __align__(16) float s_y[];      // [K]
+    __shared__ double s_part[4];
+    const int64_t K = w.ne[0], col = blockIdx.y;
+    const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
+    const float * xc = x + col * x_stride;
+    double sum = 0.0;
+    for (int64_t i = t; i < K; i += 256) {
+        const float v = xc[i];
+        s_y[i] = v;
+        sum += (double) (v * v);
+    }
+    sum = wave_sum_d(sum);
+    if (lane == 0) s_part[wave] = sum;
+    __syncthreads();
+    const double total = s_part[0] + s_part[1] + s_part[2] + s_part[3];
+    const float mean = (float) (total / (double) K);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t i = t; i < K; i += 256) {
+        const float o = (s_y[i] * scale) * nw[i];
+        s_y[i] = o;
+        if (blockIdx.x == 0) y_out[col * y_stride + i] = o;
+    }
+    __syncthreads();
+    const int64_t o = (int64_t) blockIdx.x * 4 + wave;
+    if (o >= w.ne[1]) return;
+    const float * a = (const float *) (w.data + o * w.nb[1]);
+    const int nch = (int) (K / 8);
+    double acc = 0.0;
+    for (int c0 = 0; c0 < nch; c0 += MR_BATCH * WAVE) {
+        float wv[MR_BATCH][8], v[MR_BATCH][8];
+#pragma unroll
+        for (int j = 0; j < MR_BATCH; j++) {
+            const int c = min(c0 + j * WAVE + lane, nch - 1);
+            const float4 x0 = ((const float4 *) s_y)[2 * c], x1 = ((const float4 *) s_y)[2 * c + 1];
+            v[j][0] = x0.x; v[j][1] = x0.y; v[j][2] = x0.z; v[j][3] = x0.w;
+            v[j][4] = x1.x; v[j][5] = x1.y; v[j][6] = x1.z; v[j][7] = x1.w;
+            const float4 a0 = ((const float4 *) a)[2 * c], a1 = ((const float4 *) a)[2 * c + 1];
+            wv[j][0] = a0.x; wv[j][1] = a0.y; wv[j][2] = a0.z; wv[j][3] = a0.w;
+            wv[j][4] = a1.x; wv[j][5] = a1.y; wv[j][6] = a1.z; wv[j][7] = a1.w;
+        }
+#pragma unroll
+        for (int j = 0; j < MR_BATCH; j++) {
+            if (c0 + j * WAVE + lane >= nch) continue;
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc += (double) (wv[j][e] * v[j][e]);
+        }
+    }
+    acc = wave_sum_d(acc);
+    if (lane == 0) *(float *) at(d, o, col, 0, 0) = (float) acc;
+}
+
+bool mul_mat_rows_norm_supported(const tview & w, int64_t K) {
+    return w.type == GGML_TYPE_F32 && w.ne[0] == K && K % 8 == 0 && K <= MUL_MAT_ROWS_NORM_MAX_K && w.nb[0] == 4 &&
+           w.ne[2] == 1 && w.ne[3] == 1 && ((uintptr_t) w.data % 16) == 0 && w.nb[1] % 16 == 0;
+}
+
+void launch_mul_mat_rows_norm(const tview & w, const float * x, int64_t x_stride, const float * nw, float eps, float * y_out,
+                              int64_t y_stride, const tview & dst, int64_t ncols, hipStream_t st) {
+    if (!mul_mat_rows_norm_supported(w, w.ne[0]) || dst.ne[0] != w.ne[1] || dst.ne[1] != ncols || dst.nb[0] != 4) {
+        HIP_ABORT("mul_mat_rows_norm: unsupported operands");
+    }
+    launch(mul_mat_rows_norm_kernel, dim3((unsigned) ((w.ne[1] + 3) / 4), (unsigned) ncols), dim3(256),
+           (size_t) w.ne[0] * sizeof(float), st, w, x, x_stride, nw, eps, y_out, y_stride, dst);
+}
+
 void launch_mul_mat_generic(const tview & src0, const tview & src1, const tview & dst, hipStream_t st) {
     const int64_t n = nelem(dst);
     if (n == 0) return;

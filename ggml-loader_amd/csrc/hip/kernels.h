@@ -246,6 +246,12 @@ void launch_argmax_row(const tview & a, int32_t * out, float * part_v, int * par
 
 // generic F32/F16/BF16 mul_mat (src0 rows contiguous): one wave per output element
 void launch_mul_mat_generic(const tview & src0, const tview & src1, const tview & dst, hipStream_t st);
+// dst[:, c] = W^T (rms_norm(x[:, c]) * nw) for an F32 W [K, rows] (the MoE router), also writing
+// the normalized columns to y_out (the rms_norm -> mul output, for the norm's other consumers)
+constexpr int64_t MUL_MAT_ROWS_NORM_MAX_K = 8192;
+bool mul_mat_rows_norm_supported(const tview & w, int64_t K);
+void launch_mul_mat_rows_norm(const tview & w, const float * x, int64_t x_stride, const float * nw, float eps, float * y_out,
+                              int64_t y_stride, const tview & dst, int64_t ncols, hipStream_t st);
 
 // MoE routing of one token per workgroup: softmax over the router logits (the soft_max op's
 // arithmetic), the k most probable experts in the stable descending order of argsort (ties: the

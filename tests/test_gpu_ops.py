@@ -739,6 +739,33 @@ def test_moe_ffn(hip, cpu, qtype, n_tok):
     assert (n_tok >= 2) == ("moe_group" in names), names   # several tokens: experts read once for all of theirs
 
 
+@pytest.mark.parametrize("n_tok", [1, 5])
+def test_moe_ffn_norm_folded_into_router(hip, cpu, n_tok):
+    """The MoE FFN norm (rms_norm -> mul) whose first reader is the F32 router: no launch of its own;
+    the router launch normalizes each column (the rms_norm op's roundings) and writes the normalized
+    activation the expert GEMVs read afterwards."""
+    n_embd, E, k, ff = 512, 32, 8, 256
+    r = rng(74)
+    x = (r.standard_normal((n_tok, n_embd)) * 3).astype(np.float32)
+    nw = (1 + 0.01 * r.standard_normal(n_embd)).astype(np.float32)
+    router = (r.standard_normal((E, n_embd)) * 0.05).astype(np.float32)
+    wg, wu = (qweight(gl.Q4_K, n_embd, E * ff, s, std=0.05) for s in (75, 76))
+    wd = qweight(gl.Q4_K, ff, E * n_embd, 77, std=0.05)
+
+    def build(g):
+        xt = g.tensor(gl.F32, n_embd, n_tok, data=x)
+        y = g.mul(g.rms_norm(xt, 1e-6), g.tensor(gl.F32, n_embd, data=nw))
+        return moe_ffn_graph(g, y, g.tensor(gl.F32, n_embd, E, data=router),
+                             g.tensor(gl.Q4_K, n_embd, ff, E, data=wg), g.tensor(gl.Q4_K, n_embd, ff, E, data=wu),
+                             g.tensor(gl.Q4_K, ff, n_embd, E, data=wd), k, xt)
+
+    for fusion in (True, False):
+        a, b = both(hip, cpu, build, fusion)
+        assert np.array_equal(a, b), (fusion, rel_err(a, b))
+    _, names = profiled(hip, lambda: run_on(hip, build))
+    assert "router_norm" in names and "rms_norm_mul" not in names, names
+
+
 @pytest.mark.parametrize("E,k,n_tok", [(128, 8, 1), (128, 8, 16), (60, 4, 3), (1024, 32, 2), (8, 8, 1)])
 def test_moe_route_fused(hip, cpu, E, k, n_tok):
     """Router softmax -> top-k -> renormalized weights in one kernel: the same ids (ties: the lower
