@@ -124,7 +124,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
     constexpr int STRIDE = HD2 + 1;
     __shared__ uint32_t s_k[ATT_CHUNK * STRIDE];
     extern __shared__ float s_dyn[];
-    const int split = blockIdx.x, kvh = blockIdx.y;
+    // blockIdx.y: a group of G consecutive heads (all heads of KV head kvh, or a part of them when
+    // the launch splits a large GQA group over several workgroups); h0 its first head
+    const int split = blockIdx.x, h0 = blockIdx.y * G, kvh = h0 / (A.n_head / A.n_head_kv);
+    const bool kv_writer = h0 % (A.n_head / A.n_head_kv) == 0;   // the first group of a KV head appends K and V
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int t0 = split * ATT_CHUNK;
     const int nt = min(ATT_CHUNK, A.n_kv - t0);
@@ -158,7 +161,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
     for (int j = 0; j < QR; j++) {
         const int i = min(t + j * ATT_THREADS, nqe - 1);
         const int pr = i / HD;
-        qv[j] = qb[(int64_t) (kvh * G + pr % G) * qs1 + (int64_t) (q0 + pr / G) * qs2 + i % HD];
+        qv[j] = qb[(int64_t) (h0 + pr % G) * qs1 + (int64_t) (q0 + pr / G) * qs2 + i % HD];
     }
     const float * kb = !A.rope ? qb : knorm ? A.kn.x : (const float *) A.rk.src.data;
     const int64_t ks1 = !A.rope ? qs1 : knorm ? A.kn.nb1 : A.rk.src.nb[1] / 4;
@@ -277,16 +280,18 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
                 const float kr = rope_value_with(A.rk.p, d, s_cs + tk * np, [&](int e) {
                     return knorm ? (xr[e] * sc) * s_kw[e] : xr[e];
                 });
-                st(at(A.rk.dst, d, kvh, tk, 0), GGML_TYPE_F16, kr);
+                if (kv_writer) {
+                    st(at(A.rk.dst, d, kvh, tk, 0), GGML_TYPE_F16, kr);
+                    st(at(A.rv.dst, d, kvh, tk, 0), GGML_TYPE_F16, s_vx[i]);
+                }
                 ((__half *) (s_k + (pos - t0) * STRIDE))[d] = __float2half_rn(as_f32(kr));
-                st(at(A.rv.dst, d, kvh, tk, 0), GGML_TYPE_F16, s_vx[i]);
             }
         }
     }
     __syncthreads();
 
     for (int pr = wave; pr < n_q * G; pr += ATT_WAVES) {
-        const int q = pr / G, g = pr % G, h = kvh * G + g;
+        const int q = pr / G, g = pr % G, h = h0 + g;
         float sv = -INFINITY;
         if (lane < nt) {
             const uint32_t * kr = s_k + lane * STRIDE;
@@ -360,7 +365,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     constexpr int R = ATT_MAX_Q * G;
     __shared__ uint32_t s_v[PV_CHUNK * STRIDE];
     __shared__ float s_p[R][PV_CHUNK];
-    const int split = blockIdx.x, kvh = blockIdx.y;
+    const int split = blockIdx.x, h0 = blockIdx.y * G, kvh = h0 / (A.n_head / A.n_head_kv);   // as in the scores kernel
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
     const int t0 = split * PV_CHUNK;
     const int nt = min(PV_CHUNK, A.n_kv - t0);
@@ -385,7 +390,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     const int nseg = attn_segs(A.n_kv);
     if ((int) threadIdx.x < n_rows) {
         const int pr = threadIdx.x;
-        const int64_t row = (int64_t) (q0 + pr / G) * A.n_head + kvh * G + pr % G;
+        const int64_t row = (int64_t) (q0 + pr / G) * A.n_head + h0 + pr % G;
         double tot = 0.0;
         for (int k = 0; k < nseg; k++) tot += S.ssum[row * nseg + k];
         s_M[pr] = S.rmax[row];
@@ -394,7 +399,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     __syncthreads();
     for (int i = threadIdx.x; i < n_rows * PV_CHUNK; i += ATT_THREADS) {
         const int pr = i / PV_CHUNK, t = i % PV_CHUNK;
-        const int64_t row = (int64_t) (q0 + pr / G) * A.n_head + kvh * G + pr % G;
+        const int64_t row = (int64_t) (q0 + pr / G) * A.n_head + h0 + pr % G;
         float p = 0.0f;
         if (t < nt) {
             const float M = s_M[pr], inv = s_inv[pr];
@@ -413,7 +418,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     __syncthreads();
 
     for (int pr = wave; pr < n_rows; pr += ATT_WAVES) {
-        const int q = q0 + pr / G, h = kvh * G + pr % G;
+        const int q = q0 + pr / G, h = h0 + pr % G;
         if (lane < HD2) {
             // two independent chains per dimension (even and odd positions; exact sums as above;
             // p is 0 past nt)
@@ -476,15 +481,18 @@ static void launch_attn_t(const attn_launch & A, hipStream_t st) {
     const int splits = (A.n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
     const int pv_splits = (A.n_kv + PV_CHUNK - 1) / PV_CHUNK;
     const int qz = (A.n_q + ATT_MAX_Q - 1) / ATT_MAX_Q;   // groups of up to ATT_MAX_Q queries
-    launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head_kv, qz), dim3(ATT_THREADS),
+    // G: heads per workgroup (the GQA group, or a part of it); grid.y = head groups
+    launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head / G, qz), dim3(ATT_THREADS),
            scores_dyn_floats<HD, G>(std::min(A.n_q, ATT_MAX_Q)) * sizeof(float), st, A);
     launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
-    launch((attn_pv_kernel<HD, G>), dim3(pv_splits, A.n_head_kv, qz), dim3(ATT_THREADS), 0, st, A);
+    launch((attn_pv_kernel<HD, G>), dim3(pv_splits, A.n_head / G, qz), dim3(ATT_THREADS), 0, st, A);
     launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(HD), 0, st, A, pv_splits);
 }
 
 template <int HD>
 static void launch_attn_hd(const attn_launch & A, hipStream_t st) {
+    // heads per workgroup: the GQA group, halved for groups of 8 (two workgroups per KV head and
+    // chunk: half the rows each, twice the workgroups; K and V are read by both, from L2)
     const int G = A.n_head / A.n_head_kv;
     switch (G) {
         case 1: launch_attn_t<HD, 1>(A, st); break;
@@ -494,7 +502,7 @@ static void launch_attn_hd(const attn_launch & A, hipStream_t st) {
         case 5: launch_attn_t<HD, 5>(A, st); break;
         case 6: launch_attn_t<HD, 6>(A, st); break;
         case 7: launch_attn_t<HD, 7>(A, st); break;
-        case 8: launch_attn_t<HD, 8>(A, st); break;
+        case 8: launch_attn_t<HD, 4>(A, st); break;
         default: HIP_ABORT("attn: unsupported GQA group %d", G);
     }
 }
