@@ -491,10 +491,15 @@ static void launch_attn_t(const attn_launch & A, hipStream_t st) {
 
 template <int HD>
 static void launch_attn_hd(const attn_launch & A, hipStream_t st) {
-    // heads per workgroup: the GQA group, halved for groups of 8 (two workgroups per KV head and
-    // chunk: half the rows each, twice the workgroups; K and V are read by both, from L2)
+    // heads per workgroup: the GQA group, halved while a workgroup would hold more than 4 (query,
+    // head) rows for one query, 8 for several (more workgroups with fewer rows each; the split
+    // workgroups of a KV head read its K and V chunk each, mostly from L2). Measured: one query
+    // with 8 heads per KV head runs best at 4 heads per workgroup, 16-query steps at 2.
     const int G = A.n_head / A.n_head_kv;
-    switch (G) {
+    const int max_rows = A.n_q > 1 ? 8 : 4;
+    int hp = G;
+    while (hp % 2 == 0 && hp * std::min(A.n_q, ATT_MAX_Q) > max_rows) hp /= 2;
+    switch (hp) {
         case 1: launch_attn_t<HD, 1>(A, st); break;
         case 2: launch_attn_t<HD, 2>(A, st); break;
         case 3: launch_attn_t<HD, 3>(A, st); break;
@@ -502,7 +507,7 @@ static void launch_attn_hd(const attn_launch & A, hipStream_t st) {
         case 5: launch_attn_t<HD, 5>(A, st); break;
         case 6: launch_attn_t<HD, 6>(A, st); break;
         case 7: launch_attn_t<HD, 7>(A, st); break;
-        case 8: launch_attn_t<HD, 4>(A, st); break;
+        case 8: launch_attn_t<HD, 8>(A, st); break;
         default: HIP_ABORT("attn: unsupported GQA group %d", G);
     }
 }
