@@ -440,23 +440,32 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     }
 }
 
-// one thread per output element (head, dim) of one query: the chunk partials added in chunk order
+// two threads per output element (head, dim) of one query: each adds half of the chunk partials in
+// chunk order, then the two halves are added (the sums are exact for these operands, so the
+// grouping does not change the result)
 template <int HD>
-__global__ __launch_bounds__(HD) void attn_combine_kernel(const attn_launch A, int n_splits) {
-    const int h = blockIdx.x, q = blockIdx.y, d = threadIdx.x;
+__global__ __launch_bounds__(2 * HD) void attn_combine_kernel(const attn_launch A, int n_splits) {
+    __shared__ double s_half[HD];
+    const int h = blockIdx.x, q = blockIdx.y, d = threadIdx.x % HD, part = threadIdx.x / HD;
     const attn_scratch S = scratch_of(A);
     const double * pp = S.parts + ((int64_t) q * A.n_head + h) * HD + d;
     const int64_t step = (int64_t) A.n_q * A.n_head * HD;
+    const int mid = (n_splits + 1) / 2;
+    const int s0 = part ? mid : 0, s1 = part ? n_splits : mid;
     double acc = 0.0;
-    int s = 0;
-    for (; s + 8 <= n_splits; s += 8) {
+    int s = s0;
+    for (; s + 8 <= s1; s += 8) {
         double v[8];
 #pragma unroll
         for (int k = 0; k < 8; k++) v[k] = pp[(s + k) * step];
 #pragma unroll
         for (int k = 0; k < 8; k++) acc += v[k];
     }
-    for (; s < n_splits; s++) acc += pp[s * step];
+    for (; s < s1; s++) acc += pp[s * step];
+    if (part) s_half[d] = acc;
+    __syncthreads();
+    if (part) return;
+    acc += s_half[d];
     const float v = (float) acc;
     const int64_t oi = (int64_t) h * HD + d;
     A.out[(int64_t) q * A.out_nb1 + oi] = v;
@@ -486,7 +495,7 @@ static void launch_attn_t(const attn_launch & A, hipStream_t st) {
            scores_dyn_floats<HD, G>(std::min(A.n_q, ATT_MAX_Q)) * sizeof(float), st, A);
     launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
     launch((attn_pv_kernel<HD, G>), dim3(pv_splits, A.n_head / G, qz), dim3(ATT_THREADS), 0, st, A);
-    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(HD), 0, st, A, pv_splits);
+    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(2 * HD), 0, st, A, pv_splits);
 }
 
 template <int HD>
