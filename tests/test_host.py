@@ -343,3 +343,43 @@ def test_oracle_forward_against_float64_model(models, arch):
             assert np.all(np.isfinite(lc))
             tok = int(np.argmax(lc))
     assert checked >= 1
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 exits with a message instead of a number."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_bench_pmc_summary_scales_by_the_copy_kernel(tmp_path):
+    """The HBM traffic per launch: each counter (KiB per dispatch) scaled by what it reads for the
+    copy kernel of known size, averaged over the matching dispatches."""
+    import csv
+    import importlib.util
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(root, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+
+    def write(d, rows):
+        os.makedirs(d / "run", exist_ok=True)
+        with open(d / "run" / "x_counter_collection.csv", "w", newline="") as f:
+            w = csv.DictWriter(f, fieldnames=["Kernel_Name", "Counter_Value"])
+            w.writeheader()
+            for name, v in rows:
+                w.writerow({"Kernel_Name": name, "Counter_Value": v})
+
+    mb = 256
+    write(tmp_path / "cf", [("cpy_kernel(tview)", mb * 1024 / 2)])        # FETCH_SIZE reads half the bytes
+    write(tmp_path / "cw", [("cpy_kernel(tview)", mb * 1024)])
+    write(tmp_path / "f", [("void gemv_kernel<2, 16>", 100.0), ("void gemv_kernel<2, 32>", 300.0), ("other", 1e6)])
+    write(tmp_path / "w", [("void gemv_kernel<2, 16>", 2.0), ("void gemv_kernel<2, 32>", 4.0)])
+    out = bench.summarize_pmc(str(tmp_path / "f"), str(tmp_path / "w"), str(tmp_path / "cf"), str(tmp_path / "cw"), mb,
+                              "void gemv_kernel<2,")
+    assert out["dispatches"] == 2
+    assert out["fetch_scale"] == 2.0 and out["write_scale"] == 1.0
+    assert out["traffic_bytes_per_launch"] == round(200.0 * 1024 * 2 + 3.0 * 1024)
