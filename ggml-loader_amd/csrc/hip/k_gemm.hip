@@ -530,8 +530,9 @@ void launch_gemm(const gemm_launch & G, hipStream_t st) {
     }
     if (G.type == GGML_TYPE_Q4_K) {
         if (!G.xbs || ((uintptr_t) G.xbs % 8) || ((uintptr_t) G.xd % 4)) HIP_ABORT("gemm: Q4_K needs Q8_K columns with 8-byte aligned bsums");
-        // 64 x 64 tiles where they still give every CU two workgroups, else 32 x 64
-        if (n_tiles(G, 64, 64) >= 512) launch_gemm_q4k_t<2, 2>(G, st);
+        // 64 x 64 tiles where they give every CU a workgroup, else 32 x 64 (measured: the larger
+        // tile is faster down to one workgroup per CU)
+        if (n_tiles(G, 64, 64) >= 256) launch_gemm_q4k_t<2, 2>(G, st);
         else launch_gemm_q4k_t<1, 2>(G, st);
         return;
     }
