@@ -789,6 +789,13 @@ private:
         for (int j : members) {
             if (g_->nodes[j]->op == GGML_OP_ROPE) materialize_norm(g_->nodes[j]->src[0]);
         }
+        // many tokens (prefill): the rotations read one (cos, sin) table per graph instead of
+        // forming the same angles for every head of every layer
+        for (int k = 0; k < B.n_jobs; k++) {
+            rope_job & J = B.job[k];
+            const int64_t n_pos = J.src.ne[2];
+            if (J.pos && n_pos >= ROPE_TABLE_MIN_TOKENS && J.p.n_dims >= 2) J.cs = rope_table_of(J, n_pos);
+        }
         {
             prof_scope ps(this, "rope", 0);
             launch_rope_batch(B, st_);
@@ -808,6 +815,22 @@ private:
     int cs_n_ = 0;
     rope_params cs_p_{};
     pending_rope prope_;
+    // the (cos, sin) table of a multi-token RoPE (prefill), formed once per graph for the rotations of
+    // the same positions and parameters (Q and K of every layer)
+    struct rope_table { float2 * tab; const int32_t * pos; const float * ff; int64_t n; rope_params p; };
+    std::vector<rope_table> rope_tabs_;
+    const float2 * rope_table_of(const rope_job & J, int64_t n_pos) {
+        for (const rope_table & t : rope_tabs_) {
+            if (t.pos == J.pos && t.ff == J.ff && t.n == n_pos && memcmp(&t.p, &J.p, sizeof(rope_params)) == 0) return t.tab;
+        }
+        float2 * tab = (float2 *) c_.scratch.alloc((size_t) n_pos * (J.p.n_dims / 2) * sizeof(float2));
+        {
+            prof_scope ps(this, "rope_table", 0);
+            launch_rope_table(J.pos, n_pos, J.p, J.ff, tab, st_);
+        }
+        rope_tabs_.push_back(rope_table{ tab, J.pos, J.ff, n_pos, J.p });
+        return tab;
+    }
 
     bool defer_rope(const rope_batch & B, const std::vector<int> & members) {
         if (!fuse(FUSE_ATTN) || B.n_jobs != 3 || members.size() != 4) return false;

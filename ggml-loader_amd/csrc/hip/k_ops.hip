@@ -424,12 +424,14 @@ __device__ __forceinline__ void rope_pair(const rope_job & J, int64_t li) {
         for (int k = 0; k < 2; k++) st(at(d, i0 + k, i1, i2, i3), d.type, *(const float *) at(x, i0 + k, i1, i2, i3));
         return;
     }
-    // theta after i0/2 multiplications by theta_scale, in float, as the CPU cache builds it
-    float theta = (float) J.pos[i2];
-    for (int k = 0; k < i0 / 2; k++) theta *= p.theta_scale;
-    const float f = J.ff ? J.ff[i0 / 2] : 1.0f;
     float c, sn;
-    rope_cs(theta / f, p, i0, c, sn);
+    if (J.cs) {
+        const float2 v = J.cs[i2 * (p.n_dims / 2) + i0 / 2];
+        c = v.x;
+        sn = v.y;
+    } else {
+        rope_pair_cs(p, J.ff, J.pos[i2], i0 / 2, c, sn);
+    }
     int64_t a0, a1;
     if (p.mode & GGML_ROPE_TYPE_NEOX) { a0 = i0 / 2; a1 = i0 / 2 + p.n_dims / 2; }
     else { a0 = i0; a1 = i0 + 1; }
@@ -467,6 +469,23 @@ void launch_rope_batch(rope_batch & B, hipStream_t st) {
     }
     if (blocks == 0) return;
     launch(rope_batch_kernel, dim3((unsigned) blocks), dim3(256), 0, st, B);
+}
+
+// one thread per (token, rotation pair): rope_pair_cs (theta after ip multiplications by
+// theta_scale in float, as the CPU cache builds it; then the correctly rounded cos and sin)
+__global__ void rope_table_kernel(const int32_t * pos, int64_t n_pos, rope_params p, const float * ff, float2 * out) {
+    const int half = p.n_dims / 2;
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_pos * half) return;
+    float c, s;
+    rope_pair_cs(p, ff, pos[i / half], (int) (i % half), c, s);
+    out[i] = make_float2(c, s);
+}
+
+void launch_rope_table(const int32_t * pos, int64_t n_pos, const rope_params & p, const float * ff, float2 * out, hipStream_t st) {
+    const int64_t n = n_pos * (p.n_dims / 2);
+    if (n <= 0) return;
+    launch(rope_table_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, pos, n_pos, p, ff, out);
 }
 
 void launch_rope(const tview & src, const int32_t * pos, const float * freq_factors, const tview & dst,

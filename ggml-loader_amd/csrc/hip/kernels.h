@@ -210,6 +210,7 @@ struct rope_job {
     const float * ff;          // optional frequency factors
     rope_params p;
     int64_t n;                 // work items: rotation pairs, or elements for a copy
+    const float2 * cs;         // optional (cos, sin) table [token][n_dims / 2] (launch_rope_table)
 };
 struct rope_batch {
     rope_job job[ROPE_MAX_JOBS];
@@ -217,6 +218,11 @@ struct rope_batch {
     int n_jobs;
 };
 void launch_rope_batch(rope_batch & B, hipStream_t st);
+constexpr int64_t ROPE_TABLE_MIN_TOKENS = 16;   // RoPE jobs over at least this many tokens read a table
+// (cos, sin) of every rotation pair of n_pos tokens at positions pos, [n_pos][p.n_dims / 2]: what
+// every rotation of those tokens with these parameters uses (prefill: all heads of Q and K of every
+// layer), formed once
+void launch_rope_table(const int32_t * pos, int64_t n_pos, const rope_params & p, const float * ff, float2 * out, hipStream_t st);
 
 void launch_soft_max(const tview & a, const tview * mask, const tview & dst, float scale, float max_bias, hipStream_t st);
 // dst = silu(gate) * up (2-D f32 views), with its Q8_0 (q) or Q8_K (qk) quantization when set
