@@ -1211,7 +1211,7 @@ private:
         if (mc) {
             if (act_.count(x) && act_.at(x).kind == kind) {
                 xa = &act_.at(x);
-            } else if (nz != norm_.end() && K <= gemv_prologue_max_k(wtype, nz->second.rms != 0)) {
+            } else if (nz != norm_.end() && K <= act_quant_max_k(wtype, nz->second.rms != 0)) {
                 act_entry e = alloc_act(kind, K, ggml_nrows(x));
                 gemv_launch Q{};
                 Q.type = wtype;
@@ -1314,9 +1314,15 @@ private:
             S.m[0].y_stride = (int64_t) (mn->nb[1] / sizeof(float));
             S.m[0].add = nullptr;
             sb -= (double) (g_->nodes[gate]->ne[0] * ncols * 4); // gate/up outputs are not written, act is
-            // the GEMVs reading act (the down projection) quantize it in their prologue
+            // the GEMVs reading act (the down projection): Q8_0 consumers read it pre-quantized, the
+            // launch writing its blocks; others quantize it in their prologue
             const int dtype = fuse(FUSE_ACTQ) && !mc ? gemv_only_consumers(mulnode) : -1;
-            if (dtype >= 0 && mn->ne[0] <= gemv_prologue_max_k(dtype, false) && ((uintptr_t) mn->data) % 16 == 0) {
+            if (dtype >= 0 && dot_kind(dtype) == 1 && gemv_q_supported(S) && K <= GEMV_SWIGLU_QOUT_MAX_K && mn->ne[0] % 32 == 0 &&
+                is_2d_contig(mn)) {
+                act_entry e = alloc_act(1, mn->ne[0], ggml_nrows(mn));
+                S.out_q = e.q8;
+                act_[mn] = e;
+            } else if (dtype >= 0 && mn->ne[0] <= gemv_prologue_max_k(dtype, false) && ((uintptr_t) mn->data) % 16 == 0) {
                 norm_[mn] = gemv_norm{ (const float *) mn->data, (int64_t) (mn->nb[1] / sizeof(float)), nullptr, 0.0f, 0 };
             }
             {

@@ -78,6 +78,41 @@ __device__ __forceinline__ float group_max(float v) {
     return v;
 }
 
+// DPP lane exchanges (v_mov_dpp): quad_perm xor 1 (0xB1) and xor 2 (0x4E), row_half_mirror (0x141:
+// lane i <-> 7 - i within 8 lanes), row_mirror (0x140: i <-> 15 - i within 16). One VALU op each,
+// where __shfl_xor goes through ds_bpermute (an LDS round trip). Every lane of the groups involved
+// must be active.
+template <int CTRL> __device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+template <int CTRL> __device__ __forceinline__ double dpp_d(double v) {
+    const int lo = dpp_i<CTRL>(__double2loint(v)), hi = dpp_i<CTRL>(__double2hiint(v));
+    return __hiloint2double(hi, lo);
+}
+// max / sum over aligned groups of 8 lanes (every lane gets the result)
+__device__ __forceinline__ float max8_dpp(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    return fmaxf(v, dpp_f<0x141>(v));
+}
+__device__ __forceinline__ int sum8_dpp(int v) {
+    v += dpp_i<0xB1>(v);
+    v += dpp_i<0x4E>(v);
+    return v + dpp_i<0x141>(v);
+}
+// sum of a double over the wave: exchanges within each row of 16 lanes, then the four row sums
+// added in row order (uniform result)
+__device__ __forceinline__ double wave_sum_d_dpp(double v) {
+    v += dpp_d<0xB1>(v);
+    v += dpp_d<0x4E>(v);
+    v += dpp_d<0x141>(v);
+    v += dpp_d<0x140>(v);
+    const int lo = __double2loint(v), hi = __double2hiint(v);
+    double r[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) r[k] = __hiloint2double(__builtin_amdgcn_readlane(hi, 16 * k), __builtin_amdgcn_readlane(lo, 16 * k));
+    return ((r[0] + r[1]) + r[2]) + r[3];
+}
+
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 // Transcendentals of the float ops are evaluated in double and rounded once, i.e. the correctly

@@ -458,7 +458,7 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const gemv_launch L, q8_
 }
 
 void launch_act_quant(const gemv_launch & L, const q8_act & q8, const q8k_act & q8k, hipStream_t st) {
-    if (!L.norm.x || L.K > gemv_prologue_max_k(L.type, L.norm.rms != 0)) HIP_ABORT("act_quant: K=%d unsupported", L.K);
+    if (!L.norm.x || L.K > act_quant_max_k(L.type, L.norm.rms != 0)) HIP_ABORT("act_quant: K=%d unsupported", L.K);
     switch (L.type) {
         case GGML_TYPE_Q4_0: case GGML_TYPE_Q8_0:
             launch(act_quant_kernel<GGML_TYPE_Q4_0>, dim3(L.ncols), dim3(256), gemv_lds_bytes<GGML_TYPE_Q4_0>(L.K, 0, 0), st, L, q8, q8k);
@@ -808,10 +808,12 @@ void launch_gemv(const gemv_launch & L, hipStream_t st) {
     if (L.swiglu && (L.n_mats != 2 || L.m[0].n_rows != L.m[1].n_rows)) HIP_ABORT("gemv: swiglu needs two equal matrices");
     if (L.ids && (L.n_slots < 1 || L.x_cols < 1 || L.n_experts < 1 || L.ncols % L.n_slots)) HIP_ABORT("gemv: bad mul_mat_id geometry");
     if (L.norm.x) {
-        const int max_k = gemv_prologue_max_k(L.type, L.norm.rms != 0);
+        const int max_k = act_quant_max_k(L.type, L.norm.rms != 0);
         if (L.K > max_k) HIP_ABORT("gemv: the activation prologue handles K <= %d (K=%d)", max_k, L.K);
         if (((uintptr_t) L.norm.x | (uintptr_t) L.norm.w) % 16 || L.norm.x_stride % 4) HIP_ABORT("gemv: RMSNorm prologue operands must be 16-byte aligned");
     }
+    if (gemv_q_supported(L)) return launch_gemv_q(L, st);
+    if (L.out_q.qs) HIP_ABORT("gemv: quantized SwiGLU output needs the Q4_0 / Q8_0 kernel");
     switch (L.type) {
         case GGML_TYPE_Q4_0:
             if (L.K % 32 || L.K > GEMV_MAX_K) HIP_ABORT("gemv q4_0: K=%d unsupported", L.K);

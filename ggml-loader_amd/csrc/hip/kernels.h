@@ -109,11 +109,20 @@ struct gemv_norm {
     int           rms;
 };
 
-// largest K of the prologue: with rms, one 32-element Q8_0 block or one 16-element Q8_K group per
-// thread of a 256-thread workgroup; without, up to 8 of them per thread
-constexpr int gemv_prologue_max_k(int type, bool rms) {
+// largest K the act_quant kernel (and the Q4_K GEMV's prologue) handles: with rms, one 32-element
+// Q8_0 block or one 16-element Q8_K group per thread of a 256-thread workgroup; without, up to 8 of
+// them per thread
+constexpr int act_quant_max_k(int type, bool rms) {
     return (type == 12 /* GGML_TYPE_Q4_K */ ? 16 : 32) * 256 * (rms ? 1 : 8);
 }
+// largest K a GEMV's activation prologue handles: the Q4_0 / Q8_0 kernel holds up to 2 (rms) or 4
+// float4 chunks per thread of a 512-thread workgroup
+constexpr int gemv_prologue_max_k(int type, bool rms) {
+    return type == 12 /* GGML_TYPE_Q4_K */ ? act_quant_max_k(type, rms) : (rms ? 4096 : 8192);
+}
+// SwiGLU launches that quantize act for the down projection (out_q): 32 rows per workgroup of 1024
+// threads, K up to 4096
+constexpr int GEMV_SWIGLU_QOUT_MAX_K = 4096;
 // longest row of the register-resident rms_norm kernel (32 elements per thread); longer rows go
 // through the strided kernel
 constexpr int RMS_NORM_MAX_ROW = 256 * 32;
@@ -142,9 +151,16 @@ struct gemv_launch {
     int64_t    expert_rows;
     // SwiGLU epilogue: m[0] = gate, m[1] = up (same n_rows); writes act = silu(g) * u to m[0].y
     bool       swiglu;
+    // with swiglu (Q4_0 / Q8_0 weights, n_rows % 32 == 0, K <= GEMV_SWIGLU_QOUT_MAX_K): act also
+    // quantized to Q8_0 here (quantize_row_q8_0 semantics; column c's blocks at +c * n_rows), for a
+    // down projection that reads it pre-quantized
+    q8_act     out_q;
 };
 
 void launch_gemv(const gemv_launch & L, hipStream_t st);
+// the single-column Q4_0 / Q8_0 kernel (k_gemv_q.hip), which launch_gemv uses when this holds
+bool gemv_q_supported(const gemv_launch & L);
+void launch_gemv_q(const gemv_launch & L, hipStream_t st);
 // Several activation columns per workgroup (k_gemv_mc.hip): each weight row block is read once for
 // up to GEMV_MC_MAX_COLS columns; the activation must be quantized already (L.xq, no L.norm). With
 // groups (mul_mat_id): the workgroups of expert e take the columns the ids route to e, listed by
