@@ -88,6 +88,8 @@ template <int CTRL> __device__ __forceinline__ double dpp_d(double v) {
     const int lo = dpp_i<CTRL>(__double2loint(v)), hi = dpp_i<CTRL>(__double2hiint(v));
     return __hiloint2double(hi, lo);
 }
+// the value of v in lane l (uniform)
+__device__ __forceinline__ float lane_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
 // max / sum over aligned groups of 8 lanes (every lane gets the result)
 __device__ __forceinline__ float max8_dpp(float v) {
     v = fmaxf(v, dpp_f<0xB1>(v));

@@ -121,9 +121,10 @@ __host__ __device__ constexpr int scores_dyn_floats(int n_q) {
 template <int HD, int G>
 __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_launch A) {
     constexpr int HD2 = HD / 2;
-    constexpr int STRIDE = HD2 + 1;
-    __shared__ uint32_t s_k[ATT_CHUNK * STRIDE];
-    extern __shared__ float s_dyn[];
+    constexpr int STRIDE = HD2 + 4;   // dwords per staged K row: 16-byte aligned, rows offset by 4 banks
+    __shared__ __align__(16) uint32_t s_k[ATT_CHUNK * STRIDE];
+    __shared__ float s_cm[ATT_WAVES][ATT_MAX_Q * 8];
+    extern __shared__ __align__(16) float s_dyn[];
     // blockIdx.y: a group of G consecutive heads (all heads of KV head kvh, or a part of them when
     // the launch splits a large GQA group over several workgroups); h0 its first head
     const int split = blockIdx.x, h0 = blockIdx.y * G, kvh = h0 / (A.n_head / A.n_head_kv);
@@ -290,31 +291,59 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
     }
     __syncthreads();
 
-    for (int pr = wave; pr < n_q * G; pr += ATT_WAVES) {
-        const int q = pr / G, g = pr % G, h = h0 + g;
-        float sv = -INFINITY;
-        if (lane < nt) {
-            const uint32_t * kr = s_k + lane * STRIDE;
-            const float * qv2 = s_q + pr * HD;
-            // four independent chains (the sums are exact for these operands, so their order
-            // does not change the result)
-            double acc4[4] = { 0.0, 0.0, 0.0, 0.0 };
-#pragma unroll 8
-            for (int d2 = 0; d2 < HD2; d2++) {
-                const __half2 k2 = *(const __half2 *) &kr[d2];
-                const float2 kf = __half22float2(k2);
-                acc4[(2 * d2) % 4] += (double) (kf.x * qv2[2 * d2]);
-                acc4[(2 * d2 + 1) % 4] += (double) (kf.y * qv2[2 * d2 + 1]);
-            }
-            const double acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
-            // softmax input as the graph forms it: (float) kq * scale + mask
-            const float s = (float) acc * A.scale + (mask32 ? s_mk[q * ATT_CHUNK + lane] : mask_at(A, q0 + q, t0 + lane));
-            S.scores[((int64_t) (q0 + q) * A.n_head + h) * A.n_kv + t0 + lane] = s;
-            sv = s;
+    // ---- dots: wave w takes positions 16w .. 16w + 15 of the chunk; lane = (position, quarter of
+    // the head dims). The lane's K slice stays in registers for every (query, head) row of the
+    // group; products of two F16 values are exact in f32 and their sum accumulates in double (exact
+    // for these operands, so splitting it over chains and quarters does not change it), then the
+    // four quarters are added by DPP within each quad of lanes. ----
+    constexpr int DQ = HD / 4;                          // dims per lane
+    const int pi = lane / 4, dq = lane % 4;
+    const int tl = wave * 16 + pi;                      // position in the chunk
+    const bool ok = tl < nt;
+    uint32_t kk[DQ / 2];
+    {
+        const uint4 * kp = (const uint4 *) (s_k + tl * STRIDE + dq * (DQ / 2));
+#pragma unroll
+        for (int j = 0; j < DQ / 8; j++) {
+            const uint4 v = kp[j];
+            kk[4 * j] = v.x; kk[4 * j + 1] = v.y; kk[4 * j + 2] = v.z; kk[4 * j + 3] = v.w;
         }
-        // the chunk's maximum of the row, for the statistics
-        sv = wave_max(sv);
-        if (lane == 0) S.cmax[((int64_t) (q0 + q) * A.n_head + h) * attn_chunks(A.n_kv) + split] = sv;
+    }
+    for (int pr = 0; pr < n_q * G; pr++) {
+        const int q = pr / G, h = h0 + pr % G;
+        const float4 * qv = (const float4 *) (s_q + pr * HD + dq * DQ);
+        double a[4] = { 0.0, 0.0, 0.0, 0.0 };
+#pragma unroll
+        for (int j = 0; j < DQ / 4; j++) {
+            const float4 q4 = qv[j];
+            const float2 k01 = __half22float2(*(const __half2 *) &kk[2 * j]);
+            const float2 k23 = __half22float2(*(const __half2 *) &kk[2 * j + 1]);
+            a[0] += (double) (k01.x * q4.x);
+            a[1] += (double) (k01.y * q4.y);
+            a[2] += (double) (k23.x * q4.z);
+            a[3] += (double) (k23.y * q4.w);
+        }
+        double dot = (a[0] + a[1]) + (a[2] + a[3]);
+        dot += dpp_d<0xB1>(dot);
+        dot += dpp_d<0x4E>(dot);
+        // softmax input as the graph forms it: (float) kq * scale + mask
+        float sv = -INFINITY;
+        if (ok) {
+            sv = (float) dot * A.scale + (mask32 ? s_mk[q * ATT_CHUNK + tl] : mask_at(A, q0 + q, t0 + tl));
+            if (dq == 0) S.scores[((int64_t) (q0 + q) * A.n_head + h) * A.n_kv + t0 + tl] = sv;
+        }
+        // the row's maximum over this wave's 16 positions (every lane of a quad holds its value)
+        sv = fmaxf(sv, dpp_f<0x141>(sv));
+        sv = fmaxf(sv, dpp_f<0x140>(sv));
+        sv = fmaxf(fmaxf(lane_f(sv, 0), lane_f(sv, 16)), fmaxf(lane_f(sv, 32), lane_f(sv, 48)));
+        if (lane == 0) s_cm[wave][pr] = sv;
+    }
+    __syncthreads();
+    // the chunk's maximum of each row, for the statistics
+    if (t < n_q * G) {
+        const int q = t / G, h = h0 + t % G;
+        const float m = fmaxf(fmaxf(s_cm[0][t], s_cm[1][t]), fmaxf(s_cm[2][t], s_cm[3][t]));
+        S.cmax[((int64_t) (q0 + q) * A.n_head + h) * attn_chunks(A.n_kv) + split] = m;
     }
 }
 
@@ -358,85 +387,135 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_laun
     }
 }
 
+// rows (query, head) of one PV workgroup: at most 8 (launch_attn_t picks the queries per workgroup)
+constexpr int PV_MAX_ROWS = 8;
+constexpr int PV_NP = PV_CHUNK / ATT_WAVES;               // positions per wave
+constexpr int PV_SC = (PV_MAX_ROWS * PV_CHUNK + ATT_THREADS - 1) / ATT_THREADS;   // scores per thread
+
+template <int HD>
+constexpr int pv_lds_bytes() {
+    // [V chunk: PV_CHUNK][HD / 2] dwords, reused for the waves' partials [4][PV_MAX_ROWS][HD] doubles
+    return (PV_CHUNK * HD * 2 > ATT_WAVES * PV_MAX_ROWS * HD * 8 ? PV_CHUNK * HD * 2 : ATT_WAVES * PV_MAX_ROWS * HD * 8);
+}
+
 template <int HD, int G>
-__global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch A) {
+__global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch A, int pvq) {
     constexpr int HD2 = HD / 2;
-    constexpr int STRIDE = HD2;   // rows read along dims: consecutive lanes, consecutive dwords
-    constexpr int R = ATT_MAX_Q * G;
-    __shared__ uint32_t s_v[PV_CHUNK * STRIDE];
-    __shared__ float s_p[R][PV_CHUNK];
+    constexpr int PIECES = HD / 8;                        // 16-byte pieces per V row
+    constexpr int ITER = PV_CHUNK * PIECES / ATT_THREADS;
+    __shared__ __align__(16) uint8_t s_buf[pv_lds_bytes<HD>()];
+    __shared__ __align__(16) double s_p[PV_MAX_ROWS][PV_CHUNK];
+    __shared__ float s_M[PV_MAX_ROWS], s_inv[PV_MAX_ROWS];
+    uint32_t * s_v = (uint32_t *) s_buf;                  // [PV_CHUNK][HD2]
+    double * s_part = (double *) s_buf;                   // [ATT_WAVES][PV_MAX_ROWS][HD], after the dots
     const int split = blockIdx.x, h0 = blockIdx.y * G, kvh = h0 / (A.n_head / A.n_head_kv);   // as in the scores kernel
-    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int t0 = split * PV_CHUNK;
     const int nt = min(PV_CHUNK, A.n_kv - t0);
-    const int q0 = blockIdx.z * ATT_MAX_Q;            // this workgroup's queries: q0 .. q0 + n_q - 1
-    const int n_rows = min(ATT_MAX_Q, A.n_q - q0) * G;
+    const int q0 = blockIdx.z * pvq;                  // this workgroup's queries: q0 .. q0 + pvq - 1
+    const int n_rows = min(pvq, A.n_q - q0) * G;      // <= PV_MAX_ROWS (pvq = PV_MAX_ROWS / G or 1)
     const attn_scratch S = scratch_of(A);
+    const int nseg = attn_segs(A.n_kv);
+    auto row_of = [&](int pr) { return (int64_t) (q0 + pr / G) * A.n_head + h0 + pr % G; };
 
-    // the V chunk's loads go out first; p is formed while they are in flight
-    constexpr int PIECES = HD / 8;
-    constexpr int ITER = PV_CHUNK * PIECES / ATT_THREADS;
+    // loads, in the order they are needed (they complete in issue order): the chunk's scores of
+    // every row, each row's maximum and segment sums, then the chunk's V rows (16-byte pieces).
+    // Indices clamped, values past the ends unused.
+    float sc[PV_SC];
+#pragma unroll
+    for (int k = 0; k < PV_SC; k++) {
+        const int i = min(t + k * ATT_THREADS, n_rows * PV_CHUNK - 1);
+        const int pr = i / PV_CHUNK, tt = min(i % PV_CHUNK, nt - 1);
+        sc[k] = S.scores[row_of(pr) * A.n_kv + t0 + tt];
+    }
+    float rmax = 0.0f;
+    double ssum = 0.0;
+    if (t < n_rows) {
+        rmax = S.rmax[row_of(t)];
+        for (int k = 0; k < nseg; k++) ssum += S.ssum[row_of(t) * nseg + k];   // segment order
+    }
     uint4 vv[ITER];
     const __half * vbase = A.v + (int64_t) kvh * A.v_nb1;
 #pragma unroll
     for (int it = 0; it < ITER; it++) {
-        const int pc = threadIdx.x + it * ATT_THREADS;
+        const int pc = t + it * ATT_THREADS;
         const int r = pc / PIECES, c = pc % PIECES;
-        vv[it] = make_uint4(0, 0, 0, 0);
-        if (r < nt) vv[it] = *(const uint4 *) (vbase + (int64_t) (t0 + r) * A.v_nb2 + c * 8);
+        vv[it] = *(const uint4 *) (vbase + (int64_t) (t0 + min(r, nt - 1)) * A.v_nb2 + c * 8);
+        if (r >= nt) vv[it] = make_uint4(0, 0, 0, 0);   // padding rows: no term
     }
-    // each row's M and 1/S (S: the segment sums added in segment order)
-    __shared__ float s_M[R], s_inv[R];
-    const int nseg = attn_segs(A.n_kv);
-    if ((int) threadIdx.x < n_rows) {
-        const int pr = threadIdx.x;
-        const int64_t row = (int64_t) (q0 + pr / G) * A.n_head + h0 + pr % G;
-        double tot = 0.0;
-        for (int k = 0; k < nseg; k++) tot += S.ssum[row * nseg + k];
-        s_M[pr] = S.rmax[row];
-        s_inv[pr] = tot > 0.0 ? (float) (1.0 / tot) : 0.0f;
+    if (t < n_rows) {
+        s_M[t] = rmax;
+        s_inv[t] = ssum > 0.0 ? (float) (1.0 / ssum) : 0.0f;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < n_rows * PV_CHUNK; i += ATT_THREADS) {
-        const int pr = i / PV_CHUNK, t = i % PV_CHUNK;
-        const int64_t row = (int64_t) (q0 + pr / G) * A.n_head + h0 + pr % G;
-        float p = 0.0f;
-        if (t < nt) {
-            const float M = s_M[pr], inv = s_inv[pr];
-            const float e = M == -INFINITY ? 0.0f : exp_cr(S.scores[row * A.n_kv + t0 + t] - M);
-            p = __half2float(__float2half_rn(as_f32(e * inv)));
+    // p = F16(exp(s - M) * (1/S)) for the chunk's positions (0 past the end), kept as doubles
+#pragma unroll
+    for (int k = 0; k < PV_SC; k++) {
+        const int i = t + k * ATT_THREADS;
+        if (i < n_rows * PV_CHUNK) {
+            const int pr = i / PV_CHUNK, tt = i % PV_CHUNK;
+            float p = 0.0f;
+            if (tt < nt) {
+                const float M = s_M[pr];
+                const float e = M == -INFINITY ? 0.0f : exp_cr(sc[k] - M);
+                p = __half2float(__float2half_rn(as_f32(e * s_inv[pr])));
+            }
+            s_p[pr][tt] = (double) p;
         }
-        s_p[pr][t] = p;
     }
 #pragma unroll
     for (int it = 0; it < ITER; it++) {
-        const int pc = threadIdx.x + it * ATT_THREADS;
+        const int pc = t + it * ATT_THREADS;
         const int r = pc / PIECES, c = pc % PIECES;
-        uint32_t * d = s_v + r * STRIDE + c * 4;
+        uint32_t * d = s_v + r * HD2 + c * 4;
         d[0] = vv[it].x; d[1] = vv[it].y; d[2] = vv[it].z; d[3] = vv[it].w;
     }
     __syncthreads();
 
-    for (int pr = wave; pr < n_rows; pr += ATT_WAVES) {
-        const int q = q0 + pr / G, h = h0 + pr % G;
-        if (lane < HD2) {
-            // two independent chains per dimension (even and odd positions; exact sums as above;
-            // p is 0 past nt)
-            double a0 = 0.0, a1 = 0.0, b0 = 0.0, b1 = 0.0;
+    // P V over this wave's positions (lane: dims 2 lane, 2 lane + 1): each V value widened once and
+    // multiplied into up to four rows at a time; a product of two F16 values is exact in double, so
+    // fma(p, v, acc) rounds as acc + p*v does (the sums are exact for these operands)
+    const int d2 = min(lane, HD2 - 1);
+    // rows r0 .. r0 + 3 (clamped; rows past n_rows are computed and dropped)
+    auto dot_rows = [&](int r0, double (&acc)[4][2]) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[r][0] = acc[r][1] = 0.0;
 #pragma unroll 4
-            for (int t = 0; t < nt; t += 2) {
-                const float p = s_p[pr][t], pn = s_p[pr][t + 1];
-                const float2 vf = __half22float2(*(const __half2 *) &s_v[t * STRIDE + lane]);
-                const float2 vn = __half22float2(*(const __half2 *) &s_v[(t + 1) * STRIDE + lane]);
-                a0 += (double) (p * vf.x);
-                a1 += (double) (p * vf.y);
-                b0 += (double) (pn * vn.x);
-                b1 += (double) (pn * vn.y);
+        for (int j = 0; j < PV_NP; j++) {
+            const int tt = wave * PV_NP + j;
+            const float2 vf = __half22float2(*(const __half2 *) &s_v[tt * HD2 + d2]);
+            const double v0 = (double) vf.x, v1 = (double) vf.y;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const double p = s_p[min(r0 + r, PV_MAX_ROWS - 1)][tt];
+                acc[r][0] = fma(p, v0, acc[r][0]);
+                acc[r][1] = fma(p, v1, acc[r][1]);
             }
-            double * part = S.parts + (((int64_t) split * A.n_q + q) * A.n_head + h) * HD;
-            part[2 * lane] = a0 + b0;
-            part[2 * lane + 1] = a1 + b1;
         }
+    };
+    double acc_a[4][2], acc_b[4][2];
+    dot_rows(0, acc_a);
+    if (n_rows > 4) dot_rows(4, acc_b);
+    __syncthreads();                                  // every wave is done with the V chunk
+    if (lane < HD2) {
+#pragma unroll
+        for (int r = 0; r < PV_MAX_ROWS; r++) {
+            if (r < n_rows) {
+                const double a0 = r < 4 ? acc_a[r % 4][0] : acc_b[r % 4][0];
+                const double a1 = r < 4 ? acc_a[r % 4][1] : acc_b[r % 4][1];
+                s_part[(wave * PV_MAX_ROWS + r) * HD + 2 * lane] = a0;
+                s_part[(wave * PV_MAX_ROWS + r) * HD + 2 * lane + 1] = a1;
+            }
+        }
+    }
+    __syncthreads();
+    // the chunk's partial of each (row, dim): the waves' sums added in wave order
+    for (int i = t; i < n_rows * HD; i += ATT_THREADS) {
+        const int r = i / HD, d = i % HD;
+        const double v = ((s_part[(0 * PV_MAX_ROWS + r) * HD + d] + s_part[(1 * PV_MAX_ROWS + r) * HD + d]) +
+                          s_part[(2 * PV_MAX_ROWS + r) * HD + d]) + s_part[(3 * PV_MAX_ROWS + r) * HD + d];
+        const int q = q0 + r / G, h = h0 + r % G;
+        S.parts[(((int64_t) split * A.n_q + q) * A.n_head + h) * HD + d] = v;
     }
 }
 
@@ -491,10 +570,17 @@ static void launch_attn_t(const attn_launch & A, hipStream_t st) {
     const int pv_splits = (A.n_kv + PV_CHUNK - 1) / PV_CHUNK;
     const int qz = (A.n_q + ATT_MAX_Q - 1) / ATT_MAX_Q;   // groups of up to ATT_MAX_Q queries
     // G: heads per workgroup (the GQA group, or a part of it); grid.y = head groups
-    launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head / G, qz), dim3(ATT_THREADS),
-           scores_dyn_floats<HD, G>(std::min(A.n_q, ATT_MAX_Q)) * sizeof(float), st, A);
+    const size_t dyn = scores_dyn_floats<HD, G>(std::min(A.n_q, ATT_MAX_Q)) * sizeof(float);
+    static bool big_lds = false;
+    if (dyn > 32768 && !big_lds) {
+        HIP_CHECK(hipFuncSetAttribute((const void *) attn_scores_kernel<HD, G>, hipFuncAttributeMaxDynamicSharedMemorySize, 98304));
+        big_lds = true;
+    }
+    launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head / G, qz), dim3(ATT_THREADS), dyn, st, A);
     launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
-    launch((attn_pv_kernel<HD, G>), dim3(pv_splits, A.n_head / G, qz), dim3(ATT_THREADS), 0, st, A);
+    static_assert(G <= PV_MAX_ROWS, "PV rows");
+    const int pvq = std::max(1, std::min(ATT_MAX_Q, PV_MAX_ROWS / G));   // queries per PV workgroup
+    launch((attn_pv_kernel<HD, G>), dim3(pv_splits, A.n_head / G, (A.n_q + pvq - 1) / pvq), dim3(ATT_THREADS), 0, st, A, pvq);
     launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(2 * HD), 0, st, A, pv_splits);
 }
 
