@@ -199,6 +199,7 @@ def _declare(core, hip, loader):
     _sig(hip, "ggml_backend_hip_get_device_description", None, i32, C.c_char_p, sz)
     _sig(hip, "ggml_backend_hip_init", vp, i32)
     _sig(hip, "ggml_backend_is_hip", C.c_bool, vp)
+    _sig(hip, "ggml_backend_hip_graph_compute_static", i32, vp, vp)
     _sig(hip, "ggml_backend_hip_set_fusion", None, vp, C.c_bool)
     _sig(hip, "ggml_backend_hip_set_graph_replay", None, vp, C.c_bool)
     _sig(hip, "ggml_backend_hip_set_profiling", None, vp, C.c_bool)

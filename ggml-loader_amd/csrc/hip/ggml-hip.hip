@@ -36,10 +36,19 @@ namespace {
 // ---------------------------------------------------------------------------------------------
 // devices
 
+// Scratch of ggml_backend_hip_graph_compute_static: the kernels' partial results (attention
+// scores and partials, quantized activations, expert groups, argmax parts) for callers that cannot
+// allocate. Every GPU the library runs on holds its own copy until the process ends; host code
+// uses the per-device address hipGetSymbolAddress resolves (hip_device::static_scratch), never
+// this name.
+static __device__ __align__(256) uint8_t scratch[GGML_HIP_STATIC_SCRATCH_BYTES];
+
 struct hip_device {
     int id = 0;
     bool ready = false;
     hipStream_t stream = nullptr;
+    // this device's copy of `scratch` (nullptr until resolved at backend init)
+    uint8_t * static_scratch = nullptr;
     // device staging for repacked uploads/downloads
     uint8_t * staging = nullptr;
     size_t staging_size = 0;
@@ -265,13 +274,20 @@ struct prof_entry { int64_t launches = 0; double ms = 0.0; double bytes = 0.0; }
 
 struct pending_event { std::string name; double bytes; hipEvent_t a, b; };
 
+// thrown by a fixed arena (graph_compute_static) when a compute needs more than it holds
+struct scratch_overflow {
+    size_t needed;
+};
+
 struct scratch_arena {
     std::vector<std::pair<uint8_t *, size_t>> chunks;
     size_t chunk = 0, off = 0;
+    bool fixed = false;          // one caller-provided chunk, never grown (no allocation)
     void reset() { chunk = 0; off = 0; }
     void * alloc(size_t size) {
         size = (size + 255) & ~(size_t) 255;
         while (chunk < chunks.size() && off + size > chunks[chunk].second) { chunk++; off = 0; }
+        if (chunk == chunks.size() && fixed) throw scratch_overflow{ chunks.empty() ? size : chunks[0].second + size };
         if (chunk == chunks.size()) {
             const size_t cap = std::max(size, (size_t) 64 << 20);
             uint8_t * p = nullptr;
@@ -284,7 +300,9 @@ struct scratch_arena {
         return r;
     }
     void release() {
-        for (auto & c : chunks) HIP_CHECK(hipFree(c.first));
+        if (!fixed) {
+            for (auto & c : chunks) HIP_CHECK(hipFree(c.first));
+        }
         chunks.clear();
         reset();
     }
@@ -1793,6 +1811,36 @@ enum ggml_status be_compute(ggml_backend_t b, ggml_cgraph * g) {
     return GGML_STATUS_SUCCESS;
 }
 
+// graph_compute with every kernel's scratch in this device's static array (no allocation)
+enum ggml_status compute_static(hip_backend_ctx * c, ggml_cgraph * g) {
+    hip_device & d = dev(c->device);
+    if (!d.static_scratch) {
+        fprintf(stderr, "ggml-hip: graph_compute_static: the static scratch of device %d is not resolved\n", c->device);
+        return GGML_STATUS_FAILED;
+    }
+    if (c->profiling) {
+        fprintf(stderr, "ggml-hip: graph_compute_static: profiling creates events; turn it off first\n");
+        return GGML_STATUS_FAILED;
+    }
+    scratch_arena own = std::move(c->scratch);
+    c->scratch = scratch_arena{};
+    c->scratch.fixed = true;
+    c->scratch.chunks.push_back({ d.static_scratch, (size_t) GGML_HIP_STATIC_SCRATCH_BYTES });
+    enum ggml_status st = GGML_STATUS_SUCCESS;
+    try {
+        executor ex(*c, g);
+        ex.run();
+    } catch (const scratch_overflow & o) {
+        fprintf(stderr, "ggml-hip: graph_compute_static: the graph needs more than %d bytes of scratch (at least %zu)\n",
+                GGML_HIP_STATIC_SCRATCH_BYTES, o.needed);
+        st = GGML_STATUS_ALLOC_FAILED;
+    }
+    HIP_CHECK(hipStreamSynchronize(d.stream));
+    drained(d);
+    c->scratch = std::move(own);
+    return st;
+}
+
 void be_set_eval_callback(ggml_backend_t b, ggml_backend_eval_callback cb, void * user) {
     hip_backend_ctx * c = (hip_backend_ctx *) b->context;
     c->cb = cb;
@@ -1841,7 +1889,16 @@ ggml_backend_buffer_type_t ggml_backend_hip_buffer_type(int device) {
 
 ggml_backend_t ggml_backend_hip_init(int device) {
     if (device < 0 || device >= device_count()) return nullptr;
-    dev(device);
+    hip_device & d = dev(device);   // makes the device current
+    if (!d.static_scratch) {
+        void * p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            fprintf(stderr, "ggml-hip: device %d: no address for the static scratch (%s)\n", device, hipGetErrorString(e));
+            return nullptr;
+        }
+        d.static_scratch = (uint8_t *) p;
+    }
     ggml_backend_hip_buffer_type(device);
     hip_backend_ctx * c = new hip_backend_ctx();
     c->device = device;
@@ -1859,6 +1916,11 @@ ggml_backend_t ggml_backend_hip_init(int device) {
 }
 
 bool ggml_backend_is_hip(ggml_backend_t backend) { return backend && backend->iface.graph_compute == be_compute; }
+
+enum ggml_status ggml_backend_hip_graph_compute_static(ggml_backend_t backend, struct ggml_cgraph * cgraph) {
+    if (!ggml_backend_is_hip(backend) || !cgraph) return GGML_STATUS_FAILED;
+    return compute_static((hip_backend_ctx *) backend->context, cgraph);
+}
 
 void ggml_backend_hip_set_fusion(ggml_backend_t backend, bool enable) {
     if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->fusion = enable;

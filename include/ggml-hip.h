@@ -24,6 +24,21 @@ GGML_API ggml_backend_buffer_type_t ggml_backend_hip_buffer_type(int device);
 
 // ---- extensions of this backend (no counterpart in the reference) ----
 
+// Bytes of device scratch ggml_backend_hip_graph_compute_static can give a graph's kernels.
+#define GGML_HIP_STATIC_SCRATCH_BYTES (64 << 20)
+
+// ggml_backend_graph_compute without any device allocation: no counterpart in the reference; for
+// callers that cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid
+// hipMalloc). The kernels' scratch (attention scores and partials, quantized activations, expert
+// groups, argmax parts) comes from a file-scope device array of GGML_HIP_STATIC_SCRATCH_BYTES
+// that every GPU the library runs on holds until the process ends; the graph's tensors are the
+// caller's as with ggml_backend_graph_compute, and the result is the same. A graph needing more
+// scratch is rejected with GGML_STATUS_ALLOC_FAILED and a message (kernels enqueued before the
+// point where the arena ran out have run; the outputs are undefined). Calls share their GPU's
+// array and keep its last contents (no kernel relies on it starting at zero): calls that overlap
+// on one GPU (several threads or backends) race. Fails with profiling on (it creates events).
+GGML_API enum ggml_status ggml_backend_hip_graph_compute_static(ggml_backend_t backend, struct ggml_cgraph * cgraph);
+
 // Graph-level fusion (fused norm+quantize, QKV/gate-up multi-GEMV, rope+KV append, split-KV
 // decode attention). On by default; off runs one kernel per ggml node. Used by the parity tests
 // to check both paths against the oracle.
