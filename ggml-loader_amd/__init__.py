@@ -131,6 +131,15 @@ def _declare(core, hip, loader):
     _sig(core, "ggml_flash_attn_ext", T, vp, T, T, T, T, f32, f32, f32)
     _sig(core, "ggml_argmax", T, vp, T)
     _sig(core, "ggml_div", T, vp, T, T)
+    _sig(core, "ggml_sub", T, vp, T, T)
+    _sig(core, "ggml_abs", T, vp, T)
+    _sig(core, "ggml_softplus", T, vp, T)
+    _sig(core, "ggml_l2_norm", T, vp, T, f32)
+    _sig(core, "ggml_concat", T, vp, T, T, i32)
+    _sig(core, "ggml_swiglu_split", T, vp, T, T)
+    _sig(core, "ggml_ssm_conv", T, vp, T, T)
+    _sig(core, "ggml_ssm_scan", T, vp, T, T, T, T, T, T, T, i32)
+    _sig(core, "ggml_gated_delta_net", T, vp, T, T, T, T, T, T, i32)
     _sig(core, "ggml_sum_rows", T, vp, T)
     _sig(core, "ggml_argsort", T, vp, T, i32)
     _sig(core, "ggml_top_k", T, vp, T, i32)
@@ -193,7 +202,7 @@ def _declare(core, hip, loader):
     _sig(core, "gguf_get_tensor_offset", sz, vp, i64)
     _sig(core, "gguf_get_tensor_size", sz, vp, i64)
     _sig(core, "gguf_get_tensor_n_dims", i32, vp, i64)
-    _sig(core, "gguf_get_tensor_ne", i64, vp, i64, i32)
+    _sig(core, "gguf_get_tensor_ne", C.POINTER(C.c_int64), vp, i64)
 
     _sig(hip, "ggml_backend_hip_get_device_count", i32)
     _sig(hip, "ggml_backend_hip_get_device_description", None, i32, C.c_char_p, sz)

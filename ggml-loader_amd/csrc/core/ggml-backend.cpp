@@ -1,6 +1,7 @@
 // ggml-backend.cpp — backend-independent half of the backend API: buffer/tensor plumbing,
 // context allocation (ggml_backend_alloc_ctx_tensors) and the backend registry.
 #include "ggml-backend-impl.h"
+#include "ggml-vulkan.h"
 
 #include <cstdio>
 #include <dlfcn.h>
@@ -193,6 +194,18 @@ bool ggml_backend_load(const char * path) {
 }
 
 size_t ggml_backend_reg_count(void) { std::lock_guard<std::mutex> lk(reg_mutex()); return reg_list().size(); }
+
+// ggml-vulkan.h: this build has no Vulkan backend (model.cpp:800-813 then reports that no Vulkan
+// device is available)
+int ggml_backend_vk_get_device_count(void) { return 0; }
+void ggml_backend_vk_get_device_description(int device, char * description, size_t description_size) {
+    (void) device;
+    if (description && description_size) description[0] = '\0';
+}
+ggml_backend_t ggml_backend_vk_init(size_t dev_num) {
+    (void) dev_num;
+    return nullptr;
+}
 const char * ggml_backend_reg_name(size_t i) {
     std::lock_guard<std::mutex> lk(reg_mutex());
     return i < reg_list().size() ? reg_list()[i].name.c_str() : nullptr;

@@ -86,7 +86,8 @@ const char * ggml_op_name(enum ggml_op op) {
     static const char * names[GGML_OP_COUNT] = {
         "NONE", "DUP", "ADD", "MUL", "SCALE", "SQR", "RMS_NORM", "MUL_MAT", "MUL_MAT_ID", "CPY", "CONT",
         "RESHAPE", "VIEW", "PERMUTE", "TRANSPOSE", "GET_ROWS", "SOFT_MAX", "ROPE", "FLASH_ATTN_EXT",
-        "ARGMAX", "UNARY", "DIV", "SUM_ROWS", "ARGSORT",
+        "ARGMAX", "UNARY", "DIV", "SUM_ROWS", "ARGSORT", "SUB", "CONCAT", "L2_NORM", "GLU", "SSM_CONV",
+        "SSM_SCAN", "GATED_DELTA_NET",
     };
     return ((int) op >= 0 && op < GGML_OP_COUNT) ? names[op] : "?";
 }
@@ -433,6 +434,73 @@ static ggml_tensor * binary_op(ggml_context * ctx, ggml_tensor * a, ggml_tensor 
 struct ggml_tensor * ggml_mul(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b) { return binary_op(ctx, a, b, GGML_OP_MUL); }
 struct ggml_tensor * ggml_add(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b) { return binary_op(ctx, a, b, GGML_OP_ADD); }
 struct ggml_tensor * ggml_div(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b) { return binary_op(ctx, a, b, GGML_OP_DIV); }
+struct ggml_tensor * ggml_sub(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b) { return binary_op(ctx, a, b, GGML_OP_SUB); }
+
+struct ggml_tensor * ggml_l2_norm(struct ggml_context * ctx, struct ggml_tensor * a, float eps) {
+    ggml_tensor * r = ggml_dup_tensor(ctx, a);
+    set_op_param_f32(r, 0, eps);
+    r->op = GGML_OP_L2_NORM;
+    r->src[0] = a;
+    return r;
+}
+
+struct ggml_tensor * ggml_concat(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b, int dim) {
+    GGML_CHECK(dim >= 0 && dim < GGML_MAX_DIMS && a->type == b->type);
+    int64_t ne[GGML_MAX_DIMS];
+    for (int d = 0; d < GGML_MAX_DIMS; d++) {
+        if (d == dim) {
+            ne[d] = a->ne[d] + b->ne[d];
+        } else {
+            GGML_CHECK(a->ne[d] == b->ne[d]);
+            ne[d] = a->ne[d];
+        }
+    }
+    ggml_tensor * r = ggml_new_tensor(ctx, a->type, GGML_MAX_DIMS, ne);
+    set_op_param_i32(r, 0, dim);
+    r->op = GGML_OP_CONCAT;
+    r->src[0] = a;
+    r->src[1] = b;
+    return r;
+}
+
+struct ggml_tensor * ggml_swiglu_split(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b) {
+    GGML_CHECK(ggml_are_same_shape(a, b));
+    ggml_tensor * r = ggml_dup_tensor(ctx, a);
+    set_op_param_i32(r, 0, GGML_GLU_OP_SWIGLU);
+    r->op = GGML_OP_GLU;
+    r->src[0] = a;
+    r->src[1] = b;
+    return r;
+}
+
+struct ggml_tensor * ggml_ssm_conv(struct ggml_context * ctx, struct ggml_tensor * sx, struct ggml_tensor * c) {
+    GGML_CHECK(sx->ne[1] == c->ne[1] && sx->ne[0] >= c->ne[0] - 1);
+    const int64_t n_t = sx->ne[0] - c->ne[0] + 1;
+    ggml_tensor * r = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, c->ne[1], n_t, sx->ne[2]);
+    r->op = GGML_OP_SSM_CONV;
+    r->src[0] = sx;
+    r->src[1] = c;
+    return r;
+}
+
+struct ggml_tensor * ggml_ssm_scan(struct ggml_context * ctx, struct ggml_tensor * s, struct ggml_tensor * x,
+        struct ggml_tensor * dt, struct ggml_tensor * A, struct ggml_tensor * B, struct ggml_tensor * C,
+        struct ggml_tensor * ids, int version) {
+    ggml_tensor * r = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, ggml_nelements(x) + ggml_nelements(s));
+    set_op_param_i32(r, 0, version);
+    r->op = GGML_OP_SSM_SCAN;
+    r->src[0] = s; r->src[1] = x; r->src[2] = dt; r->src[3] = A; r->src[4] = B; r->src[5] = C; r->src[6] = ids;
+    return r;
+}
+
+struct ggml_tensor * ggml_gated_delta_net(struct ggml_context * ctx, struct ggml_tensor * q, struct ggml_tensor * k,
+        struct ggml_tensor * v, struct ggml_tensor * g, struct ggml_tensor * beta, struct ggml_tensor * state, int version) {
+    ggml_tensor * r = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, ggml_nelements(v) + ggml_nelements(state));
+    set_op_param_i32(r, 0, version);
+    r->op = GGML_OP_GATED_DELTA_NET;
+    r->src[0] = q; r->src[1] = k; r->src[2] = v; r->src[3] = g; r->src[4] = beta; r->src[5] = state;
+    return r;
+}
 
 struct ggml_tensor * ggml_scale(struct ggml_context * ctx, struct ggml_tensor * a, float s) {
     ggml_tensor * r = ggml_dup_tensor(ctx, a);
@@ -663,6 +731,8 @@ struct ggml_tensor * ggml_unary(struct ggml_context * ctx, struct ggml_tensor * 
 struct ggml_tensor * ggml_silu(struct ggml_context * ctx, struct ggml_tensor * a) { return ggml_unary(ctx, a, GGML_UNARY_OP_SILU); }
 struct ggml_tensor * ggml_relu(struct ggml_context * ctx, struct ggml_tensor * a) { return ggml_unary(ctx, a, GGML_UNARY_OP_RELU); }
 struct ggml_tensor * ggml_sigmoid(struct ggml_context * ctx, struct ggml_tensor * a) { return ggml_unary(ctx, a, GGML_UNARY_OP_SIGMOID); }
+struct ggml_tensor * ggml_abs(struct ggml_context * ctx, struct ggml_tensor * a) { return ggml_unary(ctx, a, GGML_UNARY_OP_ABS); }
+struct ggml_tensor * ggml_softplus(struct ggml_context * ctx, struct ggml_tensor * a) { return ggml_unary(ctx, a, GGML_UNARY_OP_SOFTPLUS); }
 enum ggml_unary_op ggml_get_unary_op(const struct ggml_tensor * t) { return (enum ggml_unary_op) t->op_params[0]; }
 
 struct ggml_tensor * ggml_flash_attn_ext(struct ggml_context * ctx, struct ggml_tensor * q, struct ggml_tensor * k,

@@ -320,10 +320,7 @@ const char * gguf_get_tensor_name(const struct gguf_context * c, int64_t id) { r
 enum ggml_type gguf_get_tensor_type(const struct gguf_context * c, int64_t id) { return tinfo(c, id).type; }
 size_t gguf_get_tensor_size(const struct gguf_context * c, int64_t id) { return tinfo(c, id).size; }
 int gguf_get_tensor_n_dims(const struct gguf_context * c, int64_t id) { return tinfo(c, id).n_dims; }
-int64_t gguf_get_tensor_ne(const struct gguf_context * c, int64_t id, int dim) {
-    if (dim < 0 || dim >= GGML_MAX_DIMS) fail("dim out of range", nullptr);
-    return tinfo(c, id).ne[dim];
-}
+const int64_t * gguf_get_tensor_ne(const struct gguf_context * c, int64_t id) { return tinfo(c, id).ne; }
 
 // ---- writer ----
 

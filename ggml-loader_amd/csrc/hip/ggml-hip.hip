@@ -606,6 +606,26 @@ private:
             case GGML_OP_ADD: { prof_scope ps(this, "add", 0); launch_binary(0, tv(n->src[0]), tv(n->src[1]), tv(n), st_); return; }
             case GGML_OP_MUL: { prof_scope ps(this, "mul", 0); launch_binary(1, tv(n->src[0]), tv(n->src[1]), tv(n), st_); return; }
             case GGML_OP_DIV: { prof_scope ps(this, "div", 0); launch_binary(2, tv(n->src[0]), tv(n->src[1]), tv(n), st_); return; }
+            case GGML_OP_SUB: { prof_scope ps(this, "sub", 0); launch_binary(3, tv(n->src[0]), tv(n->src[1]), tv(n), st_); return; }
+            case GGML_OP_L2_NORM: {
+                float eps;
+                memcpy(&eps, n->op_params, 4);
+                prof_scope ps(this, "l2_norm", 0);
+                launch_l2_norm(tv(n->src[0]), tv(n), eps, st_);
+                return;
+            }
+            case GGML_OP_CONCAT: {
+                if (n->type != GGML_TYPE_F32 && n->type != GGML_TYPE_F16 && n->type != GGML_TYPE_I32) HIP_ABORT("concat of type %d", n->type);
+                prof_scope ps(this, "concat", 0);
+                launch_concat(tv(n->src[0]), tv(n->src[1]), tv(n), n->op_params[0], st_);
+                return;
+            }
+            case GGML_OP_GLU: {
+                if (n->op_params[0] != GGML_GLU_OP_SWIGLU) HIP_ABORT("unsupported glu op %d", n->op_params[0]);
+                prof_scope ps(this, "glu", 0);
+                launch_glu(tv(n->src[0]), tv(n->src[1]), tv(n), st_);
+                return;
+            }
             case GGML_OP_SUM_ROWS: { prof_scope ps(this, "sum_rows", 0); launch_sum_rows(tv(n->src[0]), tv(n), st_); return; }
             case GGML_OP_ARGSORT: {
                 prof_scope ps(this, "argsort", 0);
@@ -622,7 +642,8 @@ private:
             case GGML_OP_SQR: { prof_scope ps(this, "sqr", 0); launch_unary(3, 0, tv(n->src[0]), tv(n), st_); return; }
             case GGML_OP_UNARY: {
                 const int u = n->op_params[0];
-                const int op = u == GGML_UNARY_OP_SILU ? 0 : u == GGML_UNARY_OP_RELU ? 1 : u == GGML_UNARY_OP_SIGMOID ? 2 : -1;
+                const int op = u == GGML_UNARY_OP_SILU ? 0 : u == GGML_UNARY_OP_RELU ? 1 : u == GGML_UNARY_OP_SIGMOID ? 2 :
+                               u == GGML_UNARY_OP_ABS ? 5 : u == GGML_UNARY_OP_SOFTPLUS ? 6 : -1;
                 if (op < 0) HIP_ABORT("unsupported unary op %d", u);
                 prof_scope ps(this, "unary", 0);
                 launch_unary(op, 0, tv(n->src[0]), tv(n), st_);

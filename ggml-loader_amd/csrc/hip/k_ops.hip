@@ -182,7 +182,7 @@ __global__ void binary_kernel(int op, tview a, tview b, tview d, int64_t n) {
     const idx4 k = unflatten(i, d.ne);
     const float x = ld(at(a, k.i0, k.i1, k.i2, k.i3), a.type);
     const float y = ld(at(b, k.i0 % b.ne[0], k.i1 % b.ne[1], k.i2 % b.ne[2], k.i3 % b.ne[3]), b.type);
-    st(at(d, k.i0, k.i1, k.i2, k.i3), d.type, op == 0 ? x + y : op == 1 ? x * y : x / y);
+    st(at(d, k.i0, k.i1, k.i2, k.i3), d.type, op == 0 ? x + y : op == 1 ? x * y : op == 3 ? x - y : x / y);
 }
 
 void launch_binary(int op, const tview & a, const tview & b, const tview & dst, hipStream_t st) {
@@ -268,9 +268,71 @@ __global__ void unary_kernel(int op, float s, tview a, tview d, int64_t n) {
         case 1: y = x > 0.0f ? x : 0.0f; break;
         case 2: y = 1.0f / (1.0f + exp_cr(-x)); break;
         case 3: y = x * x; break;
+        case 5: y = fabsf(x); break;
+        case 6: y = x > 20.0f ? x : (float) log1p(exp((double) x)); break;   // softplus, rounded once
         default: y = x * s; break;
     }
     st(at(d, k.i0, k.i1, k.i2, k.i3), d.type, y);
+}
+
+// l2_norm: one wave per row over ne0: the sum of f32 squares in double (exact for these operands
+// in practice, so the order does not matter), scale = 1 / max(sqrtf(sum), eps), y = x * scale
+__global__ void l2_norm_kernel(tview a, tview d, float eps, int64_t rows) {
+    const int64_t r = (int64_t) blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+    const int lane = threadIdx.x % WAVE;
+    if (r >= rows) return;
+    const int64_t i1 = r % a.ne[1], i2 = (r / a.ne[1]) % a.ne[2], i3 = r / (a.ne[1] * a.ne[2]);
+    double sum = 0.0;
+    for (int64_t i0 = lane; i0 < a.ne[0]; i0 += WAVE) {
+        const float x = ld(at(a, i0, i1, i2, i3), a.type);
+        sum += (double) (x * x);
+    }
+    sum = wave_sum_d(sum);
+    const float scale = 1.0f / fmaxf(sqrtf((float) sum), eps);
+    for (int64_t i0 = lane; i0 < a.ne[0]; i0 += WAVE) st(at(d, i0, i1, i2, i3), d.type, ld(at(a, i0, i1, i2, i3), a.type) * scale);
+}
+
+void launch_l2_norm(const tview & a, const tview & dst, float eps, hipStream_t st) {
+    const int64_t rows = a.ne[1] * a.ne[2] * a.ne[3];
+    if (rows == 0) return;
+    launch(l2_norm_kernel, dim3(grid1(rows, 4)), dim3(256), 0, st, a, dst, eps, rows);
+}
+
+// concat along dim: element i of that dim comes from a while i < a.ne[dim], else from b (same types)
+__global__ void concat_kernel(tview a, tview b, tview d, int dim, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const idx4 k = unflatten(i, d.ne);
+    int64_t ix[4] = { k.i0, k.i1, k.i2, k.i3 };
+    const tview * s = &a;
+    if (ix[dim] >= a.ne[dim]) { ix[dim] -= a.ne[dim]; s = &b; }
+    const char * sp = at(*s, ix[0], ix[1], ix[2], ix[3]);
+    char * dp = at(d, k.i0, k.i1, k.i2, k.i3);
+    if (d.type == GGML_TYPE_F32 || d.type == GGML_TYPE_I32) *(uint32_t *) dp = *(const uint32_t *) sp;
+    else *(uint16_t *) dp = *(const uint16_t *) sp;
+}
+
+void launch_concat(const tview & a, const tview & b, const tview & dst, int dim, hipStream_t st) {
+    const int64_t n = nelem(dst);
+    if (n == 0) return;
+    launch(concat_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, a, b, dst, dim, n);
+}
+
+// swiglu_split: silu(a) * b with the silu and mul ops' roundings
+__global__ void glu_kernel(tview a, tview b, tview d, int64_t n) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const idx4 k = unflatten(i, d.ne);
+    const float x = ld(at(a, k.i0, k.i1, k.i2, k.i3), a.type);
+    const float g = ld(at(b, k.i0, k.i1, k.i2, k.i3), b.type);
+    const float sl = x / (1.0f + exp_cr(-x));
+    st(at(d, k.i0, k.i1, k.i2, k.i3), d.type, sl * g);
+}
+
+void launch_glu(const tview & a, const tview & b, const tview & dst, hipStream_t st) {
+    const int64_t n = nelem(dst);
+    if (n == 0) return;
+    launch(glu_kernel, dim3(grid1(n, 256)), dim3(256), 0, st, a, b, dst, n);
 }
 
 // act = silu(gate) * up over 2-D f32 views (the silu and mul ops' roundings), and optionally its

@@ -195,10 +195,16 @@ void launch_rms_norm(const float * x, int64_t x_stride, const float * w, float *
 // generic strided rms_norm over ne0 of every row
 void launch_rms_norm_strided(const tview & x, const tview & y, float eps, hipStream_t st);
 
-// dst = a (op) broadcast(b); op: 0 add, 1 mul
+// dst = a (op) broadcast(b); op: 0 add, 1 mul, 2 div, 3 sub
 void launch_binary(int op, const tview & a, const tview & b, const tview & dst, hipStream_t st);
-// unary: 0 silu, 1 relu, 2 sigmoid, 3 sqr, 4 scale(s)
+// unary: 0 silu, 1 relu, 2 sigmoid, 3 sqr, 4 scale(s), 5 abs, 6 softplus
 void launch_unary(int op, float s, const tview & a, const tview & dst, hipStream_t st);
+// each row over ne0 divided by max(|row|_2, eps) (ggml_l2_norm)
+void launch_l2_norm(const tview & a, const tview & dst, float eps, hipStream_t st);
+// a and b joined along dim (ggml_concat; F32 / F16 / I32)
+void launch_concat(const tview & a, const tview & b, const tview & dst, int dim, hipStream_t st);
+// silu(a) * b (ggml_swiglu_split)
+void launch_glu(const tview & a, const tview & b, const tview & dst, hipStream_t st);
 // element-wise copy with type conversion in row-major element order (shapes may differ)
 void launch_cpy(const tview & src, const tview & dst, hipStream_t st);
 // dst rows = dequantized rows of a selected by I32 ids

@@ -183,7 +183,7 @@ static int cmd_inspect(int argc, char ** argv) {
     }
     for (int64_t i = 0; i < gguf_get_n_tensors(g); i++) {
         printf("  %-40s %-6s [", gguf_get_tensor_name(g, i), ggml_type_name(gguf_get_tensor_type(g, i)));
-        for (int d = 0; d < gguf_get_tensor_n_dims(g, i); d++) printf(d ? ", %lld" : "%lld", (long long) gguf_get_tensor_ne(g, i, d));
+        for (int d = 0; d < gguf_get_tensor_n_dims(g, i); d++) printf(d ? ", %lld" : "%lld", (long long) gguf_get_tensor_ne(g, i)[d]);
         printf("] %zu bytes @ %zu\n", gguf_get_tensor_size(g, i), gguf_get_tensor_offset(g, i));
     }
     gguf_free(g);

@@ -6,12 +6,16 @@
 // free_decode_session (model.cpp:1492).
 #pragma once
 
-#include "ggml-backend.h"
+#include "ggml.h"
 
 #ifdef __cplusplus
 extern "C" {
 #endif
 
+// the buffer-type handle of ggml-backend.h (declared here as well, so that ggml-backend.h can
+// include this header the way the reference's model.h expects: model.h:380 names ggml_gallocr_t
+// with only ggml-backend.h included)
+typedef struct ggml_backend_buffer_type * ggml_backend_buffer_type_t;
 typedef struct ggml_gallocr * ggml_gallocr_t;
 
 GGML_API ggml_gallocr_t ggml_gallocr_new(ggml_backend_buffer_type_t buft);

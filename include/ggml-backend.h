@@ -12,6 +12,7 @@
 #pragma once
 
 #include "ggml.h"
+#include "ggml-alloc.h"
 
 #ifdef __cplusplus
 extern "C" {

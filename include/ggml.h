@@ -97,6 +97,15 @@ enum ggml_op {
     GGML_OP_DIV,
     GGML_OP_SUM_ROWS,
     GGML_OP_ARGSORT,
+    // ops of the reference's other graphs (model.cpp:1156-1295 Mamba2 / gated-delta mixers,
+    // dory.c:722-724): built by the constructors below
+    GGML_OP_SUB,
+    GGML_OP_CONCAT,
+    GGML_OP_L2_NORM,
+    GGML_OP_GLU,
+    GGML_OP_SSM_CONV,
+    GGML_OP_SSM_SCAN,
+    GGML_OP_GATED_DELTA_NET,
     GGML_OP_COUNT,
 };
 
@@ -104,7 +113,13 @@ enum ggml_unary_op {
     GGML_UNARY_OP_RELU = 0,
     GGML_UNARY_OP_SILU,
     GGML_UNARY_OP_SIGMOID,
+    GGML_UNARY_OP_ABS,
+    GGML_UNARY_OP_SOFTPLUS,
     GGML_UNARY_OP_COUNT,
+};
+
+enum ggml_glu_op {
+    GGML_GLU_OP_SWIGLU = 0,
 };
 
 enum ggml_tensor_flag {
@@ -252,6 +267,29 @@ GGML_API struct ggml_tensor * ggml_flash_attn_ext(struct ggml_context * ctx, str
 
 // index of the max of each row (first max wins) -> I32 [a->ne[1]]
 GGML_API struct ggml_tensor * ggml_argmax(struct ggml_context * ctx, struct ggml_tensor * a);
+
+// ---- ops of the reference's other architectures (model.cpp:1156-1295, dory.c:722-724) ----
+// a - b, b repeated over a (like ggml_add)
+GGML_API struct ggml_tensor * ggml_sub(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b);
+GGML_API struct ggml_tensor * ggml_abs(struct ggml_context * ctx, struct ggml_tensor * a);
+// log(1 + exp(x)) (x itself above 20)
+GGML_API struct ggml_tensor * ggml_softplus(struct ggml_context * ctx, struct ggml_tensor * a);
+// each row over ne0 divided by max(|row|_2, eps)
+GGML_API struct ggml_tensor * ggml_l2_norm(struct ggml_context * ctx, struct ggml_tensor * a, float eps);
+// a and b joined along dim (the other extents equal)
+GGML_API struct ggml_tensor * ggml_concat(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b, int dim);
+// silu(a) * b (same shapes)
+GGML_API struct ggml_tensor * ggml_swiglu_split(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b);
+// sx: [d_conv - 1 + n_t, d_inner, n_s], c: [d_conv, d_inner] -> F32 [d_inner, n_t, n_s]
+GGML_API struct ggml_tensor * ggml_ssm_conv(struct ggml_context * ctx, struct ggml_tensor * sx, struct ggml_tensor * c);
+// selective scan: F32 1-D [nelements(x) + nelements(s)], y followed by the new state (model.cpp:1187-1196)
+GGML_API struct ggml_tensor * ggml_ssm_scan(struct ggml_context * ctx, struct ggml_tensor * s, struct ggml_tensor * x,
+        struct ggml_tensor * dt, struct ggml_tensor * A, struct ggml_tensor * B, struct ggml_tensor * C,
+        struct ggml_tensor * ids, int version);
+// gated delta rule: F32 1-D [nelements(v) + nelements(state)], y followed by the new state
+// (model.cpp:1273-1281)
+GGML_API struct ggml_tensor * ggml_gated_delta_net(struct ggml_context * ctx, struct ggml_tensor * q, struct ggml_tensor * k,
+        struct ggml_tensor * v, struct ggml_tensor * g, struct ggml_tensor * beta, struct ggml_tensor * state, int version);
 
 // ---- MoE routing (the router of qwen_model.c:551-606 as graph ops) ----
 enum ggml_sort_order {

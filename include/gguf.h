@@ -87,7 +87,8 @@ GGML_API const char *   gguf_get_tensor_name  (const struct gguf_context * ctx, 
 GGML_API enum ggml_type gguf_get_tensor_type  (const struct gguf_context * ctx, int64_t tensor_id);
 GGML_API size_t         gguf_get_tensor_size  (const struct gguf_context * ctx, int64_t tensor_id);
 GGML_API int            gguf_get_tensor_n_dims(const struct gguf_context * ctx, int64_t tensor_id);
-GGML_API int64_t        gguf_get_tensor_ne    (const struct gguf_context * ctx, int64_t tensor_id, int dim);
+// the tensor's GGML_MAX_DIMS extents (unused dims 1), owned by ctx (cmd_inspect.cpp:76)
+GGML_API const int64_t * gguf_get_tensor_ne   (const struct gguf_context * ctx, int64_t tensor_id);
 
 // ---- writer ----
 GGML_API void gguf_set_val_u8  (struct gguf_context * ctx, const char * key, uint8_t  val);

@@ -40,6 +40,9 @@ static inline float exp_cr(float x) { return (float) exp((double) x); }
 static inline float cos_cr(float x) { return (float) cos((double) x); }
 static inline float sin_cr(float x) { return (float) sin((double) x); }
 static inline float log_cr(float x) { return (float) log((double) x); }
+// softplus (ggml's GGML_UNARY_OP_SOFTPLUS): x above 20, else log(1 + exp(x)), in double rounded
+// once. No reference source or fixture holds this op: parity unpinned beyond its closed form.
+static inline float softplus_cr(float x) { return x > 20.0f ? x : (float) log1p(exp((double) x)); }
 
 /* ------------------------------------------------------------------------------------------ */
 /* binary16 — the branch-free formulation of the FP16 library (fp16_ieee_{from,to}_fp32_value),
@@ -718,7 +721,7 @@ static void op_binary(struct ggml_tensor * dst, const struct ggml_tensor * a, co
         for (int64_t i0 = 0; i0 < a->ne[0]; i0++) {
             const float x = load_f(a, ELEM(a, i0, i1, i2, i3));
             const float y = load_f(b, ELEM(b, i0 % b->ne[0], i1 % b->ne[1], i2 % b->ne[2], i3 % b->ne[3]));
-            store_f(dst, ELEM(dst, i0, i1, i2, i3), op == GGML_OP_ADD ? x + y : op == GGML_OP_MUL ? x * y : x / y);
+            store_f(dst, ELEM(dst, i0, i1, i2, i3), op == GGML_OP_ADD ? x + y : op == GGML_OP_MUL ? x * y : op == GGML_OP_SUB ? x - y : x / y);
         }
     }
 }
@@ -739,8 +742,62 @@ static void op_unary(struct ggml_tensor * dst, const struct ggml_tensor * a, int
             else if (kind == GGML_UNARY_OP_SILU) y = x / (1.0f + exp_cr(-x));
             else if (kind == GGML_UNARY_OP_RELU) y = x > 0.f ? x : 0.f;
             else if (kind == GGML_UNARY_OP_SIGMOID) y = 1.0f / (1.0f + exp_cr(-x));
+            else if (kind == GGML_UNARY_OP_ABS) y = fabsf(x);
+            else if (kind == GGML_UNARY_OP_SOFTPLUS) y = softplus_cr(x);
             else { fprintf(stderr, "oracle: unary op %d\n", kind); abort(); }
             store_f(dst, ELEM(dst, i0, i1, i2, i3), y);
+        }
+    }
+}
+
+// ggml_l2_norm (upstream ggml-cpu's l2_norm: the row's sum of f32 squares in double, then
+// scale = 1 / max(sqrtf(sum), eps), y = x * scale)
+static void op_l2_norm(struct ggml_tensor * dst, const struct ggml_tensor * a, int nth) {
+    float eps;
+    memcpy(&eps, dst->op_params, 4);
+    #pragma omp parallel for collapse(3) num_threads(nth) schedule(static)
+    for (int64_t i3 = 0; i3 < a->ne[3]; i3++)
+    for (int64_t i2 = 0; i2 < a->ne[2]; i2++)
+    for (int64_t i1 = 0; i1 < a->ne[1]; i1++) {
+        ggml_float sum = 0.0;
+        for (int64_t i0 = 0; i0 < a->ne[0]; i0++) {
+            const float x = load_f(a, ELEM(a, i0, i1, i2, i3));
+            sum += (ggml_float) (x * x);
+        }
+        const float scale = 1.0f / fmaxf(sqrtf((float) sum), eps);
+        for (int64_t i0 = 0; i0 < a->ne[0]; i0++) {
+            store_f(dst, ELEM(dst, i0, i1, i2, i3), load_f(a, ELEM(a, i0, i1, i2, i3)) * scale);
+        }
+    }
+}
+
+// ggml_concat: element i of dim `dim` comes from a while i < a->ne[dim], else from b
+static void op_concat(struct ggml_tensor * dst, const struct ggml_tensor * a, const struct ggml_tensor * b) {
+    const int dim = dst->op_params[0];
+    const size_t es = ggml_type_size(dst->type);
+    for (int64_t i3 = 0; i3 < dst->ne[3]; i3++)
+    for (int64_t i2 = 0; i2 < dst->ne[2]; i2++)
+    for (int64_t i1 = 0; i1 < dst->ne[1]; i1++)
+    for (int64_t i0 = 0; i0 < dst->ne[0]; i0++) {
+        int64_t ix[4] = { i0, i1, i2, i3 };
+        const struct ggml_tensor * s = a;
+        if (ix[dim] >= a->ne[dim]) { ix[dim] -= a->ne[dim]; s = b; }
+        memcpy(ELEM(dst, i0, i1, i2, i3), ELEM(s, ix[0], ix[1], ix[2], ix[3]), es);
+    }
+}
+
+// ggml_swiglu_split: silu(a) * b with the silu and mul ops' roundings
+static void op_glu(struct ggml_tensor * dst, const struct ggml_tensor * a, const struct ggml_tensor * b, int nth) {
+    if (dst->op_params[0] != GGML_GLU_OP_SWIGLU) { fprintf(stderr, "oracle: glu op %d\n", dst->op_params[0]); abort(); }
+    #pragma omp parallel for collapse(3) num_threads(nth) schedule(static)
+    for (int64_t i3 = 0; i3 < a->ne[3]; i3++)
+    for (int64_t i2 = 0; i2 < a->ne[2]; i2++)
+    for (int64_t i1 = 0; i1 < a->ne[1]; i1++) {
+        for (int64_t i0 = 0; i0 < a->ne[0]; i0++) {
+            const float x = load_f(a, ELEM(a, i0, i1, i2, i3));
+            const float g = load_f(b, ELEM(b, i0, i1, i2, i3));
+            const float sl = x / (1.0f + exp_cr(-x));
+            store_f(dst, ELEM(dst, i0, i1, i2, i3), sl * g);
         }
     }
 }
@@ -977,7 +1034,10 @@ static void compute_node(struct ggml_tensor * t, int nth) {
         case GGML_OP_CPY: op_dup(t, t->src[0], nth); return;
         case GGML_OP_GET_ROWS: op_get_rows(t, t->src[0], t->src[1], nth); return;
         case GGML_OP_RMS_NORM: op_rms_norm(t, t->src[0], nth); return;
-        case GGML_OP_ADD: case GGML_OP_MUL: case GGML_OP_DIV: op_binary(t, t->src[0], t->src[1], nth); return;
+        case GGML_OP_ADD: case GGML_OP_MUL: case GGML_OP_DIV: case GGML_OP_SUB: op_binary(t, t->src[0], t->src[1], nth); return;
+        case GGML_OP_L2_NORM: op_l2_norm(t, t->src[0], nth); return;
+        case GGML_OP_CONCAT: op_concat(t, t->src[0], t->src[1]); return;
+        case GGML_OP_GLU: op_glu(t, t->src[0], t->src[1], nth); return;
         case GGML_OP_SUM_ROWS: op_sum_rows(t, t->src[0]); return;
         case GGML_OP_ARGSORT: op_argsort(t, t->src[0]); return;
         case GGML_OP_SCALE: case GGML_OP_SQR: case GGML_OP_UNARY: op_unary(t, t->src[0], nth); return;

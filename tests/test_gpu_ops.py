@@ -793,3 +793,25 @@ def test_moe_route_fused(hip, cpu, E, k, n_tok):
     assert np.array_equal(wa, wb)
     order = np.argsort(-lg, axis=1, kind="stable")[:, :k]
     assert np.array_equal(ia.reshape(n_tok, k).astype(np.int64), order)
+
+
+def test_other_arch_ops(hip, cpu):
+    """The ops the reference's other graphs add (model.cpp:1156-1295, dory.c:722-724): sub, abs,
+    softplus, l2_norm, concat, swiglu_split, bit-exact against the oracle."""
+    r = rng(31)
+    a = (r.standard_normal((3, 5, 130)) * 6).astype(np.float32)
+    b = r.standard_normal((3, 5, 130)).astype(np.float32)
+    c = r.standard_normal((3, 2, 130)).astype(np.float32)
+    row = r.standard_normal(130).astype(np.float32)
+
+    def build(g):
+        ta = g.tensor(gl.F32, 130, 5, 3, data=a)
+        tb = g.tensor(gl.F32, 130, 5, 3, data=b)
+        tc = g.tensor(gl.F32, 130, 2, 3, data=c)
+        tr = g.tensor(gl.F32, 130, data=row)
+        return [g.sub(ta, tr), g.abs(ta), g.softplus(ta), g.l2_norm(ta, 1e-6), g.concat(ta, tc, 1),
+                g.concat(ta, tb, 2), g.swiglu_split(ta, tb)]
+
+    got, ref = run_on(hip, build), run_on(cpu, build)
+    for k, (x, y) in enumerate(zip(got, ref)):
+        assert np.array_equal(x, y), k

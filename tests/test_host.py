@@ -22,6 +22,7 @@ LIB_DIR = os.path.join(ROOT, "ggml-loader_amd", "lib")
 HEADER_LIB = {
     "ggml.h": "libggml.so", "gguf.h": "libggml.so", "ggml-alloc.h": "libggml.so", "ggml-backend.h": "libggml.so",
     "ggml-hip.h": "libggml-hip.so", "ggml-loader.h": "libggml-loader.so", "ggml-cpu.h": ORACLE_SO,
+    "ggml-vulkan.h": "libggml.so",
 }
 
 TINY = {
@@ -109,7 +110,7 @@ def read_with_c(path):
         for i in range(core.gguf_get_n_tensors(ctx)):
             name = core.gguf_get_tensor_name(ctx, i).decode()
             nd = core.gguf_get_tensor_n_dims(ctx, i)
-            info["tensors"][name] = (core.gguf_get_tensor_type(ctx, i), [core.gguf_get_tensor_ne(ctx, i, j) for j in range(nd)],
+            info["tensors"][name] = (core.gguf_get_tensor_type(ctx, i), list(core.gguf_get_tensor_ne(ctx, i)[:nd]),
                                      core.gguf_get_tensor_offset(ctx, i), core.gguf_get_tensor_size(ctx, i))
         return info
     finally:
