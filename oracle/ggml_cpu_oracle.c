@@ -877,6 +877,80 @@ static void op_rope(struct ggml_tensor * dst, const struct ggml_tensor * a, cons
 }
 
 /* dst[i01, i11, i12, i13] = src0[:, i01, i12/r2, i13/r3] . src1[:, i11, i12, i13] */
+/* Q4_0 / Q8_0 weights against many Q8_0 columns, tiled (16 rows x 64 columns): the block scales
+   of the tile's rows and of every column are converted from fp16 once instead of once per dot.
+   Each output is oracle_vec_dot_q4_0_q8_0 / _q8_0_q8_0's value: the same integer block sums and
+   the same float expression per block, added in block order. */
+static void mul_mat_q_tiled(struct ggml_tensor * dst, const struct ggml_tensor * src0, const struct ggml_tensor * src1,
+                            const char * wdata, size_t drs, int nth) {
+    const int wt = src0->type;
+    const int64_t K = src0->ne[0], nb = K / 32, nr = src0->ne[1];
+    const int64_t n1 = src1->ne[1], n2 = src1->ne[2], n3 = src1->ne[3];
+    const int64_t r2 = n2 / src0->ne[2], r3 = n3 / src0->ne[3];
+    const int64_t ncols = n1 * n2 * n3;
+    const int64_t TR = 16, TC = 64;
+    const int64_t nrt = (nr + TR - 1) / TR, nct = (ncols + TC - 1) / TC;
+    float * xs = (float *) malloc((size_t) (ncols * nb) * sizeof(float));
+    for (int64_t c = 0; c < ncols; c++) {
+        const bq8_0 * y = (const bq8_0 *) (wdata + drs * (size_t) c);
+        for (int64_t ib = 0; ib < nb; ib++) xs[c * nb + ib] = F16(y[ib].d);
+    }
+    #pragma omp parallel for collapse(2) num_threads(nth) schedule(static)
+    for (int64_t rt = 0; rt < nrt; rt++)
+    for (int64_t ct = 0; ct < nct; ct++) {
+        float ws[16 * 512];
+        const int64_t r0 = rt * TR, r1 = r0 + TR < nr ? r0 + TR : nr;
+        const int64_t c0 = ct * TC, c1 = c0 + TC < ncols ? c0 + TC : ncols;
+        const int fits = nb <= 512;
+        for (int64_t c = c0; c < c1; c++) {
+            const int64_t i11 = c % n1, i12 = (c / n1) % n2, i13 = c / (n1 * n2);
+            const char * base = (const char *) src0->data + (i12 / r2) * src0->nb[2] + (i13 / r3) * src0->nb[3];
+            if (fits && (c == c0 || (c % (n1 * n2)) == 0 || ((c / n1) % n2) != (((c - 1) / n1) % n2))) {
+                for (int64_t i01 = r0; i01 < r1; i01++) {
+                    const char * w = base + i01 * src0->nb[1];
+                    for (int64_t ib = 0; ib < nb; ib++) {
+                        const uint16_t d = wt == GGML_TYPE_Q4_0 ? ((const bq4_0 *) w)[ib].d : ((const bq8_0 *) w)[ib].d;
+                        ws[(i01 - r0) * nb + ib] = F16(d);
+                    }
+                }
+            }
+            const bq8_0 * y = (const bq8_0 *) (wdata + drs * (size_t) c);
+            const float * yd = xs + c * nb;
+            for (int64_t i01 = r0; i01 < r1; i01++) {
+                const char * w = base + i01 * src0->nb[1];
+                float sumf = 0;
+                if (!fits) {
+                    sumf = wt == GGML_TYPE_Q4_0 ? oracle_vec_dot_q4_0_q8_0(K, w, y) : oracle_vec_dot_q8_0_q8_0(K, w, y);
+                } else if (wt == GGML_TYPE_Q4_0) {
+                    const bq4_0 * x = (const bq4_0 *) w;
+                    const float * wd = ws + (i01 - r0) * nb;
+                    for (int64_t ib = 0; ib < nb; ++ib) {
+                        int sumi0 = 0, sumi1 = 0;
+                        for (int j = 0; j < 16; ++j) {
+                            const int v0 = (x[ib].qs[j] & 0x0F) - 8;
+                            const int v1 = (x[ib].qs[j] >> 4) - 8;
+                            sumi0 += v0 * y[ib].qs[j];
+                            sumi1 += v1 * y[ib].qs[j + 16];
+                        }
+                        const int sumi = sumi0 + sumi1;
+                        sumf += sumi * wd[ib] * yd[ib];
+                    }
+                } else {
+                    const bq8_0 * x = (const bq8_0 *) w;
+                    const float * wd = ws + (i01 - r0) * nb;
+                    for (int64_t ib = 0; ib < nb; ++ib) {
+                        int sumi = 0;
+                        for (int j = 0; j < 32; j++) sumi += x[ib].qs[j] * y[ib].qs[j];
+                        sumf += sumi * (wd[ib] * yd[ib]);
+                    }
+                }
+                *(float *) ELEM(dst, i01, i11, i12, i13) = sumf;
+            }
+        }
+    }
+    free(xs);
+}
+
 static void op_mul_mat(struct ggml_tensor * dst, const struct ggml_tensor * src0, const struct ggml_tensor * src1, int nth) {
     const int wt = src0->type;
     const int dt = dot_type_of(wt);
@@ -897,12 +971,25 @@ static void op_mul_mat(struct ggml_tensor * dst, const struct ggml_tensor * src0
         free(row);
     }
     const int64_t nr = src0->ne[1];
+    // tiles of 16 weight rows x 64 columns, so a tile's rows stay in cache across its columns
+    // (each output is the same row_dot either way)
+    const int64_t TR = 16, TC = 64;
+    const int64_t nrt = (nr + TR - 1) / TR, nct = (ncols + TC - 1) / TC;
+    if ((wt == GGML_TYPE_Q4_0 || wt == GGML_TYPE_Q8_0) && ncols >= 8) {
+        mul_mat_q_tiled(dst, src0, src1, wdata, drs, nth);
+        free(wdata);
+        return;
+    }
     #pragma omp parallel for collapse(2) num_threads(nth) schedule(static)
-    for (int64_t c = 0; c < ncols; c++)
-    for (int64_t i01 = 0; i01 < nr; i01++) {
-        const int64_t i11 = c % n1, i12 = (c / n1) % n2, i13 = c / (n1 * n2);
-        const char * w = (const char *) src0->data + i01 * src0->nb[1] + (i12 / r2) * src0->nb[2] + (i13 / r3) * src0->nb[3];
-        *(float *) ELEM(dst, i01, i11, i12, i13) = row_dot(wt, w, wdata + drs * (size_t) c, K);
+    for (int64_t rt = 0; rt < nrt; rt++)
+    for (int64_t ct = 0; ct < nct; ct++) {
+        for (int64_t c = ct * TC; c < ncols && c < (ct + 1) * TC; c++) {
+            const int64_t i11 = c % n1, i12 = (c / n1) % n2, i13 = c / (n1 * n2);
+            for (int64_t i01 = rt * TR; i01 < nr && i01 < (rt + 1) * TR; i01++) {
+                const char * w = (const char *) src0->data + i01 * src0->nb[1] + (i12 / r2) * src0->nb[2] + (i13 / r3) * src0->nb[3];
+                *(float *) ELEM(dst, i01, i11, i12, i13) = row_dot(wt, w, wdata + drs * (size_t) c, K);
+            }
+        }
     }
     free(wdata);
 }
