@@ -64,6 +64,16 @@ ggml_tensor._fields_ = [
 T = C.POINTER(ggml_tensor)
 
 
+class ggml_hip_sampler_params(C.Structure):
+    _fields_ = [("temp", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float), ("repeat_penalty", C.c_float),
+                ("repeat_last_n", C.c_int32)]
+
+
+class gl_sampler_params(C.Structure):
+    _fields_ = [("temp", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float), ("repeat_penalty", C.c_float),
+                ("repeat_last_n", C.c_int32), ("seed", C.c_uint32)]
+
+
 class gl_synth_params(C.Structure):
     _fields_ = [
         ("arch", C.c_char_p),
@@ -209,6 +219,8 @@ def _declare(core, hip, loader):
     _sig(hip, "ggml_backend_hip_init", vp, i32)
     _sig(hip, "ggml_backend_is_hip", C.c_bool, vp)
     _sig(hip, "ggml_backend_hip_graph_compute_static", i32, vp, vp)
+    _sig(hip, "ggml_backend_hip_sample", i32, vp, vp, i64, C.POINTER(ggml_hip_sampler_params), vp, sz,
+         C.c_double, C.POINTER(C.c_int32), C.POINTER(C.c_bool))
     _sig(hip, "ggml_backend_hip_set_fusion", None, vp, C.c_bool)
     _sig(hip, "ggml_backend_hip_set_graph_replay", None, vp, C.c_bool)
     _sig(hip, "ggml_backend_hip_set_profiling", None, vp, C.c_bool)
@@ -226,6 +238,8 @@ def _declare(core, hip, loader):
     _sig(loader, "gl_session_get", i64, vp, C.c_char_p)
     _sig(loader, "gl_forward_step", i32, vp, i64, C.POINTER(C.c_int32), i64, C.POINTER(C.c_float), eb, sz)
     _sig(loader, "gl_decode_loop", i32, vp, i64, C.c_int32, i32, i32, C.POINTER(C.c_int32), C.POINTER(C.c_double), eb, sz)
+    _sig(loader, "gl_generate", i32, vp, i64, C.POINTER(C.c_int32), i64, i32, C.POINTER(gl_sampler_params),
+         C.POINTER(C.c_int32), C.POINTER(C.c_double), eb, sz)
     _sig(loader, "gl_kv_fill_random", i32, vp, i64, C.c_uint64, eb, sz)
     _sig(loader, "gl_kv_read", i32, vp, i32, i32, vp, sz, sz)
     _sig(loader, "gl_synth_model", i32, C.c_char_p, C.POINTER(gl_synth_params), eb, sz)
@@ -252,6 +266,21 @@ def libs() -> dict:
 
 def hip_device_count() -> int:
     return int(libs()["hip"].ggml_backend_hip_get_device_count())
+
+
+def hip_sample(backend, logits_tensor, row: int, recent, u: float, *, temp: float, top_k: int = 40,
+               top_p: float = 0.95, repeat_penalty: float = 1.0, repeat_last_n: int = 64):
+    """ggml_backend_hip_sample on one row of an F32 tensor in the backend's buffer:
+    (token id, whether u was used)."""
+    import numpy as np
+    r = np.ascontiguousarray(np.asarray(recent, dtype=np.int32))
+    sp = ggml_hip_sampler_params(temp, top_k, top_p, repeat_penalty, repeat_last_n)
+    tok, used = C.c_int32(-1), C.c_bool(False)
+    st = libs()["hip"].ggml_backend_hip_sample(backend, logits_tensor, row, C.byref(sp), r.ctypes.data_as(C.c_void_p),
+                                               r.size, u, C.byref(tok), C.byref(used))
+    if st != 0:
+        raise RuntimeError(f"ggml_backend_hip_sample failed ({st})")
+    return int(tok.value), bool(used.value)
 
 
 def hip_backend(device: int = 0):
@@ -347,6 +376,22 @@ class Session:
         err = C.create_string_buffer(512)
         rc = self._l.gl_decode_loop(self.h, n_past, first_token, n_steps, int(fixed_pos),
                                     toks.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(secs), err, 512)
+        if rc != 0:
+            raise RuntimeError(err.value.decode())
+        return toks[:n_steps], secs.value
+
+    def generate(self, n_past: int, prompt, n_steps: int, *, temp: float, top_k: int = 40, top_p: float = 0.95,
+                 repeat_penalty: float = 1.0, repeat_last_n: int = 64, seed: int = 1):
+        """gl_generate: the prompt at n_past, then n_steps sampled tokens (the first from the prompt's
+        logits); returns (tokens, seconds)."""
+        import numpy as np
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
+        toks = np.zeros(max(n_steps, 1), dtype=np.int32)
+        sp = gl_sampler_params(temp, top_k, top_p, repeat_penalty, repeat_last_n, seed)
+        secs = C.c_double()
+        err = C.create_string_buffer(512)
+        rc = self._l.gl_generate(self.h, n_past, p.ctypes.data_as(C.POINTER(C.c_int32)), len(p), n_steps, C.byref(sp),
+                                 toks.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(secs), err, 512)
         if rc != 0:
             raise RuntimeError(err.value.decode())
         return toks[:n_steps], secs.value

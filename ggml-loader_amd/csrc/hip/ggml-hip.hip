@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <climits>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -59,6 +60,12 @@ struct hip_device {
     // pinned host landing area for downloads
     uint8_t * down = nullptr;
     size_t down_size = 0;
+    // token sampling: device words (3 result ints, then the penalty table) and the sorted path's
+    // workspace
+    int * smp = nullptr;
+    size_t smp_ints = 0;
+    uint8_t * smp_ws = nullptr;
+    size_t smp_ws_size = 0;
     ggml_backend_buffer_type buft{};
     char name[64] = { 0 };
 };
@@ -1941,6 +1948,112 @@ bool ggml_backend_is_hip(ggml_backend_t backend) { return backend && backend->if
 enum ggml_status ggml_backend_hip_graph_compute_static(ggml_backend_t backend, struct ggml_cgraph * cgraph) {
     if (!ggml_backend_is_hip(backend) || !cgraph) return GGML_STATUS_FAILED;
     return compute_static((hip_backend_ctx *) backend->context, cgraph);
+}
+
+// model.cpp:1675-1728 (see the declaration for the contract)
+enum ggml_status ggml_backend_hip_sample(ggml_backend_t backend, const struct ggml_tensor * logits, int64_t row,
+                                         const struct ggml_hip_sampler_params * p, const int32_t * recent,
+                                         size_t n_recent, double u, int32_t * token, bool * used_draw) {
+    auto fail = [](const char * why) {
+        fprintf(stderr, "ggml_backend_hip_sample: %s\n", why);
+        return GGML_STATUS_FAILED;
+    };
+    if (!ggml_backend_is_hip(backend)) return fail("not a HIP backend");
+    if (!logits || !p || !token || (n_recent && !recent)) return fail("null argument");
+    hip_backend_ctx * c = (hip_backend_ctx *) backend->context;
+    if (logits->type != GGML_TYPE_F32 || !logits->data || logits->nb[0] != sizeof(float)) return fail("logits must be F32 with contiguous rows");
+    if (!logits->buffer || ggml_backend_buffer_get_type(logits->buffer) != ggml_backend_hip_buffer_type(c->device)) {
+        return fail("logits are not in this backend's device buffer");
+    }
+    const int64_t n = logits->ne[0];
+    if (n < 1 || n > INT_MAX / 4) return fail("row length out of range");
+    if (row < 0 || row >= ggml_nrows(logits)) return fail("row out of range");
+    const int64_t i1 = row % logits->ne[1], i2 = (row / logits->ne[1]) % logits->ne[2], i3 = row / (logits->ne[1] * logits->ne[2]);
+    const float * base = (const float *) ((const char *) logits->data + i1 * logits->nb[1] + i2 * logits->nb[2] + i3 * logits->nb[3]);
+
+    // the window (model.cpp:1677-1681) as distinct ids with their occurrence counts
+    std::vector<int32_t> win;
+    if (p->repeat_penalty != 1.0f && n_recent > 0) {
+        const size_t start = n_recent > (size_t) p->repeat_last_n ? n_recent - (size_t) p->repeat_last_n : 0;
+        for (size_t i = start; i < n_recent; i++) {
+            if (recent[i] >= 0 && (int64_t) recent[i] < n) win.push_back(recent[i]);
+        }
+        std::sort(win.begin(), win.end());
+    }
+    std::vector<int32_t> table;           // ids, then counts
+    int n_pen = 0;
+    for (size_t i = 0; i < win.size();) {
+        size_t j = i;
+        while (j < win.size() && win[j] == win[i]) j++;
+        table.push_back(win[i]);
+        n_pen++;
+        i = j;
+    }
+    for (size_t i = 0; i < win.size();) {
+        size_t j = i;
+        while (j < win.size() && win[j] == win[i]) j++;
+        table.push_back((int32_t) (j - i));
+        i = j;
+    }
+
+    hip_device & d = dev(c->device);
+    const size_t ints = 4 + table.size();
+    if (ints > d.smp_ints) {
+        HIP_CHECK(hipStreamSynchronize(d.stream));
+        if (d.smp) HIP_CHECK(hipFree(d.smp));
+        d.smp_ints = std::max(ints, (size_t) 4096);
+        HIP_CHECK(hipMalloc(&d.smp, d.smp_ints * sizeof(int)));
+    }
+    if (!table.empty()) {
+        const size_t bytes = table.size() * sizeof(int32_t);
+        if (uint8_t * slot = upload_slot(d, bytes)) {
+            memcpy(slot, table.data(), bytes);
+            HIP_CHECK(hipMemcpyAsync(d.smp + 4, slot, bytes, hipMemcpyHostToDevice, d.stream));
+        } else {
+            HIP_CHECK(hipMemcpyAsync(d.smp + 4, table.data(), bytes, hipMemcpyHostToDevice, d.stream));
+            HIP_CHECK(hipStreamSynchronize(d.stream));
+        }
+    }
+    sample_request r;
+    r.logits = base;
+    r.n = (int) n;
+    r.pen_ids = d.smp + 4;
+    r.pen_cnt = d.smp + 4 + n_pen;
+    r.n_pen = n_pen;
+    r.temp = p->temp;
+    r.top_k = p->top_k;
+    r.top_p = p->top_p;
+    r.penalty = p->repeat_penalty;
+    r.u = u;
+    r.out = d.smp;
+    int res[3] = { 0, 0, SMP_OVERFLOW };
+    auto read_result = [&]() {
+        int * area = (int *) download_area(d, sizeof(res));
+        HIP_CHECK(hipMemcpyAsync(area, d.smp, sizeof(res), hipMemcpyDeviceToHost, d.stream));
+        HIP_CHECK(hipStreamSynchronize(d.stream));
+        drained(d);
+        memcpy(res, area, sizeof(res));
+    };
+    if (sample_fast_path(r)) {
+        launch_sample(r, d.stream);
+        read_result();
+    }
+    if (res[2] == SMP_OVERFLOW) {
+        const size_t ws = sample_sorted_ws_bytes((int) n);
+        if (ws > d.smp_ws_size) {
+            HIP_CHECK(hipStreamSynchronize(d.stream));
+            if (d.smp_ws) HIP_CHECK(hipFree(d.smp_ws));
+            d.smp_ws_size = ws;
+            HIP_CHECK(hipMalloc(&d.smp_ws, ws));
+        }
+        launch_sample_sorted(r, d.smp_ws, d.smp_ws_size, d.stream);
+        read_result();
+    }
+    if (res[2] == SMP_NONFINITE) return fail("the largest logit is not finite");
+    if (res[2] != SMP_OK) return fail("sampling kernel reported an error");
+    *token = res[0];
+    if (used_draw) *used_draw = res[1] != 0;
+    return GGML_STATUS_SUCCESS;
 }
 
 void ggml_backend_hip_set_fusion(ggml_backend_t backend, bool enable) {

@@ -353,3 +353,32 @@ void launch_attn_decode(const attn_launch & A, hipStream_t st);
 // quantized output); n_kv up to attn_prefill_max_kv(hd), 0 for an unsupported head dim
 int attn_prefill_max_kv(int hd);
 void launch_attn_prefill(const attn_launch & A, hipStream_t st);
+
+// ---- token sampling (k_sample.hip) ----
+// One row of F32 logits, the window's penalized ids (distinct, ascending) with their occurrence
+// counts, the sampler's parameters and the uniform variate u of the draw. out (device, 3 ints):
+// the token id, whether u was used (the weighted draw ran over two or more weights), a status.
+constexpr int SMP_BOUND_K = 1024;    // largest top-k of the one-launch path
+constexpr int SMP_MAX_CAND = 4096;   // candidates the one-launch path holds (and rows it sorts whole)
+constexpr int SMP_MAX_PEN = 1024;    // penalized ids the one-launch path holds
+constexpr int SMP_CHUNK = 4096;      // probabilities staged per pass of the sequential sums
+enum { SMP_OK = 0, SMP_OVERFLOW = 1, SMP_NONFINITE = 2 };
+struct sample_request {
+    const float * logits;
+    int           n;
+    const int *   pen_ids;
+    const int *   pen_cnt;
+    int           n_pen;
+    float         temp;
+    int           top_k;
+    float         top_p;
+    float         penalty;
+    double        u;
+    int *         out;
+};
+// the one-launch path takes the request (it may still report SMP_OVERFLOW: then take the sorted path)
+bool sample_fast_path(const sample_request & r);
+void launch_sample(const sample_request & r, hipStream_t st);
+// the sorted path: ws of sample_sorted_ws_bytes(n) bytes
+size_t sample_sorted_ws_bytes(int n);
+void launch_sample_sorted(const sample_request & r, void * ws, size_t ws_bytes, hipStream_t st);

@@ -101,6 +101,44 @@ int gl_forward_step(gl_session * s, int64_t n_past, const int32_t * tokens, int6
     return 0;
 }
 
+int gl_generate(gl_session * s, int64_t n_past, const int32_t * prompt, int64_t n_prompt, int n_steps,
+                const gl_sampler_params * params, int32_t * tokens_out, double * seconds, char * err, size_t err_size) {
+    try {
+        if (!params || !prompt || n_prompt < 1 || n_steps < 1) throw gl_error("gl_generate: bad arguments");
+        for (int64_t i = 0; i < n_prompt; i++) {
+            if (prompt[i] < 0 || prompt[i] >= s->n_vocab) throw gl_error("token id out of range");
+        }
+        sampler_params sp;
+        sp.temp = params->temp;
+        sp.top_k = params->top_k;
+        sp.top_p = params->top_p;
+        sp.repeat_penalty = params->repeat_penalty;
+        sp.repeat_last_n = params->repeat_last_n;
+        sp.seed = params->seed;
+        sampler smp = init_sampler(sp);
+        auto t0 = std::chrono::steady_clock::now();
+        // cmd_run.cpp:503-510: the prompt in one step, then the first sample over all_tokens
+        std::vector<int32_t> all_tokens(prompt, prompt + n_prompt);
+        int64_t pos = n_past + n_prompt;
+        int32_t next = forward_step_sample(s->m, s->hp, s->kv, s->ds, s->backend, n_past, all_tokens, s->n_vocab, smp,
+                                           all_tokens);
+        tokens_out[0] = next;
+        // cmd_run.cpp:582-619: feed the token, extend all_tokens, sample again
+        for (int i = 1; i < n_steps; i++) {
+            all_tokens.push_back(next);
+            next = forward_step_sample(s->m, s->hp, s->kv, s->ds, s->backend, pos, { next }, s->n_vocab, smp, all_tokens);
+            pos++;
+            tokens_out[i] = next;
+        }
+        auto t1 = std::chrono::steady_clock::now();
+        if (seconds) *seconds = std::chrono::duration<double>(t1 - t0).count();
+    } catch (const std::exception & e) {
+        set_err(err, err_size, e.what());
+        return 1;
+    }
+    return 0;
+}
+
 int gl_decode_loop(gl_session * s, int64_t n_past, int32_t first_token, int n_steps, int fixed_pos,
                    int32_t * tokens_out, double * seconds, char * err, size_t err_size) {
     try {

@@ -8,6 +8,7 @@
 #include "ggml-hip.h"
 
 #include <algorithm>
+#include <random>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -471,9 +472,15 @@ void free_decode_session(decode_session & ds) {
 // model.cpp:1496-1597. logits_out (n_vocab floats, may be null) receives the last column's logits; with greedy_out
 // set instead, the graph ends in the argmax of that column (ggml_argmax: the first index of the
 // maximum, the pick of argmax() below) and only the index is read back.
+struct sample_job {
+    sampler * smp;
+    const std::vector<int32_t> * recent;
+    int32_t token;
+};
+
 static void run_step(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds, ggml_backend_t backend,
                      int64_t n_past, const std::vector<int32_t> & new_tokens, int64_t n_vocab, float * logits_out,
-                     int32_t * greedy_out) {
+                     int32_t * greedy_out, sample_job * sj = nullptr) {
     const int64_t n_new = (int64_t) new_tokens.size();
     const int64_t n_kv  = n_past + n_new;
     if (n_new <= 0) throw gl_error("forward_step: no tokens");
@@ -489,6 +496,13 @@ static void run_step(const model & m, const hparams & hp, kv_cache & kv, decode_
         pick = ggml_argmax(gctx_build, last);
         ggml_set_output(pick);
         ggml_build_forward_expand(bg.gf, pick);
+    }
+    if (sj) {
+        if (!ggml_backend_is_hip(backend)) {
+            ggml_free(gctx_build);
+            throw gl_error("forward_step_sample: device sampling needs the hip backend");
+        }
+        ggml_set_output(bg.logits);
     }
 
     if (!ggml_gallocr_alloc_graph(ds.galloc, bg.gf)) {
@@ -511,7 +525,24 @@ static void run_step(const model & m, const hparams & hp, kv_cache & kv, decode_
 
     ggml_backend_graph_compute(backend, bg.gf);
 
-    if (greedy_out) {
+    if (sj) {
+        // model.cpp:1675-1728 on the last column, with the generator's next variate
+        sampler & smp = *sj->smp;
+        if (!smp.has_u) {
+            smp.u = std::generate_canonical<double, 53>(smp.rng);
+            smp.has_u = true;
+        }
+        const ggml_hip_sampler_params sp = { smp.params.temp, smp.params.top_k, smp.params.top_p,
+                                             smp.params.repeat_penalty, smp.params.repeat_last_n };
+        bool used = false;
+        const enum ggml_status st = ggml_backend_hip_sample(backend, bg.logits, n_new - 1, &sp, sj->recent->data(),
+                                                            sj->recent->size(), smp.u, &sj->token, &used);
+        if (st != GGML_STATUS_SUCCESS) {
+            ggml_free(gctx_build);
+            throw gl_error("forward_step_sample: device sampling failed");
+        }
+        if (used) smp.has_u = false;
+    } else if (greedy_out) {
         ggml_backend_tensor_get(pick, greedy_out, 0, sizeof(int32_t));
     } else if (logits_out) {
         const size_t last_col_offset = (size_t) (n_new - 1) * n_vocab * sizeof(float);
@@ -539,6 +570,22 @@ int32_t forward_step_greedy(const model & m, const hparams & hp, kv_cache & kv, 
     int32_t tok = 0;
     run_step(m, hp, kv, ds, backend, n_past, new_tokens, n_vocab, nullptr, &tok);
     return tok;
+}
+
+// model.cpp:1668-1673
+sampler init_sampler(const sampler_params & params) {
+    sampler smp;
+    smp.params = params;
+    smp.rng.seed(params.seed != 0 ? params.seed : std::random_device{}());
+    return smp;
+}
+
+int32_t forward_step_sample(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds,
+                            ggml_backend_t backend, int64_t n_past, const std::vector<int32_t> & new_tokens,
+                            int64_t n_vocab, sampler & smp, const std::vector<int32_t> & recent_tokens) {
+    sample_job sj = { &smp, &recent_tokens, 0 };
+    run_step(m, hp, kv, ds, backend, n_past, new_tokens, n_vocab, nullptr, nullptr, &sj);
+    return sj.token;
 }
 
 // model.cpp:1624-1657 (the Vulkan-only chunking policy is kept for callers that ask for it)

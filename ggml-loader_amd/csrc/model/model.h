@@ -14,6 +14,7 @@
 #include "gguf.h"
 
 #include <cstdint>
+#include <random>
 #include <string>
 #include <vector>
 
@@ -134,3 +135,28 @@ std::vector<float> prefill(const model & m, const hparams & hp, kv_cache & kv, d
                            int64_t n_vocab, bool use_chunking);
 
 int32_t argmax(const std::vector<float> & logits);
+
+// model.h:410-430: sampling parameters (temp <= 0 is greedy) and state. The generator is the
+// reference's std::mt19937; a uniform variate it has produced for a draw stays pending until a
+// draw consumes it (the reference's generator is not advanced when no draw happens).
+struct sampler_params {
+    float    temp           = 0.0f;
+    int      top_k          = 40;
+    float    top_p          = 0.95f;
+    float    repeat_penalty = 1.0f;
+    int      repeat_last_n  = 64;
+    uint32_t seed           = 0;   // 0 = seed from std::random_device
+};
+struct sampler {
+    sampler_params params;
+    std::mt19937 rng;
+    bool has_u = false;
+    double u = 0.0;
+};
+// model.cpp:1668-1673
+sampler init_sampler(const sampler_params & params);
+// forward_step + sample(smp, logits, recent_tokens) (model.cpp:1675-1728) of the last column, on
+// the device (HIP backend): only the token id is read back
+int32_t forward_step_sample(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds,
+                            ggml_backend_t backend, int64_t n_past, const std::vector<int32_t> & new_tokens,
+                            int64_t n_vocab, sampler & smp, const std::vector<int32_t> & recent_tokens);

@@ -39,6 +39,33 @@ GGML_API ggml_backend_buffer_type_t ggml_backend_hip_buffer_type(int device);
 // on one GPU (several threads or backends) race. Fails with profiling on (it creates events).
 GGML_API enum ggml_status ggml_backend_hip_graph_compute_static(ggml_backend_t backend, struct ggml_cgraph * cgraph);
 
+// Token sampling on the device: replaces `int32_t sample(sampler &, std::vector<float> & logits,
+// const std::vector<int32_t> & recent_tokens)` (model.h:432-435, model.cpp:1675-1728) for logits
+// that stay in device memory. Same parameters (model.h:418-425, minus the seed) and the same result:
+// the repetition penalty over the last repeat_last_n entries of recent (a negative repeat_last_n
+// takes all of them; ids outside the row are skipped), then argmax for temp <= 0 (first index of
+// the maximum), else temperature, top-k (top_k <= 0 or >= the row length: no cut), top-p (>= 1:
+// no cut) and the weighted draw of std::discrete_distribution on the uniform variate u in [0, 1)
+// that the caller's generator supplies (libstdc++ draws it as std::generate_canonical<double, 53>
+// of its std::mt19937). *used_draw reports whether the draw consumed u: it does not for temp <= 0
+// or when fewer than two tokens survive the cuts, and the reference's generator is then not
+// advanced either, so a caller keeps u for its next call. Logits with equal values are ordered by
+// ascending token id before the cuts (std::partial_sort leaves their order unspecified). logits:
+// an F32 tensor in this backend's buffer, row `row` (ggml row index over ne[1..3]) contiguous.
+// Synchronous: returns when the token id is on the host. Fails (GGML_STATUS_FAILED, with a message
+// on stderr) for another backend or buffer, a bad row, or a maximum that is not finite.
+struct ggml_hip_sampler_params {
+    float   temp;
+    int32_t top_k;
+    float   top_p;
+    float   repeat_penalty;
+    int32_t repeat_last_n;
+};
+GGML_API enum ggml_status ggml_backend_hip_sample(ggml_backend_t backend, const struct ggml_tensor * logits, int64_t row,
+                                                  const struct ggml_hip_sampler_params * params,
+                                                  const int32_t * recent, size_t n_recent, double u,
+                                                  int32_t * token, bool * used_draw);
+
 // Graph-level fusion (fused norm+quantize, QKV/gate-up multi-GEMV, rope+KV append, split-KV
 // decode attention). On by default; off runs one kernel per ggml node. Used by the parity tests
 // to check both paths against the oracle.

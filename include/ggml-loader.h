@@ -8,6 +8,8 @@
 //   gl_forward_step   forward_step (model.cpp:1496-1597): logits of the last new token
 //   gl_decode_loop    run_cycle's tg loop (cmd_bench.cpp:52-59): n steps of forward_step + argmax
 //                     (the argmax runs on the backend; one index is read back per step)
+//   gl_generate       cmd_run's sampled generation (temperature / top-k / top-p / repeat penalty
+//                     sampled on the device; one index is read back per step)
 //   gl_synth_model    writes the seeded synthetic GGUF models the benchmark configs describe
 // Errors return non-zero (or NULL) and write a message into err; nothing here calls exit().
 #pragma once
@@ -37,6 +39,24 @@ GGML_API int gl_forward_step(gl_session * s, int64_t n_past, const int32_t * tok
 // (n_steps entries, may be NULL) receives each step's argmax; *seconds receives the wall time.
 GGML_API int gl_decode_loop(gl_session * s, int64_t n_past, int32_t first_token, int n_steps, int fixed_pos,
                             int32_t * tokens_out, double * seconds, char * err, size_t err_size);
+
+// Sampled generation as cmd_run drives it (cmd_run.cpp:503-510, 576-620), on the HIP backend:
+// forward_step of the prompt at n_past, then n_steps - 1 single-token steps, each followed by
+// sample(smp, logits, all_tokens) (model.cpp:1675-1728) of the last logits column on the device,
+// where all_tokens is the prompt plus every token fed so far and smp is init_sampler(params)
+// (model.cpp:1668-1673; seed 0 = std::random_device). tokens_out (n_steps entries) receives the
+// sampled tokens: the first from the prompt's logits, then one per step. No stop tokens.
+typedef struct gl_sampler_params {
+    float    temp;
+    int32_t  top_k;
+    float    top_p;
+    float    repeat_penalty;
+    int32_t  repeat_last_n;
+    uint32_t seed;
+} gl_sampler_params;
+GGML_API int gl_generate(gl_session * s, int64_t n_past, const int32_t * prompt, int64_t n_prompt, int n_steps,
+                         const gl_sampler_params * params, int32_t * tokens_out, double * seconds, char * err,
+                         size_t err_size);
 
 // Fills positions [0, n_pos) of every layer's K and V cache with N(0,1) values stored as F16
 // (seeded, deterministic).

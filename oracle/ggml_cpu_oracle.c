@@ -613,6 +613,105 @@ void oracle_moe_route(const float * logits, int n_expert, int top_k, int32_t * i
 }
 
 /* ------------------------------------------------------------------------------------------ */
+/* Token sampler, restating sample() (model.cpp:1675-1728) and argmax() (model.cpp:1659-1666). The
+   weighted draw restates libstdc++'s std::discrete_distribution (GCC 11, bits/random.tcc:
+   param_type::_M_initialize and operator()): weights widened to double, divided by their double
+   sum, partial sums in order with the last set to 1, then the first partial sum not below u, where
+   u is the std::generate_canonical<double, 53> value the generator would have produced (the
+   caller supplies it); with fewer than two weights the result is 0 and no u is used. Logits order
+   by value, then ascending id among equal values (std::partial_sort leaves that order open);
+   a NaN orders and weighs as -inf. */
+
+static const float * g_sample_keys;
+
+static int sample_cmp(const void * a, const void * b) {
+    const int32_t ia = *(const int32_t *) a, ib = *(const int32_t *) b;
+    const float va = g_sample_keys[ia], vb = g_sample_keys[ib];
+    if (va > vb) return -1;
+    if (va < vb) return 1;
+    return ia < ib ? -1 : (ia > ib);
+}
+
+int32_t oracle_sample(const float * logits, int64_t n, const int32_t * recent, int64_t n_recent, float temp,
+                      int32_t top_k, float top_p, float repeat_penalty, int32_t repeat_last_n, double u,
+                      int32_t * used_draw) {
+    float * l = (float *) malloc((size_t) n * sizeof(float));
+    memcpy(l, logits, (size_t) n * sizeof(float));
+    *used_draw = 0;
+    /* model.cpp:1678-1687 */
+    if (repeat_penalty != 1.0f && n_recent > 0) {
+        const size_t nr = (size_t) n_recent;
+        const size_t start = nr > (size_t) repeat_last_n ? nr - (size_t) repeat_last_n : 0;
+        for (size_t i = start; i < nr; i++) {
+            const int32_t id = recent[i];
+            if (id < 0 || (int64_t) id >= n) continue;
+            l[id] = l[id] > 0.0f ? l[id] / repeat_penalty : l[id] * repeat_penalty;
+        }
+    }
+    /* model.cpp:1689-1691, 1659-1666 */
+    if (temp <= 0.0f) {
+        int32_t best = 0;
+        float bv = l[0];
+        for (int64_t i = 1; i < n; i++) {
+            if (l[i] > bv) { bv = l[i]; best = (int32_t) i; }
+        }
+        free(l);
+        return best;
+    }
+    for (int64_t i = 0; i < n; i++) if (isnan(l[i])) l[i] = -INFINITY;
+    int32_t * ids = (int32_t *) malloc((size_t) n * sizeof(int32_t));
+    for (int64_t i = 0; i < n; i++) ids[i] = (int32_t) i;
+    /* model.cpp:1693-1698 */
+    const int64_t k = (top_k > 0 && (int64_t) top_k < n) ? top_k : n;
+    g_sample_keys = l;
+    qsort(ids, (size_t) n, sizeof(int32_t), sample_cmp);
+    const float max_logit = l[ids[0]];
+    if (!isfinite(max_logit)) {
+        free(ids);
+        free(l);
+        return -1;
+    }
+    /* model.cpp:1700-1707 */
+    float * probs = (float *) malloc((size_t) k * sizeof(float));
+    float sum = 0.0f;
+    for (int64_t i = 0; i < k; i++) {
+        probs[i] = exp_cr((l[ids[i]] - max_logit) / temp);
+        sum += probs[i];
+    }
+    for (int64_t i = 0; i < k; i++) probs[i] /= sum;
+    /* model.cpp:1711-1724 */
+    int64_t cutoff = k;
+    if (top_p < 1.0f) {
+        float cum = 0.0f;
+        for (int64_t i = 0; i < k; i++) {
+            cum += probs[i];
+            if (cum >= top_p) { cutoff = i + 1; break; }
+        }
+        float s = 0.0f;
+        for (int64_t i = 0; i < cutoff; i++) s += probs[i];
+        for (int64_t i = 0; i < cutoff; i++) probs[i] /= s;
+    }
+    /* model.cpp:1726-1727 with discrete_distribution */
+    int64_t idx = 0;
+    if (cutoff >= 2) {
+        double sd = 0.0;
+        for (int64_t i = 0; i < cutoff; i++) sd += (double) probs[i];
+        double cp = 0.0;
+        idx = cutoff - 1;
+        for (int64_t i = 0; i < cutoff - 1; i++) {
+            cp += (double) probs[i] / sd;
+            if (!(cp < u)) { idx = i; break; }
+        }
+        *used_draw = 1;
+    }
+    const int32_t tok = ids[idx];
+    free(probs);
+    free(ids);
+    free(l);
+    return tok;
+}
+
+/* ------------------------------------------------------------------------------------------ */
 /* graph executor                                                                              */
 
 #define ELEM(t, i0, i1, i2, i3) ((char *) (t)->data + (i0) * (t)->nb[0] + (i1) * (t)->nb[1] + (i2) * (t)->nb[2] + (i3) * (t)->nb[3])

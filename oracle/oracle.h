@@ -32,6 +32,10 @@
  *   attention chain            n_kv = 1 -> V; equal keys -> mean of V (exact); fp64 GQA brute force
  *                              that also rejects the h % n_head_kv mapping
  *   moe_route                  brute-force top-k (ties -> lower id) and renormalized softmax
+ *   sample                     the reference's own sample() built from model.cpp (Makefile.ref):
+ *                              identical ids over seeded draw sequences on tie-free logits, and the
+ *                              same weight slot with ties; closed forms (top-k 1, two tokens, the
+ *                              draw as a step function of u with steps of the probabilities)
  *   forward_step               float64 numpy transformer on synthetic GGUFs of 4 archs, rejecting
  *                              the other RoPE pair layout
  */
@@ -76,6 +80,14 @@ void oracle_rope(float * dst, const float * src, int64_t ne0, int n_dims, int mo
 /* MoE router as in the reference's moe_route (qwen_model.c:551-606): softmax over n_expert
    logits, top-k by insertion (ties keep the lower id), renormalize the k weights */
 void oracle_moe_route(const float * logits, int n_expert, int top_k, int32_t * ids, float * w);
+
+/* sample() (model.cpp:1675-1728) on n logits with the window recent[0..n_recent) and the
+   uniform variate u of the weighted draw; *used_draw = 1 when the draw consumed u. Equal logits
+   order by ascending id. Returns the token id, or -1 when temp > 0 and the largest logit is not
+   finite. */
+int32_t oracle_sample(const float * logits, int64_t n, const int32_t * recent, int64_t n_recent, float temp,
+                      int32_t top_k, float top_p, float repeat_penalty, int32_t repeat_last_n, double u,
+                      int32_t * used_draw);
 
 #ifdef __cplusplus
 }

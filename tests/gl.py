@@ -17,6 +17,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG_INIT = os.path.join(ROOT, "ggml-loader_amd", "__init__.py")
 ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "libggml-cpu-oracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libmoe_ref.so")
+REF_SAMPLER_SO = os.path.join(ROOT, "oracle", "_ref", "libref_sampler.so")
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
@@ -63,8 +64,84 @@ def oracle():
         o.oracle_rope.argtypes = [vp, vp, i64, C.c_int, C.c_int, C.c_int32] + [C.c_float] * 6 + [C.c_int, vp]
         o.oracle_moe_route.restype = None
         o.oracle_moe_route.argtypes = [vp, C.c_int, C.c_int, vp, vp]
+        o.oracle_sample.restype = C.c_int32
+        o.oracle_sample.argtypes = [vp, i64, vp, i64, C.c_float, C.c_int32, C.c_float, C.c_float, C.c_int32,
+                                    C.c_double, C.POINTER(C.c_int32)]
         _oracle = o
     return _oracle
+
+
+# ---- sampling ----
+class Draws:
+    """The uniform variates libstdc++'s std::discrete_distribution takes from a std::mt19937 seeded
+    with `seed` (the reference's init_sampler, model.cpp:1668-1673): generate_canonical<double, 53>
+    of two 32-bit outputs, (a + b * 2^32) / 2^64, kept below 1 (GCC 11 bits/random.tcc). numpy's
+    MT19937 with legacy seeding is std::mt19937's generator and seeding. A variate stays pending
+    until a sampling call reports that it consumed it (the reference's generator only advances
+    then)."""
+
+    def __init__(self, seed: int):
+        self.bg = np.random.MT19937()
+        self.bg._legacy_seeding(seed)
+        self.pending = None
+
+    def peek(self) -> float:
+        if self.pending is None:
+            a, b = (float(v) for v in self.bg.random_raw(2))
+            u = (a + b * 4294967296.0) / 18446744073709551616.0
+            self.pending = u if u < 1.0 else float(np.nextafter(1.0, 0.0))
+        return self.pending
+
+    def consume(self) -> None:
+        self.pending = None
+
+
+SAMPLER_DEFAULTS = dict(temp=0.0, top_k=40, top_p=0.95, repeat_penalty=1.0, repeat_last_n=64)
+
+
+def oracle_sample(logits, recent=(), u=0.5, **params):
+    """oracle_sample on one row: (token id, whether u was used)."""
+    p = dict(SAMPLER_DEFAULTS, **params)
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    r = np.ascontiguousarray(recent, dtype=np.int32)
+    used = C.c_int32(0)
+    tok = oracle().oracle_sample(ptr(x), x.size, ptr(r), r.size, p["temp"], p["top_k"], p["top_p"],
+                                 p["repeat_penalty"], p["repeat_last_n"], u, C.byref(used))
+    return int(tok), bool(used.value)
+
+
+def oracle_sample_seq(logits, recent, seed, n_calls, **params):
+    """n_calls samples of the same row with one generator running on, as the reference's
+    decode loop calls sample()."""
+    d, out = Draws(seed), []
+    for _ in range(n_calls):
+        tok, used = oracle_sample(logits, recent, d.peek(), **params)
+        if used:
+            d.consume()
+        out.append(tok)
+    return out
+
+
+def ref_sampler():
+    """The reference's own init_sampler/sample (oracle/_ref/libref_sampler.so), or None."""
+    if not os.path.exists(REF_SAMPLER_SO):
+        return None
+    gl.libs()
+    lib = C.CDLL(REF_SAMPLER_SO)
+    lib.ref_sample_run.restype = C.c_int
+    lib.ref_sample_run.argtypes = [C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_float, C.c_int32, C.c_float,
+                                   C.c_float, C.c_int32, C.c_uint32, C.c_int, C.c_void_p]
+    return lib
+
+
+def ref_sample_seq(lib, logits, recent, seed, n_calls, **params):
+    p = dict(SAMPLER_DEFAULTS, **params)
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    r = np.ascontiguousarray(recent, dtype=np.int32)
+    out = np.zeros(n_calls, dtype=np.int32)
+    lib.ref_sample_run(ptr(x), x.size, ptr(r), r.size, p["temp"], p["top_k"], p["top_p"], p["repeat_penalty"],
+                       p["repeat_last_n"], seed, n_calls, ptr(out))
+    return [int(v) for v in out]
 
 
 def cpu_backend(n_threads: int = 8):
