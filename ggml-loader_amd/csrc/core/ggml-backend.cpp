@@ -126,6 +126,10 @@ enum ggml_status ggml_backend_graph_compute(ggml_backend_t backend, struct ggml_
     ggml_backend_synchronize(backend);
     return st;
 }
+enum ggml_status ggml_backend_graph_compute_async(ggml_backend_t backend, struct ggml_cgraph * cgraph) {
+    if (backend->iface.graph_compute_async) return backend->iface.graph_compute_async(backend, cgraph);
+    return backend->iface.graph_compute(backend, cgraph);
+}
 
 // ---- allocate every data-less tensor of a context in one buffer ----
 ggml_backend_buffer_t ggml_backend_alloc_ctx_tensors_from_buft(struct ggml_context * ctx, ggml_backend_buffer_type_t buft) {

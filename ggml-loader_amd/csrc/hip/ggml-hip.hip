@@ -167,7 +167,8 @@ struct buf_ctx {
 
 void buf_free(ggml_backend_buffer_t b) {
     buf_ctx * c = (buf_ctx *) b->context;
-    HIP_CHECK(hipSetDevice(c->device));
+    // queued kernels may still use the buffer (asynchronous graph computes)
+    HIP_CHECK(hipStreamSynchronize(dev(c->device).stream));
     HIP_CHECK(hipFree(c->base));
     delete c;
 }
@@ -1820,7 +1821,8 @@ void collect_profile(hip_backend_ctx * c) {
     c->event_next = 0;
 }
 
-enum ggml_status be_compute(ggml_backend_t b, ggml_cgraph * g) {
+// queues the graph's kernels on the device stream; a timed (profiled) compute also waits for them
+enum ggml_status be_compute_async(ggml_backend_t b, ggml_cgraph * g) {
     hip_backend_ctx * c = (hip_backend_ctx *) b->context;
     hip_device & d = dev(c->device);
     c->timing = c->profiling && (c->computes++ % c->profile_every) == 0;
@@ -1833,10 +1835,20 @@ enum ggml_status be_compute(ggml_backend_t b, ggml_cgraph * g) {
         e.launches++;
         e.ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     }
+    if (c->timing) {
+        HIP_CHECK(hipStreamSynchronize(d.stream));
+        drained(d);
+        collect_profile(c);
+    }
+    return GGML_STATUS_SUCCESS;
+}
+
+enum ggml_status be_compute(ggml_backend_t b, ggml_cgraph * g) {
+    const enum ggml_status st = be_compute_async(b, g);
+    hip_device & d = dev(((hip_backend_ctx *) b->context)->device);
     HIP_CHECK(hipStreamSynchronize(d.stream));
     drained(d);
-    if (c->timing) collect_profile(c);
-    return GGML_STATUS_SUCCESS;
+    return st;
 }
 
 // graph_compute with every kernel's scratch in this device's static array (no allocation)
@@ -1937,6 +1949,7 @@ ggml_backend_t ggml_backend_hip_init(int device) {
     b->iface.free = be_free;
     b->iface.get_default_buffer_type = be_buft;
     b->iface.graph_compute = be_compute;
+    b->iface.graph_compute_async = be_compute_async;
     b->iface.synchronize = be_sync;
     b->iface.set_eval_callback = be_set_eval_callback;
     b->context = c;

@@ -143,17 +143,28 @@ int gl_decode_loop(gl_session * s, int64_t n_past, int32_t first_token, int n_st
                    int32_t * tokens_out, double * seconds, char * err, size_t err_size) {
     try {
         if (first_token < 0 || first_token >= s->n_vocab) throw gl_error("token id out of range");
-        int32_t next = first_token;
-        // cmd_bench.cpp:52-61: time the n_tg loop of forward_step + argmax (the argmax of the last
-        // logits column runs on the backend, so a step reads back one index instead of n_vocab floats)
-        auto t0 = std::chrono::steady_clock::now();
-        for (int i = 0; i < n_steps; i++) {
-            const int64_t pos = fixed_pos ? n_past : n_past + i;
-            next = forward_step_greedy(s->m, s->hp, s->kv, s->ds, s->backend, pos, { next }, s->n_vocab);
-            if (tokens_out) tokens_out[i] = next;
+        if (n_steps < 1) throw gl_error("n_steps must be >= 1");
+        // cmd_bench.cpp:52-61: the n_tg loop of forward_step + argmax. The argmax of the last logits
+        // column runs on the backend and feeds the next step there (decode_chain), so the host
+        // queues step after step without waiting; the timed region ends when the last step is done.
+        decode_chain dc = init_decode_chain(s->backend, first_token, n_steps);
+        try {
+            ggml_backend_synchronize(s->backend);
+            auto t0 = std::chrono::steady_clock::now();
+            for (int i = 0; i < n_steps; i++) {
+                const int64_t pos = fixed_pos ? n_past : n_past + i;
+                forward_step_chained(s->m, s->hp, s->kv, s->ds, s->backend, pos, s->n_vocab, dc, i);
+            }
+            ggml_backend_synchronize(s->backend);
+            auto t1 = std::chrono::steady_clock::now();
+            if (seconds) *seconds = std::chrono::duration<double>(t1 - t0).count();
+            if (tokens_out) ggml_backend_tensor_get(dc.hist, tokens_out, 0, (size_t) n_steps * sizeof(int32_t));
+        } catch (...) {
+            ggml_backend_synchronize(s->backend);
+            free_decode_chain(dc);
+            throw;
         }
-        auto t1 = std::chrono::steady_clock::now();
-        if (seconds) *seconds = std::chrono::duration<double>(t1 - t0).count();
+        free_decode_chain(dc);
     } catch (const std::exception & e) {
         set_err(err, err_size, e.what());
         return 1;

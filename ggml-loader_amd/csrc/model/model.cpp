@@ -338,7 +338,8 @@ static size_t graph_size_of(const hparams & hp) {
 
 // model.cpp:1296-1474 (transformer archs)
 static built_graph build_graph(struct ggml_context * ctx, const model & m, const hparams & hp, kv_cache & kv,
-                               int64_t n_past, int64_t n_new, bool use_flash_attn) {
+                               int64_t n_past, int64_t n_new, bool use_flash_attn,
+                               struct ggml_tensor * tokens_in = nullptr) {
     built_graph bg{};
     bg.gf = ggml_new_graph_custom(ctx, graph_size_of(hp), false);
 
@@ -346,7 +347,7 @@ static built_graph build_graph(struct ggml_context * ctx, const model & m, const
     const int64_t n_kv     = n_past + n_new;
     const float   kq_scale = 1.0f / sqrtf((float) head_dim);
 
-    bg.tokens    = ggml_new_tensor_1d(ctx, GGML_TYPE_I32, n_new);
+    bg.tokens    = tokens_in ? tokens_in : ggml_new_tensor_1d(ctx, GGML_TYPE_I32, n_new);
     bg.positions = ggml_new_tensor_1d(ctx, GGML_TYPE_I32, n_new);
     bg.mask      = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, n_kv, n_new);
 
@@ -478,9 +479,16 @@ struct sample_job {
     int32_t token;
 };
 
+// a step of a device-fed greedy chain: its token is chain->tok, its argmax goes back there and to
+// chain->hist[index]
+struct chain_job {
+    decode_chain * chain;
+    int64_t index;
+};
+
 static void run_step(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds, ggml_backend_t backend,
                      int64_t n_past, const std::vector<int32_t> & new_tokens, int64_t n_vocab, float * logits_out,
-                     int32_t * greedy_out, sample_job * sj = nullptr) {
+                     int32_t * greedy_out, sample_job * sj = nullptr, chain_job * cj = nullptr) {
     const int64_t n_new = (int64_t) new_tokens.size();
     const int64_t n_kv  = n_past + n_new;
     if (n_new <= 0) throw gl_error("forward_step: no tokens");
@@ -489,9 +497,16 @@ static void run_step(const model & m, const hparams & hp, kv_cache & kv, decode_
     struct ggml_init_params gip = { ds.graph_buf.size(), ds.graph_buf.data(), /*.no_alloc =*/ true };
     struct ggml_context * gctx_build = ggml_init(gip);
 
-    built_graph bg = build_graph(gctx_build, m, hp, kv, n_past, n_new, ds.use_flash_attn);
+    built_graph bg = build_graph(gctx_build, m, hp, kv, n_past, n_new, ds.use_flash_attn, cj ? cj->chain->tok : nullptr);
     struct ggml_tensor * pick = nullptr;
-    if (greedy_out) {
+    if (cj) {
+        struct ggml_tensor * last = ggml_view_1d(gctx_build, bg.logits, n_vocab, (size_t) (n_new - 1) * bg.logits->nb[1]);
+        pick = ggml_argmax(gctx_build, last);
+        struct ggml_tensor * next = ggml_cpy(gctx_build, pick, cj->chain->tok);
+        struct ggml_tensor * rec = ggml_cpy(gctx_build, pick, ggml_view_1d(gctx_build, cj->chain->hist, 1, (size_t) cj->index * sizeof(int32_t)));
+        ggml_build_forward_expand(bg.gf, next);
+        ggml_build_forward_expand(bg.gf, rec);
+    } else if (greedy_out) {
         struct ggml_tensor * last = ggml_view_1d(gctx_build, bg.logits, n_vocab, (size_t) (n_new - 1) * bg.logits->nb[1]);
         pick = ggml_argmax(gctx_build, last);
         ggml_set_output(pick);
@@ -510,7 +525,7 @@ static void run_step(const model & m, const hparams & hp, kv_cache & kv, decode_
         throw gl_error("graph allocation failed");
     }
 
-    ggml_backend_tensor_set(bg.tokens, new_tokens.data(), 0, n_new * sizeof(int32_t));
+    if (!cj) ggml_backend_tensor_set(bg.tokens, new_tokens.data(), 0, n_new * sizeof(int32_t));
 
     std::vector<int32_t> positions(n_new);
     for (int64_t i = 0; i < n_new; i++) positions[i] = (int32_t) (n_past + i);
@@ -523,6 +538,12 @@ static void run_step(const model & m, const hparams & hp, kv_cache & kv, decode_
     }
     ggml_backend_tensor_set(bg.mask, mask.data(), 0, mask.size() * sizeof(float));
 
+    if (cj) {
+        // queued: the next step's graph is built while this one runs
+        ggml_backend_graph_compute_async(backend, bg.gf);
+        ggml_free(gctx_build);
+        return;
+    }
     ggml_backend_graph_compute(backend, bg.gf);
 
     if (sj) {
@@ -570,6 +591,35 @@ int32_t forward_step_greedy(const model & m, const hparams & hp, kv_cache & kv, 
     int32_t tok = 0;
     run_step(m, hp, kv, ds, backend, n_past, new_tokens, n_vocab, nullptr, &tok);
     return tok;
+}
+
+decode_chain init_decode_chain(ggml_backend_t backend, int32_t first_token, int64_t n_steps) {
+    decode_chain dc;
+    struct ggml_init_params ip = { 2 * ggml_tensor_overhead(), nullptr, /*.no_alloc =*/ true };
+    dc.ctx = ggml_init(ip);
+    dc.tok = ggml_new_tensor_1d(dc.ctx, GGML_TYPE_I32, 1);
+    dc.hist = ggml_new_tensor_1d(dc.ctx, GGML_TYPE_I32, std::max<int64_t>(n_steps, 1));
+    dc.buf = ggml_backend_alloc_ctx_tensors(dc.ctx, backend);
+    if (!dc.buf) {
+        ggml_free(dc.ctx);
+        throw gl_error("decode chain: allocation failed");
+    }
+    ggml_backend_tensor_set(dc.tok, &first_token, 0, sizeof(int32_t));
+    dc.n_steps = n_steps;
+    return dc;
+}
+
+void free_decode_chain(decode_chain & dc) {
+    if (dc.buf) ggml_backend_buffer_free(dc.buf);
+    if (dc.ctx) ggml_free(dc.ctx);
+    dc = decode_chain{};
+}
+
+void forward_step_chained(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds, ggml_backend_t backend,
+                          int64_t n_past, int64_t n_vocab, decode_chain & chain, int64_t index) {
+    if (index < 0 || index >= chain.n_steps) throw gl_error("forward_step_chained: step index out of range");
+    chain_job cj = { &chain, index };
+    run_step(m, hp, kv, ds, backend, n_past, { 0 }, n_vocab, nullptr, nullptr, nullptr, &cj);
 }
 
 // model.cpp:1668-1673

@@ -136,6 +136,24 @@ std::vector<float> prefill(const model & m, const hparams & hp, kv_cache & kv, d
 
 int32_t argmax(const std::vector<float> & logits);
 
+// A greedy decode fed on the device: the token of a step lives in a one-element device tensor
+// (tok) that the step's graph reads (get_rows) and overwrites with the argmax of its last logits
+// column (ggml_cpy), which is also copied into hist[index]. Each step is queued with
+// ggml_backend_graph_compute_async, so the host builds the next step while the device runs this
+// one and never waits in between; ggml_backend_synchronize then hist give the tokens, the ones
+// argmax(forward_step(...)) would have picked step by step.
+struct decode_chain {
+    struct ggml_context * ctx = nullptr;
+    ggml_backend_buffer_t buf = nullptr;
+    struct ggml_tensor * tok = nullptr;    // I32 [1]
+    struct ggml_tensor * hist = nullptr;   // I32 [n_steps]
+    int64_t n_steps = 0;
+};
+decode_chain init_decode_chain(ggml_backend_t backend, int32_t first_token, int64_t n_steps);
+void free_decode_chain(decode_chain & dc);
+void forward_step_chained(const model & m, const hparams & hp, kv_cache & kv, decode_session & ds, ggml_backend_t backend,
+                          int64_t n_past, int64_t n_vocab, decode_chain & chain, int64_t index);
+
 // model.h:410-430: sampling parameters (temp <= 0 is greedy) and state. The generator is the
 // reference's std::mt19937; a uniform variate it has produced for a draw stays pending until a
 // draw consumes it (the reference's generator is not advanced when no draw happens).

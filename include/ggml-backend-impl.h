@@ -55,6 +55,7 @@ struct ggml_backend_i {
     enum ggml_status (*graph_compute)(ggml_backend_t backend, struct ggml_cgraph * cgraph);
     void         (*synchronize)(ggml_backend_t backend); // may be NULL
     void         (*set_eval_callback)(ggml_backend_t backend, ggml_backend_eval_callback cb, void * user_data); // may be NULL
+    enum ggml_status (*graph_compute_async)(ggml_backend_t backend, struct ggml_cgraph * cgraph); // may be NULL
 };
 
 struct ggml_backend {

@@ -56,6 +56,10 @@ GGML_API ggml_backend_buffer_t      ggml_backend_alloc_buffer(ggml_backend_t bac
 GGML_API size_t ggml_backend_get_alignment(ggml_backend_t backend);
 GGML_API void   ggml_backend_synchronize(ggml_backend_t backend);
 GGML_API enum ggml_status ggml_backend_graph_compute(ggml_backend_t backend, struct ggml_cgraph * cgraph);
+// ggml's asynchronous variant: the graph's work is queued on the backend and may still run after
+// the call returns (ggml_backend_synchronize waits for it). Tensor uploads and later graphs on the
+// same backend are ordered after it. Backends without queued execution compute synchronously.
+GGML_API enum ggml_status ggml_backend_graph_compute_async(ggml_backend_t backend, struct ggml_cgraph * cgraph);
 
 // Called after a backend has computed a node (its data is complete and readable with
 // ggml_backend_tensor_get). `ask` is always false here; return false to stop reporting. Used by
