@@ -84,6 +84,34 @@ def oracle_helpers():
     return helpers
 
 
+def physical_cores():
+    """Distinct (physical id, core id) pairs of /proc/cpuinfo: the host's physical cores."""
+    cores, phys = set(), "0"
+    try:
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "physical id":
+                phys = v
+            elif k == "core id":
+                cores.add((phys, v))
+    except OSError:
+        pass
+    return len(cores) or (os.cpu_count() or 1)
+
+
+def cpu_threads():
+    """Thread counts of the CPU baseline: every core this process may use (its CPU affinity, at
+    most the host's physical cores and at most 16, the CPU share of a one-GPU box), then 8, the
+    reference's own count (cmd_bench.cpp:107)."""
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    n = max(1, min(16, allowed, physical_cores()))
+    return [n, 8] if n != 8 else [8]
+
+
 def cpu_baseline(gl, model_path, n_pos, tokens, seconds, threads):
     """The oracle (CPU restatement of ggml-cpu, this repository's oracle/) timed on the host cores
     on a bounded sample of the same workload: steps of len(tokens) new tokens at the same position,
@@ -113,6 +141,7 @@ def cpu_baseline(gl, model_path, n_pos, tokens, seconds, threads):
     v, n, t = runs[main_nt]
     what = "decode steps" if batch == 1 else f"{batch}-token steps"
     return {"value": round(v, 3), "unit": "tok/s", "cores": main_nt, "kind": "port",
+            "host_physical_cores": physical_cores(), "host_logical_cpus": os.cpu_count(),
             "sample": f"{n} {what} at position {n_pos} ({t:.1f}s) of the same synthetic model on the oracle/ "
                       f"CPU restatement of ggml-cpu (restated ggml-cpu semantics; upstream ggml unavailable offline), "
                       f"{main_nt} threads",
@@ -153,6 +182,36 @@ def summarize_pmc(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_mb,
             "fetch_size_bytes_per_dispatch": round(f), "write_size_bytes_per_dispatch": round(w),
             "fetch_scale": round(fs, 4), "write_scale": round(ws, 4),
             "copy_kernel_bytes": copy_bytes, "traffic_bytes_per_launch": round(f * fs + w * ws)}
+
+
+def summarize_pmc_all(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_mb):
+    """Per-kernel HBM bytes per dispatch from the same four rocprofv3 --pmc runs: every kernel name
+    (its text before the argument list) with its dispatch count, the scaled FETCH_SIZE and
+    WRITE_SIZE and their sum."""
+    import csv
+    import glob
+
+    def per_kernel(d):
+        acc = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+                v = acc.setdefault(name, [0, 0.0])
+                v[0] += 1
+                v[1] += float(r["Counter_Value"]) * 1024.0
+        return acc
+
+    copy_bytes = copy_mb * (1 << 20)
+    cf, cw = per_kernel(copy_fetch_dir), per_kernel(copy_write_dir)
+    fs = copy_bytes / (cf["cpy_kernel"][1] / cf["cpy_kernel"][0])
+    ws = copy_bytes / (cw["cpy_kernel"][1] / cw["cpy_kernel"][0])
+    f, w = per_kernel(fetch_dir), per_kernel(write_dir)
+    out = {}
+    for name, (n, tot) in sorted(f.items(), key=lambda kv: -kv[1][1]):
+        wn, wt = w.get(name, (n, 0.0))
+        fb, wb = tot / n * fs, wt / max(wn, 1) * ws
+        out[name] = {"dispatches": n, "fetch_bytes": round(fb), "write_bytes": round(wb), "traffic_bytes": round(fb + wb)}
+    return {"fetch_scale": round(fs, 4), "write_scale": round(ws, 4), "kernels": out}
 
 
 def copy_kernel(gl, mb, reps):
@@ -347,10 +406,15 @@ def main():
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
                     help="print the HBM bytes per launch of the dominant kernel from rocprofv3 --pmc runs")
     ap.add_argument("--copy-mb-of-pmc", type=int, default=256, help="size of the copy kernel of the calibration runs")
+    ap.add_argument("--pmc-prefix", default="void gemv_q_kernel<2,", help="kernel name prefix of --summarize-pmc")
+    ap.add_argument("--pmc-all", action="store_true", help="--summarize-pmc: every kernel's bytes per dispatch")
     args = ap.parse_args()
 
     if args.summarize_pmc:
-        print(json.dumps(summarize_pmc(*args.summarize_pmc, args.copy_mb_of_pmc, "void gemv_kernel<2,")), flush=True)
+        if args.pmc_all:
+            print(json.dumps(summarize_pmc_all(*args.summarize_pmc, args.copy_mb_of_pmc), indent=1), flush=True)
+        else:
+            print(json.dumps(summarize_pmc(*args.summarize_pmc, args.copy_mb_of_pmc, args.pmc_prefix)), flush=True)
         return
 
     if args.gpus != 1:
@@ -471,6 +535,20 @@ def decode_bench(gl, args):
                   f"{PROFILE_EVERY}th of {args.steps} steps run again right after the timed region "
                   f"({1000 * secs_ev / args.steps:.3f} ms/step with the events)",
     }
+    if "attn_decode" in prof:
+        # the layer's decode attention (scores, statistics, PV, combination launches together), from
+        # the breakdown steps; algorithmic bytes: the K and V rows read, Q in, the output out, the mask
+        n_a, ms_a, by_a = prof["attn_decode"]
+        a_ach = by_a / (ms_a * 1e-3) / 1e9 if ms_a > 0 else 0.0
+        aj = os.path.join(ROOT, "profiles", f"attn_{wname}_{args.config}_decode_traffic.json")
+        roofline["attention"] = {
+            "bound": "hbm", "achieved": round(a_ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(a_ach / PEAK_HBM_GBS, 4),
+            "traffic": json.load(open(aj))["traffic_bytes_per_layer"] if batch == 1 and os.path.exists(aj) else None,
+            "kernel": "decode attention of one layer (attn_scores + attn_stats + attn_pv + attn_combine)",
+            "us_per_layer": round(ms_a / n_a * 1e3, 2), "bytes_per_layer": round(by_a / n_a),
+            "timing": f"HIP events around each layer's attention launches in {args.breakdown_steps} untimed steps",
+        }
     if moe and batch > 1:
         roofline["bytes_note"] = ("mul_mat_id launches count the selected experts' bytes once per (token, slot) "
                                   "column, so repeated experts are counted again")
@@ -478,8 +556,7 @@ def decode_bench(gl, args):
     cpu = None
     if not args.no_cpu_baseline:
         try:
-            n_cpu = min(16, os.cpu_count() or 1)
-            cpu = cpu_baseline(gl, model_path, n_past, tokens, args.cpu_seconds, [n_cpu, 8] if n_cpu != 8 else [8])
+            cpu = cpu_baseline(gl, model_path, n_past, tokens, args.cpu_seconds, cpu_threads())
         except Exception as e:  # the baseline is reported, never required
             log(f"[bench] cpu baseline failed: {e}")
 
