@@ -813,6 +813,7 @@ void launch_gemv(const gemv_launch & L, hipStream_t st) {
         if (((uintptr_t) L.norm.x | (uintptr_t) L.norm.w) % 16 || L.norm.x_stride % 4) HIP_ABORT("gemv: RMSNorm prologue operands must be 16-byte aligned");
     }
     if (gemv_q_supported(L)) return launch_gemv_q(L, st);
+    if (gemv_q4k_enabled() && gemv_q4k_supported(L)) return launch_gemv_q4k(L, st);
     if (L.out_q.qs) HIP_ABORT("gemv: quantized SwiGLU output needs the Q4_0 / Q8_0 kernel");
     switch (L.type) {
         case GGML_TYPE_Q4_0:

@@ -161,6 +161,10 @@ void launch_gemv(const gemv_launch & L, hipStream_t st);
 // the single-column Q4_0 / Q8_0 kernel (k_gemv_q.hip), which launch_gemv uses when this holds
 bool gemv_q_supported(const gemv_launch & L);
 void launch_gemv_q(const gemv_launch & L, hipStream_t st);
+// the single-column Q4_K kernel (k_gemv_q4k.hip), likewise (GGML_HIP_NO_Q4K_GEMV=1 turns it off)
+bool gemv_q4k_enabled();
+bool gemv_q4k_supported(const gemv_launch & L);
+void launch_gemv_q4k(const gemv_launch & L, hipStream_t st);
 // Several activation columns per workgroup (k_gemv_mc.hip): each weight row block is read once for
 // up to GEMV_MC_MAX_COLS columns; the activation must be quantized already (L.xq, no L.norm). With
 // groups (mul_mat_id): the workgroups of expert e take the columns the ids route to e, listed by
