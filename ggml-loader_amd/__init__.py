@@ -222,7 +222,6 @@ def _declare(core, hip, loader):
     _sig(hip, "ggml_backend_hip_sample", i32, vp, vp, i64, C.POINTER(ggml_hip_sampler_params), vp, sz,
          C.c_double, C.POINTER(C.c_int32), C.POINTER(C.c_bool))
     _sig(hip, "ggml_backend_hip_set_fusion", None, vp, C.c_bool)
-    _sig(hip, "ggml_backend_hip_set_graph_replay", None, vp, C.c_bool)
     _sig(hip, "ggml_backend_hip_set_profiling", None, vp, C.c_bool)
     _sig(hip, "ggml_backend_hip_set_profile_filter", None, vp, C.c_char_p)
     _sig(hip, "ggml_backend_hip_set_profile_sampling", None, vp, i32)

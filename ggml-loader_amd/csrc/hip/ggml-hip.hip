@@ -342,7 +342,6 @@ struct hip_backend_ctx {
     int device = 0;
     bool fusion = true;
     int fuse_mask = FUSE_ALL;
-    bool graph_replay = true;
     bool profiling = false;
     int profile_every = 1;           // time one graph compute in every profile_every
     int64_t computes = 0;
@@ -2071,9 +2070,6 @@ enum ggml_status ggml_backend_hip_sample(ggml_backend_t backend, const struct gg
 
 void ggml_backend_hip_set_fusion(ggml_backend_t backend, bool enable) {
     if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->fusion = enable;
-}
-void ggml_backend_hip_set_graph_replay(ggml_backend_t backend, bool enable) {
-    if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->graph_replay = enable;
 }
 void ggml_backend_hip_set_profiling(ggml_backend_t backend, bool enable) {
     if (ggml_backend_is_hip(backend)) ((hip_backend_ctx *) backend->context)->profiling = enable;

@@ -70,9 +70,6 @@ GGML_API enum ggml_status ggml_backend_hip_sample(ggml_backend_t backend, const 
 // decode attention). On by default; off runs one kernel per ggml node. Used by the parity tests
 // to check both paths against the oracle.
 GGML_API void ggml_backend_hip_set_fusion(ggml_backend_t backend, bool enable);
-// Reserved for replaying the per-token launch sequence through a captured HIP graph. This build
-// stores the flag and launches every kernel from the host either way.
-GGML_API void ggml_backend_hip_set_graph_replay(ggml_backend_t backend, bool enable);
 
 // Per-kernel timing with HIP events recorded on the backend's own stream. While enabled, every
 // launch of graph_compute is bracketed by events; stats accumulate per kernel name until reset.
