@@ -16,7 +16,8 @@ import os
 import subprocess
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_DIR = os.path.join(PKG_DIR, "lib")
+# GGML_LOADER_LIB_DIR: another build of the same libraries (the sanitized one, _asan/lib)
+LIB_DIR = os.environ.get("GGML_LOADER_LIB_DIR") or os.path.join(PKG_DIR, "lib")
 BIN_DIR = os.path.join(PKG_DIR, "bin")
 
 # ggml type ids (GGUF on-disk ids)

@@ -159,33 +159,66 @@ static int cmd_synth(int argc, char ** argv) {
     return 0;
 }
 
-static int cmd_inspect(int argc, char ** argv) {
-    if (argc < 3) { fprintf(stderr, "usage: ggml-loader inspect <model.gguf>\n"); return 1; }
-    gguf_init_params gp = { true, nullptr };
-    gguf_context * g = gguf_init_from_file(argv[2], gp);
-    if (!g) return 1;
-    printf("gguf v%u, %lld kv, %lld tensors, alignment %zu, data offset %zu\n", gguf_get_version(g), (long long) gguf_get_n_kv(g),
-           (long long) gguf_get_n_tensors(g), gguf_get_alignment(g), gguf_get_data_offset(g));
-    for (int64_t i = 0; i < gguf_get_n_kv(g); i++) {
-        const enum gguf_type t = gguf_get_kv_type(g, i);
-        printf("  %-48s %-5s ", gguf_get_key(g, i), gguf_type_name(t));
-        switch (t) {
-            case GGUF_TYPE_STRING: printf("%s", gguf_get_val_str(g, i)); break;
-            case GGUF_TYPE_UINT32: printf("%u", gguf_get_val_u32(g, i)); break;
-            case GGUF_TYPE_INT32: printf("%d", gguf_get_val_i32(g, i)); break;
-            case GGUF_TYPE_FLOAT32: printf("%g", gguf_get_val_f32(g, i)); break;
-            case GGUF_TYPE_UINT64: printf("%llu", (unsigned long long) gguf_get_val_u64(g, i)); break;
-            case GGUF_TYPE_BOOL: printf("%s", gguf_get_val_bool(g, i) ? "true" : "false"); break;
-            case GGUF_TYPE_ARRAY: printf("[%zu x %s]", gguf_get_arr_n(g, i), gguf_type_name(gguf_get_arr_type(g, i))); break;
-            default: printf("..."); break;
+// cmd_inspect.cpp:11-38: the value column of a metadata key (integers and floats as
+// std::to_string prints them, strings cut to 77 characters + "..." past 80, arrays as
+// array<type>[n])
+static std::string inspect_value(const gguf_context * g, int64_t i) {
+    switch (gguf_get_kv_type(g, i)) {
+        case GGUF_TYPE_UINT8:   return std::to_string(gguf_get_val_u8(g, i));
+        case GGUF_TYPE_INT8:    return std::to_string(gguf_get_val_i8(g, i));
+        case GGUF_TYPE_UINT16:  return std::to_string(gguf_get_val_u16(g, i));
+        case GGUF_TYPE_INT16:   return std::to_string(gguf_get_val_i16(g, i));
+        case GGUF_TYPE_UINT32:  return std::to_string(gguf_get_val_u32(g, i));
+        case GGUF_TYPE_INT32:   return std::to_string(gguf_get_val_i32(g, i));
+        case GGUF_TYPE_FLOAT32: return std::to_string(gguf_get_val_f32(g, i));
+        case GGUF_TYPE_UINT64:  return std::to_string(gguf_get_val_u64(g, i));
+        case GGUF_TYPE_INT64:   return std::to_string(gguf_get_val_i64(g, i));
+        case GGUF_TYPE_FLOAT64: return std::to_string(gguf_get_val_f64(g, i));
+        case GGUF_TYPE_BOOL:    return gguf_get_val_bool(g, i) ? "true" : "false";
+        case GGUF_TYPE_STRING: {
+            const std::string v = gguf_get_val_str(g, i);
+            return v.size() > 80 ? v.substr(0, 77) + "..." : v;
         }
-        printf("\n");
+        case GGUF_TYPE_ARRAY:
+            return "array<" + std::string(gguf_type_name(gguf_get_arr_type(g, i))) + ">[" +
+                   std::to_string(gguf_get_arr_n(g, i)) + "]";
+        default:
+            return "?";
     }
-    for (int64_t i = 0; i < gguf_get_n_tensors(g); i++) {
-        printf("  %-40s %-6s [", gguf_get_tensor_name(g, i), ggml_type_name(gguf_get_tensor_type(g, i)));
-        for (int d = 0; d < gguf_get_tensor_n_dims(g, i); d++) printf(d ? ", %lld" : "%lld", (long long) gguf_get_tensor_ne(g, i)[d]);
-        printf("] %zu bytes @ %zu\n", gguf_get_tensor_size(g, i), gguf_get_tensor_offset(g, i));
+}
+
+// cmd_inspect.cpp:41-90: file header, metadata keys, tensor directory, total tensor bytes, in the
+// reference's layout (a model given as a file path; Ollama references are not resolved here)
+static int cmd_inspect(int argc, char ** argv) {
+    if (argc != 3) {
+        fprintf(stderr, "usage: %s <model.gguf>\n", argv[1]);
+        return 1;
     }
+    const char * path = argv[2];
+    gguf_init_params gp = { true, nullptr };
+    gguf_context * g = gguf_init_from_file(path, gp);
+    if (!g) {
+        fprintf(stderr, "error: failed to load '%s' as GGUF\n", path);
+        return 1;
+    }
+    printf("file:      %s\n", path);
+    printf("version:   %u\n", gguf_get_version(g));
+    printf("alignment: %zu\n", gguf_get_alignment(g));
+    const int64_t n_kv = gguf_get_n_kv(g);
+    printf("\n-- metadata (%lld keys) --\n", (long long) n_kv);
+    for (int64_t i = 0; i < n_kv; i++) printf("  %-40s = %s\n", gguf_get_key(g, i), inspect_value(g, i).c_str());
+    const int64_t n_t = gguf_get_n_tensors(g);
+    size_t total = 0;
+    printf("\n-- tensors (%lld) --\n", (long long) n_t);
+    for (int64_t i = 0; i < n_t; i++) {
+        const int64_t * ne = gguf_get_tensor_ne(g, i);
+        const size_t size = gguf_get_tensor_size(g, i);
+        total += size;
+        printf("  %-40s %6s  [%5lld, %5lld, %5lld, %5lld]  %10zu bytes\n", gguf_get_tensor_name(g, i),
+               ggml_type_name(gguf_get_tensor_type(g, i)), (long long) ne[0], (long long) ne[1], (long long) ne[2],
+               (long long) ne[3], size);
+    }
+    printf("\ntotal tensor data: %.2f MiB\n", total / 1024.0 / 1024.0);
     gguf_free(g);
     return 0;
 }

@@ -15,7 +15,8 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG_INIT = os.path.join(ROOT, "ggml-loader_amd", "__init__.py")
-ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "libggml-cpu-oracle.so")
+# GGML_LOADER_ORACLE_SO: another build of the oracle (the sanitized one, oracle/_asan)
+ORACLE_SO = os.environ.get("GGML_LOADER_ORACLE_SO") or os.path.join(ROOT, "oracle", "_build", "libggml-cpu-oracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libmoe_ref.so")
 REF_SAMPLER_SO = os.path.join(ROOT, "oracle", "_ref", "libref_sampler.so")
 GOLDEN = os.path.join(ROOT, "tests", "golden")
