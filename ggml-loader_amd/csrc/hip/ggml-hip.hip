@@ -1113,7 +1113,10 @@ private:
             }
         }
         {
-            prof_scope ps(this, w->type == GGML_TYPE_Q4_0 ? "gemm_q4_0" : w->type == GGML_TYPE_Q4_K ? "gemm_q4_K" : "gemm_q8_0", bytes);
+            // named with the workgroup tile, e.g. gemm_q8_0_2x4x2
+            const std::string pname = std::string(w->type == GGML_TYPE_Q4_0 ? "gemm_q4_0" : w->type == GGML_TYPE_Q4_K ? "gemm_q4_K" : "gemm_q8_0") +
+                                      "_" + gemm_tile_name(G);
+            prof_scope ps(this, pname.c_str(), bytes);
             launch_gemm(G, st_);
         }
         wrote_.push_back(written);

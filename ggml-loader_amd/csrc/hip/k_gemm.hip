@@ -504,18 +504,41 @@ void launch_gemm_t(const gemm_launch & G, hipStream_t st) {
 
 int64_t n_tiles(const gemm_launch & G, int bm, int bn) { return ((G.n_rows + bm - 1) / bm) * ((G.ncols + bn - 1) / bn); }
 
+// The workgroup tile of a launch. Q4_0 / Q8_0: the largest tile that still gives every CU two
+// workgroups (Q4_0) or four (Q8_0, whose staging moves twice the weight bytes per block; measured:
+// Phi-3 prefill 26.1 -> 24.9 ms, while Q4_0 is slower with the smaller tiles). Q4_K: 64 x 64 tiles
+// where they give every CU a workgroup, else 32 x 64 (measured: the larger tile is faster down to
+// one workgroup per CU).
+enum gemm_tile { TILE_4x4x2, TILE_2x4x2, TILE_1x2x4, TILE_Q4K_2x2, TILE_Q4K_1x2 };
+
+gemm_tile tile_of(const gemm_launch & G) {
+    if (G.type == GGML_TYPE_Q4_K) return n_tiles(G, 64, 64) >= 256 ? TILE_Q4K_2x2 : TILE_Q4K_1x2;
+    const int64_t target = G.type == GGML_TYPE_Q8_0 ? 1024 : 512;
+    if (n_tiles(G, 128, 128) >= target) return TILE_4x4x2;
+    if (n_tiles(G, 64, 128) >= target) return TILE_2x4x2;
+    return TILE_1x2x4;
+}
+
 template <int TYPE>
 void launch_gemm_type(const gemm_launch & G, hipStream_t st) {
-    // the largest workgroup tile that still gives every CU two workgroups (Q4_0) or four (Q8_0,
-    // whose staging moves twice the weight bytes per block; measured: Phi-3 prefill 26.1 -> 24.9 ms,
-    // while Q4_0 is slower with the smaller tiles)
-    constexpr int64_t target = TYPE == GGML_TYPE_Q8_0 ? 1024 : 512;
-    if (n_tiles(G, 128, 128) >= target) launch_gemm_t<TYPE, 4, 4, 2>(G, st);
-    else if (n_tiles(G, 64, 128) >= target) launch_gemm_t<TYPE, 2, 4, 2>(G, st);
-    else launch_gemm_t<TYPE, 1, 2, 4>(G, st);
+    switch (tile_of(G)) {
+        case TILE_4x4x2: launch_gemm_t<TYPE, 4, 4, 2>(G, st); break;
+        case TILE_2x4x2: launch_gemm_t<TYPE, 2, 4, 2>(G, st); break;
+        default: launch_gemm_t<TYPE, 1, 2, 4>(G, st); break;
+    }
 }
 
 } // namespace
+
+const char * gemm_tile_name(const gemm_launch & G) {
+    switch (tile_of(G)) {
+        case TILE_4x4x2: return "4x4x2";
+        case TILE_2x4x2: return "2x4x2";
+        case TILE_1x2x4: return "1x2x4";
+        case TILE_Q4K_2x2: return "2x2";
+        default: return "1x2";
+    }
+}
 
 bool gemm_supported(int type, int64_t K, int64_t n_rows) {
     if (type == GGML_TYPE_Q4_K) return K > 0 && K % 256 == 0 && n_rows > 0;
@@ -533,9 +556,7 @@ void launch_gemm(const gemm_launch & G, hipStream_t st) {
     }
     if (G.type == GGML_TYPE_Q4_K) {
         if (!G.xbs || ((uintptr_t) G.xbs % 8) || ((uintptr_t) G.xd % 4)) HIP_ABORT("gemm: Q4_K needs Q8_K columns with 8-byte aligned bsums");
-        // 64 x 64 tiles where they give every CU a workgroup, else 32 x 64 (measured: the larger
-        // tile is faster down to one workgroup per CU)
-        if (n_tiles(G, 64, 64) >= 256) launch_gemm_q4k_t<2, 2>(G, st);
+        if (tile_of(G) == TILE_Q4K_2x2) launch_gemm_q4k_t<2, 2>(G, st);
         else launch_gemm_q4k_t<1, 2>(G, st);
         return;
     }

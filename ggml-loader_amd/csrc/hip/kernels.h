@@ -97,6 +97,9 @@ struct gemm_launch {
 
 bool gemm_supported(int type, int64_t K, int64_t n_rows);
 void launch_gemm(const gemm_launch & G, hipStream_t st);
+// the workgroup tile launch_gemm picks (kernel template arguments: "4x4x2", "2x4x2", "1x2x4" for
+// Q4_0 / Q8_0 warp tiles x k-blocks; "2x2", "1x2" for Q4_K), for profile names
+const char * gemm_tile_name(const gemm_launch & G);
 
 // Activation prologue of a GEMV: every workgroup quantizes its column of x itself, either as
 // rms_norm(x) * w (rms set: ggml's rms_norm -> mul -> quantize_row_q8_0 / q8_K chain, same

@@ -147,7 +147,7 @@ def profiled(hip, fn):
     (gl.Q4_0, 256, 100),     # rows end inside a 16-row tile
     (gl.Q8_0, 128, 4),       # one row group, one 4-block step
     (gl.Q8_0, 384, 36),
-    (gl.Q4_K, 2560, 1024),   # Qwen3-shape rows, 64 x 64 tiles
+    (gl.Q4_K, 2560, 1024),   # Qwen3-shape rows (32 x 64 tiles: at most 128 of 64 x 64)
     (gl.Q4_K, 4096, 72),     # 32 x 64 tiles, rows end inside a 16-row tile
     (gl.Q4_K, 256, 100),     # one super-block per row
 ])
@@ -166,6 +166,34 @@ def test_gemm_prefill(hip, cpu, qtype, K, N, ncols):
     a, names = profiled(hip, lambda: run_on(hip, build))
     b = run_on(cpu, build)
     assert any(n.startswith("gemm_") for n in names), names
+    assert np.array_equal(a, b), rel_err(a, b)
+
+
+@pytest.mark.parametrize("qtype,K,N,ncols,tile", [
+    (gl.Q4_0, 128, 16384, 512, "4x4x2"),     # 128 x 128 tiles: 512 of them
+    (gl.Q4_0, 128, 16424, 529, "4x4x2"),     # partial row and column tiles of the largest shape
+    (gl.Q4_0, 128, 8192, 512, "2x4x2"),      # 64 x 128 tiles: 512
+    (gl.Q8_0, 128, 16384, 512, "2x4x2"),     # Q8_0 wants 1024 tiles: 64 x 128 ones
+    (gl.Q8_0, 128, 16400, 520, "2x4x2"),
+    (gl.Q8_0, 128, 32768, 512, "4x4x2"),     # 1024 tiles of 128 x 128
+    (gl.Q8_0, 256, 4096, 512, "1x2x4"),      # below both thresholds
+    (gl.Q4_K, 256, 4096, 512, "2x2"),        # 64 x 64 tiles: 512 (>= 256)
+    (gl.Q4_K, 512, 4120, 515, "2x2"),        # partial tiles, two super-blocks per row
+    (gl.Q4_K, 256, 1024, 512, "1x2"),        # 128 tiles of 64 x 64: 32 x 64 instead
+])
+def test_gemm_tile_variants(hip, cpu, qtype, K, N, ncols, tile):
+    """Each workgroup tile of the prefill GEMM (the launch picks it from the tile count), pinned by
+    the profile name and bit-exact against the oracle; small K keeps the oracle cheap."""
+    w = qweight(qtype, K, N, K + 7 * N + ncols)
+    x = rng(K + ncols + 5).standard_normal((ncols, K)).astype(np.float32)
+
+    def build(g):
+        return g.mul_mat(g.tensor(qtype, K, N, data=w), g.tensor(gl.F32, K, ncols, data=x))
+
+    a, names = profiled(hip, lambda: run_on(hip, build))
+    b = run_on(cpu, build)
+    gemm = [n for n in names if n.startswith("gemm_")]
+    assert gemm and all(n.endswith("_" + tile) for n in gemm), (gemm, tile)
     assert np.array_equal(a, b), rel_err(a, b)
 
 
@@ -198,7 +226,7 @@ def test_gemm_q4k_extreme_blocks(hip, cpu, sign):
 
     a, names = profiled(hip, lambda: run_on(hip, build))
     b = run_on(cpu, build)
-    assert "gemm_q4_K" in names, names
+    assert any(n.startswith("gemm_q4_K") for n in names), names
     assert np.array_equal(a, b), rel_err(a, b)
 
 
