@@ -363,9 +363,42 @@ int oracle_dequantize(int type, const void * vx, float * y, int64_t k) {
 /* ------------------------------------------------------------------------------------------ */
 /* block dots (ggml_vec_dot_*_generic)                                                        */
 
+/* Experiment hook (tests/exactness_experiment.py only): the order in which the Q4_0 / Q8_0 dots
+   add their block terms. 0 (the default, and the oracle's definition) is ggml-cpu's generic order,
+   sumf += term block by block. 1 is a 32-lane wave reduction: lane l adds blocks l, l + 32, ... in
+   order, then the lanes are added pairwise (l + 16 into l, then l + 8, ... 1). The block terms
+   themselves are the same floats in both. */
+static int g_block_sum_order = 0;
+void oracle_set_block_sum_order(int mode) { g_block_sum_order = mode; }
+
+static float sum_block_terms(const float * t, int64_t n) {
+    if (g_block_sum_order == 0) {
+        float s = 0;
+        for (int64_t i = 0; i < n; i++) s += t[i];
+        return s;
+    }
+    float p[32] = { 0 };
+    for (int64_t i = 0; i < n; i++) p[i % 32] += t[i];
+    for (int o = 16; o >= 1; o >>= 1) {
+        for (int l = 0; l < o; l++) p[l] = p[l] + p[l + o];
+    }
+    return p[0];
+}
+
 float oracle_vec_dot_q4_0_q8_0(int64_t n, const void * vx, const void * vy) {
     const bq4_0 * x = (const bq4_0 *) vx;
     const bq8_0 * y = (const bq8_0 *) vy;
+    if (g_block_sum_order != 0) {
+        float * t = (float *) malloc((size_t) (n / 32) * sizeof(float));
+        for (int64_t ib = 0; ib < n / 32; ++ib) {
+            int sumi = 0;
+            for (int j = 0; j < 16; ++j) sumi += ((x[ib].qs[j] & 0x0F) - 8) * y[ib].qs[j] + ((x[ib].qs[j] >> 4) - 8) * y[ib].qs[j + 16];
+            t[ib] = sumi * F16(x[ib].d) * F16(y[ib].d);
+        }
+        const float s = sum_block_terms(t, n / 32);
+        free(t);
+        return s;
+    }
     float sumf = 0;
     for (int64_t ib = 0; ib < n / 32; ++ib) {
         int sumi0 = 0, sumi1 = 0;
@@ -384,6 +417,17 @@ float oracle_vec_dot_q4_0_q8_0(int64_t n, const void * vx, const void * vy) {
 float oracle_vec_dot_q8_0_q8_0(int64_t n, const void * vx, const void * vy) {
     const bq8_0 * x = (const bq8_0 *) vx;
     const bq8_0 * y = (const bq8_0 *) vy;
+    if (g_block_sum_order != 0) {
+        float * t = (float *) malloc((size_t) (n / 32) * sizeof(float));
+        for (int64_t ib = 0; ib < n / 32; ++ib) {
+            int sumi = 0;
+            for (int j = 0; j < 32; j++) sumi += x[ib].qs[j] * y[ib].qs[j];
+            t[ib] = sumi * (F16(x[ib].d) * F16(y[ib].d));
+        }
+        const float s = sum_block_terms(t, n / 32);
+        free(t);
+        return s;
+    }
     float sumf = 0;
     for (int64_t ib = 0; ib < n / 32; ++ib) {
         int sumi = 0;
@@ -1074,7 +1118,7 @@ static void op_mul_mat(struct ggml_tensor * dst, const struct ggml_tensor * src0
     // (each output is the same row_dot either way)
     const int64_t TR = 16, TC = 64;
     const int64_t nrt = (nr + TR - 1) / TR, nct = (ncols + TC - 1) / TC;
-    if ((wt == GGML_TYPE_Q4_0 || wt == GGML_TYPE_Q8_0) && ncols >= 8) {
+    if ((wt == GGML_TYPE_Q4_0 || wt == GGML_TYPE_Q8_0) && ncols >= 8 && g_block_sum_order == 0) {
         mul_mat_q_tiled(dst, src0, src1, wdata, drs, nth);
         free(wdata);
         return;

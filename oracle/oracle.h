@@ -81,6 +81,10 @@ void oracle_rope(float * dst, const float * src, int64_t ne0, int n_dims, int mo
    logits, top-k by insertion (ties keep the lower id), renormalize the k weights */
 void oracle_moe_route(const float * logits, int n_expert, int top_k, int32_t * ids, float * w);
 
+/* experiment hook: the order of the Q4_0 / Q8_0 dots' block-term sums (0 = ggml-cpu's block
+   order, the default; 1 = a 32-lane wave reduction), tests/exactness_experiment.py only */
+void oracle_set_block_sum_order(int mode);
+
 /* sample() (model.cpp:1675-1728) on n logits with the window recent[0..n_recent) and the
    uniform variate u of the weighted draw; *used_draw = 1 when the draw consumed u. Equal logits
    order by ascending id. Returns the token id, or -1 when temp > 0 and the largest logit is not
