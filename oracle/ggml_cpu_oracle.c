@@ -371,6 +371,14 @@ int oracle_dequantize(int type, const void * vx, float * y, int64_t k) {
 static int g_block_sum_order = 0;
 void oracle_set_block_sum_order(int mode) { g_block_sum_order = mode; }
 
+/* Test hook (tests/test_ref_qwen.py only): plants a known attention mistake so that a test can show
+   its fixture catches it. 0, the default, plants nothing. Bit 1: a query head h reads KV head
+   h % n_head_kv instead of h / (n_head / n_head_kv) (mul_mat's and flash_attn_ext's head
+   broadcast). Bit 2: rope rotates the other pairing (NEOX's (i, i + n_dims/2) and NORMAL's
+   (2i, 2i + 1) exchanged). Bit 4: soft_max and flash_attn_ext drop the scale (1/sqrt(head_dim)). */
+static int g_planted = 0;
+void oracle_set_planted(int bits) { g_planted = bits; }
+
 static float sum_block_terms(const float * t, int64_t n) {
     if (g_block_sum_order == 0) {
         float s = 0;
@@ -949,6 +957,7 @@ static void op_soft_max(struct ggml_tensor * dst, const struct ggml_tensor * a, 
     float scale, max_bias;
     memcpy(&scale, &dst->op_params[0], 4);
     memcpy(&max_bias, &dst->op_params[1], 4);
+    if (g_planted & 4) scale = 1.0f;
     const int64_t nc = a->ne[0];
     const uint32_t n_head = (uint32_t) a->ne[2];
     const uint32_t n_head_log2 = n_head ? 1u << (uint32_t) floor(log2((double) n_head)) : 1u;
@@ -1010,7 +1019,7 @@ static void op_rope(struct ggml_tensor * dst, const struct ggml_tensor * a, cons
         for (int64_t i1 = 0; i1 < a->ne[1]; i1++) {
             for (int64_t i0 = 0; i0 < ne0; i0++) tmp[i0] = load_f(a, ELEM(a, i0, i1, i2, i3));
             float * out = (float *) malloc((size_t) ne0 * sizeof(float));
-            rope_apply(out, tmp, ne0, n_dims, mode, cache);
+            rope_apply(out, tmp, ne0, n_dims, g_planted & 2 ? mode ^ GGML_ROPE_TYPE_NEOX : mode, cache);
             for (int64_t i0 = 0; i0 < ne0; i0++) store_f(dst, ELEM(dst, i0, i1, i2, i3), out[i0]);
             free(out);
         }
@@ -1129,7 +1138,8 @@ static void op_mul_mat(struct ggml_tensor * dst, const struct ggml_tensor * src0
         for (int64_t c = ct * TC; c < ncols && c < (ct + 1) * TC; c++) {
             const int64_t i11 = c % n1, i12 = (c / n1) % n2, i13 = c / (n1 * n2);
             for (int64_t i01 = rt * TR; i01 < nr && i01 < (rt + 1) * TR; i01++) {
-                const char * w = (const char *) src0->data + i01 * src0->nb[1] + (i12 / r2) * src0->nb[2] + (i13 / r3) * src0->nb[3];
+                const int64_t i02 = g_planted & 1 ? i12 % src0->ne[2] : i12 / r2;
+                const char * w = (const char *) src0->data + i01 * src0->nb[1] + i02 * src0->nb[2] + (i13 / r3) * src0->nb[3];
                 *(float *) ELEM(dst, i01, i11, i12, i13) = row_dot(wt, w, wdata + drs * (size_t) c, K);
             }
         }
@@ -1175,6 +1185,7 @@ static void op_flash_attn(struct ggml_tensor * dst, const struct ggml_tensor * q
     memcpy(&scale, &dst->op_params[0], 4);
     memcpy(&max_bias, &dst->op_params[1], 4);
     memcpy(&softcap, &dst->op_params[2], 4);
+    if (g_planted & 4) scale = 1.0f;
     const int64_t D = q->ne[0], DV = v->ne[0], n_kv = k->ne[1];
     const int64_t rk2 = q->ne[2] / k->ne[2], rv2 = q->ne[2] / v->ne[2];
     #pragma omp parallel for collapse(3) num_threads(nth) schedule(static)
@@ -1189,7 +1200,7 @@ static void op_flash_attn(struct ggml_tensor * dst, const struct ggml_tensor * q
             const float mv = mask ? load_f(mask, (const char *) mask->data + ic * mask->nb[0] + iq1 * mask->nb[1]) : 0.0f;
             if (mv == -INFINITY) continue;
             ggml_float s = 0.0;
-            for (int64_t i = 0; i < D; i++) s += (ggml_float) (load_f(k, ELEM(k, i, ic, iq2 / rk2, iq3)) * F16(q16[i]));
+            for (int64_t i = 0; i < D; i++) s += (ggml_float) (load_f(k, ELEM(k, i, ic, g_planted & 1 ? iq2 % k->ne[2] : iq2 / rk2, iq3)) * F16(q16[i]));
             float sf = (float) s * scale;
             if (softcap != 0.0f) sf = softcap * tanhf(sf / softcap);
             sf += mv;
@@ -1202,7 +1213,7 @@ static void op_flash_attn(struct ggml_tensor * dst, const struct ggml_tensor * q
             } else {
                 vs = exp_cr(sf - M);
             }
-            for (int64_t i = 0; i < DV; i++) acc[i] += load_f(v, ELEM(v, i, ic, iq2 / rv2, iq3)) * vs;
+            for (int64_t i = 0; i < DV; i++) acc[i] += load_f(v, ELEM(v, i, ic, g_planted & 1 ? iq2 % v->ne[2] : iq2 / rv2, iq3)) * vs;
             S = S * ms + vs;
         }
         const float inv = S == 0.0f ? 0.0f : 1.0f / S;

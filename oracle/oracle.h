@@ -30,7 +30,13 @@
  *   rope                       reference sc_rope golden (NEOX); position 0 identity; pair norms;
  *                              theta_0 = pos; NORMAL == NEOX on interleaved pairs; partial dims
  *   attention chain            n_kv = 1 -> V; equal keys -> mean of V (exact); fp64 GQA brute force
- *                              that also rejects the h % n_head_kv mapping
+ *                              that also rejects the h % n_head_kv mapping; the reference MoE
+ *                              engine's own qwen3moe forward (qwen_model.c attention_block: q/k
+ *                              norms, NEOX rope, f32 KV, GQA) built by Makefile.ref: logits of 32
+ *                              decode steps at 32/4 heads x 128 within 1e-3 (F32 matrices) or
+ *                              2.5e-2 median / 1e-1 (Q4_K), fixtures made by
+ *                              tests/golden/make_qwen_ref.py; a planted head mapping, rope pairing
+ *                              or dropped softmax scale (oracle_set_planted) fails that check
  *   moe_route                  brute-force top-k (ties -> lower id) and renormalized softmax
  *   sample                     the reference's own sample() built from model.cpp (Makefile.ref):
  *                              identical ids over seeded draw sequences on tie-free logits, and the
@@ -84,6 +90,11 @@ void oracle_moe_route(const float * logits, int n_expert, int top_k, int32_t * i
 /* experiment hook: the order of the Q4_0 / Q8_0 dots' block-term sums (0 = ggml-cpu's block
    order, the default; 1 = a 32-lane wave reduction), tests/exactness_experiment.py only */
 void oracle_set_block_sum_order(int mode);
+
+/* test hook: plants a known attention mistake (0 = none, the default; bit 1 = query head h reads
+   KV head h % n_head_kv; bit 2 = rope's NEOX and NORMAL pairings exchanged; bit 4 = soft_max and
+   flash_attn_ext without their scale), tests/test_ref_qwen.py only */
+void oracle_set_planted(int bits);
 
 /* sample() (model.cpp:1675-1728) on n logits with the window recent[0..n_recent) and the
    uniform variate u of the weighted draw; *used_draw = 1 when the draw consumed u. Equal logits

@@ -19,6 +19,7 @@ PKG_INIT = os.path.join(ROOT, "ggml-loader_amd", "__init__.py")
 ORACLE_SO = os.environ.get("GGML_LOADER_ORACLE_SO") or os.path.join(ROOT, "oracle", "_build", "libggml-cpu-oracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libmoe_ref.so")
 REF_SAMPLER_SO = os.path.join(ROOT, "oracle", "_ref", "libref_sampler.so")
+REF_QWEN_SO = os.path.join(ROOT, "oracle", "_ref", "libqwen_ref.so")
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
@@ -143,6 +144,42 @@ def ref_sample_seq(lib, logits, recent, seed, n_calls, **params):
     lib.ref_sample_run(ptr(x), x.size, ptr(r), r.size, p["temp"], p["top_k"], p["top_p"], p["repeat_penalty"],
                        p["repeat_last_n"], seed, n_calls, ptr(out))
     return [int(v) for v in out]
+
+
+def ref_qwen():
+    """The reference MoE engine's scalar qwen3moe forward (oracle/_ref/libqwen_ref.so), or None."""
+    if not os.path.exists(REF_QWEN_SO):
+        return None
+    lib = C.CDLL(REF_QWEN_SO)
+    lib.qwen_load.restype = C.c_void_p
+    lib.qwen_load.argtypes = [C.c_char_p, C.c_size_t, C.c_int, C.c_int, C.c_int]
+    lib.qwen_forward.restype = C.c_int
+    lib.qwen_forward.argtypes = [C.c_void_p, C.c_int]
+    lib.qwen_logits.restype = C.POINTER(C.c_float)
+    lib.qwen_logits.argtypes = [C.c_void_p]
+    lib.qwen_vocab_size.restype = C.c_int
+    lib.qwen_vocab_size.argtypes = [C.c_void_p]
+    lib.qwen_free.restype = None
+    lib.qwen_free.argtypes = [C.c_void_p]
+    return lib
+
+
+def ref_qwen_logits(lib, path, tokens, max_seq=64):
+    """qwen_load, then qwen_forward token by token from position 0 (qwen_model.c:972-1016): the
+    logits after each token, one row per token."""
+    m = lib.qwen_load(path.encode(), 64 << 20, 1, max_seq, 0)
+    if not m:
+        raise RuntimeError(f"qwen_load failed on {path}")
+    try:
+        n_vocab = lib.qwen_vocab_size(m)
+        out = np.zeros((len(tokens), n_vocab), np.float32)
+        for i, t in enumerate(tokens):
+            if lib.qwen_forward(m, int(t)) != 0:
+                raise RuntimeError(f"qwen_forward failed at step {i}")
+            out[i] = np.ctypeslib.as_array(lib.qwen_logits(m), (n_vocab,))
+        return out
+    finally:
+        lib.qwen_free(m)
 
 
 def cpu_backend(n_threads: int = 8):
