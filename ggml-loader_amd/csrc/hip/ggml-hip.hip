@@ -1774,6 +1774,7 @@ private:
         A.out_nb1 = (int64_t) (n->nb[2] / 4);
         A.n_kv = n_kv; A.n_q = n_q; A.n_head = n_head; A.n_head_kv = n_head_kv; A.hd = hd;
         A.scale = scale;
+        A.skip_masked = 1;
         const double bytes = (double) n_kv * n_head_kv * hd * 2 * 2 + (double) n_head * hd * n_q * 8;
         if (n_q > 4 && prefill_attn_ok(n_kv, hd, k->data, k->nb[1], k->nb[2], v->data, v->nb[1], v->nb[2])) {
             prof_scope ps(this, "attn_prefill", bytes);

@@ -329,7 +329,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
         // softmax input as the graph forms it: (float) kq * scale + mask
         float sv = -INFINITY;
         if (ok) {
-            sv = (float) dot * A.scale + (mask32 ? s_mk[q * ATT_CHUNK + tl] : mask_at(A, q0 + q, t0 + tl));
+            const float mv = mask32 ? s_mk[q * ATT_CHUNK + tl] : mask_at(A, q0 + q, t0 + tl);
+            sv = mv == -INFINITY ? -INFINITY : (float) dot * A.scale + mv;
             if (dq == 0) S.scores[((int64_t) (q0 + q) * A.n_head + h) * A.n_kv + t0 + tl] = sv;
         }
         // the row's maximum over this wave's 16 positions (every lane of a quad holds its value)
@@ -442,6 +443,17 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
         const int r = pc / PIECES, c = pc % PIECES;
         vv[it] = *(const uint4 *) (vbase + (int64_t) (t0 + min(r, nt - 1)) * A.v_nb2 + c * 8);
         if (r >= nt) vv[it] = make_uint4(0, 0, 0, 0);   // padding rows: no term
+    }
+    if (A.skip_masked && A.mask) {
+        // rows masked for every query of the workgroup read as zero (their p is 0 for every row)
+        const int nq = min(pvq, A.n_q - q0);
+#pragma unroll
+        for (int it = 0; it < ITER; it++) {
+            const int r = (t + it * ATT_THREADS) / PIECES;
+            bool dead = r < nt;
+            for (int q = 0; q < nq && dead; q++) dead = mask_at(A, q0 + q, t0 + r) == -INFINITY;
+            if (dead) vv[it] = make_uint4(0, 0, 0, 0);
+        }
     }
     if (t < n_rows) {
         s_M[t] = rmax;
@@ -672,8 +684,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
         s_q[qi * KSTR + d] = __float2half_rn(A.q[(int64_t) h * A.q_nb1 + (int64_t) q * A.q_nb2 + d]);
     }
 
-    // rows [t0, t0 + nt) of a cache view into s_kv, zero past nt; every load before the first store
-    auto stage = [&](const __half * base, int64_t nb_pos, int t0, int nt) {
+    // rows [t0, t0 + nt) of a cache view into s_kv, zero past nt; every load before the first store.
+    // zero_dead: rows masked for every query of the tile also read as zero (skip_masked)
+    auto stage = [&](const __half * base, int64_t nb_pos, int t0, int nt, bool zero_dead) {
         constexpr int ITER = (APF_CHUNK * PIECES + ATT_THREADS - 1) / ATT_THREADS;
         uint4 v[ITER];
 #pragma unroll
@@ -682,6 +695,15 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
             const int r = pc / PIECES, c = pc % PIECES;
             v[it] = make_uint4(0, 0, 0, 0);
             if (pc < APF_CHUNK * PIECES && r < nt) v[it] = *(const uint4 *) (base + (int64_t) (t0 + r) * nb_pos + c * 8);
+        }
+        if (zero_dead) {
+#pragma unroll
+            for (int it = 0; it < ITER; it++) {
+                const int r = (threadIdx.x + it * ATT_THREADS) / PIECES;
+                bool dead = r < nt;
+                for (int q = q0; q < min(q0 + APF_Q, n_q) && dead; q++) dead = mask_at(A, q, t0 + r) == -INFINITY;
+                if (dead) v[it] = make_uint4(0, 0, 0, 0);
+            }
         }
 #pragma unroll
         for (int it = 0; it < ITER; it++) {
@@ -712,7 +734,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
             }
             continue;
         }
-        stage(kbase, A.k_nb2, t0, nt);
+        stage(kbase, A.k_nb2, t0, nt, false);
         __syncthreads();
         v4d acc = { 0.0, 0.0, 0.0, 0.0 };
         const __half * qr = s_q + (lane % 16) * KSTR + lane / 16;
@@ -729,7 +751,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
             for (int r = 0; r < 4; r++) {
                 const int qi = lane / 16 + 4 * r;
                 const int q = min(q0 + qi, n_q - 1);
-                s_s[qi * SS + t0 + t] = (float) acc[r] * A.scale + mask_at(A, q, t0 + t);
+                const float mv = mask_at(A, q, t0 + t);
+                s_s[qi * SS + t0 + t] = mv == -INFINITY ? -INFINITY : (float) acc[r] * A.scale + mv;
             }
         }
     }
@@ -762,7 +785,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
         __syncthreads();                         // s_live / p visible; previous s_kv reads done
         if (!s_live[ch]) continue;
         const int t0 = ch * APF_CHUNK, nt = min(APF_CHUNK, n_kv - t0);
-        stage(vbase, A.v_nb2, t0, nt);
+        stage(vbase, A.v_nb2, t0, nt, A.skip_masked && A.mask);
         __syncthreads();
         for (int k0 = 0; k0 < APF_CHUNK; k0 += 4) {
             const int t = k0 + lane / 16;

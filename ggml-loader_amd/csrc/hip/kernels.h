@@ -350,6 +350,13 @@ struct attn_launch {
     // stores it here (cs_mode 1, workgroup 0), the later ones read it (cs_mode 2); 0: compute only
     float2 *       cs_tab;
     int            cs_mode;
+    // flash_attn_ext's contract: a position whose mask is -inf takes no part in that query's row,
+    // whatever its K and V hold (ggml-cpu skips it; the never-written cells of a ring cache may hold
+    // any bits). Every path gives such a position the score -inf without reading its dot; with
+    // skip_masked the V rows of positions masked for every query of a workgroup are also read as
+    // zero, so that 0 * (non-finite V) cannot reach the sums. The manual chain, which never attends
+    // an unwritten position, leaves it 0.
+    int            skip_masked;
 };
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd);
 // split-KV decode attention for 1 <= n_q <= ATT_DECODE_MAX_Q queries (groups of 4 per workgroup;

@@ -20,6 +20,7 @@ ORACLE_SO = os.environ.get("GGML_LOADER_ORACLE_SO") or os.path.join(ROOT, "oracl
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libmoe_ref.so")
 REF_SAMPLER_SO = os.path.join(ROOT, "oracle", "_ref", "libref_sampler.so")
 REF_QWEN_SO = os.path.join(ROOT, "oracle", "_ref", "libqwen_ref.so")
+REF_RUNTIME_SO = os.path.join(ROOT, "oracle", "_ref", "libref_runtime.so")
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
@@ -180,6 +181,63 @@ def ref_qwen_logits(lib, path, tokens, max_seq=64):
         return out
     finally:
         lib.qwen_free(m)
+
+
+class RefRuntime:
+    """The reference's own model runtime (model.cpp + dory.c via oracle/_ref/libref_runtime.so) on a
+    backend handle: load_weights .. init_decode_session at open, forward_step / prefill per call."""
+    _lib = None
+
+    @classmethod
+    def lib(cls):
+        if cls._lib is None:
+            gl.libs()
+            lib = C.CDLL(REF_RUNTIME_SO)
+            lib.ref_rt_open.restype = C.c_void_p
+            lib.ref_rt_open.argtypes = [C.c_char_p, C.c_void_p, C.c_int64, C.c_int]
+            lib.ref_rt_n_vocab.restype = C.c_int64
+            lib.ref_rt_n_vocab.argtypes = [C.c_void_p]
+            lib.ref_rt_kv_fill.restype = None
+            lib.ref_rt_kv_fill.argtypes = [C.c_void_p, C.c_uint8]
+            lib.ref_rt_forward.restype = C.c_int
+            lib.ref_rt_forward.argtypes = [C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_void_p]
+            lib.ref_rt_prefill.restype = C.c_int
+            lib.ref_rt_prefill.argtypes = [C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_int, C.c_void_p]
+            lib.ref_rt_close.restype = None
+            lib.ref_rt_close.argtypes = [C.c_void_p]
+            cls._lib = lib
+        return cls._lib
+
+    def __init__(self, path, backend, n_ctx=64, flash_attn=False, kv_fill=None):
+        self.l = self.lib()
+        self.h = self.l.ref_rt_open(path.encode(), backend, n_ctx, int(flash_attn))
+        self.n_vocab = int(self.l.ref_rt_n_vocab(self.h))
+        if kv_fill is not None:
+            self.l.ref_rt_kv_fill(self.h, kv_fill)
+
+    def _call(self, fn, n_past, tokens, *extra):
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.zeros(self.n_vocab, np.float32)
+        if fn(self.h, n_past, ptr(t), t.size, *extra, ptr(out)) != 0:
+            raise RuntimeError("reference runtime call failed")
+        return out
+
+    def forward(self, n_past, tokens):
+        return self._call(self.l.ref_rt_forward, n_past, tokens)
+
+    def prefill(self, n_past, tokens, use_chunking=False):
+        return self._call(self.l.ref_rt_prefill, n_past, tokens, int(use_chunking))
+
+    def close(self):
+        if self.h:
+            self.l.ref_rt_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
 
 
 def cpu_backend(n_threads: int = 8):
