@@ -1059,7 +1059,9 @@ private:
 
     // a quantized mul_mat over a prefill-width batch: the int8-MFMA GEMM (same floats as the GEMV)
     bool gemm_route(const ggml_tensor * mm) const {
-        return mm->op == GGML_OP_MUL_MAT && mm->src[1]->ne[1] >= GEMM_MIN_COLS && gemv_capable(mm) &&
+        const int64_t cols = mm->src[1]->ne[1];
+        const bool wide = cols >= GEMM_MIN_COLS || (cols >= GEMM_WIDE_MIN_COLS && mm->src[0]->ne[1] >= GEMM_WIDE_MIN_ROWS);
+        return mm->op == GGML_OP_MUL_MAT && wide && gemv_capable(mm) &&
                gemm_supported(mm->src[0]->type, mm->src[0]->ne[0], mm->src[0]->ne[1]) &&
                (mm->nb[1] / sizeof(float)) % 4 == 0 && ((uintptr_t) mm->data) % 16 == 0;
     }

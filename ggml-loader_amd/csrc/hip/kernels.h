@@ -77,7 +77,12 @@ struct gemv_mat {
 // prefill GEMM on the matrix cores: y[c][r] = W[r] . x[c] (+ add[c][r]) for Q4_0 / Q8_0 weights
 // in the plane layout with Q8_0-quantized activation columns, or Q4_K weights (ggml blocks) with
 // Q8_K-quantized columns; the same floats as the GEMV.
-constexpr int GEMM_MIN_COLS = 64;   // narrower products stay on the GEMV
+constexpr int GEMM_MIN_COLS = 64;   // narrower products stay on the GEMV, except:
+// an output projection this tall (an LM head) takes the GEMM from GEMM_WIDE_MIN_COLS columns: its
+// weights stream once at the GEMM's rate, where the multi-column GEMV would stage every column's
+// activation once per 16-row workgroup
+constexpr int GEMM_WIDE_MIN_COLS = 16;
+constexpr int64_t GEMM_WIDE_MIN_ROWS = 65536;
 
 struct gemm_launch {
     int             type;      // GGML_TYPE_Q4_0 / Q8_0 / Q4_K
