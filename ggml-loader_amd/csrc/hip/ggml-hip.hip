@@ -953,6 +953,18 @@ private:
         return first;
     }
 
+    // the highest node index that reads node u's data, directly or through views (INT_MAX: an
+    // output, live to the end of the graph)
+    int last_reader(int u) const {
+        if (is_output(u)) return INT_MAX;
+        int last = -1;
+        for (int j : users_[u]) {
+            const ggml_tensor * t = g_->nodes[j];
+            last = std::max(last, is_view_op(t->op) ? std::max(j, last_reader(j)) : j);
+        }
+        return last;
+    }
+
     // The MoE FFN norm: rms_norm -> mul(w) whose first reader in node order is the F32 router
     // mul_mat (build_moe_ffn's ffn_gate_inp product). Nothing is launched here: the router launch
     // normalizes each column itself and writes the mul's output for the later readers (the expert
@@ -969,6 +981,13 @@ private:
             x->nb[1] % 4) {
             return false;
         }
+        // the router launch reads x at node r, later than the allocator planned for, and writes m:
+        // x must be disjoint from m and stay live up to r (read again at or after r, or not a node
+        // of this graph), else the allocator may have placed m or a node before r over it
+        const char * xb = (const char *) x->data, * mb = (const char *) m->data;
+        if (xb < mb + ggml_nbytes(m) && mb < xb + ggml_nbytes(x)) return false;
+        const int xi = node_index(x->view_src ? x->view_src : x);
+        if (xi >= 0 && last_reader(xi) < r) return false;
         router_norm_[r] = router_norm{ i, u, eps };
         done_[u] = true;
         return true;

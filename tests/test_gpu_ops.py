@@ -794,6 +794,35 @@ def test_moe_ffn_norm_folded_into_router(hip, cpu, n_tok):
     assert "router_norm" in names and "rms_norm_mul" not in names, names
 
 
+@pytest.mark.parametrize("n_tok", [1, 5])
+def test_moe_router_norm_kept_apart_when_its_input_dies(hip, cpu, n_tok):
+    """The norm's input computed in the graph and read by nothing after the norm: the allocator may
+    reuse its memory before the router runs, so the norm keeps a launch of its own instead of being
+    folded into the router launch (which reads the input later), and the result is the oracle's."""
+    n_embd, E, k, ff = 512, 32, 8, 256
+    r = rng(78)
+    x = (r.standard_normal((n_tok, n_embd)) * 3).astype(np.float32)
+    res = r.standard_normal((n_tok, n_embd)).astype(np.float32)
+    nw = (1 + 0.01 * r.standard_normal(n_embd)).astype(np.float32)
+    router = (r.standard_normal((E, n_embd)) * 0.05).astype(np.float32)
+    wg, wu = (qweight(gl.Q4_K, n_embd, E * ff, s, std=0.05) for s in (79, 80))
+    wd = qweight(gl.Q4_K, ff, E * n_embd, 81, std=0.05)
+
+    def build(g):
+        xin = g.tensor(gl.F32, n_embd, n_tok, data=x)
+        xt = g.scale(xin, 0.5)                                  # a node: dead after the norm
+        y = g.mul(g.rms_norm(xt, 1e-6), g.tensor(gl.F32, n_embd, data=nw))
+        return moe_ffn_graph(g, y, g.tensor(gl.F32, n_embd, E, data=router),
+                             g.tensor(gl.Q4_K, n_embd, ff, E, data=wg), g.tensor(gl.Q4_K, n_embd, ff, E, data=wu),
+                             g.tensor(gl.Q4_K, ff, n_embd, E, data=wd), k, g.tensor(gl.F32, n_embd, n_tok, data=res))
+
+    for fusion in (True, False):
+        a, b = both(hip, cpu, build, fusion)
+        assert np.array_equal(a, b), (fusion, rel_err(a, b))
+    _, names = profiled(hip, lambda: run_on(hip, build))
+    assert "router_norm" not in names, names
+
+
 @pytest.mark.parametrize("E,k,n_tok", [(128, 8, 1), (128, 8, 16), (60, 4, 3), (1024, 32, 2), (8, 8, 1)])
 def test_moe_route_fused(hip, cpu, E, k, n_tok):
     """Router softmax -> top-k -> renormalized weights in one kernel: the same ids (ties: the lower
