@@ -214,6 +214,33 @@ def summarize_pmc_all(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy
     return {"fetch_scale": round(fs, 4), "write_scale": round(ws, 4), "kernels": out}
 
 
+def summarize_activity(pmc_dir):
+    """Per-kernel wave activity from one rocprofv3 --pmc run of SQ_WAVES, SQ_INSTS_VALU,
+    SQ_INSTS_LDS, SQ_ACTIVE_INST_VALU, SQ_ACTIVE_INST_ANY and SQ_WAIT_ANY: waves per dispatch, VALU
+    and LDS instructions per wave, and the shares of the waves' cycles spent issuing VALU and
+    waiting (SQ_WAIT_ANY over SQ_WAIT_ANY + SQ_ACTIVE_INST_ANY)."""
+    import csv
+    import glob
+
+    acc, disp = {}, {}
+    for f in glob.glob(os.path.join(pmc_dir, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+            c = acc.setdefault(name, {})
+            c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+            disp.setdefault(name, set()).add(r["Dispatch_Id"])
+    out = {}
+    for name, c in sorted(acc.items(), key=lambda kv: -kv[1].get("SQ_INSTS_VALU", 0.0)):
+        waves = max(c.get("SQ_WAVES", 0.0), 1.0)
+        cyc = max(c.get("SQ_WAIT_ANY", 0.0) + c.get("SQ_ACTIVE_INST_ANY", 0.0), 1.0)
+        out[name] = {"dispatches": len(disp[name]), "waves_per_dispatch": round(waves / len(disp[name])),
+                     "valu_per_wave": round(c.get("SQ_INSTS_VALU", 0.0) / waves, 1),
+                     "lds_per_wave": round(c.get("SQ_INSTS_LDS", 0.0) / waves, 1),
+                     "valu_issue_share": round(c.get("SQ_ACTIVE_INST_VALU", 0.0) / cyc, 3),
+                     "wait_share": round(c.get("SQ_WAIT_ANY", 0.0) / cyc, 3)}
+    return out
+
+
 def copy_kernel(gl, mb, reps):
     """Runs the backend's own contiguous f32 copy (a ggml_cpy graph node) over mb MiB reps times:
     the known-size kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
@@ -408,8 +435,13 @@ def main():
     ap.add_argument("--copy-mb-of-pmc", type=int, default=256, help="size of the copy kernel of the calibration runs")
     ap.add_argument("--pmc-prefix", default="void gemv_q_kernel<2,", help="kernel name prefix of --summarize-pmc")
     ap.add_argument("--pmc-all", action="store_true", help="--summarize-pmc: every kernel's bytes per dispatch")
+    ap.add_argument("--summarize-activity", metavar="PMC_DIR",
+                    help="print per-kernel wave activity from a rocprofv3 --pmc run of the SQ counters and exit")
     args = ap.parse_args()
 
+    if args.summarize_activity:
+        print(json.dumps(summarize_activity(args.summarize_activity), indent=1), flush=True)
+        return
     if args.summarize_pmc:
         if args.pmc_all:
             print(json.dumps(summarize_pmc_all(*args.summarize_pmc, args.copy_mb_of_pmc), indent=1), flush=True)
