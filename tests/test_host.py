@@ -384,3 +384,31 @@ def test_bench_pmc_summary_scales_by_the_copy_kernel(tmp_path):
     assert out["dispatches"] == 2
     assert out["fetch_scale"] == 2.0 and out["write_scale"] == 1.0
     assert out["traffic_bytes_per_launch"] == round(200.0 * 1024 * 2 + 3.0 * 1024)
+
+
+def test_bench_activity_summary(tmp_path):
+    """Wave activity per kernel: counters summed over a kernel's dispatches, divided by its waves
+    (instructions per wave) or by its waves' cycles (issue and wait shares)."""
+    import csv
+    import importlib.util
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(root, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    os.makedirs(tmp_path / "run")
+    rows = []
+    for disp, (waves, valu, lds, act_valu, act_any, wait) in ((1, (100, 6000, 500, 200, 300, 700)),
+                                                              (2, (100, 4000, 300, 100, 200, 800))):
+        for name, v in (("SQ_WAVES", waves), ("SQ_INSTS_VALU", valu), ("SQ_INSTS_LDS", lds),
+                        ("SQ_ACTIVE_INST_VALU", act_valu), ("SQ_ACTIVE_INST_ANY", act_any), ("SQ_WAIT_ANY", wait)):
+            rows.append({"Dispatch_Id": disp, "Kernel_Name": "(anonymous namespace)::k<1>(args)", "Counter_Name": name,
+                         "Counter_Value": v})
+    with open(tmp_path / "run" / "p_counter_collection.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        w.writerows(rows)
+    out = bench.summarize_activity(str(tmp_path))
+    k = out["k<1>"]
+    assert k["dispatches"] == 2 and k["waves_per_dispatch"] == 100
+    assert k["valu_per_wave"] == 50.0 and k["lds_per_wave"] == 4.0
+    assert k["valu_issue_share"] == 0.15 and k["wait_share"] == 0.75
