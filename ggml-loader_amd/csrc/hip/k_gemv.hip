@@ -240,13 +240,15 @@ __device__ __forceinline__ void quant_chunk(const float (&v)[C], int c, bool has
                 if (a > ax) { ax = a; idx = c * C + e; val = v[e]; }
             }
         }
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            const float ax2 = __shfl_xor(ax, o, WAVE);
-            const int idx2 = __shfl_xor(idx, o, WAVE);
-            const float val2 = __shfl_xor(val, o, WAVE);
+        // across the super-block's 16 lanes: quad lanes xor 1, xor 2, then the mirrored lane of the
+        // half row and of the row (the combine is a total order, so the pairing does not matter)
+        auto take = [&](float ax2, int idx2, float val2) {
             if (ax2 > ax || (ax2 == ax && idx2 < idx)) { ax = ax2; idx = idx2; val = val2; }
-        }
+        };
+        take(dpp_f<0xB1>(ax), dpp_i<0xB1>(idx), dpp_f<0xB1>(val));
+        take(dpp_f<0x4E>(ax), dpp_i<0x4E>(idx), dpp_f<0x4E>(val));
+        take(dpp_f<0x141>(ax), dpp_i<0x141>(idx), dpp_f<0x141>(val));
+        take(dpp_f<0x140>(ax), dpp_i<0x140>(idx), dpp_f<0x140>(val));
         if (!has) return;
         int q[C];
         int bsum = 0;
@@ -600,11 +602,11 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                 // the 4 units of a super-block sit on 4 consecutive lanes: combine (exact integers)
 #pragma unroll
                 for (int k = 0; k < 8; k++) {
-                    aux[k] += __shfl_xor(aux[k], 1, WAVE);
-                    aux[k] += __shfl_xor(aux[k], 2, WAVE);
+                    aux[k] += dpp_i<0xB1>(aux[k]);   // quad lanes xor 1
+                    aux[k] += dpp_i<0x4E>(aux[k]);   // quad lanes xor 2
                 }
-                mins += __shfl_xor(mins, 1, WAVE);
-                mins += __shfl_xor(mins, 2, WAVE);
+                mins += dpp_i<0xB1>(mins);
+                mins += dpp_i<0x4E>(mins);
                 if (has) {
                     const uint32_t dd = hd[ch][it].x;
                     const float yd = s.xd[sb];

@@ -174,11 +174,11 @@ __global__ __launch_bounds__(MC_THREADS) void gemv_mc_kernel(const gemv_mc_args 
                     // the 4 units of a super-block sit on 4 consecutive lanes: combine (exact integers)
 #pragma unroll
                     for (int q = 0; q < 8; q++) {
-                        aux[q] += __shfl_xor(aux[q], 1, WAVE);
-                        aux[q] += __shfl_xor(aux[q], 2, WAVE);
+                        aux[q] += dpp_i<0xB1>(aux[q]);   // quad lanes xor 1
+                        aux[q] += dpp_i<0x4E>(aux[q]);   // quad lanes xor 2
                     }
-                    mins += __shfl_xor(mins, 1, WAVE);
-                    mins += __shfl_xor(mins, 2, WAVE);
+                    mins += dpp_i<0xB1>(mins);
+                    mins += dpp_i<0x4E>(mins);
                     if (has) {
                         const float yd = ((const float *) (act + K))[sb];
                         const float d = __half2float(__ushort_as_half((unsigned short) (dd & 0xffff))) * yd;
