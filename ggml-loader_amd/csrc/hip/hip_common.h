@@ -45,39 +45,6 @@ constexpr int Q4_K_BYTES = 144;
 struct q4k_block { __half d; __half dmin; uint8_t scales[12]; uint8_t qs[128]; };
 static_assert(sizeof(q4k_block) == 144, "q4_K block");
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
-}
-
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
-
-// sum within aligned groups of G lanes (G a power of two <= 64)
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
-
-template <int G>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
-}
-
 // DPP lane exchanges (v_mov_dpp): quad_perm xor 1 (0xB1) and xor 2 (0x4E), row_half_mirror (0x141:
 // lane i <-> 7 - i within 8 lanes), row_mirror (0x140: i <-> 15 - i within 16). One VALU op each,
 // where __shfl_xor goes through ds_bpermute (an LDS round trip). Every lane of the groups involved
@@ -113,6 +80,44 @@ __device__ __forceinline__ double wave_sum_d_dpp(double v) {
 #pragma unroll
     for (int k = 0; k < 4; k++) r[k] = __hiloint2double(__builtin_amdgcn_readlane(hi, 16 * k), __builtin_amdgcn_readlane(lo, 16 * k));
     return ((r[0] + r[1]) + r[2]) + r[3];
+}
+
+// Whole-wave reductions (every lane active; uniform result). The double sums of the kernels add
+// exact quantities (products of F16 values, exps of floats, squares of floats) whose double sum is
+// exact in practice, so the pairing does not change them.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) { return wave_sum_d_dpp(v); }
+
+// sum / max within aligned groups of G lanes (G a power of two <= 64; every lane gets its group's
+// result): DPP within rows of 16 lanes, lane shuffles across rows. The sums add integers held as
+// floats, exact in any order.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    if (G >= 2) v += dpp_f<0xB1>(v);
+    if (G >= 4) v += dpp_f<0x4E>(v);
+    if (G >= 8) v += dpp_f<0x141>(v);
+    if (G >= 16) v += dpp_f<0x140>(v);
+    if (G >= 32) v += __shfl_xor(v, 16, WAVE);
+    if (G >= 64) v += __shfl_xor(v, 32, WAVE);
+    return v;
+}
+
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+    if (G >= 2) v = fmaxf(v, dpp_f<0xB1>(v));
+    if (G >= 4) v = fmaxf(v, dpp_f<0x4E>(v));
+    if (G >= 8) v = fmaxf(v, dpp_f<0x141>(v));
+    if (G >= 16) v = fmaxf(v, dpp_f<0x140>(v));
+    if (G >= 32) v = fmaxf(v, __shfl_xor(v, 16, WAVE));
+    if (G >= 64) v = fmaxf(v, __shfl_xor(v, 32, WAVE));
+    return v;
 }
 
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
