@@ -4,19 +4,20 @@
 // ggml-cpu computes every output of a quantized mul_mat as a float sum over the weight row's
 // 32-element blocks, in block order, of an exact integer block dot scaled by the two fp16 block
 // scales: Q8_0 sumf += sumi * (d_w * d_x), Q4_0 sumf += (sumi * d_w) * d_x. The integer quants are
-// staged as f16 (integers of magnitude <= 128 are exact in f16), so one v_mfma_f32_16x16x32_f16
-// yields the block dots of a tile of 16 weight rows x 16 activation columns as f32 — exact, since
-// every product and partial sum is an integer below 2^24 — and the kernel adds the scaled terms to
-// f32 accumulators in block order: every output is the same float as the GEMV's and the CPU
-// reference's. The per-term float work (two multiplies, one add) runs on the VALU and bounds the
-// kernel, not the MFMA rate.
+// staged as int8 (Q4_0 nibbles as nibble - 8), so one v_mfma_i32_16x16x32_i8 yields the exact
+// block dots of a tile of 16 weight rows x 16 activation columns, and the kernel adds the scaled
+// terms (the block dot converted to float, exactly: it is below 2^24 in magnitude) to f32
+// accumulators in block order: every output is the same float as the GEMV's and the CPU
+// reference's. The per-term float work (a conversion, two multiplies, one add) runs on the VALU
+// and bounds the kernel, not the MFMA rate.
 //
 // Tiling: a workgroup is 2 x 2 waves; a wave owns WTM x WTN MFMA tiles. Each pipeline stage moves
 // KB blocks of the workgroup's weight rows and activation columns from global memory (16-byte
-// loads, consecutive threads on consecutive bytes) into LDS, converting the quants to f16 and the
-// fp16 weight scales to float on the way; the next stage's loads are in flight while the current
-// stage is reduced, with one barrier per stage. In a tile, lane l reads weight row l%16 and
-// activation column l%16, k-slice 8(l/16)..8(l/16)+7 of the block (one 16-byte LDS read each), and
+// loads, consecutive threads on consecutive bytes) into LDS as int8 rows (Q4_0 unpacked on the
+// way) and the fp16 weight scales as floats; the next stage's loads are in flight while the
+// current stage is reduced, with one barrier per stage. In a tile, lane l reads weight row l%16
+// and activation column l%16, k-slice 8(l/16)..8(l/16)+7 of the block (one 8-byte LDS read each;
+// rows are 8 bytes longer than their blocks, so the 16 rows of a read fall on distinct banks), and
 // receives the results of rows 4(l/16)..4(l/16)+3 of column l%16. Workgroups are numbered so that
 // the column tiles of one row tile run on one XCD and share its L2.
 //
@@ -28,6 +29,7 @@
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -42,50 +44,37 @@ __device__ __forceinline__ void i8x4_to_f16(uint32_t v, uint32_t & lo, uint32_t 
     hi = __builtin_bit_cast(uint32_t, __hadd2(__builtin_bit_cast(__half2, hi), bias));
 }
 
-// 4 nibbles (the low or high halves of one dword) -> 4 f16 of value nibble - 8
-__device__ __forceinline__ void u4x4_to_f16(uint32_t n, uint32_t & lo, uint32_t & hi) {
-    lo = __builtin_amdgcn_perm(0x64646464u, n, 0x04010400u);
-    hi = __builtin_amdgcn_perm(0x64646464u, n, 0x04030402u);
-    const __half2 bias = __halves2half2(__ushort_as_half(0xE408), __ushort_as_half(0xE408));   // -1032
-    lo = __builtin_bit_cast(uint32_t, __hadd2(__builtin_bit_cast(__half2, lo), bias));
-    hi = __builtin_bit_cast(uint32_t, __hadd2(__builtin_bit_cast(__half2, hi), bias));
-}
-
-// 32 int8 -> 32 f16 (64 bytes) at dst
-__device__ __forceinline__ void store_i8x32(_Float16 * dst, const uint4 & a, const uint4 & b) {
-    const uint32_t w[8] = { a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w };
+// one Q4_0 block's 16 bytes -> its 32 weights as int8 of value nibble - 8 (low nibbles are elements
+// 0-15, high 16-31), 8 bytes per store: per byte n in 0..15, ((n | 0x80) - 8) ^ 0x80 = n - 8 with no
+// borrow between bytes
+__device__ __forceinline__ void store_q4x32_i8(int8_t * dst, const uint4 & a) {
+    const uint32_t w[4] = { a.x, a.y, a.z, a.w };
+    uint32_t lo[4], hi[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        uint32_t l0, h0, l1, h1;
-        i8x4_to_f16(w[2 * k], l0, h0);
-        i8x4_to_f16(w[2 * k + 1], l1, h1);
-        *(uint4 *) (dst + 8 * k) = make_uint4(l0, h0, l1, h1);
+        lo[k] = (((w[k] & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+        hi[k] = ((((w[k] >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
     }
+    uint2 * d = (uint2 *) dst;
+    d[0] = make_uint2(lo[0], lo[1]); d[1] = make_uint2(lo[2], lo[3]);
+    d[2] = make_uint2(hi[0], hi[1]); d[3] = make_uint2(hi[2], hi[3]);
 }
 
-// one Q4_0 block's 16 bytes -> its 32 weights (low nibbles are elements 0-15, high 16-31) as f16
-__device__ __forceinline__ void store_q4x32(_Float16 * dst, const uint4 & a) {
-    const uint32_t w[4] = { a.x, a.y, a.z, a.w };
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-        uint32_t l0, h0, l1, h1;
-        u4x4_to_f16(w[2 * k] & 0x0F0F0F0Fu, l0, h0);
-        u4x4_to_f16(w[2 * k + 1] & 0x0F0F0F0Fu, l1, h1);
-        *(uint4 *) (dst + 8 * k) = make_uint4(l0, h0, l1, h1);
-        u4x4_to_f16((w[2 * k] >> 4) & 0x0F0F0F0Fu, l0, h0);
-        u4x4_to_f16((w[2 * k + 1] >> 4) & 0x0F0F0F0Fu, l1, h1);
-        *(uint4 *) (dst + 16 + 8 * k) = make_uint4(l0, h0, l1, h1);
-    }
+// 32 int8 (two 16-byte loads) to an 8-byte aligned LDS row
+__device__ __forceinline__ void store_i8x32_raw(int8_t * dst, const uint4 & a, const uint4 & b) {
+    uint2 * d = (uint2 *) dst;
+    d[0] = make_uint2(a.x, a.y); d[1] = make_uint2(a.z, a.w);
+    d[2] = make_uint2(b.x, b.y); d[3] = make_uint2(b.z, b.w);
 }
 
 template <int TYPE, int WTM, int WTN, int KB>
 struct gemm_cfg {
     static constexpr int QB = TYPE == GGML_TYPE_Q4_0 ? Q4_0_QS : Q8_0_QS;
     static constexpr int BM = 32 * WTM, BN = 32 * WTN;
-    static constexpr int ROW = KB * 32 + 8;                               // f16 per LDS row (16-byte pad)
+    static constexpr int ROW = KB * 32 + 8;                               // int8 per LDS row (8-byte pad)
     static constexpr int UA = (BM * KB + 255) / 256, UB = (BN * KB + 255) / 256;   // staged blocks per thread
-    static constexpr int A_HALVES = BM * ROW, B_HALVES = BN * ROW;
-    static constexpr size_t LDS = 2 * ((size_t) (A_HALVES + B_HALVES) * 2 + (size_t) KB * (BM + BN) * 4);
+    static constexpr int A_BYTES = BM * ROW, B_BYTES = BN * ROW;
+    static constexpr size_t LDS = 2 * ((size_t) (A_BYTES + B_BYTES) + (size_t) KB * (BM + BN) * 4);
 };
 
 template <int TYPE, int WTM, int WTN, int KB>
@@ -93,9 +82,9 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const gemm_launch G) {
     using C = gemm_cfg<TYPE, WTM, WTN, KB>;
     constexpr int QB = C::QB, BM = C::BM, BN = C::BN, ROW = C::ROW;
     extern __shared__ __align__(16) uint8_t g_lds[];
-    _Float16 * sA = (_Float16 *) g_lds;                       // [2][BM][ROW]
-    _Float16 * sB = sA + 2 * C::A_HALVES;                     // [2][BN][ROW]
-    float * sdw = (float *) (sB + 2 * C::B_HALVES);           // [2][KB][BM]
+    int8_t * sA = (int8_t *) g_lds;                           // [2][BM][ROW]
+    int8_t * sB = sA + 2 * C::A_BYTES;                        // [2][BN][ROW]
+    float * sdw = (float *) (sB + 2 * C::B_BYTES);            // [2][KB][BM]
     float * sdx = sdw + 2 * KB * BM;                          // [2][KB][BN]
 
     const int64_t M = G.n_rows, N = G.ncols, K = G.K, nb = K / 32;
@@ -143,9 +132,9 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const gemm_launch G) {
             const int u = tid + 256 * k;
             if (u < BM * KB) {
                 const int r = u / KB, kb = u % KB;
-                _Float16 * dst = sA + buf * C::A_HALVES + r * ROW + kb * 32;
-                if constexpr (QB == 32) store_i8x32(dst, ra[k][0], ra[k][1]);
-                else store_q4x32(dst, ra[k][0]);
+                int8_t * dst = sA + buf * C::A_BYTES + r * ROW + kb * 32;
+                if constexpr (QB == 32) store_i8x32_raw(dst, ra[k][0], ra[k][1]);
+                else store_q4x32_i8(dst, ra[k][0]);
                 sdw[(buf * KB + kb) * BM + r] = __half2float(rd[k]);
             }
         }
@@ -154,7 +143,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const gemm_launch G) {
             const int u = tid + 256 * k;
             if (u < BN * KB) {
                 const int cc = u / KB, kb = u % KB;
-                store_i8x32(sB + buf * C::B_HALVES + cc * ROW + kb * 32, rb[k][0], rb[k][1]);
+                store_i8x32_raw(sB + buf * C::B_BYTES + cc * ROW + kb * 32, rb[k][0], rb[k][1]);
                 sdx[(buf * KB + kb) * BN + cc] = rx[k];
             }
         }
@@ -175,35 +164,36 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const gemm_launch G) {
     for (int64_t s = 0; s < n_stages; s++) {
         const int buf = (int) (s & 1);
         if (s + 1 < n_stages) load((s + 1) * KB);
-        const _Float16 * A = sA + buf * C::A_HALVES;
-        const _Float16 * B = sB + buf * C::B_HALVES;
+        const int8_t * A = sA + buf * C::A_BYTES;
+        const int8_t * B = sB + buf * C::B_BYTES;
 #pragma unroll
         for (int kb = 0; kb < KB; kb++) {
-            f16x8 a[WTM], b[WTN];
+            long a[WTM], b[WTN];
             f32x4 dw[WTM];
             float dx[WTN];
 #pragma unroll
             for (int i = 0; i < WTM; i++) {
-                a[i] = *(const f16x8 *) (A + (wr + 16 * i + c) * ROW + kb * 32 + 8 * q);
+                a[i] = *(const long *) (A + (wr + 16 * i + c) * ROW + kb * 32 + 8 * q);
                 dw[i] = *(const f32x4 *) (sdw + (buf * KB + kb) * BM + wr + 16 * i + 4 * q);
             }
 #pragma unroll
             for (int j = 0; j < WTN; j++) {
-                b[j] = *(const f16x8 *) (B + (wc + 16 * j + c) * ROW + kb * 32 + 8 * q);
+                b[j] = *(const long *) (B + (wc + 16 * j + c) * ROW + kb * 32 + 8 * q);
                 dx[j] = sdx[(buf * KB + kb) * BN + wc + 16 * j + c];
             }
 #pragma unroll
             for (int i = 0; i < WTM; i++)
 #pragma unroll
                 for (int j = 0; j < WTN; j++) {
-                    const f32x4 sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+                    const i32x4 si = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b[j], i32x4{ 0, 0, 0, 0 }, 0, 0, 0);
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
+                        const float sv = (float) si[r];
                         if constexpr (TYPE == GGML_TYPE_Q8_0) {
                             const float dd = dw[i][r] * dx[j];
-                            acc[i][j][r] += sv[r] * dd;
+                            acc[i][j][r] += sv * dd;
                         } else {
-                            acc[i][j][r] += (sv[r] * dw[i][r]) * dx[j];
+                            acc[i][j][r] += (sv * dw[i][r]) * dx[j];
                         }
                     }
                 }
