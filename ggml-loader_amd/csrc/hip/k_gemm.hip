@@ -78,7 +78,7 @@ struct gemm_cfg {
 };
 
 template <int TYPE, int WTM, int WTN, int KB>
-__global__ __launch_bounds__(256) void gemm_q_kernel(const gemm_launch G) {
+__global__ __launch_bounds__(256, WTM == 1 ? 4 : 1) void gemm_q_kernel(const gemm_launch G) {
     using C = gemm_cfg<TYPE, WTM, WTN, KB>;
     constexpr int QB = C::QB, BM = C::BM, BN = C::BN, ROW = C::ROW;
     extern __shared__ __align__(16) uint8_t g_lds[];
