@@ -684,11 +684,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
         s_q[qi * KSTR + d] = __float2half_rn(A.q[(int64_t) h * A.q_nb1 + (int64_t) q * A.q_nb2 + d]);
     }
 
-    // rows [t0, t0 + nt) of a cache view into s_kv, zero past nt; every load before the first store.
+    // rows [t0, t0 + nt) of a cache view into registers (zero past nt), and from there into s_kv.
     // zero_dead: rows masked for every query of the tile also read as zero (skip_masked)
-    auto stage = [&](const __half * base, int64_t nb_pos, int t0, int nt, bool zero_dead) {
-        constexpr int ITER = (APF_CHUNK * PIECES + ATT_THREADS - 1) / ATT_THREADS;
-        uint4 v[ITER];
+    constexpr int ITER = (APF_CHUNK * PIECES + ATT_THREADS - 1) / ATT_THREADS;
+    auto load_rows = [&](uint4 (&v)[ITER], const __half * base, int64_t nb_pos, int t0, int nt) {
 #pragma unroll
         for (int it = 0; it < ITER; it++) {
             const int pc = threadIdx.x + it * ATT_THREADS;
@@ -696,6 +695,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
             v[it] = make_uint4(0, 0, 0, 0);
             if (pc < APF_CHUNK * PIECES && r < nt) v[it] = *(const uint4 *) (base + (int64_t) (t0 + r) * nb_pos + c * 8);
         }
+    };
+    auto store_rows = [&](uint4 (&v)[ITER], int t0, int nt, bool zero_dead) {
         if (zero_dead) {
 #pragma unroll
             for (int it = 0; it < ITER; it++) {
@@ -714,28 +715,48 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
             d[0] = v[it].x; d[1] = v[it].y; d[2] = v[it].z; d[3] = v[it].w;
         }
     };
+    auto next_live = [&](int ch) {
+        while (ch < n_chunks && !s_live[ch]) ch++;
+        return ch;
+    };
 
-    // ---- scores ----
-    for (int ch = 0; ch < n_chunks; ch++) {
+    // the tile's mask rows into s_s (rows past n_q repeat the last query's; 0 without a mask), read
+    // once here instead of in every chunk
+    for (int idx = threadIdx.x; idx < APF_Q * n_kv; idx += ATT_THREADS) {
+        const int qi = idx / n_kv, t = idx % n_kv;
+        s_s[qi * SS + t] = A.mask ? mask_at(A, min(q0 + qi, n_q - 1), t) : 0.0f;
+    }
+    __syncthreads();
+    // chunk liveness, one wave per chunk: a chunk whose mask is -inf for every query of the tile is
+    // not computed, its scores are -inf (as the chain forms them)
+    for (int ch = wave; ch < n_chunks; ch += ATT_WAVES) {
         const int t0 = ch * APF_CHUNK, nt = min(APF_CHUNK, n_kv - t0);
-        bool any = !A.mask;
-        if (A.mask) {
-            for (int idx = threadIdx.x; idx < APF_Q * APF_CHUNK; idx += ATT_THREADS) {
-                const int qi = idx / APF_CHUNK, t = idx % APF_CHUNK;
-                if (q0 + qi < n_q && t < nt && mask_at(A, q0 + qi, t0 + t) != -INFINITY) any = true;
-            }
+        int any = !A.mask;
+        for (int idx = lane; idx < APF_Q * APF_CHUNK && !any; idx += WAVE) {
+            const int qi = idx / APF_CHUNK, t = idx % APF_CHUNK;
+            if (q0 + qi < n_q && t < nt && s_s[qi * SS + t0 + t] != -INFINITY) any = 1;
         }
-        const bool live = __syncthreads_or(any);   // also orders the previous chunk's s_kv reads
-        if (threadIdx.x == 0) s_live[ch] = live;
+        const bool live = __any(any);
         if (!live) {
-            for (int idx = threadIdx.x; idx < APF_Q * APF_CHUNK; idx += ATT_THREADS) {
+            for (int idx = lane; idx < APF_Q * APF_CHUNK; idx += WAVE) {
                 const int qi = idx / APF_CHUNK, t = idx % APF_CHUNK;
                 if (t < nt) s_s[qi * SS + t0 + t] = -INFINITY;
             }
-            continue;
         }
-        stage(kbase, A.k_nb2, t0, nt, false);
+        if (lane == 0) s_live[ch] = live;
+    }
+    __syncthreads();
+
+    // ---- scores, over the live chunks; the next live chunk's K rows load while this one is used ----
+    uint4 kv[ITER];
+    int ch = next_live(0);
+    if (ch < n_chunks) load_rows(kv, kbase, A.k_nb2, ch * APF_CHUNK, min(APF_CHUNK, n_kv - ch * APF_CHUNK));
+    while (ch < n_chunks) {
+        const int t0 = ch * APF_CHUNK, nt = min(APF_CHUNK, n_kv - t0);
+        store_rows(kv, t0, nt, false);
         __syncthreads();
+        const int nx = next_live(ch + 1);
+        if (nx < n_chunks) load_rows(kv, kbase, A.k_nb2, nx * APF_CHUNK, min(APF_CHUNK, n_kv - nx * APF_CHUNK));
         v4d acc = { 0.0, 0.0, 0.0, 0.0 };
         const __half * qr = s_q + (lane % 16) * KSTR + lane / 16;
         const __half * kr = s_kv + (wave * 16 + lane % 16) * KSTR + lane / 16;
@@ -750,11 +771,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int qi = lane / 16 + 4 * r;
-                const int q = min(q0 + qi, n_q - 1);
-                const float mv = mask_at(A, q, t0 + t);
-                s_s[qi * SS + t0 + t] = mv == -INFINITY ? -INFINITY : (float) acc[r] * A.scale + mv;
+                float * sp = s_s + qi * SS + t0 + t;
+                const float mv = *sp;
+                *sp = mv == -INFINITY ? -INFINITY : (float) acc[r] * A.scale + mv;
             }
         }
+        __syncthreads();                         // every wave's reads of this chunk's s_kv are done
+        ch = nx;
     }
     __syncthreads();
 
@@ -781,12 +804,14 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
     v4d acc[TPW];
 #pragma unroll
     for (int k = 0; k < TPW; k++) acc[k] = v4d{ 0.0, 0.0, 0.0, 0.0 };
-    for (int ch = 0; ch < n_chunks; ch++) {
-        __syncthreads();                         // s_live / p visible; previous s_kv reads done
-        if (!s_live[ch]) continue;
+    ch = next_live(0);
+    if (ch < n_chunks) load_rows(kv, vbase, A.v_nb2, ch * APF_CHUNK, min(APF_CHUNK, n_kv - ch * APF_CHUNK));
+    while (ch < n_chunks) {
         const int t0 = ch * APF_CHUNK, nt = min(APF_CHUNK, n_kv - t0);
-        stage(vbase, A.v_nb2, t0, nt, A.skip_masked && A.mask);
-        __syncthreads();
+        store_rows(kv, t0, nt, A.skip_masked && A.mask);
+        __syncthreads();                         // p of every row and this chunk's V rows visible
+        const int nx = next_live(ch + 1);
+        if (nx < n_chunks) load_rows(kv, vbase, A.v_nb2, nx * APF_CHUNK, min(APF_CHUNK, n_kv - nx * APF_CHUNK));
         for (int k0 = 0; k0 < APF_CHUNK; k0 += 4) {
             const int t = k0 + lane / 16;
             const double a = t < nt ? (double) s_s[(lane % 16) * SS + t0 + t] : 0.0;
@@ -799,6 +824,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
                 }
             }
         }
+        __syncthreads();                         // every wave's reads of this chunk's s_kv are done
+        ch = nx;
     }
 #pragma unroll
     for (int k = 0; k < TPW; k++) {
