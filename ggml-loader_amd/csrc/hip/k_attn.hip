@@ -13,8 +13,9 @@
 // projection, and any drift shifts values across int8 rounding boundaries, which the following
 // layers amplify.
 //
-// Four launches, each issuing its memory reads in independent batches (a dependent load per loop
-// iteration would put one L2/HBM round trip per iteration on the critical path):
+// Four launches (three for one query over at most PV_FS_MAX_KV positions), each issuing its memory
+// reads in independent batches (a dependent load per loop iteration would put one L2/HBM round
+// trip per iteration on the critical path):
 //   scores   (64-position chunk, KV head) workgroups: the chunk's K rows staged through LDS with
 //            coalesced 16-byte loads (rows padded by one dword so lane t reading row t is
 //            conflict-free); one wave per (query, head of the GQA group), lane = position; each
@@ -24,10 +25,12 @@
 //   pv       (128-position chunk, KV head) workgroups: 1/S from the segment sums (added in segment
 //            order), p = F16(exp(s - M) * (1/S)) for the chunk, the chunk's V rows staged in LDS
 //            (every load issued up front), one partial per (chunk, query, head) accumulated in
-//            double; one wave per (query, head), two dims per lane.
+//            double; one wave per (query, head), two dims per lane. For one query over a short
+//            row, (chunk, head) workgroups that form M and S themselves, and no stats launch.
 //   combine  one thread per output element: the partials added in chunk order (+ Q8_0 blocks).
 // Workgroups exchange results only across launch boundaries: a flag-and-fence hand-off inside a
-// launch costs a write-back and invalidation of the L2 of every XCD that takes part.
+// launch costs a write-back and invalidation of the L2 of every XCD that takes part (measured: the
+// combine folded into the PV launch behind a last-workgroup count took it from 8.6 to 44 us).
 // Scratch: see attn_scratch.
 #include "kernels.h"
 #include "tview_ops.h"
@@ -392,6 +395,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_laun
 constexpr int PV_MAX_ROWS = 8;
 constexpr int PV_NP = PV_CHUNK / ATT_WAVES;               // positions per wave
 constexpr int PV_SC = (PV_MAX_ROWS * PV_CHUNK + ATT_THREADS - 1) / ATT_THREADS;   // scores per thread
+// scores per thread of a PV workgroup that forms its own statistics (FSK below). Measured: 9 (rows
+// up to 2304 positions) beats the statistics launch (Llama-3B at 2049: 8.3 us against 6.3 + 4.0);
+// 17 (4097 positions, Qwen3-MoE attention) loses (16.5 us against 10.5 + 3.9).
+constexpr int PV_FS_SPT = 9;
+constexpr int PV_FS_MAX_KV = PV_FS_SPT * ATT_THREADS;
 
 template <int HD>
 constexpr int pv_lds_bytes() {
@@ -399,7 +407,65 @@ constexpr int pv_lds_bytes() {
     return (PV_CHUNK * HD * 2 > ATT_WAVES * PV_MAX_ROWS * HD * 8 ? PV_CHUNK * HD * 2 : ATT_WAVES * PV_MAX_ROWS * HD * 8);
 }
 
-template <int HD, int G>
+// The output of (head h, query q): two threads per dim each add half of the chunk partials in
+// chunk order, then the two halves are added (the sums are exact for these operands, so the
+// grouping does not change the result); stored as F32 and, with out_q, as Q8_0 blocks. Every
+// thread of the workgroup calls it (threads from 2 HD on only take part in its barrier).
+template <int HD>
+__device__ __forceinline__ void combine_head(const attn_launch & A, const attn_scratch & S, int h, int q, int n_splits,
+                                             double * s_half) {
+    const int d = threadIdx.x % HD, part = threadIdx.x / HD;
+    double acc = 0.0;
+    if (part < 2) {
+        const double * pp = S.parts + ((int64_t) q * A.n_head + h) * HD + d;
+        const int64_t step = (int64_t) A.n_q * A.n_head * HD;
+        const int mid = (n_splits + 1) / 2;
+        const int s0 = part ? mid : 0, s1 = part ? n_splits : mid;
+        int s = s0;
+        for (; s + 8 <= s1; s += 8) {
+            double v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = pp[(s + k) * step];
+#pragma unroll
+            for (int k = 0; k < 8; k++) acc += v[k];
+        }
+        for (; s < s1; s++) acc += pp[s * step];
+    }
+    if (part == 1) s_half[d] = acc;
+    __syncthreads();
+    if (part != 0) return;
+    acc += s_half[d];
+    const float v = (float) acc;
+    const int64_t oi = (int64_t) h * HD + d;
+    A.out[(int64_t) q * A.out_nb1 + oi] = v;
+    if (A.out_q.qs) {
+        // Q8_0 blocks of 32 consecutive dims (HD % 32 == 0): lanes d..d+31 share a half-wave
+        const float amax = group_max<32>(fabsf(v));
+        const float dd = amax / 127;
+        const float id = dd ? 1.0f / dd : 0.0f;
+        const int qv = (int) roundf(v * id);
+        const float qsum = group_sum<32>((float) qv);
+        const int64_t K = (int64_t) A.n_head * HD;
+        A.out_q.qs[q * K + oi] = (int8_t) qv;
+        if ((d % 32) == 0) {
+            A.out_q.d[q * (K / 32) + oi / 32] = __half2float(__float2half_rn(dd));
+            A.out_q.s[q * (K / 32) + oi / 32] = (int32_t) qsum;
+        }
+    }
+}
+
+// one workgroup of 2 HD threads per (head, query)
+template <int HD>
+__global__ __launch_bounds__(2 * HD) void attn_combine_kernel(const attn_launch A, int n_splits) {
+    __shared__ double s_half[HD];
+    combine_head<HD>(A, scratch_of(A), blockIdx.x, blockIdx.y, n_splits, s_half);
+}
+
+// FSK > 0 (one query, one head per workgroup, n_kv <= FSK * ATT_THREADS): the workgroup forms its row's
+// statistics itself, from the chunk maxima and every score of the row, instead of reading them from
+// the statistics launch; the sum is the statistics kernel's, exp(s - M) in double over the row's
+// positions (exact in practice, so its grouping does not matter). The statistics launch is not made.
+template <int HD, int G, int FSK>
 __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch A, int pvq) {
     constexpr int HD2 = HD / 2;
     constexpr int PIECES = HD / 8;                        // 16-byte pieces per V row
@@ -430,8 +496,26 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
         sc[k] = S.scores[row_of(pr) * A.n_kv + t0 + tt];
     }
     float rmax = 0.0f;
-    double ssum = 0.0;
-    if (t < n_rows) {
+    double ssum = 0.0, seg_sum = 0.0;
+    constexpr bool FS = FSK > 0;
+    constexpr int FR = FS ? G : 1, FK = FS ? FSK : 1;
+    float cm[FR], fv[FR][FK];
+    if constexpr (FS) {
+        // each row's chunk maxima (nch <= ATT_THREADS) and scores (FSK per thread)
+        const int nch = attn_chunks(A.n_kv);
+#pragma unroll
+        for (int r = 0; r < G; r++) cm[r] = S.cmax[row_of(r) * nch + min(t, nch - 1)];
+#pragma unroll
+        for (int r = 0; r < G; r++) {
+#pragma unroll
+            for (int k = 0; k < FK; k++) fv[r][k] = S.scores[row_of(r) * A.n_kv + min(t + k * ATT_THREADS, A.n_kv - 1)];
+        }
+    } else if (n_rows * nseg <= ATT_THREADS) {
+        // one segment sum per thread, issued with the other loads (a loop of dependent loads here
+        // would hold back the V loads below); added per row after the loads
+        if (t < n_rows) rmax = S.rmax[row_of(t)];
+        if (t < n_rows * nseg) seg_sum = S.ssum[row_of(t / nseg) * nseg + t % nseg];
+    } else if (t < n_rows) {
         rmax = S.rmax[row_of(t)];
         for (int k = 0; k < nseg; k++) ssum += S.ssum[row_of(t) * nseg + k];   // segment order
     }
@@ -454,6 +538,46 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
             for (int q = 0; q < nq && dead; q++) dead = mask_at(A, q0 + q, t0 + r) == -INFINITY;
             if (dead) vv[it] = make_uint4(0, 0, 0, 0);
         }
+    }
+    if constexpr (FS) {
+        __shared__ float s_fm[ATT_WAVES][FR];
+        __shared__ double s_fs[ATT_WAVES][FR];
+#pragma unroll
+        for (int r = 0; r < G; r++) {
+            const float m = wave_max(cm[r]);
+            if (lane == 0) s_fm[wave][r] = m;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < G; r++) {
+            const float M = fmaxf(fmaxf(s_fm[0][r], s_fm[1][r]), fmaxf(s_fm[2][r], s_fm[3][r]));
+            // every exp evaluated (clamped positions repeat a valid score) and the ones past the
+            // end dropped, so that the independent evaluations interleave
+            double a = 0.0;
+            if (M != -INFINITY) {
+                double e[FK];
+#pragma unroll
+                for (int k = 0; k < FK; k++) e[k] = (double) exp_cr(fv[r][k] - M);
+#pragma unroll
+                for (int k = 0; k < FK; k++) a += t + k * ATT_THREADS < A.n_kv ? e[k] : 0.0;
+            }
+            a = wave_sum_d(a);
+            if (lane == 0) s_fs[wave][r] = a;
+        }
+        __syncthreads();
+        if (t < G) {
+            rmax = fmaxf(fmaxf(s_fm[0][t], s_fm[1][t]), fmaxf(s_fm[2][t], s_fm[3][t]));
+            ssum = ((s_fs[0][t] + s_fs[1][t]) + s_fs[2][t]) + s_fs[3][t];
+        }
+    }
+    if (!FS && n_rows * nseg <= ATT_THREADS) {
+        double * s_seg = &s_p[0][0];  // s_p is not yet in use: the segment sums, [row][segment]
+        s_seg[t] = seg_sum;
+        __syncthreads();
+        if (t < n_rows) {
+            for (int k = 0; k < nseg; k++) ssum += s_seg[t * nseg + k];   // segment order
+        }
+        __syncthreads();
     }
     if (t < n_rows) {
         s_M[t] = rmax;
@@ -531,51 +655,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     }
 }
 
-// two threads per output element (head, dim) of one query: each adds half of the chunk partials in
-// chunk order, then the two halves are added (the sums are exact for these operands, so the
-// grouping does not change the result)
-template <int HD>
-__global__ __launch_bounds__(2 * HD) void attn_combine_kernel(const attn_launch A, int n_splits) {
-    __shared__ double s_half[HD];
-    const int h = blockIdx.x, q = blockIdx.y, d = threadIdx.x % HD, part = threadIdx.x / HD;
-    const attn_scratch S = scratch_of(A);
-    const double * pp = S.parts + ((int64_t) q * A.n_head + h) * HD + d;
-    const int64_t step = (int64_t) A.n_q * A.n_head * HD;
-    const int mid = (n_splits + 1) / 2;
-    const int s0 = part ? mid : 0, s1 = part ? n_splits : mid;
-    double acc = 0.0;
-    int s = s0;
-    for (; s + 8 <= s1; s += 8) {
-        double v[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = pp[(s + k) * step];
-#pragma unroll
-        for (int k = 0; k < 8; k++) acc += v[k];
-    }
-    for (; s < s1; s++) acc += pp[s * step];
-    if (part) s_half[d] = acc;
-    __syncthreads();
-    if (part) return;
-    acc += s_half[d];
-    const float v = (float) acc;
-    const int64_t oi = (int64_t) h * HD + d;
-    A.out[(int64_t) q * A.out_nb1 + oi] = v;
-    if (A.out_q.qs) {
-        // Q8_0 blocks of 32 consecutive dims (HD % 32 == 0): lanes d..d+31 share a half-wave
-        const float amax = group_max<32>(fabsf(v));
-        const float dd = amax / 127;
-        const float id = dd ? 1.0f / dd : 0.0f;
-        const int qv = (int) roundf(v * id);
-        const float qsum = group_sum<32>((float) qv);
-        const int64_t K = (int64_t) A.n_head * HD;
-        A.out_q.qs[q * K + oi] = (int8_t) qv;
-        if ((d % 32) == 0) {
-            A.out_q.d[q * (K / 32) + oi / 32] = __half2float(__float2half_rn(dd));
-            A.out_q.s[q * (K / 32) + oi / 32] = (int32_t) qsum;
-        }
-    }
-}
-
 template <int HD, int G>
 static void launch_attn_t(const attn_launch & A, hipStream_t st) {
     const int splits = (A.n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
@@ -589,10 +668,16 @@ static void launch_attn_t(const attn_launch & A, hipStream_t st) {
         big_lds = true;
     }
     launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head / G, qz), dim3(ATT_THREADS), dyn, st, A);
-    launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
     static_assert(G <= PV_MAX_ROWS, "PV rows");
     const int pvq = std::max(1, std::min(ATT_MAX_Q, PV_MAX_ROWS / G));   // queries per PV workgroup
-    launch((attn_pv_kernel<HD, G>), dim3(pv_splits, A.n_head / G, (A.n_q + pvq - 1) / pvq), dim3(ATT_THREADS), 0, st, A, pvq);
+    const dim3 pv_grid(pv_splits, A.n_head / G, (A.n_q + pvq - 1) / pvq);
+    if (A.n_q == 1 && A.n_kv <= PV_FS_MAX_KV) {
+        // one head per workgroup: each workgroup evaluates the exp of every score of its rows
+        launch((attn_pv_kernel<HD, 1, PV_FS_SPT>), dim3(pv_splits, A.n_head, 1), dim3(ATT_THREADS), 0, st, A, 1);
+    } else {
+        launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
+        launch((attn_pv_kernel<HD, G, 0>), pv_grid, dim3(ATT_THREADS), 0, st, A, pvq);
+    }
     launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(2 * HD), 0, st, A, pv_splits);
 }
 

@@ -531,6 +531,8 @@ def test_argmax_wide_row(hip, cpu, n, ties):
 
 @pytest.mark.parametrize("hd,n_head,n_head_kv,n_kv,n_new", [
     (128, 24, 8, 2049, 1),    # Llama-3B shape at position 2048
+    (128, 24, 8, 2304, 1),    # the longest row whose PV workgroups form the softmax statistics
+    (128, 24, 8, 2305, 1),    # the shortest row with the statistics launch
     (128, 32, 8, 8193, 1),    # Qwen3 shape at position 8192
     (128, 32, 4, 4097, 1),    # MoE config attention
     (96, 32, 32, 130, 1),     # Phi-3 head dim
