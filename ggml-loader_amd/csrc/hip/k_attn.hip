@@ -86,46 +86,22 @@ __device__ __forceinline__ float mask_at(const attn_launch & A, int q, int t) {
     return A.mask_f16 ? __half2float(((const __half *) row)[t]) : ((const float *) row)[t];
 }
 
-// stage rows [t0, t0+nt) of a [pos][hd] F16 cache view (row stride nb_pos halves) into LDS rows of
-// STRIDE dwords; rows nt..ROWS-1 are zero. Every load is issued before the first LDS store.
-struct no_work { __device__ void operator()() const {} };
-
-template <int HD, int STRIDE, int ROWS, typename F = no_work>
-__device__ __forceinline__ void stage_rows(uint32_t * dst, const __half * base, int64_t nb_pos, int t0, int nt, F while_loading = F()) {
-    constexpr int PIECES = HD / 8;                                   // 16-byte pieces per row
-    constexpr int ITER = ROWS * PIECES / ATT_THREADS;
-    uint4 v[ITER];
-#pragma unroll
-    for (int it = 0; it < ITER; it++) {
-        const int pc = threadIdx.x + it * ATT_THREADS;
-        const int r = pc / PIECES, c = pc % PIECES;
-        v[it] = make_uint4(0, 0, 0, 0);
-        if (r < nt) v[it] = *(const uint4 *) (base + (int64_t) (t0 + r) * nb_pos + c * 8);
-    }
-    while_loading();
-#pragma unroll
-    for (int it = 0; it < ITER; it++) {
-        const int pc = threadIdx.x + it * ATT_THREADS;
-        const int r = pc / PIECES, c = pc % PIECES;
-        uint32_t * d = dst + r * STRIDE + c * 4;
-        d[0] = v[it].x; d[1] = v[it].y; d[2] = v[it].z; d[3] = v[it].w;
-    }
-}
-
-// Dynamic LDS of the scores kernel, sized for the launch's n_q new tokens (floats): the Q rows
-// [n_q * G][HD] (sources, then rotated in place), the new K and V source rows [n_q][HD] each, the
-// norm weights of Q and K [HD] each, the chunk's mask rows [n_q][ATT_CHUNK], the (cos, sin) pairs
-// [n_q][HD / 2] and the norm scales [n_q * G + n_q].
+// Dynamic LDS of the scores kernel, sized for the launch's n_q new tokens (in floats): the Q rows
+// as the dots read them [n_q * G][HD], the Q source rows [n_q * G][HD], the new K and V source
+// rows [n_q][HD] each, the norm weights of Q and K [HD] each, the chunk's mask rows
+// [n_q][ATT_CHUNK], the (cos, sin) pairs [n_q][HD / 2] and the norm scales [n_q * G + n_q].
 template <int HD, int G>
 __host__ __device__ constexpr int scores_dyn_floats(int n_q) {
-    return n_q * G * HD + 2 * n_q * HD + 2 * HD + n_q * ATT_CHUNK + n_q * HD + n_q * G + n_q;
+    return 2 * n_q * G * HD + 2 * n_q * HD + 2 * HD + n_q * ATT_CHUNK + n_q * HD + n_q * G + n_q;
 }
 
+// Register budget: four waves per SIMD, so that four workgroups of a long row share each CU.
 template <int HD, int G>
-__global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_launch A) {
+__global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_launch A) {
     constexpr int HD2 = HD / 2;
     constexpr int STRIDE = HD2 + 4;   // dwords per staged K row: 16-byte aligned, rows offset by 4 banks
     __shared__ __align__(16) uint32_t s_k[ATT_CHUNK * STRIDE];
+    __shared__ __align__(16) uint32_t s_knew[ATT_MAX_Q * HD2];   // the new tokens' rotated K rows (F16)
     __shared__ float s_cm[ATT_WAVES][ATT_MAX_Q * 8];
     extern __shared__ __align__(16) float s_dyn[];
     // blockIdx.y: a group of G consecutive heads (all heads of KV head kvh, or a part of them when
@@ -138,7 +114,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
     const int q0 = blockIdx.z * ATT_MAX_Q;            // this workgroup's queries: q0 .. q0 + n_q - 1
     const int n_q = min(ATT_MAX_Q, A.n_q - q0);
     const attn_scratch S = scratch_of(A);
-    float * s_q = s_dyn;                              // [n_q * G][HD]
+    float * s_qr = s_dyn;                             // [n_q * G][HD]
+    float * s_q = s_qr + n_q * G * HD;                // [n_q * G][HD]
     float * s_kx = s_q + n_q * G * HD;                // [n_q][HD]
     float * s_vx = s_kx + n_q * HD;                   // [n_q][HD]
     float * s_qw = s_vx + n_q * HD;                   // [HD]
@@ -194,24 +171,38 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
         mk[q] = mrow[mask32 ? (int64_t) (q0 + min(q, n_q - 1)) * (A.mask_nb1 / 4) + t0 + min(lane, nt - 1) : 0];
     }
 
-    // While the chunk's K rows are in flight: the loaded values into LDS and the (cos, sin) of every
-    // rotation pair of the new tokens (one pair per thread; Q and K rotate with the same positions
-    // and parameters). The stores are unconditional, at the clamped indices (a thread past the end
-    // stores the last value again): a guarded store would let the compiler move its load behind the
-    // K loads.
-    stage_rows<HD, STRIDE, ATT_CHUNK>(s_k, A.k + (int64_t) kvh * A.k_nb1, A.k_nb2, t0, nt, [&]() {
+    // The chunk's K rows (16-byte pieces; every load unconditional, at a clamped row, since a
+    // guarded load makes the compiler wait for all loads before the next one) stay in registers
+    // while everything else happens: the loaded values into LDS and the (cos, sin) of every rotation pair of the new
+    // tokens (one pair per thread; Q and K rotate with the same positions and parameters), then
+    // QK-Norm and RoPE. Only then are the K rows stored to LDS, which waits for them. The stores
+    // are unconditional, at the clamped indices (a thread past the end stores the last value
+    // again): a guarded store would let the compiler move its load behind the K loads.
+    constexpr int PIECES = HD / 8;                                   // 16-byte pieces per K row
+    constexpr int KITER = ATT_CHUNK * PIECES / ATT_THREADS;
+    uint4 kv[KITER];
+    {
+        const __half * kbase = A.k + (int64_t) kvh * A.k_nb1;
 #pragma unroll
-        for (int j = 0; j < QR; j++) s_q[min(t + j * ATT_THREADS, nqe - 1)] = qv[j];
-#pragma unroll
-        for (int j = 0; j < KR; j++) {
-            const int i = min(t + j * ATT_THREADS, nke - 1);
-            s_kx[i] = kx[j];
-            s_vx[i] = vx[j];
+        for (int it = 0; it < KITER; it++) {
+            const int pc = t + it * ATT_THREADS;
+            const int r = pc / PIECES, c = pc % PIECES;
+            kv[it] = *(const uint4 *) (kbase + (int64_t) (t0 + min(r, nt - 1)) * A.k_nb2 + c * 8);
         }
-        s_qw[min(t, HD - 1)] = qw;
-        s_kw[min(t, HD - 1)] = kw;
+    }
 #pragma unroll
-        for (int q = 0; q < ATT_MAX_Q; q++) s_mk[min(q, n_q - 1) * ATT_CHUNK + min(lane, nt - 1)] = mk[q];
+    for (int j = 0; j < QR; j++) s_q[min(t + j * ATT_THREADS, nqe - 1)] = qv[j];
+#pragma unroll
+    for (int j = 0; j < KR; j++) {
+        const int i = min(t + j * ATT_THREADS, nke - 1);
+        s_kx[i] = kx[j];
+        s_vx[i] = vx[j];
+    }
+    s_qw[min(t, HD - 1)] = qw;
+    s_kw[min(t, HD - 1)] = kw;
+#pragma unroll
+    for (int q = 0; q < ATT_MAX_Q; q++) s_mk[min(q, n_q - 1) * ATT_CHUNK + min(lane, nt - 1)] = mk[q];
+    {
         float c = 1.0f, sn = 0.0f;
         if (cs_read) {
             c = cs_in.x;
@@ -221,8 +212,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
             if (A.cs_mode == 1 && blockIdx.x == 0 && blockIdx.y == 0 && t < n_q * half) A.cs_tab[tp] = make_float2(c, sn);
         }
         s_cs[tp] = make_float2(c, sn);
-    });
-    __syncthreads();   // K chunk, source rows, weights, mask, (cos, sin) in LDS
+    }
+    __syncthreads();   // source rows, weights, mask, (cos, sin) in LDS (the K rows may still be loading)
 
     // QK-Norm folded in: the scale of each Q row of the group and of each new K row, one wave per
     // row (the sum of squares in double, as the rms_norm op)
@@ -245,14 +236,15 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
         }
         __syncthreads();
     }
-    // Q rows in place: [normalized,] rotated, rounded to F16 (the mul_mat's conversion of Q). One
-    // rotation pair, or one element past n_dims, per item, so each item owns the values it rewrites.
+    // the Q rows as the dots read them: [normalized,] rotated, rounded to F16 (the mul_mat's
+    // conversion of Q). One rotation pair, or one element past n_dims, per item.
     const int np = A.rope ? A.rq.p.n_dims / 2 : 0;
     const bool neox = (A.rq.p.mode & GGML_ROPE_TYPE_NEOX) != 0;
     const int per_row = HD - np;
     for (int i = t; i < n_q * G * per_row; i += ATT_THREADS) {
         const int pr = i / per_row, k = i % per_row;
-        float * xr = s_q + pr * HD;
+        const float * xr = s_q + pr * HD;
+        float * yr = s_qr + pr * HD;
         const float sc = qnorm ? s_qs[pr] : 1.0f;
         if (k < np) {
             const int a0 = neox ? k : 2 * k, a1 = neox ? k + np : 2 * k + 1;
@@ -262,69 +254,85 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(const attn_lau
                 x1 = (x1 * sc) * s_qw[a1];
             }
             const float2 cs = s_cs[(pr / G) * np + k];
-            xr[a0] = __half2float(__float2half_rn(as_f32(x0 * cs.x - x1 * cs.y)));
-            xr[a1] = __half2float(__float2half_rn(as_f32(x0 * cs.y + x1 * cs.x)));
+            yr[a0] = __half2float(__float2half_rn(as_f32(x0 * cs.x - x1 * cs.y)));
+            yr[a1] = __half2float(__float2half_rn(as_f32(x0 * cs.y + x1 * cs.x)));
         } else {
             const int d = 2 * np + (k - np);
             float v = xr[d];
             if (qnorm) v = (v * sc) * s_qw[d];
-            xr[d] = __half2float(__float2half_rn(as_f32(v)));
+            yr[d] = __half2float(__float2half_rn(as_f32(v)));
         }
     }
-    if (A.rope) {
-        // the new positions of this chunk: K rotated into the cache and over its staged row, V appended
-        const int first_new = A.n_kv - n_q;
-        if (first_new + n_q > t0 && first_new < t0 + nt) {
-            for (int i = t; i < nke; i += ATT_THREADS) {
-                const int tk = i / HD, d = i % HD;
-                const int pos = first_new + tk;
-                if (pos < t0 || pos >= t0 + nt) continue;
-                const float * xr = s_kx + tk * HD;
-                const float sc = knorm ? s_ks[tk] : 1.0f;
-                const float kr = rope_value_with(A.rk.p, d, s_cs + tk * np, [&](int e) {
-                    return knorm ? (xr[e] * sc) * s_kw[e] : xr[e];
-                });
-                if (kv_writer) {
-                    st(at(A.rk.dst, d, kvh, tk, 0), GGML_TYPE_F16, kr);
-                    st(at(A.rv.dst, d, kvh, tk, 0), GGML_TYPE_F16, s_vx[i]);
-                }
-                ((__half *) (s_k + (pos - t0) * STRIDE))[d] = __float2half_rn(as_f32(kr));
+    // the new positions of this chunk: K rotated into the cache (by the workgroup of the KV head's
+    // first head group) and into s_knew, which the dots read for these positions; V appended
+    const int first_new = A.n_kv - n_q;
+    const bool has_new = A.rope && first_new + n_q > t0 && first_new < t0 + nt;
+    if (has_new) {
+        for (int i = t; i < nke; i += ATT_THREADS) {
+            const int tk = i / HD, d = i % HD;
+            const int pos = first_new + tk;
+            if (pos < t0 || pos >= t0 + nt) continue;
+            const float * xr = s_kx + tk * HD;
+            const float sc = knorm ? s_ks[tk] : 1.0f;
+            const float kr = rope_value_with(A.rk.p, d, s_cs + tk * np, [&](int e) {
+                return knorm ? (xr[e] * sc) * s_kw[e] : xr[e];
+            });
+            if (kv_writer) {
+                st(at(A.rk.dst, d, kvh, tk, 0), GGML_TYPE_F16, kr);
+                st(at(A.rv.dst, d, kvh, tk, 0), GGML_TYPE_F16, s_vx[i]);
             }
+            ((__half *) (s_knew + tk * HD2))[d] = __float2half_rn(as_f32(kr));
         }
+    }
+    asm volatile("" ::: "memory");   // the K rows' LDS stores (and their wait) stay after the above
+#pragma unroll
+    for (int it = 0; it < KITER; it++) {
+        const int pc = t + it * ATT_THREADS;
+        const int r = pc / PIECES, c = pc % PIECES;
+        const bool live = r < nt;            // rows past the end: zero (their loads read the last row)
+        uint32_t * d = s_k + r * STRIDE + c * 4;
+        d[0] = live ? kv[it].x : 0u; d[1] = live ? kv[it].y : 0u; d[2] = live ? kv[it].z : 0u; d[3] = live ? kv[it].w : 0u;
     }
     __syncthreads();
 
     // ---- dots: wave w takes positions 16w .. 16w + 15 of the chunk; lane = (position, quarter of
-    // the head dims). The lane's K slice stays in registers for every (query, head) row of the
-    // group; products of two F16 values are exact in f32 and their sum accumulates in double (exact
-    // for these operands, so splitting it over chains and quarters does not change it), then the
-    // four quarters are added by DPP within each quad of lanes. ----
+    // the head dims). The lane's K slice is widened to double once and kept in registers for every
+    // (query, head) row of the group. Each product of two F16 values is exact in double, so
+    // fma(k, q, acc) rounds as acc + (double) (k * q) does: the sum accumulates in double (exact for
+    // these operands, so splitting it over chains and quarters does not change it), then the four
+    // quarters are added by DPP within each quad of lanes. ----
     constexpr int DQ = HD / 4;                          // dims per lane
     const int pi = lane / 4, dq = lane % 4;
     const int tl = wave * 16 + pi;                      // position in the chunk
     const bool ok = tl < nt;
-    uint32_t kk[DQ / 2];
+    double kd[DQ];
     {
-        const uint4 * kp = (const uint4 *) (s_k + tl * STRIDE + dq * (DQ / 2));
+        const bool is_new = has_new && ok && t0 + tl >= first_new;
+        const uint32_t * src = is_new ? s_knew + (t0 + tl - first_new) * HD2 : s_k + tl * STRIDE;
+        const uint4 * kp = (const uint4 *) (src + dq * (DQ / 2));
 #pragma unroll
         for (int j = 0; j < DQ / 8; j++) {
             const uint4 v = kp[j];
-            kk[4 * j] = v.x; kk[4 * j + 1] = v.y; kk[4 * j + 2] = v.z; kk[4 * j + 3] = v.w;
+            const uint32_t w[4] = { v.x, v.y, v.z, v.w };
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float2 f = __half22float2(*(const __half2 *) &w[e]);
+                kd[8 * j + 2 * e] = (double) f.x;
+                kd[8 * j + 2 * e + 1] = (double) f.y;
+            }
         }
     }
     for (int pr = 0; pr < n_q * G; pr++) {
         const int q = pr / G, h = h0 + pr % G;
-        const float4 * qv = (const float4 *) (s_q + pr * HD + dq * DQ);
+        const float4 * qv4 = (const float4 *) (s_qr + pr * HD + dq * DQ);
         double a[4] = { 0.0, 0.0, 0.0, 0.0 };
 #pragma unroll
         for (int j = 0; j < DQ / 4; j++) {
-            const float4 q4 = qv[j];
-            const float2 k01 = __half22float2(*(const __half2 *) &kk[2 * j]);
-            const float2 k23 = __half22float2(*(const __half2 *) &kk[2 * j + 1]);
-            a[0] += (double) (k01.x * q4.x);
-            a[1] += (double) (k01.y * q4.y);
-            a[2] += (double) (k23.x * q4.z);
-            a[3] += (double) (k23.y * q4.w);
+            const float4 q4 = qv4[j];
+            a[0] = fma(kd[4 * j], (double) q4.x, a[0]);
+            a[1] = fma(kd[4 * j + 1], (double) q4.y, a[1]);
+            a[2] = fma(kd[4 * j + 2], (double) q4.z, a[2]);
+            a[3] = fma(kd[4 * j + 3], (double) q4.w, a[3]);
         }
         double dot = (a[0] + a[1]) + (a[2] + a[3]);
         dot += dpp_d<0xB1>(dot);
@@ -526,17 +534,22 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
         const int pc = t + it * ATT_THREADS;
         const int r = pc / PIECES, c = pc % PIECES;
         vv[it] = *(const uint4 *) (vbase + (int64_t) (t0 + min(r, nt - 1)) * A.v_nb2 + c * 8);
-        if (r >= nt) vv[it] = make_uint4(0, 0, 0, 0);   // padding rows: no term
     }
+    // rows staged as zero: padding rows past the end (their loads read the last row; no term) and,
+    // with skip_masked, rows masked for every query of the workgroup (their p is 0 for every row).
+    // Applied when the rows are stored to LDS: zeroing a register right after its load would make
+    // the compiler wait for every load issued so far.
+    bool vzero[ITER];
+#pragma unroll
+    for (int it = 0; it < ITER; it++) vzero[it] = (t + it * ATT_THREADS) / PIECES >= nt;
     if (A.skip_masked && A.mask) {
-        // rows masked for every query of the workgroup read as zero (their p is 0 for every row)
         const int nq = min(pvq, A.n_q - q0);
 #pragma unroll
         for (int it = 0; it < ITER; it++) {
             const int r = (t + it * ATT_THREADS) / PIECES;
             bool dead = r < nt;
             for (int q = 0; q < nq && dead; q++) dead = mask_at(A, q0 + q, t0 + r) == -INFINITY;
-            if (dead) vv[it] = make_uint4(0, 0, 0, 0);
+            vzero[it] = vzero[it] || dead;
         }
     }
     if constexpr (FS) {
@@ -604,7 +617,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
         const int pc = t + it * ATT_THREADS;
         const int r = pc / PIECES, c = pc % PIECES;
         uint32_t * d = s_v + r * HD2 + c * 4;
-        d[0] = vv[it].x; d[1] = vv[it].y; d[2] = vv[it].z; d[3] = vv[it].w;
+        const bool z = vzero[it];
+        d[0] = z ? 0u : vv[it].x; d[1] = z ? 0u : vv[it].y; d[2] = z ? 0u : vv[it].z; d[3] = z ? 0u : vv[it].w;
     }
     __syncthreads();
 
