@@ -157,12 +157,17 @@ __global__ __launch_bounds__(256, WTM == 1 ? 4 : 1) void gemm_q_kernel(const gem
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
+    // Stage s's loads are issued before stage s - 1's dots and stored to LDS at the top of
+    // iteration s, so the previous stage's MFMAs and epilogue cover their latency (stored at the end
+    // of the iteration, the compiler would move the stores and their wait ahead of the epilogue).
+    // One barrier per stage: a stage's stores go to the buffer that the stage before last read, and
+    // every wave passed the last barrier after that.
     const int64_t n_stages = nb / KB;
     load(0);
-    store(0);
-    __syncthreads();
     for (int64_t s = 0; s < n_stages; s++) {
         const int buf = (int) (s & 1);
+        store(buf);
+        __syncthreads();
         if (s + 1 < n_stages) load((s + 1) * KB);
         const int8_t * A = sA + buf * C::A_BYTES;
         const int8_t * B = sB + buf * C::B_BYTES;
@@ -198,8 +203,6 @@ __global__ __launch_bounds__(256, WTM == 1 ? 4 : 1) void gemm_q_kernel(const gem
                     }
                 }
         }
-        if (s + 1 < n_stages) store(buf ^ 1);
-        __syncthreads();
     }
 
 #pragma unroll
