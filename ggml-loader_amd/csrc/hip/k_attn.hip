@@ -766,8 +766,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
     __shared__ __half s_q[APF_Q * KSTR];
     __shared__ __half s_kv[APF_CHUNK * KSTR];
     __shared__ int s_live[APF_MAX_CHUNKS];
+    __shared__ int s_live_end;       // one past the last live chunk
     extern __shared__ float s_s[];   // [APF_Q][SS]: scores, then e, then p
-    const int q0 = blockIdx.x * APF_Q, h = blockIdx.y;
+    // the last query tiles first: under a causal mask they see the most positions, and started
+    // last they would leave the chip waiting on a few long workgroups
+    const int q0 = (gridDim.x - 1 - blockIdx.x) * APF_Q, h = blockIdx.y;
     const int kvh = h / (A.n_head / A.n_head_kv);
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
     const int n_kv = A.n_kv, n_q = A.n_q;
@@ -783,35 +786,40 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
         s_q[qi * KSTR + d] = __float2half_rn(A.q[(int64_t) h * A.q_nb1 + (int64_t) q * A.q_nb2 + d]);
     }
 
-    // rows [t0, t0 + nt) of a cache view into registers (zero past nt), and from there into s_kv.
-    // zero_dead: rows masked for every query of the tile also read as zero (skip_masked)
-    constexpr int ITER = (APF_CHUNK * PIECES + ATT_THREADS - 1) / ATT_THREADS;
+    // rows [t0, t0 + nt) of a cache view into registers, and from there into s_kv (zero past nt;
+    // with zero_dead, rows masked for every query of the tile also read as zero: skip_masked). The
+    // loads are unconditional, at clamped rows, and the zeroing happens at the LDS store: a guarded
+    // load, or a register zeroed right after its load, makes the compiler wait for every load.
+    static_assert(APF_CHUNK * PIECES % ATT_THREADS == 0, "whole 16-byte pieces per thread");
+    constexpr int ITER = APF_CHUNK * PIECES / ATT_THREADS;
     auto load_rows = [&](uint4 (&v)[ITER], const __half * base, int64_t nb_pos, int t0, int nt) {
 #pragma unroll
         for (int it = 0; it < ITER; it++) {
             const int pc = threadIdx.x + it * ATT_THREADS;
             const int r = pc / PIECES, c = pc % PIECES;
-            v[it] = make_uint4(0, 0, 0, 0);
-            if (pc < APF_CHUNK * PIECES && r < nt) v[it] = *(const uint4 *) (base + (int64_t) (t0 + r) * nb_pos + c * 8);
+            v[it] = *(const uint4 *) (base + (int64_t) (t0 + min(r, nt - 1)) * nb_pos + c * 8);
         }
     };
     auto store_rows = [&](uint4 (&v)[ITER], int t0, int nt, bool zero_dead) {
+        bool zero[ITER];
+#pragma unroll
+        for (int it = 0; it < ITER; it++) zero[it] = (threadIdx.x + it * ATT_THREADS) / PIECES >= nt;
         if (zero_dead) {
 #pragma unroll
             for (int it = 0; it < ITER; it++) {
                 const int r = (threadIdx.x + it * ATT_THREADS) / PIECES;
                 bool dead = r < nt;
                 for (int q = q0; q < min(q0 + APF_Q, n_q) && dead; q++) dead = mask_at(A, q, t0 + r) == -INFINITY;
-                if (dead) v[it] = make_uint4(0, 0, 0, 0);
+                zero[it] = zero[it] || dead;
             }
         }
 #pragma unroll
         for (int it = 0; it < ITER; it++) {
             const int pc = threadIdx.x + it * ATT_THREADS;
-            if (pc >= APF_CHUNK * PIECES) break;
             const int r = pc / PIECES, c = pc % PIECES;
             uint32_t * d = (uint32_t *) (s_kv + r * KSTR + c * 8);
-            d[0] = v[it].x; d[1] = v[it].y; d[2] = v[it].z; d[3] = v[it].w;
+            const bool z = zero[it];
+            d[0] = z ? 0u : v[it].x; d[1] = z ? 0u : v[it].y; d[2] = z ? 0u : v[it].z; d[3] = z ? 0u : v[it].w;
         }
     };
     auto next_live = [&](int ch) {
@@ -820,29 +828,44 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
     };
 
     // the tile's mask rows into s_s (rows past n_q repeat the last query's; 0 without a mask), read
-    // once here instead of in every chunk
-    for (int idx = threadIdx.x; idx < APF_Q * n_kv; idx += ATT_THREADS) {
-        const int qi = idx / n_kv, t = idx % n_kv;
-        s_s[qi * SS + t] = A.mask ? mask_at(A, min(q0 + qi, n_q - 1), t) : 0.0f;
-    }
-    __syncthreads();
-    // chunk liveness, one wave per chunk: a chunk whose mask is -inf for every query of the tile is
-    // not computed, its scores are -inf (as the chain forms them)
-    for (int ch = wave; ch < n_chunks; ch += ATT_WAVES) {
-        const int t0 = ch * APF_CHUNK, nt = min(APF_CHUNK, n_kv - t0);
-        int any = !A.mask;
-        for (int idx = lane; idx < APF_Q * APF_CHUNK && !any; idx += WAVE) {
-            const int qi = idx / APF_CHUNK, t = idx % APF_CHUNK;
-            if (q0 + qi < n_q && t < nt && s_s[qi * SS + t0 + t] != -INFINITY) any = 1;
-        }
-        const bool live = __any(any);
-        if (!live) {
-            for (int idx = lane; idx < APF_Q * APF_CHUNK; idx += WAVE) {
-                const int qi = idx / APF_CHUNK, t = idx % APF_CHUNK;
-                if (t < nt) s_s[qi * SS + t0 + t] = -INFINITY;
+    // once here instead of in every chunk: one position per thread and row at a time, the loads of
+    // all APF_Q rows in flight together (unconditional, at clamped positions)
+    if (threadIdx.x == 0) s_live_end = 0;
+    auto stage_mask = [&](auto load) {
+        for (int t0 = 0; t0 < n_kv; t0 += ATT_THREADS) {
+            const int t = min(t0 + (int) threadIdx.x, n_kv - 1);
+            float v[APF_Q];
+#pragma unroll
+            for (int qi = 0; qi < APF_Q; qi++) v[qi] = load(min(q0 + qi, n_q - 1), t);
+            if (t0 + (int) threadIdx.x < n_kv) {
+#pragma unroll
+                for (int qi = 0; qi < APF_Q; qi++) s_s[qi * SS + t] = v[qi];
             }
         }
-        if (lane == 0) s_live[ch] = live;
+    };
+    if (!A.mask) stage_mask([&](int, int) { return 0.0f; });
+    else if (A.mask_f16) stage_mask([&](int q, int t) { return __half2float(((const __half *) ((const char *) A.mask + (int64_t) q * A.mask_nb1))[t]); });
+    else stage_mask([&](int q, int t) { return ((const float *) ((const char *) A.mask + (int64_t) q * A.mask_nb1))[t]; });
+    __syncthreads();
+    // chunk liveness, one wave per chunk (lane = position): a chunk whose mask is -inf for every
+    // query of the tile is not computed. Its staged values are then -inf in every row (rows past
+    // n_q repeat the last query's), which are the scores the chain forms for it.
+    static_assert(APF_CHUNK == WAVE, "one position per lane");
+    for (int ch = wave; ch < n_chunks; ch += ATT_WAVES) {
+        const int t = ch * APF_CHUNK + lane;
+        bool any = !A.mask;
+        if (t < n_kv) {
+            float v[APF_Q];
+#pragma unroll
+            for (int qi = 0; qi < APF_Q; qi++) v[qi] = s_s[qi * SS + t];
+#pragma unroll
+            for (int qi = 0; qi < APF_Q; qi++) any = any || (q0 + qi < n_q && v[qi] != -INFINITY);
+        }
+        const bool live = __any(any);
+        if (lane == 0) {
+            s_live[ch] = live;
+            if (live) atomicMax(&s_live_end, ch + 1);
+        }
     }
     __syncthreads();
 
@@ -856,15 +879,20 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
         __syncthreads();
         const int nx = next_live(ch + 1);
         if (nx < n_chunks) load_rows(kv, kbase, A.k_nb2, nx * APF_CHUNK, min(APF_CHUNK, n_kv - nx * APF_CHUNK));
-        v4d acc = { 0.0, 0.0, 0.0, 0.0 };
+        // two independent accumulation chains (dims 8i .. 8i + 3 and 8i + 4 .. 8i + 7), added at
+        // the end: the double sums are exact for these operands, so the grouping does not matter
+        v4d acc = { 0.0, 0.0, 0.0, 0.0 }, acc2 = { 0.0, 0.0, 0.0, 0.0 };
         const __half * qr = s_q + (lane % 16) * KSTR + lane / 16;
         const __half * kr = s_kv + (wave * 16 + lane % 16) * KSTR + lane / 16;
+        static_assert(HD % 8 == 0, "pairs of 4-dim steps");
 #pragma unroll 4
-        for (int d0 = 0; d0 < HD; d0 += 4) {
-            const double a = (double) __half2float(qr[d0]);
-            const double b = (double) __half2float(kr[d0]);
+        for (int d0 = 0; d0 < HD; d0 += 8) {
+            const double a = (double) __half2float(qr[d0]), a2 = (double) __half2float(qr[d0 + 4]);
+            const double b = (double) __half2float(kr[d0]), b2 = (double) __half2float(kr[d0 + 4]);
             acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(a2, b2, acc2, 0, 0, 0);
         }
+        acc += acc2;
         const int t = wave * 16 + lane % 16;
         if (t < nt) {
 #pragma unroll
@@ -880,29 +908,37 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
     }
     __syncthreads();
 
-    // ---- row statistics and probabilities ----
+    // ---- row statistics and probabilities, over the positions before the end of the last live
+    // chunk (later ones are -inf, take no part in the sums and are never read again); unrolled so
+    // that independent exps interleave ----
+    const int n_pos = min(s_live_end * APF_CHUNK, n_kv);
     for (int qi = wave; qi < APF_Q; qi += ATT_WAVES) {
         float * row = s_s + qi * SS;
         float m = -INFINITY;
-        for (int t = lane; t < n_kv; t += WAVE) m = fmaxf(m, row[t]);
+        for (int t = lane; t < n_pos; t += WAVE) m = fmaxf(m, row[t]);
         m = wave_max(m);
         double sum = 0.0;
-        for (int t = lane; t < n_kv; t += WAVE) {
-            const float e = m == -INFINITY ? 0.0f : exp_cr(row[t] - m);
-            row[t] = e;
-            sum += (double) e;
+        if (m != -INFINITY) {
+#pragma unroll 4
+            for (int t = lane; t < n_pos; t += WAVE) {
+                const float e = exp_cr(row[t] - m);
+                row[t] = e;
+                sum += (double) e;
+            }
+        } else {
+            for (int t = lane; t < n_pos; t += WAVE) row[t] = 0.0f;   // a row masked throughout: p = 0
         }
         sum = wave_sum_d(sum);
         const float inv = sum > 0.0 ? (float) (1.0 / sum) : 0.0f;
-        for (int t = lane; t < n_kv; t += WAVE) row[t] = __half2float(__float2half_rn(as_f32(row[t] * inv)));
+        for (int t = lane; t < n_pos; t += WAVE) row[t] = __half2float(__float2half_rn(as_f32(row[t] * inv)));
     }
 
     // ---- P V ----
     constexpr int NT = HD / 16;                  // 16-dim output tiles
     constexpr int TPW = (NT + ATT_WAVES - 1) / ATT_WAVES;
-    v4d acc[TPW];
+    v4d acc[TPW], acc2[TPW];
 #pragma unroll
-    for (int k = 0; k < TPW; k++) acc[k] = v4d{ 0.0, 0.0, 0.0, 0.0 };
+    for (int k = 0; k < TPW; k++) acc[k] = acc2[k] = v4d{ 0.0, 0.0, 0.0, 0.0 };
     ch = next_live(0);
     if (ch < n_chunks) load_rows(kv, vbase, A.v_nb2, ch * APF_CHUNK, min(APF_CHUNK, n_kv - ch * APF_CHUNK));
     while (ch < n_chunks) {
@@ -911,15 +947,19 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
         __syncthreads();                         // p of every row and this chunk's V rows visible
         const int nx = next_live(ch + 1);
         if (nx < n_chunks) load_rows(kv, vbase, A.v_nb2, nx * APF_CHUNK, min(APF_CHUNK, n_kv - nx * APF_CHUNK));
-        for (int k0 = 0; k0 < APF_CHUNK; k0 += 4) {
-            const int t = k0 + lane / 16;
+        // two accumulation chains per output tile (positions 8i .. 8i + 3 and 8i + 4 .. 8i + 7)
+        for (int k0 = 0; k0 < APF_CHUNK; k0 += 8) {
+            const int t = k0 + lane / 16, t2 = t + 4;
             const double a = t < nt ? (double) s_s[(lane % 16) * SS + t0 + t] : 0.0;
+            const double a2 = t2 < nt ? (double) s_s[(lane % 16) * SS + t0 + t2] : 0.0;
 #pragma unroll
             for (int k = 0; k < TPW; k++) {
                 const int jt = wave + k * ATT_WAVES;
                 if (jt < NT) {
                     const double b = (double) __half2float(s_kv[t * KSTR + jt * 16 + lane % 16]);
+                    const double b2 = (double) __half2float(s_kv[t2 * KSTR + jt * 16 + lane % 16]);
                     acc[k] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[k], 0, 0, 0);
+                    acc2[k] = __builtin_amdgcn_mfma_f64_16x16x4f64(a2, b2, acc2[k], 0, 0, 0);
                 }
             }
         }
@@ -930,6 +970,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
     for (int k = 0; k < TPW; k++) {
         const int jt = wave + k * ATT_WAVES;
         if (jt >= NT) continue;
+        acc[k] += acc2[k];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int q = q0 + lane / 16 + 4 * r;
