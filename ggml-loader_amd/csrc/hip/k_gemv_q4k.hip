@@ -31,6 +31,7 @@
 namespace {
 
 constexpr int Q4K_MAX_WAVES = 16;
+constexpr int Q4K_BS_PER = 4;      // 16-element sums of a pre-quantized column per thread (K / 16 <= 4 threads)
 
 __host__ __device__ constexpr int q4k_term_stride(int lpr) { return (lpr / 4) * 9 + 1; }
 
@@ -151,6 +152,8 @@ __global__ __launch_bounds__(MAXT) void gemv_q4k_kernel(const gemv_kargs a) {
     // the pre-quantized column's 32-byte sub-blocks (two per thread at most) ----
     float4 xv[CPT], wv[CPT];
     int4 pa[2], pb[2];
+    int16_t bsv[Q4K_BS_PER];
+    float xdv = 0.0f;
     if constexpr (PRO != 0) {
         const float4 * x4 = (const float4 *) (L.norm.x + (int64_t) xcol * L.norm.x_stride);
         const float4 * w4 = (const float4 *) (PRO == 1 && L.norm.w ? L.norm.w : L.norm.x);
@@ -168,9 +171,18 @@ __global__ __launch_bounds__(MAXT) void gemv_q4k_kernel(const gemv_kargs a) {
             pa[k] = *(const int4 *) (xq + sub * 32);
             pb[k] = *(const int4 *) (xq + sub * 32 + 16);
         }
+        // the column's 16-element sums and super-block scales too (unconditional, at clamped
+        // indices): loaded in a loop after the weights, each would wait for every weight load
+        const int16_t * gbs = L.xbs + (int64_t) xcol * (K / 16);
+#pragma unroll
+        for (int k = 0; k < Q4K_BS_PER; k++) bsv[k] = gbs[min(t + k * nt, K / 16 - 1)];
+        xdv = L.xd[(int64_t) xcol * nsb + min(t, nsb - 1)];
     }
 
-    // ---- every weight load of this lane (row and unit clamped into the matrix) ----
+    // ---- every weight load of this lane (row and unit clamped into the matrix), issued after the
+    // activation's (the empty asm keeps the compiler from moving any of those behind them:
+    // waiting for one would then wait for the weights) ----
+    asm volatile("" ::: "memory");
     uint4 hd[NCH][ITS], qa[NCH][ITS], qb[NCH][ITS];
     const int64_t row_bytes = (int64_t) nsb * Q4_K_BYTES;
 #pragma unroll
@@ -190,9 +202,11 @@ __global__ __launch_bounds__(MAXT) void gemv_q4k_kernel(const gemv_kargs a) {
     // ---- the activation into LDS ----
     if constexpr (PRO == 0) {
         const int nsub = K / 32;
-        const int16_t * gbs = L.xbs + (int64_t) xcol * (K / 16);
-        for (int i = t; i < K / 16; i += nt) s.xbs[i] = gbs[i];
-        for (int i = t; i < nsb; i += nt) s.xd[i] = L.xd[(int64_t) xcol * nsb + i];
+#pragma unroll
+        for (int k = 0; k < Q4K_BS_PER; k++) {
+            if (t + k * nt < K / 16) s.xbs[t + k * nt] = bsv[k];
+        }
+        if (t < nsb) s.xd[t] = xdv;
 #pragma unroll
         for (int k = 0; k < 2; k++) {
             const int sub = t + k * nt;
@@ -440,6 +454,9 @@ void launch_gemv_q4k(const gemv_launch & L, hipStream_t st) {
     q4k_shape_of(L.K / 64, L.swiglu, sh);
     q4k_prologue_of(pro, L.K, sh);
     ka.rows_per_block = sh.waves * (WAVE / sh.lpr);
+    const int nthr = sh.waves * WAVE;
+    if (pro == 0 && (L.K / 32 > 2 * nthr || L.K / 16 > Q4K_BS_PER * nthr || L.K / 256 > nthr))
+        HIP_ABORT("gemv q4_K: a pre-quantized column of K=%d needs more than %d threads", L.K, nthr);
     if (L.swiglu) {
         if (L.n_mats != 2 || L.m[0].n_rows != L.m[1].n_rows) HIP_ABORT("gemv: swiglu needs two equal matrices");
         for (int i = 0; i <= GEMV_MAX_MATS; i++) ka.row_begin[i] = 0;
