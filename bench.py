@@ -568,7 +568,7 @@ def decode_bench(gl, args):
                   f"({1000 * secs_ev / args.steps:.3f} ms/step with the events)",
     }
     if "attn_decode" in prof:
-        # the layer's decode attention (scores, statistics, PV, combination launches together), from
+        # the layer's decode attention (scores, [statistics,] PV, combination launches together), from
         # the breakdown steps; algorithmic bytes: the K and V rows read, Q in, the output out, the mask
         n_a, ms_a, by_a = prof["attn_decode"]
         a_ach = by_a / (ms_a * 1e-3) / 1e9 if ms_a > 0 else 0.0
@@ -577,7 +577,7 @@ def decode_bench(gl, args):
             "bound": "hbm", "achieved": round(a_ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(a_ach / PEAK_HBM_GBS, 4),
             "traffic": json.load(open(aj))["traffic_bytes_per_layer"] if batch == 1 and os.path.exists(aj) else None,
-            "kernel": "decode attention of one layer (attn_scores + attn_stats + attn_pv + attn_combine)",
+            "kernel": "decode attention of one layer (attn_scores, attn_pv, attn_combine; attn_stats too past 2304 positions)",
             "us_per_layer": round(ms_a / n_a * 1e3, 2), "bytes_per_layer": round(by_a / n_a),
             "timing": f"HIP events around each layer's attention launches in {args.breakdown_steps} untimed steps",
         }

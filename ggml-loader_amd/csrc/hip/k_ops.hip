@@ -470,17 +470,20 @@ void launch_get_rows(const tview & a, const tview & ids, const tview & dst, cons
 // ---------------------------------------------------------------------------------------------
 // RoPE: one thread per rotated pair of one (head, token) row
 
-// pair li of a RoPE job (row-major over pairs of the src rows); the result is stored in dst's type
-__device__ __forceinline__ void rope_pair(const rope_job & J, int64_t li) {
+// pair li of a RoPE job (row-major over pairs of the src rows); the result is stored in dst's type.
+// IDX: the index type of the unflattening (32-bit when the job's items fit, which costs a fraction
+// of the 64-bit divisions: this kernel's time is mostly its index arithmetic)
+template <typename IDX>
+__device__ __forceinline__ void rope_pair(const rope_job & J, IDX li) {
     const tview & x = J.src;
     const tview & d = J.dst;
     const rope_params & p = J.p;
-    const int64_t half = x.ne[0] / 2;
-    const int64_t ip = li % half;
-    int64_t r = li / half;
-    const int64_t i1 = r % x.ne[1]; r /= x.ne[1];
-    const int64_t i2 = r % x.ne[2]; r /= x.ne[2];
-    const int64_t i3 = r;
+    const IDX half = (IDX) (x.ne[0] / 2), n1 = (IDX) x.ne[1], n2 = (IDX) x.ne[2];
+    const IDX ip = li % half;
+    IDX r = li / half;
+    const IDX i1 = r % n1; r /= n1;
+    const IDX i2 = r % n2; r /= n2;
+    const IDX i3 = r;
     const int i0 = (int) (2 * ip);
     if (i0 >= p.n_dims) {
         for (int k = 0; k < 2; k++) st(at(d, i0 + k, i1, i2, i3), d.type, *(const float *) at(x, i0 + k, i1, i2, i3));
@@ -504,10 +507,20 @@ __device__ __forceinline__ void rope_pair(const rope_job & J, int64_t li) {
 }
 
 // element li of a copy job (row-major over src, written row-major over dst, converted to dst's type)
-__device__ __forceinline__ void copy_elem(const rope_job & J, int64_t li) {
-    const idx4 a = unflatten(li, J.src.ne);
-    const idx4 b = unflatten(li, J.dst.ne);
-    st(at(J.dst, b.i0, b.i1, b.i2, b.i3), J.dst.type, ld(at(J.src, a.i0, a.i1, a.i2, a.i3), J.src.type));
+template <typename IDX>
+__device__ __forceinline__ void copy_elem(const rope_job & J, IDX li) {
+    auto unflat = [](IDX i, const int64_t ne[4], IDX (&o)[4]) {
+        const IDX n0 = (IDX) ne[0], n1 = (IDX) ne[1], n2 = (IDX) ne[2];
+        o[0] = i % n0; i /= n0;
+        o[1] = i % n1; i /= n1;
+        o[2] = i % n2; o[3] = i / n2;
+    };
+    IDX a[4], b[4];
+    unflat(li, J.src.ne, a);
+    const bool same = J.src.ne[0] == J.dst.ne[0] && J.src.ne[1] == J.dst.ne[1] && J.src.ne[2] == J.dst.ne[2];
+    if (same) { b[0] = a[0]; b[1] = a[1]; b[2] = a[2]; b[3] = a[3]; }
+    else unflat(li, J.dst.ne, b);
+    st(at(J.dst, b[0], b[1], b[2], b[3]), J.dst.type, ld(at(J.src, a[0], a[1], a[2], a[3]), J.src.type));
 }
 
 // Independent RoPE and copy jobs of one decode step in one launch (Q rotation; K rotation stored
@@ -519,8 +532,13 @@ __global__ __launch_bounds__(256) void rope_batch_kernel(const rope_batch B) {
     const rope_job & J = B.job[j];
     const int64_t li = ((int64_t) blockIdx.x - B.first_block[j]) * blockDim.x + threadIdx.x;
     if (li >= J.n) return;
-    if (J.pos) rope_pair(J, li);
-    else copy_elem(J, li);
+    if (J.n <= (int64_t) UINT32_MAX) {
+        if (J.pos) rope_pair<uint32_t>(J, (uint32_t) li);
+        else copy_elem<uint32_t>(J, (uint32_t) li);
+    } else {
+        if (J.pos) rope_pair<int64_t>(J, li);
+        else copy_elem<int64_t>(J, li);
+    }
 }
 
 void launch_rope_batch(rope_batch & B, hipStream_t st) {
