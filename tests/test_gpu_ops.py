@@ -169,6 +169,29 @@ def test_gemm_prefill(hip, cpu, qtype, K, N, ncols):
     assert np.array_equal(a, b), rel_err(a, b)
 
 
+@pytest.mark.parametrize("qtype", [gl.Q8_0, gl.Q4_0])
+def test_gemm_subnormal_scales(hip, cpu, qtype):
+    """Blocks whose F16 scales are subnormal (d below 2^-14) in the weights, the activations and
+    both, among normal blocks: the block terms formed exactly, whichever unit forms the scale
+    products."""
+    K, N, ncols = 512, 256, 64
+    w = rng(91).standard_normal((N, K)).astype(np.float32) * 0.02
+    w[:, :256] *= 1e-2 if qtype == gl.Q8_0 else 1e-3      # Q4_0's d is amax / 8
+    x = rng(92).standard_normal((ncols, K)).astype(np.float32)
+    x[:, 128:384] *= 2e-4
+    wq = quantize(w, qtype, impl="product")
+    d16 = np.frombuffer(wq, np.uint8).reshape(N, -1)[:, :2].copy().view(np.float16)   # first block's d
+    assert (np.abs(d16.astype(np.float32)) < 2.0 ** -14).all()
+
+    def build(g):
+        return g.mul_mat(g.tensor(qtype, K, N, data=wq), g.tensor(gl.F32, K, ncols, data=x))
+
+    a, names = profiled(hip, lambda: run_on(hip, build))
+    b = run_on(cpu, build)
+    assert any(n.startswith("gemm_") for n in names), names
+    assert np.array_equal(a, b), rel_err(a, b)
+
+
 @pytest.mark.parametrize("qtype,K,N,ncols,tile", [
     (gl.Q4_0, 128, 16384, 512, "4x4x2"),     # 128 x 128 tiles: 512 of them
     (gl.Q4_0, 128, 16424, 529, "4x4x2"),     # partial row and column tiles of the largest shape
