@@ -87,12 +87,13 @@ __device__ __forceinline__ float mask_at(const attn_launch & A, int q, int t) {
 }
 
 // Dynamic LDS of the scores kernel, sized for the launch's n_q new tokens (in floats): the Q rows
-// as the dots read them [n_q * G][HD], the Q source rows [n_q * G][HD], the new K and V source
+// as the dots read them, as doubles [n_q * G][HD + 8] (each quarter of a row padded by two doubles,
+// so that the four quarters the lanes of a quad read start in different banks), the Q source rows [n_q * G][HD], the new K and V source
 // rows [n_q][HD] each, the norm weights of Q and K [HD] each, the chunk's mask rows
 // [n_q][ATT_CHUNK], the (cos, sin) pairs [n_q][HD / 2] and the norm scales [n_q * G + n_q].
 template <int HD, int G>
 __host__ __device__ constexpr int scores_dyn_floats(int n_q) {
-    return 2 * n_q * G * HD + 2 * n_q * HD + 2 * HD + n_q * ATT_CHUNK + n_q * HD + n_q * G + n_q;
+    return 2 * n_q * G * (HD + 8) + n_q * G * HD + 2 * n_q * HD + 2 * HD + n_q * ATT_CHUNK + n_q * HD + n_q * G + n_q;
 }
 
 // Register budget: four waves per SIMD, so that four workgroups of a long row share each CU.
@@ -114,8 +115,10 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
     const int q0 = blockIdx.z * ATT_MAX_Q;            // this workgroup's queries: q0 .. q0 + n_q - 1
     const int n_q = min(ATT_MAX_Q, A.n_q - q0);
     const attn_scratch S = scratch_of(A);
-    float * s_qr = s_dyn;                             // [n_q * G][HD]
-    float * s_q = s_qr + n_q * G * HD;                // [n_q * G][HD]
+    constexpr int DQ = HD / 4;                        // head dims per quarter (per lane in the dots)
+    constexpr int QRS = 4 * (DQ + 2);                 // doubles per staged Q row
+    double * s_qr = (double *) s_dyn;                 // [n_q * G][QRS]
+    float * s_q = (float *) (s_qr + n_q * G * QRS);   // [n_q * G][HD]
     float * s_kx = s_q + n_q * G * HD;                // [n_q][HD]
     float * s_vx = s_kx + n_q * HD;                   // [n_q][HD]
     float * s_qw = s_vx + n_q * HD;                   // [HD]
@@ -127,7 +130,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
 
     // Everything else this workgroup reads goes out before the chunk's K loads, so that waiting for
     // it never waits for them (loads complete in issue order): the Q source rows (before QK-Norm and
-    // RoPE), the new tokens' K and V source rows, norm weights and positions (RoPE), the chunk's F32
+    // RoPE), the new tokens' K and V source rows, norm weights and positions (RoPE), the chunk's
     // mask values. Indices are clamped and the loads unconditional; values past the ends are never
     // used. Without RoPE the K / V / weight / position loads read Q again (valid, unused).
     constexpr int QR = (ATT_MAX_Q * G * HD + ATT_THREADS - 1) / ATT_THREADS;
@@ -163,12 +166,18 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
     const int32_t my_pos = posp[tp / half];
     const bool cs_read = A.rope && A.cs_mode == 2;
     const float2 cs_in = (cs_read ? A.cs_tab : (const float2 *) qb)[cs_read ? tp : 0];
-    const bool mask32 = A.mask && !A.mask_f16;
-    const float * mrow = (const float *) (mask32 ? A.mask : (const void *) qb);
+    // the chunk's mask values (0 without a mask): an F32 and an F16 load per query, both
+    // unconditional (the one of the other type reads Q), so that the dots below load nothing
+    const bool mask32 = A.mask && !A.mask_f16, mask16 = A.mask && A.mask_f16;
+    const float * mrow32 = (const float *) (mask32 ? A.mask : (const void *) qb);
+    const __half * mrow16 = (const __half *) (mask16 ? A.mask : (const void *) qb);
     float mk[ATT_MAX_Q];
 #pragma unroll
     for (int q = 0; q < ATT_MAX_Q; q++) {
-        mk[q] = mrow[mask32 ? (int64_t) (q0 + min(q, n_q - 1)) * (A.mask_nb1 / 4) + t0 + min(lane, nt - 1) : 0];
+        const int64_t mq = q0 + min(q, n_q - 1), mt = t0 + min(lane, nt - 1);
+        const float m32 = mrow32[mask32 ? mq * (A.mask_nb1 / 4) + mt : 0];
+        const __half m16 = mrow16[mask16 ? mq * (A.mask_nb1 / 2) + mt : 0];
+        mk[q] = mask32 ? m32 : mask16 ? __half2float(m16) : 0.0f;
     }
 
     // The chunk's K rows (16-byte pieces; every load unconditional, at a clamped row, since a
@@ -244,7 +253,8 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
     for (int i = t; i < n_q * G * per_row; i += ATT_THREADS) {
         const int pr = i / per_row, k = i % per_row;
         const float * xr = s_q + pr * HD;
-        float * yr = s_qr + pr * HD;
+        double * yr = s_qr + pr * QRS;
+        auto qr_at = [](int d) { return d / DQ * (DQ + 2) + d % DQ; };
         const float sc = qnorm ? s_qs[pr] : 1.0f;
         if (k < np) {
             const int a0 = neox ? k : 2 * k, a1 = neox ? k + np : 2 * k + 1;
@@ -254,13 +264,13 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
                 x1 = (x1 * sc) * s_qw[a1];
             }
             const float2 cs = s_cs[(pr / G) * np + k];
-            yr[a0] = __half2float(__float2half_rn(as_f32(x0 * cs.x - x1 * cs.y)));
-            yr[a1] = __half2float(__float2half_rn(as_f32(x0 * cs.y + x1 * cs.x)));
+            yr[qr_at(a0)] = (double) __half2float(__float2half_rn(as_f32(x0 * cs.x - x1 * cs.y)));
+            yr[qr_at(a1)] = (double) __half2float(__float2half_rn(as_f32(x0 * cs.y + x1 * cs.x)));
         } else {
             const int d = 2 * np + (k - np);
             float v = xr[d];
             if (qnorm) v = (v * sc) * s_qw[d];
-            yr[d] = __half2float(__float2half_rn(as_f32(v)));
+            yr[qr_at(d)] = (double) __half2float(__float2half_rn(as_f32(v)));
         }
     }
     // the new positions of this chunk: K rotated into the cache (by the workgroup of the KV head's
@@ -301,7 +311,6 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
     // fma(k, q, acc) rounds as acc + (double) (k * q) does: the sum accumulates in double (exact for
     // these operands, so splitting it over chains and quarters does not change it), then the four
     // quarters are added by DPP within each quad of lanes. ----
-    constexpr int DQ = HD / 4;                          // dims per lane
     const int pi = lane / 4, dq = lane % 4;
     const int tl = wave * 16 + pi;                      // position in the chunk
     const bool ok = tl < nt;
@@ -324,15 +333,15 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
     }
     for (int pr = 0; pr < n_q * G; pr++) {
         const int q = pr / G, h = h0 + pr % G;
-        const float4 * qv4 = (const float4 *) (s_qr + pr * HD + dq * DQ);
+        const double2 * qv2 = (const double2 *) (s_qr + pr * QRS + dq * (DQ + 2));
         double a[4] = { 0.0, 0.0, 0.0, 0.0 };
 #pragma unroll
         for (int j = 0; j < DQ / 4; j++) {
-            const float4 q4 = qv4[j];
-            a[0] = fma(kd[4 * j], (double) q4.x, a[0]);
-            a[1] = fma(kd[4 * j + 1], (double) q4.y, a[1]);
-            a[2] = fma(kd[4 * j + 2], (double) q4.z, a[2]);
-            a[3] = fma(kd[4 * j + 3], (double) q4.w, a[3]);
+            const double2 qa = qv2[2 * j], qb2 = qv2[2 * j + 1];
+            a[0] = fma(kd[4 * j], qa.x, a[0]);
+            a[1] = fma(kd[4 * j + 1], qa.y, a[1]);
+            a[2] = fma(kd[4 * j + 2], qb2.x, a[2]);
+            a[3] = fma(kd[4 * j + 3], qb2.y, a[3]);
         }
         double dot = (a[0] + a[1]) + (a[2] + a[3]);
         dot += dpp_d<0xB1>(dot);
@@ -340,7 +349,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
         // softmax input as the graph forms it: (float) kq * scale + mask
         float sv = -INFINITY;
         if (ok) {
-            const float mv = mask32 ? s_mk[q * ATT_CHUNK + tl] : mask_at(A, q0 + q, t0 + tl);
+            const float mv = s_mk[q * ATT_CHUNK + tl];
             sv = mv == -INFINITY ? -INFINITY : (float) dot * A.scale + mv;
             if (dq == 0) S.scores[((int64_t) (q0 + q) * A.n_head + h) * A.n_kv + t0 + tl] = sv;
         }
