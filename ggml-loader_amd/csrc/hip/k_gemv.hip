@@ -283,8 +283,13 @@ __device__ __forceinline__ void load_chunk(float (&v)[C], const float * p) {
 // Loads complete in issue order, so the prologue's loads go out before the weight stream: the
 // prologue then computes while the weights are in flight instead of after they arrive. The first
 // 32 values per thread (one Q8_0 block, or two Q8_K groups in the quantize-only mode) are loaded by
-// prologue_load into registers; further chunks are loaded when they are quantized.
+// prologue_load into registers, and so is one more chunk in the quantize-only mode (in the
+// registers that hold the norm weights in the rms mode); further chunks are loaded when they are
+// quantized, after the weights (each such load waits for every weight load).
 constexpr int PRO_REGS = 32;
+// threads of every gemv_kernel and act_quant_kernel workgroup: a constant, so that the prologue's
+// addresses need no load of the launch's workgroup size ahead of the weight loads
+constexpr int GEMV_NT = 256;
 
 template <int TYPE, bool PRO>
 __device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, float (&xv)[PRO_REGS], float (&wv)[PRO_REGS]) {
@@ -303,7 +308,7 @@ __device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, fl
         const int8_t * xq = L.xq + (int64_t) col * K;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const int i = min(t + k * (int) blockDim.x, K / 16 - 1);
+            const int i = min(t + k * GEMV_NT, K / 16 - 1);
             const int4 v = *(const int4 *) (xq + i * 16);
             xv[4 * k] = __int_as_float(v.x); xv[4 * k + 1] = __int_as_float(v.y);
             xv[4 * k + 2] = __int_as_float(v.z); xv[4 * k + 3] = __int_as_float(v.w);
@@ -312,7 +317,7 @@ __device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, fl
             const int nb = K / 32;
 #pragma unroll
             for (int k = 0; k < 2; k++) {
-                const int i = min(t + k * (int) blockDim.x, nb - 1);
+                const int i = min(t + k * GEMV_NT, nb - 1);
                 wv[k] = L.xd[(int64_t) col * nb + i];
                 wv[2 + k] = __int_as_float(L.xs[(int64_t) col * nb + i]);
             }
@@ -321,18 +326,23 @@ __device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, fl
             wv[0] = L.xd[(int64_t) col * nsb + min(t, nsb - 1)];
             const int * bs = (const int *) (L.xbs + (int64_t) col * (K / 16));
 #pragma unroll
-            for (int k = 0; k < 2; k++) wv[1 + k] = __int_as_float(bs[min(t + k * (int) blockDim.x, K / 32 - 1)]);
+            for (int k = 0; k < 2; k++) wv[1 + k] = __int_as_float(bs[min(t + k * GEMV_NT, K / 32 - 1)]);
         }
         return;
     } else {
         const int nchunk = L.K / C;
         const float * xcol = L.norm.x + (int64_t) col * L.norm.x_stride;
         load_chunk(*reinterpret_cast<float (*)[C]>(&xv[0]), xcol + (int64_t) min(t, nchunk - 1) * C);
-        if (L.norm.rms && L.norm.w) load_chunk(*reinterpret_cast<float (*)[C]>(&wv[0]), L.norm.w + (int64_t) min(t, nchunk - 1) * C);
+        // wv: the norm weights (rms mode) or, in the quantize-only mode, the chunk after the ones
+        // xv holds (one unconditional load either way; unused in the rms mode without weights)
+        const bool wload = L.norm.rms && L.norm.w;
+        load_chunk(*reinterpret_cast<float (*)[C]>(&wv[0]),
+                   wload ? L.norm.w + (int64_t) min(t, nchunk - 1) * C
+                         : xcol + (int64_t) min(t + (PRO_REGS / C) * GEMV_NT, nchunk - 1) * C);
         if (C * 2 == PRO_REGS) {
             // the quantize-only mode's second chunk; loaded (and left unused) in the rms mode too, so
             // that no branch joins before the weight loads (the join would wait for these loads)
-            load_chunk(*reinterpret_cast<float (*)[C]>(&xv[PRO_REGS - C]), xcol + (int64_t) min(t + (int) blockDim.x, nchunk - 1) * C);
+            load_chunk(*reinterpret_cast<float (*)[C]>(&xv[PRO_REGS - C]), xcol + (int64_t) min(t + GEMV_NT, nchunk - 1) * C);
         }
     }
 }
@@ -347,13 +357,15 @@ __device__ __forceinline__ void prologue_finish(const gemv_launch & L, int col, 
     float (&x0)[C] = *reinterpret_cast<float (*)[C]>(&xv[0]);
     if (!L.norm.rms) {
         quant_chunk<TYPE, C>(x0, t, t < nchunk, s);
-        int c0 = blockDim.x;
+        int c0 = GEMV_NT;
         if (C * 2 == PRO_REGS) {
             quant_chunk<TYPE, C>(*reinterpret_cast<float (*)[C]>(&xv[PRO_REGS - C]), c0 + t, c0 + t < nchunk, s);
-            c0 += blockDim.x;
+            c0 += GEMV_NT;
         }
+        quant_chunk<TYPE, C>(*reinterpret_cast<const float (*)[C]>(&wv[0]), c0 + t, c0 + t < nchunk, s);
+        c0 += GEMV_NT;
         const float * xcol = L.norm.x + (int64_t) col * L.norm.x_stride;
-        for (; c0 < nchunk; c0 += blockDim.x) {
+        for (; c0 < nchunk; c0 += GEMV_NT) {
             const int c = c0 + t;
             const bool has = c < nchunk;
             float v[C];
@@ -374,7 +386,7 @@ __device__ __forceinline__ void prologue_finish(const gemv_launch & L, int col, 
     if (lane == 0) s_red[wave] = ss;
     __syncthreads();
     double total = 0.0;
-    for (int w = 0; w < (int) (blockDim.x / WAVE); w++) total += s_red[w];
+    for (int w = 0; w < GEMV_NT / WAVE; w++) total += s_red[w];
     const float mean = (float) (total / (double) K);
     const float scale = 1.0f / sqrtf(mean + L.norm.eps);
 #pragma unroll
@@ -393,12 +405,12 @@ __device__ __forceinline__ void stage_x(const gemv_launch & L, int col, const ge
     if constexpr (PRO) {
         prologue_finish<TYPE>(L, col, xv, wv, s, s_red);
     } else if constexpr (TYPE == GGML_TYPE_Q4_K) {
-        // from the registers prologue_load filled; a row longer than they cover (K > 64 * blockDim)
+        // from the registers prologue_load filled; a row longer than they cover (K > 64 * GEMV_NT)
         // copies the rest here
         // The stores are unconditional: a thread past the end stores the last element it loaded
         // (the index was clamped) over that same element. A guarded store would let the compiler
         // sink its load behind the weight loads, where waiting for it waits for all of them.
-        const int nsb = K / 256, nt = blockDim.x;
+        const int nsb = K / 256, nt = GEMV_NT;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const int i = min((int) threadIdx.x + k * nt, K / 16 - 1);
@@ -414,18 +426,18 @@ __device__ __forceinline__ void stage_x(const gemv_launch & L, int col, const ge
         for (int k = 0; k < 2; k++) sbs[min((int) threadIdx.x + k * nt, K / 32 - 1)] = __float_as_int(wv[1 + k]);
         for (int i = threadIdx.x + 2 * nt; i < K / 32; i += nt) sbs[i] = gbs[i];
     } else {
-        // from the registers prologue_load filled (K <= 64 * blockDim, nb <= 2 * blockDim), with
+        // from the registers prologue_load filled (K <= 64 * GEMV_NT, nb <= 2 * GEMV_NT), with
         // unconditional stores as in the Q8_K copy above
         const int nb = K / 32;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const int i = min((int) (threadIdx.x + k * blockDim.x), K / 16 - 1);
+            const int i = min((int) (threadIdx.x + k * GEMV_NT), K / 16 - 1);
             *(int4 *) (s.xq + i * 16) = make_int4(__float_as_int(xv[4 * k]), __float_as_int(xv[4 * k + 1]),
                                                   __float_as_int(xv[4 * k + 2]), __float_as_int(xv[4 * k + 3]));
         }
 #pragma unroll
         for (int k = 0; k < 2; k++) {
-            const int i = min((int) (threadIdx.x + k * blockDim.x), nb - 1);
+            const int i = min((int) (threadIdx.x + k * GEMV_NT), nb - 1);
             s.xd[i] = wv[k];
             s.xs[i] = __float_as_int(wv[2 + k]);
         }
@@ -436,9 +448,9 @@ __device__ __forceinline__ void stage_x(const gemv_launch & L, int col, const ge
 // The prologue run once per column into global memory, for consumers too wide to redo it in every
 // workgroup (the LM head): same arithmetic, so the GEMV that copies the result computes the same floats.
 template <int TYPE>
-__global__ __launch_bounds__(256) void act_quant_kernel(const gemv_launch L, q8_act q8, q8k_act q8k) {
+__global__ __launch_bounds__(GEMV_NT) void act_quant_kernel(const gemv_launch L, q8_act q8, q8k_act q8k) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ double s_red[256 / WAVE];
+    __shared__ double s_red[GEMV_NT / WAVE];
     const int col = blockIdx.x;
     const int K = L.K;
     const gemv_lds s = lds_layout<TYPE>(smem, K);
@@ -447,12 +459,12 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const gemv_launch L, q8_
     prologue_finish<TYPE>(L, col, xv, wv, s, s_red);
     __syncthreads();
     int8_t * qs = (TYPE == GGML_TYPE_Q4_K ? q8k.qs : q8.qs) + (int64_t) col * K;
-    for (int i = threadIdx.x * 16; i < K; i += blockDim.x * 16) *(int4 *) (qs + i) = *(const int4 *) (s.xq + i);
+    for (int i = threadIdx.x * 16; i < K; i += GEMV_NT * 16) *(int4 *) (qs + i) = *(const int4 *) (s.xq + i);
     if (TYPE == GGML_TYPE_Q4_K) {
-        for (int i = threadIdx.x; i < K / 256; i += blockDim.x) q8k.d[(int64_t) col * (K / 256) + i] = s.xd[i];
-        for (int i = threadIdx.x; i < K / 16; i += blockDim.x) q8k.bsums[(int64_t) col * (K / 16) + i] = s.xbs[i];
+        for (int i = threadIdx.x; i < K / 256; i += GEMV_NT) q8k.d[(int64_t) col * (K / 256) + i] = s.xd[i];
+        for (int i = threadIdx.x; i < K / 16; i += GEMV_NT) q8k.bsums[(int64_t) col * (K / 16) + i] = s.xbs[i];
     } else {
-        for (int i = threadIdx.x; i < K / 32; i += blockDim.x) {
+        for (int i = threadIdx.x; i < K / 32; i += GEMV_NT) {
             q8.d[(int64_t) col * (K / 32) + i] = s.xd[i];
             q8.s[(int64_t) col * (K / 32) + i] = s.xs[i];
         }
@@ -463,10 +475,10 @@ void launch_act_quant(const gemv_launch & L, const q8_act & q8, const q8k_act & 
     if (!L.norm.x || L.K > act_quant_max_k(L.type, L.norm.rms != 0)) HIP_ABORT("act_quant: K=%d unsupported", L.K);
     switch (L.type) {
         case GGML_TYPE_Q4_0: case GGML_TYPE_Q8_0:
-            launch(act_quant_kernel<GGML_TYPE_Q4_0>, dim3(L.ncols), dim3(256), gemv_lds_bytes<GGML_TYPE_Q4_0>(L.K, 0, 0), st, L, q8, q8k);
+            launch(act_quant_kernel<GGML_TYPE_Q4_0>, dim3(L.ncols), dim3(GEMV_NT), gemv_lds_bytes<GGML_TYPE_Q4_0>(L.K, 0, 0), st, L, q8, q8k);
             break;
         case GGML_TYPE_Q4_K:
-            launch(act_quant_kernel<GGML_TYPE_Q4_K>, dim3(L.ncols), dim3(256), gemv_lds_bytes<GGML_TYPE_Q4_K>(L.K, 0, 0), st, L, q8, q8k);
+            launch(act_quant_kernel<GGML_TYPE_Q4_K>, dim3(L.ncols), dim3(GEMV_NT), gemv_lds_bytes<GGML_TYPE_Q4_K>(L.K, 0, 0), st, L, q8, q8k);
             break;
         default:
             HIP_ABORT("act_quant: unsupported weight type %d", L.type);
@@ -707,6 +719,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
 template <int TYPE, int LPR, bool SWIGLU, int ITS>
 static void launch_gemv_its(gemv_kargs & ka, int waves, hipStream_t st) {
     constexpr int RPW = WAVE / LPR;
+    if (waves * WAVE != GEMV_NT) HIP_ABORT("gemv: %d-thread workgroups (the kernel assumes %d)", waves * WAVE, GEMV_NT);
     ka.rows_per_block = waves * RPW;
     if (!SWIGLU) {
         // every matrix starts on a workgroup boundary
