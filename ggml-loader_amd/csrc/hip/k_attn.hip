@@ -635,7 +635,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     // multiplied into up to four rows at a time; a product of two F16 values is exact in double, so
     // fma(p, v, acc) rounds as acc + p*v does (the sums are exact for these operands)
     const int d2 = min(lane, HD2 - 1);
-    // rows r0 .. r0 + 3 (clamped; rows past n_rows are computed and dropped)
+    // rows r0 .. r0 + NR - 1 (clamped; rows past n_rows are computed and dropped): NR = 4, or the
+    // G rows of a launch that forms its own statistics (one query), all of which are live
+    constexpr int NR = FS ? G : 4;
+    static_assert(NR <= 4, "PV rows per pass");
     auto dot_rows = [&](int r0, double (&acc)[4][2]) {
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[r][0] = acc[r][1] = 0.0;
@@ -645,7 +648,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
             const float2 vf = __half22float2(*(const __half2 *) &s_v[tt * HD2 + d2]);
             const double v0 = (double) vf.x, v1 = (double) vf.y;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
+            for (int r = 0; r < NR; r++) {
                 const double p = s_p[min(r0 + r, PV_MAX_ROWS - 1)][tt];
                 acc[r][0] = fma(p, v0, acc[r][0]);
                 acc[r][1] = fma(p, v1, acc[r][1]);
