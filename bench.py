@@ -75,6 +75,20 @@ def describe(cfg, n_past, batch):
             f"vocab {cfg['n_vocab']}, {WNAME[cfg['wtype']].upper()})")
 
 
+def timed_reps(run, n_steps, reps):
+    """The timed steps split into reps of near-equal size, each timed on its own by run(k) -> seconds
+    (cmd_bench.cpp:30-38, 135-147 reports the mean and sample standard deviation over its reps).
+    Returns the total seconds of the n_steps steps and the per-rep statistics."""
+    import statistics
+    reps = max(1, min(reps, n_steps))
+    sizes = [n_steps // reps + (1 if i < n_steps % reps else 0) for i in range(reps)]
+    times = [run(k) for k in sizes]
+    rates = [k / t for k, t in zip(sizes, times)]
+    stats = {"n": reps, "steps_per_rep": sizes, "steps_per_s_mean": round(statistics.fmean(rates), 3),
+             "steps_per_s_stddev": round(statistics.stdev(rates), 3) if reps > 1 else 0.0}
+    return sum(times), stats
+
+
 def oracle_helpers():
     """tests/gl.py, whose oracle() registers the oracle's CPU backend (the cpu_baseline leg only)."""
     spec = importlib.util.spec_from_file_location("gl_test_helpers", os.path.join(ROOT, "tests", "gl.py"))
@@ -134,13 +148,16 @@ def cpu_baseline(gl, model_path, n_pos, tokens, seconds, threads):
 
             t1 = steps(1)  # warmup, also sizes the sample
             n = max(1, min(64, int(seconds / len(threads) / max(t1, 1e-6))))
-            t = steps(n)
-        runs[nt] = (n * batch / t, n, t)
-        log(f"[bench] cpu baseline {nt} threads: {n} steps in {t:.2f}s -> {n * batch / t:.2f} tok/s")
+            t, reps = timed_reps(steps, n, 3)
+        runs[nt] = (n * batch / t, n, t, reps)
+        log(f"[bench] cpu baseline {nt} threads: {n} steps in {t:.2f}s -> {n * batch / t:.2f} tok/s "
+            f"({reps['steps_per_s_mean'] * batch:.2f} +- {reps['steps_per_s_stddev'] * batch:.2f} over {reps['n']} reps)")
     main_nt = threads[0]
-    v, n, t = runs[main_nt]
+    v, n, t, reps = runs[main_nt]
     what = "decode steps" if batch == 1 else f"{batch}-token steps"
     return {"value": round(v, 3), "unit": "tok/s", "cores": main_nt, "kind": "port",
+            "reps": {"n": reps["n"], "tok_s_mean": round(reps["steps_per_s_mean"] * batch, 3),
+                     "tok_s_stddev": round(reps["steps_per_s_stddev"] * batch, 3)},
             "host_physical_cores": physical_cores(), "host_logical_cpus": os.cpu_count(),
             "sample": f"{n} {what} at position {n_pos} ({t:.1f}s) of the same synthetic model on the oracle/ "
                       f"CPU restatement of ggml-cpu (restated ggml-cpu semantics; upstream ggml unavailable offline), "
@@ -280,10 +297,13 @@ def prefill_bench(gl, args):
     with gl.Session(model_path, "hip", n_ctx=n) as s:
         for _ in range(args.warmup):
             s.forward(0, tokens)
-        t = time.perf_counter()
-        for _ in range(args.steps):
-            s.forward(0, tokens)
-        secs = time.perf_counter() - t
+        def run(k):
+            t = time.perf_counter()
+            for _ in range(k):
+                s.forward(0, tokens)
+            return time.perf_counter() - t
+
+        secs, reps = timed_reps(run, args.steps, args.reps)
         hipl.ggml_backend_hip_set_profile_filter(s.backend, b"")
         hipl.ggml_backend_hip_reset_profile(s.backend)
         hipl.ggml_backend_hip_set_profiling(s.backend, True)
@@ -301,6 +321,8 @@ def prefill_bench(gl, args):
     print(json.dumps({
         "metric": f"prefill tokens/s ({n}-token prompt)", "value": round(n / (secs / args.steps), 1), "unit": "tok/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 3),
+        "reps": {"n": reps["n"], "steps_per_rep": reps["steps_per_rep"],
+                 "tok_s_mean": round(reps["steps_per_s_mean"] * n, 1), "tok_s_stddev": round(reps["steps_per_s_stddev"] * n, 1)},
         "higher_is_better": True, "data": f"synthetic (seeded random-init weights quantized to {wname.upper()})",
         "config": {"workload": f"{args.config}: prefill of {n} tokens at position 0", "n_tokens": n},
         "kernel_ms_per_step": {k: v["ms"] for k, v in breakdown.items()},
@@ -418,6 +440,7 @@ def main():
     # 0.2 s region (GPU clock ramp, host scheduling), and 50 warmup steps bring the clocks up first
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--reps", type=int, default=5, help="the timed steps in this many separately timed reps (mean +- sd)")
     ap.add_argument("--config", default="llama3b")
     ap.add_argument("--n-past", type=int, default=None, help="KV positions before the step (default: per config)")
     ap.add_argument("--batch", type=int, default=1, help="new tokens per decode step")
@@ -501,9 +524,11 @@ def decode_bench(gl, args):
         # timed region: K steps with no events in them. Once a launch carries dispatch-stamped HIP
         # events, the runtime timestamps every later dispatch of the process too (measured: 1.97 ->
         # 2.40 ms per Llama-3B step), so no event is used before this region ends.
-        secs = steps(args.steps)
+        secs, reps = timed_reps(steps, args.steps, args.reps)
         value = args.steps * batch / secs
-        log(f"[bench] {args.steps} steps in {secs:.4f}s -> {value:.1f} tok/s ({1000 * secs / args.steps:.3f} ms/step)")
+        tok_mean, tok_sd = reps["steps_per_s_mean"] * batch, reps["steps_per_s_stddev"] * batch
+        log(f"[bench] {args.steps} steps in {secs:.4f}s -> {value:.1f} tok/s ({1000 * secs / args.steps:.3f} ms/step); "
+            f"over {reps['n']} reps {tok_mean:.1f} +- {tok_sd:.1f} tok/s")
 
         # the dominant kernel's launch durations: the same K steps again, where in every 10th step
         # its launches (and only those) carry HIP events stamped by their own dispatches on the
@@ -581,9 +606,9 @@ def decode_bench(gl, args):
             "us_per_layer": round(ms_a / n_a * 1e3, 2), "bytes_per_layer": round(by_a / n_a),
             "timing": f"HIP events around each layer's attention launches in {args.breakdown_steps} untimed steps",
         }
-    if moe and batch > 1:
-        roofline["bytes_note"] = ("mul_mat_id launches count the selected experts' bytes once per (token, slot) "
-                                  "column, so repeated experts are counted again")
+    if moe:
+        roofline["bytes_note"] = ("mul_mat_id launches count each distinct selected expert's bytes once, from the "
+                                  "step's routing ids (read back in the profiled steps only)")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -605,6 +630,8 @@ def decode_bench(gl, args):
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(1000 * secs / args.steps, 4),
+        "reps": {"n": reps["n"], "steps_per_rep": reps["steps_per_rep"], "tok_s_mean": round(tok_mean, 2),
+                 "tok_s_stddev": round(tok_sd, 2)},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -85,6 +85,7 @@ class gl_synth_params(C.Structure):
         ("wtype", C.c_int32), ("embd_type", C.c_int32), ("output_type", C.c_int32), ("tied_output", C.c_int32),
         ("w_std", C.c_float), ("norm_std", C.c_float),
         ("seed", C.c_uint64), ("n_threads", C.c_int32), ("share_experts", C.c_int32),
+        ("rope_scaling_orig_ctx", C.c_int32), ("rope_attn_factor", C.c_float),
     ]
 
 
@@ -320,7 +321,8 @@ def synth_model(path: str, *, arch: str, n_embd: int, n_layer: int, n_head: int,
                 n_ff: int, n_vocab: int, n_ctx_train: int = 4096, rope_theta: float = 10000.0, rms_eps: float = 1e-5,
                 wtype: int = Q4_0, embd_type: int | None = None, output_type: int | None = None, tied: bool = False,
                 w_std: float = 0.02, norm_std: float = 0.01, seed: int = 1, n_threads: int = 0, n_expert: int = 0,
-                n_expert_used: int = 0, n_ff_exp: int = 0, share_experts: bool = False) -> None:
+                n_expert_used: int = 0, n_ff_exp: int = 0, share_experts: bool = False,
+                rope_scaling_orig_ctx: int = 0, rope_attn_factor: float = 1.0) -> None:
     """Write a seeded synthetic GGUF model (weights ~ N(0, w_std), quantized by the ggml reference quantizers)."""
     p = gl_synth_params()
     p.arch = arch.encode()
@@ -334,6 +336,7 @@ def synth_model(path: str, *, arch: str, n_embd: int, n_layer: int, n_head: int,
     p.tied_output = 1 if tied else 0
     p.w_std, p.norm_std, p.seed, p.n_threads = w_std, norm_std, seed, n_threads
     p.share_experts = 1 if share_experts else 0
+    p.rope_scaling_orig_ctx, p.rope_attn_factor = rope_scaling_orig_ctx, rope_attn_factor
     err = C.create_string_buffer(512)
     if libs()["loader"].gl_synth_model(path.encode(), C.byref(p), err, 512) != 0:
         raise RuntimeError(err.value.decode())

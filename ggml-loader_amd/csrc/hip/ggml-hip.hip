@@ -1183,6 +1183,21 @@ private:
         return nc;
     }
 
+    // distinct values in [0, n) of an I32 ids tensor [slots, tokens] (copied back synchronously)
+    int64_t distinct_ids(const ggml_tensor * ids, int64_t n) {
+        const int64_t ns = ids->ne[0], nt = ids->ne[1];
+        std::vector<int32_t> h((size_t) (ns * nt));
+        HIP_CHECK(hipMemcpy2DAsync(h.data(), (size_t) ns * 4, ids->data, ids->nb[1], (size_t) ns * 4, (size_t) nt,
+                                   hipMemcpyDeviceToHost, st_));
+        HIP_CHECK(hipStreamSynchronize(st_));
+        std::vector<char> seen((size_t) n, 0);
+        int64_t k = 0;
+        for (int32_t v : h) {
+            if (v >= 0 && v < n && !seen[(size_t) v]) { seen[(size_t) v] = 1; k++; }
+        }
+        return k;
+    }
+
     // The columns of a mul_mat_id grouped by expert (once per ids tensor and graph compute)
     std::unordered_map<const ggml_tensor *, expert_groups> groups_;
     const expert_groups & expert_groups_of(const ggml_tensor * ids, int n_experts) {
@@ -1309,6 +1324,10 @@ private:
             xa = ensure_act(x, kind);
         }
 
+        // profiled steps only: the ids back on the host, to count the distinct experts a
+        // mul_mat_id reads (a synchronization, never inside a timed region)
+        int64_t n_unique_experts = -1;
+        if (by_id && c_.timing) n_unique_experts = distinct_ids(ids, n->src[0]->ne[2]);
         auto fill_mat = [&](gemv_mat & gm, int j, double & bytes, bool epilogue) {
             ggml_tensor * mm = g_->nodes[j];
             const ggml_tensor * w = mm->src[0];
@@ -1326,8 +1345,11 @@ private:
             gm.add = nullptr;
             gm.add_stride = 0;
             // the weights one launch must read: every row, or the rows of the selected experts
-            const double wbytes = by_id ? std::min((double) ggml_nbytes(w), (double) ncols * (double) w->nb[2])
-                                        : (double) ggml_nbytes(w);
+            // (each distinct one once: counted from the ids in profiled steps, else bounded by the
+            // columns)
+            const double wbytes = !by_id ? (double) ggml_nbytes(w)
+                                  : n_unique_experts >= 0 ? (double) n_unique_experts * (double) w->nb[2]
+                                  : std::min((double) ggml_nbytes(w), (double) ncols * (double) w->nb[2]);
             bytes += wbytes + (double) (w->ne[1] * ncols * 4);
             const ggml_tensor * written = mm;
             // residual add epilogue
@@ -1796,6 +1818,7 @@ private:
         A.n_kv = n_kv; A.n_q = n_q; A.n_head = n_head; A.n_head_kv = n_head_kv; A.hd = hd;
         A.scale = scale;
         A.skip_masked = 1;
+        A.p_f32 = 1;
         const double bytes = (double) n_kv * n_head_kv * hd * 2 * 2 + (double) n_head * hd * n_q * 8;
         if (n_q > 4 && prefill_attn_ok(n_kv, hd, k->data, k->nb[1], k->nb[2], v->data, v->nb[1], v->nb[2])) {
             prof_scope ps(this, "attn_prefill", bytes);

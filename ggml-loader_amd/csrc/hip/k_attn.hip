@@ -5,7 +5,8 @@
 //   * QK dot: Q rounded to F16 (ggml converts the F32 operand of an F16 mul_mat), products of the
 //     two F16 values (exact in f32) summed in double, the sum rounded to float once;
 //   * softmax over the whole row: w = kq*scale + mask, M = max w, e = exp(w - M), S = sum e in
-//     double, p = e * (float)(1/S), then p rounded to F16 (the operand conversion of the V mul_mat);
+//     double, p = e * (float)(1/S), then p rounded to F16 (the operand conversion of the V mul_mat;
+//     flash_attn_ext, which has no such operand, keeps p a float: attn_launch::p_f32);
 //   * PV: products of F16 p and F16 V (exact in f32) summed in double, rounded to float once.
 // The double sums are exact for these operands in practice, so the result does not depend on the
 // summation order and equals the CPU reference's float. V is read in place (never transposed).
@@ -48,6 +49,32 @@ constexpr int STATS_SEG = ATT_THREADS * STATS_PER_THREAD;    // positions per st
 
 __host__ __device__ inline int attn_chunks(int n_kv) { return (n_kv + ATT_CHUNK - 1) / ATT_CHUNK; }
 __host__ __device__ inline int attn_segs(int n_kv) { return (n_kv + STATS_SEG - 1) / STATS_SEG; }
+
+// Workgroup numbering of the scores and PV launches (1-D grids). A launch's workgroups go to the
+// part's 8 XCDs in turn (workgroup i to XCD i % 8), and each XCD has an L2 of its own. The
+// workgroups that read one position chunk of one KV head -- the head groups of that KV head, and
+// the query groups of a multi-token step: `members` of them -- get ids congruent mod 8, so they run
+// on one XCD and the chunk comes from HBM once. Sets (KV head, chunk) are numbered chunk fastest;
+// ids past the last set (at most 7 sets' worth) exit at once.
+constexpr int N_XCD = 8;
+struct attn_wg {
+    int chunk, hg, qg;   // position chunk, head group (heads hg * G ..), query group
+    bool live;
+};
+__host__ __device__ inline int attn_grid(int n_chunks, int n_head_kv, int members) {
+    return (n_chunks * n_head_kv + N_XCD - 1) / N_XCD * N_XCD * members;
+}
+__device__ __forceinline__ attn_wg attn_wg_of(int n_chunks, int n_head_kv, int hg_per_kv, int n_qg) {
+    const int L = blockIdx.x, xcd = L % N_XCD, r = L / N_XCD;
+    const int members = hg_per_kv * n_qg;
+    const int m = r % members, set = r / members * N_XCD + xcd;
+    attn_wg w;
+    w.live = set < n_chunks * n_head_kv;
+    w.chunk = set % n_chunks;
+    w.hg = set / n_chunks * hg_per_kv + m % hg_per_kv;
+    w.qg = m / hg_per_kv;
+    return w;
+}
 
 // Scratch (all per row = (query, head)): scores f32 [n_kv], the maximum of each 64-position chunk
 // f32 [chunks], the row maximum f32, the sum of exp(s - max) over each statistics segment f64
@@ -105,14 +132,17 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
     __shared__ __align__(16) uint32_t s_knew[ATT_MAX_Q * HD2];   // the new tokens' rotated K rows (F16)
     __shared__ float s_cm[ATT_WAVES][ATT_MAX_Q * 8];
     extern __shared__ __align__(16) float s_dyn[];
-    // blockIdx.y: a group of G consecutive heads (all heads of KV head kvh, or a part of them when
-    // the launch splits a large GQA group over several workgroups); h0 its first head
-    const int split = blockIdx.x, h0 = blockIdx.y * G, kvh = h0 / (A.n_head / A.n_head_kv);
+    // W.hg: a group of G consecutive heads (all heads of KV head kvh, or a part of them when the
+    // launch splits a large GQA group over several workgroups); h0 its first head
+    const attn_wg W = attn_wg_of(attn_chunks(A.n_kv), A.n_head_kv, A.n_head / A.n_head_kv / G,
+                                 (A.n_q + ATT_MAX_Q - 1) / ATT_MAX_Q);
+    if (!W.live) return;
+    const int split = W.chunk, h0 = W.hg * G, kvh = h0 / (A.n_head / A.n_head_kv);
     const bool kv_writer = h0 % (A.n_head / A.n_head_kv) == 0;   // the first group of a KV head appends K and V
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int t0 = split * ATT_CHUNK;
     const int nt = min(ATT_CHUNK, A.n_kv - t0);
-    const int q0 = blockIdx.z * ATT_MAX_Q;            // this workgroup's queries: q0 .. q0 + n_q - 1
+    const int q0 = W.qg * ATT_MAX_Q;                  // this workgroup's queries: q0 .. q0 + n_q - 1
     const int n_q = min(ATT_MAX_Q, A.n_q - q0);
     const attn_scratch S = scratch_of(A);
     constexpr int DQ = HD / 4;                        // head dims per quarter (per lane in the dots)
@@ -218,7 +248,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
             sn = cs_in.y;
         } else if (A.rope) {
             rope_pair_cs(A.rq.p, A.rq.ff, my_pos, tp % half, c, sn);
-            if (A.cs_mode == 1 && blockIdx.x == 0 && blockIdx.y == 0 && t < n_q * half) A.cs_tab[tp] = make_float2(c, sn);
+            if (A.cs_mode == 1 && split == 0 && W.hg == 0 && t < n_q * half) A.cs_tab[tp] = make_float2(c, sn);
         }
         s_cs[tp] = make_float2(c, sn);
     }
@@ -492,11 +522,14 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     __shared__ float s_M[PV_MAX_ROWS], s_inv[PV_MAX_ROWS];
     uint32_t * s_v = (uint32_t *) s_buf;                  // [PV_CHUNK][HD2]
     double * s_part = (double *) s_buf;                   // [ATT_WAVES][PV_MAX_ROWS][HD], after the dots
-    const int split = blockIdx.x, h0 = blockIdx.y * G, kvh = h0 / (A.n_head / A.n_head_kv);   // as in the scores kernel
+    const attn_wg W = attn_wg_of((A.n_kv + PV_CHUNK - 1) / PV_CHUNK, A.n_head_kv, A.n_head / A.n_head_kv / G,
+                                 (A.n_q + pvq - 1) / pvq);
+    if (!W.live) return;
+    const int split = W.chunk, h0 = W.hg * G, kvh = h0 / (A.n_head / A.n_head_kv);   // as in the scores kernel
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int t0 = split * PV_CHUNK;
     const int nt = min(PV_CHUNK, A.n_kv - t0);
-    const int q0 = blockIdx.z * pvq;                  // this workgroup's queries: q0 .. q0 + pvq - 1
+    const int q0 = W.qg * pvq;                        // this workgroup's queries: q0 .. q0 + pvq - 1
     const int n_rows = min(pvq, A.n_q - q0) * G;      // <= PV_MAX_ROWS (pvq = PV_MAX_ROWS / G or 1)
     const attn_scratch S = scratch_of(A);
     const int nseg = attn_segs(A.n_kv);
@@ -606,7 +639,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
         s_inv[t] = ssum > 0.0 ? (float) (1.0 / ssum) : 0.0f;
     }
     __syncthreads();
-    // p = F16(exp(s - M) * (1/S)) for the chunk's positions (0 past the end), kept as doubles
+    // p = F16(exp(s - M) * (1/S)) for the chunk's positions (0 past the end; with p_f32 not rounded
+    // to F16), kept as doubles
 #pragma unroll
     for (int k = 0; k < PV_SC; k++) {
         const int i = t + k * ATT_THREADS;
@@ -616,7 +650,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
             if (tt < nt) {
                 const float M = s_M[pr];
                 const float e = M == -INFINITY ? 0.0f : exp_cr(sc[k] - M);
-                p = __half2float(__float2half_rn(as_f32(e * s_inv[pr])));
+                p = as_f32(e * s_inv[pr]);
+                if (!A.p_f32) p = __half2float(__float2half_rn(p));
             }
             s_p[pr][tt] = (double) p;
         }
@@ -693,13 +728,15 @@ static void launch_attn_t(const attn_launch & A, hipStream_t st) {
         HIP_CHECK(hipFuncSetAttribute((const void *) attn_scores_kernel<HD, G>, hipFuncAttributeMaxDynamicSharedMemorySize, 98304));
         big_lds = true;
     }
-    launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head / G, qz), dim3(ATT_THREADS), dyn, st, A);
+    const int hg_per_kv = A.n_head / A.n_head_kv / G;
+    launch((attn_scores_kernel<HD, G>), dim3(attn_grid(splits, A.n_head_kv, hg_per_kv * qz)), dim3(ATT_THREADS), dyn, st, A);
     static_assert(G <= PV_MAX_ROWS, "PV rows");
     const int pvq = std::max(1, std::min(ATT_MAX_Q, PV_MAX_ROWS / G));   // queries per PV workgroup
-    const dim3 pv_grid(pv_splits, A.n_head / G, (A.n_q + pvq - 1) / pvq);
+    const dim3 pv_grid(attn_grid(pv_splits, A.n_head_kv, hg_per_kv * ((A.n_q + pvq - 1) / pvq)));
     if (A.n_q == 1 && A.n_kv <= PV_FS_MAX_KV) {
         // one head per workgroup: each workgroup evaluates the exp of every score of its rows
-        launch((attn_pv_kernel<HD, 1, PV_FS_SPT>), dim3(pv_splits, A.n_head, 1), dim3(ATT_THREADS), 0, st, A, 1);
+        launch((attn_pv_kernel<HD, 1, PV_FS_SPT>), dim3(attn_grid(pv_splits, A.n_head_kv, A.n_head / A.n_head_kv)),
+               dim3(ATT_THREADS), 0, st, A, 1);
     } else {
         launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
         launch((attn_pv_kernel<HD, G, 0>), pv_grid, dim3(ATT_THREADS), 0, st, A, pvq);
@@ -751,8 +788,9 @@ void launch_attn_decode(const attn_launch & A, hipStream_t st) {
 //           head dimension (the F16 operands are exact in double, the sum accumulates in double as
 //           the chain's), rounded to float, times scale, plus mask. A chunk whose mask is -inf for
 //           every query of the tile is not computed: its scores are -inf, as the chain forms them.
-//   stats   per row: M = max, e = exp(s - M), S = sum e in double, p = F16(e * (float)(1/S)).
-//   pv      V rows staged per chunk; out[query][dim] from the f64 MFMA over positions with the F16
+//   stats   per row: M = max, e = exp(s - M), S = sum e in double, p = F16(e * (float)(1/S))
+//           (flash_attn_ext, p_f32: p = e * (float)(1/S), not rounded to F16).
+//   pv      V rows staged per chunk; out[query][dim] from the f64 MFMA over positions with the
 //           p (skipped chunks have p = 0 throughout and add nothing), rounded to float.
 // f64 MFMA 16x16x4 lane layout: A[i][k] at lane i + 16k, B[k][j] at lane j + 16k, D[i][j] in
 // register i / 4 of lane j + 16 (i % 4).
@@ -942,7 +980,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
         }
         sum = wave_sum_d(sum);
         const float inv = sum > 0.0 ? (float) (1.0 / sum) : 0.0f;
-        for (int t = lane; t < n_pos; t += WAVE) row[t] = __half2float(__float2half_rn(as_f32(row[t] * inv)));
+        if (A.p_f32) {
+            for (int t = lane; t < n_pos; t += WAVE) row[t] = as_f32(row[t] * inv);
+        } else {
+            for (int t = lane; t < n_pos; t += WAVE) row[t] = __half2float(__float2half_rn(as_f32(row[t] * inv)));
+        }
     }
 
     // ---- P V ----

@@ -362,6 +362,9 @@ struct attn_launch {
     // zero, so that 0 * (non-finite V) cannot reach the sums. The manual chain, which never attends
     // an unwritten position, leaves it 0.
     int            skip_masked;
+    // flash_attn_ext's probabilities: ggml's flash op never materializes KQ, so p = exp(s - M) / S
+    // stays a float into the PV sums (1); the manual chain's V mul_mat converts p to F16 first (0)
+    int            p_f32;
 };
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd);
 // split-KV decode attention for 1 <= n_q <= ATT_DECODE_MAX_Q queries (groups of 4 per workgroup;

@@ -81,6 +81,10 @@ extern "C" int gl_synth_model(const char * path, const gl_synth_params * p, char
     const float ws = p->w_std, ns = p->norm_std;
     add("token_embd.weight", (ggml_type) p->embd_type, { E, V }, 0.0f, ws);
     add("output_norm.weight", GGML_TYPE_F32, { E }, 1.0f, ns);
+    if (p->rope_scaling_orig_ctx > 0) {
+        if (!phi3) return fail("synth: LongRoPE keys are written for phi3 only");
+        add("rope_factors_short.weight", GGML_TYPE_F32, { hd / 2 }, 2.0f, 0.25f);
+    }
     if (!p->tied_output) add("output.weight", (ggml_type) p->output_type, { E, V }, 0.0f, ws);
     for (int64_t il = 0; il < p->n_layer; il++) {
         const std::string b = "blk." + std::to_string(il) + ".";
@@ -139,6 +143,10 @@ extern "C" int gl_synth_model(const char * path, const gl_synth_params * p, char
     gguf_set_val_f32(g, key("attention.layer_norm_rms_epsilon").c_str(), p->rms_eps);
     gguf_set_val_f32(g, key("rope.freq_base").c_str(), p->rope_theta);
     gguf_set_val_u32(g, key("rope.dimension_count").c_str(), (uint32_t) hd);
+    if (p->rope_scaling_orig_ctx > 0) {
+        gguf_set_val_u32(g, key("rope.scaling.original_context_length").c_str(), (uint32_t) p->rope_scaling_orig_ctx);
+        gguf_set_val_f32(g, key("rope.scaling.attn_factor").c_str(), p->rope_attn_factor);
+    }
     if (moe) {
         gguf_set_val_u32(g, key("expert_count").c_str(), (uint32_t) p->n_expert);
         gguf_set_val_u32(g, key("expert_used_count").c_str(), (uint32_t) p->n_expert_used);

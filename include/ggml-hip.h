@@ -28,15 +28,19 @@ GGML_API ggml_backend_buffer_type_t ggml_backend_hip_buffer_type(int device);
 #define GGML_HIP_STATIC_SCRATCH_BYTES (64 << 20)
 
 // ggml_backend_graph_compute without any device allocation: no counterpart in the reference; for
-// callers that cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid
-// hipMalloc). The kernels' scratch (attention scores and partials, quantized activations, expert
-// groups, argmax parts) comes from a file-scope device array of GGML_HIP_STATIC_SCRATCH_BYTES
-// that every GPU the library runs on holds until the process ends; the graph's tensors are the
-// caller's as with ggml_backend_graph_compute, and the result is the same. A graph needing more
-// scratch is rejected with GGML_STATUS_ALLOC_FAILED and a message (kernels enqueued before the
-// point where the arena ran out have run; the outputs are undefined). Calls share their GPU's
-// array and keep its last contents (no kernel relies on it starting at zero): calls that overlap
-// on one GPU (several threads or backends) race. Fails with profiling on (it creates events).
+// callers that cannot allocate (serving loops, harnesses that forbid hipMalloc). The kernels'
+// scratch (attention scores and partials, quantized activations, expert groups, argmax parts)
+// comes from a file-scope device array of GGML_HIP_STATIC_SCRATCH_BYTES that every GPU the
+// library runs on holds until the process ends; the graph's tensors are the caller's as with
+// ggml_backend_graph_compute, and the result is the same. Like ggml_backend_graph_compute it
+// launches on the backend's own stream and returns after the device finished, so it cannot be
+// recorded by a caller's HIP graph capture. A graph needing more scratch is rejected with
+// GGML_STATUS_ALLOC_FAILED and a message, but only at the node where the array ran out: the
+// kernels queued before that node have run, including any KV-cache append folded into an earlier
+// attention, so cache rows of the step may already be written; the outputs are undefined. Calls
+// share their GPU's array and keep its last contents (no kernel relies on it starting at zero):
+// calls that overlap on one GPU (several threads or backends) race. Fails with profiling on (it
+// creates events).
 GGML_API enum ggml_status ggml_backend_hip_graph_compute_static(ggml_backend_t backend, struct ggml_cgraph * cgraph);
 
 // Token sampling on the device: replaces `int32_t sample(sampler &, std::vector<float> & logits,

@@ -78,6 +78,9 @@ typedef struct {
     uint64_t seed;
     int32_t n_threads;
     int32_t share_experts;   // non-zero: every layer's expert tensors hold layer 0's values
+    int32_t rope_scaling_orig_ctx; // non-zero: phi3 LongRoPE keys ({arch}.rope.scaling.original_context_length
+                                   // = this, .rope.scaling.attn_factor) and rope_factors_short.weight
+    float   rope_attn_factor;      // the LongRoPE attention factor written with those keys
 } gl_synth_params;
 
 // Weights are N(0, w_std) floats from a counter-based generator (splitmix64 -> Box-Muller in
@@ -85,6 +88,8 @@ typedef struct {
 // (qwen3moe) writes layer 0's quantized expert tensors into every layer: the expert weights of a
 // 48-layer, 128-expert model are 29e9 values, minutes of quantization; routers, attention and norm
 // weights stay distinct per layer, so routing still differs from layer to layer.
+// rope_scaling_orig_ctx (phi3 LongRoPE, reference model.cpp:145-153, 555-557): the frequency
+// factors rope_factors_short.weight F32[head_dim / 2] are 2 + N(0, 0.25) values (seeded).
 GGML_API int gl_synth_model(const char * path, const gl_synth_params * p, char * err, size_t err_size);
 
 // The seeded normal generator the synthetic models use: out[i] = mean + std * z(seed, first + i).

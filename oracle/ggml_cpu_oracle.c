@@ -31,6 +31,10 @@
 
 typedef double ggml_float;
 
+/* planted-mistake bits (oracle_set_planted in oracle.h): 0 in every normal use */
+static int g_planted = 0;
+void oracle_set_planted(int bits) { g_planted = bits; }
+
 /* Transcendentals of the float ops (RoPE cos/sin, softmax and SiLU exp) are the correctly rounded
  * float results: evaluated in double and rounded once. ggml-cpu calls the platform's cosf/sinf/
  * expf, whose last-ulp behaviour differs between libms (glibc's cosf/sinf are off by one ulp on
@@ -130,8 +134,9 @@ void oracle_quantize_q4_0(const float * x, void * vy, int64_t k) {
         for (int j = 0; j < 16; ++j) {
             const float x0 = x[i * 32 + j] * id;
             const float x1 = x[i * 32 + 16 + j] * id;
-            const int8_t a = (int8_t) (x0 + 8.5f);
-            const int8_t b = (int8_t) (x1 + 8.5f);
+            const float half = g_planted & 8 ? 8.0f : 8.5f;
+            const int8_t a = (int8_t) (x0 + half);
+            const int8_t b = (int8_t) (x1 + half);
             const uint8_t xi0 = (uint8_t) (a < 15 ? a : 15);
             const uint8_t xi1 = (uint8_t) (b < 15 ? b : 15);
             y[i].qs[j] = (uint8_t) (xi0 | (xi1 << 4));
@@ -198,6 +203,7 @@ static float make_qkx2_quants(int n, int nmax, const float * x, const float * we
         *the_min = -min;
         return 0.f;
     }
+    if (g_planted & 16) nstep = -1;
     float iscale = nmax / (max - min);
     float scale = 1 / iscale;
     float best_error = 0;
@@ -246,6 +252,14 @@ static float make_qkx2_quants(int n, int nmax, const float * x, const float * we
     return scale;
 }
 
+/* exported for the tests: one sub-block's grid fit, exactly as oracle_quantize_q4_K calls it */
+float oracle_make_qkx2_quants(int n, int nmax, const float * x, const float * weights, uint8_t * L, float * the_min,
+                              float rmin, float rdelta, int nstep) {
+    uint8_t Laux[256];
+    if (n > 256) return -1.f;
+    return make_qkx2_quants(n, nmax, x, weights, L, the_min, Laux, rmin, rdelta, nstep);
+}
+
 void oracle_quantize_q4_K(const float * x, void * vy, int64_t k) {
     bq4_K * y = (bq4_K *) vy;
     uint8_t L[256], Laux[32];
@@ -257,7 +271,7 @@ void oracle_quantize_q4_K(const float * x, void * vy, int64_t k) {
             float sum_x2 = 0;
             for (int l = 0; l < 32; ++l) sum_x2 += xb[32 * j + l] * xb[32 * j + l];
             const float av_x = sqrtf(sum_x2 / 32);
-            for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(xb[32 * j + l]);
+            for (int l = 0; l < 32; ++l) weights[l] = g_planted & 32 ? 1.0f : av_x + fabsf(xb[32 * j + l]);
             scales[j] = make_qkx2_quants(32, 15, xb + 32 * j, weights, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20);
             if (scales[j] > max_scale) max_scale = scales[j];
             if (mins[j] > max_min) max_min = mins[j];
@@ -376,8 +390,6 @@ void oracle_set_block_sum_order(int mode) { g_block_sum_order = mode; }
    h % n_head_kv instead of h / (n_head / n_head_kv) (mul_mat's and flash_attn_ext's head
    broadcast). Bit 2: rope rotates the other pairing (NEOX's (i, i + n_dims/2) and NORMAL's
    (2i, 2i + 1) exchanged). Bit 4: soft_max and flash_attn_ext drop the scale (1/sqrt(head_dim)). */
-static int g_planted = 0;
-void oracle_set_planted(int bits) { g_planted = bits; }
 
 static float sum_block_terms(const float * t, int64_t n) {
     if (g_block_sum_order == 0) {
@@ -578,7 +590,8 @@ static void rope_yarn(float theta_extrap, float freq_scale, const float corr_dim
     float theta = theta_interp;
     if (ext_factor != 0.0f) {
         const float ramp_mix = yarn_ramp(corr_dims[0], corr_dims[1], (int) i0) * ext_factor;
-        theta = theta_interp * (1 - ramp_mix) + theta_extrap * ramp_mix;
+        theta = g_planted & 64 ? theta_extrap * (1 - ramp_mix) + theta_interp * ramp_mix
+                               : theta_interp * (1 - ramp_mix) + theta_extrap * ramp_mix;
         mscale *= 1.0f + 0.1f * log_cr(1.0f / freq_scale);
     }
     *cos_theta = cos_cr(theta) * mscale;
@@ -597,7 +610,8 @@ static void rope_cache(int32_t pos, float freq_scale, const float * freq_factors
     float theta = (float) pos;
     for (int64_t i0 = 0; i0 < ne0; i0 += 2) {
         const float ff = freq_factors ? freq_factors[i0 / 2] : 1.0f;
-        rope_yarn(theta / ff, freq_scale, corr_dims, i0, ext_factor, mscale, &cache[i0 + 0], &cache[i0 + 1]);
+        rope_yarn(g_planted & 128 ? theta * ff : theta / ff, freq_scale, corr_dims, i0, ext_factor, mscale,
+                  &cache[i0 + 0], &cache[i0 + 1]);
         theta *= theta_scale;
     }
 }

@@ -16,19 +16,25 @@
  *   fp16 <-> fp32              IEEE binary16 (numpy): all 65536 codes; 3M f32 patterns incl. ties
  *   Q4_0 decode                closed form over every nibble at every position, 8 scales
  *   Q8_0, Q4_K decode          reference dequant_row golden vectors, bit-exact (dequant.c:94-251)
- *   Q4_0/Q8_0/Q8_K quantizers  error bounds (round to nearest within d/2, the +8 clip of Q4_0),
- *                              zero and constant blocks, Q8_K block sums; the product's quantizer
- *                              byte-identical. Byte-level equality with upstream ggml's
- *                              quantize_row_*_ref: parity unpinned (upstream ggml is absent)
- *   Q4_K quantizer             RMS-error bound, zero block, product byte-identical; byte-level
- *                              equality with upstream ggml: parity unpinned
+ *   Q4_0 quantizer             tests/test_oracle_pins.py: d = binary16(max / -8), codes x/d rounded
+ *                              half up (constructed ties at power-of-two scales), clipped to 15
+ *                              exactly where x/d >= 7.5; a planted truncation fails
+ *   Q8_0/Q8_K quantizers       error bounds (round to nearest within d/2), zero and constant
+ *                              blocks, Q8_K block sums; the product's quantizers byte-identical
+ *   Q4_K quantizer             tests/test_oracle_pins.py: make_qkx2_quants against a float64
+ *                              statement of ggml's search (same pick where float32 rounding cannot
+ *                              decide it), scale/min codes of the float64 optimum under weights
+ *                              av_x + |x|, d/dmin = binary16(max / 63), nibbles re-rounded; planted
+ *                              mistakes (no search, unit weights) fail
  *   vec dots / gemv            fp64 brute force over the same quantized operands; one-hot columns;
  *                              reference sc_matmul golden (Q4_K) within the activation-quantization
  *                              bound. ggml-cpu's block-sum order itself: parity unpinned
  *   rms_norm, softmax, silu    reference sc_rmsnorm / sc_softmax / sc_swiglu golden vectors
  *                              (tolerance: float vs double sums); softmax masks and row sums
  *   rope                       reference sc_rope golden (NEOX); position 0 identity; pair norms;
- *                              theta_0 = pos; NORMAL == NEOX on interleaved pairs; partial dims
+ *                              theta_0 = pos; NORMAL == NEOX on interleaved pairs; partial dims;
+ *                              frequency factors, attn_factor, freq_scale and the YaRN ramp by
+ *                              identities and float64 rotations (tests/test_oracle_pins.py)
  *   attention chain            n_kv = 1 -> V; equal keys -> mean of V (exact); fp64 GQA brute force
  *                              that also rejects the h % n_head_kv mapping; the reference MoE
  *                              engine's own qwen3moe forward (qwen_model.c attention_block: q/k
@@ -65,6 +71,11 @@ void oracle_quantize_q8_0(const float * x, void * y, int64_t k);
 void oracle_quantize_q4_K(const float * x, void * y, int64_t k);
 void oracle_quantize_q8_K(const float * x, void * y, int64_t k);
 
+/* ggml's make_qkx2_quants (the per-sub-block weighted grid search inside the Q4_K quantizer):
+   n <= 256 values with weights, codes 0..nmax into L, returns the scale and writes -min */
+float oracle_make_qkx2_quants(int n, int nmax, const float * x, const float * weights, uint8_t * L, float * the_min,
+                              float rmin, float rdelta, int nstep);
+
 /* row decoders (type = ggml type id: 0 f32, 1 f16, 2 q4_0, 8 q8_0, 12 q4_K, 30 bf16); 0 on unknown type */
 int oracle_dequantize(int type, const void * x, float * y, int64_t k);
 
@@ -91,9 +102,13 @@ void oracle_moe_route(const float * logits, int n_expert, int top_k, int32_t * i
    order, the default; 1 = a 32-lane wave reduction), tests/exactness_experiment.py only */
 void oracle_set_block_sum_order(int mode);
 
-/* test hook: plants a known attention mistake (0 = none, the default; bit 1 = query head h reads
-   KV head h % n_head_kv; bit 2 = rope's NEOX and NORMAL pairings exchanged; bit 4 = soft_max and
-   flash_attn_ext without their scale), tests/test_ref_qwen.py only */
+/* test hook: plants a known mistake (0 = none, the default), to show that a check fails on it:
+   bit 1 = query head h reads KV head h % n_head_kv; bit 2 = rope's NEOX and NORMAL pairings
+   exchanged; bit 4 = soft_max and flash_attn_ext without their scale (tests/test_ref_qwen.py);
+   bit 8 = Q4_0 codes truncated (x/d + 8) instead of rounded (+ 8.5); bit 16 = make_qkx2_quants
+   without its scale search; bit 32 = Q4_K sub-block weights 1 instead of av_x + |x|; bit 64 = the
+   YaRN ramp's extrapolated and interpolated angles exchanged; bit 128 = rope freq_factors
+   multiplying the angle instead of dividing it (tests/test_oracle_pins.py) */
 void oracle_set_planted(int bits);
 
 /* sample() (model.cpp:1675-1728) on n logits with the window recent[0..n_recent) and the

@@ -65,6 +65,8 @@ def oracle():
         o.oracle_gemv.argtypes = [C.c_int, vp, i64, i64, vp, vp, C.c_int]
         o.oracle_rope.restype = None
         o.oracle_rope.argtypes = [vp, vp, i64, C.c_int, C.c_int, C.c_int32] + [C.c_float] * 6 + [C.c_int, vp]
+        o.oracle_make_qkx2_quants.restype = C.c_float
+        o.oracle_make_qkx2_quants.argtypes = [C.c_int, C.c_int, vp, vp, vp, vp, C.c_float, C.c_float, C.c_int]
         o.oracle_moe_route.restype = None
         o.oracle_moe_route.argtypes = [vp, C.c_int, C.c_int, vp, vp]
         o.oracle_sample.restype = C.c_int32

@@ -10,7 +10,7 @@ import os
 import numpy as np
 import pytest
 
-from gl import cpu_backend, gl, rel_err
+from gl import cpu_backend, gl, rel_err, rel_err_floor
 
 pytestmark = pytest.mark.gpu
 
@@ -25,6 +25,10 @@ TINY = {
                   n_vocab=900, rope_theta=1e6, wtype=gl.Q8_0),
     "phi3": dict(arch="phi3", n_embd=384, n_layer=2, n_head=4, n_head_kv=4, head_dim=96, n_ff=512,
                  n_vocab=700, wtype=gl.Q8_0),
+    # phi3 LongRoPE (model.cpp:145-153, 555-557, 1312-1316): rope_factors_short divides each pair's
+    # angle, ext_factor 1 with beta 32 / 1 and the attention factor scale cos and sin
+    "phi3_longrope": dict(arch="phi3", n_embd=384, n_layer=2, n_head=4, n_head_kv=4, head_dim=96, n_ff=512,
+                          n_vocab=700, wtype=gl.Q8_0, rope_scaling_orig_ctx=4096, rope_attn_factor=1.1902),
     "qwen3moe": dict(arch="qwen3moe", n_embd=512, n_layer=2, n_head=8, n_head_kv=2, head_dim=64, n_ff=512,
                      n_vocab=800, n_expert=32, n_expert_used=8, n_ff_exp=256, rope_theta=1e6, rms_eps=1e-6,
                      wtype=gl.Q4_K),
@@ -66,7 +70,7 @@ def test_decode_parity_tiny(models, arch, fusion):
             tok = int(np.argmax(lc))
 
 
-@pytest.mark.parametrize("arch", ["llama", "phi3", "qwen2", "qwen3", "qwen3moe"])
+@pytest.mark.parametrize("arch", ["llama", "phi3", "phi3_longrope", "qwen2", "qwen3", "qwen3moe"])
 def test_prefill_parity_long_prompt(models, arch):
     """A 100-token prompt in one forward_step (the quantized projections run on the prefill GEMM,
     attention on the graph's own K^T Q -> softmax -> V chain), then decode steps on its KV cache."""
@@ -116,5 +120,5 @@ def test_llama3b_decode_step_full_size(tmp_path_factory):
     with gl.Session(p, "cpu", n_ctx=2049 + 1, n_threads=16) as c:
         c.kv_fill_random(2048, seed=3)
         lc = c.forward(2048, [12345])
-    assert rel_err(lh, lc) < TOL
+    assert rel_err_floor(lh, lc) < TOL
     assert int(np.argmax(lh)) == int(np.argmax(lc))

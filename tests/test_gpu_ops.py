@@ -11,7 +11,7 @@ rel_err in gl.py), the ggml test-backend-ops bar for that op.
 import numpy as np
 import pytest
 
-from gl import Graph, attention_graph, cpu_backend, gl, moe_ffn_graph, quantize, rel_err, run_on
+from gl import Graph, attention_graph, cpu_backend, gl, moe_ffn_graph, quantize, rel_err, rel_err_floor, run_on
 
 pytestmark = pytest.mark.gpu
 
@@ -584,7 +584,8 @@ def test_attention_decode(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
             continue
         a, b = both(hip, cpu, build, fusion)
         if flash:
-            assert rel_err(a, b) < TOL, (fusion, rel_err(a, b))
+            # ggml-cpu's online softmax against one pass with float p: per element within 2e-3
+            assert rel_err_floor(a, b) < TOL, (fusion, rel_err_floor(a, b))
         else:
             # the graph's chain of float roundings is reproduced exactly, fused or not
             assert np.array_equal(a, b), (fusion, rel_err(a, b))
@@ -593,6 +594,40 @@ def test_attention_decode(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
         grp = n_head // n_head_kv
         expect = np.repeat(vc[0].astype(np.float32), grp, axis=0).reshape(-1)
         assert rel_err(a, expect) < 1e-6
+
+
+@pytest.mark.parametrize("n_new", [2, 20])     # the decode kernels, the prefill kernel
+def test_attention_masked_nonfinite_k_row(hip, cpu, n_new):
+    """The fused attention gives a position masked for a query the score -inf without reading its
+    dot, on every path. ggml-cpu's manual chain forms NaN * scale + (-inf) = NaN there and spreads
+    it over the row: a documented deviation. In forward_step the manual chain masks only the step's
+    own later tokens, whose K rows come from the same activations, so it shows only when those are
+    already non-finite. Queries that cannot see the row equal the chain over a finite row; the
+    query that attends it is NaN on both."""
+    hd, n_head, n_head_kv, n_kv = 128, 8, 2, 70
+    G = n_head // n_head_kv
+    r = rng(70 + n_new)
+    n_ctx = n_kv + 3
+    kc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+    vc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+    q = r.standard_normal((n_new, n_head, hd)).astype(np.float32)
+    mask = np.zeros((n_new, n_kv), dtype=np.float32)
+    for i in range(n_new):
+        mask[i, n_kv - n_new + i + 1:] = -np.inf
+    bad, finite = kc.copy(), kc.copy()
+    bad[n_kv - 1, 0, :] = np.nan                  # the last new token's K row of KV head 0
+    finite[n_kv - 1, 0, :] = 0.5
+
+    def build(k):
+        return lambda g: attention_graph(g, hd, n_head, n_head_kv, n_kv, n_new, n_ctx, k, vc, q, mask, False)
+
+    a = run_on(hip, build(bad)).reshape(n_new, n_head, hd)
+    b = run_on(cpu, build(finite)).reshape(n_new, n_head, hd)
+    c = run_on(cpu, build(bad)).reshape(n_new, n_head, hd)
+    assert np.array_equal(a[:-1], b[:-1])
+    assert np.array_equal(a[-1, G:], b[-1, G:])
+    assert np.isnan(a[-1, :G]).all() and np.isnan(c[-1, :G]).all()
+    assert np.isnan(c[0, :G]).all()               # the chain itself spreads the masked NaN
 
 
 @pytest.mark.parametrize("hd,n_head,n_head_kv,n_kv,n_new", [
@@ -623,7 +658,7 @@ def test_attention_prefill(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
     b = run_on(cpu, build)
     assert "attn_prefill" in names, names
     if flash:
-        assert rel_err(a, b) < TOL, rel_err(a, b)
+        assert rel_err_floor(a, b) < TOL, rel_err_floor(a, b)
     else:
         assert np.array_equal(a, b), rel_err(a, b)
 
@@ -657,7 +692,7 @@ def test_attention_long_context_query_groups(hip, cpu, hd, n_head, n_head_kv, n_
     b = run_on(cpu, build)
     assert "attn_decode" in names and "attn_prefill" not in names, names
     if flash:
-        assert rel_err(a, b) < TOL, rel_err(a, b)
+        assert rel_err_floor(a, b) < TOL, rel_err_floor(a, b)
     else:
         assert np.array_equal(a, b), rel_err(a, b)
 

@@ -23,8 +23,8 @@ GPU tier:
 * The same reference runtime on ggml_backend_hip_init(0) is bit-identical to itself on the oracle
   backend for the four architectures, and to the product session on hip.
 * dory on hip, NaN-filled rings, against the float64 statement (its top token within 0.1 logit
-  standard deviation of the statement's best). hip's flash_attn_ext forms the softmax as the
-  manual chain does (p rounded to F16), not by ggml-cpu's online rescaling.
+  standard deviation of the statement's best). hip's flash_attn_ext forms the softmax in one
+  pass with float probabilities, not by ggml-cpu's online rescaling.
   - F32 matrices: within relative L2 1e-3 of the statement and of the oracle backend (measured
     4.8e-4 and 4.9e-4).
   - Q8_0 and Q4_K matrices: every matrix requantizes its input to 8 bits, which amplifies any
@@ -44,7 +44,10 @@ pytestmark = pytest.mark.skipif(not os.path.exists(REF_RUNTIME_SO),
                                 reason="oracle/_ref/libref_runtime.so not built (no /root/reference)")
 
 # the reference's model.cpp knows no qwen3moe (its MoE engine is qwen_model.c, checked in test_ref_qwen.py)
-ARCHS = [("llama", gl.Q4_0, {}), ("qwen2", gl.Q8_0, {}), ("qwen3", gl.Q4_K, {}), ("phi3", gl.Q8_0, {})]
+ARCHS = [("llama", gl.Q4_0, {}), ("qwen2", gl.Q8_0, {}), ("qwen3", gl.Q4_K, {}), ("phi3", gl.Q8_0, {}),
+         # phi3 with LongRoPE keys: the reference reads rope_factors_short and passes ext_factor 1
+         ("phi3", gl.Q8_0, {"rope_scaling_orig_ctx": 4096, "rope_attn_factor": 1.1902})]
+ARCH_IDS = [a[0] + ("-longrope" if a[2] else "") for a in ARCHS]
 TOKENS = np.array([1, 5, 9, 100, 200, 300, 7, 8, 11, 2], np.int32)
 N_PROMPT = 6
 N_CTX = 64
@@ -84,7 +87,7 @@ def oracle_backend():
     gl.libs()["core"].ggml_backend_free(b)
 
 
-@pytest.mark.parametrize("arch,wtype,extra", ARCHS, ids=[a[0] for a in ARCHS])
+@pytest.mark.parametrize("arch,wtype,extra", ARCHS, ids=ARCH_IDS)
 def test_reference_runtime_equals_product_runtime_on_the_oracle(oracle_backend, tmp_path, arch, wtype, extra):
     path = synth(tmp_path, arch, wtype, extra)
     ref = ref_runtime_logits(path, oracle_backend)
@@ -153,7 +156,7 @@ def hip_backend():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("arch,wtype,extra", ARCHS, ids=[a[0] for a in ARCHS])
+@pytest.mark.parametrize("arch,wtype,extra", ARCHS, ids=ARCH_IDS)
 def test_reference_runtime_on_hip(oracle_backend, hip_backend, tmp_path, arch, wtype, extra):
     path = synth(tmp_path, arch, wtype, extra)
     on_hip = ref_runtime_logits(path, hip_backend)

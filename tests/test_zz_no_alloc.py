@@ -4,9 +4,12 @@ static device array) against ggml_backend_graph_compute on the same graphs, thro
 Bar: bit-identical outputs (both run the same kernels; only where their scratch lives differs).
 Two calls in a row with the second graph smaller, so the second static call runs over the first
 one's leftovers in the shared array; and a graph needing more scratch than the array holds is
-rejected with GGML_STATUS_ALLOC_FAILED before its attention is launched, after which both entry
-points still work.
+rejected with GGML_STATUS_ALLOC_FAILED (kernels queued before the arena ran out have run), after
+which both entry points still work. The device's free memory (hipMemGetInfo) is the same just
+before and just after each static call, so the call allocated nothing.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -62,8 +65,24 @@ def build_layer(g, d):
     return [o, u]
 
 
-def compute(backend, d, static):
-    """(status, outputs) of one graph compute through either entry point."""
+_hip_rt = None
+
+
+def free_device_bytes():
+    """hipMemGetInfo's free bytes of the current device (the HIP runtime the backend loaded)."""
+    global _hip_rt
+    if _hip_rt is None:
+        _hip_rt = C.CDLL("libamdhip64.so")
+        _hip_rt.hipMemGetInfo.restype = C.c_int
+        _hip_rt.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+    free, total = C.c_size_t(0), C.c_size_t(0)
+    assert _hip_rt.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    return free.value
+
+
+def compute(backend, d, static, probe=None):
+    """(status, outputs) of one graph compute through either entry point; with probe (a list), the
+    device's free bytes just before and just after the compute call are appended to it."""
     core, hip = gl.libs()["core"], gl.libs()["hip"]
     with Graph() as g:
         outs = build_layer(g, d)
@@ -74,10 +93,14 @@ def compute(backend, d, static):
         g.buf = core.ggml_backend_alloc_ctx_tensors(g.ctx, backend)
         for t, a in g.inputs:
             core.ggml_backend_tensor_set(t, a.ctypes.data, 0, a.nbytes)
+        if probe is not None:
+            probe.append(free_device_bytes())
         if static:
             st = hip.ggml_backend_hip_graph_compute_static(backend, gf)
         else:
             st = core.ggml_backend_graph_compute(backend, gf)
+        if probe is not None:
+            probe.append(free_device_bytes())
         return st, ([g.read(t) for t in outs] if st == 0 else None)
 
 
@@ -87,10 +110,17 @@ def test_static_compute_matches_graph_compute(hip, n_new):
     for n_kv in (700, 150):
         d = layer_inputs(n_kv, n_new)
         st_a, ref = compute(hip, d, static=False)
-        st_b, got = compute(hip, d, static=True)
+        probe = []
+        st_b, got = compute(hip, d, static=True, probe=probe)
         assert st_a == 0 and st_b == 0
         for a, b in zip(ref, got):
             assert np.array_equal(a, b), (n_kv, n_new)
+        # the static call itself takes no device memory (the runtime's own first-use allocations
+        # aside: checked on a repeat of the same call)
+        probe = []
+        st_c, again = compute(hip, d, static=True, probe=probe)
+        assert st_c == 0 and all(np.array_equal(a, b) for a, b in zip(ref, again))
+        assert probe[0] == probe[1], (n_kv, n_new, probe)
 
 
 def test_static_compute_rejects_oversized_scratch(hip):
@@ -101,7 +131,9 @@ def test_static_compute_rejects_oversized_scratch(hip):
     # both entry points still work afterwards, and agree
     d = layer_inputs(300, 1, seed=4)
     st_a, ref = compute(hip, d, static=False)
-    st_b, got = compute(hip, d, static=True)
+    probe = []
+    st_b, got = compute(hip, d, static=True, probe=probe)
     assert st_a == 0 and st_b == 0
     for a, b in zip(ref, got):
         assert np.array_equal(a, b)
+    assert probe[0] == probe[1], probe
