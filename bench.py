@@ -76,17 +76,18 @@ def describe(cfg, n_past, batch):
 
 
 def timed_reps(run, n_steps, reps):
-    """The timed steps split into reps of near-equal size, each timed on its own by run(k) -> seconds
-    (cmd_bench.cpp:30-38, 135-147 reports the mean and sample standard deviation over its reps).
-    Returns the total seconds of the n_steps steps and the per-rep statistics."""
+    """One timed loop of n_steps steps (run(k) -> seconds), which gives the reported value, then
+    reps - 1 more loops of the same steps for the spread (cmd_bench.cpp:30-38, 135-147 reports the
+    mean and sample standard deviation over its reps). Each loop starts from an idle device, so the
+    reps are whole loops rather than slices of one: a slice would expose the pipeline's fill once
+    per slice. Returns the first loop's seconds and the statistics over all loops."""
     import statistics
-    reps = max(1, min(reps, n_steps))
-    sizes = [n_steps // reps + (1 if i < n_steps % reps else 0) for i in range(reps)]
-    times = [run(k) for k in sizes]
-    rates = [k / t for k, t in zip(sizes, times)]
-    stats = {"n": reps, "steps_per_rep": sizes, "steps_per_s_mean": round(statistics.fmean(rates), 3),
+    reps = max(1, reps)
+    times = [run(n_steps) for _ in range(reps)]
+    rates = [n_steps / t for t in times]
+    stats = {"n": reps, "steps_per_rep": n_steps, "steps_per_s_mean": round(statistics.fmean(rates), 3),
              "steps_per_s_stddev": round(statistics.stdev(rates), 3) if reps > 1 else 0.0}
-    return sum(times), stats
+    return times[0], stats
 
 
 def oracle_helpers():
@@ -148,7 +149,8 @@ def cpu_baseline(gl, model_path, n_pos, tokens, seconds, threads):
 
             t1 = steps(1)  # warmup, also sizes the sample
             n = max(1, min(64, int(seconds / len(threads) / max(t1, 1e-6))))
-            t, reps = timed_reps(steps, n, 3)
+            t, reps = timed_reps(steps, max(1, n // 3), 3)
+            n = max(1, n // 3)
         runs[nt] = (n * batch / t, n, t, reps)
         log(f"[bench] cpu baseline {nt} threads: {n} steps in {t:.2f}s -> {n * batch / t:.2f} tok/s "
             f"({reps['steps_per_s_mean'] * batch:.2f} +- {reps['steps_per_s_stddev'] * batch:.2f} over {reps['n']} reps)")
@@ -440,7 +442,7 @@ def main():
     # 0.2 s region (GPU clock ramp, host scheduling), and 50 warmup steps bring the clocks up first
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--reps", type=int, default=5, help="the timed steps in this many separately timed reps (mean +- sd)")
+    ap.add_argument("--reps", type=int, default=3, help="timed loops of --steps steps: the first gives the value, all give mean +- sd")
     ap.add_argument("--config", default="llama3b")
     ap.add_argument("--n-past", type=int, default=None, help="KV positions before the step (default: per config)")
     ap.add_argument("--batch", type=int, default=1, help="new tokens per decode step")

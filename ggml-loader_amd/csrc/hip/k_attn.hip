@@ -50,32 +50,6 @@ constexpr int STATS_SEG = ATT_THREADS * STATS_PER_THREAD;    // positions per st
 __host__ __device__ inline int attn_chunks(int n_kv) { return (n_kv + ATT_CHUNK - 1) / ATT_CHUNK; }
 __host__ __device__ inline int attn_segs(int n_kv) { return (n_kv + STATS_SEG - 1) / STATS_SEG; }
 
-// Workgroup numbering of the scores and PV launches (1-D grids). A launch's workgroups go to the
-// part's 8 XCDs in turn (workgroup i to XCD i % 8), and each XCD has an L2 of its own. The
-// workgroups that read one position chunk of one KV head -- the head groups of that KV head, and
-// the query groups of a multi-token step: `members` of them -- get ids congruent mod 8, so they run
-// on one XCD and the chunk comes from HBM once. Sets (KV head, chunk) are numbered chunk fastest;
-// ids past the last set (at most 7 sets' worth) exit at once.
-constexpr int N_XCD = 8;
-struct attn_wg {
-    int chunk, hg, qg;   // position chunk, head group (heads hg * G ..), query group
-    bool live;
-};
-__host__ __device__ inline int attn_grid(int n_chunks, int n_head_kv, int members) {
-    return (n_chunks * n_head_kv + N_XCD - 1) / N_XCD * N_XCD * members;
-}
-__device__ __forceinline__ attn_wg attn_wg_of(int n_chunks, int n_head_kv, int hg_per_kv, int n_qg) {
-    const int L = blockIdx.x, xcd = L % N_XCD, r = L / N_XCD;
-    const int members = hg_per_kv * n_qg;
-    const int m = r % members, set = r / members * N_XCD + xcd;
-    attn_wg w;
-    w.live = set < n_chunks * n_head_kv;
-    w.chunk = set % n_chunks;
-    w.hg = set / n_chunks * hg_per_kv + m % hg_per_kv;
-    w.qg = m / hg_per_kv;
-    return w;
-}
-
 // Scratch (all per row = (query, head)): scores f32 [n_kv], the maximum of each 64-position chunk
 // f32 [chunks], the row maximum f32, the sum of exp(s - max) over each statistics segment f64
 // [segs], and the PV partials f64 [pv chunks][n_q][n_head][hd].
@@ -132,17 +106,14 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
     __shared__ __align__(16) uint32_t s_knew[ATT_MAX_Q * HD2];   // the new tokens' rotated K rows (F16)
     __shared__ float s_cm[ATT_WAVES][ATT_MAX_Q * 8];
     extern __shared__ __align__(16) float s_dyn[];
-    // W.hg: a group of G consecutive heads (all heads of KV head kvh, or a part of them when the
-    // launch splits a large GQA group over several workgroups); h0 its first head
-    const attn_wg W = attn_wg_of(attn_chunks(A.n_kv), A.n_head_kv, A.n_head / A.n_head_kv / G,
-                                 (A.n_q + ATT_MAX_Q - 1) / ATT_MAX_Q);
-    if (!W.live) return;
-    const int split = W.chunk, h0 = W.hg * G, kvh = h0 / (A.n_head / A.n_head_kv);
+    // blockIdx.y: a group of G consecutive heads (all heads of KV head kvh, or a part of them when
+    // the launch splits a large GQA group over several workgroups); h0 its first head
+    const int split = blockIdx.x, h0 = blockIdx.y * G, kvh = h0 / (A.n_head / A.n_head_kv);
     const bool kv_writer = h0 % (A.n_head / A.n_head_kv) == 0;   // the first group of a KV head appends K and V
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int t0 = split * ATT_CHUNK;
     const int nt = min(ATT_CHUNK, A.n_kv - t0);
-    const int q0 = W.qg * ATT_MAX_Q;                  // this workgroup's queries: q0 .. q0 + n_q - 1
+    const int q0 = blockIdx.z * ATT_MAX_Q;            // this workgroup's queries: q0 .. q0 + n_q - 1
     const int n_q = min(ATT_MAX_Q, A.n_q - q0);
     const attn_scratch S = scratch_of(A);
     constexpr int DQ = HD / 4;                        // head dims per quarter (per lane in the dots)
@@ -248,7 +219,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
             sn = cs_in.y;
         } else if (A.rope) {
             rope_pair_cs(A.rq.p, A.rq.ff, my_pos, tp % half, c, sn);
-            if (A.cs_mode == 1 && split == 0 && W.hg == 0 && t < n_q * half) A.cs_tab[tp] = make_float2(c, sn);
+            if (A.cs_mode == 1 && blockIdx.x == 0 && blockIdx.y == 0 && t < n_q * half) A.cs_tab[tp] = make_float2(c, sn);
         }
         s_cs[tp] = make_float2(c, sn);
     }
@@ -522,14 +493,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     __shared__ float s_M[PV_MAX_ROWS], s_inv[PV_MAX_ROWS];
     uint32_t * s_v = (uint32_t *) s_buf;                  // [PV_CHUNK][HD2]
     double * s_part = (double *) s_buf;                   // [ATT_WAVES][PV_MAX_ROWS][HD], after the dots
-    const attn_wg W = attn_wg_of((A.n_kv + PV_CHUNK - 1) / PV_CHUNK, A.n_head_kv, A.n_head / A.n_head_kv / G,
-                                 (A.n_q + pvq - 1) / pvq);
-    if (!W.live) return;
-    const int split = W.chunk, h0 = W.hg * G, kvh = h0 / (A.n_head / A.n_head_kv);   // as in the scores kernel
+    const int split = blockIdx.x, h0 = blockIdx.y * G, kvh = h0 / (A.n_head / A.n_head_kv);   // as in the scores kernel
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int t0 = split * PV_CHUNK;
     const int nt = min(PV_CHUNK, A.n_kv - t0);
-    const int q0 = W.qg * pvq;                        // this workgroup's queries: q0 .. q0 + pvq - 1
+    const int q0 = blockIdx.z * pvq;                  // this workgroup's queries: q0 .. q0 + pvq - 1
     const int n_rows = min(pvq, A.n_q - q0) * G;      // <= PV_MAX_ROWS (pvq = PV_MAX_ROWS / G or 1)
     const attn_scratch S = scratch_of(A);
     const int nseg = attn_segs(A.n_kv);
@@ -728,15 +696,13 @@ static void launch_attn_t(const attn_launch & A, hipStream_t st) {
         HIP_CHECK(hipFuncSetAttribute((const void *) attn_scores_kernel<HD, G>, hipFuncAttributeMaxDynamicSharedMemorySize, 98304));
         big_lds = true;
     }
-    const int hg_per_kv = A.n_head / A.n_head_kv / G;
-    launch((attn_scores_kernel<HD, G>), dim3(attn_grid(splits, A.n_head_kv, hg_per_kv * qz)), dim3(ATT_THREADS), dyn, st, A);
+    launch((attn_scores_kernel<HD, G>), dim3(splits, A.n_head / G, qz), dim3(ATT_THREADS), dyn, st, A);
     static_assert(G <= PV_MAX_ROWS, "PV rows");
     const int pvq = std::max(1, std::min(ATT_MAX_Q, PV_MAX_ROWS / G));   // queries per PV workgroup
-    const dim3 pv_grid(attn_grid(pv_splits, A.n_head_kv, hg_per_kv * ((A.n_q + pvq - 1) / pvq)));
+    const dim3 pv_grid(pv_splits, A.n_head / G, (A.n_q + pvq - 1) / pvq);
     if (A.n_q == 1 && A.n_kv <= PV_FS_MAX_KV) {
         // one head per workgroup: each workgroup evaluates the exp of every score of its rows
-        launch((attn_pv_kernel<HD, 1, PV_FS_SPT>), dim3(attn_grid(pv_splits, A.n_head_kv, A.n_head / A.n_head_kv)),
-               dim3(ATT_THREADS), 0, st, A, 1);
+        launch((attn_pv_kernel<HD, 1, PV_FS_SPT>), dim3(pv_splits, A.n_head, 1), dim3(ATT_THREADS), 0, st, A, 1);
     } else {
         launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
         launch((attn_pv_kernel<HD, G, 0>), pv_grid, dim3(ATT_THREADS), 0, st, A, pvq);
