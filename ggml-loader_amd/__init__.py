@@ -21,7 +21,7 @@ LIB_DIR = os.environ.get("GGML_LOADER_LIB_DIR") or os.path.join(PKG_DIR, "lib")
 BIN_DIR = os.path.join(PKG_DIR, "bin")
 
 # ggml type ids (GGUF on-disk ids)
-F32, F16, Q4_0, Q8_0, Q4_K, Q8_K, I32, BF16 = 0, 1, 2, 8, 12, 15, 26, 30
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, I32, BF16 = 0, 1, 2, 8, 12, 13, 14, 15, 26, 30
 ROPE_NORMAL, ROPE_NEOX = 0, 2
 SORT_ASC, SORT_DESC = 0, 1
 UNARY_SILU = 1

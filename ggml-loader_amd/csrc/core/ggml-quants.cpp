@@ -6,12 +6,18 @@
 //   Q8_0  34 B / 32 w : fp16 d, i8 qs[32]; w[j] = qs[j] d
 //   Q4_K 144 B / 256 w: fp16 d, fp16 dmin, u8 scales[12] (8 x 6-bit scale + 8 x 6-bit min),
 //                       u8 qs[128]; w = d sc_j q - dmin m_j per 32-weight sub-block j
+//   Q5_K 176 B / 256 w: fp16 d, fp16 dmin, u8 scales[12] (as Q4_K), u8 qh[32] (bit j of qh[l]: the
+//                       fifth bit of element l of sub-block j), u8 qs[128] (low nibbles as Q4_K)
+//   Q6_K 210 B / 256 w: u8 ql[128], u8 qh[64], i8 scales[16], fp16 d; per 128-weight half h and
+//                       element 32 g + l of it: q = nibble (g >> 1) of ql[64 h + 32 (g & 1) + l] |
+//                       bits 2g..2g+1 of qh[32 h + l] << 4; w = d scales[8 h + 2 g + l / 16] (q - 32)
 //   Q8_K 292 B / 256 w: f32 d, i8 qs[256], i16 bsums[16] (sum of each 16 quants)
 // The quantizers restate ggml's published reference quantizers (quantize_row_*_ref), which are
 // what "quantized with ggml's own quantize_row_q4_0" in the benchmark configs means. This file
 // is compiled with -ffp-contract=off so its float operation order is the written one.
 #include "ggml.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <cstdio>
@@ -23,6 +29,10 @@ struct blk_q4_0 { ggml_fp16_t d; uint8_t qs[16]; };
 struct blk_q8_0 { ggml_fp16_t d; int8_t qs[32]; };
 struct blk_q4_K { ggml_fp16_t d; ggml_fp16_t dmin; uint8_t scales[12]; uint8_t qs[128]; };
 struct blk_q8_K { float d; int8_t qs[256]; int16_t bsums[16]; };
+struct blk_q5_K { ggml_fp16_t d; ggml_fp16_t dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; };
+struct blk_q6_K { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; ggml_fp16_t d; };
+static_assert(sizeof(blk_q5_K) == 176, "q5_K block");
+static_assert(sizeof(blk_q6_K) == 210, "q6_K block");
 static_assert(sizeof(blk_q4_0) == 18, "q4_0 block");
 static_assert(sizeof(blk_q8_0) == 34, "q8_0 block");
 static_assert(sizeof(blk_q4_K) == 144, "q4_K block");
@@ -111,6 +121,78 @@ float fit_scale_min(int n, int nmax, const float * x, const float * w, uint8_t *
     }
     *neg_min = -mn;
     return scale;
+}
+
+// The 8 sub-block scales and mins of a Q4_K / Q5_K block as 6-bit codes relative to their
+// maxima, packed into the 12 scale bytes (the layout q4k_scale_min reads).
+void pack_k4_scales(const float * scales, const float * mins, float max_scale, float max_min, uint8_t * dst) {
+    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    memset(dst, 0, 12);
+    for (int j = 0; j < QK_K / 32; ++j) {
+        const int ls = std::min(63, round_half_even(inv_scale * scales[j]));
+        const int lm = std::min(63, round_half_even(inv_min * mins[j]));
+        if (j < 4) {
+            dst[j] = (uint8_t) ls;
+            dst[j + 4] = (uint8_t) lm;
+        } else {
+            dst[j + 4] = (uint8_t) ((ls & 0xf) | ((lm & 0xf) << 4));
+            dst[j - 4] |= (uint8_t) ((ls >> 4) << 6);
+            dst[j] |= (uint8_t) ((lm >> 4) << 6);
+        }
+    }
+}
+
+// Symmetric fit of codes -nmax..nmax-1 to n values with squared weights x^2, searching the scale
+// over 18 rescalings (nmax + 0.1 is) of the largest-magnitude value (is = -9..9, 0 skipped): the
+// one with the largest sum(w x l)^2 / sum(w l^2) wins. Codes + nmax land in L. Restatement of
+// ggml's make_qx_quants (rmse_type 1, no importance weights).
+float fit_symmetric(int n, int nmax, const float * x, int8_t * L) {
+    int imax = 0;
+    for (int i = 1; i < n; ++i) if (fabsf(x[i]) > fabsf(x[imax])) imax = i;
+    const float vmax = x[imax];
+    if (fabsf(vmax) < 1e-15f) {
+        memset(L, 0, (size_t) n);
+        return 0.f;
+    }
+    auto code = [&](float iscale, int i) { return std::max(-nmax, std::min(nmax - 1, round_half_even(iscale * x[i]))); };
+    auto moments = [&](float iscale, float & sxl, float & sl2) {
+        sxl = 0; sl2 = 0;
+        for (int i = 0; i < n; ++i) {
+            const int l = code(iscale, i);
+            const float w = x[i] * x[i];
+            sxl += w * x[i] * l;
+            sl2 += w * l * l;
+        }
+    };
+    float iscale = -nmax / vmax;
+    float sxl, sl2;
+    moments(iscale, sxl, sl2);
+    for (int i = 0; i < n; ++i) L[i] = (int8_t) (code(iscale, i) + nmax);
+    float scale = sl2 ? sxl / sl2 : 0.0f;
+    float best = scale * sxl;
+    for (int is = -9; is <= 9; ++is) {
+        if (is == 0) continue;
+        iscale = -(nmax + 0.1f * is) / vmax;
+        moments(iscale, sxl, sl2);
+        if (sl2 > 0 && sxl * sxl > best * sl2) {
+            for (int i = 0; i < n; ++i) L[i] = (int8_t) (code(iscale, i) + nmax);
+            scale = sxl / sl2;
+            best = scale * sxl;
+        }
+    }
+    return scale;
+}
+
+// fifth bit j (0/1) of element l of a Q5_K block
+inline int q5k_hbit(const blk_q5_K & b, int j, int l) { return (b.qh[l] >> j) & 1; }
+
+// 6-bit code of element e (0..255) of a Q6_K block, before the -32
+inline int q6k_code(const blk_q6_K & b, int e) {
+    const int h = e / 128, g = (e % 128) / 32, l = e % 32;
+    const int lo = (b.ql[64 * h + 32 * (g & 1) + l] >> (4 * (g >> 1))) & 0xf;
+    const int hi = (b.qh[32 * h + l] >> (2 * g)) & 3;
+    return lo | (hi << 4);
 }
 
 } // namespace
@@ -244,6 +326,83 @@ void quantize_row_q4_K_ref(const float * x, void * vy, int64_t k) {
     }
 }
 
+// ggml's quantize_row_q5_K_ref: Q4_K's scheme with 5-bit codes (0..31) and a scale search of 16
+// rescalings starting at -0.5
+void quantize_row_q5_K_ref(const float * x, void * vy, int64_t k) {
+    blk_q5_K * y = (blk_q5_K *) vy;
+    uint8_t L[QK_K], Laux[32];
+    float weights[32], mins[QK_K / 32], scales[QK_K / 32];
+    for (int64_t i = 0; i < k / QK_K; i++) {
+        const float * xb = x + i * QK_K;
+        float max_scale = 0, max_min = 0;
+        for (int j = 0; j < QK_K / 32; ++j) {
+            const float * xs = xb + 32 * j;
+            float sum_x2 = 0;
+            for (int l = 0; l < 32; ++l) sum_x2 += xs[l] * xs[l];
+            const float av_x = sqrtf(sum_x2 / 32);
+            for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(xs[l]);
+            scales[j] = fit_scale_min(32, 31, xs, weights, L + 32 * j, &mins[j], Laux, -0.5f, 0.1f, 15);
+            max_scale = std::max(max_scale, scales[j]);
+            max_min = std::max(max_min, mins[j]);
+        }
+        pack_k4_scales(scales, mins, max_scale, max_min, y[i].scales);
+        y[i].d = ggml_fp32_to_fp16(max_scale / 63.f);
+        y[i].dmin = ggml_fp32_to_fp16(max_min / 63.f);
+        for (int j = 0; j < QK_K / 32; ++j) {
+            uint8_t sc, m;
+            q4k_scale_min(j, y[i].scales, &sc, &m);
+            const float d = ggml_fp16_to_fp32(y[i].d) * sc;
+            if (!d) continue;
+            const float dm = ggml_fp16_to_fp32(y[i].dmin) * m;
+            for (int l = 0; l < 32; ++l) L[32 * j + l] = (uint8_t) std::max(0, std::min(31, round_half_even((xb[32 * j + l] + dm) / d)));
+        }
+        memset(y[i].qh, 0, sizeof(y[i].qh));
+        for (int j = 0; j < QK_K / 32; ++j) {       // sub-block j: nibble j % 2 of qs[32 (j / 2) + l]
+            for (int l = 0; l < 32; ++l) {
+                const int q = L[32 * j + l];
+                uint8_t & dst = y[i].qs[32 * (j / 2) + l];
+                dst = (j & 1) ? (uint8_t) ((dst & 0x0f) | ((q & 15) << 4)) : (uint8_t) (q & 15);
+                y[i].qh[l] |= (uint8_t) ((q >> 4) << j);
+            }
+        }
+    }
+}
+
+// ggml's quantize_row_q6_K_ref: 16 sub-blocks of 16 fitted symmetrically (codes -32..31), the
+// sub-block scales as signed 8-bit codes of the largest-magnitude one (-> -128), the codes
+// re-rounded under the decoded scales
+void quantize_row_q6_K_ref(const float * x, void * vy, int64_t k) {
+    blk_q6_K * y = (blk_q6_K *) vy;
+    int8_t L[QK_K];
+    float scales[QK_K / 16];
+    for (int64_t i = 0; i < k / QK_K; i++) {
+        const float * xb = x + i * QK_K;
+        float max_scale = 0, max_abs = 0;
+        for (int j = 0; j < QK_K / 16; ++j) {
+            scales[j] = fit_symmetric(16, 32, xb + 16 * j, L + 16 * j);
+            if (fabsf(scales[j]) > max_abs) {
+                max_abs = fabsf(scales[j]);
+                max_scale = scales[j];
+            }
+        }
+        memset(&y[i], 0, sizeof(blk_q6_K));
+        if (max_abs < 1e-15f) continue;
+        const float iscale = -128.f / max_scale;
+        y[i].d = ggml_fp32_to_fp16(1 / iscale);
+        for (int j = 0; j < QK_K / 16; ++j) y[i].scales[j] = (int8_t) std::min(127, round_half_even(iscale * scales[j]));
+        for (int j = 0; j < QK_K / 16; ++j) {
+            const float d = ggml_fp16_to_fp32(y[i].d) * y[i].scales[j];
+            if (!d) continue;
+            for (int l = 0; l < 16; ++l) L[16 * j + l] = (int8_t) (std::max(-32, std::min(31, round_half_even(xb[16 * j + l] / d))) + 32);
+        }
+        for (int e = 0; e < QK_K; ++e) {            // the code of element e into its nibble and bit pair
+            const int h = e / 128, g = (e % 128) / 32, l = e % 32, q = L[e];
+            y[i].ql[64 * h + 32 * (g & 1) + l] |= (uint8_t) ((q & 15) << (4 * (g >> 1)));
+            y[i].qh[32 * h + l] |= (uint8_t) ((q >> 4) << (2 * g));
+        }
+    }
+}
+
 void dequantize_row_q4_0(const void * vx, float * y, int64_t k) {
     const blk_q4_0 * x = (const blk_q4_0 *) vx;
     for (int64_t i = 0; i < k / 32; i++) {
@@ -286,6 +445,34 @@ void dequantize_row_q4_K(const void * vx, float * y, int64_t k) {
     }
 }
 
+void dequantize_row_q5_K(const void * vx, float * y, int64_t k) {
+    const blk_q5_K * x = (const blk_q5_K *) vx;
+    for (int64_t i = 0; i < k / QK_K; i++) {
+        const float d = ggml_fp16_to_fp32(x[i].d), dmin = ggml_fp16_to_fp32(x[i].dmin);
+        for (int j = 0; j < QK_K / 32; ++j) {
+            uint8_t sc, m;
+            q4k_scale_min(j, x[i].scales, &sc, &m);
+            const float dj = d * sc, mj = dmin * m;
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t b = x[i].qs[32 * (j / 2) + l];
+                const int q = ((j & 1) ? (b >> 4) : (b & 0xf)) + 16 * q5k_hbit(x[i], j, l);
+                *y++ = dj * q - mj;
+            }
+        }
+    }
+}
+
+void dequantize_row_q6_K(const void * vx, float * y, int64_t k) {
+    const blk_q6_K * x = (const blk_q6_K *) vx;
+    for (int64_t i = 0; i < k / QK_K; i++) {
+        const float d = ggml_fp16_to_fp32(x[i].d);
+        for (int e = 0; e < QK_K; ++e) {
+            const int h = e / 128, g = (e % 128) / 32, l = e % 32;
+            *y++ = d * x[i].scales[8 * h + 2 * g + l / 16] * (q6k_code(x[i], e) - 32);
+        }
+    }
+}
+
 bool ggml_dequantize_row(enum ggml_type type, const void * x, float * y, int64_t k) {
     switch (type) {
         case GGML_TYPE_F32: memcpy(y, x, (size_t) k * 4); return true;
@@ -294,6 +481,8 @@ bool ggml_dequantize_row(enum ggml_type type, const void * x, float * y, int64_t
         case GGML_TYPE_Q4_0: dequantize_row_q4_0(x, y, k); return true;
         case GGML_TYPE_Q8_0: dequantize_row_q8_0(x, y, k); return true;
         case GGML_TYPE_Q4_K: dequantize_row_q4_K(x, y, k); return true;
+        case GGML_TYPE_Q5_K: dequantize_row_q5_K(x, y, k); return true;
+        case GGML_TYPE_Q6_K: dequantize_row_q6_K(x, y, k); return true;
         default: return false;
     }
 }
@@ -315,6 +504,8 @@ size_t ggml_quantize_chunk(enum ggml_type type, const float * src, void * dst, i
             case GGML_TYPE_Q4_0: quantize_row_q4_0_ref(xr, yr, n_per_row); break;
             case GGML_TYPE_Q8_0: quantize_row_q8_0_ref(xr, yr, n_per_row); break;
             case GGML_TYPE_Q4_K: quantize_row_q4_K_ref(xr, yr, n_per_row); break;
+            case GGML_TYPE_Q5_K: quantize_row_q5_K_ref(xr, yr, n_per_row); break;
+            case GGML_TYPE_Q6_K: quantize_row_q6_K_ref(xr, yr, n_per_row); break;
             case GGML_TYPE_Q8_K: quantize_row_q8_K_ref(xr, yr, n_per_row); break;
             case GGML_TYPE_F16: ggml_fp32_to_fp16_row(xr, (ggml_fp16_t *) yr, n_per_row); break;
             case GGML_TYPE_F32: memcpy(yr, xr, (size_t) n_per_row * 4); break;

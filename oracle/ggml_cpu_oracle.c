@@ -95,11 +95,15 @@ typedef struct { uint16_t d; uint8_t qs[16]; } bq4_0;
 typedef struct { uint16_t d; int8_t qs[32]; } bq8_0;
 typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[12]; uint8_t qs[128]; } bq4_K;
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } bq8_K;
+typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } bq5_K;
+typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } bq6_K;
 
 _Static_assert(sizeof(bq4_0) == 18, "q4_0");
 _Static_assert(sizeof(bq8_0) == 34, "q8_0");
 _Static_assert(sizeof(bq4_K) == 144, "q4_K");
 _Static_assert(sizeof(bq8_K) == 292, "q8_K");
+_Static_assert(sizeof(bq5_K) == 176, "q5_K");
+_Static_assert(sizeof(bq6_K) == 210, "q6_K");
 
 /* ggml's nearest_int: round half to even through the float mantissa, |v| < 2^22 */
 static inline int nearest_int(float v) {
@@ -314,6 +318,172 @@ void oracle_quantize_q4_K(const float * x, void * vy, int64_t k) {
     }
 }
 
+/* The 6-bit scale and min codes of eight sub-blocks packed into 12 bytes (the layout
+   scale_min_k4 reads back), from the float scales and mins and their maxima. */
+static void pack_scale_min_k4(const float * scales, const float * mins, float max_scale, float max_min, uint8_t * out) {
+    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    memset(out, 0, 12);
+    for (int j = 0; j < 8; ++j) {
+        uint8_t ls = (uint8_t) nearest_int(inv_scale * scales[j]);
+        uint8_t lm = (uint8_t) nearest_int(inv_min * mins[j]);
+        ls = ls < 63 ? ls : 63;
+        lm = lm < 63 ? lm : 63;
+        if (j < 4) {
+            out[j] = ls;
+            out[j + 4] = lm;
+        } else {
+            out[j + 4] = (uint8_t) ((ls & 0xF) | ((lm & 0xF) << 4));
+            out[j - 4] |= (uint8_t) ((ls >> 4) << 6);
+            out[j - 0] |= (uint8_t) ((lm >> 4) << 6);
+        }
+    }
+}
+
+/* ggml's quantize_row_q5_K_ref: as Q4_K with 5-bit codes (0..31), the grid search of each
+   sub-block over 16 rescalings starting at -0.5; the fifth bit of element l of sub-block j goes
+   to bit j of qh[l]. */
+void oracle_quantize_q5_K(const float * x, void * vy, int64_t k) {
+    bq5_K * y = (bq5_K *) vy;
+    uint8_t L[256], Laux[32];
+    float weights[32], mins[8], scales[8];
+    for (int64_t i = 0; i < k / 256; i++) {
+        const float * xb = x + i * 256;
+        float max_scale = 0, max_min = 0;
+        for (int j = 0; j < 8; ++j) {
+            float sum_x2 = 0;
+            for (int l = 0; l < 32; ++l) sum_x2 += xb[32 * j + l] * xb[32 * j + l];
+            const float av_x = sqrtf(sum_x2 / 32);
+            for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(xb[32 * j + l]);
+            scales[j] = make_qkx2_quants(32, 31, xb + 32 * j, weights, L + 32 * j, &mins[j], Laux, -0.5f, 0.1f, 15);
+            if (scales[j] > max_scale) max_scale = scales[j];
+            if (mins[j] > max_min) max_min = mins[j];
+        }
+        pack_scale_min_k4(scales, mins, max_scale, max_min, y[i].scales);
+        y[i].d = oracle_fp32_to_fp16(max_scale / 63.f);
+        y[i].dmin = oracle_fp32_to_fp16(max_min / 63.f);
+        for (int j = 0; j < 8; ++j) {
+            uint8_t sc, m;
+            scale_min_k4(j, y[i].scales, &sc, &m);
+            const float d = F16(y[i].d) * sc;
+            if (!d) continue;
+            const float dm = F16(y[i].dmin) * m;
+            for (int ii = 0; ii < 32; ++ii) {
+                int l = nearest_int((xb[32 * j + ii] + dm) / d);
+                L[32 * j + ii] = (uint8_t) (l < 0 ? 0 : (l > 31 ? 31 : l));
+            }
+        }
+        memset(y[i].qh, 0, 32);
+        for (int j = 0; j < 4; ++j) {                   /* sub-blocks 2j (low nibbles), 2j + 1 (high) */
+            for (int l = 0; l < 32; ++l) {
+                const int a = L[64 * j + l], b = L[64 * j + 32 + l];
+                y[i].qs[32 * j + l] = (uint8_t) ((a & 15) | ((b & 15) << 4));
+                y[i].qh[l] |= (uint8_t) (((a >> 4) << (2 * j)) | ((b >> 4) << (2 * j + 1)));
+            }
+        }
+    }
+}
+
+/* ggml's make_qx_quants with rmse_type 1 (weights x^2): symmetric codes -nmax..nmax-1 around the
+   element of largest magnitude, then 18 rescalings (nmax + 0.1 is) / max, is = -9..9, kept when
+   they raise sum(w x l)^2 / sum(w l^2). Returns the scale; L gets codes + nmax. */
+static float make_qx_quants(int n, int nmax, const float * x, int8_t * L) {
+    float max = 0, amax = 0;
+    for (int i = 0; i < n; ++i) {
+        const float ax = fabsf(x[i]);
+        if (ax > amax) { amax = ax; max = x[i]; }
+    }
+    if (amax < 1e-15f) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        return 0.f;
+    }
+    float iscale = -nmax / max;
+    float sumlx = 0, suml2 = 0;
+    for (int i = 0; i < n; ++i) {
+        int l = nearest_int(iscale * x[i]);
+        l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+        L[i] = (int8_t) (l + nmax);
+        const float w = x[i] * x[i];
+        sumlx += w * x[i] * l;
+        suml2 += w * l * l;
+    }
+    float scale = suml2 ? sumlx / suml2 : 0.0f;
+    float best = scale * sumlx;
+    if (g_planted & 256) return scale;
+    for (int is = -9; is <= 9; ++is) {
+        if (is == 0) continue;
+        iscale = -(nmax + 0.1f * is) / max;
+        sumlx = suml2 = 0;
+        for (int i = 0; i < n; ++i) {
+            int l = nearest_int(iscale * x[i]);
+            l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+            const float w = x[i] * x[i];
+            sumlx += w * x[i] * l;
+            suml2 += w * l * l;
+        }
+        if (suml2 > 0 && sumlx * sumlx > best * suml2) {
+            for (int i = 0; i < n; ++i) {
+                int l = nearest_int(iscale * x[i]);
+                L[i] = (int8_t) (nmax + (l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l)));
+            }
+            scale = sumlx / suml2;
+            best = scale * sumlx;
+        }
+    }
+    return scale;
+}
+
+float oracle_make_qx_quants(int n, int nmax, const float * x, int8_t * L) {
+    return n > 256 ? -1.f : make_qx_quants(n, nmax, x, L);
+}
+
+/* ggml's quantize_row_q6_K_ref: 16 sub-blocks of 16 with signed 8-bit scales (the largest-magnitude
+   sub-block scale maps to -128), 6-bit codes (-32..31, stored + 32) re-rounded under the decoded
+   scales; element 32 g + l of each 128-half in the low (g < 2) or high nibble of ql, bits 2g, 2g+1
+   of qh[l]. */
+void oracle_quantize_q6_K(const float * x, void * vy, int64_t k) {
+    bq6_K * y = (bq6_K *) vy;
+    int8_t L[256];
+    float scales[16];
+    for (int64_t i = 0; i < k / 256; i++) {
+        const float * xb = x + i * 256;
+        float max_scale = 0, max_abs_scale = 0;
+        for (int ib = 0; ib < 16; ++ib) {
+            const float sc = make_qx_quants(16, 32, xb + 16 * ib, L + 16 * ib);
+            scales[ib] = sc;
+            if (fabsf(sc) > max_abs_scale) { max_abs_scale = fabsf(sc); max_scale = sc; }
+        }
+        memset(&y[i], 0, sizeof(bq6_K));
+        if (max_abs_scale < 1e-15f) continue;
+        const float iscale = -128.f / max_scale;
+        y[i].d = oracle_fp32_to_fp16(1 / iscale);
+        for (int ib = 0; ib < 16; ++ib) {
+            const int v = nearest_int(iscale * scales[ib]);
+            y[i].scales[ib] = (int8_t) (v < 127 ? v : 127);
+        }
+        for (int j = 0; j < 16; ++j) {
+            const float d = F16(y[i].d) * y[i].scales[j];
+            if (!d) continue;
+            for (int ii = 0; ii < 16; ++ii) {
+                int l = nearest_int(xb[16 * j + ii] / d);
+                l = l < -32 ? -32 : (l > 31 ? 31 : l);
+                L[16 * j + ii] = (int8_t) (l + 32);
+            }
+        }
+        for (int h = 0; h < 2; ++h) {
+            const int8_t * Lh = L + 128 * h;
+            uint8_t * ql = y[i].ql + 64 * h;
+            uint8_t * qh = y[i].qh + 32 * h;
+            for (int l = 0; l < 32; ++l) {
+                const int q0 = Lh[l], q1 = Lh[l + 32], q2 = Lh[l + 64], q3 = Lh[l + 96];
+                ql[l] = (uint8_t) ((q0 & 15) | ((q2 & 15) << 4));
+                ql[l + 32] = (uint8_t) ((q1 & 15) | ((q3 & 15) << 4));
+                qh[l] = (uint8_t) ((q0 >> 4) | ((q1 >> 4) << 2) | ((q2 >> 4) << 4) | ((q3 >> 4) << 6));
+            }
+        }
+    }
+}
+
 /* moe_stream/dequant.c:143-171 (dequant_q4_K), :237-244 (dequant_q8_0); Q4_0 by its layout */
 int oracle_dequantize(int type, const void * vx, float * y, int64_t k) {
     switch (type) {
@@ -367,6 +537,47 @@ int oracle_dequantize(int type, const void * vx, float * y, int64_t k) {
                     q += 32;
                     is += 2;
                 }
+            }
+            return 1;
+        }
+        case GGML_TYPE_Q5_K: {      /* moe_stream/dequant.c:135-168 */
+            const bq5_K * x = (const bq5_K *) vx;
+            for (int64_t i = 0; i < k / 256; i++) {
+                const float d = F16(x[i].d), dmin = F16(x[i].dmin);
+                for (int j = 0; j < 4; ++j) {
+                    uint8_t sa, ma, sb, mb;
+                    scale_min_k4(2 * j, x[i].scales, &sa, &ma);
+                    scale_min_k4(2 * j + 1, x[i].scales, &sb, &mb);
+                    const float da = d * sa, mna = dmin * ma, db = d * sb, mnb = dmin * mb;
+                    for (int l = 0; l < 32; ++l) {
+                        const int hi = (x[i].qh[l] >> (2 * j)) & 1;
+                        *y++ = da * (float) ((x[i].qs[32 * j + l] & 0x0F) + 16 * hi) - mna;
+                    }
+                    for (int l = 0; l < 32; ++l) {
+                        const int hi = (x[i].qh[l] >> (2 * j + 1)) & 1;
+                        *y++ = db * (float) ((x[i].qs[32 * j + l] >> 4) + 16 * hi) - mnb;
+                    }
+                }
+            }
+            return 1;
+        }
+        case GGML_TYPE_Q6_K: {      /* moe_stream/dequant.c:170-197 */
+            const bq6_K * x = (const bq6_K *) vx;
+            for (int64_t i = 0; i < k / 256; i++) {
+                const float d = F16(x[i].d);
+                for (int h = 0; h < 2; ++h) {
+                    const uint8_t * ql = x[i].ql + 64 * h;
+                    const uint8_t * qh = x[i].qh + 32 * h;
+                    const int8_t * sc = x[i].scales + 8 * h;
+                    for (int g = 0; g < 4; ++g) {       /* element 32 g + l of the half */
+                        for (int l = 0; l < 32; ++l) {
+                            const int lo = (ql[l + 32 * (g & 1)] >> (4 * (g >> 1))) & 0xF;
+                            const int q = (lo | (((qh[l] >> (2 * g)) & 3) << 4)) - 32;
+                            y[128 * h + 32 * g + l] = d * (float) sc[2 * g + l / 16] * (float) q;
+                        }
+                    }
+                }
+                y += 256;
             }
             return 1;
         }
@@ -488,6 +699,65 @@ float oracle_vec_dot_q4_K_q8_K(int64_t n, const void * vx, const void * vy) {
     return sumf;
 }
 
+/* ggml_vec_dot_q5_K_q8_K_generic: the Q4_K kernel with the fifth bit of each code */
+float oracle_vec_dot_q5_K_q8_K(int64_t n, const void * vx, const void * vy) {
+    const bq5_K * x = (const bq5_K *) vx;
+    const bq8_K * y = (const bq8_K *) vy;
+    float sums[8] = { 0 };
+    float sumf = 0;
+    for (int64_t i = 0; i < n / 256; ++i) {
+        int32_t aux32[8] = { 0 };
+        int sumi_min = 0;
+        uint8_t sc[8], mn[8];
+        for (int j = 0; j < 8; j++) scale_min_k4(j, x[i].scales, &sc[j], &mn[j]);
+        for (int j = 0; j < 16; ++j) sumi_min += y[i].bsums[j] * mn[j / 2];
+        for (int j = 0; j < 8; ++j) {
+            const uint8_t * q4 = x[i].qs + 32 * (j / 2);
+            const int8_t * q8 = y[i].qs + 32 * j;
+            for (int l = 0; l < 32; ++l) {
+                const int a = ((j & 1) ? (q4[l] >> 4) : (q4[l] & 0xF)) + 16 * ((x[i].qh[l] >> j) & 1);
+                aux32[l & 7] += (int32_t) sc[j] * (int32_t) (int16_t) (q8[l] * a);
+            }
+        }
+        const float d = F16(x[i].d) * y[i].d;
+        for (int l = 0; l < 8; ++l) sums[l] += d * aux32[l];
+        const float dmin = F16(x[i].dmin) * y[i].d;
+        sumf -= dmin * sumi_min;
+    }
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+/* ggml_vec_dot_q6_K_q8_K_generic: 16 sub-blocks of 16 with signed scales, codes - 32, no mins */
+float oracle_vec_dot_q6_K_q8_K(int64_t n, const void * vx, const void * vy) {
+    const bq6_K * x = (const bq6_K *) vx;
+    const bq8_K * y = (const bq8_K *) vy;
+    float sums[8] = { 0 };
+    float sumf = 0;
+    for (int64_t i = 0; i < n / 256; ++i) {
+        int8_t a[256];
+        for (int h = 0; h < 2; ++h) {
+            const uint8_t * ql = x[i].ql + 64 * h;
+            const uint8_t * qh = x[i].qh + 32 * h;
+            for (int g = 0; g < 4; ++g) {
+                for (int l = 0; l < 32; ++l) {
+                    const int lo = (ql[l + 32 * (g & 1)] >> (4 * (g >> 1))) & 0xF;
+                    a[128 * h + 32 * g + l] = (int8_t) ((lo | (((qh[l] >> (2 * g)) & 3) << 4)) - 32);
+                }
+            }
+        }
+        int32_t aux32[8] = { 0 };
+        for (int j = 0; j < 16; ++j) {
+            const int scale = x[i].scales[j];
+            for (int e = 16 * j; e < 16 * j + 16; ++e) aux32[e & 7] += scale * (int32_t) (int16_t) (y[i].qs[e] * a[e]);
+        }
+        const float d = F16(x[i].d) * y[i].d;
+        for (int l = 0; l < 8; ++l) sums[l] += d * aux32[l];
+    }
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
 static float vec_dot_f16(int64_t n, const uint16_t * x, const uint16_t * y) {
     ggml_float sumf = 0.0;
     for (int64_t i = 0; i < n; ++i) sumf += (ggml_float) (F16(x[i]) * F16(y[i]));
@@ -506,7 +776,7 @@ static float vec_dot_f32(int64_t n, const float * x, const float * y) {
 static int dot_type_of(int wtype) {
     switch (wtype) {
         case GGML_TYPE_Q4_0: case GGML_TYPE_Q8_0: return GGML_TYPE_Q8_0;
-        case GGML_TYPE_Q4_K: return GGML_TYPE_Q8_K;
+        case GGML_TYPE_Q4_K: case GGML_TYPE_Q5_K: case GGML_TYPE_Q6_K: return GGML_TYPE_Q8_K;
         case GGML_TYPE_F16: return GGML_TYPE_F16;
         case GGML_TYPE_BF16: return GGML_TYPE_BF16;
         case GGML_TYPE_F32: return GGML_TYPE_F32;
@@ -544,6 +814,8 @@ static float row_dot(int wtype, const void * w, const void * xd, int64_t k) {
         case GGML_TYPE_Q4_0: return oracle_vec_dot_q4_0_q8_0(k, w, xd);
         case GGML_TYPE_Q8_0: return oracle_vec_dot_q8_0_q8_0(k, w, xd);
         case GGML_TYPE_Q4_K: return oracle_vec_dot_q4_K_q8_K(k, w, xd);
+        case GGML_TYPE_Q5_K: return oracle_vec_dot_q5_K_q8_K(k, w, xd);
+        case GGML_TYPE_Q6_K: return oracle_vec_dot_q6_K_q8_K(k, w, xd);
         case GGML_TYPE_F16: return vec_dot_f16(k, (const uint16_t *) w, (const uint16_t *) xd);
         case GGML_TYPE_BF16: {
             ggml_float s = 0.0;
@@ -561,6 +833,8 @@ static size_t weight_row_size(int wtype, int64_t k) {
         case GGML_TYPE_Q4_0: return (size_t) (k / 32) * 18;
         case GGML_TYPE_Q8_0: return (size_t) (k / 32) * 34;
         case GGML_TYPE_Q4_K: return (size_t) (k / 256) * 144;
+        case GGML_TYPE_Q5_K: return (size_t) (k / 256) * 176;
+        case GGML_TYPE_Q6_K: return (size_t) (k / 256) * 210;
         case GGML_TYPE_F16: case GGML_TYPE_BF16: return (size_t) k * 2;
         default: return (size_t) k * 4;
     }

@@ -21,6 +21,10 @@
  *                              exactly where x/d >= 7.5; a planted truncation fails
  *   Q8_0/Q8_K quantizers       error bounds (round to nearest within d/2), zero and constant
  *                              blocks, Q8_K block sums; the product's quantizers byte-identical
+ *   Q5_K/Q6_K decode           reference dequant_row golden vectors (dequant.c:135-197), bit-exact
+ *   Q5_K/Q6_K quantizers, dots tests/test_kquants.py: codes within half a step under the decoded
+ *                              scales, largest scale codes, make_qx_quants against a float64
+ *                              statement of its search; dots against fp64 brute force
  *   Q4_K quantizer             tests/test_oracle_pins.py: make_qkx2_quants against a float64
  *                              statement of ggml's search (same pick where float32 rounding cannot
  *                              decide it), scale/min codes of the float64 optimum under weights
@@ -70,19 +74,28 @@ void oracle_quantize_q4_0(const float * x, void * y, int64_t k);
 void oracle_quantize_q8_0(const float * x, void * y, int64_t k);
 void oracle_quantize_q4_K(const float * x, void * y, int64_t k);
 void oracle_quantize_q8_K(const float * x, void * y, int64_t k);
+void oracle_quantize_q5_K(const float * x, void * y, int64_t k);
+void oracle_quantize_q6_K(const float * x, void * y, int64_t k);
 
 /* ggml's make_qkx2_quants (the per-sub-block weighted grid search inside the Q4_K quantizer):
    n <= 256 values with weights, codes 0..nmax into L, returns the scale and writes -min */
 float oracle_make_qkx2_quants(int n, int nmax, const float * x, const float * weights, uint8_t * L, float * the_min,
                               float rmin, float rdelta, int nstep);
 
-/* row decoders (type = ggml type id: 0 f32, 1 f16, 2 q4_0, 8 q8_0, 12 q4_K, 30 bf16); 0 on unknown type */
+/* ggml's make_qx_quants with rmse_type 1 (the Q6_K sub-block search): n <= 256 values, codes
+   -nmax..nmax-1 stored + nmax in L; returns the scale */
+float oracle_make_qx_quants(int n, int nmax, const float * x, int8_t * L);
+
+/* row decoders (type = ggml type id: 0 f32, 1 f16, 2 q4_0, 8 q8_0, 12 q4_K, 13 q5_K, 14 q6_K,
+   30 bf16); 0 on unknown type */
 int oracle_dequantize(int type, const void * x, float * y, int64_t k);
 
 /* block dot products with the activation already in the weight's dot type */
 float oracle_vec_dot_q4_0_q8_0(int64_t n, const void * x, const void * y);
 float oracle_vec_dot_q8_0_q8_0(int64_t n, const void * x, const void * y);
 float oracle_vec_dot_q4_K_q8_K(int64_t n, const void * x, const void * y);
+float oracle_vec_dot_q5_K_q8_K(int64_t n, const void * x, const void * y);
+float oracle_vec_dot_q6_K_q8_K(int64_t n, const void * x, const void * y);
 
 /* y[r] = W[r] . x for nrows rows of a weight of type `type`, with ggml-cpu's activation
    quantization (Q4_0/Q8_0 -> Q8_0, Q4_K -> Q8_K, F16 -> F16, F32 exact) */
@@ -108,7 +121,8 @@ void oracle_set_block_sum_order(int mode);
    bit 8 = Q4_0 codes truncated (x/d + 8) instead of rounded (+ 8.5); bit 16 = make_qkx2_quants
    without its scale search; bit 32 = Q4_K sub-block weights 1 instead of av_x + |x|; bit 64 = the
    YaRN ramp's extrapolated and interpolated angles exchanged; bit 128 = rope freq_factors
-   multiplying the angle instead of dividing it (tests/test_oracle_pins.py) */
+   multiplying the angle instead of dividing it; bit 256 = make_qx_quants without its rescaling
+   search (tests/test_oracle_pins.py, tests/test_kquants.py) */
 void oracle_set_planted(int bits);
 
 /* sample() (model.cpp:1675-1728) on n logits with the window recent[0..n_recent) and the

@@ -53,18 +53,22 @@ def oracle():
         o.oracle_fp16_to_fp32.argtypes = [C.c_uint16]
         o.oracle_fp32_to_fp16.restype = C.c_uint16
         o.oracle_fp32_to_fp16.argtypes = [C.c_float]
-        for n in ("oracle_quantize_q4_0", "oracle_quantize_q8_0", "oracle_quantize_q4_K", "oracle_quantize_q8_K"):
+        for n in ("oracle_quantize_q4_0", "oracle_quantize_q8_0", "oracle_quantize_q4_K", "oracle_quantize_q8_K",
+                  "oracle_quantize_q5_K", "oracle_quantize_q6_K"):
             getattr(o, n).restype = None
             getattr(o, n).argtypes = [vp, vp, i64]
         o.oracle_dequantize.restype = C.c_int
         o.oracle_dequantize.argtypes = [C.c_int, vp, vp, i64]
-        for n in ("oracle_vec_dot_q4_0_q8_0", "oracle_vec_dot_q8_0_q8_0", "oracle_vec_dot_q4_K_q8_K"):
+        for n in ("oracle_vec_dot_q4_0_q8_0", "oracle_vec_dot_q8_0_q8_0", "oracle_vec_dot_q4_K_q8_K",
+                  "oracle_vec_dot_q5_K_q8_K", "oracle_vec_dot_q6_K_q8_K"):
             getattr(o, n).restype = C.c_float
             getattr(o, n).argtypes = [i64, vp, vp]
         o.oracle_gemv.restype = None
         o.oracle_gemv.argtypes = [C.c_int, vp, i64, i64, vp, vp, C.c_int]
         o.oracle_rope.restype = None
         o.oracle_rope.argtypes = [vp, vp, i64, C.c_int, C.c_int, C.c_int32] + [C.c_float] * 6 + [C.c_int, vp]
+        o.oracle_make_qx_quants.restype = C.c_float
+        o.oracle_make_qx_quants.argtypes = [C.c_int, C.c_int, vp, vp]
         o.oracle_make_qkx2_quants.restype = C.c_float
         o.oracle_make_qkx2_quants.argtypes = [C.c_int, C.c_int, vp, vp, vp, vp, C.c_float, C.c_float, C.c_int]
         o.oracle_moe_route.restype = None
@@ -255,7 +259,8 @@ def ptr(a: np.ndarray):
 
 
 # ---- quantization helpers (through the oracle) ----
-BLOCK = {gl.Q4_0: (32, 18), gl.Q8_0: (32, 34), gl.Q4_K: (256, 144), gl.Q8_K: (256, 292)}
+BLOCK = {gl.Q4_0: (32, 18), gl.Q8_0: (32, 34), gl.Q4_K: (256, 144), gl.Q5_K: (256, 176), gl.Q6_K: (256, 210),
+         gl.Q8_K: (256, 292)}
 
 
 def quantize(x: np.ndarray, qtype: int, impl: str = "oracle") -> np.ndarray:
@@ -265,7 +270,7 @@ def quantize(x: np.ndarray, qtype: int, impl: str = "oracle") -> np.ndarray:
     out = np.zeros(x.size // qk * bs, dtype=np.uint8)
     if impl == "oracle":
         fn = {gl.Q4_0: "oracle_quantize_q4_0", gl.Q8_0: "oracle_quantize_q8_0", gl.Q4_K: "oracle_quantize_q4_K",
-              gl.Q8_K: "oracle_quantize_q8_K"}[qtype]
+              gl.Q5_K: "oracle_quantize_q5_K", gl.Q6_K: "oracle_quantize_q6_K", gl.Q8_K: "oracle_quantize_q8_K"}[qtype]
         getattr(oracle(), fn)(ptr(x), ptr(out), x.size)
     else:
         n_per_row = x.shape[-1] if x.ndim > 1 else x.size

@@ -9,6 +9,8 @@ the product's own decoders) against them without needing the reference at run ti
 
 Fixtures:
   dequant_ref.npz   Q4_K and Q8_0 blocks -> dequant_row (dequant.c:199-251), incl. edge blocks
+  kquant_ref.npz    Q5_K and Q6_K blocks -> dequant_row (dequant.c:135-197, 208-251): arbitrary
+                    bytes with edge scales, and blocks of the product's quantizers
   scalar_ref.npz    sc_rmsnorm, sc_softmax, sc_swiglu, sc_rope (NEOX, tables as qwen_model.c:346-355)
                     and sc_matmul on Q4_K rows with f32 activations (compute_backend.c:14-96)
 
@@ -26,7 +28,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libmoe_ref.so")
 sys.path.insert(0, os.path.dirname(HERE))
 
-T_F32, T_F16, T_Q4_K, T_Q8_0 = 0, 1, 12, 8
+T_F32, T_F16, T_Q4_K, T_Q5_K, T_Q6_K, T_Q8_0 = 0, 1, 12, 13, 14, 8
 
 fp = C.POINTER(C.c_float)
 MATMUL = C.CFUNCTYPE(None, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, fp, fp)
@@ -84,6 +86,52 @@ def q4k_blocks(r):
     blocks.append(b)
     from_quant = product_quantize((r.standard_normal(256 * 7) * 0.05).astype(np.float32), 12)
     return np.concatenate(blocks + [from_quant])
+
+
+def q5k_blocks(r):
+    """Arbitrary Q5_K blocks (every fifth bit pattern through random qh bytes; d, dmin of both
+    signs, zero, subnormal; all 6-bit scales and mins at 63), then quantizer-made blocks."""
+    blocks = []
+    for d, dm in zip([0.01, -0.02, 0.0, 6e-8, 1.0, 2e-3], [0.003, 0.0, -0.01, 6e-8, 0.25, 0.0]):
+        b = r.integers(0, 256, 176, dtype=np.uint8)
+        b[0:2] = fp16_bits(d).view(np.uint8)
+        b[2:4] = fp16_bits(dm).view(np.uint8)
+        blocks.append(b)
+    b = r.integers(0, 256, 176, dtype=np.uint8)
+    b[4:16] = 0xFF
+    b[16:48] = 0xFF                           # every fifth bit set
+    blocks.append(b)
+    x = (r.standard_normal(256 * 5) * 0.05).astype(np.float32)
+    x[256:512] += 0.03                        # a block with an offset
+    return np.concatenate(blocks + [product_quantize(x, T_Q5_K)])
+
+
+def q6k_blocks(r):
+    """Arbitrary Q6_K blocks (random ql/qh/scales bytes: signed scales of both signs incl. -128
+    and 127; d of both signs, zero, subnormal), then quantizer-made blocks."""
+    blocks = []
+    for d in [0.01, -0.02, 0.0, 6e-8, 1.0, 3e-5]:
+        b = r.integers(0, 256, 210, dtype=np.uint8)
+        b[208:210] = fp16_bits(d).view(np.uint8)
+        blocks.append(b)
+    b = r.integers(0, 256, 210, dtype=np.uint8)
+    b[192:208] = np.array([-128, 127] * 8, dtype=np.int8).view(np.uint8)
+    b[128:192] = 0xFF                         # every code's high bits set
+    b[208:210] = fp16_bits(0.125).view(np.uint8)
+    blocks.append(b)
+    x = (r.standard_normal(256 * 5) * 0.05).astype(np.float32)
+    x[:256] *= 20                             # a block of larger range
+    return np.concatenate(blocks + [product_quantize(x, T_Q6_K)])
+
+
+def kquant_fixture(lib):
+    r = np.random.default_rng(20261202)
+    q5 = q5k_blocks(r)
+    q6 = q6k_blocks(r)
+    n5, n6 = q5.size // 176 * 256, q6.size // 210 * 256
+    np.savez(os.path.join(HERE, "kquant_ref.npz"),
+             q5k_in=q5, q5k_out=dequant(lib, T_Q5_K, q5, n5),
+             q6k_in=q6, q6k_out=dequant(lib, T_Q6_K, q6, n6))
 
 
 def q8_0_blocks(r):
@@ -176,7 +224,8 @@ def main():
              swi_gate=gate, swi_up=up, swi_out=swi,
              rope_hd=np.int32(hd), rope_base=np.float32(base), rope_pos=pos, rope_x=rv, rope_out=ro,
              mm_w=W, mm_k=np.int32(K), mm_n=np.int32(N), mm_x=mx, mm_y=my)
-    for f in ("dequant_ref.npz", "scalar_ref.npz"):
+    kquant_fixture(lib)
+    for f in ("dequant_ref.npz", "scalar_ref.npz", "kquant_ref.npz"):
         print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")
 
 
