@@ -85,7 +85,7 @@ class gl_synth_params(C.Structure):
         ("wtype", C.c_int32), ("embd_type", C.c_int32), ("output_type", C.c_int32), ("tied_output", C.c_int32),
         ("w_std", C.c_float), ("norm_std", C.c_float),
         ("seed", C.c_uint64), ("n_threads", C.c_int32), ("share_experts", C.c_int32),
-        ("rope_scaling_orig_ctx", C.c_int32), ("rope_attn_factor", C.c_float),
+        ("rope_scaling_orig_ctx", C.c_int32), ("rope_attn_factor", C.c_float), ("kquant_mix", C.c_int32),
     ]
 
 
@@ -322,7 +322,7 @@ def synth_model(path: str, *, arch: str, n_embd: int, n_layer: int, n_head: int,
                 wtype: int = Q4_0, embd_type: int | None = None, output_type: int | None = None, tied: bool = False,
                 w_std: float = 0.02, norm_std: float = 0.01, seed: int = 1, n_threads: int = 0, n_expert: int = 0,
                 n_expert_used: int = 0, n_ff_exp: int = 0, share_experts: bool = False,
-                rope_scaling_orig_ctx: int = 0, rope_attn_factor: float = 1.0) -> None:
+                rope_scaling_orig_ctx: int = 0, rope_attn_factor: float = 1.0, kquant_mix: int = 0) -> None:
     """Write a seeded synthetic GGUF model (weights ~ N(0, w_std), quantized by the ggml reference quantizers)."""
     p = gl_synth_params()
     p.arch = arch.encode()
@@ -337,6 +337,7 @@ def synth_model(path: str, *, arch: str, n_embd: int, n_layer: int, n_head: int,
     p.w_std, p.norm_std, p.seed, p.n_threads = w_std, norm_std, seed, n_threads
     p.share_experts = 1 if share_experts else 0
     p.rope_scaling_orig_ctx, p.rope_attn_factor = rope_scaling_orig_ctx, rope_attn_factor
+    p.kquant_mix = kquant_mix
     err = C.create_string_buffer(512)
     if libs()["loader"].gl_synth_model(path.encode(), C.byref(p), err, 512) != 0:
         raise RuntimeError(err.value.decode())

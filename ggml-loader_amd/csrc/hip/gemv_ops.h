@@ -135,6 +135,55 @@ __device__ __forceinline__ void q4k_unit_dot(const q4k_unit & U, int p, const in
     mins = U.m_a * ((int) xbs[4 * p] + (int) xbs[4 * p + 1]) + U.m_b * ((int) xbs[4 * p + 2] + (int) xbs[4 * p + 3]);
 }
 
+// A Q5_K unit (sub-block pair p): the Q4_K unit's nibbles (U, from the block's header and the
+// pair's 32 bytes of qs) with each code's fifth bit, bit 2p (low nibbles: sub-block 2p) or 2p + 1
+// (high nibbles) of qh[l] for element position l; the 32 qh bytes (h0, h1) grouped by l as the
+// nibbles are. Codes 0..31 fit a signed byte, so the dots are Q4_K's; the mins term is Q4_K's too.
+// The integers are those of ggml's generic q5_K x q8_K kernel.
+__device__ __forceinline__ void q5k_unit_dot(const q4k_unit & U, uint4 h0, uint4 h1, int p, const int * xa, const int * xb,
+                                             const int16_t * xbs, int aux[8], int & mins) {
+    uint32_t h[8] = { h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w };
+    q4k_group_by_l(h);
+#pragma unroll
+    for (int l = 0; l < 8; l++) {
+        const int lo = (int) ((U.q[l] & 0x0F0F0F0Fu) | (((h[l] >> (2 * p)) & 0x01010101u) << 4));
+        const int hi = (int) (((U.q[l] >> 4) & 0x0F0F0F0Fu) | (((h[l] >> (2 * p + 1)) & 0x01010101u) << 4));
+        aux[l] = U.sc_a * dot4(lo, xa[l], 0) + U.sc_b * dot4(hi, xb[l], 0);
+    }
+    mins = U.m_a * ((int) xbs[4 * p] + (int) xbs[4 * p + 1]) + U.m_b * ((int) xbs[4 * p + 2] + (int) xbs[4 * p + 3]);
+}
+
+// A Q6_K unit u = (super-block u/4, p = u%4): elements 64p .. 64p + 63, the 32-runs A (group
+// g = 2 (p & 1) of half p >> 1) and B (group g + 1). Their codes: nibble p & 1 of ql bytes 0..31
+// (A) and 32..63 (B) of the half (ql[0..3], 64 bytes), with bits 2g, 2g + 1 (A) and 2g + 2, 2g + 3
+// (B) of the half's 32 qh bytes (h0, h1) as bits 4-5; minus 32 as signed bytes. Each run's first
+// and second 16 elements have their own int8 scale (sc4: the unit's four scales, bytes 4p .. 4p +
+// 3 of the block's). Grouped by l, a dword holds elements l, l + 8 (first 16) and l + 16, l + 24
+// (second 16), so one v_dot4 per scale takes the dword with the other two bytes masked off. No
+// mins. aux[l] is the integer ggml's generic q6_K x q8_K kernel accumulates.
+__device__ __forceinline__ void q6k_unit_dot(const uint4 (&ql)[4], uint4 h0, uint4 h1, uint32_t sc4, int p,
+                                             const int * xa, const int * xb, int aux[8]) {
+    uint32_t a[8] = { ql[0].x, ql[0].y, ql[0].z, ql[0].w, ql[1].x, ql[1].y, ql[1].z, ql[1].w };
+    uint32_t b[8] = { ql[2].x, ql[2].y, ql[2].z, ql[2].w, ql[3].x, ql[3].y, ql[3].z, ql[3].w };
+    uint32_t h[8] = { h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w };
+    q4k_group_by_l(a);
+    q4k_group_by_l(b);
+    q4k_group_by_l(h);
+    const int nib = 4 * (p & 1), ga = 4 * (p & 1);
+    const int s0 = (int) (int8_t) (sc4 & 0xff), s1 = (int) (int8_t) ((sc4 >> 8) & 0xff);
+    const int s2 = (int) (int8_t) ((sc4 >> 16) & 0xff), s3 = (int) (int8_t) (sc4 >> 24);
+#pragma unroll
+    for (int l = 0; l < 8; l++) {
+        const uint32_t qa = ((a[l] >> nib) & 0x0F0F0F0Fu) | (((h[l] >> ga) & 0x03030303u) << 4);
+        const uint32_t qb = ((b[l] >> nib) & 0x0F0F0F0Fu) | (((h[l] >> (ga + 2)) & 0x03030303u) << 4);
+        // q - 32 per byte without borrows: bytes 0x80..0xBF minus 0x20 stay positive, then flip bit 7
+        const int wa = (int) (((qa | 0x80808080u) - 0x20202020u) ^ 0x80808080u);
+        const int wb = (int) (((qb | 0x80808080u) - 0x20202020u) ^ 0x80808080u);
+        aux[l] = s0 * dot4(wa & 0x0000FFFF, xa[l], 0) + s1 * dot4(wa & (int) 0xFFFF0000u, xa[l], 0) +
+                 s2 * dot4(wb & 0x0000FFFF, xb[l], 0) + s3 * dot4(wb & (int) 0xFFFF0000u, xb[l], 0);
+    }
+}
+
 // floats between the term rows of two Q4_0/Q8_0 chains: 4 more than the terms, so the 16-byte
 // reads of consecutive chains (one lane each) start on different LDS banks
 __host__ __device__ constexpr int gemv_term_stride(int nb) { return nb + 4; }

@@ -133,13 +133,16 @@ uint8_t * download_area(hip_device & d, size_t size) {
     return d.down;
 }
 
-bool is_repacked(int type) { return type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0; }
-int qs_bytes_of(int type) { return type == GGML_TYPE_Q4_0 ? Q4_0_QS : Q8_0_QS; }
+bool is_repacked(int type) { return type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0 || type == GGML_TYPE_Q6_K; }
+int qs_bytes_of(int type) { return type == GGML_TYPE_Q4_0 ? Q4_0_QS : type == GGML_TYPE_Q8_0 ? Q8_0_QS : 128; }
 
-// planes of a repacked tensor: base allocation (view_src or self) and the block index of t
+// planes of a repacked tensor: base allocation (view_src or self) and the block index of t.
+// Q4_0 / Q8_0: [qs][d]; Q6_K: [ql = qs][qh][sc][d] (q6k_planes)
 struct planes {
     uint8_t * qs;
     __half * d;
+    uint8_t * qh;         // Q6_K
+    int8_t * sc;          // Q6_K
     int64_t first_block;  // block index of t->data within the base tensor
     int64_t base_blocks;
 };
@@ -149,12 +152,33 @@ planes planes_of(const ggml_tensor * t) {
     const size_t bs = ggml_type_size(t->type);
     planes p;
     p.base_blocks = (int64_t) (ggml_nbytes(base) / bs);
-    p.qs = (uint8_t *) base->data;
-    p.d = (__half *) ((uint8_t *) base->data + p.base_blocks * qs_bytes_of(t->type));
+    uint8_t * b0 = (uint8_t *) base->data;
+    p.qs = b0;
+    p.qh = nullptr;
+    p.sc = nullptr;
+    if (t->type == GGML_TYPE_Q6_K) {
+        p.qh = b0 + p.base_blocks * 128;
+        p.sc = (int8_t *) (b0 + p.base_blocks * 192);
+        p.d = (__half *) (b0 + p.base_blocks * 208);
+    } else {
+        p.d = (__half *) (b0 + p.base_blocks * qs_bytes_of(t->type));
+    }
     const size_t off = (size_t) ((const char *) t->data - (const char *) base->data);
     if (off % bs) HIP_ABORT("tensor '%s': view offset is not block aligned", t->name);
     p.first_block = (int64_t) (off / bs);
     return p;
+}
+
+q6k_planes q6k_of(const planes & p) { return q6k_planes{ p.qs, p.qh, p.sc, p.d }; }
+
+void repack_blocks(const ggml_tensor * t, const planes & p, const uint8_t * raw, int64_t nblocks, int64_t first, hipStream_t st) {
+    if (t->type == GGML_TYPE_Q6_K) launch_repack_q6k(raw, q6k_of(p), nblocks, first, st);
+    else launch_repack_q(t->type, raw, p.qs, p.d, nblocks, first, st);
+}
+
+void unpack_blocks(const ggml_tensor * t, const planes & p, uint8_t * raw, int64_t nblocks, int64_t first, hipStream_t st) {
+    if (t->type == GGML_TYPE_Q6_K) launch_unpack_q6k(raw, q6k_of(p), nblocks, first, st);
+    else launch_unpack_q(t->type, raw, p.qs, p.d, nblocks, first, st);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -186,7 +210,7 @@ void buf_set(ggml_backend_buffer_t b, ggml_tensor * t, const void * data, size_t
             const size_t n = std::min(chunk, size - done);
             uint8_t * st = staging(d, n);
             HIP_CHECK(hipMemcpyAsync(st, (const uint8_t *) data + done, n, hipMemcpyHostToDevice, d.stream));
-            launch_repack_q(t->type, st, p.qs, p.d, (int64_t) (n / bs), p.first_block + (int64_t) ((off + done) / bs), d.stream);
+            repack_blocks(t, p, st, (int64_t) (n / bs), p.first_block + (int64_t) ((off + done) / bs), d.stream);
             HIP_CHECK(hipStreamSynchronize(d.stream));
             drained(d);
         }
@@ -213,7 +237,7 @@ void buf_get(ggml_backend_buffer_t b, const ggml_tensor * t, void * data, size_t
         for (size_t done = 0; done < size; done += chunk) {
             const size_t n = std::min(chunk, size - done);
             uint8_t * st = staging(d, n);
-            launch_unpack_q(t->type, st, p.qs, p.d, (int64_t) (n / bs), p.first_block + (int64_t) ((off + done) / bs), d.stream);
+            unpack_blocks(t, p, st, (int64_t) (n / bs), p.first_block + (int64_t) ((off + done) / bs), d.stream);
             HIP_CHECK(hipMemcpyAsync((uint8_t *) data + done, st, n, hipMemcpyDeviceToHost, d.stream));
             HIP_CHECK(hipStreamSynchronize(d.stream));
             drained(d);
@@ -242,6 +266,10 @@ void buf_memset(ggml_backend_buffer_t b, ggml_tensor * t, uint8_t v, size_t off,
         const int64_t b0 = p.first_block + (int64_t) (off / bs), nb = (int64_t) (size / bs);
         HIP_CHECK(hipMemsetAsync(p.qs + b0 * qs_bytes_of(t->type), 0, nb * qs_bytes_of(t->type), d.stream));
         HIP_CHECK(hipMemsetAsync(p.d + b0, 0, nb * sizeof(__half), d.stream));
+        if (t->type == GGML_TYPE_Q6_K) {
+            HIP_CHECK(hipMemsetAsync(p.qh + b0 * 64, 0, nb * 64, d.stream));
+            HIP_CHECK(hipMemsetAsync(p.sc + b0 * 16, 0, nb * 16, d.stream));
+        }
     } else {
         HIP_CHECK(hipMemsetAsync((char *) t->data + off, v, size, d.stream));
     }
@@ -367,9 +395,20 @@ tview tv(const ggml_tensor * t) {
     return v;
 }
 
+// profile names of the GEMV launches, by weight type
+const char * gemv_prof_name(int wtype, bool swiglu) {
+    switch (wtype) {
+        case GGML_TYPE_Q4_0: return swiglu ? "gemv_q4_0_swiglu" : "gemv_q4_0";
+        case GGML_TYPE_Q8_0: return swiglu ? "gemv_q8_0_swiglu" : "gemv_q8_0";
+        case GGML_TYPE_Q5_K: return swiglu ? "gemv_q5_K_swiglu" : "gemv_q5_K";
+        case GGML_TYPE_Q6_K: return swiglu ? "gemv_q6_K_swiglu" : "gemv_q6_K";
+        default: return swiglu ? "gemv_q4_K_swiglu" : "gemv_q4_K";
+    }
+}
+
 int dot_kind(int wtype) {
     if (wtype == GGML_TYPE_Q4_0 || wtype == GGML_TYPE_Q8_0) return 1;
-    if (wtype == GGML_TYPE_Q4_K) return 2;
+    if (is_kquant(wtype)) return 2;
     return 0;
 }
 
@@ -696,7 +735,7 @@ private:
         planes p{};
         if (is_repacked(a->type)) p = planes_of(a);
         prof_scope ps(this, "get_rows", (double) ggml_nbytes(n));
-        launch_get_rows(tv(a), tv(n->src[1]), tv(n), p.qs, p.d, p.first_block, st_);
+        launch_get_rows(tv(a), tv(n->src[1]), tv(n), p.qs, p.d, q6k_of(p), p.first_block, st_);
     }
 
     static bool is_view_op(int op) {
@@ -1062,7 +1101,7 @@ private:
         const ggml_tensor * w = mm->src[0];
         const ggml_tensor * x = mm->src[1];
         if (!dot_kind(w->type)) return false;
-        if (w->ne[0] % (w->type == GGML_TYPE_Q4_K ? 256 : 32)) return false;
+        if (w->ne[0] % (is_kquant(w->type) ? 256 : 32)) return false;
         if (x->type != GGML_TYPE_F32 || x->nb[0] != sizeof(float)) return false;
         if (mm->op == GGML_OP_MUL_MAT_ID) {
             // experts [K, N, n_expert] stored contiguously; activation [K, x_cols, n_tok] with evenly
@@ -1331,10 +1370,16 @@ private:
         auto fill_mat = [&](gemv_mat & gm, int j, double & bytes, bool epilogue) {
             ggml_tensor * mm = g_->nodes[j];
             const ggml_tensor * w = mm->src[0];
+            gm.wqh = nullptr;
+            gm.wsc = nullptr;
             if (is_repacked(w->type)) {
                 const planes p = planes_of(w);
                 gm.w = p.qs + p.first_block * qs_bytes_of(w->type);
                 gm.wd = p.d + p.first_block;
+                if (w->type == GGML_TYPE_Q6_K) {
+                    gm.wqh = p.qh + p.first_block * 64;
+                    gm.wsc = p.sc + p.first_block * 16;
+                }
             } else {
                 gm.w = (const uint8_t *) w->data;
                 gm.wd = nullptr;
@@ -1418,8 +1463,7 @@ private:
                 norm_[mn] = gemv_norm{ (const float *) mn->data, (int64_t) (mn->nb[1] / sizeof(float)), nullptr, 0.0f, 0 };
             }
             {
-                prof_scope ps(this, wtype == GGML_TYPE_Q4_0 ? "gemv_q4_0_swiglu" :
-                                    wtype == GGML_TYPE_Q8_0 ? "gemv_q8_0_swiglu" : "gemv_q4_K_swiglu", sb);
+                prof_scope ps(this, gemv_prof_name(wtype, true), sb);
                 run(S);
             }
             wrote_.push_back(mn);
@@ -1435,7 +1479,7 @@ private:
         L.n_mats = (int) group.size();
         for (size_t k = 0; k < group.size(); k++) fill_mat(L.m[k], group[k], bytes, true);
         {
-            prof_scope ps(this, wtype == GGML_TYPE_Q4_0 ? "gemv_q4_0" : wtype == GGML_TYPE_Q8_0 ? "gemv_q8_0" : "gemv_q4_K", bytes);
+            prof_scope ps(this, gemv_prof_name(wtype, false), bytes);
             run(L);
         }
         for (int j : group) done_[j] = true;

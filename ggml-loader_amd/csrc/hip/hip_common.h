@@ -41,9 +41,13 @@ constexpr int WAVE = 64;
 constexpr int Q4_0_QS = 16;
 constexpr int Q8_0_QS = 32;
 constexpr int Q4_K_BYTES = 144;
+constexpr int Q5_K_BYTES = 176;
 
 struct q4k_block { __half d; __half dmin; uint8_t scales[12]; uint8_t qs[128]; };
 static_assert(sizeof(q4k_block) == 144, "q4_K block");
+// GGUF order: the Q4_K header, the fifth bits (bit j of qh[l]: element l of sub-block j), the nibbles
+struct q5k_block { __half d; __half dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; };
+static_assert(sizeof(q5k_block) == 176, "q5_K block");
 
 // DPP lane exchanges (v_mov_dpp): quad_perm xor 1 (0xB1) and xor 2 (0x4E), row_half_mirror (0x141:
 // lane i <-> 7 - i within 8 lanes), row_mirror (0x140: i <-> 15 - i within 16). One VALU op each,

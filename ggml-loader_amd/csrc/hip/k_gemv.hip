@@ -41,6 +41,41 @@ __global__ void unpack_q_kernel(int qs_bytes, int blk_bytes, uint8_t * __restric
     for (int i = 0; i < qs_bytes; i++) dst[2 + i] = sq[i];
 }
 
+// Q6_K GGUF blocks <-> the four planes (q6k_planes), one thread per block
+__global__ void repack_q6k_kernel(const uint8_t * __restrict__ raw, q6k_planes p, int64_t nblocks, int64_t first) {
+    const int64_t b = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint8_t * src = raw + b * 210;
+    const int64_t o = first + b;
+    for (int i = 0; i < 128; i++) p.ql[o * 128 + i] = src[i];
+    for (int i = 0; i < 64; i++) p.qh[o * 64 + i] = src[128 + i];
+    for (int i = 0; i < 16; i++) p.sc[o * 16 + i] = (int8_t) src[192 + i];
+    p.d[o] = __ushort_as_half((unsigned short) (src[208] | (src[209] << 8)));
+}
+
+__global__ void unpack_q6k_kernel(uint8_t * __restrict__ raw, q6k_planes p, int64_t nblocks, int64_t first) {
+    const int64_t b = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    uint8_t * dst = raw + b * 210;
+    const int64_t o = first + b;
+    for (int i = 0; i < 128; i++) dst[i] = p.ql[o * 128 + i];
+    for (int i = 0; i < 64; i++) dst[128 + i] = p.qh[o * 64 + i];
+    for (int i = 0; i < 16; i++) dst[192 + i] = (uint8_t) p.sc[o * 16 + i];
+    const unsigned short h = __half_as_ushort(p.d[o]);
+    dst[208] = (uint8_t) (h & 0xff);
+    dst[209] = (uint8_t) (h >> 8);
+}
+
+void launch_repack_q6k(const uint8_t * raw, q6k_planes p, int64_t nblocks, int64_t first_block, hipStream_t st) {
+    if (nblocks <= 0) return;
+    launch(repack_q6k_kernel, dim3((unsigned) ((nblocks + 255) / 256)), dim3(256), 0, st, raw, p, nblocks, first_block);
+}
+
+void launch_unpack_q6k(uint8_t * raw, q6k_planes p, int64_t nblocks, int64_t first_block, hipStream_t st) {
+    if (nblocks <= 0) return;
+    launch(unpack_q6k_kernel, dim3((unsigned) ((nblocks + 255) / 256)), dim3(256), 0, st, raw, p, nblocks, first_block);
+}
+
 static void qs_geometry(int type, int & qs_bytes, int & blk_bytes) {
     if (type == GGML_TYPE_Q4_0) { qs_bytes = Q4_0_QS; blk_bytes = 18; return; }
     if (type == GGML_TYPE_Q8_0) { qs_bytes = Q8_0_QS; blk_bytes = 34; return; }
@@ -477,7 +512,7 @@ void launch_act_quant(const gemv_launch & L, const q8_act & q8, const q8k_act & 
         case GGML_TYPE_Q4_0: case GGML_TYPE_Q8_0:
             launch(act_quant_kernel<GGML_TYPE_Q4_0>, dim3(L.ncols), dim3(GEMV_NT), gemv_lds_bytes<GGML_TYPE_Q4_0>(L.K, 0, 0), st, L, q8, q8k);
             break;
-        case GGML_TYPE_Q4_K:
+        case GGML_TYPE_Q4_K: case GGML_TYPE_Q5_K: case GGML_TYPE_Q6_K:   // Q8_K activations
             launch(act_quant_kernel<GGML_TYPE_Q4_K>, dim3(L.ncols), dim3(GEMV_NT), gemv_lds_bytes<GGML_TYPE_Q4_K>(L.K, 0, 0), st, L, q8, q8k);
             break;
         default:
@@ -504,7 +539,8 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
     const int lrow = SWIGLU ? row : row - a.row_begin[mi];
     const bool valid = row < a.total_rows && lrow < L.m[mi].n_rows;
 
-    const gemv_lds s = lds_layout<TYPE>(smem, K);
+    constexpr int AT = is_kquant(TYPE) ? GGML_TYPE_Q4_K : TYPE;   // the activation's layout: Q8_K or Q8_0
+    const gemv_lds s = lds_layout<AT>(smem, K);
     __shared__ double s_red[512 / WAVE];
 
     // mul_mat_id: the expert of this column and its activation column
@@ -569,29 +605,49 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                 }
             }
         }
-    } else { // Q4_K: per (super-block, l) products d*aux32[l] and dmin*mins
+    } else { // K-quants: per (super-block, l) products d*aux32[l] and dmin*mins
         // as above: the prologue's loads, then every weight load of this lane (ITS units of 64
-        // weights: the block header and the pair's 32 quant bytes; unit and row clamped into the
-        // matrix), then the prologue's arithmetic while the weights are in flight
+        // weights; unit and row clamped into the matrix), then the prologue's arithmetic while the
+        // weights are in flight. A unit's 16-byte pieces: Q4_K the block header and the pair's 32
+        // quant bytes; Q5_K those and the block's 32 qh bytes; Q6_K (planes) the half's 64 ql and 32
+        // qh bytes, plus its four scales and the block's d.
         float xv[PRO_REGS], wv[PRO_REGS];
-        prologue_load<TYPE, PRO>(L, xcol, xv, wv);
+        prologue_load<AT, PRO>(L, xcol, xv, wv);
         const int units = K / 64, nsb = K / 256;
-        const int64_t row_bytes = (int64_t) nsb * Q4_K_BYTES;
-        uint4 hd[NCH][ITS], qa[NCH][ITS], qb[NCH][ITS];
+        constexpr int NW = TYPE == GGML_TYPE_Q4_K ? 3 : TYPE == GGML_TYPE_Q5_K ? 5 : 6;
+        constexpr int BB = TYPE == GGML_TYPE_Q4_K ? Q4_K_BYTES : Q5_K_BYTES;
+        uint4 wq[NCH][ITS][NW];
+        uint32_t wsc[NCH][ITS], wdd[NCH][ITS];
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++) {
             const gemv_mat & wm = L.m[SWIGLU ? ch : mi];
-            const uint8_t * wrow = wm.w + (erow + min(lrow, wm.n_rows - 1)) * row_bytes;
+            const int64_t wr = erow + min(lrow, wm.n_rows - 1);
 #pragma unroll
             for (int it = 0; it < ITS; it++) {
                 const int u = min(l + it * LPR, units - 1);
-                const uint8_t * blk = wrow + (int64_t) (u >> 2) * Q4_K_BYTES;
-                hd[ch][it] = *(const uint4 *) blk;
-                qa[ch][it] = *(const uint4 *) (blk + 16 + 32 * (u & 3));
-                qb[ch][it] = *(const uint4 *) (blk + 32 + 32 * (u & 3));
+                const int sb = u >> 2, p = u & 3;
+                if constexpr (TYPE == GGML_TYPE_Q6_K) {
+                    const int64_t b = wr * nsb + sb;
+                    const uint4 * ql = (const uint4 *) (wm.w + b * 128 + 64 * (p >> 1));
+                    const uint4 * qh = (const uint4 *) (wm.wqh + b * 64 + 32 * (p >> 1));
+                    wq[ch][it][0] = ql[0]; wq[ch][it][1] = ql[1]; wq[ch][it][2] = ql[2]; wq[ch][it][3] = ql[3];
+                    wq[ch][it][4] = qh[0]; wq[ch][it][5] = qh[1];
+                    wsc[ch][it] = *(const uint32_t *) (wm.wsc + b * 16 + 4 * p);
+                    wdd[ch][it] = ((const unsigned short *) wm.wd)[b];
+                } else {
+                    const uint8_t * blk = wm.w + (wr * nsb + sb) * BB;
+                    wq[ch][it][0] = *(const uint4 *) blk;
+                    const int qoff = TYPE == GGML_TYPE_Q4_K ? 16 : 48;
+                    wq[ch][it][1] = *(const uint4 *) (blk + qoff + 32 * p);
+                    wq[ch][it][2] = *(const uint4 *) (blk + qoff + 16 + 32 * p);
+                    if constexpr (TYPE == GGML_TYPE_Q5_K) {
+                        wq[ch][it][3] = *(const uint4 *) (blk + 16);
+                        wq[ch][it][4] = *(const uint4 *) (blk + 32);
+                    }
+                }
             }
         }
-        stage_x<TYPE, PRO>(L, xcol, s, s_red, xv, wv);
+        stage_x<AT, PRO>(L, xcol, s, s_red, xv, wv);
         // the staged activation's sub-blocks grouped by l
         group_by_l_lds(s.xq, K / 32);
         __syncthreads();
@@ -609,7 +665,15 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                 for (int k = 0; k < 8; k++) aux[k] = 0;
                 if (has) {
                     const int * xs = (const int *) (s.xq + sb * 256 + 64 * p);
-                    q4k_unit_dot(q4k_prepare(hd[ch][it], qa[ch][it], qb[ch][it], p), p, xs, xs + 8, s.xbs + sb * 16, aux, mins);
+                    const uint4 (&w)[NW] = wq[ch][it];
+                    if constexpr (TYPE == GGML_TYPE_Q4_K) {
+                        q4k_unit_dot(q4k_prepare(w[0], w[1], w[2], p), p, xs, xs + 8, s.xbs + sb * 16, aux, mins);
+                    } else if constexpr (TYPE == GGML_TYPE_Q5_K) {
+                        q5k_unit_dot(q4k_prepare(w[0], w[1], w[2], p), w[3], w[4], p, xs, xs + 8, s.xbs + sb * 16, aux, mins);
+                    } else {
+                        const uint4 ql[4] = { w[0], w[1], w[2], w[3] };
+                        q6k_unit_dot(ql, w[4], w[5], wsc[ch][it], p, xs, xs + 8, aux);
+                    }
                 }
                 // the 4 units of a super-block sit on 4 consecutive lanes: combine (exact integers)
 #pragma unroll
@@ -620,10 +684,12 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                 mins += dpp_i<0xB1>(mins);
                 mins += dpp_i<0x4E>(mins);
                 if (has) {
-                    const uint32_t dd = hd[ch][it].x;
                     const float yd = s.xd[sb];
+                    // Q4_K/Q5_K: d and dmin from the block header; Q6_K: d from its plane, no mins
+                    // (a zero mins term leaves ggml's sumf = 0 + sums[0] + ... unchanged)
+                    const uint32_t dd = TYPE == GGML_TYPE_Q6_K ? wdd[ch][it] : wq[ch][it][0].x;
                     const float d = __half2float(__ushort_as_half((unsigned short) (dd & 0xffff))) * yd;
-                    const float dmin = __half2float(__ushort_as_half((unsigned short) (dd >> 16))) * yd;
+                    const float dmin = TYPE == GGML_TYPE_Q6_K ? 0.0f : __half2float(__ushort_as_half((unsigned short) (dd >> 16))) * yd;
                     // this lane stores the products for l = 2p, 2p+1 (static register indexing)
                     float t0 = 0.0f, t1 = 0.0f;
 #pragma unroll
@@ -634,7 +700,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                     float * tt = terms + sb * 9;
                     tt[2 * p] = t0;
                     tt[2 * p + 1] = t1;
-                    if (p == 0) tt[8] = dmin * (float) mins;
+                    if (p == 0) tt[8] = TYPE == GGML_TYPE_Q6_K ? 0.0f : dmin * (float) mins;
                 }
             }
         }
@@ -667,7 +733,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
         return;
     }
 
-    // a Q4_K row's terms were written by lanes of its own wave: a wave-level ordering point suffices
+    // a K-quant row's terms were written by lanes of its own wave: a wave-level ordering point suffices
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -732,8 +798,9 @@ static void launch_gemv_its(gemv_kargs & ka, int waves, hipStream_t st) {
         ka.total_rows = r;
     }
     const int grid_x = (ka.total_rows + ka.rows_per_block - 1) / ka.rows_per_block;
-    const size_t lds = gemv_lds_bytes<TYPE>(ka.L.K, ka.rows_per_block, SWIGLU ? 2 : 1);
-    if (TYPE != GGML_TYPE_Q4_K && ka.rows_per_block * (SWIGLU ? 2 : 1) > WAVE) {
+    constexpr int AT = is_kquant(TYPE) ? GGML_TYPE_Q4_K : TYPE;
+    const size_t lds = gemv_lds_bytes<AT>(ka.L.K, ka.rows_per_block, SWIGLU ? 2 : 1);
+    if (!is_kquant(TYPE) && ka.rows_per_block * (SWIGLU ? 2 : 1) > WAVE) {
         HIP_ABORT("gemv: %d chains per workgroup exceed one wave", ka.rows_per_block * (SWIGLU ? 2 : 1));
     }
     if (lds > 160 * 1024) HIP_ABORT("gemv: K=%d needs %zu bytes of LDS", ka.L.K, lds);
@@ -743,9 +810,30 @@ static void launch_gemv_its(gemv_kargs & ka, int waves, hipStream_t st) {
 
 // ITS = weight blocks per lane for Q4_0/Q8_0, held in registers from the up-front loads. The ladder
 // stops where the registers of both SwiGLU chains would spill (12) and at 16 for a single chain.
+// largest K-quant units (64 weights) per lane held in registers: 3, 5 or 6 16-byte pieces per
+// unit (Q4_K, Q5_K, Q6_K), per chain
+template <int TYPE, bool SWIGLU>
+constexpr int kq_max_its() {
+    return TYPE == GGML_TYPE_Q4_K ? (SWIGLU ? 4 : 10) : TYPE == GGML_TYPE_Q5_K ? (SWIGLU ? 3 : 6) : (SWIGLU ? 2 : 4);
+}
+
 template <int TYPE, int LPR, bool SWIGLU>
 static void launch_gemv_t(gemv_kargs & ka, int waves, hipStream_t st) {
-    if constexpr (TYPE == GGML_TYPE_Q4_K) {
+    if constexpr (is_kquant(TYPE) && TYPE != GGML_TYPE_Q4_K) {
+        // Q5_K / Q6_K: units of 64 weights per lane, up to kq_max_its
+        const int its = (ka.L.K / 64 + LPR - 1) / LPR;
+        constexpr int MAXI = kq_max_its<TYPE, SWIGLU>();
+        if (its > MAXI) HIP_ABORT("gemv type %d: K=%d needs %d units per lane (at most %d)", TYPE, ka.L.K, its, MAXI);
+        if (its <= 1) launch_gemv_its<TYPE, LPR, SWIGLU, 1>(ka, waves, st);
+        else if (its <= 2) launch_gemv_its<TYPE, LPR, SWIGLU, 2>(ka, waves, st);
+        else if constexpr (MAXI >= 3) {
+            if (its <= 3) launch_gemv_its<TYPE, LPR, SWIGLU, 3>(ka, waves, st);
+            else if constexpr (MAXI >= 4) {
+                if (its <= 4) launch_gemv_its<TYPE, LPR, SWIGLU, 4>(ka, waves, st);
+                else if constexpr (MAXI >= 6) launch_gemv_its<TYPE, LPR, SWIGLU, 6>(ka, waves, st);
+            }
+        }
+    } else if constexpr (TYPE == GGML_TYPE_Q4_K) {
         // units of 64 weights per lane
         const int its = (ka.L.K / 64 + LPR - 1) / LPR;
         if (its <= 1) launch_gemv_its<TYPE, LPR, SWIGLU, 1>(ka, waves, st);
@@ -810,6 +898,20 @@ static void launch_gemv_q4k_lanes(gemv_kargs & ka, hipStream_t st) {
     else launch_gemv_t<GGML_TYPE_Q4_K, 64, SWIGLU>(ka, WAVES, st);
 }
 
+// Lanes per row for Q5_K / Q6_K launches of 4-wave workgroups: the fewest that keep a lane's units
+// within kq_max_its and still give about two workgroups per CU (SwiGLU: at least 32, as for Q4_K)
+template <int TYPE, bool SWIGLU>
+static void launch_gemv_kq_lanes(gemv_kargs & ka, hipStream_t st) {
+    constexpr int WAVES = 4, TARGET_BLOCKS = 512, MAXI = kq_max_its<TYPE, SWIGLU>();
+    const int rows = ka.total_rows, units = ka.L.K / 64;
+    const auto blocks = [&](int lpr) { return (rows + WAVES * (WAVE / lpr) - 1) / (WAVES * (WAVE / lpr)) * ka.L.ncols; };
+    if constexpr (!SWIGLU) {
+        if (units <= 16 * MAXI && blocks(16) >= TARGET_BLOCKS) return launch_gemv_t<TYPE, 16, SWIGLU>(ka, WAVES, st);
+    }
+    if (units <= 32 * MAXI && blocks(32) >= TARGET_BLOCKS) launch_gemv_t<TYPE, 32, SWIGLU>(ka, WAVES, st);
+    else launch_gemv_t<TYPE, 64, SWIGLU>(ka, WAVES, st);
+}
+
 void launch_gemv(const gemv_launch & L, hipStream_t st) {
     gemv_kargs ka;
     ka.L = L;
@@ -845,6 +947,16 @@ void launch_gemv(const gemv_launch & L, hipStream_t st) {
             if (L.K % 256 || L.K / 64 > 640) HIP_ABORT("gemv q4_K: K=%d unsupported", L.K);
             if (L.swiglu) launch_gemv_q4k_lanes<true>(ka, st);
             else launch_gemv_q4k_lanes<false>(ka, st);
+            break;
+        case GGML_TYPE_Q5_K:
+            if (L.K % 256 || L.K / 64 > 64 * kq_max_its<GGML_TYPE_Q5_K, false>()) HIP_ABORT("gemv q5_K: K=%d unsupported", L.K);
+            if (L.swiglu) launch_gemv_kq_lanes<GGML_TYPE_Q5_K, true>(ka, st);
+            else launch_gemv_kq_lanes<GGML_TYPE_Q5_K, false>(ka, st);
+            break;
+        case GGML_TYPE_Q6_K:
+            if (L.K % 256 || L.K / 64 > 64 * kq_max_its<GGML_TYPE_Q6_K, false>()) HIP_ABORT("gemv q6_K: K=%d unsupported", L.K);
+            if (L.swiglu) launch_gemv_kq_lanes<GGML_TYPE_Q6_K, true>(ka, st);
+            else launch_gemv_kq_lanes<GGML_TYPE_Q6_K, false>(ka, st);
             break;
         default:
             HIP_ABORT("gemv: unsupported weight type %d", L.type);

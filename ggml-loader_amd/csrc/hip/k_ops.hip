@@ -413,7 +413,8 @@ void launch_cpy(const tview & src, const tview & dst, hipStream_t st) {
 // ---------------------------------------------------------------------------------------------
 // get_rows: dst[:, i10, i11, i12] = dequant(a[:, ids[i10, i11, i12], i11, i12])
 
-__global__ void get_rows_kernel(tview a, tview ids, tview d, const uint8_t * qs, const __half * dpl, int64_t first_block) {
+__global__ void get_rows_kernel(tview a, tview ids, tview d, const uint8_t * qs, const __half * dpl, q6k_planes q6,
+                                int64_t first_block) {
     const int64_t r = blockIdx.x;
     const int64_t i10 = r % ids.ne[0], i11 = (r / ids.ne[0]) % ids.ne[1], i12 = r / (ids.ne[0] * ids.ne[1]);
     const int32_t row = *(const int32_t *) at(ids, i10, i11, i12, 0);
@@ -452,6 +453,31 @@ __global__ void get_rows_kernel(tview a, tview ids, tview d, const uint8_t * qs,
                 v = dd * (float) q - mm;
                 break;
             }
+            case GGML_TYPE_Q5_K: {
+                const q5k_block * b = (const q5k_block *) (a.data + byte_off) + e / 256;
+                const int k = (int) (e % 256);
+                const int j = k / 32, l = k % 32;
+                const uint8_t * s = b->scales;
+                int sc, m;
+                if (j < 4) { sc = s[j] & 63; m = s[j + 4] & 63; }
+                else { sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4); m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+                const uint8_t qb = b->qs[32 * (j / 2) + l];
+                const int q = ((j & 1) ? (qb >> 4) : (qb & 0x0F)) + 16 * ((b->qh[l] >> j) & 1);
+                const float dd = __half2float(b->d) * (float) sc;
+                const float mm = __half2float(b->dmin) * (float) m;
+                v = dd * (float) q - mm;
+                break;
+            }
+            case GGML_TYPE_Q6_K: {
+                const int64_t blk = first_block + byte_off / 210 + e / 256;
+                const int k = (int) (e % 256);
+                const int h = k / 128, g = (k % 128) / 32, l = k % 32;
+                const int lo = (q6.ql[blk * 128 + 64 * h + 32 * (g & 1) + l] >> (4 * (g >> 1))) & 0x0F;
+                const int hi = (q6.qh[blk * 64 + 32 * h + l] >> (2 * g)) & 3;
+                const float ds = __half2float(q6.d[blk]) * (float) q6.sc[blk * 16 + 8 * h + 2 * g + l / 16];
+                v = ds * (float) ((lo | (hi << 4)) - 32);
+                break;
+            }
             default:
                 v = ld(a.data + byte_off + e * a.nb[0], a.type);
                 break;
@@ -461,10 +487,10 @@ __global__ void get_rows_kernel(tview a, tview ids, tview d, const uint8_t * qs,
 }
 
 void launch_get_rows(const tview & a, const tview & ids, const tview & dst, const uint8_t * qs_plane,
-                     const __half * d_plane, int64_t first_block, hipStream_t st) {
+                     const __half * d_plane, const q6k_planes & q6, int64_t first_block, hipStream_t st) {
     const int64_t rows = ids.ne[0] * ids.ne[1] * ids.ne[2];
     if (rows == 0) return;
-    launch(get_rows_kernel, dim3((unsigned) rows), dim3(256), 0, st, a, ids, dst, qs_plane, d_plane, first_block);
+    launch(get_rows_kernel, dim3((unsigned) rows), dim3(256), 0, st, a, ids, dst, qs_plane, d_plane, q6, first_block);
 }
 
 // ---------------------------------------------------------------------------------------------

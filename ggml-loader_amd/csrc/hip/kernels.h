@@ -38,12 +38,28 @@ struct tview {
     int64_t nb[4];
 };
 
+// the K-quant weight types (Q4_K, Q5_K, Q6_K): 256-weight super-blocks, dotted against Q8_K
+// activations
+__host__ __device__ constexpr bool is_kquant(int type) { return type == 12 || type == 13 || type == 14; }
+
 // ---------------------------------------------------------------------------------------------
 // weight layout conversion (GGUF bytes <-> device planes), on the stream
 void launch_repack_q(int type, const uint8_t * raw, uint8_t * qs_plane, __half * d_plane,
                      int64_t nblocks, int64_t first_block, hipStream_t st);
 void launch_unpack_q(int type, uint8_t * raw, const uint8_t * qs_plane, const __half * d_plane,
                      int64_t nblocks, int64_t first_block, hipStream_t st);
+// Q6_K blocks (210 bytes, so only 2-byte aligned in GGUF order: {ql[128], qh[64], i8 scales[16],
+// f16 d}) as four planes inside the tensor's
+// own allocation, same size: [ql: nb x 128][qh: nb x 64][scales: nb x 16][d: nb x f16], block b's
+// fields at ql + 128 b, qh + 64 b, sc + 16 b, d + b; every 16-byte piece a kernel loads is aligned
+struct q6k_planes {
+    uint8_t * ql;
+    uint8_t * qh;
+    int8_t *  sc;
+    __half *  d;
+};
+void launch_repack_q6k(const uint8_t * raw, q6k_planes p, int64_t nblocks, int64_t first_block, hipStream_t st);
+void launch_unpack_q6k(uint8_t * raw, q6k_planes p, int64_t nblocks, int64_t first_block, hipStream_t st);
 
 // ---------------------------------------------------------------------------------------------
 // activation quantization of ncols columns of K floats (column c at x + c*x_col_stride floats)
@@ -60,12 +76,15 @@ constexpr int GEMV_MAX_MATS = 4;
 constexpr int GEMV_MAX_K = 16384;          // Q4_0 / Q8_0 rows
 // longest rows of a gate/up pair in one SwiGLU launch (both chains' weight blocks stay in registers)
 constexpr int gemv_swiglu_max_k(int type) {
-    return type == 8 /* GGML_TYPE_Q8_0 */ ? 4096 : type == 12 /* GGML_TYPE_Q4_K */ ? 16384 : 6144;
+    return type == 8 /* GGML_TYPE_Q8_0 */ ? 4096 : type == 12 /* GGML_TYPE_Q4_K */ ? 16384
+         : type == 13 /* GGML_TYPE_Q5_K */ ? 12288 : type == 14 /* GGML_TYPE_Q6_K */ ? 8192 : 6144;
 }
 
 struct gemv_mat {
-    const uint8_t * w;     // Q4_0/Q8_0: qs plane of the first row; Q4_K: first block
-    const __half *  wd;    // Q4_0/Q8_0: d plane of the first row
+    const uint8_t * w;     // Q4_0/Q8_0: qs plane of the first row; Q4_K/Q5_K: first block; Q6_K: ql plane
+    const __half *  wd;    // Q4_0/Q8_0/Q6_K: d plane of the first row
+    const uint8_t * wqh;   // Q6_K: qh plane of the first row
+    const int8_t *  wsc;   // Q6_K: scales plane of the first row
     float *         y;     // output column 0
     const float *   add;   // optional residual added to the output (nullptr: none)
     int64_t         y_stride;   // floats between output columns
@@ -121,12 +140,12 @@ struct gemv_norm {
 // Q8_0 block or one 16-element Q8_K group per thread of a 256-thread workgroup; without, up to 8 of
 // them per thread
 constexpr int act_quant_max_k(int type, bool rms) {
-    return (type == 12 /* GGML_TYPE_Q4_K */ ? 16 : 32) * 256 * (rms ? 1 : 8);
+    return (is_kquant(type) ? 16 : 32) * 256 * (rms ? 1 : 8);
 }
 // largest K a GEMV's activation prologue handles: the Q4_0 / Q8_0 kernel holds up to 2 (rms) or 4
 // float4 chunks per thread of a 512-thread workgroup
 constexpr int gemv_prologue_max_k(int type, bool rms) {
-    return type == 12 /* GGML_TYPE_Q4_K */ ? act_quant_max_k(type, rms) : (rms ? 4096 : 8192);
+    return is_kquant(type) ? act_quant_max_k(type, rms) : (rms ? 4096 : 8192);
 }
 // SwiGLU launches that quantize act for the down projection (out_q): 32 rows per workgroup of 1024
 // threads, K up to 4096
@@ -219,9 +238,10 @@ void launch_concat(const tview & a, const tview & b, const tview & dst, int dim,
 void launch_glu(const tview & a, const tview & b, const tview & dst, hipStream_t st);
 // element-wise copy with type conversion in row-major element order (shapes may differ)
 void launch_cpy(const tview & src, const tview & dst, hipStream_t st);
-// dst rows = dequantized rows of a selected by I32 ids
+// dst rows = dequantized rows of a selected by I32 ids (Q4_0 / Q8_0: qs_plane, d_plane; Q6_K: q6;
+// with first_block the block of a's first element in them)
 void launch_get_rows(const tview & a, const tview & ids, const tview & dst, const uint8_t * qs_plane,
-                     const __half * d_plane, int64_t first_block, hipStream_t st);
+                     const __half * d_plane, const q6k_planes & q6, int64_t first_block, hipStream_t st);
 
 struct rope_params {
     int   n_dims;

@@ -69,6 +69,15 @@ extern "C" int gl_synth_model(const char * path, const gl_synth_params * p, char
     const int64_t E = p->n_embd, hd = p->head_dim, nh = p->n_head, nkv = p->n_head_kv, ff = p->n_ff, V = p->n_vocab;
     if (E <= 0 || hd <= 0 || nh <= 0 || nkv <= 0 || V <= 0 || p->n_layer <= 0) return fail("synth: bad shape");
     const ggml_type wt = (ggml_type) p->wtype;
+    if (p->kquant_mix && wt != GGML_TYPE_Q4_K) return fail("synth: kquant_mix needs wtype Q4_K");
+    // the matrix type of a layer's tensor under kquant_mix (role: 'v' attn_v / ffn_down, 'q' attn_q /
+    // ffn_gate / ffn_up, anything else keeps wtype)
+    auto mix = [&](int64_t il, char role) {
+        if (!p->kquant_mix) return wt;
+        if (role == 'v' && il % 2 == 0) return GGML_TYPE_Q6_K;
+        if (role == 'q' && il % 2 == 1) return GGML_TYPE_Q5_K;
+        return wt;
+    };
     auto fits = [&](ggml_type t, int64_t k) { return ggml_type_size(t) > 0 && k % ggml_blck_size(t) == 0; };
 
     std::vector<tensor_spec> specs;
@@ -85,16 +94,16 @@ extern "C" int gl_synth_model(const char * path, const gl_synth_params * p, char
         if (!phi3) return fail("synth: LongRoPE keys are written for phi3 only");
         add("rope_factors_short.weight", GGML_TYPE_F32, { hd / 2 }, 2.0f, 0.25f);
     }
-    if (!p->tied_output) add("output.weight", (ggml_type) p->output_type, { E, V }, 0.0f, ws);
+    if (!p->tied_output) add("output.weight", p->kquant_mix ? GGML_TYPE_Q6_K : (ggml_type) p->output_type, { E, V }, 0.0f, ws);
     for (int64_t il = 0; il < p->n_layer; il++) {
         const std::string b = "blk." + std::to_string(il) + ".";
         add(b + "attn_norm.weight", GGML_TYPE_F32, { E }, 1.0f, ns);
         if (phi3) {
             add(b + "attn_qkv.weight", wt, { E, (nh + 2 * nkv) * hd }, 0.0f, ws);
         } else {
-            add(b + "attn_q.weight", wt, { E, nh * hd }, 0.0f, ws);
+            add(b + "attn_q.weight", mix(il, 'q'), { E, nh * hd }, 0.0f, ws);
             add(b + "attn_k.weight", wt, { E, nkv * hd }, 0.0f, ws);
-            add(b + "attn_v.weight", wt, { E, nkv * hd }, 0.0f, ws);
+            add(b + "attn_v.weight", mix(il, 'v'), { E, nkv * hd }, 0.0f, ws);
             if (qwen2) {
                 add(b + "attn_q.bias", GGML_TYPE_F32, { nh * hd }, 0.0f, ws);
                 add(b + "attn_k.bias", GGML_TYPE_F32, { nkv * hd }, 0.0f, ws);
@@ -110,16 +119,16 @@ extern "C" int gl_synth_model(const char * path, const gl_synth_params * p, char
         if (moe) {
             const int64_t ne_ = p->n_expert, fe = p->n_ff_exp;
             add(b + "ffn_gate_inp.weight", GGML_TYPE_F32, { E, ne_ }, 0.0f, ws);
-            add(b + "ffn_gate_exps.weight", wt, { E, fe, ne_ }, 0.0f, ws);
-            add(b + "ffn_up_exps.weight", wt, { E, fe, ne_ }, 0.0f, ws);
-            add(b + "ffn_down_exps.weight", wt, { fe, E, ne_ }, 0.0f, ws);
+            add(b + "ffn_gate_exps.weight", mix(il, 'q'), { E, fe, ne_ }, 0.0f, ws);
+            add(b + "ffn_up_exps.weight", mix(il, 'q'), { E, fe, ne_ }, 0.0f, ws);
+            add(b + "ffn_down_exps.weight", mix(il, 'v'), { fe, E, ne_ }, 0.0f, ws);
         } else if (phi3) {
             add(b + "ffn_up.weight", wt, { E, 2 * ff }, 0.0f, ws);
             add(b + "ffn_down.weight", wt, { ff, E }, 0.0f, ws);
         } else {
-            add(b + "ffn_gate.weight", wt, { E, ff }, 0.0f, ws);
-            add(b + "ffn_up.weight", wt, { E, ff }, 0.0f, ws);
-            add(b + "ffn_down.weight", wt, { ff, E }, 0.0f, ws);
+            add(b + "ffn_gate.weight", mix(il, 'q'), { E, ff }, 0.0f, ws);
+            add(b + "ffn_up.weight", mix(il, 'q'), { E, ff }, 0.0f, ws);
+            add(b + "ffn_down.weight", mix(il, 'v'), { ff, E }, 0.0f, ws);
         }
     }
     for (const tensor_spec & s : specs) {

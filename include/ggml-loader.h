@@ -81,6 +81,7 @@ typedef struct {
     int32_t rope_scaling_orig_ctx; // non-zero: phi3 LongRoPE keys ({arch}.rope.scaling.original_context_length
                                    // = this, .rope.scaling.attn_factor) and rope_factors_short.weight
     float   rope_attn_factor;      // the LongRoPE attention factor written with those keys
+    int32_t kquant_mix;            // 1 (with wtype Q4_K): a Q4_K_M-style mix of K-quant types, see below
 } gl_synth_params;
 
 // Weights are N(0, w_std) floats from a counter-based generator (splitmix64 -> Box-Muller in
@@ -90,6 +91,10 @@ typedef struct {
 // weights stay distinct per layer, so routing still differs from layer to layer.
 // rope_scaling_orig_ctx (phi3 LongRoPE, reference model.cpp:145-153, 555-557): the frequency
 // factors rope_factors_short.weight F32[head_dim / 2] are 2 + N(0, 0.25) values (seeded).
+// kquant_mix 1 mixes types the way llama.cpp's Q4_K_M files do (the reference's published
+// workloads: README.md:162, moe_stream/VULKAN.md:646-651): output.weight Q6_K; attn_v and
+// ffn_down (ffn_down_exps) Q6_K in even layers; attn_q, ffn_gate and ffn_up (and their _exps) Q5_K
+// in odd layers; every other matrix wtype.
 GGML_API int gl_synth_model(const char * path, const gl_synth_params * p, char * err, size_t err_size);
 
 // The seeded normal generator the synthetic models use: out[i] = mean + std * z(seed, first + i).

@@ -32,6 +32,13 @@ TINY = {
     "qwen3moe": dict(arch="qwen3moe", n_embd=512, n_layer=2, n_head=8, n_head_kv=2, head_dim=64, n_ff=512,
                      n_vocab=800, n_expert=32, n_expert_used=8, n_ff_exp=256, rope_theta=1e6, rms_eps=1e-6,
                      wtype=gl.Q4_K),
+    # Q4_K_M-style K-quant mixes (the reference's published checkpoints): Q6_K output, V and down
+    # projections in even layers; Q5_K Q, gate and up in odd layers
+    "qwen3_kmix": dict(arch="qwen3", n_embd=512, n_layer=2, n_head=8, n_head_kv=2, head_dim=128, n_ff=768,
+                       n_vocab=1200, rope_theta=1e6, rms_eps=1e-6, wtype=gl.Q4_K, kquant_mix=1),
+    "qwen3moe_kmix": dict(arch="qwen3moe", n_embd=512, n_layer=2, n_head=8, n_head_kv=2, head_dim=64, n_ff=512,
+                          n_vocab=800, n_expert=32, n_expert_used=8, n_ff_exp=256, rope_theta=1e6, rms_eps=1e-6,
+                          wtype=gl.Q4_K, kquant_mix=1),
 }
 
 
@@ -70,7 +77,8 @@ def test_decode_parity_tiny(models, arch, fusion):
             tok = int(np.argmax(lc))
 
 
-@pytest.mark.parametrize("arch", ["llama", "phi3", "phi3_longrope", "qwen2", "qwen3", "qwen3moe"])
+@pytest.mark.parametrize("arch", ["llama", "phi3", "phi3_longrope", "qwen2", "qwen3", "qwen3moe", "qwen3_kmix",
+                                  "qwen3moe_kmix"])
 def test_prefill_parity_long_prompt(models, arch):
     """A 100-token prompt in one forward_step (the quantized projections run on the prefill GEMM,
     attention on the graph's own K^T Q -> softmax -> V chain), then decode steps on its KV cache."""

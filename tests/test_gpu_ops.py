@@ -51,7 +51,7 @@ def qweight(qtype, K, N, seed, std=0.02):
 
 # ---------------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K])
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K, gl.Q5_K, gl.Q6_K])
 def test_weight_repack_roundtrip(hip, qtype):
     K, N = 512, 96
     q = qweight(qtype, K, N, 1)
@@ -62,7 +62,7 @@ def test_weight_repack_roundtrip(hip, qtype):
     assert np.array_equal(back, q)
 
 
-@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K, gl.F16, gl.F32])
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K, gl.Q5_K, gl.Q6_K, gl.F16, gl.F32])
 def test_get_rows(hip, cpu, qtype):
     K, N = 512, 40
     if qtype in (gl.F16, gl.F32):
@@ -90,6 +90,13 @@ def test_get_rows(hip, cpu, qtype):
     (gl.Q4_K, 2560, 1024),
     (gl.Q4_K, 9728, 512),
     (gl.Q4_K, 768, 200),
+    (gl.Q5_K, 2560, 1024),
+    (gl.Q5_K, 9728, 512),
+    (gl.Q5_K, 768, 200),
+    (gl.Q6_K, 2560, 1024),
+    (gl.Q6_K, 9728, 512),
+    (gl.Q6_K, 4096, 300),
+    (gl.Q6_K, 256, 70),
 ])
 @pytest.mark.parametrize("ncols", [1, 3, 8, 13, 17, 40])
 def test_gemv(hip, cpu, qtype, K, N, ncols):
@@ -103,6 +110,28 @@ def test_gemv(hip, cpu, qtype, K, N, ncols):
 
     a, b = both(hip, cpu, build)
     assert np.array_equal(a, b), rel_err(a, b)
+
+
+@pytest.mark.parametrize("qtype", [gl.Q5_K, gl.Q6_K])
+@pytest.mark.parametrize("ncols", [1, 2])
+def test_gemv_kquant_lm_head_width(hip, cpu, qtype, ncols):
+    """A Q6_K (or Q5_K) output matrix wider than 32768 rows, as a Q4_K_M checkpoint's LM head: its
+    activation is quantized once (act_quant) rather than in every workgroup; a view of the upper
+    rows checks the planes' block offsets."""
+    K, N = 2560, 40000
+    w = qweight(qtype, K, N, 31)
+    x = rng(32).standard_normal((ncols, K)).astype(np.float32)
+    rb = {gl.Q5_K: 176, gl.Q6_K: 210}[qtype] * K // 256
+
+    def build(g):
+        wt = g.tensor(qtype, K, N, data=w)
+        xt = g.tensor(gl.F32, K, ncols, data=x)
+        top = g.view_2d(wt, K, 1000, rb, rb * (N - 1000))
+        return [g.mul_mat(wt, xt), g.mul_mat(top, xt)]
+
+    hs, cs = both(hip, cpu, build)
+    for a, b in zip(hs, cs):
+        assert np.array_equal(a, b), rel_err(a, b)
 
 
 @pytest.mark.parametrize("wtype", [gl.F32, gl.F16])
@@ -278,7 +307,7 @@ def test_gemm_norm_qkv_residual(hip, cpu, qtype):
             assert np.array_equal(a, b), (fusion, rel_err(a, b))
 
 
-@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q4_K])
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q4_K, gl.Q5_K, gl.Q6_K])
 def test_gemv_residual_and_qkv_group(hip, cpu, qtype):
     K = 1024
     Nq, Nk = 1024, 256
@@ -301,7 +330,7 @@ def test_gemv_residual_and_qkv_group(hip, cpu, qtype):
             assert np.array_equal(a, b), (fusion, rel_err(a, b))
 
 
-@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K])
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K, gl.Q5_K, gl.Q6_K])
 @pytest.mark.parametrize("ncols", [1, 2, 16, 21])
 def test_swiglu_ffn(hip, cpu, qtype, ncols):
     E, F = 512, 1536
@@ -341,7 +370,7 @@ def test_rms_norm_mul_then_gemv(hip, cpu, n, rows):
 
 
 @pytest.mark.parametrize("qtype,n", [(gl.Q4_0, 3072), (gl.Q8_0, 4096), (gl.Q4_K, 2560), (gl.Q4_K, 4096),
-                                     (gl.Q4_0, 96), (gl.Q4_0, 9216)])
+                                     (gl.Q4_0, 96), (gl.Q4_0, 9216), (gl.Q5_K, 2560), (gl.Q6_K, 3072)])
 @pytest.mark.parametrize("ncols", [1, 3])
 def test_rms_norm_folded_into_gemv(hip, cpu, qtype, n, ncols):
     """rms_norm * w read only by GEMVs (Q, K and V; a gate/up pair with SwiGLU): the GEMVs compute
@@ -801,7 +830,7 @@ def test_argsort_sum_rows_div(hip, cpu, n):
     assert np.array_equal(hs[0].view(np.int32).reshape(3, n), np.argsort(-x, axis=1, kind="stable"))
 
 
-@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K])
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K, gl.Q5_K, gl.Q6_K])
 @pytest.mark.parametrize("n_tok", [1, 3, 16, 37])
 def test_moe_ffn(hip, cpu, qtype, n_tok):
     """The routed expert FFN (router, top-k, renormalized weights, mul_mat_id gate/up/down, SwiGLU,
@@ -824,7 +853,11 @@ def test_moe_ffn(hip, cpu, qtype, n_tok):
         assert np.array_equal(a, b), (fusion, rel_err(a, b))
     _, names = profiled(hip, lambda: run_on(hip, build))
     assert "moe_route" in names and "argsort" not in names, names
-    assert (n_tok >= 2) == ("moe_group" in names), names   # several tokens: experts read once for all of theirs
+    if qtype in (gl.Q5_K, gl.Q6_K):
+        # no multi-column kernel for these types: each (token, slot) column reads its expert
+        assert "moe_group" not in names, names
+    else:
+        assert (n_tok >= 2) == ("moe_group" in names), names   # several tokens: experts read once for all of theirs
 
 
 @pytest.mark.parametrize("n_tok", [1, 5])
