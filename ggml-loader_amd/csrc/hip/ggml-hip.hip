@@ -1121,7 +1121,8 @@ private:
         const bool wide = cols >= GEMM_MIN_COLS || (cols >= GEMM_WIDE_MIN_COLS && mm->src[0]->ne[1] >= GEMM_WIDE_MIN_ROWS);
         return mm->op == GGML_OP_MUL_MAT && wide && gemv_capable(mm) &&
                gemm_supported(mm->src[0]->type, mm->src[0]->ne[0], mm->src[0]->ne[1]) &&
-               (mm->nb[1] / sizeof(float)) % 4 == 0 && ((uintptr_t) mm->data) % 16 == 0;
+               (mm->nb[1] / sizeof(float)) % 4 == 0 && ((uintptr_t) mm->data) % 16 == 0 &&
+               (is_repacked(mm->src[0]->type) || ((uintptr_t) mm->src[0]->data) % 16 == 0);
     }
     bool gemm_consumer(int u) const {
         for (int j : users_[u]) if (gemm_route(g_->nodes[j])) return true;
@@ -1140,7 +1141,15 @@ private:
         G.n_rows = w->ne[1];
         G.ncols = x->ne[1];
         if (kind == 2) {
-            G.w = (const uint8_t *) w->data;
+            if (w->type == GGML_TYPE_Q6_K) {
+                const planes p = planes_of(w);
+                G.w = p.qs + p.first_block * 128;
+                G.wqh = p.qh + p.first_block * 64;
+                G.wsc = p.sc + p.first_block * 16;
+                G.wd = p.d + p.first_block;
+            } else {
+                G.w = (const uint8_t *) w->data;
+            }
             G.xq = xa->q8k.qs;
             G.xd = xa->q8k.d;
             G.xbs = xa->q8k.bsums;
@@ -1174,8 +1183,7 @@ private:
         }
         {
             // named with the workgroup tile, e.g. gemm_q8_0_2x4x2
-            const std::string pname = std::string(w->type == GGML_TYPE_Q4_0 ? "gemm_q4_0" : w->type == GGML_TYPE_Q4_K ? "gemm_q4_K" : "gemm_q8_0") +
-                                      "_" + gemm_tile_name(G);
+            const std::string pname = std::string("gemm_") + ggml_type_name(w->type) + "_" + gemm_tile_name(G);
             prof_scope ps(this, pname.c_str(), bytes);
             launch_gemm(G, st_);
         }

@@ -21,7 +21,7 @@
 // receives the results of rows 4(l/16)..4(l/16)+3 of column l%16. Workgroups are numbered so that
 // the column tiles of one row tile run on one XCD and share its L2.
 //
-// Q4_K weights run on gemm_q4k_kernel (below) against Q8_K activation columns.
+// Q4_K, Q5_K and Q6_K weights run on gemm_k_kernel (below) against Q8_K activation columns.
 #include "kernels.h"
 #include "gemv_ops.h"
 
@@ -229,20 +229,25 @@ __global__ __launch_bounds__(256, WTM == 1 ? 4 : 1) void gemm_q_kernel(const gem
 }
 
 // ---------------------------------------------------------------------------------------------
-// Q4_K x Q8_K. ggml-cpu's generic q4_K x q8_K dot (ggml-cpu/arch-fallback: the oracle's
-// oracle_vec_dot_q4_K_q8_K) keeps eight float accumulators per output, one per element index mod 8:
-// for every 256-element super-block, aux32[l] = sum over the 32 elements e = 8k + l of
-// sc[e / 32] * q4[e] * q8[e] (an exact integer), sums[l] += (d_w * d_x) * aux32[l]; the mins act as
-// sumf -= (dmin_w * d_x) * sum_j bsums[j] * m[j / 2]; the output is sumf + sums[0] + ... + sums[7].
+// K-quants x Q8_K. ggml-cpu's generic q4_K / q5_K / q6_K x q8_K dots (ggml-cpu/arch-fallback: the
+// oracle's oracle_vec_dot_q{4,5,6}_K_q8_K) keep eight float accumulators per output, one per
+// element index mod 8: for every 256-element super-block, aux32[l] = sum over the 32 elements
+// e = 8k + l of sc[sub-block of e] * q[e] * q8[e] (an exact integer), sums[l] += (d_w * d_x) *
+// aux32[l]; Q4_K and Q5_K subtract their mins as sumf -= (dmin_w * d_x) * sum_j bsums[j] * m[j / 2];
+// the output is sumf + sums[0] + ... + sums[7].
 // Staged in LDS as f16 in the order p = 32 l + k, each l-slice of a super-block is one contiguous
 // 32-element run, so one v_mfma_f32_16x16x32_f16 per slice yields aux32[l] for a 16 x 16 tile: the
-// weight operand is sc * q4 (at most 63 * 15 = 945, exact in f16) and every product and partial
-// sum is an integer below 2^24. The mins term is one v_mfma_f32_16x16x16_f16 of the mins (each
-// repeated for its two 16-element halves) against the 16 bsums (|bsum| <= 16 * 127, exact in f16).
-// Per output the kernel holds the 9 accumulators in registers and adds them in ggml's order, so
-// every output is the GEMV's and the CPU reference's float. A stage is one super-block of the
-// workgroup's rows and columns; the next stage's global loads are in flight while the current one
-// is reduced.
+// weight operand is sc * q, exact in f16 for Q4_K (at most 63 * 15 = 945) and Q5_K (63 * 31 =
+// 1953), and every product and partial sum is an integer of magnitude at most 2^24. Q6_K's
+// sc * (q - 32) reaches 4096 in magnitude, and above 2048 f16 holds only even integers: it is
+// staged as two f16 parts, hi = sc * (q - 32) rounded to f16 and lo = the remainder (-1, 0 or 1,
+// exact from one fused multiply-add), and aux32[l] = mfma(hi) + mfma(lo): two exact integers whose
+// sum, aux32[l] itself, is at most 32 * 4096 * 127 < 2^24. The mins term is one
+// v_mfma_f32_16x16x16_f16 of the mins (each repeated for its two 16-element halves) against the 16
+// bsums (|bsum| <= 16 * 127, exact in f16). Per output the kernel holds the 9 accumulators in
+// registers and adds them in ggml's order, so every output is the GEMV's and the CPU reference's
+// float. A stage is one super-block of the workgroup's rows and columns; the next stage's global
+// loads are in flight while the current one is reduced.
 
 // 4 nibbles (0..15 in the byte lanes of n) -> 4 f16 of value nibble * sc, exact
 __device__ __forceinline__ void u4x4_scaled(uint32_t n, __half2 sc, uint32_t & lo, uint32_t & hi) {
@@ -253,28 +258,57 @@ __device__ __forceinline__ void u4x4_scaled(uint32_t n, __half2 sc, uint32_t & l
     hi = __builtin_bit_cast(uint32_t, __hmul2(__hadd2(__builtin_bit_cast(__half2, hi), bias), sc));
 }
 
+// 4 biased 6-bit quants (q in 0..63 in the byte lanes of n) times the scales sa (lanes 0, 1) and sb
+// (lanes 2, 3) as two f16 parts: hi = sc * (q - 32) rounded to f16, lo = sc * (q - 32) - hi exactly
+// (one fused multiply-add; -1, 0 or 1)
+__device__ __forceinline__ void q6x4_split(uint32_t n, __half2 sa, __half2 sb, uint32_t & h0, uint32_t & h1,
+                                           uint32_t & l0, uint32_t & l1) {
+    const __half2 bias = __halves2half2(__ushort_as_half(0xE420), __ushort_as_half(0xE420));   // -1056
+    const __half2 qa = __hadd2(__builtin_bit_cast(__half2, __builtin_amdgcn_perm(0x64646464u, n, 0x04010400u)), bias);
+    const __half2 qb = __hadd2(__builtin_bit_cast(__half2, __builtin_amdgcn_perm(0x64646464u, n, 0x04030402u)), bias);
+    const __half2 ha = __hmul2(qa, sa), hb = __hmul2(qb, sb);
+    h0 = __builtin_bit_cast(uint32_t, ha);
+    h1 = __builtin_bit_cast(uint32_t, hb);
+    l0 = __builtin_bit_cast(uint32_t, __hfma2(qa, sa, __hneg2(ha)));
+    l1 = __builtin_bit_cast(uint32_t, __hfma2(qb, sb, __hneg2(hb)));
+}
+
+// int8 byte b of v as an f16 pair (exact)
+__device__ __forceinline__ __half2 sbyte_h2(uint32_t v, int b) {
+    const __half h = __short2half_rn((short) (int8_t) (v >> (8 * b)));
+    return __halves2half2(h, h);
+}
+
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-template <int WTM, int WTN>
+template <int TYPE, int WTM, int WTN>
 struct gemm_k_cfg {
+    static constexpr bool Q6 = TYPE == GGML_TYPE_Q6_K;
+    static constexpr bool MINS = !Q6;
+    static constexpr int BLK = TYPE == GGML_TYPE_Q4_K ? 144 : 176;        // Q4_K / Q5_K block bytes (GGUF layout)
     static constexpr int BM = 32 * WTM, BN = 32 * WTN;
     static constexpr int ROW = 256 + 8;                                    // f16 per LDS row (16-byte pad)
-    static constexpr int UA = (BM * 4 + 255) / 256, UB = (BN * 4 + 255) / 256;   // (row | column, sub-block pair) units per thread
-    static constexpr size_t LDS = (size_t) (BM + BN) * ROW * 2 + (size_t) (BM + BN) * 16 * 2 + (size_t) (2 * BM + BN) * 4;
+    static constexpr int UPR = Q6 ? 2 : 4;                                 // staging units per weight row and super-block
+    static constexpr int UA = (BM * UPR + 255) / 256, UB = (BN * 4 + 255) / 256;
+    static constexpr int A_PARTS = Q6 ? 2 : 1;
+    static constexpr size_t LDS = (size_t) (A_PARTS * BM + BN) * ROW * 2 + (MINS ? (size_t) (BM + BN) * 16 * 2 : 0) +
+                                  (size_t) ((MINS ? 2 : 1) * BM + BN) * 4;
 };
 
-template <int WTM, int WTN>
-__global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const gemm_launch G) {
-    using C = gemm_k_cfg<WTM, WTN>;
-    constexpr int BM = C::BM, BN = C::BN, ROW = C::ROW;
+template <int TYPE, int WTM, int WTN>
+__global__ __launch_bounds__(256, 2) void gemm_k_kernel(const gemm_launch G) {
+    using C = gemm_k_cfg<TYPE, WTM, WTN>;
+    constexpr bool Q6 = C::Q6, MINS = C::MINS;
+    constexpr int BM = C::BM, BN = C::BN, ROW = C::ROW, UPR = C::UPR;
     extern __shared__ __align__(16) uint8_t g_lds[];
-    _Float16 * sA = (_Float16 *) g_lds;            // [BM][ROW]: sc * q4 of the super-block, slice-major
-    _Float16 * sB = sA + BM * ROW;                 // [BN][ROW]: q8, same order
-    _Float16 * sM = sB + BN * ROW;                 // [BM][16]: the min of 16-element group j (m[j / 2])
-    _Float16 * sS = sM + BM * 16;                  // [BN][16]: bsums
-    float * sdw = (float *) (sS + BN * 16);        // [BM] d
-    float * sdm = sdw + BM;                        // [BM] dmin
-    float * sdx = sdm + BM;                        // [BN] activation d
+    _Float16 * sA = (_Float16 *) g_lds;                     // [BM][ROW]: sc * q of the super-block (Q6_K: hi), slice-major
+    _Float16 * sL = sA + BM * ROW;                          // Q6_K [BM][ROW]: lo
+    _Float16 * sB = sL + (Q6 ? BM * ROW : 0);               // [BN][ROW]: q8, same order
+    _Float16 * sM = sB + BN * ROW;                          // Q4_K / Q5_K [BM][16]: the min of 16-element group j (m[j / 2])
+    _Float16 * sS = sM + (MINS ? BM * 16 : 0);              // Q4_K / Q5_K [BN][16]: bsums
+    float * sdw = (float *) (sS + (MINS ? BN * 16 : 0));    // [BM] d
+    float * sdm = sdw + BM;                                 // Q4_K / Q5_K [BM] dmin
+    float * sdx = sdm + (MINS ? BM : 0);                    // [BN] activation d
 
     const int64_t M = G.n_rows, N = G.ncols, K = G.K, nsb = K / 256;
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
@@ -286,21 +320,45 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const gemm_launch G) {
     const int64_t m0 = (t / n_ct) * BM, n0 = (t % n_ct) * BN;
     const int wr = (wave / 2) * 16 * WTM, wc = (wave % 2) * 16 * WTN;
 
-    // staging units u = (row or column u / 4, sub-block pair u % 4); rows / columns past the end
-    // repeat the last one
-    uint4 rh[C::UA], rq[C::UA][2], rx[C::UB][4];
-    uint2 rs[C::UB];
+    // staging units: weights u = (row u / UPR, sub-block pair u % 4 | Q6_K: 128-element half u % 2),
+    // activations u = (column u / 4, sub-block pair u % 4); rows / columns past the end repeat the
+    // last one
+    uint4 rh[C::UA], rq[C::UA][Q6 ? 4 : 2], rqh[C::UA][2], rx[C::UB][4];
+    uint2 rsc[C::UA], rs[C::UB];
+    __half rdq[C::UA];
     float rd[C::UB];
     auto load = [&](int64_t sb) {
 #pragma unroll
         for (int k = 0; k < C::UA; k++) {
             const int u = tid + 256 * k;
-            if (u < BM * 4) {
-                const int64_t row = min(m0 + u / 4, M - 1);
-                const uint4 * p = (const uint4 *) (G.w + (row * nsb + sb) * 144);
-                rh[k] = p[0];
-                rq[k][0] = p[1 + 2 * (u % 4)];
-                rq[k][1] = p[2 + 2 * (u % 4)];
+            if (u < BM * UPR) {
+                const int64_t row = min(m0 + u / UPR, M - 1);
+                const int64_t blk = row * nsb + sb;
+                const int p = u % UPR;
+                if constexpr (Q6) {
+                    // planes: low bits [blocks][128], high bits [blocks][64], scales [blocks][16], d
+                    const uint4 * ql = (const uint4 *) (G.w + blk * 128 + 64 * p);
+                    const uint4 * qh = (const uint4 *) (G.wqh + blk * 64 + 32 * p);
+#pragma unroll
+                    for (int v = 0; v < 4; v++) rq[k][v] = ql[v];
+                    rqh[k][0] = qh[0];
+                    rqh[k][1] = qh[1];
+                    rsc[k] = *(const uint2 *) (G.wsc + blk * 16 + 8 * p);
+                    rdq[k] = G.wd[blk];
+                } else {
+                    const uint4 * b = (const uint4 *) (G.w + blk * C::BLK);
+                    rh[k] = b[0];
+                    if constexpr (TYPE == GGML_TYPE_Q5_K) {
+                        // d, dmin, scales | qh[32] | qs[128]
+                        rqh[k][0] = b[1];
+                        rqh[k][1] = b[2];
+                        rq[k][0] = b[3 + 2 * p];
+                        rq[k][1] = b[4 + 2 * p];
+                    } else {
+                        rq[k][0] = b[1 + 2 * p];
+                        rq[k][1] = b[2 + 2 * p];
+                    }
+                }
             }
         }
 #pragma unroll
@@ -311,7 +369,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const gemm_launch G) {
                 const uint4 * p = (const uint4 *) (G.xq + col * K + sb * 256 + 64 * (u % 4));
 #pragma unroll
                 for (int v = 0; v < 4; v++) rx[k][v] = p[v];
-                rs[k] = *(const uint2 *) (G.xbs + col * (K / 16) + sb * 16 + 4 * (u % 4));
+                if constexpr (MINS) rs[k] = *(const uint2 *) (G.xbs + col * (K / 16) + sb * 16 + 4 * (u % 4));
                 rd[k] = G.xd[col * nsb + sb];
             }
         }
@@ -320,27 +378,74 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const gemm_launch G) {
 #pragma unroll
         for (int k = 0; k < C::UA; k++) {
             const int u = tid + 256 * k;
-            if (u < BM * 4) {
-                const int r = u / 4, p = u % 4;
-                int sca, ma, scb, mb;
-                q4k_sc_m(rh[k].y, rh[k].z, rh[k].w, 2 * p, sca, ma);
-                q4k_sc_m(rh[k].y, rh[k].z, rh[k].w, 2 * p + 1, scb, mb);
-                uint32_t w[8] = { rq[k][0].x, rq[k][0].y, rq[k][0].z, rq[k][0].w, rq[k][1].x, rq[k][1].y, rq[k][1].z, rq[k][1].w };
-                q4k_group_by_l(w);      // dword l: the pair's bytes l, l+8, l+16, l+24
-                const __half2 ha = __float2half2_rn((float) sca), hb = __float2half2_rn((float) scb);
+            if (u < BM * UPR) {
+                const int r = u / UPR, p = u % UPR;
+                if constexpr (Q6) {
+                    // half p: ql bytes 0-31 (a) and 32-63 (b), qh bytes 0-31; element 128 p + 32 m + j
+                    // for byte j takes nibble m / 2 of a (m even) or b (m odd) and qh bits 2m, 2m + 1,
+                    // and scale 8 p + 2 m + j / 16. Grouped by l, dword l holds bytes j = l + 8 t
+                    // (t = 0..3): elements k = 16 p + 4 m + t of slice l, scales 2 m (t < 2), 2 m + 1.
+                    uint32_t a[8] = { rq[k][0].x, rq[k][0].y, rq[k][0].z, rq[k][0].w, rq[k][1].x, rq[k][1].y, rq[k][1].z, rq[k][1].w };
+                    uint32_t b[8] = { rq[k][2].x, rq[k][2].y, rq[k][2].z, rq[k][2].w, rq[k][3].x, rq[k][3].y, rq[k][3].z, rq[k][3].w };
+                    uint32_t h[8] = { rqh[k][0].x, rqh[k][0].y, rqh[k][0].z, rqh[k][0].w, rqh[k][1].x, rqh[k][1].y, rqh[k][1].z, rqh[k][1].w };
+                    q4k_group_by_l(a);
+                    q4k_group_by_l(b);
+                    q4k_group_by_l(h);
+                    __half2 sc[8];
 #pragma unroll
-                for (int l = 0; l < 8; l++) {
-                    // k = 8p + 0..3: sub-block 2p (low nibbles); k = 8p + 4..7: sub-block 2p + 1
-                    uint32_t l0, h0, l1, h1;
-                    u4x4_scaled(w[l] & 0x0F0F0F0Fu, ha, l0, h0);
-                    u4x4_scaled((w[l] >> 4) & 0x0F0F0F0Fu, hb, l1, h1);
-                    *(uint4 *) (sA + r * ROW + l * 32 + 8 * p) = make_uint4(l0, h0, l1, h1);
-                }
-                const __half2 mma = __float2half2_rn((float) ma), mmb = __float2half2_rn((float) mb);
-                *(uint2 *) (sM + r * 16 + 4 * p) = make_uint2(__builtin_bit_cast(uint32_t, mma), __builtin_bit_cast(uint32_t, mmb));
-                if (p == 0) {
-                    sdw[r] = __half2float(__ushort_as_half((unsigned short) (rh[k].x & 0xffff)));
-                    sdm[r] = __half2float(__ushort_as_half((unsigned short) (rh[k].x >> 16)));
+                    for (int g = 0; g < 8; g++) sc[g] = sbyte_h2(g < 4 ? rsc[k].x : rsc[k].y, g % 4);
+#pragma unroll
+                    for (int l = 0; l < 8; l++) {
+                        const uint32_t v[4] = {
+                            (a[l] & 0x0F0F0F0Fu) | ((h[l] & 0x03030303u) << 4),
+                            (b[l] & 0x0F0F0F0Fu) | (((h[l] >> 2) & 0x03030303u) << 4),
+                            ((a[l] >> 4) & 0x0F0F0F0Fu) | (((h[l] >> 4) & 0x03030303u) << 4),
+                            ((b[l] >> 4) & 0x0F0F0F0Fu) | (((h[l] >> 6) & 0x03030303u) << 4),
+                        };
+                        uint32_t hi[8], lo[8];
+#pragma unroll
+                        for (int m = 0; m < 4; m++) q6x4_split(v[m], sc[2 * m], sc[2 * m + 1], hi[2 * m], hi[2 * m + 1], lo[2 * m], lo[2 * m + 1]);
+                        uint4 * dh = (uint4 *) (sA + r * ROW + l * 32 + 16 * p);
+                        uint4 * dl = (uint4 *) (sL + r * ROW + l * 32 + 16 * p);
+                        dh[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                        dh[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+                        dl[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                        dl[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+                    }
+                    if (p == 0) sdw[r] = __half2float(rdq[k]);
+                } else {
+                    int sca, ma, scb, mb;
+                    q4k_sc_m(rh[k].y, rh[k].z, rh[k].w, 2 * p, sca, ma);
+                    q4k_sc_m(rh[k].y, rh[k].z, rh[k].w, 2 * p + 1, scb, mb);
+                    uint32_t w[8] = { rq[k][0].x, rq[k][0].y, rq[k][0].z, rq[k][0].w, rq[k][1].x, rq[k][1].y, rq[k][1].z, rq[k][1].w };
+                    q4k_group_by_l(w);      // dword l: the pair's bytes l, l+8, l+16, l+24
+                    uint32_t h[8];
+                    if constexpr (TYPE == GGML_TYPE_Q5_K) {
+                        // the fifth bit of byte j's low nibble is bit 2 p of qh[j], of its high nibble bit 2 p + 1
+                        h[0] = rqh[k][0].x; h[1] = rqh[k][0].y; h[2] = rqh[k][0].z; h[3] = rqh[k][0].w;
+                        h[4] = rqh[k][1].x; h[5] = rqh[k][1].y; h[6] = rqh[k][1].z; h[7] = rqh[k][1].w;
+                        q4k_group_by_l(h);
+                    }
+                    const __half2 ha = __float2half2_rn((float) sca), hb = __float2half2_rn((float) scb);
+#pragma unroll
+                    for (int l = 0; l < 8; l++) {
+                        // k = 8p + 0..3: sub-block 2p (low nibbles); k = 8p + 4..7: sub-block 2p + 1
+                        uint32_t nl = w[l] & 0x0F0F0F0Fu, nh = (w[l] >> 4) & 0x0F0F0F0Fu;
+                        if constexpr (TYPE == GGML_TYPE_Q5_K) {
+                            nl |= ((h[l] >> (2 * p)) & 0x01010101u) << 4;
+                            nh |= ((h[l] >> (2 * p + 1)) & 0x01010101u) << 4;
+                        }
+                        uint32_t l0, h0, l1, h1;
+                        u4x4_scaled(nl, ha, l0, h0);
+                        u4x4_scaled(nh, hb, l1, h1);
+                        *(uint4 *) (sA + r * ROW + l * 32 + 8 * p) = make_uint4(l0, h0, l1, h1);
+                    }
+                    const __half2 mma = __float2half2_rn((float) ma), mmb = __float2half2_rn((float) mb);
+                    *(uint2 *) (sM + r * 16 + 4 * p) = make_uint2(__builtin_bit_cast(uint32_t, mma), __builtin_bit_cast(uint32_t, mmb));
+                    if (p == 0) {
+                        sdw[r] = __half2float(__ushort_as_half((unsigned short) (rh[k].x & 0xffff)));
+                        sdm[r] = __half2float(__ushort_as_half((unsigned short) (rh[k].x >> 16)));
+                    }
                 }
             }
         }
@@ -364,9 +469,11 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const gemm_launch G) {
                     i8x4_to_f16(l < 4 ? tb[l] : td[l - 4], b0, b1);
                     *(uint4 *) (sB + cc * ROW + l * 32 + 8 * p) = make_uint4(a0, a1, b0, b1);
                 }
-                const __half2 s01 = __halves2half2(__short2half_rn((short) (rs[k].x & 0xffff)), __short2half_rn((short) (rs[k].x >> 16)));
-                const __half2 s23 = __halves2half2(__short2half_rn((short) (rs[k].y & 0xffff)), __short2half_rn((short) (rs[k].y >> 16)));
-                *(uint2 *) (sS + cc * 16 + 4 * p) = make_uint2(__builtin_bit_cast(uint32_t, s01), __builtin_bit_cast(uint32_t, s23));
+                if constexpr (MINS) {
+                    const __half2 s01 = __halves2half2(__short2half_rn((short) (rs[k].x & 0xffff)), __short2half_rn((short) (rs[k].x >> 16)));
+                    const __half2 s23 = __halves2half2(__short2half_rn((short) (rs[k].y & 0xffff)), __short2half_rn((short) (rs[k].y >> 16)));
+                    *(uint2 *) (sS + cc * 16 + 4 * p) = make_uint2(__builtin_bit_cast(uint32_t, s01), __builtin_bit_cast(uint32_t, s23));
+                }
                 if (p == 0) sdx[cc] = rd[k];
             }
         }
@@ -397,41 +504,55 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const gemm_launch G) {
 #pragma unroll
             for (int i = 0; i < WTM; i++) {
                 dw[i] = *(const f32x4 *) (sdw + wr + 16 * i + 4 * q);
-                dm[i] = *(const f32x4 *) (sdm + wr + 16 * i + 4 * q);
+                if constexpr (MINS) dm[i] = *(const f32x4 *) (sdm + wr + 16 * i + 4 * q);
             }
-            f16x4 am[WTM], bm[WTN];
 #pragma unroll
-            for (int i = 0; i < WTM; i++) am[i] = *(const f16x4 *) (sM + (wr + 16 * i + c) * 16 + 4 * q);
-#pragma unroll
-            for (int j = 0; j < WTN; j++) {
-                dx[j] = sdx[wc + 16 * j + c];
-                bm[j] = *(const f16x4 *) (sS + (wc + 16 * j + c) * 16 + 4 * q);
-            }
+            for (int j = 0; j < WTN; j++) dx[j] = sdx[wc + 16 * j + c];
 #pragma unroll
             for (int i = 0; i < WTM; i++)
 #pragma unroll
-                for (int j = 0; j < WTN; j++) {
-                    const f32x4 mv = __builtin_amdgcn_mfma_f32_16x16x16f16(am[i], bm[j], f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+                for (int j = 0; j < WTN; j++)
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        dd[i][j][r] = dw[i][r] * dx[j];
-                        const float dmin = dm[i][r] * dx[j];
-                        mins[i][j][r] = mins[i][j][r] - dmin * mv[r];
+                    for (int r = 0; r < 4; r++) dd[i][j][r] = dw[i][r] * dx[j];
+            if constexpr (MINS) {
+                f16x4 am[WTM], bm[WTN];
+#pragma unroll
+                for (int i = 0; i < WTM; i++) am[i] = *(const f16x4 *) (sM + (wr + 16 * i + c) * 16 + 4 * q);
+#pragma unroll
+                for (int j = 0; j < WTN; j++) bm[j] = *(const f16x4 *) (sS + (wc + 16 * j + c) * 16 + 4 * q);
+#pragma unroll
+                for (int i = 0; i < WTM; i++)
+#pragma unroll
+                    for (int j = 0; j < WTN; j++) {
+                        const f32x4 mv = __builtin_amdgcn_mfma_f32_16x16x16f16(am[i], bm[j], f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const float dmin = dm[i][r] * dx[j];
+                            mins[i][j][r] = mins[i][j][r] - dmin * mv[r];
+                        }
                     }
-                }
+            }
         }
 #pragma unroll
         for (int l = 0; l < 8; l++) {
-            f16x8 a[WTM], b[WTN];
+            f16x8 a[WTM], al[WTM], b[WTN];
 #pragma unroll
-            for (int i = 0; i < WTM; i++) a[i] = *(const f16x8 *) (sA + (wr + 16 * i + c) * ROW + l * 32 + 8 * q);
+            for (int i = 0; i < WTM; i++) {
+                a[i] = *(const f16x8 *) (sA + (wr + 16 * i + c) * ROW + l * 32 + 8 * q);
+                if constexpr (Q6) al[i] = *(const f16x8 *) (sL + (wr + 16 * i + c) * ROW + l * 32 + 8 * q);
+            }
 #pragma unroll
             for (int j = 0; j < WTN; j++) b[j] = *(const f16x8 *) (sB + (wc + 16 * j + c) * ROW + l * 32 + 8 * q);
 #pragma unroll
             for (int i = 0; i < WTM; i++)
 #pragma unroll
                 for (int j = 0; j < WTN; j++) {
-                    const f32x4 sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+                    f32x4 sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+                    if constexpr (Q6) {
+                        const f32x4 sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], f32x4{ 0.0f, 0.0f, 0.0f, 0.0f }, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; r++) sv[r] = sv[r] + sl[r];
+                    }
 #pragma unroll
                     for (int r = 0; r < 4; r++) sums[i][j][l][r] = sums[i][j][l][r] + dd[i][j][r] * sv[r];
                 }
@@ -469,17 +590,17 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const gemm_launch G) {
     }
 }
 
-template <int WTM, int WTN>
-void launch_gemm_q4k_t(const gemm_launch & G, hipStream_t st) {
-    using C = gemm_k_cfg<WTM, WTN>;
+template <int TYPE, int WTM, int WTN>
+void launch_gemm_k_t(const gemm_launch & G, hipStream_t st) {
+    using C = gemm_k_cfg<TYPE, WTM, WTN>;
     static bool attr = false;
     if (!attr && C::LDS > 65536) {
-        HIP_CHECK(hipFuncSetAttribute((const void *) gemm_q4k_kernel<WTM, WTN>,
+        HIP_CHECK(hipFuncSetAttribute((const void *) gemm_k_kernel<TYPE, WTM, WTN>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int) C::LDS));
     }
     attr = true;
     const int64_t tiles = ((G.n_rows + C::BM - 1) / C::BM) * ((G.ncols + C::BN - 1) / C::BN);
-    launch(gemm_q4k_kernel<WTM, WTN>, dim3((unsigned) tiles), dim3(256), C::LDS, st, G);
+    launch(gemm_k_kernel<TYPE, WTM, WTN>, dim3((unsigned) tiles), dim3(256), C::LDS, st, G);
 }
 
 template <int TYPE, int WTM, int WTN, int KB>
@@ -499,13 +620,15 @@ int64_t n_tiles(const gemm_launch & G, int bm, int bn) { return ((G.n_rows + bm 
 
 // The workgroup tile of a launch. Q4_0 / Q8_0: the largest tile that still gives every CU two
 // workgroups (Q4_0) or four (Q8_0, whose staging moves twice the weight bytes per block; measured:
-// Phi-3 prefill 26.1 -> 24.9 ms, while Q4_0 is slower with the smaller tiles). Q4_K: 64 x 64 tiles
-// where they give every CU a workgroup, else 32 x 64 (measured: the larger tile is faster down to
-// one workgroup per CU).
-enum gemm_tile { TILE_4x4x2, TILE_2x4x2, TILE_1x2x4, TILE_Q4K_2x2, TILE_Q4K_1x2 };
+// Phi-3 prefill 26.1 -> 24.9 ms, while Q4_0 is slower with the smaller tiles). K-quants: 64 x 64
+// tiles where they give every CU a workgroup, else 32 x 64 (measured on Q4_K: the larger tile is
+// faster down to one workgroup per CU).
+enum gemm_tile { TILE_4x4x2, TILE_2x4x2, TILE_1x2x4, TILE_K_2x2, TILE_K_1x2 };
+
+bool is_k_type(int type) { return type == GGML_TYPE_Q4_K || type == GGML_TYPE_Q5_K || type == GGML_TYPE_Q6_K; }
 
 gemm_tile tile_of(const gemm_launch & G) {
-    if (G.type == GGML_TYPE_Q4_K) return n_tiles(G, 64, 64) >= 256 ? TILE_Q4K_2x2 : TILE_Q4K_1x2;
+    if (is_k_type(G.type)) return n_tiles(G, 64, 64) >= 256 ? TILE_K_2x2 : TILE_K_1x2;
     const int64_t target = G.type == GGML_TYPE_Q8_0 ? 1024 : 512;
     if (n_tiles(G, 128, 128) >= target) return TILE_4x4x2;
     if (n_tiles(G, 64, 128) >= target) return TILE_2x4x2;
@@ -528,13 +651,13 @@ const char * gemm_tile_name(const gemm_launch & G) {
         case TILE_4x4x2: return "4x4x2";
         case TILE_2x4x2: return "2x4x2";
         case TILE_1x2x4: return "1x2x4";
-        case TILE_Q4K_2x2: return "2x2";
+        case TILE_K_2x2: return "2x2";
         default: return "1x2";
     }
 }
 
 bool gemm_supported(int type, int64_t K, int64_t n_rows) {
-    if (type == GGML_TYPE_Q4_K) return K > 0 && K % 256 == 0 && n_rows > 0;
+    if (is_k_type(type)) return K > 0 && K % 256 == 0 && n_rows > 0;
     return (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0) && K > 0 && K % 128 == 0 && n_rows > 0;
 }
 
@@ -547,10 +670,18 @@ void launch_gemm(const gemm_launch & G, hipStream_t st) {
     if (align % 16 || G.y_stride % 4 || (G.add && G.add_stride % 4)) {
         HIP_ABORT("gemm: operands must be 16-byte aligned with strides of whole float4s");
     }
-    if (G.type == GGML_TYPE_Q4_K) {
-        if (!G.xbs || ((uintptr_t) G.xbs % 8) || ((uintptr_t) G.xd % 4)) HIP_ABORT("gemm: Q4_K needs Q8_K columns with 8-byte aligned bsums");
-        if (tile_of(G) == TILE_Q4K_2x2) launch_gemm_q4k_t<2, 2>(G, st);
-        else launch_gemm_q4k_t<1, 2>(G, st);
+    if (is_k_type(G.type)) {
+        if (G.type != GGML_TYPE_Q6_K && (!G.xbs || ((uintptr_t) G.xbs % 8))) HIP_ABORT("gemm: Q4_K / Q5_K need Q8_K columns with 8-byte aligned bsums");
+        if ((uintptr_t) G.xd % 4) HIP_ABORT("gemm: misaligned Q8_K scales");
+        if (G.type == GGML_TYPE_Q6_K && (!G.wqh || !G.wsc || !G.wd || ((uintptr_t) G.wqh % 16) || ((uintptr_t) G.wsc % 8))) {
+            HIP_ABORT("gemm: Q6_K needs its high-bit plane 16-byte and its scale plane 8-byte aligned");
+        }
+        const bool big = tile_of(G) == TILE_K_2x2;
+        switch (G.type) {
+            case GGML_TYPE_Q4_K: big ? launch_gemm_k_t<GGML_TYPE_Q4_K, 2, 2>(G, st) : launch_gemm_k_t<GGML_TYPE_Q4_K, 1, 2>(G, st); break;
+            case GGML_TYPE_Q5_K: big ? launch_gemm_k_t<GGML_TYPE_Q5_K, 2, 2>(G, st) : launch_gemm_k_t<GGML_TYPE_Q5_K, 1, 2>(G, st); break;
+            default: big ? launch_gemm_k_t<GGML_TYPE_Q6_K, 2, 2>(G, st) : launch_gemm_k_t<GGML_TYPE_Q6_K, 1, 2>(G, st); break;
+        }
         return;
     }
     if (G.type == GGML_TYPE_Q4_0) launch_gemm_type<GGML_TYPE_Q4_0>(G, st);

@@ -104,12 +104,14 @@ constexpr int GEMM_WIDE_MIN_COLS = 16;
 constexpr int64_t GEMM_WIDE_MIN_ROWS = 65536;
 
 struct gemm_launch {
-    int             type;      // GGML_TYPE_Q4_0 / Q8_0 / Q4_K
-    int64_t         K;         // row length (a multiple of 128; of 256 for Q4_K)
+    int             type;      // GGML_TYPE_Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K
+    int64_t         K;         // row length (a multiple of 128; of 256 for the K-quants)
     int64_t         n_rows;
     int64_t         ncols;
-    const uint8_t * w;         // Q4_0 / Q8_0: qs plane of row 0; Q4_K: row 0's first block
-    const __half *  wd;        // Q4_0 / Q8_0: d plane of row 0
+    const uint8_t * w;         // Q4_0 / Q8_0: qs plane of row 0; Q4_K / Q5_K: row 0's first block; Q6_K: its low-bit plane
+    const __half *  wd;        // Q4_0 / Q8_0 / Q6_K: d plane of row 0
+    const uint8_t * wqh;       // Q6_K: high-bit plane of row 0 (64 bytes per block)
+    const int8_t *  wsc;       // Q6_K: scale plane of row 0 (16 per block)
     const int8_t *  xq;        // activation column c at xq + c * K
     const float *   xd;        // and its scales at xd + c * K / 32 (Q8_0) or xd + c * K / 256 (Q8_K)
     const int16_t * xbs;       // Q8_K: the column's 16-element sums at xbs + c * K / 16
@@ -122,7 +124,7 @@ struct gemm_launch {
 bool gemm_supported(int type, int64_t K, int64_t n_rows);
 void launch_gemm(const gemm_launch & G, hipStream_t st);
 // the workgroup tile launch_gemm picks (kernel template arguments: "4x4x2", "2x4x2", "1x2x4" for
-// Q4_0 / Q8_0 warp tiles x k-blocks; "2x2", "1x2" for Q4_K), for profile names
+// Q4_0 / Q8_0 warp tiles x k-blocks; "2x2", "1x2" for the K-quants), for profile names
 const char * gemm_tile_name(const gemm_launch & G);
 
 // Activation prologue of a GEMV: every workgroup quantizes its column of x itself, either as

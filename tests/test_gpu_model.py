@@ -130,3 +130,23 @@ def test_llama3b_decode_step_full_size(tmp_path_factory):
         lc = c.forward(2048, [12345])
     assert rel_err_floor(lh, lc) < TOL
     assert int(np.argmax(lh)) == int(np.argmax(lc))
+
+
+@pytest.mark.skipif(os.environ.get("GL_SKIP_FULL") == "1", reason="full-size check disabled")
+def test_qwen3_kmix_full_size(tmp_path_factory):
+    """BASELINE configs[2]'s shape with a Q4_K_M-style mix (Q6_K output and, in even layers, V and
+    down projections; Q5_K Q, gate and up in odd layers; Q4_K elsewhere): a 64-token prompt (the
+    K-quant prefill GEMMs) and two decode steps on its cache, bit-identical to the oracle."""
+    p = str(tmp_path_factory.mktemp("c3kmix") / "qwen3_kmix.gguf")
+    gl.synth_model(p, seed=2, kquant_mix=1, **gl.CONFIGS["qwen3"])
+    prompt = [int(t) for t in np.random.default_rng(12).integers(0, 151936, 64)]
+    with gl.Session(p, "hip", n_ctx=128) as h, gl.Session(p, "cpu", n_ctx=128, n_threads=16) as c:
+        lh = h.forward(0, prompt)
+        lc = c.forward(0, prompt)
+        assert np.array_equal(lh, lc), ("prefill", rel_err(lh, lc))
+        n_past, tok = len(prompt), int(np.argmax(lc))
+        for step in range(2):
+            lh = h.forward(n_past, [tok])
+            lc = c.forward(n_past, [tok])
+            assert np.array_equal(lh, lc), (step, rel_err(lh, lc))
+            n_past, tok = n_past + 1, int(np.argmax(lc))

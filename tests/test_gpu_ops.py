@@ -179,6 +179,11 @@ def profiled(hip, fn):
     (gl.Q4_K, 2560, 1024),   # Qwen3-shape rows (32 x 64 tiles: at most 128 of 64 x 64)
     (gl.Q4_K, 4096, 72),     # 32 x 64 tiles, rows end inside a 16-row tile
     (gl.Q4_K, 256, 100),     # one super-block per row
+    (gl.Q5_K, 2560, 1024),
+    (gl.Q5_K, 256, 100),
+    (gl.Q6_K, 2560, 1024),
+    (gl.Q6_K, 4096, 72),
+    (gl.Q6_K, 256, 100),
 ])
 @pytest.mark.parametrize("ncols", [64, 100, 512])
 def test_gemm_prefill(hip, cpu, qtype, K, N, ncols):
@@ -232,6 +237,10 @@ def test_gemm_subnormal_scales(hip, cpu, qtype):
     (gl.Q4_K, 256, 4096, 512, "2x2"),        # 64 x 64 tiles: 512 (>= 256)
     (gl.Q4_K, 512, 4120, 515, "2x2"),        # partial tiles, two super-blocks per row
     (gl.Q4_K, 256, 1024, 512, "1x2"),        # 128 tiles of 64 x 64: 32 x 64 instead
+    (gl.Q5_K, 256, 4096, 512, "2x2"),
+    (gl.Q5_K, 512, 1000, 70, "1x2"),
+    (gl.Q6_K, 512, 4120, 515, "2x2"),
+    (gl.Q6_K, 256, 1024, 512, "1x2"),
 ])
 def test_gemm_tile_variants(hip, cpu, qtype, K, N, ncols, tile):
     """Each workgroup tile of the prefill GEMM (the launch picks it from the tile count), pinned by
@@ -282,7 +291,72 @@ def test_gemm_q4k_extreme_blocks(hip, cpu, sign):
     assert np.array_equal(a, b), rel_err(a, b)
 
 
-@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K])
+@pytest.mark.parametrize("qtype", [gl.Q5_K, gl.Q6_K])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_gemm_kquant_extreme_blocks(hip, cpu, qtype, sign):
+    """The Q5_K / Q6_K GEMM's exactness bounds at their extremes, on odd rows against activations
+    that quantize to -127 or +127 everywhere. Q5_K: every scale and min 63 and every quant 31
+    (sc * q5 = 1953). Q6_K: in the first super-block of a row every scale -128 and every quant 0
+    (sc * (q - 32) = 4096, |aux32| = 32 * 4096 * 127); in the others random scales and quants, so
+    that most products are odd integers above 2048, which f16 cannot hold (the kernel's hi / lo
+    split). Even rows are ordinary quantized weights."""
+    K, N, ncols = 1024, 96, 64
+    bs = {gl.Q5_K: 176, gl.Q6_K: 210}[qtype]
+    w = qweight(qtype, K, N, 87).reshape(N, -1).copy()
+    nb = K // 256
+    r = rng(88)
+    for row in range(1, N, 2):
+        blocks = w[row].reshape(nb, bs)
+        for b in range(nb):
+            if qtype == gl.Q5_K:
+                blocks[b, :] = 0xFF
+                blocks[b, 0:2] = np.frombuffer(np.float16(0.001 * (1 + r.random())).tobytes(), dtype=np.uint8)
+                blocks[b, 2:4] = np.frombuffer(np.float16(0.0005 * (1 + r.random())).tobytes(), dtype=np.uint8)
+            else:
+                # ql[128] qh[64] scales[16] d
+                if b == 0:
+                    blocks[b, :208] = 0
+                    blocks[b, 192:208] = 0x80
+                else:
+                    blocks[b, :208] = r.integers(0, 256, 208, dtype=np.uint8)
+                blocks[b, 208:210] = np.frombuffer(np.float16(0.0001 * (1 + r.random())).tobytes(), dtype=np.uint8)
+    x = np.full((ncols, K), 3.0, dtype=np.float32)
+    if sign < 0:
+        x[:, ::256] = -3.0
+    x[::3] *= 0.5
+    x[1::3] = rng(89).standard_normal((len(x[1::3]), K)).astype(np.float32)
+
+    def build(g):
+        return g.mul_mat(g.tensor(qtype, K, N, data=w.reshape(-1)), g.tensor(gl.F32, K, ncols, data=x))
+
+    a, names = profiled(hip, lambda: run_on(hip, build))
+    b = run_on(cpu, build)
+    assert any(n.startswith("gemm_" + {gl.Q5_K: "q5_K", gl.Q6_K: "q6_K"}[qtype]) for n in names), names
+    assert np.array_equal(a, b), rel_err(a, b)
+
+
+def test_gemm_q6k_lm_head_width(hip, cpu):
+    """A Q6_K LM head (at least 65536 rows) takes the GEMM from 16 columns; a view of its upper
+    rows checks the planes' block offsets on that path."""
+    K, N, ncols = 256, 66600, 16
+    w = qweight(gl.Q6_K, K, N, 41)
+    x = rng(42).standard_normal((ncols, K)).astype(np.float32)
+    rb = 210 * K // 256
+
+    def build(g):
+        wt = g.tensor(gl.Q6_K, K, N, data=w)
+        xt = g.tensor(gl.F32, K, ncols, data=x)
+        top = g.view_2d(wt, K, N - 1000, rb, rb * 1000)
+        return [g.mul_mat(wt, xt), g.mul_mat(top, xt)]
+
+    (hs, names) = profiled(hip, lambda: run_on(hip, build))
+    cs = run_on(cpu, build)
+    assert any(n.startswith("gemm_q6_K") for n in names) and not any(n.startswith("gemv") for n in names), names
+    for a, b in zip(hs, cs):
+        assert np.array_equal(a, b), rel_err(a, b)
+
+
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K, gl.Q5_K, gl.Q6_K])
 def test_gemm_norm_qkv_residual(hip, cpu, qtype):
     """rms_norm * w feeding three prefill-width GEMMs (normalized and quantized once), and a GEMM
     whose residual add is fused into its store."""
