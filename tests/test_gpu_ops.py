@@ -62,11 +62,19 @@ def test_weight_repack_roundtrip(hip, qtype):
     assert np.array_equal(back, q)
 
 
-@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K, gl.Q5_K, gl.Q6_K, gl.F16, gl.F32])
+def bf16_bits(x):
+    """float32 -> bfloat16 bit patterns, rounded to nearest even (ggml's fp32_to_bf16 on finite values)"""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q8_0, gl.Q4_K, gl.Q5_K, gl.Q6_K, gl.F16, gl.F32, gl.BF16])
 def test_get_rows(hip, cpu, qtype):
     K, N = 512, 40
     if qtype in (gl.F16, gl.F32):
         w = (rng(2).standard_normal((N, K)) * 0.1).astype(np.float16 if qtype == gl.F16 else np.float32)
+    elif qtype == gl.BF16:
+        w = bf16_bits(rng(2).standard_normal((N, K)) * 0.1)
     else:
         w = qweight(qtype, K, N, 2, std=0.1)
     ids = np.array([3, 0, 39, 3, 17], dtype=np.int32)
@@ -134,7 +142,7 @@ def test_gemv_kquant_lm_head_width(hip, cpu, qtype, ncols):
         assert np.array_equal(a, b), rel_err(a, b)
 
 
-@pytest.mark.parametrize("wtype", [gl.F32, gl.F16])
+@pytest.mark.parametrize("wtype", [gl.F32, gl.F16, gl.BF16])
 @pytest.mark.parametrize("K,N,ncols,n2", [
     (2048, 128, 1, 1),     # the MoE router
     (2048, 128, 16, 1),
@@ -143,10 +151,12 @@ def test_gemv_kquant_lm_head_width(hip, cpu, qtype, ncols):
     (12, 9, 2, 1),         # rows too short for the vector path
 ])
 def test_mul_mat_float_weights(hip, cpu, wtype, K, N, ncols, n2):
-    """F32 / F16 weights (no quantization): float products summed in double, as ggml-cpu's
-    vec_dot_f32 / vec_dot_f16 (with the activation rounded to F16 for F16 weights)."""
+    """F32 / F16 / BF16 weights (no quantization): float products summed in double, as ggml-cpu's
+    vec_dot_f32 / vec_dot_f16 / vec_dot_bf16 (with the activation rounded to the weight's type)."""
     r = rng(K + N + ncols)
     w = r.standard_normal((n2, N, K)).astype(np.float16 if wtype == gl.F16 else np.float32)
+    if wtype == gl.BF16:
+        w = bf16_bits(w)
     x = r.standard_normal((n2, ncols, K)).astype(np.float32)
 
     def build(g):
