@@ -79,6 +79,7 @@ __device__ __forceinline__ void stage_flat(int n, LD load, STO store) {
 // expert's item, staged column by column
 template <int TYPE, int LPR, bool SWIGLU, int ITS, bool FLAT>
 __global__ __launch_bounds__(MC_THREADS) void gemv_mc_kernel(const gemv_mc_args A) {
+    prefetch_kernargs<sizeof(gemv_mc_args)>();
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int s_col[GEMV_MC_MAX_COLS];
     __shared__ int s_xcol[GEMV_MC_MAX_COLS];   // the activation column each reads

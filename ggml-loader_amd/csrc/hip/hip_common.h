@@ -126,6 +126,25 @@ __device__ __forceinline__ float group_max(float v) {
 
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// A kernel's arguments sit in device memory that no cache holds when the kernel starts: each scalar
+// load of a new 64-byte line of them goes to memory, and the address set-up of a kernel is a chain
+// of such loads (an index read from one field selects the next). Measured inside the decode GEMVs:
+// about 1 us per link, three to four links before the first weight load went out. Called first in
+// a kernel, this reads one dword of every line of its first BYTES bytes of arguments with
+// independent loads and waits for them once, so the chain that follows hits the scalar cache.
+// Every offset read lies inside the explicit arguments.
+template <int BYTES>
+__device__ __forceinline__ void prefetch_kernargs() {
+    constexpr int LINES = (BYTES + 63) / 64;
+    const uint32_t * k = (const uint32_t *) __builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t v[LINES + 1];
+#pragma unroll
+    for (int i = 0; i < LINES; i++) v[i] = k[i * 16];
+    v[LINES] = k[(BYTES - 4) / 4];
+#pragma unroll
+    for (int i = 0; i <= LINES; i++) asm volatile("" ::"s"(v[i]) : "memory");
+}
+
 // Transcendentals of the float ops are evaluated in double and rounded once, i.e. the correctly
 // rounded float result (barring astronomically rare double-rounding cases). The CPU oracle defines
 // the same semantics, so RoPE angles, softmax weights and SiLU agree bit-for-bit across backends

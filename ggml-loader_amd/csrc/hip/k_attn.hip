@@ -100,6 +100,7 @@ __host__ __device__ constexpr int scores_dyn_floats(int n_q) {
 // Register budget: four waves per SIMD, so that four workgroups of a long row share each CU.
 template <int HD, int G>
 __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_launch A) {
+    prefetch_kernargs<sizeof(attn_launch)>();
     constexpr int HD2 = HD / 2;
     constexpr int STRIDE = HD2 + 4;   // dwords per staged K row: 16-byte aligned, rows offset by 4 banks
     __shared__ __align__(16) uint32_t s_k[ATT_CHUNK * STRIDE];
@@ -372,6 +373,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
 // one workgroup per (head, query, segment of STATS_SEG positions): the row maximum M from the chunk
 // maxima, and sum exp(s - M) in double over the segment's positions
 __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_launch A) {
+    prefetch_kernargs<sizeof(attn_launch)>();
     __shared__ float s_m[ATT_WAVES];
     __shared__ double s_s[ATT_WAVES];
     const int h = blockIdx.x, q = blockIdx.y, seg = blockIdx.z;
@@ -475,6 +477,7 @@ __device__ __forceinline__ void combine_head(const attn_launch & A, const attn_s
 // one workgroup of 2 HD threads per (head, query)
 template <int HD>
 __global__ __launch_bounds__(2 * HD) void attn_combine_kernel(const attn_launch A, int n_splits) {
+    prefetch_kernargs<sizeof(attn_launch) + 4>();
     __shared__ double s_half[HD];
     combine_head<HD>(A, scratch_of(A), blockIdx.x, blockIdx.y, n_splits, s_half);
 }
@@ -485,6 +488,7 @@ __global__ __launch_bounds__(2 * HD) void attn_combine_kernel(const attn_launch 
 // positions (exact in practice, so its grouping does not matter). The statistics launch is not made.
 template <int HD, int G, int FSK>
 __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch A, int pvq) {
+    prefetch_kernargs<sizeof(attn_launch) + 4>();
     constexpr int HD2 = HD / 2;
     constexpr int PIECES = HD / 8;                        // 16-byte pieces per V row
     constexpr int ITER = PV_CHUNK * PIECES / ATT_THREADS;
@@ -777,6 +781,7 @@ __host__ __device__ inline int apf_row_stride(int n_kv) {
 
 template <int HD>
 __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_launch A) {
+    prefetch_kernargs<sizeof(attn_launch)>();
     constexpr int KSTR = HD + 2;     // halves per staged row (one dword of padding)
     constexpr int PIECES = HD / 8;   // 16-byte pieces per row
     __shared__ __half s_q[APF_Q * KSTR];

@@ -79,6 +79,7 @@ struct gemm_cfg {
 
 template <int TYPE, int WTM, int WTN, int KB>
 __global__ __launch_bounds__(256, WTM == 1 ? 4 : 1) void gemm_q_kernel(const gemm_launch G) {
+    prefetch_kernargs<sizeof(gemm_launch)>();
     using C = gemm_cfg<TYPE, WTM, WTN, KB>;
     constexpr int QB = C::QB, BM = C::BM, BN = C::BN, ROW = C::ROW;
     extern __shared__ __align__(16) uint8_t g_lds[];
@@ -297,6 +298,7 @@ struct gemm_k_cfg {
 
 template <int TYPE, int WTM, int WTN>
 __global__ __launch_bounds__(256, 2) void gemm_k_kernel(const gemm_launch G) {
+    prefetch_kernargs<sizeof(gemm_launch)>();
     using C = gemm_k_cfg<TYPE, WTM, WTN>;
     constexpr bool Q6 = C::Q6, MINS = C::MINS;
     constexpr int BM = C::BM, BN = C::BN, ROW = C::ROW, UPR = C::UPR;

@@ -484,6 +484,7 @@ __device__ __forceinline__ void stage_x(const gemv_launch & L, int col, const ge
 // workgroup (the LM head): same arithmetic, so the GEMV that copies the result computes the same floats.
 template <int TYPE>
 __global__ __launch_bounds__(GEMV_NT) void act_quant_kernel(const gemv_launch L, q8_act q8, q8k_act q8k) {
+    prefetch_kernargs<sizeof(gemv_launch) + sizeof(q8_act) + sizeof(q8k_act)>();
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double s_red[GEMV_NT / WAVE];
     const int col = blockIdx.x;
@@ -522,6 +523,7 @@ void launch_act_quant(const gemv_launch & L, const q8_act & q8, const q8k_act & 
 
 template <int TYPE, int LPR, bool SWIGLU, int ITS, bool PRO>
 __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
+    prefetch_kernargs<sizeof(gemv_kargs)>();
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int RPW = WAVE / LPR;
     constexpr int NCH = SWIGLU ? 2 : 1;          // gate and up chains

@@ -88,6 +88,7 @@ __device__ __forceinline__ int q8_quant4(float v0, float v1, float v2, float v3,
 
 template <int TYPE, int LPR, int ITS, bool SWIGLU, int PRO, int CPT, int MAXT>
 __global__ __launch_bounds__(MAXT) void gemv_q_kernel(const gemv_kargs a) {
+    prefetch_kernargs<sizeof(gemv_kargs)>();
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int RPW = WAVE / LPR;
     constexpr int NCH = SWIGLU ? 2 : 1;

@@ -242,6 +242,7 @@ void launch_argsort(const tview & a, const tview & dst, bool desc, hipStream_t s
 // out[:, t] = ((e[:, 0, t] * w[0, t] + e[:, 1, t] * w[1, t]) + ...) (+ res[:, t]): the graph's
 // mul by the routing weights, its chain of adds over the slots in order, and the residual add
 __global__ void moe_wsum_kernel(moe_wsum M) {
+    prefetch_kernargs<sizeof(moe_wsum)>();
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t t = blockIdx.y;
     if (i >= M.n_embd) return;
@@ -340,6 +341,7 @@ void launch_glu(const tview & a, const tview & b, const tview & dst, hipStream_t
 // quantization (a workgroup's 256 elements are one super-block): one thread per element, grid.y
 // over the columns
 __global__ __launch_bounds__(256) void swiglu_kernel(tview g, tview u, tview d, q8_act q, q8k_act qk) {
+    prefetch_kernargs<3 * sizeof(tview) + sizeof(q8_act) + sizeof(q8k_act)>();
     const int64_t K = d.ne[0], nblk = K / 32, c = blockIdx.y;
     const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
     const bool ok = i < K;
@@ -390,6 +392,7 @@ void launch_unary(int op, float s, const tview & a, const tview & dst, hipStream
 
 // element i (row-major over the src shape) -> element i (row-major over the dst shape)
 __global__ void cpy_kernel(tview s, tview d, int64_t n) {
+    prefetch_kernargs<2 * sizeof(tview) + 8>();
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const idx4 a = unflatten(i, s.ne);
@@ -415,6 +418,7 @@ void launch_cpy(const tview & src, const tview & dst, hipStream_t st) {
 
 __global__ void get_rows_kernel(tview a, tview ids, tview d, const uint8_t * qs, const __half * dpl, q6k_planes q6,
                                 int64_t first_block) {
+    prefetch_kernargs<3 * sizeof(tview) + 16 + sizeof(q6k_planes) + 8>();
     const int64_t r = blockIdx.x;
     const int64_t i10 = r % ids.ne[0], i11 = (r / ids.ne[0]) % ids.ne[1], i12 = r / (ids.ne[0] * ids.ne[1]);
     const int32_t row = *(const int32_t *) at(ids, i10, i11, i12, 0);
@@ -552,6 +556,7 @@ __device__ __forceinline__ void copy_elem(const rope_job & J, IDX li) {
 // Independent RoPE and copy jobs of one decode step in one launch (Q rotation; K rotation stored
 // straight into the F16 KV cache; V appended to it). Each job owns a whole number of workgroups.
 __global__ __launch_bounds__(256) void rope_batch_kernel(const rope_batch B) {
+    prefetch_kernargs<sizeof(rope_batch)>();
     int j = 0;
 #pragma unroll
     for (int k = 1; k < ROPE_MAX_JOBS; k++) if (k < B.n_jobs && (int64_t) blockIdx.x >= B.first_block[k]) j = k;
@@ -659,6 +664,7 @@ void launch_soft_max(const tview & a, const tview * mask, const tview & dst, flo
 // MoE routing (one workgroup per token)
 
 __global__ __launch_bounds__(256) void moe_route_kernel(const moe_route R) {
+    prefetch_kernargs<sizeof(moe_route)>();
     __shared__ float s_p[MOE_ROUTE_MAX_EXPERTS];
     __shared__ int s_ids[MOE_ROUTE_MAX_K];
     __shared__ float s_red[4];
@@ -770,6 +776,7 @@ __device__ void argmax_block(float & bv, int & bi) {
 }
 
 __global__ __launch_bounds__(256) void argmax_parts_kernel(tview a, int64_t chunk, float * pv, int * pi) {
+    prefetch_kernargs<sizeof(tview) + 24>();
     const int64_t i0 = (int64_t) blockIdx.x * chunk, i1 = min(i0 + chunk, a.ne[0]);
     float bv = -INFINITY;
     int bi = 0x7fffffff;
@@ -892,6 +899,7 @@ __global__ __launch_bounds__(256) void mul_mat_rows_kernel(tview s0, tview s1, t
 __global__ __launch_bounds__(256) void mul_mat_rows_norm_kernel(tview w, const float * __restrict__ x, int64_t x_stride,
                                                                 const float * __restrict__ nw, float eps,
                                                                 float * __restrict__ y_out, int64_t y_stride, tview d) {
+    prefetch_kernargs<2 * sizeof(tview) + 48>();
     extern __shared__ __align__(16) float s_y[];      // [K]
     __shared__ double s_part[4];
     const int64_t K = w.ne[0], col = blockIdx.y;
