@@ -133,16 +133,38 @@ __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdg
 // a kernel, this reads one dword of every line of its first BYTES bytes of arguments with
 // independent loads and waits for them once, so the chain that follows hits the scalar cache.
 // Every offset read lies inside the explicit arguments.
+typedef const __attribute__((address_space(4))) uint32_t * kernarg_ptr;
+
 template <int BYTES>
-__device__ __forceinline__ void prefetch_kernargs() {
+__device__ __forceinline__ kernarg_ptr prefetch_kernarg_lines() {
     constexpr int LINES = (BYTES + 63) / 64;
-    const uint32_t * k = (const uint32_t *) __builtin_amdgcn_kernarg_segment_ptr();
+    kernarg_ptr k = (kernarg_ptr) __builtin_amdgcn_kernarg_segment_ptr();
     uint32_t v[LINES + 1];
 #pragma unroll
     for (int i = 0; i < LINES; i++) v[i] = k[i * 16];
     v[LINES] = k[(BYTES - 4) / 4];
+    // the returned pointer depends on every load: whatever is read through it comes after them
 #pragma unroll
-    for (int i = 0; i <= LINES; i++) asm volatile("" ::"s"(v[i]) : "memory");
+    for (int i = 0; i <= LINES; i++) asm volatile("" : "+s"(k) : "s"(v[i]));
+    return k;
+}
+
+template <int BYTES>
+__device__ __forceinline__ void prefetch_kernargs() {
+    (void) prefetch_kernarg_lines<BYTES>();
+    // nothing is scheduled across this point: the loads above go out first, before any load of
+    // the kernel's own and its wait
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// For a kernel whose first argument is arg: the prefetch above, and arg read back through a pointer
+// that depends on it. The compiler hoists a kernel's argument loads, and the address arithmetic on
+// them, above anything that does not feed them; reading the arguments through this reference keeps
+// every one of those loads after the prefetch.
+template <typename T>
+__device__ __forceinline__ const T & kernargs_prefetched(const T & arg) {
+    (void) arg;
+    return *(const T *) (const __attribute__((address_space(4))) T *) prefetch_kernarg_lines<(int) sizeof(T)>();
 }
 
 // Transcendentals of the float ops are evaluated in double and rounded once, i.e. the correctly

@@ -99,8 +99,8 @@ __host__ __device__ constexpr int scores_dyn_floats(int n_q) {
 
 // Register budget: four waves per SIMD, so that four workgroups of a long row share each CU.
 template <int HD, int G>
-__global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_launch A) {
-    prefetch_kernargs<sizeof(attn_launch)>();
+__global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_launch A_) {
+    const attn_launch & A = kernargs_prefetched(A_);
     constexpr int HD2 = HD / 2;
     constexpr int STRIDE = HD2 + 4;   // dwords per staged K row: 16-byte aligned, rows offset by 4 banks
     __shared__ __align__(16) uint32_t s_k[ATT_CHUNK * STRIDE];
@@ -372,8 +372,8 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
 
 // one workgroup per (head, query, segment of STATS_SEG positions): the row maximum M from the chunk
 // maxima, and sum exp(s - M) in double over the segment's positions
-__global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_launch A) {
-    prefetch_kernargs<sizeof(attn_launch)>();
+__global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_launch A_) {
+    const attn_launch & A = kernargs_prefetched(A_);
     __shared__ float s_m[ATT_WAVES];
     __shared__ double s_s[ATT_WAVES];
     const int h = blockIdx.x, q = blockIdx.y, seg = blockIdx.z;
@@ -476,8 +476,8 @@ __device__ __forceinline__ void combine_head(const attn_launch & A, const attn_s
 
 // one workgroup of 2 HD threads per (head, query)
 template <int HD>
-__global__ __launch_bounds__(2 * HD) void attn_combine_kernel(const attn_launch A, int n_splits) {
-    prefetch_kernargs<sizeof(attn_launch) + 4>();
+__global__ __launch_bounds__(2 * HD) void attn_combine_kernel(const attn_launch A_, int n_splits) {
+    const attn_launch & A = kernargs_prefetched(A_);
     __shared__ double s_half[HD];
     combine_head<HD>(A, scratch_of(A), blockIdx.x, blockIdx.y, n_splits, s_half);
 }
@@ -487,8 +487,8 @@ __global__ __launch_bounds__(2 * HD) void attn_combine_kernel(const attn_launch 
 // the statistics launch; the sum is the statistics kernel's, exp(s - M) in double over the row's
 // positions (exact in practice, so its grouping does not matter). The statistics launch is not made.
 template <int HD, int G, int FSK>
-__global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch A, int pvq) {
-    prefetch_kernargs<sizeof(attn_launch) + 4>();
+__global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch A_, int pvq) {
+    const attn_launch & A = kernargs_prefetched(A_);
     constexpr int HD2 = HD / 2;
     constexpr int PIECES = HD / 8;                        // 16-byte pieces per V row
     constexpr int ITER = PV_CHUNK * PIECES / ATT_THREADS;
