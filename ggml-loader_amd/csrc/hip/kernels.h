@@ -194,6 +194,10 @@ void launch_gemv_q(const gemv_launch & L, hipStream_t st);
 bool gemv_q4k_enabled();
 bool gemv_q4k_supported(const gemv_launch & L);
 void launch_gemv_q4k(const gemv_launch & L, hipStream_t st);
+// Dense Q4_K products of 2 or more pre-quantized columns with K <= 4096 on the matrix cores
+// (k_gemv_mfma.hip): 16 rows x 16 columns per workgroup, the same floats as the GEMV
+bool gemv_mfma_supported(const gemv_launch & L);
+void launch_gemv_mfma(const gemv_launch & L, hipStream_t st);
 // Several activation columns per workgroup (k_gemv_mc.hip): each weight row block is read once for
 // up to GEMV_MC_MAX_COLS columns; the activation must be quantized already (L.xq, no L.norm). With
 // groups (mul_mat_id): the workgroups of expert e take the columns the ids route to e, listed by

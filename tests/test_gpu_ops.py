@@ -98,6 +98,7 @@ def test_get_rows(hip, cpu, qtype):
     (gl.Q4_K, 2560, 1024),
     (gl.Q4_K, 9728, 512),
     (gl.Q4_K, 768, 200),
+    (gl.Q4_K, 4096, 2048),
     (gl.Q5_K, 2560, 1024),
     (gl.Q5_K, 9728, 512),
     (gl.Q5_K, 768, 200),
@@ -392,16 +393,19 @@ def test_gemm_norm_qkv_residual(hip, cpu, qtype):
 
 
 @pytest.mark.parametrize("qtype", [gl.Q4_0, gl.Q4_K, gl.Q5_K, gl.Q6_K])
-def test_gemv_residual_and_qkv_group(hip, cpu, qtype):
+@pytest.mark.parametrize("ncols", [1, 16, 19])
+def test_gemv_residual_and_qkv_group(hip, cpu, qtype, ncols):
+    """Q, K and V in one launch (matrices starting on workgroup boundaries) and the O projection
+    with its residual add; several columns take the multi-column kernels (Q4_K: the matrix cores)."""
     K = 1024
-    Nq, Nk = 1024, 256
+    Nq, Nk = 1024, 200
     wq, wk, wv, wo = (qweight(qtype, K, n, s) for n, s in ((Nq, 11), (Nk, 12), (Nk, 13), (K, 14)))
-    x = rng(3).standard_normal((1, K)).astype(np.float32)
-    r = rng(4).standard_normal((1, K)).astype(np.float32)
+    x = rng(3).standard_normal((ncols, K)).astype(np.float32)
+    r = rng(4).standard_normal((ncols, K)).astype(np.float32)
 
     def build(g):
-        xt = g.tensor(gl.F32, K, 1, data=x)
-        rt = g.tensor(gl.F32, K, 1, data=r)
+        xt = g.tensor(gl.F32, K, ncols, data=x)
+        rt = g.tensor(gl.F32, K, ncols, data=r)
         q = g.mul_mat(g.tensor(qtype, K, Nq, data=wq), xt)
         k = g.mul_mat(g.tensor(qtype, K, Nk, data=wk), xt)
         v = g.mul_mat(g.tensor(qtype, K, Nk, data=wv), xt)
