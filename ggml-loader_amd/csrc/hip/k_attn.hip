@@ -789,9 +789,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
     __shared__ int s_live[APF_MAX_CHUNKS];
     __shared__ int s_live_end;       // one past the last live chunk
     extern __shared__ float s_s[];   // [APF_Q][SS]: scores, then e, then p
-    // the last query tiles first: under a causal mask they see the most positions, and started
-    // last they would leave the chip waiting on a few long workgroups
-    const int q0 = (gridDim.x - 1 - blockIdx.x) * APF_Q, h = blockIdx.y;
+    // the last query tiles first, every head's before any head's shorter ones (the head is the
+    // fastest grid index): under a causal mask they see the most positions, and started last they
+    // would leave the chip waiting on a few long workgroups
+    const int q0 = (gridDim.y - 1 - blockIdx.y) * APF_Q, h = blockIdx.x;
     const int kvh = h / (A.n_head / A.n_head_kv);
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
     const int n_kv = A.n_kv, n_q = A.n_q;
@@ -864,9 +865,43 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
             }
         }
     };
-    if (!A.mask) stage_mask([&](int, int) { return 0.0f; });
-    else if (A.mask_f16) stage_mask([&](int q, int t) { return __half2float(((const __half *) ((const char *) A.mask + (int64_t) q * A.mask_nb1))[t]); });
-    else stage_mask([&](int q, int t) { return ((const float *) ((const char *) A.mask + (int64_t) q * A.mask_nb1))[t]; });
+    if (!A.mask) {
+        stage_mask([&](int, int) { return 0.0f; });
+    } else if (A.mask_f16 && n_kv % 8 == 0 && A.mask_nb1 % 16 == 0 && (uintptr_t) A.mask % 16 == 0) {
+        // eight positions per 16-byte load, up to eight loads in flight per thread
+        const int per_row = n_kv / 8, total = APF_Q * per_row;
+        for (int base = 0; base < total; base += 8 * ATT_THREADS) {
+            uint4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = min(base + u * ATT_THREADS + (int) threadIdx.x, total - 1);
+                const int qi = i / per_row, pc = i % per_row;
+                v[u] = *(const uint4 *) ((const char *) A.mask + (int64_t) min(q0 + qi, n_q - 1) * A.mask_nb1 + pc * 16);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = base + u * ATT_THREADS + (int) threadIdx.x;
+                if (i < total) {
+                    const int qi = i / per_row, pc = i % per_row;
+                    const uint32_t w[4] = { v[u].x, v[u].y, v[u].z, v[u].w };
+                    float f[8];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float2 x2 = __half22float2(*(const __half2 *) &w[e]);
+                        f[2 * e] = x2.x;
+                        f[2 * e + 1] = x2.y;
+                    }
+                    float4 * d = (float4 *) (s_s + qi * SS + pc * 8);
+                    d[0] = make_float4(f[0], f[1], f[2], f[3]);
+                    d[1] = make_float4(f[4], f[5], f[6], f[7]);
+                }
+            }
+        }
+    } else if (A.mask_f16) {
+        stage_mask([&](int q, int t) { return __half2float(((const __half *) ((const char *) A.mask + (int64_t) q * A.mask_nb1))[t]); });
+    } else {
+        stage_mask([&](int q, int t) { return ((const float *) ((const char *) A.mask + (int64_t) q * A.mask_nb1))[t]; });
+    }
     __syncthreads();
     // chunk liveness, one wave per chunk (lane = position): a chunk whose mask is -inf for every
     // query of the tile is not computed. Its staged values are then -inf in every row (rows past
@@ -891,6 +926,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
     __syncthreads();
 
     // ---- scores, over the live chunks; the next live chunk's K rows load while this one is used ----
+    // The Q tile as the MFMA A operands, converted once: lane (i + 16 k) holds Q[i][4 j + k] for every
+    // 4-dim step j
+    constexpr int NJ = HD / 4;
+    double qd[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) qd[j] = (double) __half2float(s_q[(lane % 16) * KSTR + 4 * j + lane / 16]);
     uint4 kv[ITER];
     int ch = next_live(0);
     if (ch < n_chunks) load_rows(kv, kbase, A.k_nb2, ch * APF_CHUNK, min(APF_CHUNK, n_kv - ch * APF_CHUNK));
@@ -903,15 +944,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
         // two independent accumulation chains (dims 8i .. 8i + 3 and 8i + 4 .. 8i + 7), added at
         // the end: the double sums are exact for these operands, so the grouping does not matter
         v4d acc = { 0.0, 0.0, 0.0, 0.0 }, acc2 = { 0.0, 0.0, 0.0, 0.0 };
-        const __half * qr = s_q + (lane % 16) * KSTR + lane / 16;
         const __half * kr = s_kv + (wave * 16 + lane % 16) * KSTR + lane / 16;
         static_assert(HD % 8 == 0, "pairs of 4-dim steps");
-#pragma unroll 4
-        for (int d0 = 0; d0 < HD; d0 += 8) {
-            const double a = (double) __half2float(qr[d0]), a2 = (double) __half2float(qr[d0 + 4]);
-            const double b = (double) __half2float(kr[d0]), b2 = (double) __half2float(kr[d0 + 4]);
-            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(a2, b2, acc2, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < NJ; j += 2) {
+            const double b = (double) __half2float(kr[4 * j]), b2 = (double) __half2float(kr[4 * j + 4]);
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(qd[j], b, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(qd[j + 1], b2, acc2, 0, 0, 0);
         }
         acc += acc2;
         const int t = wave * 16 + lane % 16;
@@ -933,37 +972,55 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
     // chunk (later ones are -inf, take no part in the sums and are never read again); unrolled so
     // that independent exps interleave ----
     const int n_pos = min(s_live_end * APF_CHUNK, n_kv);
-    for (int qi = wave; qi < APF_Q; qi += ATT_WAVES) {
-        float * row = s_s + qi * SS;
-        float m = -INFINITY;
-        for (int t = lane; t < n_pos; t += WAVE) m = fmaxf(m, row[t]);
-        m = wave_max(m);
-        double sum = 0.0;
-        if (m != -INFINITY) {
-#pragma unroll 4
-            for (int t = lane; t < n_pos; t += WAVE) {
-                const float e = exp_cr(row[t] - m);
-                row[t] = e;
-                sum += (double) e;
-            }
-        } else {
-            for (int t = lane; t < n_pos; t += WAVE) row[t] = 0.0f;   // a row masked throughout: p = 0
+    {
+        constexpr int RPW = APF_Q / ATT_WAVES;          // rows qi = wave + 4 k of this wave, together
+        float * row[RPW];
+        float m[RPW];
+#pragma unroll
+        for (int k = 0; k < RPW; k++) {
+            row[k] = s_s + (wave + ATT_WAVES * k) * SS;
+            m[k] = -INFINITY;
         }
-        sum = wave_sum_d(sum);
-        const float inv = sum > 0.0 ? (float) (1.0 / sum) : 0.0f;
-        if (A.p_f32) {
-            for (int t = lane; t < n_pos; t += WAVE) row[t] = as_f32(row[t] * inv);
-        } else {
-            for (int t = lane; t < n_pos; t += WAVE) row[t] = __half2float(__float2half_rn(as_f32(row[t] * inv)));
+        for (int t = lane; t < n_pos; t += WAVE) {
+#pragma unroll
+            for (int k = 0; k < RPW; k++) m[k] = fmaxf(m[k], row[k][t]);
+        }
+#pragma unroll
+        for (int k = 0; k < RPW; k++) m[k] = wave_max(m[k]);
+        double sum[RPW];
+#pragma unroll
+        for (int k = 0; k < RPW; k++) sum[k] = 0.0;
+#pragma unroll 2
+        for (int t = lane; t < n_pos; t += WAVE) {
+#pragma unroll
+            for (int k = 0; k < RPW; k++) {
+                // a row masked throughout (m = -inf) gets p = 0
+                const float e = m[k] == -INFINITY ? 0.0f : exp_cr(row[k][t] - m[k]);
+                row[k][t] = e;
+                sum[k] += (double) e;
+            }
+        }
+        float inv[RPW];
+#pragma unroll
+        for (int k = 0; k < RPW; k++) {
+            const double sk = wave_sum_d(sum[k]);
+            inv[k] = sk > 0.0 ? (float) (1.0 / sk) : 0.0f;
+        }
+        for (int t = lane; t < n_pos; t += WAVE) {
+#pragma unroll
+            for (int k = 0; k < RPW; k++) {
+                const float p = as_f32(row[k][t] * inv[k]);
+                row[k][t] = A.p_f32 ? p : __half2float(__float2half_rn(p));
+            }
         }
     }
 
-    // ---- P V ----
+    // ---- P V: wave w takes positions 16 w .. 16 w + 15 of every chunk for all HD / 16 output
+    // tiles; the four waves' partial sums are added at the end (double sums, exact in practice) ----
     constexpr int NT = HD / 16;                  // 16-dim output tiles
-    constexpr int TPW = (NT + ATT_WAVES - 1) / ATT_WAVES;
-    v4d acc[TPW], acc2[TPW];
+    v4d acc[NT];
 #pragma unroll
-    for (int k = 0; k < TPW; k++) acc[k] = acc2[k] = v4d{ 0.0, 0.0, 0.0, 0.0 };
+    for (int k = 0; k < NT; k++) acc[k] = v4d{ 0.0, 0.0, 0.0, 0.0 };
     ch = next_live(0);
     if (ch < n_chunks) load_rows(kv, vbase, A.v_nb2, ch * APF_CHUNK, min(APF_CHUNK, n_kv - ch * APF_CHUNK));
     while (ch < n_chunks) {
@@ -972,34 +1029,54 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
         __syncthreads();                         // p of every row and this chunk's V rows visible
         const int nx = next_live(ch + 1);
         if (nx < n_chunks) load_rows(kv, vbase, A.v_nb2, nx * APF_CHUNK, min(APF_CHUNK, n_kv - nx * APF_CHUNK));
-        // two accumulation chains per output tile (positions 8i .. 8i + 3 and 8i + 4 .. 8i + 7)
-        for (int k0 = 0; k0 < APF_CHUNK; k0 += 8) {
-            const int t = k0 + lane / 16, t2 = t + 4;
-            const double a = t < nt ? (double) s_s[(lane % 16) * SS + t0 + t] : 0.0;
-            const double a2 = t2 < nt ? (double) s_s[(lane % 16) * SS + t0 + t2] : 0.0;
 #pragma unroll
-            for (int k = 0; k < TPW; k++) {
-                const int jt = wave + k * ATT_WAVES;
-                if (jt < NT) {
-                    const double b = (double) __half2float(s_kv[t * KSTR + jt * 16 + lane % 16]);
-                    const double b2 = (double) __half2float(s_kv[t2 * KSTR + jt * 16 + lane % 16]);
-                    acc[k] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[k], 0, 0, 0);
-                    acc2[k] = __builtin_amdgcn_mfma_f64_16x16x4f64(a2, b2, acc2[k], 0, 0, 0);
-                }
+        for (int s4 = 0; s4 < 4; s4++) {
+            const int t = 16 * wave + 4 * s4 + lane / 16;      // rows past nt are staged as zero
+            const double a = t < nt ? (double) s_s[(lane % 16) * SS + t0 + t] : 0.0;
+#pragma unroll
+            for (int k = 0; k < NT; k++) {
+                const double b = (double) __half2float(s_kv[t * KSTR + k * 16 + lane % 16]);
+                acc[k] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[k], 0, 0, 0);
             }
         }
         __syncthreads();                         // every wave's reads of this chunk's s_kv are done
         ch = nx;
     }
+    // register r of lane (c + 16 g) holds row g + 4 r, column c of each tile (the f64 MFMA's D
+    // layout); waves 2, 3 hand theirs to waves 0, 1, then wave 1 to wave 0 (the dynamic LDS holds
+    // 2 * APF_Q * HD doubles)
+    double * red = (double *) s_s;
+    auto red_at = [&](int slot, int k, int r) { return red + ((slot * APF_Q + lane / 16 + 4 * r) * HD + k * 16 + lane % 16); };
+    if (wave >= 2) {
 #pragma unroll
-    for (int k = 0; k < TPW; k++) {
-        const int jt = wave + k * ATT_WAVES;
-        if (jt >= NT) continue;
-        acc[k] += acc2[k];
+        for (int k = 0; k < NT; k++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int q = q0 + lane / 16 + 4 * r;
-            if (q < n_q) A.out[(int64_t) q * A.out_nb1 + (int64_t) h * HD + jt * 16 + lane % 16] = (float) acc[k][r];
+            for (int r = 0; r < 4; r++) *red_at(wave - 2, k, r) = acc[k][r];
+    }
+    __syncthreads();
+    if (wave < 2) {
+#pragma unroll
+        for (int k = 0; k < NT; k++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[k][r] += *red_at(wave, k, r);
+    }
+    __syncthreads();
+    if (wave == 1) {
+#pragma unroll
+        for (int k = 0; k < NT; k++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) *red_at(0, k, r) = acc[k][r];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int k = 0; k < NT; k++) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int q = q0 + lane / 16 + 4 * r;
+                const double v = acc[k][r] + *red_at(0, k, r);
+                if (q < n_q) A.out[(int64_t) q * A.out_nb1 + (int64_t) h * HD + k * 16 + lane % 16] = (float) v;
+            }
         }
     }
 }
@@ -1026,11 +1103,11 @@ int attn_prefill_max_kv(int hd) {
 
 template <int HD>
 static void launch_attn_prefill_hd(const attn_launch & A, hipStream_t st) {
-    const size_t lds = (size_t) APF_Q * apf_row_stride(A.n_kv) * sizeof(float);
+    const size_t lds = std::max((size_t) APF_Q * apf_row_stride(A.n_kv) * sizeof(float), (size_t) 2 * APF_Q * HD * sizeof(double));
     if (lds + apf_static_lds<HD>() > 65536) {
         HIP_CHECK(hipFuncSetAttribute((const void *) attn_prefill_kernel<HD>, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds));
     }
-    launch(attn_prefill_kernel<HD>, dim3((A.n_q + APF_Q - 1) / APF_Q, A.n_head), dim3(ATT_THREADS), lds, st, A);
+    launch(attn_prefill_kernel<HD>, dim3(A.n_head, (A.n_q + APF_Q - 1) / APF_Q), dim3(ATT_THREADS), lds, st, A);
 }
 
 void launch_attn_prefill(const attn_launch & A, hipStream_t st) {
