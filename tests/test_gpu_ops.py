@@ -680,6 +680,8 @@ def test_argmax_wide_row(hip, cpu, n, ties):
     (128, 24, 8, 64, 1),
     (128, 24, 8, 65, 2),
     (128, 16, 8, 200, 4),
+    (128, 32, 4, 2400, 16),   # a 16-token MoE step past the prefill kernel's rows: 8 queries per scores workgroup
+    (128, 16, 8, 2400, 13),   # a partial group of queries
 ])
 @pytest.mark.parametrize("flash", [False, True])
 def test_attention_decode(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
