@@ -130,6 +130,22 @@ __global__ __launch_bounds__(MAXT) void gemv_q_kernel(const gemv_kargs a) {
             if (PRO == 1) wv[k] = w4[c];
         }
     }
+    // The rms norm's per-thread sum of squares is formed before any weight load goes out: its x
+    // loads then return from an idle memory system (behind the weight loads of every workgroup they
+    // waited about 3 us), and the weights stream while the sum is reduced and x quantized.
+    double ss = 0.0;
+    if constexpr (PRO == 1) {
+#pragma unroll
+        for (int k = 0; k < CPT; k++) {
+            if (t + k * nt < nc) {
+                ss += (double) (xv[k].x * xv[k].x);
+                ss += (double) (xv[k].y * xv[k].y);
+                ss += (double) (xv[k].z * xv[k].z);
+                ss += (double) (xv[k].w * xv[k].w);
+            }
+        }
+        asm volatile("" ::"v"(ss) : "memory");
+    }
 
     // ---- every weight load of this lane (row and block clamped into the matrix) ----
     uint4 qa[NCH][ITS], qb[NCH][ITS];
@@ -166,16 +182,6 @@ __global__ __launch_bounds__(MAXT) void gemv_q_kernel(const gemv_kargs a) {
     } else {
         float scale = 1.0f;
         if constexpr (PRO == 1) {
-            double ss = 0.0;
-#pragma unroll
-            for (int k = 0; k < CPT; k++) {
-                if (t + k * nt < nc) {
-                    ss += (double) (xv[k].x * xv[k].x);
-                    ss += (double) (xv[k].y * xv[k].y);
-                    ss += (double) (xv[k].z * xv[k].z);
-                    ss += (double) (xv[k].w * xv[k].w);
-                }
-            }
             ss = wave_sum_d_dpp(ss);
             if (lane == 0) s.red[wave] = ss;
             __syncthreads();
