@@ -313,6 +313,7 @@ def prefill_bench(gl, args):
         hipl.ggml_backend_hip_set_profiling(s.backend, False)
         prof = gl.profile(s.backend)
     prof.pop("host_enqueue", None)
+    prof.pop("host_launch_calls", None)
     ms_step = 1000 * secs / args.steps
     log(f"[bench] prefill {n}: {args.steps} steps in {secs:.4f}s -> {n / (secs / args.steps):.1f} tok/s ({ms_step:.3f} ms/step)")
     total_ms = sum(v[1] for v in prof.values())
@@ -382,6 +383,7 @@ def gemv_bench(gl, args):
     hipl.ggml_backend_hip_set_profiling(be, False)
     prof = gl.profile(be)
     prof.pop("host_enqueue", None)
+    prof.pop("host_launch_calls", None)
     y0 = np.empty(N, dtype=np.float32)
     core.ggml_backend_tensor_get(ys[0], vp(y0), 0, N * 4)
     core.ggml_backend_buffer_free(buf)
@@ -555,7 +557,9 @@ def decode_bench(gl, args):
         weights_bytes = s.get("weights_bytes")
 
     host = timed.pop("host_enqueue", None)
+    host_calls = timed.pop("host_launch_calls", None)
     prof.pop("host_enqueue", None)
+    prof.pop("host_launch_calls", None)
     total_ms = sum(v[1] for v in prof.values())
     breakdown = {}
     for k, (n, ms, by) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
@@ -648,9 +652,11 @@ def decode_bench(gl, args):
         "cpu_baseline": cpu,
         "kernel_breakdown_us_per_step": {k: round(v["launches_per_step"] * v["us_per_launch"], 1) for k, v in breakdown.items()},
         "host_enqueue_us_per_step": round(host[1] / host[0] * 1e3, 1) if host else None,
+        "host_launch_calls_us_per_step": round(host_calls[1] / host_calls[0] * 1e3, 1) if host_calls else None,
     }
     if host:
-        log(f"[bench] host enqueue {host[1] / host[0] * 1e3:.1f} us/step (graph walk + kernel submission)")
+        log(f"[bench] host enqueue {host[1] / host[0] * 1e3:.1f} us/step (graph walk + kernel submission; "
+            f"{host_calls[1] / host_calls[0] * 1e3 if host_calls else 0:.1f} us of it inside the launch calls)")
     print(json.dumps(out), flush=True)
 
 

@@ -1928,13 +1928,20 @@ enum ggml_status be_compute_async(ggml_backend_t b, ggml_cgraph * g) {
     hip_device & d = dev(c->device);
     c->timing = c->profiling && (c->computes++ % c->profile_every) == 0;
     const auto t0 = std::chrono::steady_clock::now();
+    g_launch_timing.api_on = c->profiling;
+    g_launch_timing.api_ms = 0.0;
     executor ex(*c, g);
     ex.run();
+    g_launch_timing.api_on = false;
     if (c->profiling) {
-        // host time spent walking the graph and enqueuing its kernels (the "host_enqueue" entry)
+        // host time spent walking the graph and enqueuing its kernels (the "host_enqueue" entry),
+        // and the part of it inside the kernel launch calls ("host_launch_calls")
         prof_entry & e = c->prof["host_enqueue"];
         e.launches++;
         e.ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        prof_entry & l = c->prof["host_launch_calls"];
+        l.launches++;
+        l.ms += g_launch_timing.api_ms;
     }
     if (c->timing) {
         HIP_CHECK(hipStreamSynchronize(d.stream));

@@ -7,6 +7,8 @@
 
 #include <hip/hip_ext.h>
 
+#include <chrono>
+
 // Timing of one executor op. While stop is set, the op's kernels are launched through
 // hipExtLaunchKernel, which stamps start (first launch) and stop (each launch; the last one wins)
 // from the kernel dispatches themselves, so timing puts no event markers between kernels.
@@ -14,12 +16,16 @@ struct launch_timing {
     hipEvent_t start = nullptr;
     hipEvent_t stop = nullptr;
     int launches = 0;
+    // host time spent inside the launch calls (accumulated while api_on; profiled computes only)
+    bool api_on = false;
+    double api_ms = 0.0;
 };
 extern thread_local launch_timing g_launch_timing;
 
 template <typename... KArgs, typename... Args>
 inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem, hipStream_t st, Args... args) {
     launch_timing & t = g_launch_timing;
+    const auto t0 = t.api_on ? std::chrono::steady_clock::now() : std::chrono::steady_clock::time_point{};
     if (t.stop) {
         hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t) shmem, st, t.launches == 0 ? t.start : nullptr, t.stop, 0,
                               args...);
@@ -28,6 +34,7 @@ inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem
         hipLaunchKernelGGL(kernel, grid, block, shmem, st, args...);
     }
     HIP_CHECK(hipGetLastError());
+    if (t.api_on) t.api_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
 }
 
 // A strided view of a tensor (ggml ne/nb convention, nb in bytes).
