@@ -560,6 +560,13 @@ def decode_bench(gl, args):
     host_calls = timed.pop("host_launch_calls", None)
     prof.pop("host_enqueue", None)
     prof.pop("host_launch_calls", None)
+    # host time per op handler of the executor (profiled steps), the largest first
+    host_ops = sorted(((k[8:], v) for k, v in timed.items() if k.startswith("host_op:")), key=lambda kv: -kv[1][1])
+    for k in [k for k in timed if k.startswith("host_op:")]: timed.pop(k)
+    for k in [k for k in prof if k.startswith("host_op:")]: prof.pop(k)
+    n_steps_timed = host[0] if host else 1
+    for name, (n, ms, _) in host_ops[:12]:
+        log(f"[bench]   host {name:<20} {n / n_steps_timed:7.1f} nodes/step {1e3 * ms / n_steps_timed:8.1f} us/step")
     total_ms = sum(v[1] for v in prof.values())
     breakdown = {}
     for k, (n, ms, by) in sorted(prof.items(), key=lambda kv: -kv[1][1]):

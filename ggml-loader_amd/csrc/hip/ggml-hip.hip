@@ -449,7 +449,17 @@ public:
         for (int i = 0; i < g_->n_nodes; i++) {
             if (done_[i]) continue;
             wrote_.clear();
-            exec_node(i);
+            if (c_.profiling && !c_.timing) {
+                // host time per handled node, by op ("host_op:<op>" entries of a profiled compute
+                // without events: a timed one also waits for the device)
+                const auto h0 = std::chrono::steady_clock::now();
+                exec_node(i);
+                prof_entry & e = c_.prof[std::string("host_op:") + ggml_op_name(g_->nodes[i]->op)];
+                e.launches++;
+                e.ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - h0).count();
+            } else {
+                exec_node(i);
+            }
             done_[i] = true;
             if (c_.cb) report();
         }
@@ -1928,14 +1938,16 @@ enum ggml_status be_compute_async(ggml_backend_t b, ggml_cgraph * g) {
     hip_device & d = dev(c->device);
     c->timing = c->profiling && (c->computes++ % c->profile_every) == 0;
     const auto t0 = std::chrono::steady_clock::now();
-    g_launch_timing.api_on = c->profiling;
+    g_launch_timing.api_on = c->profiling && !c->timing;
     g_launch_timing.api_ms = 0.0;
     executor ex(*c, g);
     ex.run();
     g_launch_timing.api_on = false;
-    if (c->profiling) {
+    if (c->profiling && !c->timing) {
         // host time spent walking the graph and enqueuing its kernels (the "host_enqueue" entry),
-        // and the part of it inside the kernel launch calls ("host_launch_calls")
+        // and the part of it inside the kernel launch calls ("host_launch_calls"), over the
+        // profiled computes without events (a timed compute also waits for the device: its events,
+        // and a mul_mat_id's distinct-expert count read back to the host)
         prof_entry & e = c->prof["host_enqueue"];
         e.launches++;
         e.ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
