@@ -22,12 +22,12 @@
 //            conflict-free); one wave per (query, head of the GQA group), lane = position; each
 //            row's chunk maximum.
 //   stats    (query, head, 2048-position segment) workgroups: M = the maximum of the row's chunk
-//            maxima, the segment's sum of exp(s - M) in double.
+//            maxima, e = exp(s - M) written over each score, the segment's sum of e in double.
 //   pv       (128-position chunk, KV head) workgroups: 1/S from the segment sums (added in segment
-//            order), p = F16(exp(s - M) * (1/S)) for the chunk, the chunk's V rows staged in LDS
-//            (every load issued up front), one partial per (chunk, query, head) accumulated in
-//            double; one wave per (query, head), two dims per lane. For one query over a short
-//            row, (chunk, head) workgroups that form M and S themselves, and no stats launch.
+//            order), p = F16(e * (1/S)) for the chunk, the chunk's V rows staged in LDS (every load
+//            issued up front), one partial per (chunk, query, head) accumulated in double; one wave
+//            per (query, head), two dims per lane. For one query over a short row, (chunk, head)
+//            workgroups that form M, e and S themselves, and no stats launch.
 //   combine  one thread per output element: the partials added in chunk order (+ Q8_0 blocks).
 // Workgroups exchange results only across launch boundaries: a flag-and-fence hand-off inside a
 // launch costs a write-back and invalidation of the L2 of every XCD that takes part (measured: the
@@ -37,6 +37,8 @@
 #include "tview_ops.h"
 
 #include "ggml.h"
+
+#include <type_traits>
 
 constexpr int ATT_CHUNK = 64;
 constexpr int ATT_MAX_Q = 4;
@@ -50,13 +52,12 @@ constexpr int STATS_SEG = ATT_THREADS * STATS_PER_THREAD;    // positions per st
 __host__ __device__ inline int attn_chunks(int n_kv) { return (n_kv + ATT_CHUNK - 1) / ATT_CHUNK; }
 __host__ __device__ inline int attn_segs(int n_kv) { return (n_kv + STATS_SEG - 1) / STATS_SEG; }
 
-// Scratch (all per row = (query, head)): scores f32 [n_kv], the maximum of each 64-position chunk
-// f32 [chunks], the row maximum f32, the sum of exp(s - max) over each statistics segment f64
-// [segs], and the PV partials f64 [pv chunks][n_q][n_head][hd].
+// Scratch (all per row = (query, head)): scores f32 [n_kv] (after the statistics launch: e =
+// exp(s - M), M the row maximum), the maximum of each 64-position chunk f32 [chunks], the sum of e
+// over each statistics segment f64 [segs], and the PV partials f64 [pv chunks][n_q][n_head][hd].
 struct attn_scratch {
     float * scores;
     float * cmax;
-    float * rmax;
     double * ssum;
     double * parts;
 };
@@ -66,8 +67,7 @@ __host__ __device__ inline attn_scratch scratch_of(const attn_launch & A) {
     attn_scratch s;
     s.scores = A.scratch;
     s.cmax = s.scores + nrow * A.n_kv;
-    s.rmax = s.cmax + nrow * attn_chunks(A.n_kv);
-    const int64_t nf = nrow * A.n_kv + nrow * attn_chunks(A.n_kv) + nrow;
+    const int64_t nf = nrow * A.n_kv + nrow * attn_chunks(A.n_kv);
     s.ssum = (double *) (A.scratch + nf + (nf & 1));
     s.parts = s.ssum + nrow * attn_segs(A.n_kv);
     return s;
@@ -75,7 +75,7 @@ __host__ __device__ inline attn_scratch scratch_of(const attn_launch & A) {
 
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd) {
     const int64_t nrow = (int64_t) n_q * n_head;
-    const int64_t nf = nrow * n_kv + nrow * attn_chunks(n_kv) + nrow;
+    const int64_t nf = nrow * n_kv + nrow * attn_chunks(n_kv);
     const int64_t pv_chunks = (n_kv + PV_CHUNK - 1) / PV_CHUNK;
     return (nf + (nf & 1)) * (int64_t) sizeof(float) +
            (nrow * attn_segs(n_kv) + pv_chunks * nrow * hd) * (int64_t) sizeof(double);
@@ -371,7 +371,8 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
 }
 
 // one workgroup per (head, query, segment of STATS_SEG positions): the row maximum M from the chunk
-// maxima, and sum exp(s - M) in double over the segment's positions
+// maxima, e = exp(s - M) written over each of the segment's scores (0 throughout a row masked
+// everywhere), and the sum of e in double over the segment's positions. The PV launch reads e.
 __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_launch A_) {
     const attn_launch & A = kernargs_prefetched(A_);
     __shared__ float s_m[ATT_WAVES];
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_laun
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const attn_scratch S = scratch_of(A);
     const int64_t row = (int64_t) q * A.n_head + h;
-    const float * sc = S.scores + row * A.n_kv;
+    float * sc = S.scores + row * A.n_kv;
     const int nch = attn_chunks(A.n_kv);
     // the segment's scores go out first (clamped indices, unused past the end)
     float v[STATS_PER_THREAD];
@@ -394,10 +395,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_laun
     float M = s_m[0];
     for (int w = 1; w < ATT_WAVES; w++) M = fmaxf(M, s_m[w]);
     double sum = 0.0;
-    if (M != -INFINITY) {
 #pragma unroll
-        for (int k = 0; k < STATS_PER_THREAD; k++) {
-            if (seg * STATS_SEG + k * ATT_THREADS + t < A.n_kv) sum += (double) exp_cr(v[k] - M);
+    for (int k = 0; k < STATS_PER_THREAD; k++) {
+        const int i = seg * STATS_SEG + k * ATT_THREADS + t;
+        const float e = M == -INFINITY ? 0.0f : exp_cr(v[k] - M);
+        if (i < A.n_kv) {
+            sum += (double) e;
+            sc[i] = e;
         }
     }
     sum = wave_sum_d(sum);
@@ -407,7 +411,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_laun
         double tot = 0.0;
         for (int w = 0; w < ATT_WAVES; w++) tot += s_s[w];
         S.ssum[row * attn_segs(A.n_kv) + seg] = tot;
-        if (seg == 0) S.rmax[row] = M;
     }
 }
 
@@ -485,7 +488,8 @@ __global__ __launch_bounds__(2 * HD) void attn_combine_kernel(const attn_launch 
 // FSK > 0 (one query, one head per workgroup, n_kv <= FSK * ATT_THREADS): the workgroup forms its row's
 // statistics itself, from the chunk maxima and every score of the row, instead of reading them from
 // the statistics launch; the sum is the statistics kernel's, exp(s - M) in double over the row's
-// positions (exact in practice, so its grouping does not matter). The statistics launch is not made.
+// positions (exact in practice, so its grouping does not matter), and e = exp(s - M) of the chunk's
+// positions is formed here too. The statistics launch is not made.
 template <int HD, int G, int FSK>
 __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch A_, int pvq) {
     const attn_launch & A = kernargs_prefetched(A_);
@@ -508,8 +512,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     auto row_of = [&](int pr) { return (int64_t) (q0 + pr / G) * A.n_head + h0 + pr % G; };
 
     // loads, in the order they are needed (they complete in issue order): the chunk's scores of
-    // every row, each row's maximum and segment sums, then the chunk's V rows (16-byte pieces).
-    // Indices clamped, values past the ends unused.
+    // every row (with the statistics launch: its e values), the segment sums, then the chunk's V
+    // rows (16-byte pieces). Indices clamped, values past the ends unused.
     float sc[PV_SC];
 #pragma unroll
     for (int k = 0; k < PV_SC; k++) {
@@ -535,10 +539,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     } else if (n_rows * nseg <= ATT_THREADS) {
         // one segment sum per thread, issued with the other loads (a loop of dependent loads here
         // would hold back the V loads below); added per row after the loads
-        if (t < n_rows) rmax = S.rmax[row_of(t)];
         if (t < n_rows * nseg) seg_sum = S.ssum[row_of(t / nseg) * nseg + t % nseg];
     } else if (t < n_rows) {
-        rmax = S.rmax[row_of(t)];
         for (int k = 0; k < nseg; k++) ssum += S.ssum[row_of(t) * nseg + k];   // segment order
     }
     uint4 vv[ITER];
@@ -611,8 +613,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
         s_inv[t] = ssum > 0.0 ? (float) (1.0 / ssum) : 0.0f;
     }
     __syncthreads();
-    // p = F16(exp(s - M) * (1/S)) for the chunk's positions (0 past the end; with p_f32 not rounded
-    // to F16), kept as doubles
+    // p = F16(e * (1/S)) for the chunk's positions, e = exp(s - M) (formed here with FSK, read from
+    // the statistics launch otherwise); 0 past the end; with p_f32 not rounded to F16; kept as
+    // doubles
 #pragma unroll
     for (int k = 0; k < PV_SC; k++) {
         const int i = t + k * ATT_THREADS;
@@ -620,8 +623,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
             const int pr = i / PV_CHUNK, tt = i % PV_CHUNK;
             float p = 0.0f;
             if (tt < nt) {
-                const float M = s_M[pr];
-                const float e = M == -INFINITY ? 0.0f : exp_cr(sc[k] - M);
+                float e = sc[k];
+                if constexpr (FS) {
+                    const float M = s_M[pr];
+                    e = M == -INFINITY ? 0.0f : exp_cr(sc[k] - M);
+                }
                 p = as_f32(e * s_inv[pr]);
                 if (!A.p_f32) p = __half2float(__float2half_rn(p));
             }
@@ -688,6 +694,325 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Multi-query decode (more than ATT_MAX_Q queries, RoPE not folded in): the scores and PV launches
+// on the f64 matrix cores, with the statistics and combine launches above unchanged. The rows of a
+// KV head are its (query, head) pairs, row r = q * G + (h - kvh * G) for the G heads of the KV
+// head, in tiles of 16 (one MFMA row tile per workgroup). Same sums as the chain: the F16 x F16
+// products are exact in double and their double sums exact for these operands in practice, so the
+// matrix cores' accumulation order gives the same floats as the kernels above.
+// f64 MFMA 16x16x4 lane layout: A[i][k] at lane i + 16k, B[k][j] at lane j + 16k, D[i][j] in
+// register i / 4 of lane j + 16 (i % 4).
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+constexpr int MQ_ROWS = 16;
+
+// r / g for 0 <= r < MQ_MAX_ROWS and 1 <= g <= 64, with inv_g = 1.0f / g, in three float
+// operations: (r + 0.5) / g lies at least 1 / (2 g) >= 1/128 from every integer, and the float
+// product is within MQ_MAX_ROWS * 2^-23 = 1/512 of it, so truncating it gives the quotient.
+constexpr int MQ_MAX_ROWS = 16384;
+__device__ __forceinline__ int div_small(int r, float inv_g) { return (int) (((float) r + 0.5f) * inv_g); }
+
+__host__ __device__ inline int mq_tiles(const attn_launch & A) {
+    return (A.n_q * (A.n_head / A.n_head_kv) + MQ_ROWS - 1) / MQ_ROWS;
+}
+
+// (64-position chunk, KV head, row tile) workgroups; wave w takes positions 16 w .. 16 w + 15 of the
+// chunk. Writes the scores (kq * scale + mask) and each row's chunk maximum, as attn_scores_kernel.
+template <int HD>
+__global__ __launch_bounds__(ATT_THREADS) void attn_scores_mq_kernel(const attn_launch A_) {
+    const attn_launch & A = kernargs_prefetched(A_);
+    constexpr int KSTR = HD + 2;                  // halves per staged K row (one dword of padding)
+    constexpr int PIECES = HD / 8;                // 16-byte pieces per K row
+    constexpr int ITER = ATT_CHUNK * PIECES / ATT_THREADS;
+    static_assert(ATT_CHUNK * PIECES % ATT_THREADS == 0, "whole 16-byte pieces per thread");
+    constexpr int NJ = HD / 4;                    // 4-dim MFMA steps
+    static_assert(NJ % 2 == 0, "pairs of 4-dim steps");
+    // Q tile rows of QSTR floats: the 16 rows x 4 dims that one MFMA operand read takes fall on 64
+    // distinct banks
+    constexpr int QSTR = HD + 4;
+    constexpr int QPT = HD / 16;                  // Q elements per thread: 16 threads per tile row
+    static_assert(MQ_ROWS * 16 == ATT_THREADS && QPT % 2 == 0, "one tile row per 16 threads");
+    __shared__ __align__(16) __half s_k[ATT_CHUNK * KSTR];
+    __shared__ __align__(16) float s_q[MQ_ROWS * QSTR];
+    __shared__ float s_cm[ATT_WAVES][MQ_ROWS];
+    const int split = blockIdx.x, kvh = blockIdx.y, r0 = blockIdx.z * MQ_ROWS;
+    const int G = A.n_head / A.n_head_kv, n_rows = A.n_q * G;
+    const float inv_g = 1.0f / (float) G;
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const int t0 = split * ATT_CHUNK, nt = min(ATT_CHUNK, A.n_kv - t0);
+    const attn_scratch S = scratch_of(A);
+
+    // Loads first, all unconditional at clamped indices (32-bit offsets: the launch checks that
+    // every index fits): the tile's Q rows once per workgroup, QPT consecutive dims per thread (rows
+    // past n_rows repeat the last row, their results are not stored); the mask of the lane's four
+    // outputs (rows g + 4 r, g = lane / 16, at position 16 wave + lane % 16; an F32 and an F16 load,
+    // the one of the other type reading Q); then the chunk's K rows.
+    const int qi = threadIdx.x / 16, qd0 = (threadIdx.x % 16) * QPT;
+    float qf[QPT];
+    {
+        const int ra = min(r0 + qi, n_rows - 1), qa = div_small(ra, inv_g);
+        const float * src = A.q + ((kvh * G + ra - qa * G) * (int) A.q_nb1 + qa * (int) A.q_nb2 + qd0);
+#pragma unroll
+        for (int k = 0; k < QPT; k++) qf[k] = src[k];
+    }
+    const int tl = wave * 16 + lane % 16;          // the lane's position in the chunk
+    const int tc = t0 + min(tl, nt - 1);
+    const bool mask32 = A.mask && !A.mask_f16, mask16 = A.mask && A.mask_f16;
+    const int mstride = (int) (A.mask_nb1 >> (A.mask_f16 ? 1 : 2));   // elements per mask row
+    const float * mrow32 = (const float *) (mask32 ? A.mask : (const void *) A.q);
+    const __half * mrow16 = (const __half *) (mask16 ? A.mask : (const void *) A.q);
+    float m32[4];
+    __half m16[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int mi = div_small(min(r0 + lane / 16 + 4 * r, n_rows - 1), inv_g) * mstride + tc;
+        m32[r] = mrow32[mask32 ? mi : 0];
+        m16[r] = mrow16[mask16 ? mi : 0];
+    }
+    uint4 kv[ITER];
+    {
+        const __half * kbase = A.k + kvh * A.k_nb1;
+        const int kst = (int) A.k_nb2;
+#pragma unroll
+        for (int it = 0; it < ITER; it++) {
+            const int pc = threadIdx.x + it * ATT_THREADS;
+            const int r = pc / PIECES, c = pc % PIECES;
+            kv[it] = *(const uint4 *) (kbase + ((t0 + min(r, nt - 1)) * kst + c * 8));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);            // every load above is out before any wait
+    // Q rounded to F16 (the mul_mat's conversion of its F32 operand)
+#pragma unroll
+    for (int k = 0; k < QPT; k += 2) {
+        *(float2 *) (s_q + qi * QSTR + qd0 + k) =
+            make_float2(__half2float(__float2half_rn(qf[k])), __half2float(__float2half_rn(qf[k + 1])));
+    }
+    float mk[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) mk[r] = mask32 ? m32[r] : mask16 ? __half2float(m16[r]) : 0.0f;
+    // K rows to LDS, zero past nt (their loads read the last row)
+#pragma unroll
+    for (int it = 0; it < ITER; it++) {
+        const int pc = threadIdx.x + it * ATT_THREADS;
+        const int r = pc / PIECES, c = pc % PIECES;
+        uint32_t * d = (uint32_t *) (s_k + r * KSTR + c * 8);
+        const bool z = r >= nt;
+        d[0] = z ? 0u : kv[it].x; d[1] = z ? 0u : kv[it].y; d[2] = z ? 0u : kv[it].z; d[3] = z ? 0u : kv[it].w;
+    }
+    __syncthreads();
+
+    // S[row][position] over the head dims, two accumulation chains (added at the end; the double
+    // sums are exact for these operands, so the grouping does not matter)
+    // (A operand: lane (i + 16 k) holds Q[row i][4 j + k]; B: lane (j + 16 k) holds K[position j][4 j' + k])
+    v4d acc = { 0.0, 0.0, 0.0, 0.0 }, acc2 = { 0.0, 0.0, 0.0, 0.0 };
+    const __half * kr = s_k + tl * KSTR + lane / 16;
+    const float * qr = s_q + (lane % 16) * QSTR + lane / 16;
+#pragma unroll
+    for (int j = 0; j < NJ; j += 2) {
+        const double a = (double) qr[4 * j], a2 = (double) qr[4 * j + 4];
+        const double b = (double) __half2float(kr[4 * j]), b2 = (double) __half2float(kr[4 * j + 4]);
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(a2, b2, acc2, 0, 0, 0);
+    }
+    acc += acc2;
+    // the softmax input as the graph forms it, (float) kq * scale + mask (-inf where masked, without
+    // the dot); -inf past the chunk's end (not stored, no part in the maximum)
+    float sv[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int rr = r0 + lane / 16 + 4 * r;
+        sv[r] = tl >= nt ? -INFINITY : mk[r] == -INFINITY ? -INFINITY : (float) acc[r] * A.scale + mk[r];
+        if (tl < nt && rr < n_rows) {
+            const int qq = div_small(rr, inv_g);
+            S.scores[(qq * A.n_head + kvh * G + rr - qq * G) * A.n_kv + t0 + tl] = sv[r];
+        }
+    }
+    // each row's maximum over the wave's 16 positions (the 16 lanes of one DPP row), then over the
+    // four waves
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float m = sv[r];
+        m = fmaxf(m, dpp_f<0xB1>(m));
+        m = fmaxf(m, dpp_f<0x4E>(m));
+        m = fmaxf(m, dpp_f<0x141>(m));
+        m = fmaxf(m, dpp_f<0x140>(m));
+        if (lane % 16 == 0) s_cm[wave][lane / 16 + 4 * r] = m;
+    }
+    __syncthreads();
+    if (threadIdx.x < MQ_ROWS && r0 + (int) threadIdx.x < n_rows) {
+        const int rr = r0 + threadIdx.x, i = threadIdx.x, qq = div_small(rr, inv_g);
+        const int row = qq * A.n_head + kvh * G + rr - qq * G;
+        S.cmax[row * attn_chunks(A.n_kv) + split] = fmaxf(fmaxf(s_cm[0][i], s_cm[1][i]), fmaxf(s_cm[2][i], s_cm[3][i]));
+    }
+}
+
+// (128-position chunk, KV head, row tile) workgroups: p = F16(e * (1/S)) of the tile's rows over the
+// chunk (e = exp(s - M) from the statistics launch; P32: p kept a float, flash_attn_ext), then the
+// chunk's partial P V of every (row, dim); wave w takes the 16-dim output tiles w, w + 4, ... over
+// all of the chunk's positions, so no partials are added across waves.
+template <int HD, bool P32>
+__global__ __launch_bounds__(ATT_THREADS) void attn_pv_mq_kernel(const attn_launch A_) {
+    const attn_launch & A = kernargs_prefetched(A_);
+    constexpr int PIECES = HD / 8;                // 16-byte pieces per V row
+    constexpr int ITER = PV_CHUNK * PIECES / ATT_THREADS;
+    static_assert(PV_CHUNK * PIECES % ATT_THREADS == 0, "whole 16-byte pieces per thread");
+    constexpr int NT = HD / 16;                   // 16-dim output tiles
+    constexpr int TPW = (NT + ATT_WAVES - 1) / ATT_WAVES;
+    constexpr int NS = PV_CHUNK / 4;              // 4-position MFMA steps
+    constexpr int EPT = PV_CHUNK / 16;            // positions per thread: 16 threads per tile row
+    static_assert(MQ_ROWS * 16 == ATT_THREADS && EPT == 8, "one tile row per 16 threads, 8 positions each");
+    // p rows: the 16 rows x 4 positions of one A operand read fall on distinct banks (F16: pairs
+    // of lanes share a dword)
+    using pt = typename std::conditional<P32, float, __half>::type;
+    constexpr int PSTR = P32 ? PV_CHUNK + 4 : PV_CHUNK + 8;
+    // V in the order the MFMA B operand reads it: step s, tile, lane j + 16 k -> V[4 s + k][16 tile + j]
+    __shared__ __align__(16) __half s_v[PV_CHUNK * HD];
+    __shared__ __align__(16) pt s_p[MQ_ROWS * PSTR];
+    const int split = blockIdx.x, kvh = blockIdx.y, r0 = blockIdx.z * MQ_ROWS;
+    const int G = A.n_head / A.n_head_kv, n_rows = A.n_q * G;
+    const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
+    const int t0 = split * PV_CHUNK, nt = min(PV_CHUNK, A.n_kv - t0);
+    const attn_scratch S = scratch_of(A);
+    const int nseg = attn_segs(A.n_kv);
+    // this thread's tile row and positions: row pr, positions pp0 .. pp0 + 7 of the chunk
+    const int pr = t / 16, pp0 = (t % 16) * EPT;
+    const float inv_g = 1.0f / (float) G;
+    const int rr = min(r0 + pr, n_rows - 1);      // clamped: rows past n_rows are not stored
+    const int rq = div_small(rr, inv_g);
+    const int row = rq * A.n_head + kvh * G + rr - rq * G;
+
+    // loads, in the order they are needed (they complete in issue order): the e values of the
+    // thread's positions, its row's segment sums (one per thread of the row while they fit), then
+    // the chunk's V rows. Indices clamped (32-bit offsets: the launch checks that every index
+    // fits), values past the ends unused.
+    float ev[EPT];
+    {
+        const float * esrc = S.scores + (row * A.n_kv + t0);
+#pragma unroll
+        for (int k = 0; k < EPT; k++) ev[k] = esrc[min(pp0 + k, nt - 1)];
+    }
+    const bool seg_lanes = nseg <= 16;
+    const double seg_sum = S.ssum[row * nseg + min(t % 16, nseg - 1)];
+    uint4 vv[ITER];
+    {
+        const __half * vbase = A.v + kvh * A.v_nb1;
+        const int vst = (int) A.v_nb2;
+#pragma unroll
+        for (int it = 0; it < ITER; it++) {
+            const int pc = t + it * ATT_THREADS;
+            const int r = pc / PIECES, c = pc % PIECES;
+            vv[it] = *(const uint4 *) (vbase + ((t0 + min(r, nt - 1)) * vst + c * 8));
+        }
+    }
+    // V rows staged as zero: padding rows past the end and, with skip_masked, rows masked for every
+    // query of the tile (p is 0 there for every row, and 0 * a non-finite V must not reach the sums).
+    // Applied at the LDS store: zeroing a register right after its load makes the compiler wait for
+    // every load issued so far.
+    bool vzero[ITER];
+#pragma unroll
+    for (int it = 0; it < ITER; it++) vzero[it] = (t + it * ATT_THREADS) / PIECES >= nt;
+    if (A.skip_masked && A.mask) {
+        const int qa = div_small(r0, inv_g), qb = div_small(min(r0 + MQ_ROWS, n_rows) - 1, inv_g);
+#pragma unroll
+        for (int it = 0; it < ITER; it++) {
+            const int r = (t + it * ATT_THREADS) / PIECES;
+            bool dead = r < nt;
+            for (int q = qa; q <= qb && dead; q++) dead = mask_at(A, q, t0 + r) == -INFINITY;
+            vzero[it] = vzero[it] || dead;
+        }
+    }
+    // the row's S: its segment sums added in segment order (read from the row's 16 lanes, or
+    // loaded one after another past 16 segments)
+    double ssum = 0.0;
+    if (seg_lanes) {
+        for (int k = 0; k < nseg; k++) ssum += __shfl(seg_sum, (lane & ~15) + k, WAVE);
+    } else {
+        for (int k = 0; k < nseg; k++) ssum += S.ssum[row * nseg + k];
+    }
+    const float inv = ssum > 0.0 ? (float) (1.0 / ssum) : 0.0f;
+    // p (0 past the end; rounded to F16 unless P32), eight consecutive positions per store
+    {
+        pt pv8[EPT];
+#pragma unroll
+        for (int k = 0; k < EPT; k++) {
+            // formed for every position (past the end from a repeated e) and selected after, so
+            // that no lane branches
+            const float p = as_f32(ev[k] * inv);
+            if constexpr (P32) pv8[k] = pp0 + k < nt ? p : 0.0f;
+            else pv8[k] = pp0 + k < nt ? __float2half_rn(p) : __float2half_rn(0.0f);
+        }
+        uint4 w[EPT * sizeof(pt) / 16];
+        __builtin_memcpy(w, pv8, sizeof(w));
+        uint4 * d = (uint4 *) (s_p + pr * PSTR + pp0);
+#pragma unroll
+        for (int k = 0; k < (int) (EPT * sizeof(pt) / 16); k++) d[k] = w[k];
+    }
+    // V pieces: row r = 4 s + k, dims 8 c .. 8 c + 7 = tile c / 2, j = 8 (c % 2) .. + 7
+#pragma unroll
+    for (int it = 0; it < ITER; it++) {
+        const int pc = t + it * ATT_THREADS;
+        const int r = pc / PIECES, c = pc % PIECES;
+        const bool z = vzero[it];
+        *(uint4 *) (s_v + (((r / 4) * NT + c / 2) * 4 + r % 4) * 16 + 8 * (c % 2)) =
+            z ? make_uint4(0u, 0u, 0u, 0u) : vv[it];
+    }
+    __syncthreads();
+
+    // out[row][16 tile + j] += sum over the chunk's positions of p[row][pos] V[pos][16 tile + j]; one
+    // accumulation chain per output tile (A operand: lane (i + 16 k) holds p[row i][4 s + k])
+    v4d acc[TPW];
+#pragma unroll
+    for (int k = 0; k < TPW; k++) acc[k] = v4d{ 0.0, 0.0, 0.0, 0.0 };
+    const pt * pa = s_p + (lane % 16) * PSTR + lane / 16;
+#pragma unroll 4
+    for (int s = 0; s < NS; s++) {
+        const double a = (double) (float) pa[4 * s];
+#pragma unroll
+        for (int k = 0; k < TPW; k++) {
+            const int tile = wave + ATT_WAVES * k;
+            if (tile < NT) {
+                const double b = (double) __half2float(s_v[(s * NT + tile) * WAVE + lane]);
+                acc[k] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[k], 0, 0, 0);
+            }
+        }
+    }
+    // register r of lane (c + 16 g): row g + 4 r, dim 16 tile + c
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int ro = r0 + lane / 16 + 4 * r;
+        if (ro >= n_rows) continue;
+        const int q = div_small(ro, inv_g), h = kvh * G + ro - q * G;
+        double * dst = S.parts + (((split * A.n_q + q) * A.n_head + h) * HD + lane % 16);
+#pragma unroll
+        for (int k = 0; k < TPW; k++) {
+            const int tile = wave + ATT_WAVES * k;
+            if (tile < NT) dst[16 * tile] = acc[k][r];
+        }
+    }
+}
+
+template <int HD>
+static void launch_attn_mq(const attn_launch & A, hipStream_t st) {
+    const int splits = attn_chunks(A.n_kv);
+    const int pv_splits = (A.n_kv + PV_CHUNK - 1) / PV_CHUNK;
+    const int tiles = mq_tiles(A);
+    // the kernels' quotient by the GQA group and their 32-bit offsets
+    const int64_t G = A.n_head / A.n_head_kv, lim = INT32_MAX;
+    if (A.n_q * G >= MQ_MAX_ROWS || G > 64) HIP_ABORT("attn: %d queries x %d heads per KV head past the multi-query rows", A.n_q, (int) G);
+    const bool fits = (A.n_head - 1) * A.q_nb1 + (A.n_q - 1) * A.q_nb2 + HD <= lim &&
+                      (A.n_head_kv - 1) * A.k_nb1 + (int64_t) (A.n_kv - 1) * A.k_nb2 + HD <= lim &&
+                      (A.n_head_kv - 1) * A.v_nb1 + (int64_t) (A.n_kv - 1) * A.v_nb2 + HD <= lim &&
+                      (!A.mask || (A.n_q - 1) * (A.mask_nb1 / (A.mask_f16 ? 2 : 4)) + A.n_kv <= lim) &&
+                      (int64_t) A.n_q * A.n_head * A.n_kv <= lim && (int64_t) pv_splits * A.n_q * A.n_head * HD <= lim;
+    if (!fits) HIP_ABORT("attn: multi-query operands past 32-bit element offsets");
+    launch(attn_scores_mq_kernel<HD>, dim3(splits, A.n_head_kv, tiles), dim3(ATT_THREADS), 0, st, A);
+    launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
+    if (A.p_f32) launch((attn_pv_mq_kernel<HD, true>), dim3(pv_splits, A.n_head_kv, tiles), dim3(ATT_THREADS), 0, st, A);
+    else launch((attn_pv_mq_kernel<HD, false>), dim3(pv_splits, A.n_head_kv, tiles), dim3(ATT_THREADS), 0, st, A);
+    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(2 * HD), 0, st, A, pv_splits);
+}
+
 template <int HD, int G>
 static void launch_attn_t(const attn_launch & A, hipStream_t st) {
     const int splits = (A.n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
@@ -743,6 +1068,16 @@ void launch_attn_decode(const attn_launch & A, hipStream_t st) {
     if (A.n_head % A.n_head_kv) HIP_ABORT("attn: n_head %% n_head_kv");
     if (A.scratch_bytes < attn_scratch_bytes(A.n_kv, A.n_q, A.n_head, A.hd)) HIP_ABORT("attn: scratch too small");
     if (A.out_q.qs && (A.hd % 32)) HIP_ABORT("attn: quantized output needs hd %% 32 == 0");
+    if (A.n_q > ATT_MAX_Q) {
+        // many queries: scores and PV on the matrix cores
+        switch (A.hd) {
+            case 64: launch_attn_mq<64>(A, st); break;
+            case 96: launch_attn_mq<96>(A, st); break;
+            case 128: launch_attn_mq<128>(A, st); break;
+            default: HIP_ABORT("attn: unsupported head dim %d", A.hd);
+        }
+        return;
+    }
     switch (A.hd) {
         case 64: launch_attn_hd<64>(A, st); break;
         case 96: launch_attn_hd<96>(A, st); break;
@@ -762,11 +1097,8 @@ void launch_attn_decode(const attn_launch & A, hipStream_t st) {
 //           (flash_attn_ext, p_f32: p = e * (float)(1/S), not rounded to F16).
 //   pv      V rows staged per chunk; out[query][dim] from the f64 MFMA over positions with the
 //           p (skipped chunks have p = 0 throughout and add nothing), rounded to float.
-// f64 MFMA 16x16x4 lane layout: A[i][k] at lane i + 16k, B[k][j] at lane j + 16k, D[i][j] in
-// register i / 4 of lane j + 16 (i % 4).
-typedef double v4d __attribute__((ext_vector_type(4)));
-
-constexpr int APF_Q = 16;            // queries per workgroup (one MFMA row tile)
+// (f64 MFMA lane layout as above.)
+constexpr int APF_Q = 16;           // queries per workgroup (one MFMA row tile)
 constexpr int APF_CHUNK = 64;        // positions per staged K / V chunk (one MFMA column tile per wave)
 constexpr int APF_MAX_CHUNKS = 128;  // positions <= 8192
 

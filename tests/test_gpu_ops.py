@@ -680,8 +680,8 @@ def test_argmax_wide_row(hip, cpu, n, ties):
     (128, 24, 8, 64, 1),
     (128, 24, 8, 65, 2),
     (128, 16, 8, 200, 4),
-    (128, 32, 4, 2400, 16),   # a 16-token MoE step past the prefill kernel's rows: 8 queries per scores workgroup
-    (128, 16, 8, 2400, 13),   # a partial group of queries
+    (128, 32, 4, 2400, 16),   # a 16-token MoE step past the prefill kernel's rows: 8 tiles of 16 (query, head) rows per KV head
+    (128, 16, 8, 2400, 13),   # a partial last row tile (13 queries x 2 heads)
 ])
 @pytest.mark.parametrize("flash", [False, True])
 def test_attention_decode(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
@@ -715,17 +715,21 @@ def test_attention_decode(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
         assert rel_err(a, expect) < 1e-6
 
 
-@pytest.mark.parametrize("n_new", [2, 20])     # the decode kernels, the prefill kernel
-def test_attention_masked_nonfinite_k_row(hip, cpu, n_new):
+@pytest.mark.parametrize("n_new,n_kv", [
+    (2, 70),       # the decode kernels
+    (20, 70),      # the prefill kernel
+    (20, 2400),    # the multi-query decode kernels (past the prefill kernel's rows)
+])
+def test_attention_masked_nonfinite_k_row(hip, cpu, n_new, n_kv):
     """The fused attention gives a position masked for a query the score -inf without reading its
     dot, on every path. ggml-cpu's manual chain forms NaN * scale + (-inf) = NaN there and spreads
     it over the row: a documented deviation. In forward_step the manual chain masks only the step's
     own later tokens, whose K rows come from the same activations, so it shows only when those are
     already non-finite. Queries that cannot see the row equal the chain over a finite row; the
     query that attends it is NaN on both."""
-    hd, n_head, n_head_kv, n_kv = 128, 8, 2, 70
+    hd, n_head, n_head_kv = 128, 8, 2
     G = n_head // n_head_kv
-    r = rng(70 + n_new)
+    r = rng(n_kv + n_new)
     n_ctx = n_kv + 3
     kc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
     vc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
@@ -791,9 +795,9 @@ def test_attention_prefill(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
 ])
 @pytest.mark.parametrize("flash", [False, True])
 def test_attention_long_context_query_groups(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
-    """A multi-token step over more positions than the prefill kernel holds in LDS: the decode
-    kernels with the queries in groups of 4 (launches of up to 64 queries), the chain's float
-    roundings exactly."""
+    """A multi-token step over more positions than the prefill kernel holds in LDS: the multi-query
+    decode kernels (scores and P V on the f64 matrix cores over tiles of 16 (query, head) rows,
+    launches of up to 64 queries), the chain's float roundings exactly."""
     r = rng(n_kv + 7 * n_new)
     n_ctx = n_kv + 3
     kc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
