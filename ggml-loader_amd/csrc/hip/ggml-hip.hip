@@ -1452,7 +1452,8 @@ private:
         // one column per workgroup, or several (mul_mat_id: the tokens routed to each expert)
         const expert_groups * G = mc && by_id ? &expert_groups_of(ids, (int) n->src[0]->ne[2]) : nullptr;
         auto run = [&](const gemv_launch & X) {
-            static const bool no_mfma = getenv("GL_NO_MFMA_GEMV") != nullptr;
+            // GGML_HIP_NO_MFMA_GEMV: the multi-column GEMV for every such launch (comparisons)
+            static const bool no_mfma = getenv("GGML_HIP_NO_MFMA_GEMV") != nullptr;
             if (mc && !G && !no_mfma && gemv_mfma_supported(X)) launch_gemv_mfma(X, st_);
             else if (mc) launch_gemv_mc(X, G, G ? (int) n_tok : X.ncols, st_);
             else launch_gemv(X, st_);

@@ -81,6 +81,12 @@ int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd) {
            (nrow * attn_segs(n_kv) + pv_chunks * nrow * hd) * (int64_t) sizeof(double);
 }
 
+// r / g for 0 <= r < DIV_SMALL_MAX and 1 <= g <= 64, with inv_g = 1.0f / g, in three float
+// operations: (r + 0.5) / g lies at least 1 / (2 g) >= 1/128 from every integer, and the float
+// product is within DIV_SMALL_MAX * 2^-23 = 1/512 of it, so truncating it gives the quotient.
+constexpr int DIV_SMALL_MAX = 16384;
+__device__ __forceinline__ int div_small(int r, float inv_g) { return (int) (((float) r + 0.5f) * inv_g); }
+
 __device__ __forceinline__ float mask_at(const attn_launch & A, int q, int t) {
     if (!A.mask) return 0.0f;
     const char * row = (const char *) A.mask + (int64_t) q * A.mask_nb1;
@@ -109,8 +115,9 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
     extern __shared__ __align__(16) float s_dyn[];
     // blockIdx.y: a group of G consecutive heads (all heads of KV head kvh, or a part of them when
     // the launch splits a large GQA group over several workgroups); h0 its first head
-    const int split = blockIdx.x, h0 = blockIdx.y * G, kvh = h0 / (A.n_head / A.n_head_kv);
-    const bool kv_writer = h0 % (A.n_head / A.n_head_kv) == 0;   // the first group of a KV head appends K and V
+    const int split = blockIdx.x, h0 = blockIdx.y * G;
+    const int kvh = __builtin_amdgcn_readfirstlane(div_small(h0, A.s_inv_gqa));
+    const bool kv_writer = h0 == kvh * A.s_gqa;   // the first group of a KV head appends K and V
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int t0 = split * ATT_CHUNK;
     const int nt = min(ATT_CHUNK, A.n_kv - t0);
@@ -135,51 +142,57 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
     // RoPE), the new tokens' K and V source rows, norm weights and positions (RoPE), the chunk's
     // mask values. Indices are clamped and the loads unconditional; values past the ends are never
     // used. Without RoPE the K / V / weight / position loads read Q again (valid, unused).
+    // (Source rows and strides as resolved by launch_attn_decode; each load's offset is a 32-bit
+    // per-lane part over a base that is uniform across the workgroup.)
     constexpr int QR = (ATT_MAX_Q * G * HD + ATT_THREADS - 1) / ATT_THREADS;
     constexpr int KR = (ATT_MAX_Q * HD + ATT_THREADS - 1) / ATT_THREADS;
     const bool qnorm = A.rope && A.qn.x, knorm = A.rope && A.kn.x;
-    const float * qb = !A.rope ? A.q : qnorm ? A.qn.x : (const float *) A.rq.src.data;
-    const int64_t qs1 = !A.rope ? A.q_nb1 : qnorm ? A.qn.nb1 : A.rq.src.nb[1] / 4;
-    const int64_t qs2 = !A.rope ? A.q_nb2 : qnorm ? A.qn.nb2 : A.rq.src.nb[2] / 4;
     const int nqe = n_q * G * HD, nke = n_q * HD;
     float qv[QR], kx[KR], vx[KR];
+    {
+        // (unsigned indices: quotients by constants are shifts and multiplies)
+        const float * qb = A.sq + (h0 * A.sq1 + q0 * A.sq2);
 #pragma unroll
-    for (int j = 0; j < QR; j++) {
-        const int i = min(t + j * ATT_THREADS, nqe - 1);
-        const int pr = i / HD;
-        qv[j] = qb[(int64_t) (h0 + pr % G) * qs1 + (int64_t) (q0 + pr / G) * qs2 + i % HD];
-    }
-    const float * kb = !A.rope ? qb : knorm ? A.kn.x : (const float *) A.rk.src.data;
-    const int64_t ks1 = !A.rope ? qs1 : knorm ? A.kn.nb1 : A.rk.src.nb[1] / 4;
-    const int64_t ks2 = !A.rope ? qs2 : knorm ? A.kn.nb2 : A.rk.src.nb[2] / 4;
-    const float * vb = !A.rope ? qb : (const float *) A.rv.src.data;
-    const int64_t vs1 = !A.rope ? qs1 : A.rv.src.nb[1] / 4, vs2 = !A.rope ? qs2 : A.rv.src.nb[2] / 4;
+        for (int j = 0; j < QR; j++) {
+            const unsigned i = (unsigned) min(t + j * ATT_THREADS, nqe - 1);
+            const unsigned pr = i / HD;
+            qv[j] = qb[(pr % G) * A.sq1 + (pr / G) * A.sq2 + i % HD];
+        }
+        const float * kb = A.sk + kvh * A.sk1, * vb = A.sv + kvh * A.sv1;
 #pragma unroll
-    for (int j = 0; j < KR; j++) {
-        const int i = min(t + j * ATT_THREADS, nke - 1);
-        kx[j] = kb[(int64_t) kvh * ks1 + (int64_t) (i / HD) * ks2 + i % HD];
-        vx[j] = vb[(int64_t) kvh * vs1 + (int64_t) (i / HD) * vs2 + i % HD];
+        for (int j = 0; j < KR; j++) {
+            const unsigned i = (unsigned) min(t + j * ATT_THREADS, nke - 1);
+            kx[j] = kb[(i / HD) * A.sk2 + i % HD];
+            vx[j] = vb[(i / HD) * A.sv2 + i % HD];
+        }
     }
-    const float qw = (qnorm ? A.qn.w : qb)[min(t, HD - 1)];
-    const float kw = (knorm ? A.kn.w : qb)[min(t, HD - 1)];
-    const int32_t * posp = A.rope ? A.rq.pos : (const int32_t *) qb;
-    const int half = A.rope ? A.rq.p.n_dims / 2 : 1;
+    const float qw = A.sqw[min(t, HD - 1)];
+    const float kw = A.skw[min(t, HD - 1)];
+    const int half = A.s_half;
     const int tp = min(t, n_q * half - 1);          // this thread's rotation pair (clamped)
-    const int32_t my_pos = posp[tp / half];
+    const int tq = (tp >= half) + (tp >= 2 * half) + (tp >= 3 * half);   // its token (n_q <= 4 with RoPE)
+    static_assert(ATT_MAX_Q == 4, "the token of a rotation pair");
+    const int32_t my_pos = A.spos[tq];
     const bool cs_read = A.rope && A.cs_mode == 2;
-    const float2 cs_in = (cs_read ? A.cs_tab : (const float2 *) qb)[cs_read ? tp : 0];
+    const float2 cs_in = (cs_read ? A.cs_tab : (const float2 *) A.sq)[cs_read ? tp : 0];
     // the chunk's mask values (0 without a mask): an F32 and an F16 load per query, both
     // unconditional (the one of the other type reads Q), so that the dots below load nothing
     const bool mask32 = A.mask && !A.mask_f16, mask16 = A.mask && A.mask_f16;
-    const float * mrow32 = (const float *) (mask32 ? A.mask : (const void *) qb);
-    const __half * mrow16 = (const __half *) (mask16 ? A.mask : (const void *) qb);
-    float mk[ATT_MAX_Q];
+    const int mbase = q0 * A.s_mask_stride + t0;
+    const float * mrow32 = (const float *) (mask32 ? A.mask : (const void *) A.sq) + (mask32 ? mbase : 0);
+    const __half * mrow16 = (const __half *) (mask16 ? A.mask : (const void *) A.sq) + (mask16 ? mbase : 0);
+    // (raw values here, converted after the K loads are out: a conversion here would wait for
+    // every load issued so far)
+    float m32[ATT_MAX_Q];
+    __half m16[ATT_MAX_Q];
+    {
+        const int lt = min(lane, nt - 1);
 #pragma unroll
-    for (int q = 0; q < ATT_MAX_Q; q++) {
-        const int64_t mq = q0 + min(q, n_q - 1), mt = t0 + min(lane, nt - 1);
-        const float m32 = mrow32[mask32 ? mq * (A.mask_nb1 / 4) + mt : 0];
-        const __half m16 = mrow16[mask16 ? mq * (A.mask_nb1 / 2) + mt : 0];
-        mk[q] = mask32 ? m32 : mask16 ? __half2float(m16) : 0.0f;
+        for (int q = 0; q < ATT_MAX_Q; q++) {
+            const int mo = min(q, n_q - 1) * A.s_mask_stride + lt;
+            m32[q] = mrow32[mask32 ? mo : 0];
+            m16[q] = mrow16[mask16 ? mo : 0];
+        }
     }
 
     // The chunk's K rows (16-byte pieces; every load unconditional, at a clamped row, since a
@@ -193,14 +206,18 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
     constexpr int KITER = ATT_CHUNK * PIECES / ATT_THREADS;
     uint4 kv[KITER];
     {
-        const __half * kbase = A.k + (int64_t) kvh * A.k_nb1;
+        const __half * kbase = A.k + kvh * A.k_nb1 + t0 * A.k_nb2;
 #pragma unroll
         for (int it = 0; it < KITER; it++) {
-            const int pc = t + it * ATT_THREADS;
-            const int r = pc / PIECES, c = pc % PIECES;
-            kv[it] = *(const uint4 *) (kbase + (int64_t) (t0 + min(r, nt - 1)) * A.k_nb2 + c * 8);
+            const unsigned pc = t + it * ATT_THREADS;
+            const unsigned r = pc / PIECES, c = pc % PIECES;
+            kv[it] = *(const uint4 *) (kbase + (min(r, (unsigned) nt - 1) * A.k_s2 + c * 8));
         }
     }
+    __builtin_amdgcn_sched_barrier(0);   // every load above is out before any wait
+    float mk[ATT_MAX_Q];
+#pragma unroll
+    for (int q = 0; q < ATT_MAX_Q; q++) mk[q] = mask32 ? m32[q] : mask16 ? __half2float(m16[q]) : 0.0f;
 #pragma unroll
     for (int j = 0; j < QR; j++) s_q[min(t + j * ATT_THREADS, nqe - 1)] = qv[j];
 #pragma unroll
@@ -219,7 +236,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
             c = cs_in.x;
             sn = cs_in.y;
         } else if (A.rope) {
-            rope_pair_cs(A.rq.p, A.rq.ff, my_pos, tp % half, c, sn);
+            rope_pair_cs(A.rq.p, A.rq.ff, my_pos, tp - tq * half, c, sn);
             if (A.cs_mode == 1 && blockIdx.x == 0 && blockIdx.y == 0 && t < n_q * half) A.cs_tab[tp] = make_float2(c, sn);
         }
         s_cs[tp] = make_float2(c, sn);
@@ -501,7 +518,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     __shared__ float s_M[PV_MAX_ROWS], s_inv[PV_MAX_ROWS];
     uint32_t * s_v = (uint32_t *) s_buf;                  // [PV_CHUNK][HD2]
     double * s_part = (double *) s_buf;                   // [ATT_WAVES][PV_MAX_ROWS][HD], after the dots
-    const int split = blockIdx.x, h0 = blockIdx.y * G, kvh = h0 / (A.n_head / A.n_head_kv);   // as in the scores kernel
+    const int split = blockIdx.x, h0 = blockIdx.y * G;   // as in the scores kernel
+    const int kvh = __builtin_amdgcn_readfirstlane(div_small(h0, A.s_inv_gqa));
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int t0 = split * PV_CHUNK;
     const int nt = min(PV_CHUNK, A.n_kv - t0);
@@ -509,7 +527,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     const int n_rows = min(pvq, A.n_q - q0) * G;      // <= PV_MAX_ROWS (pvq = PV_MAX_ROWS / G or 1)
     const attn_scratch S = scratch_of(A);
     const int nseg = attn_segs(A.n_kv);
-    auto row_of = [&](int pr) { return (int64_t) (q0 + pr / G) * A.n_head + h0 + pr % G; };
+    // scratch row of workgroup row pr (32-bit: launch_attn_decode checks the scratch indices)
+    auto row_of = [&](int pr) { return (q0 + pr / G) * A.n_head + h0 + pr % G; };
 
     // loads, in the order they are needed (they complete in issue order): the chunk's scores of
     // every row (with the statistics launch: its e values), the segment sums, then the chunk's V
@@ -544,12 +563,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
         for (int k = 0; k < nseg; k++) ssum += S.ssum[row_of(t) * nseg + k];   // segment order
     }
     uint4 vv[ITER];
-    const __half * vbase = A.v + (int64_t) kvh * A.v_nb1;
+    const __half * vbase = A.v + kvh * A.v_nb1 + t0 * A.v_nb2;
 #pragma unroll
     for (int it = 0; it < ITER; it++) {
-        const int pc = t + it * ATT_THREADS;
-        const int r = pc / PIECES, c = pc % PIECES;
-        vv[it] = *(const uint4 *) (vbase + (int64_t) (t0 + min(r, nt - 1)) * A.v_nb2 + c * 8);
+        const unsigned pc = t + it * ATT_THREADS;
+        const unsigned r = pc / PIECES, c = pc % PIECES;
+        vv[it] = *(const uint4 *) (vbase + (min(r, (unsigned) nt - 1) * A.v_s2 + c * 8));
     }
     // rows staged as zero: padding rows past the end (their loads read the last row; no term) and,
     // with skip_masked, rows masked for every query of the workgroup (their p is 0 for every row).
@@ -707,11 +726,6 @@ typedef double v4d __attribute__((ext_vector_type(4)));
 
 constexpr int MQ_ROWS = 16;
 
-// r / g for 0 <= r < MQ_MAX_ROWS and 1 <= g <= 64, with inv_g = 1.0f / g, in three float
-// operations: (r + 0.5) / g lies at least 1 / (2 g) >= 1/128 from every integer, and the float
-// product is within MQ_MAX_ROWS * 2^-23 = 1/512 of it, so truncating it gives the quotient.
-constexpr int MQ_MAX_ROWS = 16384;
-__device__ __forceinline__ int div_small(int r, float inv_g) { return (int) (((float) r + 0.5f) * inv_g); }
 
 __host__ __device__ inline int mq_tiles(const attn_launch & A) {
     return (A.n_q * (A.n_head / A.n_head_kv) + MQ_ROWS - 1) / MQ_ROWS;
@@ -999,7 +1013,7 @@ static void launch_attn_mq(const attn_launch & A, hipStream_t st) {
     const int tiles = mq_tiles(A);
     // the kernels' quotient by the GQA group and their 32-bit offsets
     const int64_t G = A.n_head / A.n_head_kv, lim = INT32_MAX;
-    if (A.n_q * G >= MQ_MAX_ROWS || G > 64) HIP_ABORT("attn: %d queries x %d heads per KV head past the multi-query rows", A.n_q, (int) G);
+    if (A.n_q * G >= DIV_SMALL_MAX || G > 64) HIP_ABORT("attn: %d queries x %d heads per KV head past the multi-query rows", A.n_q, (int) G);
     const bool fits = (A.n_head - 1) * A.q_nb1 + (A.n_q - 1) * A.q_nb2 + HD <= lim &&
                       (A.n_head_kv - 1) * A.k_nb1 + (int64_t) (A.n_kv - 1) * A.k_nb2 + HD <= lim &&
                       (A.n_head_kv - 1) * A.v_nb1 + (int64_t) (A.n_kv - 1) * A.v_nb2 + HD <= lim &&
@@ -1062,7 +1076,56 @@ static void launch_attn_hd(const attn_launch & A, hipStream_t st) {
     }
 }
 
-void launch_attn_decode(const attn_launch & A, hipStream_t st) {
+// The decode kernels' source rows with 32-bit element strides (attn_launch::sq and the fields after
+// it), checked so that every per-lane offset the kernels form fits 32 bits.
+static attn_launch resolve_sources(const attn_launch & A) {
+    attn_launch B = A;
+    const bool qnorm = A.rope && A.qn.x, knorm = A.rope && A.kn.x;
+    int64_t q1 = A.q_nb1, q2 = A.q_nb2;
+    B.sq = A.q;
+    if (A.rope) {
+        B.sq = qnorm ? A.qn.x : (const float *) A.rq.src.data;
+        q1 = qnorm ? A.qn.nb1 : A.rq.src.nb[1] / 4;
+        q2 = qnorm ? A.qn.nb2 : A.rq.src.nb[2] / 4;
+    }
+    int64_t k1 = q1, k2 = q2, v1 = q1, v2 = q2;
+    B.sk = B.sv = B.sq;
+    if (A.rope) {
+        B.sk = knorm ? A.kn.x : (const float *) A.rk.src.data;
+        k1 = knorm ? A.kn.nb1 : A.rk.src.nb[1] / 4;
+        k2 = knorm ? A.kn.nb2 : A.rk.src.nb[2] / 4;
+        B.sv = (const float *) A.rv.src.data;
+        v1 = A.rv.src.nb[1] / 4;
+        v2 = A.rv.src.nb[2] / 4;
+    }
+    B.sqw = qnorm ? A.qn.w : B.sq;
+    B.skw = knorm ? A.kn.w : B.sq;
+    B.spos = A.rope ? A.rq.pos : (const int32_t *) B.sq;
+    B.s_half = A.rope ? A.rq.p.n_dims / 2 : 1;
+    const int64_t ms = A.mask ? A.mask_nb1 / (A.mask_f16 ? 2 : 4) : 0;
+    const int64_t lim = INT32_MAX;
+    const bool fits = (A.n_head - 1) * q1 + (A.n_q - 1) * q2 + A.hd <= lim &&
+                      (A.n_head_kv - 1) * k1 + (A.n_q - 1) * k2 + A.hd <= lim &&
+                      (A.n_head_kv - 1) * v1 + (A.n_q - 1) * v2 + A.hd <= lim &&
+                      std::max(ATT_CHUNK, PV_CHUNK) * std::max(A.k_nb2, A.v_nb2) + A.hd <= lim &&
+                      (A.n_q - 1) * ms + A.n_kv <= lim && q1 >= 0 && q2 >= 0 && k1 >= 0 && k2 >= 0 && v1 >= 0 && v2 >= 0 &&
+                      (int64_t) A.n_q * A.n_head * A.n_kv <= lim &&
+                      (int64_t) (A.n_kv + PV_CHUNK - 1) / PV_CHUNK * A.n_q * A.n_head * A.hd <= lim;
+    if (!fits) HIP_ABORT("attn: operand strides past 32-bit element offsets");
+    B.sq1 = (int32_t) q1; B.sq2 = (int32_t) q2;
+    B.sk1 = (int32_t) k1; B.sk2 = (int32_t) k2;
+    B.sv1 = (int32_t) v1; B.sv2 = (int32_t) v2;
+    B.s_mask_stride = (int32_t) ms;
+    B.k_s2 = (int32_t) A.k_nb2;
+    B.v_s2 = (int32_t) A.v_nb2;
+    B.s_gqa = A.n_head / A.n_head_kv;
+    B.s_inv_gqa = 1.0f / (float) B.s_gqa;
+    if (A.n_head >= DIV_SMALL_MAX || B.s_gqa > 64) HIP_ABORT("attn: %d heads in groups of %d", A.n_head, B.s_gqa);
+    return B;
+}
+
+void launch_attn_decode(const attn_launch & A_in, hipStream_t st) {
+    const attn_launch A = resolve_sources(A_in);
     if (A.n_q < 1 || A.n_q > ATT_DECODE_MAX_Q) HIP_ABORT("attn: n_q %d out of range", A.n_q);
     if (A.rope && A.n_q > ATT_MAX_Q) HIP_ABORT("attn: RoPE folded in for at most %d queries", ATT_MAX_Q);
     if (A.n_head % A.n_head_kv) HIP_ABORT("attn: n_head %% n_head_kv");

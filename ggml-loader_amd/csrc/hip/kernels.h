@@ -398,6 +398,20 @@ struct attn_launch {
     // flash_attn_ext's probabilities: ggml's flash op never materializes KQ, so p = exp(s - M) / S
     // stays a float into the PV sums (1); the manual chain's V mul_mat converts p to F16 first (0)
     int            p_f32;
+    // Set by launch_attn_decode from the fields above (callers leave them zero): the rows the
+    // decode kernels read, with 32-bit element strides, so that their per-lane offsets are 32-bit.
+    // Q source rows (before QK-Norm and RoPE) at sq + head * sq1 + token * sq2; with RoPE the new
+    // tokens' K and V source rows at sk / sv + kv_head * s?1 + token * s?2, otherwise q (valid,
+    // unused), as are the QK-Norm weights sqw / skw without the norm and the positions spos
+    // without RoPE.
+    const float *  sq, * sk, * sv, * sqw, * skw;
+    const int32_t * spos;
+    int32_t        sq1, sq2, sk1, sk2, sv1, sv2;
+    int32_t        s_half;         // rotation pairs per row (1 without RoPE)
+    int32_t        s_mask_stride;  // elements per mask row
+    int32_t        k_s2, v_s2;     // k_nb2, v_nb2
+    int32_t        s_gqa;          // n_head / n_head_kv
+    float          s_inv_gqa;      // 1 / s_gqa
 };
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd);
 // split-KV decode attention for 1 <= n_q <= ATT_DECODE_MAX_Q queries (groups of 4 per workgroup;
