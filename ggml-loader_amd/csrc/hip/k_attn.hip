@@ -1320,32 +1320,42 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
     }
     __syncthreads();
 
-    // ---- scores, over the live chunks; the next live chunk's K rows load while this one is used ----
-    // The Q tile as the MFMA A operands, converted once: lane (i + 16 k) holds Q[i][4 j + k] for every
-    // 4-dim step j
+    // ---- scores, over the live chunks; wave w takes positions 16 w .. 16 w + 15 of each. The sum
+    // over the head dims is exact in any order, so lane group g = lane / 16 takes the NJ consecutive
+    // dims NJ g .. NJ g + NJ - 1 (MFMA step j: dim NJ g + j): a lane's K operands are NJ / 8
+    // 16-byte pieces of its position's row, loaded straight into registers (no LDS, no barrier),
+    // the next live chunk's while this one is used. Q as the A operands, converted once: lane
+    // (i + 16 g) holds Q[i][NJ g + j]. ----
     constexpr int NJ = HD / 4;
+    constexpr int KU = NJ / 8;                   // 16-byte pieces of a lane's K slice
+    static_assert(NJ % 8 == 0, "whole 16-byte K pieces per lane");
     double qd[NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; j++) qd[j] = (double) __half2float(s_q[(lane % 16) * KSTR + 4 * j + lane / 16]);
-    uint4 kv[ITER];
+    for (int j = 0; j < NJ; j++) qd[j] = (double) __half2float(s_q[(lane % 16) * KSTR + NJ * (lane / 16) + j]);
+    const __half * kslice = kbase + NJ * (lane / 16);
+    auto load_k = [&](uint4 (&v)[KU], int c) {
+        const int t = min(c * APF_CHUNK + wave * 16 + lane % 16, n_kv - 1);   // clamped, unused past the end
+        const uint4 * src = (const uint4 *) (kslice + (int64_t) t * A.k_nb2);
+#pragma unroll
+        for (int u = 0; u < KU; u++) v[u] = src[u];
+    };
+    uint4 kc[KU], kn[KU];
     int ch = next_live(0);
-    if (ch < n_chunks) load_rows(kv, kbase, A.k_nb2, ch * APF_CHUNK, min(APF_CHUNK, n_kv - ch * APF_CHUNK));
+    if (ch < n_chunks) load_k(kc, ch);
     while (ch < n_chunks) {
         const int t0 = ch * APF_CHUNK, nt = min(APF_CHUNK, n_kv - t0);
-        store_rows(kv, t0, nt, false);
-        __syncthreads();
         const int nx = next_live(ch + 1);
-        if (nx < n_chunks) load_rows(kv, kbase, A.k_nb2, nx * APF_CHUNK, min(APF_CHUNK, n_kv - nx * APF_CHUNK));
-        // two independent accumulation chains (dims 8i .. 8i + 3 and 8i + 4 .. 8i + 7), added at
-        // the end: the double sums are exact for these operands, so the grouping does not matter
+        if (nx < n_chunks) load_k(kn, nx);
+        // two independent accumulation chains (even and odd steps), added at the end: the double
+        // sums are exact for these operands, so the grouping does not matter
         v4d acc = { 0.0, 0.0, 0.0, 0.0 }, acc2 = { 0.0, 0.0, 0.0, 0.0 };
-        const __half * kr = s_kv + (wave * 16 + lane % 16) * KSTR + lane / 16;
-        static_assert(HD % 8 == 0, "pairs of 4-dim steps");
+        uint32_t kw[NJ / 2];
+        __builtin_memcpy(kw, kc, sizeof(kw));
 #pragma unroll
         for (int j = 0; j < NJ; j += 2) {
-            const double b = (double) __half2float(kr[4 * j]), b2 = (double) __half2float(kr[4 * j + 4]);
-            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(qd[j], b, acc, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(qd[j + 1], b2, acc2, 0, 0, 0);
+            const float2 b = __half22float2(*(const __half2 *) &kw[j / 2]);
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(qd[j], (double) b.x, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(qd[j + 1], (double) b.y, acc2, 0, 0, 0);
         }
         acc += acc2;
         const int t = wave * 16 + lane % 16;
@@ -1358,7 +1368,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
                 *sp = mv == -INFINITY ? -INFINITY : (float) acc[r] * A.scale + mv;
             }
         }
-        __syncthreads();                         // every wave's reads of this chunk's s_kv are done
+#pragma unroll
+        for (int u = 0; u < KU; u++) kc[u] = kn[u];
         ch = nx;
     }
     __syncthreads();
@@ -1416,6 +1427,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_prefill_kernel(const attn_la
     v4d acc[NT];
 #pragma unroll
     for (int k = 0; k < NT; k++) acc[k] = v4d{ 0.0, 0.0, 0.0, 0.0 };
+    uint4 kv[ITER];
     ch = next_live(0);
     if (ch < n_chunks) load_rows(kv, vbase, A.v_nb2, ch * APF_CHUNK, min(APF_CHUNK, n_kv - ch * APF_CHUNK));
     while (ch < n_chunks) {
