@@ -241,6 +241,9 @@ void launch_argsort(const tview & a, const tview & dst, bool desc, hipStream_t s
 
 // out[:, t] = ((e[:, 0, t] * w[0, t] + e[:, 1, t] * w[1, t]) + ...) (+ res[:, t]): the graph's
 // mul by the routing weights, its chain of adds over the slots in order, and the residual add
+// Up to WS_BATCH slots' values are loaded together before the sum (a loop of load -> use would put
+// one round trip per slot on the path); the products are added in slot order as before.
+constexpr int WS_BATCH = 8;
 __global__ void moe_wsum_kernel(moe_wsum M) {
     prefetch_kernargs<sizeof(moe_wsum)>();
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
@@ -248,9 +251,25 @@ __global__ void moe_wsum_kernel(moe_wsum M) {
     if (i >= M.n_embd) return;
     const float * e = M.e + t * M.e_nb2 + i;
     const float * w = M.w + t * M.w_nb2;
-    float acc = e[0] * w[0];
-    for (int s = 1; s < M.k; s++) acc = acc + e[s * M.e_nb1] * w[s * M.w_nb1];
-    if (M.res) acc = acc + M.res[t * M.res_nb1 + i];
+    const float r = M.res ? M.res[t * M.res_nb1 + i] : 0.0f;
+    float acc = 0.0f;
+    for (int s0 = 0; s0 < M.k; s0 += WS_BATCH) {
+        float ev[WS_BATCH], wv[WS_BATCH];
+#pragma unroll
+        for (int j = 0; j < WS_BATCH; j++) {
+            const int s = min(s0 + j, M.k - 1);   // clamped, unused past k
+            ev[j] = e[s * M.e_nb1];
+            wv[j] = w[s * M.w_nb1];
+        }
+        __builtin_amdgcn_sched_barrier(0);   // every load above is out before any wait
+#pragma unroll
+        for (int j = 0; j < WS_BATCH; j++) {
+            const float p = ev[j] * wv[j];
+            const float nx = s0 + j == 0 ? p : acc + p;
+            acc = s0 + j < M.k ? nx : acc;
+        }
+    }
+    if (M.res) acc = acc + r;
     M.out[t * M.out_nb1 + i] = acc;
 }
 
@@ -905,11 +924,47 @@ __global__ __launch_bounds__(256) void mul_mat_rows_norm_kernel(tview w, const f
     const int64_t K = w.ne[0], col = blockIdx.y;
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const float * xc = x + col * x_stride;
+    const int64_t o = (int64_t) blockIdx.x * 4 + wave;   // this wave's output row
+    const float * a = (const float *) (w.data + min(o, w.ne[1] - 1) * w.nb[1]);   // clamped; not stored past the end
+    const int nch = (int) (K / 8);
+    // Loads first, none depending on another and in the order they are used (loads complete in
+    // issue order): the column, the norm weight, then the first batch of this wave's weight row
+    // (which does not depend on the column). Up to RB * 256 elements (the MoE router's 2048) they
+    // are one straight batch: a loop of load -> use puts one round trip per iteration on the path,
+    // and a loop header makes the compiler wait for every load in flight. Indices clamped, values
+    // past the ends unused.
+    constexpr int RB = 8;
+    const bool one_batch = K <= RB * 256;
+    float xv[RB], nv[RB];
+    if (one_batch) {
+#pragma unroll
+        for (int j = 0; j < RB; j++) xv[j] = xc[min((int64_t) t + j * 256, K - 1)];
+#pragma unroll
+        for (int j = 0; j < RB; j++) nv[j] = nw[min((int64_t) t + j * 256, K - 1)];
+    }
+    float4 wa[MR_BATCH][2];
+#pragma unroll
+    for (int j = 0; j < MR_BATCH; j++) {
+        const int c = min(j * WAVE + lane, nch - 1);
+        wa[j][0] = ((const float4 *) a)[2 * c];
+        wa[j][1] = ((const float4 *) a)[2 * c + 1];
+    }
     double sum = 0.0;
-    for (int64_t i = t; i < K; i += 256) {
-        const float v = xc[i];
-        s_y[i] = v;
-        sum += (double) (v * v);
+    if (one_batch) {
+#pragma unroll
+        for (int j = 0; j < RB; j++) {
+            const int64_t i = t + j * 256;
+            if (i < K) {
+                s_y[i] = xv[j];
+                sum += (double) (xv[j] * xv[j]);
+            }
+        }
+    } else {
+        for (int64_t i = t; i < K; i += 256) {
+            const float v = xc[i];
+            s_y[i] = v;
+            sum += (double) (v * v);
+        }
     }
     sum = wave_sum_d(sum);
     if (lane == 0) s_part[wave] = sum;
@@ -917,18 +972,36 @@ __global__ __launch_bounds__(256) void mul_mat_rows_norm_kernel(tview w, const f
     const double total = s_part[0] + s_part[1] + s_part[2] + s_part[3];
     const float mean = (float) (total / (double) K);
     const float scale = 1.0f / sqrtf(mean + eps);
-    for (int64_t i = t; i < K; i += 256) {
-        const float o = (s_y[i] * scale) * nw[i];
-        s_y[i] = o;
-        if (blockIdx.x == 0) y_out[col * y_stride + i] = o;
+    if (one_batch) {
+#pragma unroll
+        for (int j = 0; j < RB; j++) {
+            const int64_t i = t + j * 256;
+            if (i < K) {
+                const float on = (s_y[i] * scale) * nv[j];
+                s_y[i] = on;
+                if (blockIdx.x == 0) y_out[col * y_stride + i] = on;
+            }
+        }
+    } else {
+        for (int64_t i = t; i < K; i += 256) {
+            const float on = (s_y[i] * scale) * nw[i];
+            s_y[i] = on;
+            if (blockIdx.x == 0) y_out[col * y_stride + i] = on;
+        }
     }
     __syncthreads();
-    const int64_t o = (int64_t) blockIdx.x * 4 + wave;
     if (o >= w.ne[1]) return;
-    const float * a = (const float *) (w.data + o * w.nb[1]);
-    const int nch = (int) (K / 8);
     double acc = 0.0;
     for (int c0 = 0; c0 < nch; c0 += MR_BATCH * WAVE) {
+        // the first batch's weights are already in registers; later batches load here
+        if (c0 > 0) {
+#pragma unroll
+            for (int j = 0; j < MR_BATCH; j++) {
+                const int c = min(c0 + j * WAVE + lane, nch - 1);
+                wa[j][0] = ((const float4 *) a)[2 * c];
+                wa[j][1] = ((const float4 *) a)[2 * c + 1];
+            }
+        }
         float wv[MR_BATCH][8], v[MR_BATCH][8];
 #pragma unroll
         for (int j = 0; j < MR_BATCH; j++) {
@@ -936,9 +1009,8 @@ __global__ __launch_bounds__(256) void mul_mat_rows_norm_kernel(tview w, const f
             const float4 x0 = ((const float4 *) s_y)[2 * c], x1 = ((const float4 *) s_y)[2 * c + 1];
             v[j][0] = x0.x; v[j][1] = x0.y; v[j][2] = x0.z; v[j][3] = x0.w;
             v[j][4] = x1.x; v[j][5] = x1.y; v[j][6] = x1.z; v[j][7] = x1.w;
-            const float4 a0 = ((const float4 *) a)[2 * c], a1 = ((const float4 *) a)[2 * c + 1];
-            wv[j][0] = a0.x; wv[j][1] = a0.y; wv[j][2] = a0.z; wv[j][3] = a0.w;
-            wv[j][4] = a1.x; wv[j][5] = a1.y; wv[j][6] = a1.z; wv[j][7] = a1.w;
+            wv[j][0] = wa[j][0].x; wv[j][1] = wa[j][0].y; wv[j][2] = wa[j][0].z; wv[j][3] = wa[j][0].w;
+            wv[j][4] = wa[j][1].x; wv[j][5] = wa[j][1].y; wv[j][6] = wa[j][1].z; wv[j][7] = wa[j][1].w;
         }
 #pragma unroll
         for (int j = 0; j < MR_BATCH; j++) {
