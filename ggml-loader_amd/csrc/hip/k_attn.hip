@@ -447,34 +447,38 @@ constexpr int pv_lds_bytes() {
     return (PV_CHUNK * HD * 2 > ATT_WAVES * PV_MAX_ROWS * HD * 8 ? PV_CHUNK * HD * 2 : ATT_WAVES * PV_MAX_ROWS * HD * 8);
 }
 
-// The output of (head h, query q): two threads per dim each add half of the chunk partials in
-// chunk order, then the two halves are added (the sums are exact for these operands, so the
-// grouping does not change the result); stored as F32 and, with out_q, as Q8_0 blocks. Every
-// thread of the workgroup calls it (threads from 2 HD on only take part in its barrier).
+// The output of (head h, query q): CMB_PARTS threads per dim each add a consecutive run of the
+// chunk partials in chunk order, CMB_PER at a time with all of their loads in flight (a run of
+// dependent load -> add would put one round trip per partial on the path), then the runs' sums are
+// added in run order (the sums are exact for these operands, so the grouping does not change the
+// result); stored as F32 and, with out_q, as Q8_0 blocks.
+constexpr int CMB_PARTS = 8;
+constexpr int CMB_PER = 9;
 template <int HD>
-__device__ __forceinline__ void combine_head(const attn_launch & A, const attn_scratch & S, int h, int q, int n_splits,
-                                             double * s_half) {
+__global__ __launch_bounds__(CMB_PARTS * HD) void attn_combine_kernel(const attn_launch A_, int n_splits) {
+    const attn_launch & A = kernargs_prefetched(A_);
+    __shared__ double s_run[CMB_PARTS][HD];
+    const attn_scratch S = scratch_of(A);
+    const int h = blockIdx.x, q = blockIdx.y;
     const int d = threadIdx.x % HD, part = threadIdx.x / HD;
+    const double * pp = S.parts + ((int64_t) q * A.n_head + h) * HD + d;
+    const int64_t step = (int64_t) A.n_q * A.n_head * HD;
+    const int per = (n_splits + CMB_PARTS - 1) / CMB_PARTS;
+    const int s0 = part * per, s1 = min(n_splits, s0 + per);
     double acc = 0.0;
-    if (part < 2) {
-        const double * pp = S.parts + ((int64_t) q * A.n_head + h) * HD + d;
-        const int64_t step = (int64_t) A.n_q * A.n_head * HD;
-        const int mid = (n_splits + 1) / 2;
-        const int s0 = part ? mid : 0, s1 = part ? n_splits : mid;
-        int s = s0;
-        for (; s + 8 <= s1; s += 8) {
-            double v[8];
+    for (int b = s0; b < s1; b += CMB_PER) {
+        double v[CMB_PER];
 #pragma unroll
-            for (int k = 0; k < 8; k++) v[k] = pp[(s + k) * step];
+        for (int k = 0; k < CMB_PER; k++) v[k] = pp[min(b + k, n_splits - 1) * step];   // clamped, unused past s1
 #pragma unroll
-            for (int k = 0; k < 8; k++) acc += v[k];
-        }
-        for (; s < s1; s++) acc += pp[s * step];
+        for (int k = 0; k < CMB_PER; k++) acc += b + k < s1 ? v[k] : 0.0;
     }
-    if (part == 1) s_half[d] = acc;
+    s_run[part][d] = acc;
     __syncthreads();
     if (part != 0) return;
-    acc += s_half[d];
+    acc = s_run[0][d];
+#pragma unroll
+    for (int p = 1; p < CMB_PARTS; p++) acc += s_run[p][d];
     const float v = (float) acc;
     const int64_t oi = (int64_t) h * HD + d;
     A.out[(int64_t) q * A.out_nb1 + oi] = v;
@@ -492,14 +496,6 @@ __device__ __forceinline__ void combine_head(const attn_launch & A, const attn_s
             A.out_q.s[q * (K / 32) + oi / 32] = (int32_t) qsum;
         }
     }
-}
-
-// one workgroup of 2 HD threads per (head, query)
-template <int HD>
-__global__ __launch_bounds__(2 * HD) void attn_combine_kernel(const attn_launch A_, int n_splits) {
-    const attn_launch & A = kernargs_prefetched(A_);
-    __shared__ double s_half[HD];
-    combine_head<HD>(A, scratch_of(A), blockIdx.x, blockIdx.y, n_splits, s_half);
 }
 
 // FSK > 0 (one query, one head per workgroup, n_kv <= FSK * ATT_THREADS): the workgroup forms its row's
@@ -1024,7 +1020,7 @@ static void launch_attn_mq(const attn_launch & A, hipStream_t st) {
     launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
     if (A.p_f32) launch((attn_pv_mq_kernel<HD, true>), dim3(pv_splits, A.n_head_kv, tiles), dim3(ATT_THREADS), 0, st, A);
     else launch((attn_pv_mq_kernel<HD, false>), dim3(pv_splits, A.n_head_kv, tiles), dim3(ATT_THREADS), 0, st, A);
-    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(2 * HD), 0, st, A, pv_splits);
+    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(CMB_PARTS * HD), 0, st, A, pv_splits);
 }
 
 template <int HD, int G>
@@ -1050,7 +1046,7 @@ static void launch_attn_t(const attn_launch & A, hipStream_t st) {
         launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
         launch((attn_pv_kernel<HD, G, 0>), pv_grid, dim3(ATT_THREADS), 0, st, A, pvq);
     }
-    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(2 * HD), 0, st, A, pv_splits);
+    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(CMB_PARTS * HD), 0, st, A, pv_splits);
 }
 
 template <int HD>
