@@ -812,7 +812,7 @@ private:
         const ggml_tensor * x = n->src[0];
         if (!fuse(FUSE_NORM) || !fuse(FUSE_ROPE) || !fuse(FUSE_ATTN) || n->op != GGML_OP_RMS_NORM) return false;
         if (x->type != GGML_TYPE_F32 || !ggml_is_contiguous(x) || !ggml_is_contiguous(n) || x->ne[0] > 256 ||
-            x->ne[3] != 1 || ggml_nrows(x) > 4 * 64) return false;
+            x->ne[3] != 1) return false;
         const int u = sole_user(i);
         if (u < 0) return false;
         const ggml_tensor * m = g_->nodes[u];
@@ -881,8 +881,31 @@ private:
             for (int j : members) done_[j] = true;
             return;
         }
+        // a held-back QK-Norm of a rotation's input runs inside the RoPE launch (one wave per row)
+        // where its rows fit, otherwise just before it
         for (int j : members) {
-            if (g_->nodes[j]->op == GGML_OP_ROPE) materialize_norm(g_->nodes[j]->src[0]);
+            const ggml_tensor * r = g_->nodes[j];
+            if (r->op != GGML_OP_ROPE) continue;
+            const ggml_tensor * m = r->src[0];
+            auto it = pnorm_.find(m);
+            if (it == pnorm_.end()) continue;
+            const ggml_tensor * x = it->second.x;
+            rope_job * J = nullptr;
+            for (int k = 0; k < B.n_jobs; k++) if (B.job[k].pos && B.job[k].src.data == (char *) m->data) J = &B.job[k];
+            const bool fits = J && fuse(FUSE_NORM) && x->ne[0] == m->ne[0] && x->ne[0] <= 256 && x->nb[0] == sizeof(float) &&
+                              x->ne[1] == m->ne[1] && x->ne[2] == m->ne[2] && x->ne[3] == 1 && m->ne[3] == 1 &&
+                              J->p.n_dims <= m->ne[0];
+            if (!fits) {
+                materialize_norm(m);
+                continue;
+            }
+            const qk_norm qn = qk_norm_of(m);
+            J->norm_x = qn.x;
+            J->norm_nb1 = qn.nb1;
+            J->norm_nb2 = qn.nb2;
+            J->norm_w = qn.w;
+            J->norm_eps = qn.eps;
+            J->n = m->ne[1] * m->ne[2];
         }
         // many tokens (prefill): the rotations read one (cos, sin) table per graph instead of
         // forming the same angles for every head of every layer
@@ -984,7 +1007,8 @@ private:
         const ggml_tensor * qsrc = g_->nodes[qi]->src[0], * ksrc = g_->nodes[kc]->src[0]->src[0];
         for (const ggml_tensor * src : { qsrc, ksrc }) {
             auto it = pnorm_.find(src);
-            if (it != pnorm_.end() && (it->second.x->ne[0] != hd || it->second.x->nb[0] != sizeof(float))) return false;
+            if (it != pnorm_.end() && (it->second.x->ne[0] != hd || it->second.x->nb[0] != sizeof(float) ||
+                                       ggml_nrows(it->second.x) > 4 * 64)) return false;
         }
         prope_ = pending_rope{ a, B.job[jq], B.job[jk], B.job[jv], qk_norm_of(qsrc), qk_norm_of(ksrc) };
         wrote_.push_back(g_->nodes[kc]);

@@ -572,14 +572,68 @@ __device__ __forceinline__ void copy_elem(const rope_job & J, IDX li) {
     st(at(J.dst, b[0], b[1], b[2], b[3]), J.dst.type, ld(at(J.src, a[0], a[1], a[2], a[3]), J.src.type));
 }
 
+// Row r of a RoPE job with a QK-Norm, by one wave: the row's sum of squares in double and
+// scale = 1 / sqrtf((float) (sum / hd) + eps), as the rms_norm op forms them; y = (x * scale) * w
+// (the norm's mul) into the wave's LDS row; then each rotation pair as rope_pair rotates it.
+constexpr int ROPE_NORM_MAX_HD = 256;
+__device__ __forceinline__ void rope_norm_row(const rope_job & J, int64_t r, int lane, float * s_row) {
+    const int hd = (int) J.src.ne[0];
+    const int64_t i1 = r % J.src.ne[1], i2 = r / J.src.ne[1];   // (head, token); ne[3] == 1
+    const float * xr = J.norm_x + i1 * J.norm_nb1 + i2 * J.norm_nb2;
+    constexpr int PER = ROPE_NORM_MAX_HD / WAVE;
+    float xv[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) xv[k] = xr[min(lane + WAVE * k, hd - 1)];   // clamped, unused past hd
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < PER; k++) if (lane + WAVE * k < hd) ss += (double) (xv[k] * xv[k]);
+    ss = wave_sum_d(ss);
+    const float scale = 1.0f / sqrtf((float) (ss / (double) hd) + J.norm_eps);
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int e = lane + WAVE * k;
+        if (e < hd) s_row[e] = (xv[k] * scale) * J.norm_w[e];
+    }
+    // the wave's LDS writes are visible to its own later reads (in order within a wave)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const rope_params & p = J.p;
+    const int half = p.n_dims / 2;
+    const bool neox = (p.mode & GGML_ROPE_TYPE_NEOX) != 0;
+    for (int ip = lane; ip < half; ip += WAVE) {
+        float c, sn;
+        if (J.cs) {
+            const float2 v = J.cs[i2 * half + ip];
+            c = v.x;
+            sn = v.y;
+        } else {
+            rope_pair_cs(p, J.ff, J.pos[i2], ip, c, sn);
+        }
+        const int a0 = neox ? ip : 2 * ip, a1 = neox ? ip + half : 2 * ip + 1;
+        const float x0 = s_row[a0], x1 = s_row[a1];
+        st(at(J.dst, a0, i1, i2, 0), J.dst.type, x0 * c - x1 * sn);
+        st(at(J.dst, a1, i1, i2, 0), J.dst.type, x0 * sn + x1 * c);
+    }
+    for (int e = p.n_dims + lane; e < hd; e += WAVE) st(at(J.dst, e, i1, i2, 0), J.dst.type, s_row[e]);
+}
+
 // Independent RoPE and copy jobs of one decode step in one launch (Q rotation; K rotation stored
 // straight into the F16 KV cache; V appended to it). Each job owns a whole number of workgroups.
 __global__ __launch_bounds__(256) void rope_batch_kernel(const rope_batch B) {
     prefetch_kernargs<sizeof(rope_batch)>();
+    __shared__ float s_rows[256 / WAVE][ROPE_NORM_MAX_HD];
     int j = 0;
 #pragma unroll
     for (int k = 1; k < ROPE_MAX_JOBS; k++) if (k < B.n_jobs && (int64_t) blockIdx.x >= B.first_block[k]) j = k;
     const rope_job & J = B.job[j];
+    if (J.norm_x) {
+        // one wave per row (no workgroup barrier: a wave past the rows just ends)
+        const int wave = threadIdx.x / WAVE;
+        const int64_t r = ((int64_t) blockIdx.x - B.first_block[j]) * (256 / WAVE) + wave;
+        if (r < J.n) rope_norm_row(J, r, threadIdx.x % WAVE, s_rows[wave]);
+        return;
+    }
     const int64_t li = ((int64_t) blockIdx.x - B.first_block[j]) * blockDim.x + threadIdx.x;
     if (li >= J.n) return;
     if (J.n <= (int64_t) UINT32_MAX) {
@@ -594,8 +648,13 @@ __global__ __launch_bounds__(256) void rope_batch_kernel(const rope_batch B) {
 void launch_rope_batch(rope_batch & B, hipStream_t st) {
     int64_t blocks = 0;
     for (int k = 0; k < B.n_jobs; k++) {
+        const rope_job & J = B.job[k];
+        if (J.norm_x && (J.src.ne[0] > ROPE_NORM_MAX_HD || J.src.ne[3] != 1 || J.n != J.src.ne[1] * J.src.ne[2] || !J.pos ||
+                         J.p.n_dims > J.src.ne[0])) {
+            HIP_ABORT("rope: a QK-Norm job needs rows of at most %d floats", ROPE_NORM_MAX_HD);
+        }
         B.first_block[k] = blocks;
-        blocks += grid1(B.job[k].n, 256);
+        blocks += J.norm_x ? grid1(J.n, 256 / WAVE) : grid1(J.n, 256);
     }
     if (blocks == 0) return;
     launch(rope_batch_kernel, dim3((unsigned) blocks), dim3(256), 0, st, B);

@@ -276,8 +276,15 @@ struct rope_job {
     const int32_t * pos;
     const float * ff;          // optional frequency factors
     rope_params p;
-    int64_t n;                 // work items: rotation pairs, or elements for a copy
+    int64_t n;                 // work items: rotation pairs, or elements for a copy (rows with norm_x)
     const float2 * cs;         // optional (cos, sin) table [token][n_dims / 2] (launch_rope_table)
+    // optional QK-Norm of the rows before the rotation (rms_norm(x) * w, the ops' roundings): the
+    // rotated rows are (head, token) rows of src's shape read from norm_x + head * norm_nb1 +
+    // token * norm_nb2 (floats, src.ne[0] <= 256 contiguous), one wave per row; src's data unused
+    const float * norm_x;
+    int64_t norm_nb1, norm_nb2;
+    const float * norm_w;
+    float norm_eps;
 };
 struct rope_batch {
     rope_job job[ROPE_MAX_JOBS];

@@ -542,6 +542,58 @@ def test_rope_and_kv_append_batched(hip, cpu, mode, hd, n_new):
     assert np.array_equal(ref[2].reshape(n_ctx, n_head_kv, hd)[n_past:n_past + n_new], v.astype(np.float16))
 
 
+@pytest.mark.parametrize("mode,hd,n_dims,n_new", [
+    (gl.ROPE_NEOX, 128, 128, 16),    # the MoE 16-token step (Q: 32 heads x 16 tokens = 512 rows)
+    (gl.ROPE_NORMAL, 128, 128, 5),
+    (gl.ROPE_NEOX, 64, 32, 33),      # a partial rotation: dims past n_dims are copied
+    (gl.ROPE_NORMAL, 96, 64, 20),    # and across the (cos, sin) table's threshold of 16 tokens
+])
+def test_rope_with_qk_norm_batched(hip, cpu, mode, hd, n_dims, n_new):
+    """QK-Norm (rms_norm(x) * w over the head dimension, model.cpp:1382-1387) in front of RoPE for
+    more tokens than the attention folds in: the norm runs inside the RoPE launch, one wave per
+    (head, token) row, with the rms_norm and mul ops' roundings, K stored straight into the F16
+    cache; bit-identical to the op chain, and no separate norm launch."""
+    n_head, n_head_kv, n_past = 32, 4, 9
+    n_ctx = n_past + n_new + 3
+    r = rng(90 + hd + n_new)
+    q = r.standard_normal((n_new, n_head, hd)).astype(np.float32) * 2
+    k = r.standard_normal((n_new, n_head_kv, hd)).astype(np.float32) * 2
+    qw = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
+    kw = (1 + 0.1 * r.standard_normal(hd)).astype(np.float32)
+    pos = np.arange(n_past, n_past + n_new, dtype=np.int32) + 4000
+    cache0 = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+
+    def run(backend, fusion):
+        with Graph() as g:
+            kc = g.tensor(gl.F16, hd, n_head_kv, n_ctx, data=cache0)
+            pt = g.tensor(gl.I32, n_new, data=pos)
+            qs = g.mul(g.rms_norm(g.tensor(gl.F32, hd, n_head, n_new, data=q), 1e-6), g.tensor(gl.F32, hd, data=qw))
+            ks = g.mul(g.rms_norm(g.tensor(gl.F32, hd, n_head_kv, n_new, data=k), 1e-6), g.tensor(gl.F32, hd, data=kw))
+            qr = g.rope_ext(qs, pt, None, n_dims, mode, 4096, 1e6, 1.0, 0.0, 1.0, 0.0, 0.0)
+            kr = g.rope_ext(ks, pt, None, n_dims, mode, 4096, 1e6, 1.0, 0.0, 1.0, 0.0, 0.0)
+            nb1, nb2 = hd * 2, hd * n_head_kv * 2
+            ck = g.cpy(kr, g.view_3d(kc, hd, n_head_kv, n_new, nb1, nb2, n_past * nb2))
+            gl.libs()["hip"].ggml_backend_hip_set_fusion(hip, fusion)
+            try:
+                if backend is hip:
+                    qo, names = profiled(hip, lambda: g.compute(backend, [qr, ck])[0])
+                else:
+                    qo, names = g.compute(backend, [qr, ck])[0], set()
+            finally:
+                gl.libs()["hip"].ggml_backend_hip_set_fusion(hip, True)
+            return qo, g.read(kc, np.float16), names
+
+    ref = run(cpu, True)
+    for fusion in (True, False):
+        got = run(hip, fusion)
+        assert np.array_equal(got[0], ref[0]), (fusion, rel_err(got[0], ref[0]))
+        assert np.array_equal(got[1].view(np.uint16), ref[1].view(np.uint16)), fusion
+        if fusion:
+            assert "rope" in got[2] and "rms_norm_mul" not in got[2], got[2]
+    kcache = ref[1].reshape(n_ctx, n_head_kv, hd)
+    assert np.array_equal(kcache[:n_past].view(np.uint16), cache0[:n_past].view(np.uint16))
+
+
 @pytest.mark.parametrize("mode,hd,n_head,n_head_kv,qk_norm", [
     (gl.ROPE_NORMAL, 128, 24, 8, False), (gl.ROPE_NEOX, 96, 8, 8, False), (gl.ROPE_NEOX, 64, 8, 2, False),
     (gl.ROPE_NEOX, 128, 32, 8, True),    # Qwen3: QK-Norm before the rotations
