@@ -1244,9 +1244,43 @@ private:
             const ggml_tensor * nw = m->src[1];
             wrote_.push_back(m);
             wrote_.push_back(n);
+            // the norm's other readers all K-quant GEMVs (the MoE experts): its Q8_K form too, so
+            // that they quantize nothing
+            // (directly or through a contiguous reshape that keeps the row length: build_moe_ffn's
+            // [n_embd, 1, n_tokens] view)
+            q8k_act q8k{};
+            if (fuse(FUSE_ACTQ) && m->ne[0] % 256 == 0 && is_2d_contig(m)) {
+                bool kq = false, other = false;
+                std::vector<const ggml_tensor *> readers = { m };
+                auto kq_reader = [&](const ggml_tensor * un, const ggml_tensor * src) {
+                    return (un->op == GGML_OP_MUL_MAT || un->op == GGML_OP_MUL_MAT_ID) && un->src[1] == src &&
+                           un->src[0] != src && dot_kind(un->src[0]->type) == 2;
+                };
+                for (int j : users_[rn->second.mul]) {
+                    const ggml_tensor * un = g_->nodes[j];
+                    if (j == i) continue;
+                    if (kq_reader(un, m)) {
+                        kq = true;
+                    } else if (un->op == GGML_OP_RESHAPE && un->src[0] == m && un->data == m->data && ggml_is_contiguous(un) &&
+                               un->ne[0] == m->ne[0] && !users_[j].empty()) {
+                        for (int k : users_[j]) {
+                            if (kq_reader(g_->nodes[k], un)) kq = true;
+                            else other = true;
+                        }
+                        readers.push_back(un);
+                    } else {
+                        other = true;
+                    }
+                }
+                if (kq && !other) {
+                    act_entry e = alloc_act(2, m->ne[0], m->ne[1]);
+                    q8k = e.q8k;
+                    for (const ggml_tensor * r : readers) act_[r] = e;
+                }
+            }
             prof_scope ps(this, "router_norm", (double) (ggml_nbytes(n->src[0]) + 2 * ggml_nbytes(x) + ggml_nbytes(n)));
             launch_mul_mat_rows_norm(tv(n->src[0]), (const float *) x->data, (int64_t) (x->nb[1] / 4), (const float *) nw->data,
-                                     rn->second.eps, (float *) m->data, (int64_t) (m->nb[1] / 4), tv(n), x->ne[1], st_);
+                                     rn->second.eps, (float *) m->data, (int64_t) (m->nb[1] / 4), tv(n), x->ne[1], q8k, st_);
             return;
         }
         wrote_.push_back(n);

@@ -976,8 +976,9 @@ __global__ __launch_bounds__(256) void mul_mat_rows_kernel(tview s0, tview s1, t
 // products summed in double). One wave per router row, 4 rows per workgroup, grid.y = columns.
 __global__ __launch_bounds__(256) void mul_mat_rows_norm_kernel(tview w, const float * __restrict__ x, int64_t x_stride,
                                                                 const float * __restrict__ nw, float eps,
-                                                                float * __restrict__ y_out, int64_t y_stride, tview d) {
-    prefetch_kernargs<2 * sizeof(tview) + 48>();
+                                                                float * __restrict__ y_out, int64_t y_stride, tview d,
+                                                                q8k_act q8k) {
+    prefetch_kernargs<2 * sizeof(tview) + 48 + sizeof(q8k_act)>();
     extern __shared__ __align__(16) float s_y[];      // [K]
     __shared__ double s_part[4];
     const int64_t K = w.ne[0], col = blockIdx.y;
@@ -1049,6 +1050,15 @@ __global__ __launch_bounds__(256) void mul_mat_rows_norm_kernel(tview w, const f
         }
     }
     __syncthreads();
+    // the normalized column's Q8_K form for the norm's quantized consumers (q8k set): workgroup x
+    // quantizes super-blocks x, x + gridDim.x, ... (every workgroup holds the whole column)
+    if (q8k.qs) {
+        const int64_t nsb = K / 256;
+        for (int64_t sb = blockIdx.x; sb < nsb; sb += gridDim.x) {
+            q8k_superblock(s_y[sb * 256 + t], t, q8k.qs + col * K + sb * 256, q8k.d + col * nsb + sb,
+                           q8k.bsums + col * (K / 16) + sb * 16);
+        }
+    }
     if (o >= w.ne[1]) return;
     double acc = 0.0;
     for (int c0 = 0; c0 < nch; c0 += MR_BATCH * WAVE) {
@@ -1088,12 +1098,13 @@ bool mul_mat_rows_norm_supported(const tview & w, int64_t K) {
 }
 
 void launch_mul_mat_rows_norm(const tview & w, const float * x, int64_t x_stride, const float * nw, float eps, float * y_out,
-                              int64_t y_stride, const tview & dst, int64_t ncols, hipStream_t st) {
-    if (!mul_mat_rows_norm_supported(w, w.ne[0]) || dst.ne[0] != w.ne[1] || dst.ne[1] != ncols || dst.nb[0] != 4) {
+                              int64_t y_stride, const tview & dst, int64_t ncols, q8k_act q8k, hipStream_t st) {
+    if (!mul_mat_rows_norm_supported(w, w.ne[0]) || dst.ne[0] != w.ne[1] || dst.ne[1] != ncols || dst.nb[0] != 4 ||
+        (q8k.qs && w.ne[0] % 256)) {
         HIP_ABORT("mul_mat_rows_norm: unsupported operands");
     }
     launch(mul_mat_rows_norm_kernel, dim3((unsigned) ((w.ne[1] + 3) / 4), (unsigned) ncols), dim3(256),
-           (size_t) w.ne[0] * sizeof(float), st, w, x, x_stride, nw, eps, y_out, y_stride, dst);
+           (size_t) w.ne[0] * sizeof(float), st, w, x, x_stride, nw, eps, y_out, y_stride, dst, q8k);
 }
 
 void launch_mul_mat_generic(const tview & src0, const tview & src1, const tview & dst, hipStream_t st) {

@@ -328,10 +328,11 @@ void launch_argmax_row(const tview & a, int32_t * out, float * part_v, int * par
 void launch_mul_mat_generic(const tview & src0, const tview & src1, const tview & dst, hipStream_t st);
 // dst[:, c] = W^T (rms_norm(x[:, c]) * nw) for an F32 W [K, rows] (the MoE router), also writing
 // the normalized columns to y_out (the rms_norm -> mul output, for the norm's other consumers)
+// and, with q8k.qs set (K % 256 == 0), their Q8_K quantization
 constexpr int64_t MUL_MAT_ROWS_NORM_MAX_K = 8192;
 bool mul_mat_rows_norm_supported(const tview & w, int64_t K);
 void launch_mul_mat_rows_norm(const tview & w, const float * x, int64_t x_stride, const float * nw, float eps, float * y_out,
-                              int64_t y_stride, const tview & dst, int64_t ncols, hipStream_t st);
+                              int64_t y_stride, const tview & dst, int64_t ncols, q8k_act q8k, hipStream_t st);
 
 // MoE routing of one token per workgroup: softmax over the router logits (the soft_max op's
 // arithmetic), the k most probable experts in the stable descending order of argsort (ties: the
