@@ -363,7 +363,8 @@ enum fuse_bits {
     FUSE_ROPE   = 128, // RoPE stored straight into the KV cache; independent RoPE/copies in one launch
     FUSE_ROUTE  = 256, // MoE router softmax -> top-k -> renormalized weights in one launch
     FUSE_MC     = 512, // several activation columns per GEMV workgroup; mul_mat_id grouped by expert
-    FUSE_ALL    = 1023,
+    FUSE_ROUTEG = 1024, // one token's MoE routing inside its routed gate/up GEMV launch
+    FUSE_ALL    = 2047,
 };
 
 struct hip_backend_ctx {
@@ -435,6 +436,7 @@ public:
         attn_.clear();
         norm_.clear();
         act_.clear();
+        pending_route_.clear();
         // plan the attention fusions first: the V^T copy precedes K^T Q in node order and must
         // not run when the chain is replaced
         if (fuse(FUSE_ATTN)) {
@@ -463,6 +465,7 @@ public:
             done_[i] = true;
             if (c_.cb) report();
         }
+        if (!pending_route_.empty()) HIP_ABORT("a held-back MoE routing was never run");
     }
 
 private:
@@ -478,6 +481,8 @@ private:
     std::unordered_map<int, int> silu_of_;    // mul node -> its held-back silu node (op_swiglu)
     struct router_norm { int norm, mul; float eps; };
     std::unordered_map<int, router_norm> router_norm_;   // router mul_mat node -> the norm it computes
+    // one-token routings held back by op_moe_route, keyed by the ids view the mul_mat_ids read
+    std::unordered_map<const ggml_tensor *, moe_route> pending_route_;
     std::vector<const ggml_tensor *> wrote_;
 
     bool fuse(int bit) const { return c_.fusion && (c_.fuse_mask & bit); }
@@ -1442,7 +1447,6 @@ private:
         // profiled steps only: the ids back on the host, to count the distinct experts a
         // mul_mat_id reads (a synchronization, never inside a timed region)
         int64_t n_unique_experts = -1;
-        if (by_id && c_.timing) n_unique_experts = distinct_ids(ids, n->src[0]->ne[2]);
         auto fill_mat = [&](gemv_mat & gm, int j, double & bytes, bool epilogue) {
             ggml_tensor * mm = g_->nodes[j];
             const ggml_tensor * w = mm->src[0];
@@ -1506,6 +1510,29 @@ private:
             L.n_experts = (int) n->src[0]->ne[2];
             L.expert_rows = n->src[0]->ne[1];
         }
+        // a one-token routing held back for this launch: run inside the SwiGLU launch when that is
+        // the single-column Q4_K kernel, else launched now, before anything reads its ids
+        bool route_in = false;
+        moe_route route{};
+        if (by_id) {
+            auto it = pending_route_.find(ids);
+            if (it != pending_route_.end()) {
+                route = it->second;
+                pending_route_.erase(it);
+                if (gate >= 0 && !mc && gemv_q4k_enabled()) {
+                    gemv_launch P = L;
+                    P.n_mats = 2;
+                    P.swiglu = true;
+                    P.route_logits = route.logits;
+                    P.route_w = route.w;
+                    P.route_scale = route.scale;
+                    route_in = route.n_expert == L.n_experts && route.k == L.n_slots && L.ids == route.ids &&
+                               gemv_q4k_supported(P);
+                }
+                if (!route_in) run_route(route);
+            }
+        }
+        if (by_id && c_.timing && !route_in) n_unique_experts = distinct_ids(ids, n->src[0]->ne[2]);
         const double x_bytes = (double) (K * ggml_nrows(x) * 4) + (xa ? 0.0 : (double) (K * 4));
         // one column per workgroup, or several (mul_mat_id: the tokens routed to each expert)
         const expert_groups * G = mc && by_id ? &expert_groups_of(ids, (int) n->src[0]->ne[2]) : nullptr;
@@ -1541,9 +1568,26 @@ private:
             } else if (dtype >= 0 && mn->ne[0] <= gemv_prologue_max_k(dtype, false) && ((uintptr_t) mn->data) % 16 == 0) {
                 norm_[mn] = gemv_norm{ (const float *) mn->data, (int64_t) (mn->nb[1] / sizeof(float)), nullptr, 0.0f, 0 };
             }
+            if (route_in) {
+                S.route_logits = route.logits;
+                S.route_w = route.w;
+                S.route_scale = route.scale;
+                sb += (double) (route.n_expert * 4 + route.k * 8);
+            }
             {
-                prof_scope ps(this, gemv_prof_name(wtype, true), sb);
-                run(S);
+                prof_scope ps(this, route_in ? "gemv_q4_K_swiglu_route" : gemv_prof_name(wtype, true), sb);
+                if (route_in) launch_gemv(S, st_);
+                else run(S);
+                if (route_in && c_.timing) {
+                    // the experts this launch read, known once it ran (a synchronization; profiled
+                    // steps only)
+                    n_unique_experts = distinct_ids(ids, n->src[0]->ne[2]);
+                    gemv_launch T = S;
+                    double tb = x_bytes + (double) (route.n_expert * 4 + route.k * 8);
+                    fill_mat(T.m[0], gate, tb, false);
+                    fill_mat(T.m[1], up, tb, false);
+                    ps.bytes = tb - (double) (g_->nodes[gate]->ne[0] * ncols * 4);
+                }
             }
             wrote_.push_back(mn);
             done_[gate] = done_[up] = done_[mulnode] = true;
@@ -1672,14 +1716,38 @@ private:
         R.ids_nb1 = (int64_t) (an->nb[1] / sizeof(int32_t));
         R.w = (float *) dn->data;
         R.w_nb1 = (int64_t) (dn->nb[1] / sizeof(float));
-        {
-            prof_scope ps(this, "moe_route", (double) (E * T * 4 + k * T * 8));
-            launch_moe_route(R, st_);
-        }
         for (int d : { i, as, vs, rs, gs, w2, sr, dv }) done_[d] = true;
+        if (T == 1 && route_deferrable(vs, gs, dv)) {
+            // held back for the first mul_mat_id reading the ids (op_gemv), which either routes
+            // inside its SwiGLU launch or runs launch_moe_route first
+            pending_route_[vn] = R;
+            return true;
+        }
+        run_route(R);
         wrote_.push_back(an);
         wrote_.push_back(dn);
         return true;
+    }
+
+    void run_route(const moe_route & R) {
+        prof_scope ps(this, "moe_route", (double) (R.n_expert * R.n_tok * 4 + R.k * R.n_tok * 8));
+        launch_moe_route(R, st_);
+    }
+
+    // A one-token routing (ids view vs, weights dv) may wait for the mul_mat_id that reads it first
+    // when only mul_mat_ids read the ids (besides the routing's own get_rows gs) and nothing reads
+    // the weights before that node.
+    bool route_deferrable(int vs, int gs, int dv) const {
+        if (!fuse(FUSE_ROUTEG) || c_.cb || is_output(vs) || is_output(dv)) return false;
+        int first = INT_MAX;
+        for (int u : users_[vs]) {
+            if (u == gs) continue;
+            const ggml_tensor * un = g_->nodes[u];
+            if (un->op != GGML_OP_MUL_MAT_ID || un->src[2] != g_->nodes[vs] || un->src[0] == g_->nodes[vs] ||
+                un->src[1] == g_->nodes[vs]) return false;
+            first = std::min(first, u);
+        }
+        return first != INT_MAX && first_reader(dv) > first;
     }
 
     // mul(experts [n_embd, k, T], w [1, k, T]) -> views of the k slots -> add chain in slot order

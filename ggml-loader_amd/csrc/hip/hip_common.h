@@ -183,6 +183,72 @@ __device__ __forceinline__ void sincos_cr(float x, float & s, float & c) {
     c = (float) cd;
 }
 
+// MoE routing of one token over at most 256 experts by a workgroup of exactly 256 threads, thread
+// t holding the scaled logit w of expert t (-INFINITY for t >= E). The soft_max op's arithmetic:
+// the maximum, e = exp(w - max), the sum of the e in double, p = e * (float) (1 / sum); then the
+// stable descending order of argsort (ties: the lower expert first) as a rank count over 64-bit
+// keys (the bits of p, then 255 - i): finite logits give p in [0, 1], whose bit patterns order as
+// the floats do, so rank(i) = the count of keys above expert i's is the count of p[j] > p[i], or
+// p[j] == p[i] with j < i. The keys are distinct, so the ranks are too. For E <= 128 two threads
+// count an expert's rank over half of the keys each. Leaves p[i] in s_p[i] and the expert of rank
+// r < k in s_ids[r] for every thread; every thread must call it. s_key: 256 entries, 16-byte aligned.
+__device__ __forceinline__ void moe_route_256(float w, int E, int k, float * s_p, int * s_ids, int * s_cnt,
+                                              uint64_t * s_key, float * s_red, double * s_sum) {
+    const int t = threadIdx.x;
+    float mx = wave_max(fmaxf(-INFINITY, w));
+    if ((t % 64) == 0) s_red[t / 64] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    const float v = t < E ? exp_cr(w - mx) : 0.0f;
+    double sum = t < E ? (double) v : 0.0;
+    sum = wave_sum_d(sum);
+    if ((t % 64) == 0) s_sum[t / 64] = sum;
+    __syncthreads();
+    const float inv = (float) (1.0 / (s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3]));
+    const float p = v * inv;
+    if (t < E) s_p[t] = p;
+    // padding keys (t >= E) are 0: never above another key
+    s_key[t] = t < E ? ((uint64_t) __float_as_uint(p) << 32) | (uint32_t) (255 - t) : 0;
+    __syncthreads();
+    int rank = 0;
+    if (E <= 128) {
+        const int i = t % 128;
+        const uint64_t ki = s_key[i];
+        const ulonglong2 * kk = (const ulonglong2 *) (s_key + (t / 128) * 64);
+#pragma unroll 8
+        for (int q = 0; q < 32; q++) {
+            const ulonglong2 u = kk[q];
+            rank += (u.x > ki ? 1 : 0) + (u.y > ki ? 1 : 0);
+        }
+        s_cnt[t] = rank;
+        __syncthreads();
+        if (t < E) rank = s_cnt[t] + s_cnt[t + 128];
+    } else {
+        const uint64_t ki = s_key[t];
+        const ulonglong2 * kk = (const ulonglong2 *) s_key;
+#pragma unroll 8
+        for (int q = 0; q < 128; q++) {
+            const ulonglong2 u = kk[q];
+            rank += (u.x > ki ? 1 : 0) + (u.y > ki ? 1 : 0);
+        }
+    }
+    if (t < E && rank < k) s_ids[rank] = t;
+    __syncthreads();
+}
+
+// The routing's outputs from moe_route_256's LDS, by one thread: the k expert ids and their
+// probabilities divided by their sum (added in rank order in double, rounded to float once:
+// the sum_rows and div ops).
+__device__ __forceinline__ void moe_route_store(const float * s_p, const int * s_ids, int k, int32_t * ids, float * w) {
+    double s = 0.0;
+    for (int r = 0; r < k; r++) s += (double) s_p[s_ids[r]];
+    const float sf = (float) s;
+    for (int r = 0; r < k; r++) {
+        ids[r] = s_ids[r];
+        w[r] = s_p[s_ids[r]] / sf;
+    }
+}
+
 // round half to even, valid for |v| < 2^22 (the result ggml's nearest_int gives)
 __device__ __forceinline__ int round_half_even(float v) { return __float2int_rn(v); }
 

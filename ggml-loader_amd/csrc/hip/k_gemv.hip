@@ -931,6 +931,11 @@ void launch_gemv(const gemv_launch & L, hipStream_t st) {
         if (L.K > max_k) HIP_ABORT("gemv: the activation prologue handles K <= %d (K=%d)", max_k, L.K);
         if (((uintptr_t) L.norm.x | (uintptr_t) L.norm.w) % 16 || L.norm.x_stride % 4) HIP_ABORT("gemv: RMSNorm prologue operands must be 16-byte aligned");
     }
+    if (L.route_logits) {
+        // only the single-column Q4_K kernel routes inside the launch
+        if (!gemv_q4k_supported(L)) HIP_ABORT("gemv: routing inside the launch unsupported for this launch");
+        return launch_gemv_q4k(L, st);
+    }
     if (gemv_q_supported(L)) return launch_gemv_q(L, st);
     if (gemv_q4k_enabled() && gemv_q4k_supported(L)) return launch_gemv_q4k(L, st);
     if (L.out_q.qs) HIP_ABORT("gemv: quantized SwiGLU output needs the Q4_0 / Q8_0 kernel");

@@ -116,7 +116,7 @@ __device__ __forceinline__ void q8k_quant_wave(float v0, float v1, float v2, flo
     if (lane == 0) s.xd[sb] = amax != 0.0f ? 1 / iscale : 0.0f;
 }
 
-template <int LPR, int ITS, bool SWIGLU, int PRO, int CPT, int MAXT>
+template <int LPR, int ITS, bool SWIGLU, int PRO, int CPT, int MAXT, bool ROUTE = false>
 __global__ __launch_bounds__(MAXT) void gemv_q4k_kernel(const gemv_kargs a) {
     prefetch_kernargs<sizeof(gemv_kargs)>();
     extern __shared__ __align__(16) uint8_t smem[];
@@ -142,7 +142,23 @@ __global__ __launch_bounds__(MAXT) void gemv_q4k_kernel(const gemv_kargs a) {
     // mul_mat_id: the expert of this column and its activation column
     int xcol = col;
     int64_t erow = 0;
-    if (L.ids) {
+    if constexpr (ROUTE) {
+        // one token, column = slot: the routing runs here, in every workgroup, before any load
+        // that needs the expert (256 threads, at most 256 experts)
+        __shared__ float r_p[256];
+        __shared__ int r_ids[MOE_ROUTE_MAX_K];
+        __shared__ int r_cnt[256];
+        __shared__ __align__(16) uint64_t r_key[256];   // read as 16-byte pairs
+        __shared__ float r_red[4];
+        __shared__ double r_sum[4];
+        const int E = L.n_experts;
+        const float lg = L.route_logits[min(t, E - 1)];
+        moe_route_256(t < E ? lg * L.route_scale : -INFINITY, E, L.n_slots, r_p, r_ids, r_cnt, r_key, r_red, r_sum);
+        // the ids and weights the down projection and the weighted slot sum read (later launches)
+        if (blockIdx.x == 0 && col == 0 && t == 0) moe_route_store(r_p, r_ids, L.n_slots, (int32_t *) L.ids, L.route_w);
+        xcol = col % L.x_cols;
+        erow = (int64_t) r_ids[col] * L.expert_rows;
+    } else if (L.ids) {
         const int tk = col / L.n_slots, sl = col % L.n_slots;
         xcol = tk * L.x_cols + sl % L.x_cols;
         const int e = min(max(L.ids[(int64_t) tk * L.ids_stride + sl], 0), L.n_experts - 1);
@@ -377,6 +393,14 @@ void q4k_launch_t(const gemv_kargs & ka, int waves, size_t lds, hipStream_t st) 
 
 template <int LPR, int ITS, bool SWIGLU>
 void q4k_launch_its(const gemv_kargs & ka, int pro, int waves, int cpt, size_t lds, hipStream_t st) {
+    if constexpr (SWIGLU) {
+        if (ka.L.route_logits) {
+            const dim3 grid((ka.total_rows + ka.rows_per_block - 1) / ka.rows_per_block, ka.L.ncols);
+            if (waves != 4 || (pro != 0 && (pro != 2 || cpt > 2))) HIP_ABORT("gemv q4_K: routing inside the launch needs 256 threads and an unnormalized column");
+            if (pro == 0) return launch((gemv_q4k_kernel<LPR, ITS, true, 0, 1, 256, true>), grid, dim3(256), lds, st, ka);
+            return launch((gemv_q4k_kernel<LPR, ITS, true, 2, 2, 256, true>), grid, dim3(256), lds, st, ka);
+        }
+    }
     if (pro == 0) return q4k_launch_t<LPR, ITS, SWIGLU, 0, 1>(ka, waves, lds, st);
     if (pro == 1) {
         if (cpt <= 2) return q4k_launch_t<LPR, ITS, SWIGLU, 1, 2>(ka, waves, lds, st);
@@ -442,6 +466,12 @@ bool gemv_q4k_supported(const gemv_launch & L) {
     const int pro = !L.norm.x ? 0 : L.norm.rms ? 1 : 2;
     if (!q4k_prologue_of(pro, L.K, sh)) return false;
     if (pro == 0 && L.K / 32 > 2 * sh.waves * WAVE) return false;
+    // the routing inside the launch: one token's slots, 256 threads, at most 256 experts, the
+    // column pre-quantized or quantized as is
+    if (L.route_logits && !(L.swiglu && L.ids && (pro == 0 || (pro == 2 && sh.cpt <= 2)) && sh.waves == 4 &&
+                            L.ncols == L.n_slots && L.x_cols >= 1 &&
+                            L.n_experts >= 1 && L.n_experts <= 256 && L.n_slots >= 1 && L.n_slots <= MOE_ROUTE_MAX_K &&
+                            L.n_slots <= L.n_experts && L.route_w)) return false;
     const int rows_pb = sh.waves * (WAVE / sh.lpr);
     return q4k_lds_bytes(sh.lpr, rows_pb, L.swiglu ? 2 : 1, L.K) <= 64 * 1024;
 }

@@ -745,54 +745,53 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const moe_route R) {
     prefetch_kernargs<sizeof(moe_route)>();
     __shared__ float s_p[MOE_ROUTE_MAX_EXPERTS];
     __shared__ int s_ids[MOE_ROUTE_MAX_K];
+    __shared__ int s_cnt[256];
+    __shared__ __align__(16) uint64_t s_key[256];   // read as 16-byte pairs
     __shared__ float s_red[4];
     __shared__ double s_sum[4];
     const int t = threadIdx.x, tok = blockIdx.x, E = R.n_expert;
     const float * lg = R.logits + (int64_t) tok * R.logits_nb1;
-    if (t < R.k) s_ids[t] = 0;   // (every slot is written below unless a probability is NaN)
-    // softmax, as soft_max_kernel
-    float mx = -INFINITY;
-    for (int i = t; i < E; i += 256) {
-        const float w = lg[i] * R.scale;
-        s_p[i] = w;
-        mx = fmaxf(mx, w);
-    }
-    mx = wave_max(mx);
-    if ((t % 64) == 0) s_red[t / 64] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    double sum = 0.0;
-    for (int i = t; i < E; i += 256) {
-        const float v = exp_cr(s_p[i] - mx);
-        s_p[i] = v;
-        sum += (double) v;
-    }
-    sum = wave_sum_d(sum);
-    if ((t % 64) == 0) s_sum[t / 64] = sum;
-    __syncthreads();
-    const float inv = (float) (1.0 / (s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3]));
-    for (int i = t; i < E; i += 256) s_p[i] *= inv;
-    __syncthreads();
-    // position of each expert in the stable descending order; the first k positions are the top-k
-    for (int i = t; i < E; i += 256) {
-        const float v = s_p[i];
-        int rank = 0;
-        for (int j = 0; j < E; j++) {
-            const float u = s_p[j];
-            rank += (u > v || (u == v && j < i)) ? 1 : 0;
+    if (E <= 256) {
+        // the routing the expert GEMV of a one-token step runs in its own workgroups
+        moe_route_256(t < E ? lg[t] * R.scale : -INFINITY, E, R.k, s_p, s_ids, s_cnt, s_key, s_red, s_sum);
+    } else {
+        if (t < R.k) s_ids[t] = 0;   // (every slot is written below unless a probability is NaN)
+        // softmax, as soft_max_kernel
+        float mx = -INFINITY;
+        for (int i = t; i < E; i += 256) {
+            const float w = lg[i] * R.scale;
+            s_p[i] = w;
+            mx = fmaxf(mx, w);
         }
-        if (rank < R.k) s_ids[rank] = i;
-    }
-    __syncthreads();
-    if (t == 0) {
-        double s = 0.0;
-        for (int r = 0; r < R.k; r++) s += (double) s_p[s_ids[r]];
-        const float sf = (float) s;
-        for (int r = 0; r < R.k; r++) {
-            R.ids[(int64_t) tok * R.ids_nb1 + r] = s_ids[r];
-            R.w[(int64_t) tok * R.w_nb1 + r] = s_p[s_ids[r]] / sf;
+        mx = wave_max(mx);
+        if ((t % 64) == 0) s_red[t / 64] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+        double sum = 0.0;
+        for (int i = t; i < E; i += 256) {
+            const float v = exp_cr(s_p[i] - mx);
+            s_p[i] = v;
+            sum += (double) v;
         }
+        sum = wave_sum_d(sum);
+        if ((t % 64) == 0) s_sum[t / 64] = sum;
+        __syncthreads();
+        const float inv = (float) (1.0 / (s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3]));
+        for (int i = t; i < E; i += 256) s_p[i] *= inv;
+        __syncthreads();
+        // position of each expert in the stable descending order; the first k positions are the top-k
+        for (int i = t; i < E; i += 256) {
+            const float v = s_p[i];
+            int rank = 0;
+            for (int j = 0; j < E; j++) {
+                const float u = s_p[j];
+                rank += (u > v || (u == v && j < i)) ? 1 : 0;
+            }
+            if (rank < R.k) s_ids[rank] = i;
+        }
+        __syncthreads();
     }
+    if (t == 0) moe_route_store(s_p, s_ids, R.k, R.ids + (int64_t) tok * R.ids_nb1, R.w + (int64_t) tok * R.w_nb1);
 }
 
 void launch_moe_route(const moe_route & R, hipStream_t st) {

@@ -185,8 +185,16 @@ struct gemv_launch {
     int        x_cols;
     int        n_experts;
     int64_t    expert_rows;
+    // mul_mat_id of one token whose routing has not run (route_logits set; single-column Q4_K
+    // SwiGLU kernel only): every workgroup routes the token itself from the router logits
+    // (n_experts of them, times route_scale; moe_route_256) and reads the expert of its slot, and
+    // the launch writes the n_slots expert ids to ids and their renormalized weights to route_w,
+    // which later launches read
+    const float * route_logits;
+    float *    route_w;
     // SwiGLU epilogue: m[0] = gate, m[1] = up (same n_rows); writes act = silu(g) * u to m[0].y
     bool       swiglu;
+    float      route_scale;
     // with swiglu (Q4_0 / Q8_0 weights, n_rows % 32 == 0, K <= GEMV_SWIGLU_QOUT_MAX_K): act also
     // quantized to Q8_0 here (quantize_row_q8_0 semantics; column c's blocks at +c * n_rows), for a
     // down projection that reads it pre-quantized

@@ -998,7 +998,10 @@ def test_moe_ffn(hip, cpu, qtype, n_tok):
         a, b = both(hip, cpu, build, fusion)
         assert np.array_equal(a, b), (fusion, rel_err(a, b))
     _, names = profiled(hip, lambda: run_on(hip, build))
-    assert "moe_route" in names and "argsort" not in names, names
+    assert "argsort" not in names, names
+    # one token on the single-column Q4_K kernel: the routing runs inside the gate/up launch
+    in_gemv = qtype == gl.Q4_K and n_tok == 1
+    assert ("moe_route" in names) != in_gemv and ("gemv_q4_K_swiglu_route" in names) == in_gemv, names
     if qtype in (gl.Q5_K, gl.Q6_K):
         # no multi-column kernel for these types: each (token, slot) column reads its expert
         assert "moe_group" not in names, names
@@ -1089,6 +1092,46 @@ def test_moe_route_fused(hip, cpu, E, k, n_tok):
     assert np.array_equal(wa, wb)
     order = np.argsort(-lg, axis=1, kind="stable")[:, :k]
     assert np.array_equal(ia.reshape(n_tok, k).astype(np.int64), order)
+
+
+@pytest.mark.parametrize("E,k,fold_norm", [(128, 8, True), (128, 8, False), (256, 8, False), (60, 4, True), (8, 8, False)])
+def test_moe_route_inside_gate_up_gemv(hip, cpu, E, k, fold_norm):
+    """One token's routing run by the workgroups of the routed gate/up + SwiGLU launch (no
+    launch of its own), with exact ties straddling the top-k boundary (duplicated router rows: the
+    lower expert id wins) and the column pre-quantized by the router launch (fold_norm) or
+    quantized in the prologue: the whole FFN bit-exact against the op-by-op oracle. The tied
+    experts' weights differ, so a tie decided the other way shows in the output."""
+    n_embd, ff = 1024, 256
+    r = rng(90 + E + k)
+    x = (r.standard_normal((1, n_embd)) * 2).astype(np.float32)
+    res = r.standard_normal((1, n_embd)).astype(np.float32)
+    nw = (1 + 0.01 * r.standard_normal(n_embd)).astype(np.float32)
+    router = (r.standard_normal((E, n_embd)) * 0.002).astype(np.float32)   # logits well below the planted ones
+    # router rows along x (logits about a_e, or a_e / rms(x) after the norm): the top k - 1
+    # distinct, then three equal rows at random ids, the lowest of which takes the last slot
+    u = x[0] / float(np.dot(x[0], x[0]))
+    top = r.permutation(E)[: k + 2]
+    for j, e in enumerate(top[: k - 1]):
+        router[e] = (4.0 - 0.3 * j) * u
+    for e in top[k - 1:]:
+        router[e] = 1.5 * u
+    wg, wu = (qweight(gl.Q4_K, n_embd, E * ff, s, std=0.05) for s in (91, 92))
+    wd = qweight(gl.Q4_K, ff, E * n_embd, 93, std=0.05)
+
+    def build(g):
+        xt = g.tensor(gl.F32, n_embd, 1, data=x)
+        y = g.mul(g.rms_norm(xt, 1e-6), g.tensor(gl.F32, n_embd, data=nw)) if fold_norm else xt
+        return moe_ffn_graph(g, y, g.tensor(gl.F32, n_embd, E, data=router),
+                             g.tensor(gl.Q4_K, n_embd, ff, E, data=wg), g.tensor(gl.Q4_K, n_embd, ff, E, data=wu),
+                             g.tensor(gl.Q4_K, ff, n_embd, E, data=wd), k, g.tensor(gl.F32, n_embd, 1, data=res))
+
+    for fusion in (True, False):
+        a, b = both(hip, cpu, build, fusion)
+        assert np.array_equal(a, b), (fusion, rel_err(a, b))
+    _, names = profiled(hip, lambda: run_on(hip, build))
+    assert "gemv_q4_K_swiglu_route" in names and "moe_route" not in names, names
+    if fold_norm:
+        assert "router_norm" in names, names
 
 
 def test_other_arch_ops(hip, cpu):
