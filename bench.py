@@ -605,17 +605,20 @@ def decode_bench(gl, args):
                   f"{PROFILE_EVERY}th of {args.steps} steps run again right after the timed region "
                   f"({1000 * secs_ev / args.steps:.3f} ms/step with the events)",
     }
-    if "attn_decode" in prof:
-        # the layer's decode attention (scores, [statistics,] PV, combination launches together), from
-        # the breakdown steps; algorithmic bytes: the K and V rows read, Q in, the output out, the mask
-        n_a, ms_a, by_a = prof["attn_decode"]
+    att = [prof[k] for k in ("attn_decode", "attn_decode_acc") if k in prof]
+    if att:
+        # the layer's decode attention (scores, [statistics,] PV[, combination] launches together),
+        # from the breakdown steps; algorithmic bytes: the K and V rows read, Q in, the output out, the
+        # mask. attn_decode_acc: one query whose PV launch accumulates the output for the O projection
+        n_a, ms_a, by_a = (sum(e[i] for e in att) for i in range(3))
         a_ach = by_a / (ms_a * 1e-3) / 1e9 if ms_a > 0 else 0.0
         aj = os.path.join(ROOT, "profiles", f"attn_{wname}_{args.config}_decode_traffic.json")
         roofline["attention"] = {
             "bound": "hbm", "achieved": round(a_ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(a_ach / PEAK_HBM_GBS, 4),
             "traffic": json.load(open(aj))["traffic_bytes_per_layer"] if batch == 1 and os.path.exists(aj) else None,
-            "kernel": "decode attention of one layer (attn_scores, attn_pv, attn_combine; attn_stats too past 2304 positions)",
+            "kernel": "decode attention of one layer (attn_scores, attn_pv; attn_stats too past 2304 positions; attn_combine "
+                      "unless the PV launch accumulates the one-query output for the O projection's prologue)",
             "us_per_layer": round(ms_a / n_a * 1e3, 2), "bytes_per_layer": round(by_a / n_a),
             "timing": f"HIP events around each layer's attention launches in {args.breakdown_steps} untimed steps",
         }

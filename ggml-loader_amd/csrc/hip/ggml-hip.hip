@@ -364,7 +364,8 @@ enum fuse_bits {
     FUSE_ROUTE  = 256, // MoE router softmax -> top-k -> renormalized weights in one launch
     FUSE_MC     = 512, // several activation columns per GEMV workgroup; mul_mat_id grouped by expert
     FUSE_ROUTEG = 1024, // one token's MoE routing inside its routed gate/up GEMV launch
-    FUSE_ALL    = 2047,
+    FUSE_ACCO   = 2048, // one-query attention output accumulated by PV, read as doubles by its GEMVs
+    FUSE_ALL    = 4095,
 };
 
 struct hip_backend_ctx {
@@ -1899,6 +1900,25 @@ private:
         }
     }
 
+    // A one-query attention output read only by GEMVs that take it as doubles: the PV launch adds
+    // its chunk partials into an accumulator and those GEMVs' prologue rounds and quantizes it, so
+    // the output is never materialized and the combination launch does not run.
+    bool acc_output_ok(int ct) const {
+        const ggml_tensor * ctn = g_->nodes[ct];
+        if (!fuse(FUSE_ACCO) || !fuse(FUSE_NORMQ) || c_.cb || is_output(ct) || users_[ct].empty() || ctn->ne[1] != 1 ||
+            ggml_nrows(ctn) != 1) return false;
+        for (int u : users_[ct]) {
+            const ggml_tensor * n = g_->nodes[u];
+            if (n->op != GGML_OP_MUL_MAT || n->src[1] != ctn || n->src[0] == ctn || attn_.count(u) || !gemv_capable(n)) return false;
+            gemv_launch P{};
+            P.type = n->src[0]->type;
+            P.K = (int) n->src[0]->ne[0];
+            P.ncols = 1;
+            if (!gemv_f64_input_supported(P)) return false;
+        }
+        return true;
+    }
+
     void run_attention(const attn_match & M) {
         const ggml_tensor * kp = M.kp, * qp = M.qp, * vp = M.vp, * mask = M.mask;
         ggml_tensor * ctn = g_->nodes[M.ct];
@@ -1961,12 +1981,15 @@ private:
         } else {
             A.scratch_bytes = attn_scratch_bytes(n_kv, n_q, n_head, hd);
             A.scratch = (float *) c_.scratch.alloc((size_t) A.scratch_bytes);
-            if (wanted_act_kind(M.ct) == 1) {
+            if (n_q == 1 && acc_output_ok(M.ct)) {
+                A.acc = (double *) c_.scratch.alloc((size_t) n_head * hd * sizeof(double));
+                norm_[ctn] = gemv_norm{ (const float *) A.acc, (int64_t) n_head * hd, nullptr, 0.0f, 0, 1 };
+            } else if (wanted_act_kind(M.ct) == 1) {
                 act_entry e = alloc_act(1, ctn->ne[0], n_q);
                 A.out_q = e.q8;
                 act_[ctn] = e;
             }
-            prof_scope ps(this, "attn_decode", bytes);
+            prof_scope ps(this, A.acc ? "attn_decode_acc" : "attn_decode", bytes);
             launch_attn_decode(A, st_);
         }
         done_[M.kq] = done_[M.sm] = done_[M.vt] = done_[M.kqv] = done_[M.pm] = done_[M.ct] = true;

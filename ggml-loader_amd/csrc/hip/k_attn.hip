@@ -385,6 +385,13 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
         const float m = fmaxf(fmaxf(s_cm[0][t], s_cm[1][t]), fmaxf(s_cm[2][t], s_cm[3][t]));
         S.cmax[((int64_t) (q0 + q) * A.n_head + h) * attn_chunks(A.n_kv) + split] = m;
     }
+    // the accumulator the PV launch adds its chunk partials into, zeroed by the launch before it
+    if (A.acc) {
+        const int nwg = gridDim.x * gridDim.y * gridDim.z;
+        const int wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+        const int n = A.n_q * A.n_head * HD;
+        for (int i = wg * ATT_THREADS + t; i < n; i += nwg * ATT_THREADS) A.acc[i] = 0.0;
+    }
 }
 
 // one workgroup per (head, query, segment of STATS_SEG positions): the row maximum M from the chunk
@@ -705,7 +712,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
         const double v = ((s_part[(0 * PV_MAX_ROWS + r) * HD + d] + s_part[(1 * PV_MAX_ROWS + r) * HD + d]) +
                           s_part[(2 * PV_MAX_ROWS + r) * HD + d]) + s_part[(3 * PV_MAX_ROWS + r) * HD + d];
         const int q = q0 + r / G, h = h0 + r % G;
-        S.parts[(((int64_t) split * A.n_q + q) * A.n_head + h) * HD + d] = v;
+        if (A.acc) unsafeAtomicAdd(A.acc + ((int64_t) q * A.n_head + h) * HD + d, v);
+        else S.parts[(((int64_t) split * A.n_q + q) * A.n_head + h) * HD + d] = v;
     }
 }
 
@@ -1046,7 +1054,7 @@ static void launch_attn_t(const attn_launch & A, hipStream_t st) {
         launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
         launch((attn_pv_kernel<HD, G, 0>), pv_grid, dim3(ATT_THREADS), 0, st, A, pvq);
     }
-    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(CMB_PARTS * HD), 0, st, A, pv_splits);
+    if (!A.acc) launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(CMB_PARTS * HD), 0, st, A, pv_splits);
 }
 
 template <int HD>
@@ -1127,6 +1135,7 @@ void launch_attn_decode(const attn_launch & A_in, hipStream_t st) {
     if (A.n_head % A.n_head_kv) HIP_ABORT("attn: n_head %% n_head_kv");
     if (A.scratch_bytes < attn_scratch_bytes(A.n_kv, A.n_q, A.n_head, A.hd)) HIP_ABORT("attn: scratch too small");
     if (A.out_q.qs && (A.hd % 32)) HIP_ABORT("attn: quantized output needs hd %% 32 == 0");
+    if (A.acc && (A.n_q != 1 || A.out_q.qs || ((uintptr_t) A.acc) % 16)) HIP_ABORT("attn: the accumulated output takes one query, no quantized copy, 16-byte alignment");
     if (A.n_q > ATT_MAX_Q) {
         // many queries: scores and PV on the matrix cores
         switch (A.hd) {

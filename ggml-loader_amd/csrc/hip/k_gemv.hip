@@ -326,7 +326,28 @@ constexpr int PRO_REGS = 32;
 // addresses need no load of the launch's workgroup size ahead of the weight loads
 constexpr int GEMV_NT = 256;
 
-template <int TYPE, bool PRO>
+// 16 doubles at p (16-byte aligned) into r as raw bits (double e: r[2e] its low word, r[2e + 1]
+// its high word), converted only when they are quantized
+__device__ __forceinline__ void load_chunk_f64(float (&r)[PRO_REGS], const double * p) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const double2 d = ((const double2 *) p)[k];
+        r[4 * k] = __int_as_float(__double2loint(d.x));
+        r[4 * k + 1] = __int_as_float(__double2hiint(d.x));
+        r[4 * k + 2] = __int_as_float(__double2loint(d.y));
+        r[4 * k + 3] = __int_as_float(__double2hiint(d.y));
+    }
+}
+
+__device__ __forceinline__ void chunk_from_f64(float (&v)[16], const float (&r)[PRO_REGS]) {
+#pragma unroll
+    for (int e = 0; e < 16; e++) v[e] = (float) __hiloint2double(__float_as_int(r[2 * e + 1]), __float_as_int(r[2 * e]));
+}
+
+// F64: the column holds doubles (gemv_norm::f64; Q8_K layout only), each rounded to float and
+// quantized as is: chunk t's 16 doubles are loaded into xv and chunk t + GEMV_NT's into wv (raw),
+// later chunks when they are quantized.
+template <int TYPE, bool PRO, bool F64 = false>
 __device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, float (&xv)[PRO_REGS], float (&wv)[PRO_REGS]) {
     // Every load here is unconditional (indices clamped; a thread past the end loads the last
     // chunk again and never uses it), so none of them sits in a branch that the compiler would
@@ -364,6 +385,12 @@ __device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, fl
             for (int k = 0; k < 2; k++) wv[1 + k] = __int_as_float(bs[min(t + k * GEMV_NT, K / 32 - 1)]);
         }
         return;
+    } else if constexpr (F64) {
+        static_assert(TYPE == GGML_TYPE_Q4_K, "double-valued columns are quantized to Q8_K");
+        const int nchunk = L.K / C;
+        const double * xcol = (const double *) L.norm.x + (int64_t) col * L.norm.x_stride;
+        load_chunk_f64(xv, xcol + (int64_t) min(t, nchunk - 1) * C);
+        load_chunk_f64(wv, xcol + (int64_t) min(t + GEMV_NT, nchunk - 1) * C);
     } else {
         const int nchunk = L.K / C;
         const float * xcol = L.norm.x + (int64_t) col * L.norm.x_stride;
@@ -382,13 +409,37 @@ __device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, fl
     }
 }
 
-template <int TYPE>
+template <int TYPE, bool F64 = false>
 __device__ __forceinline__ void prologue_finish(const gemv_launch & L, int col, float (&xv)[PRO_REGS], const float (&wv)[PRO_REGS],
                                                 const gemv_lds & s, double * s_red) {
     constexpr int C = TYPE == GGML_TYPE_Q4_K ? 16 : 32;
     const int K = L.K;
     const int nchunk = K / C;
     const int t = threadIdx.x;
+    if constexpr (F64) {
+        float v[16];
+        chunk_from_f64(v, xv);
+        quant_chunk<TYPE, 16>(v, t, t < nchunk, s);
+        chunk_from_f64(v, wv);
+        quant_chunk<TYPE, 16>(v, GEMV_NT + t, GEMV_NT + t < nchunk, s);
+        const double * xcol = (const double *) L.norm.x + (int64_t) col * L.norm.x_stride;
+        for (int c0 = 2 * GEMV_NT; c0 < nchunk; c0 += GEMV_NT) {
+            const int c = c0 + t;
+            const bool has = c < nchunk;
+#pragma unroll
+            for (int e = 0; e < 16; e++) v[e] = 0.0f;
+            if (has) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const double2 d = ((const double2 *) (xcol + (int64_t) c * 16))[k];
+                    v[2 * k] = (float) d.x;
+                    v[2 * k + 1] = (float) d.y;
+                }
+            }
+            quant_chunk<TYPE, 16>(v, c, has, s);
+        }
+        return;
+    }
     float (&x0)[C] = *reinterpret_cast<float (*)[C]>(&xv[0]);
     if (!L.norm.rms) {
         quant_chunk<TYPE, C>(x0, t, t < nchunk, s);
@@ -433,12 +484,12 @@ __device__ __forceinline__ void prologue_finish(const gemv_launch & L, int col, 
 }
 
 // the quantized activation column in LDS: finished by the prologue, or copied
-template <int TYPE, bool PRO>
+template <int TYPE, bool PRO, bool F64 = false>
 __device__ __forceinline__ void stage_x(const gemv_launch & L, int col, const gemv_lds & s, double * s_red,
                                         float (&xv)[PRO_REGS], const float (&wv)[PRO_REGS]) {
     const int K = L.K;
     if constexpr (PRO) {
-        prologue_finish<TYPE>(L, col, xv, wv, s, s_red);
+        prologue_finish<TYPE, F64>(L, col, xv, wv, s, s_red);
     } else if constexpr (TYPE == GGML_TYPE_Q4_K) {
         // from the registers prologue_load filled; a row longer than they cover (K > 64 * GEMV_NT)
         // copies the rest here
@@ -521,7 +572,7 @@ void launch_act_quant(const gemv_launch & L, const q8_act & q8, const q8k_act & 
     }
 }
 
-template <int TYPE, int LPR, bool SWIGLU, int ITS, bool PRO>
+template <int TYPE, int LPR, bool SWIGLU, int ITS, bool PRO, bool F64 = false>
 __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
     prefetch_kernargs<sizeof(gemv_kargs)>();
     extern __shared__ __align__(16) uint8_t smem[];
@@ -614,7 +665,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
         // quant bytes; Q5_K those and the block's 32 qh bytes; Q6_K (planes) the half's 64 ql and 32
         // qh bytes, plus its four scales and the block's d.
         float xv[PRO_REGS], wv[PRO_REGS];
-        prologue_load<AT, PRO>(L, xcol, xv, wv);
+        prologue_load<AT, PRO, F64>(L, xcol, xv, wv);
+        // (the double-valued column's loads are many: kept ahead of the weights' so that waiting
+        // for them does not wait for any weight load)
+        if constexpr (F64) asm volatile("" ::: "memory");
         const int units = K / 64, nsb = K / 256;
         constexpr int NW = TYPE == GGML_TYPE_Q4_K ? 3 : TYPE == GGML_TYPE_Q5_K ? 5 : 6;
         constexpr int BB = TYPE == GGML_TYPE_Q4_K ? Q4_K_BYTES : Q5_K_BYTES;
@@ -649,7 +703,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(const gemv_kargs a) {
                 }
             }
         }
-        stage_x<AT, PRO>(L, xcol, s, s_red, xv, wv);
+        // a double-valued column stays raw until every weight load is out (converted earlier, its
+        // registers would be reused, and the reuse waits for the loads)
+        if constexpr (F64) __builtin_amdgcn_sched_barrier(0);
+        stage_x<AT, PRO, F64>(L, xcol, s, s_red, xv, wv);
         // the staged activation's sub-blocks grouped by l
         group_by_l_lds(s.xq, K / 32);
         __syncthreads();
@@ -806,6 +863,12 @@ static void launch_gemv_its(gemv_kargs & ka, int waves, hipStream_t st) {
         HIP_ABORT("gemv: %d chains per workgroup exceed one wave", ka.rows_per_block * (SWIGLU ? 2 : 1));
     }
     if (lds > 160 * 1024) HIP_ABORT("gemv: K=%d needs %zu bytes of LDS", ka.L.K, lds);
+    if (ka.L.norm.x && ka.L.norm.f64) {
+        if constexpr (is_kquant(TYPE) && !SWIGLU) {
+            return launch((gemv_kernel<TYPE, LPR, SWIGLU, ITS, true, true>), dim3(grid_x, ka.L.ncols), dim3(waves * WAVE), lds, st, ka);
+        }
+        HIP_ABORT("gemv: a double-valued column needs K-quant weights without SwiGLU");
+    }
     if (ka.L.norm.x) launch((gemv_kernel<TYPE, LPR, SWIGLU, ITS, true>), dim3(grid_x, ka.L.ncols), dim3(waves * WAVE), lds, st, ka);
     else launch((gemv_kernel<TYPE, LPR, SWIGLU, ITS, false>), dim3(grid_x, ka.L.ncols), dim3(waves * WAVE), lds, st, ka);
 }
@@ -914,6 +977,12 @@ static void launch_gemv_kq_lanes(gemv_kargs & ka, hipStream_t st) {
     else launch_gemv_t<TYPE, 64, SWIGLU>(ka, WAVES, st);
 }
 
+bool gemv_f64_input_supported(const gemv_launch & L) {
+    if (L.swiglu || L.ids || L.ncols != 1 || L.out_q.qs) return false;
+    if (L.type == GGML_TYPE_Q4_0 || L.type == GGML_TYPE_Q8_0) return gemv_q_supported(L) && L.K <= gemv_prologue_max_k(L.type, false);
+    return is_kquant(L.type) && L.K % 256 == 0 && L.K <= act_quant_max_k(L.type, false);
+}
+
 void launch_gemv(const gemv_launch & L, hipStream_t st) {
     gemv_kargs ka;
     ka.L = L;
@@ -926,6 +995,8 @@ void launch_gemv(const gemv_launch & L, hipStream_t st) {
     ka.total_rows = L.swiglu ? L.m[0].n_rows : r;
     if (L.swiglu && (L.n_mats != 2 || L.m[0].n_rows != L.m[1].n_rows)) HIP_ABORT("gemv: swiglu needs two equal matrices");
     if (L.ids && (L.n_slots < 1 || L.x_cols < 1 || L.n_experts < 1 || L.ncols % L.n_slots)) HIP_ABORT("gemv: bad mul_mat_id geometry");
+    if (L.norm.f64 && (!L.norm.x || L.norm.rms || L.swiglu || L.ids || L.norm.x_stride % 2 || !gemv_f64_input_supported(L)))
+        HIP_ABORT("gemv: a double-valued column is quantized as is, for a plain Q4_0 / Q8_0 / K-quant launch");
     if (L.norm.x) {
         const int max_k = act_quant_max_k(L.type, L.norm.rms != 0);
         if (L.K > max_k) HIP_ABORT("gemv: the activation prologue handles K <= %d (K=%d)", max_k, L.K);

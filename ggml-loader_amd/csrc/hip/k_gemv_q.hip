@@ -19,6 +19,8 @@
 //          squares is reduced in double (DPP within rows, then across rows and waves in order), and
 //          a Q8_0 block is the chunks of 8 consecutive lanes (block max and quant sum by DPP).
 //   PRO 2  x quantized as is (the quantization ggml-cpu applies inside mul_mat), same layout.
+//   PRO 3  as PRO 2 from doubles (gemv_norm::f64: the decode attention's accumulated output), each
+//          rounded to float first; the raw doubles are loaded before the weights and converted after.
 // The prologue's loads go out before the weight loads (loads complete in issue order), so the
 // prologue runs while the weights stream; the quantized column is staged in LDS.
 //
@@ -120,7 +122,17 @@ __global__ __launch_bounds__(MAXT) void gemv_q_kernel(const gemv_kargs a) {
 
     // ---- prologue loads (before the weights): CPT float4 chunks of x (and of the norm weight) ----
     float4 xv[CPT], wv[CPT];
-    if constexpr (PRO != 0) {
+    double2 xlo[PRO == 3 ? CPT : 1], xhi[PRO == 3 ? CPT : 1];
+    if constexpr (PRO == 3) {
+        const double2 * x2 = (const double2 *) ((const double *) L.norm.x + (int64_t) xcol * L.norm.x_stride);
+#pragma unroll
+        for (int k = 0; k < CPT; k++) {
+            const int c = min(t + k * nt, nc - 1);
+            xlo[k] = x2[2 * c];
+            xhi[k] = x2[2 * c + 1];
+        }
+        asm volatile("" ::: "memory");   // these loads stay ahead of the weights'
+    } else if constexpr (PRO != 0) {
         const float4 * x4 = (const float4 *) (L.norm.x + (int64_t) xcol * L.norm.x_stride);
         const float4 * w4 = (const float4 *) (PRO == 1 && L.norm.w ? L.norm.w : L.norm.x);
 #pragma unroll
@@ -165,6 +177,9 @@ __global__ __launch_bounds__(MAXT) void gemv_q_kernel(const gemv_kargs a) {
         }
     }
 
+    // the raw doubles are converted only after every weight load is out (converted earlier, the
+    // wait for them would hold back the weight loads still to issue)
+    if constexpr (PRO == 3) __builtin_amdgcn_sched_barrier(0);
     // ---- the activation blocks this lane dots ----
     int4 xa[ITS], xb[ITS];
     float xd[ITS];
@@ -193,6 +208,7 @@ __global__ __launch_bounds__(MAXT) void gemv_q_kernel(const gemv_kargs a) {
 #pragma unroll
         for (int k = 0; k < CPT; k++) {
             const int c = t + k * nt;                 // chunk c: elements 4c .. 4c + 3 of block c / 8
+            if constexpr (PRO == 3) xv[k] = make_float4((float) xlo[k].x, (float) xlo[k].y, (float) xhi[k].x, (float) xhi[k].y);
             float v0 = xv[k].x, v1 = xv[k].y, v2 = xv[k].z, v3 = xv[k].w;
             if (PRO == 1) {
                 v0 = v0 * scale; v1 = v1 * scale; v2 = v2 * scale; v3 = v3 * scale;
@@ -344,10 +360,14 @@ void qg_launch_its(const gemv_kargs & ka, int pro, int waves, int cpt, size_t ld
     } else if (pro == 1) {
         if (cpt == 1) qg_launch_t<TYPE, LPR, ITS, SWIGLU, 1, 1>(ka, waves, lds, st);
         else qg_launch_t<TYPE, LPR, ITS, SWIGLU, 1, 2>(ka, waves, lds, st);
-    } else {
+    } else if (pro == 2 || SWIGLU) {
         if (cpt == 1) qg_launch_t<TYPE, LPR, ITS, SWIGLU, 2, 1>(ka, waves, lds, st);
         else if (cpt == 2) qg_launch_t<TYPE, LPR, ITS, SWIGLU, 2, 2>(ka, waves, lds, st);
         else qg_launch_t<TYPE, LPR, ITS, SWIGLU, 2, 4>(ka, waves, lds, st);
+    } else if constexpr (!SWIGLU) {
+        if (cpt == 1) qg_launch_t<TYPE, LPR, ITS, false, 3, 1>(ka, waves, lds, st);
+        else if (cpt == 2) qg_launch_t<TYPE, LPR, ITS, false, 3, 2>(ka, waves, lds, st);
+        else qg_launch_t<TYPE, LPR, ITS, false, 3, 4>(ka, waves, lds, st);
     }
 }
 
@@ -379,7 +399,8 @@ void launch_gemv_q(const gemv_launch & L, hipStream_t st) {
     gemv_kargs ka;
     ka.L = L;
     const int nb = L.K / 32, nc = L.K / 4;
-    const int pro = !L.norm.x ? 0 : L.norm.rms ? 1 : 2;
+    const int pro = !L.norm.x ? 0 : L.norm.f64 ? 3 : L.norm.rms ? 1 : 2;
+    if (pro == 3 && (L.swiglu || L.norm.rms || L.norm.x_stride % 2)) HIP_ABORT("gemv: a double-valued column is quantized as is, without SwiGLU");
     const bool epq = L.swiglu && L.out_q.qs;
     if (epq && L.m[0].n_rows % 32) HIP_ABORT("gemv: quantized SwiGLU output needs rows %% 32 == 0");
     qg_shape sh{};

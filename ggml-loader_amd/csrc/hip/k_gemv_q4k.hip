@@ -454,7 +454,7 @@ bool gemv_q4k_enabled() {
 }
 
 bool gemv_q4k_supported(const gemv_launch & L) {
-    if (L.type != GGML_TYPE_Q4_K || L.K % 256 || L.out_q.qs) return false;
+    if (L.type != GGML_TYPE_Q4_K || L.K % 256 || L.out_q.qs || L.norm.f64) return false;
     // taken where it measured faster than the multi-unit kernel of k_gemv.hip (C3: gate/up + SwiGLU
     // 15.9 against 17.6 us; C5: QKV 7.7 against 8.8, expert down 6.3 against 8.5): SwiGLU pairs of
     // a plain GEMV and rows of at most 2048 elements. Longer single rows (C3's QKV, O, down and the

@@ -143,6 +143,9 @@ struct gemv_norm {
     const float * w;       // norm weight [K] (rms only; nullptr: rms_norm without the multiply)
     float         eps;
     int           rms;
+    // x holds doubles (x_stride counted in doubles), each rounded to float and then quantized as
+    // is (rms 0): the decode attention's accumulated output (attn_launch::acc)
+    int           f64;
 };
 
 // largest K the act_quant kernel (and the Q4_K GEMV's prologue) handles: with rms, one 32-element
@@ -202,6 +205,9 @@ struct gemv_launch {
 };
 
 void launch_gemv(const gemv_launch & L, hipStream_t st);
+// whether launch_gemv takes a double-valued column (gemv_norm::f64) for this launch: one column,
+// no SwiGLU, no experts; Q4_0 / Q8_0 on the single-column kernel, K-quants on the multi-unit one
+bool gemv_f64_input_supported(const gemv_launch & L);
 // the single-column Q4_0 / Q8_0 kernel (k_gemv_q.hip), which launch_gemv uses when this holds
 bool gemv_q_supported(const gemv_launch & L);
 void launch_gemv_q(const gemv_launch & L, hipStream_t st);
@@ -390,6 +396,11 @@ struct attn_launch {
     int64_t        scratch_bytes;
     // quantized copy of out for the o-projection (Q8_0 semantics), optional
     q8_act         out_q;
+    // one query (n_q == 1): instead of per-chunk partials and a combination launch, the PV
+    // workgroups add their chunk partials into acc[head * hd + i] (doubles; exact sums, so their
+    // order does not matter; zeroed by the scores launch), and out / out_q are not written: the
+    // o-projection's prologue reads acc (gemv_norm::f64). nullptr: the partials and combination.
+    double *       acc;
     // RoPE of the new tokens folded in (rope set; decode only): Q is read from rq.src and rotated
     // in the scores kernel (the rotated Q is not stored); the workgroup whose position chunk holds
     // new position n_kv - n_q + t rotates K row t of rk.src into rk.dst (the K cache) and copies V

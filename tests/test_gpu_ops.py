@@ -767,6 +767,40 @@ def test_attention_decode(hip, cpu, hd, n_head, n_head_kv, n_kv, n_new, flash):
         assert rel_err(a, expect) < 1e-6
 
 
+@pytest.mark.parametrize("qtype,hd,n_head,n_head_kv,n_kv", [
+    (gl.Q4_0, 128, 24, 8, 2049),   # Llama-3B shape: PV forms its rows' statistics, two launches
+    (gl.Q8_0, 96, 32, 32, 130),    # Phi-3 head dim
+    (gl.Q4_K, 128, 32, 8, 8193),   # Qwen3 shape: the statistics launch
+    (gl.Q4_K, 128, 32, 4, 4097),   # MoE config attention
+    (gl.Q6_K, 128, 16, 8, 300),
+    (gl.Q5_K, 64, 8, 8, 1),        # first token: the output is V's row
+])
+def test_attention_output_accumulated_into_o_projection(hip, cpu, qtype, hd, n_head, n_head_kv, n_kv):
+    """One query's attention read only by its O projection: the PV workgroups add their chunk
+    partials into one double accumulator (FP64 atomics: the sums are exact, so their order does not
+    change them), no combination launch runs and the output is never written; the projection's
+    prologue rounds the doubles to float and quantizes them as the combination's output would have
+    been. Bit-exact against the oracle, fused or not."""
+    r = rng(n_kv + n_head + hd)
+    n_ctx = n_kv + 3
+    kc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+    vc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+    q = r.standard_normal((1, n_head, hd)).astype(np.float32)
+    mask = np.zeros((1, n_kv), dtype=np.float32)
+    K, rows = n_head * hd, 640
+    wo = qweight(qtype, K, rows, 95, std=0.05)
+
+    def build(g):
+        att = attention_graph(g, hd, n_head, n_head_kv, n_kv, 1, n_ctx, kc, vc, q, mask)
+        return g.mul_mat(g.tensor(qtype, K, rows, data=wo), att)
+
+    for fusion in (True, False):
+        a, b = both(hip, cpu, build, fusion)
+        assert np.array_equal(a, b), (fusion, rel_err(a, b))
+    _, names = profiled(hip, lambda: run_on(hip, build))
+    assert "attn_decode_acc" in names and "attn_decode" not in names, names
+
+
 @pytest.mark.parametrize("n_new,n_kv", [
     (2, 70),       # the decode kernels
     (20, 70),      # the prefill kernel
