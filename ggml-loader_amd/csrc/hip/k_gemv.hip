@@ -345,8 +345,8 @@ __device__ __forceinline__ void chunk_from_f64(float (&v)[16], const float (&r)[
 }
 
 // F64: the column holds doubles (gemv_norm::f64; Q8_K layout only), each rounded to float and
-// quantized as is: chunk t's 16 doubles are loaded into xv and chunk t + GEMV_NT's into wv (raw),
-// later chunks when they are quantized.
+// quantized as is: chunk t's 16 doubles are loaded into xv and, for rows of more than GEMV_NT
+// chunks, chunk t + GEMV_NT's into wv (raw); later chunks when they are quantized.
 template <int TYPE, bool PRO, bool F64 = false>
 __device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, float (&xv)[PRO_REGS], float (&wv)[PRO_REGS]) {
     // Every load here is unconditional (indices clamped; a thread past the end loads the last
@@ -390,7 +390,8 @@ __device__ __forceinline__ void prologue_load(const gemv_launch & L, int col, fl
         const int nchunk = L.K / C;
         const double * xcol = (const double *) L.norm.x + (int64_t) col * L.norm.x_stride;
         load_chunk_f64(xv, xcol + (int64_t) min(t, nchunk - 1) * C);
-        load_chunk_f64(wv, xcol + (int64_t) min(t + GEMV_NT, nchunk - 1) * C);
+        // (uniform: rows of at most GEMV_NT chunks have no second one)
+        if (nchunk > GEMV_NT) load_chunk_f64(wv, xcol + (int64_t) min(t + GEMV_NT, nchunk - 1) * C);
     } else {
         const int nchunk = L.K / C;
         const float * xcol = L.norm.x + (int64_t) col * L.norm.x_stride;
@@ -420,8 +421,10 @@ __device__ __forceinline__ void prologue_finish(const gemv_launch & L, int col, 
         float v[16];
         chunk_from_f64(v, xv);
         quant_chunk<TYPE, 16>(v, t, t < nchunk, s);
-        chunk_from_f64(v, wv);
-        quant_chunk<TYPE, 16>(v, GEMV_NT + t, GEMV_NT + t < nchunk, s);
+        if (nchunk > GEMV_NT) {
+            chunk_from_f64(v, wv);
+            quant_chunk<TYPE, 16>(v, GEMV_NT + t, GEMV_NT + t < nchunk, s);
+        }
         const double * xcol = (const double *) L.norm.x + (int64_t) col * L.norm.x_stride;
         for (int c0 = 2 * GEMV_NT; c0 < nchunk; c0 += GEMV_NT) {
             const int c = c0 + t;

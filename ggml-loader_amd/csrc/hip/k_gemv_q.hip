@@ -127,7 +127,7 @@ __global__ __launch_bounds__(MAXT) void gemv_q_kernel(const gemv_kargs a) {
         const double2 * x2 = (const double2 *) ((const double *) L.norm.x + (int64_t) xcol * L.norm.x_stride);
 #pragma unroll
         for (int k = 0; k < CPT; k++) {
-            const int c = min(t + k * nt, nc - 1);
+            const int c = wrap_index(t + k * nt, nc, t);
             xlo[k] = x2[2 * c];
             xhi[k] = x2[2 * c + 1];
         }
@@ -137,7 +137,7 @@ __global__ __launch_bounds__(MAXT) void gemv_q_kernel(const gemv_kargs a) {
         const float4 * w4 = (const float4 *) (PRO == 1 && L.norm.w ? L.norm.w : L.norm.x);
 #pragma unroll
         for (int k = 0; k < CPT; k++) {
-            const int c = min(t + k * nt, nc - 1);
+            const int c = wrap_index(t + k * nt, nc, t);
             xv[k] = x4[c];
             if (PRO == 1) wv[k] = w4[c];
         }
