@@ -73,6 +73,12 @@ __host__ __device__ inline attn_scratch scratch_of(const attn_launch & A) {
     return s;
 }
 
+// Row r of a chunk of nt rows at position t0 for a load whose value past the chunk's end is not
+// used: r itself, else the same row of the previous chunk (in bounds, and a distinct address per
+// lane) or, in the first chunk, its last row. Clamping every lane past the end to row nt - 1 would
+// make them all load one row: the last chunk of a row of 2^k + 1 positions holds one.
+__device__ __forceinline__ int tail_row(int r, int nt, int t0, int chunk) { return r < nt ? r : t0 >= chunk ? r - chunk : nt - 1; }
+
 int64_t attn_scratch_bytes(int n_kv, int n_q, int n_head, int hd) {
     const int64_t nrow = (int64_t) n_q * n_head;
     const int64_t nf = nrow * n_kv + nrow * attn_chunks(n_kv);
@@ -211,7 +217,7 @@ __global__ __launch_bounds__(ATT_THREADS, 4) void attn_scores_kernel(const attn_
         for (int it = 0; it < KITER; it++) {
             const unsigned pc = t + it * ATT_THREADS;
             const unsigned r = pc / PIECES, c = pc % PIECES;
-            kv[it] = *(const uint4 *) (kbase + (min(r, (unsigned) nt - 1) * A.k_s2 + c * 8));
+            kv[it] = *(const uint4 *) (kbase + (tail_row((int) r, nt, t0, ATT_CHUNK) * A.k_s2 + (int) c * 8));
         }
     }
     __builtin_amdgcn_sched_barrier(0);   // every load above is out before any wait
@@ -407,10 +413,14 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(const attn_laun
     const int64_t row = (int64_t) q * A.n_head + h;
     float * sc = S.scores + row * A.n_kv;
     const int nch = attn_chunks(A.n_kv);
-    // the segment's scores go out first (clamped indices, unused past the end)
+    // the segment's scores go out first (unused past the end, where a lane loads the element one
+    // segment back, or its own first one in the first segment: in bounds, distinct addresses)
     float v[STATS_PER_THREAD];
 #pragma unroll
-    for (int k = 0; k < STATS_PER_THREAD; k++) v[k] = sc[min(seg * STATS_SEG + k * ATT_THREADS + t, A.n_kv - 1)];
+    for (int k = 0; k < STATS_PER_THREAD; k++) {
+        const int i = seg * STATS_SEG + k * ATT_THREADS + t;
+        v[k] = sc[i < A.n_kv ? i : seg > 0 ? i - STATS_SEG : min(t, A.n_kv - 1)];
+    }
     float m = -INFINITY;
     for (int c = t; c < nch; c += ATT_THREADS) m = fmaxf(m, S.cmax[row * nch + c]);
     m = wave_max(m);
@@ -539,8 +549,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     float sc[PV_SC];
 #pragma unroll
     for (int k = 0; k < PV_SC; k++) {
-        const int i = min(t + k * ATT_THREADS, n_rows * PV_CHUNK - 1);
-        const int pr = i / PV_CHUNK, tt = min(i % PV_CHUNK, nt - 1);
+        const int i = wrap_index(t + k * ATT_THREADS, n_rows * PV_CHUNK, t);
+        const int pr = i / PV_CHUNK, tt = tail_row(i % PV_CHUNK, nt, t0, PV_CHUNK);
         sc[k] = S.scores[row_of(pr) * A.n_kv + t0 + tt];
     }
     float rmax = 0.0f;
@@ -556,7 +566,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
 #pragma unroll
         for (int r = 0; r < G; r++) {
 #pragma unroll
-            for (int k = 0; k < FK; k++) fv[r][k] = S.scores[row_of(r) * A.n_kv + min(t + k * ATT_THREADS, A.n_kv - 1)];
+            for (int k = 0; k < FK; k++) fv[r][k] = S.scores[row_of(r) * A.n_kv + wrap_index(t + k * ATT_THREADS, A.n_kv, t)];
         }
     } else if (n_rows * nseg <= ATT_THREADS) {
         // one segment sum per thread, issued with the other loads (a loop of dependent loads here
@@ -571,7 +581,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(const attn_launch 
     for (int it = 0; it < ITER; it++) {
         const unsigned pc = t + it * ATT_THREADS;
         const unsigned r = pc / PIECES, c = pc % PIECES;
-        vv[it] = *(const uint4 *) (vbase + (min(r, (unsigned) nt - 1) * A.v_s2 + c * 8));
+        vv[it] = *(const uint4 *) (vbase + (tail_row((int) r, nt, t0, PV_CHUNK) * A.v_s2 + (int) c * 8));
     }
     // rows staged as zero: padding rows past the end (their loads read the last row; no term) and,
     // with skip_masked, rows masked for every query of the workgroup (their p is 0 for every row).
@@ -796,7 +806,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_mq_kernel(const attn_
         for (int it = 0; it < ITER; it++) {
             const int pc = threadIdx.x + it * ATT_THREADS;
             const int r = pc / PIECES, c = pc % PIECES;
-            kv[it] = *(const uint4 *) (kbase + ((t0 + min(r, nt - 1)) * kst + c * 8));
+            kv[it] = *(const uint4 *) (kbase + ((t0 + tail_row(r, nt, t0, ATT_CHUNK)) * kst + c * 8));
         }
     }
     __builtin_amdgcn_sched_barrier(0);            // every load above is out before any wait
@@ -908,7 +918,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_mq_kernel(const attn_laun
     {
         const float * esrc = S.scores + (row * A.n_kv + t0);
 #pragma unroll
-        for (int k = 0; k < EPT; k++) ev[k] = esrc[min(pp0 + k, nt - 1)];
+        for (int k = 0; k < EPT; k++) ev[k] = esrc[tail_row(pp0 + k, nt, t0, PV_CHUNK)];
     }
     const bool seg_lanes = nseg <= 16;
     const double seg_sum = S.ssum[row * nseg + min(t % 16, nseg - 1)];
@@ -920,7 +930,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_mq_kernel(const attn_laun
         for (int it = 0; it < ITER; it++) {
             const int pc = t + it * ATT_THREADS;
             const int r = pc / PIECES, c = pc % PIECES;
-            vv[it] = *(const uint4 *) (vbase + ((t0 + min(r, nt - 1)) * vst + c * 8));
+            vv[it] = *(const uint4 *) (vbase + ((t0 + tail_row(r, nt, t0, PV_CHUNK)) * vst + c * 8));
         }
     }
     // V rows staged as zero: padding rows past the end and, with skip_masked, rows masked for every
