@@ -735,7 +735,27 @@ private:
                 if (a.ne[1] == 1 && a.ne[0] >= ARGMAX_ROW_MIN) {
                     float * pv = (float *) c_.scratch.alloc(ARGMAX_PARTS * sizeof(float));
                     int * pi = (int *) c_.scratch.alloc(ARGMAX_PARTS * sizeof(int));
-                    launch_argmax_row(a, (int32_t *) n->data, pv, pi, st_);
+                    // copies of the one index into I32 cells (the decode loop's next token and its
+                    // history slot): written by the final launch instead of two copy launches
+                    int32_t * extra[2] = { nullptr, nullptr };
+                    int ne = 0;
+                    if (fuse(FUSE_ADD) && !c_.cb) {
+                        for (int u : users_[i]) {
+                            const ggml_tensor * c = g_->nodes[u];
+                            if (c->op != GGML_OP_CPY || c->src[0] != n || c->type != GGML_TYPE_I32 || ggml_nelements(c) != 1 ||
+                                ne == 2 || done_[u]) { ne = -1; break; }
+                            extra[ne++] = (int32_t *) c->data;
+                        }
+                        if (ne > 0) {
+                            for (int u : users_[i]) {
+                                done_[u] = true;
+                                wrote_.push_back(g_->nodes[u]);
+                            }
+                        } else {
+                            extra[0] = extra[1] = nullptr;
+                        }
+                    }
+                    launch_argmax_row(a, (int32_t *) n->data, pv, pi, st_, extra[0], extra[1]);
                 } else {
                     launch_argmax(a, (int32_t *) n->data, st_);
                 }

@@ -865,24 +865,31 @@ __global__ __launch_bounds__(256) void argmax_parts_kernel(tview a, int64_t chun
     if (threadIdx.x == 0) { pv[blockIdx.x] = bv; pi[blockIdx.x] = bi; }
 }
 
-__global__ __launch_bounds__(256) void argmax_final_kernel(const float * pv, const int * pi, int n_parts, int32_t * out) {
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float * pv, const int * pi, int n_parts, int32_t * out,
+                                                           int32_t * out2, int32_t * out3) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     if ((int) threadIdx.x < n_parts) { bv = pv[threadIdx.x]; bi = pi[threadIdx.x]; }
     argmax_block(bv, bi);
-    if (threadIdx.x == 0) out[0] = bi == 0x7fffffff ? 0 : bi;
+    if (threadIdx.x == 0) {
+        const int32_t r = bi == 0x7fffffff ? 0 : bi;
+        out[0] = r;
+        if (out2) out2[0] = r;
+        if (out3) out3[0] = r;
+    }
 }
 
 void launch_argmax(const tview & a, int32_t * out, hipStream_t st) {
     launch(argmax_kernel, dim3((unsigned) a.ne[1]), dim3(256), 0, st, a, out);
 }
 
-void launch_argmax_row(const tview & a, int32_t * out, float * part_v, int * part_i, hipStream_t st) {
+void launch_argmax_row(const tview & a, int32_t * out, float * part_v, int * part_i, hipStream_t st, int32_t * out2,
+                       int32_t * out3) {
     if (a.ne[1] != 1 || a.ne[2] != 1 || a.ne[3] != 1 || a.ne[0] <= 0 || a.ne[0] > INT32_MAX) HIP_ABORT("argmax_row: one row expected");
     const int64_t chunk = (a.ne[0] + ARGMAX_PARTS - 1) / ARGMAX_PARTS;
     const int parts = (int) ((a.ne[0] + chunk - 1) / chunk);
     launch(argmax_parts_kernel, dim3((unsigned) parts), dim3(256), 0, st, a, chunk, part_v, part_i);
-    launch(argmax_final_kernel, dim3(1), dim3(256), 0, st, (const float *) part_v, (const int *) part_i, parts, out);
+    launch(argmax_final_kernel, dim3(1), dim3(256), 0, st, (const float *) part_v, (const int *) part_i, parts, out, out2, out3);
 }
 
 // ---------------------------------------------------------------------------------------------

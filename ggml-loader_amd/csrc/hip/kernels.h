@@ -336,7 +336,9 @@ void launch_argmax(const tview & a, int32_t * out, hipStream_t st);
 // entries of device scratch); the same index as launch_argmax
 constexpr int ARGMAX_PARTS = 128;
 constexpr int64_t ARGMAX_ROW_MIN = 16384;   // narrower rows take the one-workgroup kernel
-void launch_argmax_row(const tview & a, int32_t * out, float * part_v, int * part_i, hipStream_t st);
+// out2 / out3 (optional): further destinations of the index (the decode loop's copies of the pick)
+void launch_argmax_row(const tview & a, int32_t * out, float * part_v, int * part_i, hipStream_t st,
+                       int32_t * out2 = nullptr, int32_t * out3 = nullptr);
 
 // generic F32/F16/BF16 mul_mat (src0 rows contiguous): one wave per output element
 void launch_mul_mat_generic(const tview & src0, const tview & src1, const tview & dst, hipStream_t st);
