@@ -21,7 +21,7 @@
 //            coalesced 16-byte loads (rows padded by one dword so lane t reading row t is
 //            conflict-free); one wave per (query, head of the GQA group), lane = position; each
 //            row's chunk maximum.
-//   stats    (query, head, 2048-position segment) workgroups: M = the maximum of the row's chunk
+//   stats    (query, head, 1024-position segment) workgroups: M = the maximum of the row's chunk
 //            maxima, e = exp(s - M) written over each score, the segment's sum of e in double.
 //   pv       (128-position chunk, KV head) workgroups: 1/S from the segment sums (added in segment
 //            order), p = F16(e * (1/S)) for the chunk, the chunk's V rows staged in LDS (every load
@@ -46,7 +46,7 @@ constexpr int ATT_THREADS = 256;
 constexpr int ATT_WAVES = ATT_THREADS / WAVE;
 
 constexpr int PV_CHUNK = 128;
-constexpr int STATS_PER_THREAD = 8;                          // scores per thread of a statistics workgroup
+constexpr int STATS_PER_THREAD = 4;                          // scores per thread of a statistics workgroup
 constexpr int STATS_SEG = ATT_THREADS * STATS_PER_THREAD;    // positions per statistics workgroup
 
 __host__ __device__ inline int attn_chunks(int n_kv) { return (n_kv + ATT_CHUNK - 1) / ATT_CHUNK; }
