@@ -29,37 +29,84 @@ static bool launch_mc_dispatch(const gemv_launch & L, const expert_groups * G, i
 // One workgroup: the columns (token, slot) of a mul_mat_id grouped by expert. Counts and cursors
 // live in LDS (shared-memory atomics); the order inside an expert's list is arbitrary, which does
 // not change any result (every column is computed on its own).
+// inclusive sum over the workgroup's 256 threads (wave shuffles, then the waves' totals in order)
+__device__ __forceinline__ int block_scan_256(int v, int * s_w) {
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const int u = __shfl_up(v, o, WAVE);
+        if (lane >= o) v += u;
+    }
+    if (lane == WAVE - 1) s_w[wave] = v;
+    __syncthreads();
+    for (int w = 0; w < wave; w++) v += s_w[w];
+    return v;
+}
+
+// The expert lists of a mul_mat_id's columns: count per expert, each expert's start in cols, the
+// work items (expert, start, up to nc columns) in expert order, and the columns by expert. Each
+// thread takes a contiguous run of experts; its run's first column and first item come from a
+// scan over the threads' run totals, so no thread walks all experts.
 __global__ __launch_bounds__(256) void moe_group_kernel(const int32_t * ids, int64_t ids_stride, int n_slots, int n_tok,
                                                         int n_experts, const expert_groups g) {
     extern __shared__ int s_cnt[];
     int * s_cur = s_cnt + n_experts;
+    __shared__ int s_w[256 / WAVE];
     const int t = threadIdx.x, ncol = n_slots * n_tok;
     for (int e = t; e < n_experts; e += 256) s_cnt[e] = 0;
     __syncthreads();
-    for (int c = t; c < ncol; c += 256) {
-        const int e = min(max(ids[(int64_t) (c / n_slots) * ids_stride + c % n_slots], 0), n_experts - 1);
-        atomicAdd(&s_cnt[e], 1);
-    }
-    __syncthreads();
-    if (t == 0) {
-        int o = 0, n = 0;
-        for (int e = 0; e < n_experts; e++) {
-            s_cur[e] = o;
-            g.offset[e] = o;
-            g.count[e] = s_cnt[e];
-            // the expert's columns in items of at most nc
-            for (int j = 0; j < s_cnt[e]; j += g.nc, n++) {
-                g.items[3 * n] = e;
-                g.items[3 * n + 1] = o + j;
-                g.items[3 * n + 2] = min(g.nc, s_cnt[e] - j);
-            }
-            o += s_cnt[e];
+    // the column's expert (read once, kept for the scatter below when one column per thread covers
+    // the launch's columns)
+    int ec[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int c = t + k * 256;
+        ec[k] = -1;
+        if (c < ncol) {
+            const int tk = c / n_slots;
+            ec[k] = min(max(ids[(int64_t) tk * ids_stride + (c - tk * n_slots)], 0), n_experts - 1);
+            atomicAdd(&s_cnt[ec[k]], 1);
         }
-        *g.n_items = n;
+    }
+    for (int c = t + 4 * 256; c < ncol; c += 256) {
+        const int tk = c / n_slots;
+        atomicAdd(&s_cnt[min(max(ids[(int64_t) tk * ids_stride + (c - tk * n_slots)], 0), n_experts - 1)], 1);
     }
     __syncthreads();
-    for (int c = t; c < ncol; c += 256) {
-        const int e = min(max(ids[(int64_t) (c / n_slots) * ids_stride + c % n_slots], 0), n_experts - 1);
+    // this thread's run of experts [e0, e1): its columns and items, then the scans
+    const int per = (n_experts + 255) / 256;
+    const int e0 = min(t * per, n_experts), e1 = min(e0 + per, n_experts);
+    int cols = 0, its = 0;
+    for (int e = e0; e < e1; e++) {
+        cols += s_cnt[e];
+        its += (s_cnt[e] + g.nc - 1) / g.nc;
+    }
+    const int cend = block_scan_256(cols, s_w);
+    __syncthreads();                                   // s_w reused by the second scan
+    const int iend = block_scan_256(its, s_w);
+    int o = cend - cols, n = iend - its;
+    for (int e = e0; e < e1; e++) {
+        const int cnt = s_cnt[e];
+        s_cur[e] = o;
+        g.offset[e] = o;
+        g.count[e] = cnt;
+        // the expert's columns in items of at most nc
+        for (int j = 0; j < cnt; j += g.nc, n++) {
+            g.items[3 * n] = e;
+            g.items[3 * n + 1] = o + j;
+            g.items[3 * n + 2] = min(g.nc, cnt - j);
+        }
+        o += cnt;
+    }
+    if (t == 255) *g.n_items = iend;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        if (ec[k] >= 0) g.cols[atomicAdd(&s_cur[ec[k]], 1)] = t + k * 256;
+    }
+    for (int c = t + 4 * 256; c < ncol; c += 256) {
+        const int tk = c / n_slots;
+        const int e = min(max(ids[(int64_t) tk * ids_stride + (c - tk * n_slots)], 0), n_experts - 1);
         g.cols[atomicAdd(&s_cur[e], 1)] = c;
     }
 }
