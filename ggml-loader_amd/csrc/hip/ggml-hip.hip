@@ -1912,10 +1912,9 @@ private:
             A.q = A0.q + (int64_t) q0 * A0.q_nb2;
             A.mask = A0.mask ? (const char *) A0.mask + (int64_t) q0 * A0.mask_nb1 : nullptr;
             A.out = A0.out + (int64_t) q0 * A0.out_nb1;
-            if (A0.out_q.qs) {
-                const int64_t K = (int64_t) A0.n_head * A0.hd;
-                A.out_q = q8_act{ A0.out_q.qs + q0 * K, A0.out_q.d + q0 * (K / 32), A0.out_q.s + q0 * (K / 32) };
-            }
+            const int64_t K = (int64_t) A0.n_head * A0.hd;
+            if (A0.out_q.qs) A.out_q = q8_act{ A0.out_q.qs + q0 * K, A0.out_q.d + q0 * (K / 32), A0.out_q.s + q0 * (K / 32) };
+            if (A0.out_q8k.qs) A.out_q8k = q8k_act{ A0.out_q8k.qs + q0 * K, A0.out_q8k.d + q0 * (K / 256), A0.out_q8k.bsums + q0 * (K / 16) };
             launch_attn_decode(A, st_);
         }
     }
@@ -1937,6 +1936,21 @@ private:
             if (!gemv_f64_input_supported(P)) return false;
         }
         return true;
+    }
+
+    // the attention output's quantized copy for its GEMV readers, written by the combination launch
+    // (Q8_0 blocks, or Q8_K super-blocks when the head dims tile them)
+    void attn_quant_out(attn_launch & A, int ct, ggml_tensor * ctn, int n_q) {
+        const int kind = wanted_act_kind(ct);
+        if (kind == 1) {
+            act_entry e = alloc_act(1, ctn->ne[0], n_q);
+            A.out_q = e.q8;
+            act_[ctn] = e;
+        } else if (kind == 2 && (A.n_head * A.hd) % 256 == 0 && 256 % A.hd == 0) {
+            act_entry e = alloc_act(2, ctn->ne[0], n_q);
+            A.out_q8k = e.q8k;
+            act_[ctn] = e;
+        }
     }
 
     void run_attention(const attn_match & M) {
@@ -1991,11 +2005,7 @@ private:
             prof_scope ps(this, "attn_prefill", bytes);
             launch_attn_prefill(A, st_);
         } else if (n_q > 4) {
-            if (wanted_act_kind(M.ct) == 1) {
-                act_entry e = alloc_act(1, ctn->ne[0], n_q);
-                A.out_q = e.q8;
-                act_[ctn] = e;
-            }
+            attn_quant_out(A, M.ct, ctn, n_q);
             prof_scope ps(this, "attn_decode", bytes * ((n_q + 3) / 4));
             attn_decode_grouped(A);
         } else {
@@ -2004,10 +2014,8 @@ private:
             if (n_q == 1 && acc_output_ok(M.ct)) {
                 A.acc = (double *) c_.scratch.alloc((size_t) n_head * hd * sizeof(double));
                 norm_[ctn] = gemv_norm{ (const float *) A.acc, (int64_t) n_head * hd, nullptr, 0.0f, 0, 1 };
-            } else if (wanted_act_kind(M.ct) == 1) {
-                act_entry e = alloc_act(1, ctn->ne[0], n_q);
-                A.out_q = e.q8;
-                act_[ctn] = e;
+            } else {
+                attn_quant_out(A, M.ct, ctn, n_q);
             }
             prof_scope ps(this, A.acc ? "attn_decode_acc" : "attn_decode", bytes);
             launch_attn_decode(A, st_);

@@ -515,6 +515,86 @@ __global__ __launch_bounds__(CMB_PARTS * HD) void attn_combine_kernel(const attn
     }
 }
 
+// The combination with the output's Q8_K copy (out_q8k): one workgroup per (256-dim super-block,
+// query), CMB_K_PARTS threads per dim adding runs of the chunk partials as above, then the
+// super-block quantized with quantize_row_q8_K's arithmetic (the steps of quantize_q8k_kernel: the
+// value of largest magnitude, the first on ties; iscale = -127 / max; q = min(127, nearest(iscale *
+// x)); d = 1 / iscale; 16-element sums). Every thread reaches every barrier.
+constexpr int CMB_K_PARTS = 4;
+template <int HD>
+__global__ __launch_bounds__(CMB_K_PARTS * 256) void attn_combine_q8k_kernel(const attn_launch A_, int n_splits) {
+    const attn_launch & A = kernargs_prefetched(A_);
+    __shared__ double s_run[CMB_K_PARTS][256];
+    __shared__ float s_ax[4];
+    __shared__ int s_idx[4];
+    __shared__ float s_val[4];
+    __shared__ int s_q[256];
+    const attn_scratch S = scratch_of(A);
+    const int sb = blockIdx.x, q = blockIdx.y;
+    const int t = threadIdx.x, j = t % 256, part = t / 256, lane = t % WAVE, wave = t / WAVE;
+    const int h = sb * (256 / HD) + j / HD, d = j % HD;
+    const double * pp = S.parts + ((int64_t) q * A.n_head + h) * HD + d;
+    const int64_t step = (int64_t) A.n_q * A.n_head * HD;
+    const int per = (n_splits + CMB_K_PARTS - 1) / CMB_K_PARTS;
+    const int s0 = part * per, s1 = min(n_splits, s0 + per);
+    double acc = 0.0;
+    for (int b = s0; b < s1; b += CMB_PER) {
+        double v[CMB_PER];
+#pragma unroll
+        for (int k = 0; k < CMB_PER; k++) v[k] = pp[min(b + k, n_splits - 1) * step];   // clamped, unused past s1
+#pragma unroll
+        for (int k = 0; k < CMB_PER; k++) acc += b + k < s1 ? v[k] : 0.0;
+    }
+    s_run[part][j] = acc;
+    __syncthreads();
+    float v = 0.0f;
+    if (part == 0) {
+        acc = s_run[0][j];
+#pragma unroll
+        for (int p = 1; p < CMB_K_PARTS; p++) acc += s_run[p][j];
+        v = (float) acc;
+        A.out[(int64_t) q * A.out_nb1 + (int64_t) h * HD + d] = v;
+    }
+    // the super-block's value of largest magnitude (waves 0-3 hold its 256 values)
+    float ax = fabsf(v);
+    int idx = j;
+    float val = v;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ax2 = __shfl_xor(ax, o, WAVE);
+        const int idx2 = __shfl_xor(idx, o, WAVE);
+        const float val2 = __shfl_xor(val, o, WAVE);
+        if (ax2 > ax || (ax2 == ax && idx2 < idx)) { ax = ax2; idx = idx2; val = val2; }
+    }
+    if (part == 0 && lane == 0) { s_ax[wave] = ax; s_idx[wave] = idx; s_val[wave] = val; }
+    __syncthreads();
+    const int64_t K = (int64_t) A.n_head * HD, nsb = K / 256;
+    if (part == 0) {
+        float bax = s_ax[0], bval = s_val[0];
+        int bidx = s_idx[0];
+        for (int w = 1; w < 4; w++) {
+            if (s_ax[w] > bax || (s_ax[w] == bax && s_idx[w] < bidx)) { bax = s_ax[w]; bidx = s_idx[w]; bval = s_val[w]; }
+        }
+        int qv = 0;
+        if (bax != 0.0f) {
+            const float iscale = -127.f / bval;
+            qv = round_half_even(iscale * v);
+            qv = qv < 127 ? qv : 127;
+            if (j == 0) A.out_q8k.d[q * nsb + sb] = 1 / iscale;
+        } else if (j == 0) {
+            A.out_q8k.d[q * nsb + sb] = 0.0f;
+        }
+        A.out_q8k.qs[q * K + (int64_t) sb * 256 + j] = (int8_t) qv;
+        s_q[j] = qv;
+    }
+    __syncthreads();
+    if (t < 16) {
+        int sum = 0;
+        for (int i = 0; i < 16; i++) sum += s_q[t * 16 + i];
+        A.out_q8k.bsums[q * (K / 16) + (int64_t) sb * 16 + t] = (int16_t) sum;
+    }
+}
+
 // FSK > 0 (one query, one head per workgroup, n_kv <= FSK * ATT_THREADS): the workgroup forms its row's
 // statistics itself, from the chunk maxima and every score of the row, instead of reading them from
 // the statistics launch; the sum is the statistics kernel's, exp(s - M) in double over the row's
@@ -1020,6 +1100,19 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_pv_mq_kernel(const attn_laun
     }
 }
 
+// the combination launch: with out_q8k the Q8_K variant (one workgroup per 256-dim super-block)
+template <int HD>
+static void launch_combine(const attn_launch & A, int pv_splits, hipStream_t st) {
+    if constexpr (256 % HD == 0) {
+        if (A.out_q8k.qs) {
+            return launch(attn_combine_q8k_kernel<HD>, dim3(A.n_head * HD / 256, A.n_q), dim3(CMB_K_PARTS * 256), 0, st, A,
+                          pv_splits);
+        }
+    }
+    if (A.out_q8k.qs) HIP_ABORT("attn: a Q8_K output needs 256 %% hd == 0");
+    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(CMB_PARTS * HD), 0, st, A, pv_splits);
+}
+
 template <int HD>
 static void launch_attn_mq(const attn_launch & A, hipStream_t st) {
     const int splits = attn_chunks(A.n_kv);
@@ -1038,7 +1131,7 @@ static void launch_attn_mq(const attn_launch & A, hipStream_t st) {
     launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
     if (A.p_f32) launch((attn_pv_mq_kernel<HD, true>), dim3(pv_splits, A.n_head_kv, tiles), dim3(ATT_THREADS), 0, st, A);
     else launch((attn_pv_mq_kernel<HD, false>), dim3(pv_splits, A.n_head_kv, tiles), dim3(ATT_THREADS), 0, st, A);
-    launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(CMB_PARTS * HD), 0, st, A, pv_splits);
+    launch_combine<HD>(A, pv_splits, st);
 }
 
 template <int HD, int G>
@@ -1064,7 +1157,7 @@ static void launch_attn_t(const attn_launch & A, hipStream_t st) {
         launch(attn_stats_kernel, dim3(A.n_head, A.n_q, attn_segs(A.n_kv)), dim3(ATT_THREADS), 0, st, A);
         launch((attn_pv_kernel<HD, G, 0>), pv_grid, dim3(ATT_THREADS), 0, st, A, pvq);
     }
-    if (!A.acc) launch(attn_combine_kernel<HD>, dim3(A.n_head, A.n_q), dim3(CMB_PARTS * HD), 0, st, A, pv_splits);
+    if (!A.acc) launch_combine<HD>(A, pv_splits, st);
 }
 
 template <int HD>
@@ -1145,7 +1238,8 @@ void launch_attn_decode(const attn_launch & A_in, hipStream_t st) {
     if (A.n_head % A.n_head_kv) HIP_ABORT("attn: n_head %% n_head_kv");
     if (A.scratch_bytes < attn_scratch_bytes(A.n_kv, A.n_q, A.n_head, A.hd)) HIP_ABORT("attn: scratch too small");
     if (A.out_q.qs && (A.hd % 32)) HIP_ABORT("attn: quantized output needs hd %% 32 == 0");
-    if (A.acc && (A.n_q != 1 || A.out_q.qs || ((uintptr_t) A.acc) % 16)) HIP_ABORT("attn: the accumulated output takes one query, no quantized copy, 16-byte alignment");
+    if (A.acc && (A.n_q != 1 || A.out_q.qs || A.out_q8k.qs || ((uintptr_t) A.acc) % 16)) HIP_ABORT("attn: the accumulated output takes one query, no quantized copy, 16-byte alignment");
+    if (A.out_q8k.qs && (A.out_q.qs || (A.n_head * A.hd) % 256 || 256 % A.hd)) HIP_ABORT("attn: Q8_K output needs n_head * hd %% 256 == 0 and 256 %% hd == 0");
     if (A.n_q > ATT_MAX_Q) {
         // many queries: scores and PV on the matrix cores
         switch (A.hd) {

@@ -398,6 +398,9 @@ struct attn_launch {
     int64_t        scratch_bytes;
     // quantized copy of out for the o-projection (Q8_0 semantics), optional
     q8_act         out_q;
+    // or its Q8_K copy (quantize_row_q8_K semantics; n_head * hd a multiple of 256 and 256 a
+    // multiple of hd: one combination workgroup per 256-dim super-block), optional
+    q8k_act        out_q8k;
     // one query (n_q == 1): instead of per-chunk partials and a combination launch, the PV
     // workgroups add their chunk partials into acc[head * hd + i] (doubles; exact sums, so their
     // order does not matter; zeroed by the scores launch), and out / out_q are not written: the

@@ -801,6 +801,38 @@ def test_attention_output_accumulated_into_o_projection(hip, cpu, qtype, hd, n_h
     assert "attn_decode_acc" in names and "attn_decode" not in names, names
 
 
+@pytest.mark.parametrize("qtype,hd,n_head,n_head_kv,n_kv,n_new", [
+    (gl.Q4_K, 128, 32, 4, 2400, 16),   # the MoE 16-token step: the multi-query matrix-core kernels
+    (gl.Q4_K, 128, 16, 8, 300, 3),     # the four-query decode kernels
+    (gl.Q6_K, 64, 8, 8, 90, 3),        # head dim 64: four heads per super-block
+])
+def test_attention_combination_writes_q8k(hip, cpu, qtype, hd, n_head, n_head_kv, n_kv, n_new):
+    """Several queries' attention read by a K-quant O projection: the combination launch writes the
+    output's Q8_K copy itself (quantize_row_q8_K's arithmetic over each 256-dim super-block), so no
+    separate quantization launch runs; bit-exact against the oracle, fused or not."""
+    r = rng(n_kv + n_new + hd)
+    n_ctx = n_kv + 3
+    kc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+    vc = r.standard_normal((n_ctx, n_head_kv, hd)).astype(np.float16)
+    q = r.standard_normal((n_new, n_head, hd)).astype(np.float32)
+    mask = np.zeros((n_new, n_kv), dtype=np.float32)
+    n_past = n_kv - n_new
+    for i in range(n_new):
+        mask[i, n_past + i + 1:] = -np.inf
+    K, rows = n_head * hd, 640
+    wo = qweight(qtype, K, rows, 97, std=0.05)
+
+    def build(g):
+        att = attention_graph(g, hd, n_head, n_head_kv, n_kv, n_new, n_ctx, kc, vc, q, mask)
+        return g.mul_mat(g.tensor(qtype, K, rows, data=wo), att)
+
+    for fusion in (True, False):
+        a, b = both(hip, cpu, build, fusion)
+        assert np.array_equal(a, b), (fusion, rel_err(a, b))
+    _, names = profiled(hip, lambda: run_on(hip, build))
+    assert "attn_decode" in names and "quantize_q8K" not in names, names
+
+
 @pytest.mark.parametrize("n_new,n_kv", [
     (2, 70),       # the decode kernels
     (20, 70),      # the prefill kernel
