@@ -365,7 +365,8 @@ enum fuse_bits {
     FUSE_MC     = 512, // several activation columns per GEMV workgroup; mul_mat_id grouped by expert
     FUSE_ROUTEG = 1024, // one token's MoE routing inside its routed gate/up GEMV launch
     FUSE_ACCO   = 2048, // one-query attention output accumulated by PV, read as doubles by its GEMVs
-    FUSE_ALL    = 4095,
+    FUSE_WSUMQ  = 4096, // MoE weighted sum also writes the next rms_norm * w as Q8_K (several tokens)
+    FUSE_ALL    = 8191,
 };
 
 struct hip_backend_ctx {
@@ -1773,6 +1774,32 @@ private:
 
     // mul(experts [n_embd, k, T], w [1, k, T]) -> views of the k slots -> add chain in slot order
     // (-> residual add)  ==>  one kernel with the same float operations in the same order
+    // an rms_norm of x (several rows) whose sole user multiplies by an f32 weight row and whose
+    // readers are only GEMVs over K-quant weights: op_rms_norm would normalize and quantize it to
+    // Q8_K in an act_quant launch of its own. Returns the norm node, the mul node and eps.
+    bool norm_q8k_of(const ggml_tensor * x, int & nn, int & nm, float & eps) const {
+        const int xi = node_index(x);
+        if (!fuse(FUSE_WSUMQ) || !fuse(FUSE_NORM) || !fuse(FUSE_MC) || xi < 0 || x->type != GGML_TYPE_F32 || !ggml_is_contiguous(x) ||
+            x->ne[0] > RMS_NORM_MAX_ROW || ggml_nrows(x) < 2) return false;
+        for (int j : users_[xi]) {
+            const ggml_tensor * n = g_->nodes[j];
+            if (done_[j] || n->op != GGML_OP_RMS_NORM || n->src[0] != x || !ggml_is_contiguous(n)) continue;
+            const int u = sole_user(j);
+            if (u < 0) continue;
+            const ggml_tensor * m = g_->nodes[u];
+            const ggml_tensor * w = m->src[1];
+            if (m->op != GGML_OP_MUL || m->src[0] != n || w->type != GGML_TYPE_F32 || ggml_nrows(w) != 1 || w->ne[0] != x->ne[0] ||
+                !ggml_is_contiguous(w) || !ggml_is_contiguous(m) || m->ne[1] != ggml_nrows(x) ||
+                ((uintptr_t) x->data | (uintptr_t) w->data) % 16) continue;
+            if (!norm_deferrable(u, x->ne[0]) || wanted_act_kind(u) != 2) continue;
+            nn = j;
+            nm = u;
+            memcpy(&eps, n->op_params, 4);
+            return true;
+        }
+        return false;
+    }
+
     bool op_moe_wsum(int i) {
         const ggml_tensor * m = g_->nodes[i];
         const ggml_tensor * e = m->src[0], * w = m->src[1];
@@ -1828,8 +1855,22 @@ private:
         if (!is_2d_contig(last)) return false;
         M.out = (float *) last->data;
         M.out_nb1 = (int64_t) (last->nb[1] / sizeof(float));
-        {
-            prof_scope ps(this, "moe_wsum", (double) (n_embd * k * T * 4 + n_embd * T * 4 * (M.res ? 2 : 1)));
+        const double wsum_bytes = (double) (n_embd * k * T * 4 + n_embd * T * 4 * (M.res ? 2 : 1));
+        int nn = -1, nm = -1;
+        float eps = 0.0f;
+        if (T >= 2 && norm_q8k_of(last, nn, nm, eps) && wsum_norm_q8k_supported(M, (const float *) g_->nodes[nm]->src[1]->data)) {
+            // the next rms_norm * w, normalized and quantized in the same launch (what op_rms_norm
+            // would do in an act_quant launch of its own)
+            ggml_tensor * mn = g_->nodes[nm];
+            act_entry e = alloc_act(2, n_embd, T);
+            {
+                prof_scope ps(this, "moe_wsum_q8k", wsum_bytes + (double) (n_embd * 4 + n_embd * T + (n_embd / 256 * 4 + n_embd / 16 * 2) * T));
+                launch_wsum_norm_q8k(M, (const float *) mn->src[1]->data, eps, e.q8k, st_);
+            }
+            act_[mn] = e;
+            done_[nn] = done_[nm] = true;
+        } else {
+            prof_scope ps(this, "moe_wsum", wsum_bytes);
             launch_moe_wsum(M, st_);
         }
         for (int v : view) done_[v] = true;

@@ -561,6 +561,119 @@ __global__ __launch_bounds__(GEMV_NT) void act_quant_kernel(const gemv_launch L,
     }
 }
 
+// moe_wsum_kernel's weighted sum of the k expert rows (+ residual) for one token per workgroup,
+// written out as that kernel writes it, then the next rms_norm * w of the row quantized to Q8_K
+// with act_quant_kernel's arithmetic (thread t holds elements 16t .. 16t + 15, its chunk): the
+// launch that produces the residual stream also produces the next projection's quantized input.
+__global__ __launch_bounds__(GEMV_NT) void wsum_norm_q8k_kernel(const moe_wsum M, const float * nw, float eps, q8k_act q8k) {
+    prefetch_kernargs<sizeof(moe_wsum)>();
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ double s_red[GEMV_NT / WAVE];
+    __shared__ __align__(16) float s_x[16 * GEMV_NT];
+    const int K = (int) M.n_embd, tok = blockIdx.x, t = threadIdx.x;
+    const int lane = t % WAVE, wave = t / WAVE, nchunk = K / 16, nv = K / 4;
+    const int c = min(t, nchunk - 1);                 // clamped, unused past the row
+    const gemv_lds s = lds_layout<GGML_TYPE_Q4_K>(smem, K);
+    const float4 * e = (const float4 *) (M.e + (int64_t) tok * M.e_nb2);
+    const float * w = M.w + (int64_t) tok * M.w_nb2;
+    // the sum: float4 columns v0 + t and v0 + GEMV_NT + t of the row per thread (every thread, loads
+    // coalesced), the slots in order with each product rounded, as the mul and add chain; then the
+    // residual. The row goes out and into LDS, where each thread picks its 16-element chunk up.
+    for (int v0 = 0; v0 < nv; v0 += 2 * GEMV_NT) {
+        const int va = min(v0 + t, nv - 1), vb = min(v0 + GEMV_NT + t, nv - 1);   // clamped, unused past the row
+        float4 xa = make_float4(0.0f, 0.0f, 0.0f, 0.0f), xb = xa;
+        for (int s0 = 0; s0 < M.k; s0 += 8) {
+            float4 ea[8], eb[8];
+            float wv[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int sl = min(s0 + j, M.k - 1);  // clamped, unused past k
+                wv[j] = w[sl * M.w_nb1];
+                ea[j] = e[sl * (M.e_nb1 / 4) + va];
+                eb[j] = e[sl * (M.e_nb1 / 4) + vb];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                if (s0 + j < M.k) {
+                    const float4 pa = make_float4(ea[j].x * wv[j], ea[j].y * wv[j], ea[j].z * wv[j], ea[j].w * wv[j]);
+                    const float4 pb = make_float4(eb[j].x * wv[j], eb[j].y * wv[j], eb[j].z * wv[j], eb[j].w * wv[j]);
+                    if (s0 + j == 0) {
+                        xa = pa;
+                        xb = pb;
+                    } else {
+                        xa = make_float4(xa.x + pa.x, xa.y + pa.y, xa.z + pa.z, xa.w + pa.w);
+                        xb = make_float4(xb.x + pb.x, xb.y + pb.y, xb.z + pb.z, xb.w + pb.w);
+                    }
+                }
+            }
+        }
+        if (M.res) {
+            const float4 * r = (const float4 *) (M.res + (int64_t) tok * M.res_nb1);
+            const float4 ra = r[va], rb = r[vb];
+            xa = make_float4(xa.x + ra.x, xa.y + ra.y, xa.z + ra.z, xa.w + ra.w);
+            xb = make_float4(xb.x + rb.x, xb.y + rb.y, xb.z + rb.z, xb.w + rb.w);
+        }
+        float4 * o = (float4 *) (M.out + (int64_t) tok * M.out_nb1);
+        if (v0 + t < nv) {
+            o[va] = xa;
+            ((float4 *) s_x)[va] = xa;
+        }
+        if (v0 + GEMV_NT + t < nv) {
+            o[vb] = xb;
+            ((float4 *) s_x)[vb] = xb;
+        }
+    }
+    __syncthreads();
+    float x0[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float4 v = ((const float4 *) s_x)[c * 4 + q];
+        x0[4 * q] = v.x; x0[4 * q + 1] = v.y; x0[4 * q + 2] = v.z; x0[4 * q + 3] = v.w;
+    }
+    // rms_norm * w and Q8_K: the steps of prologue_finish's rms mode
+    double ss = 0.0;
+    if (t < nchunk) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) ss += (double) (x0[i] * x0[i]);
+    }
+    ss = wave_sum_d(ss);
+    if (lane == 0) s_red[wave] = ss;
+    __syncthreads();
+    double total = 0.0;
+    for (int w8 = 0; w8 < GEMV_NT / WAVE; w8++) total += s_red[w8];
+    const float mean = (float) (total / (double) K);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    const float4 * w4 = (const float4 *) (nw + c * 16);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float4 g = w4[q];
+        x0[4 * q] = x0[4 * q] * scale; x0[4 * q] = x0[4 * q] * g.x;
+        x0[4 * q + 1] = x0[4 * q + 1] * scale; x0[4 * q + 1] = x0[4 * q + 1] * g.y;
+        x0[4 * q + 2] = x0[4 * q + 2] * scale; x0[4 * q + 2] = x0[4 * q + 2] * g.z;
+        x0[4 * q + 3] = x0[4 * q + 3] * scale; x0[4 * q + 3] = x0[4 * q + 3] * g.w;
+    }
+    quant_chunk<GGML_TYPE_Q4_K, 16>(x0, t, t < nchunk, s);
+    __syncthreads();
+    int8_t * qs = q8k.qs + (int64_t) tok * K;
+    for (int i = t * 16; i < K; i += GEMV_NT * 16) *(int4 *) (qs + i) = *(const int4 *) (s.xq + i);
+    for (int i = t; i < K / 256; i += GEMV_NT) q8k.d[(int64_t) tok * (K / 256) + i] = s.xd[i];
+    for (int i = t; i < K / 16; i += GEMV_NT) q8k.bsums[(int64_t) tok * (K / 16) + i] = s.xbs[i];
+}
+
+bool wsum_norm_q8k_supported(const moe_wsum & M, const float * nw) {
+    const int64_t K = M.n_embd;
+    return K % 256 == 0 && K <= 16 * GEMV_NT && M.k >= 1 && M.n_tok >= 1 && ((uintptr_t) M.e | (uintptr_t) M.out | (uintptr_t) nw) % 16 == 0 &&
+           (!M.res || ((uintptr_t) M.res % 16 == 0 && M.res_nb1 % 4 == 0)) && M.e_nb1 % 4 == 0 && M.e_nb2 % 4 == 0 && M.out_nb1 % 4 == 0;
+}
+
+void launch_wsum_norm_q8k(const moe_wsum & M, const float * nw, float eps, q8k_act q8k, hipStream_t st) {
+    const int64_t K = M.n_embd;
+    if (!wsum_norm_q8k_supported(M, nw)) HIP_ABORT("wsum_norm_q8k: unsupported rows (n_embd %lld)", (long long) K);
+    launch(wsum_norm_q8k_kernel, dim3((unsigned) M.n_tok), dim3(GEMV_NT), gemv_lds_bytes<GGML_TYPE_Q4_K>((int) K, 0, 0), st, M, nw, eps,
+           q8k);
+}
+
 void launch_act_quant(const gemv_launch & L, const q8_act & q8, const q8k_act & q8k, hipStream_t st) {
     if (!L.norm.x || L.K > act_quant_max_k(L.type, L.norm.rms != 0)) HIP_ABORT("act_quant: K=%d unsupported", L.K);
     switch (L.type) {

@@ -331,6 +331,10 @@ struct moe_wsum {
     int k;
 };
 void launch_moe_wsum(const moe_wsum & M, hipStream_t st);
+// the weighted sum, then the next rms_norm * nw of each token's row quantized to Q8_K (one launch;
+// n_embd a multiple of 256, at most 4096; rows 16-byte aligned)
+bool wsum_norm_q8k_supported(const moe_wsum & M, const float * nw);
+void launch_wsum_norm_q8k(const moe_wsum & M, const float * nw, float eps, q8k_act q8k, hipStream_t st);
 void launch_argmax(const tview & a, int32_t * out, hipStream_t st);
 // one wide row in two launches over ARGMAX_PARTS partial results (part_v / part_i: that many
 // entries of device scratch); the same index as launch_argmax

@@ -1102,6 +1102,41 @@ def test_moe_ffn_norm_folded_into_router(hip, cpu, n_tok):
     assert "router_norm" in names and "rms_norm_mul" not in names, names
 
 
+@pytest.mark.parametrize("ptype,n_tok,with_res", [(gl.Q4_K, 16, True), (gl.Q4_K, 5, True), (gl.Q6_K, 3, False),
+                                                  (gl.Q4_0, 5, True), (gl.Q4_K, 1, True)])
+def test_moe_sum_feeds_next_norm_q8k(hip, cpu, ptype, n_tok, with_res):
+    """The MoE weighted sum (+ residual) read by the next rms_norm -> mul whose readers are K-quant
+    GEMVs, over several tokens: one launch writes the residual stream and its normalized Q8_K copy
+    (the act_quant launch's arithmetic), and every output is the oracle's."""
+    n_embd, E, k, ff = 512, 32, 8, 256
+    r = rng(82 + n_tok)
+    y = r.standard_normal((n_tok, n_embd)).astype(np.float32)
+    res = r.standard_normal((n_tok, n_embd)).astype(np.float32)
+    nw = (1 + 0.01 * r.standard_normal(n_embd)).astype(np.float32)
+    router = (r.standard_normal((E, n_embd)) * 0.05).astype(np.float32)
+    wg, wu = (qweight(gl.Q4_K, n_embd, E * ff, s, std=0.05) for s in (83, 84))
+    wd = qweight(gl.Q4_K, ff, E * n_embd, 85, std=0.05)
+    wq, wk = qweight(ptype, n_embd, 512, 86), qweight(ptype, n_embd, 256, 87)
+
+    def build(g):
+        out = moe_ffn_graph(g, g.tensor(gl.F32, n_embd, n_tok, data=y), g.tensor(gl.F32, n_embd, E, data=router),
+                            g.tensor(gl.Q4_K, n_embd, ff, E, data=wg), g.tensor(gl.Q4_K, n_embd, ff, E, data=wu),
+                            g.tensor(gl.Q4_K, ff, n_embd, E, data=wd), k,
+                            g.tensor(gl.F32, n_embd, n_tok, data=res) if with_res else None)
+        h = g.mul(g.rms_norm(out, 1e-6), g.tensor(gl.F32, n_embd, data=nw))
+        return [out, g.mul_mat(g.tensor(ptype, n_embd, 512, data=wq), h), g.mul_mat(g.tensor(ptype, n_embd, 256, data=wk), h)]
+
+    for fusion in (True, False):
+        hs, cs = both(hip, cpu, build, fusion)
+        for a, b in zip(hs, cs):
+            assert np.array_equal(a, b), (fusion, rel_err(a, b))
+    _, names = profiled(hip, lambda: run_on(hip, build))
+    fused = n_tok >= 2 and ptype != gl.Q4_0
+    assert ("moe_wsum_q8k" in names) == fused and ("moe_wsum" in names) != fused, names
+    if fused:
+        assert "act_quant" not in names and "rms_norm_mul" not in names, names
+
+
 @pytest.mark.parametrize("n_tok", [1, 5])
 def test_moe_router_norm_kept_apart_when_its_input_dies(hip, cpu, n_tok):
     """The norm's input computed in the graph and read by nothing after the norm: the allocator may
